@@ -1,0 +1,232 @@
+"""Pins the oracle's f16 conversions, quantizers and dequantizers.
+
+Anchors: the reference's own tests (src/gguf/mod.rs:1681-1714,
+src/quant/mod.rs:1287-1325), numpy's IEEE float16 conversion, and an
+independent vectorised numpy statement of the GGUF block layouts
+(src/quant/mod.rs:689-849), exercised on crafted blocks that cover every
+6-bit scale/min value, every 4-bit code and subnormal f16 scales.
+"""
+import numpy as np
+import pytest
+
+Q4_0, Q8_0, Q4_K = 2, 8, 12
+
+
+# ----------------------------------------------------------------------------- f16
+def test_f16_to_f32_exhaustive(oracle):
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = oracle.f16_to_f32(bits)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne(oracle):
+    rng = np.random.default_rng(1)
+    raw = rng.integers(0, 2**32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    x = raw.view(np.float32)
+    # every f16 value and every midpoint between neighbours (ties-to-even cases)
+    h = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = ((h[:-1] + h[1:]) / 2).astype(np.float32)
+    edge = np.array([65504, 65519.99, 65520, 65536, 1e-8, 2.98e-8, 2.9802322e-8, 5.96e-8,
+                     6.1035156e-05, 6.1e-05, 0.0, -0.0, np.inf, -np.inf], np.float32)
+    x = np.concatenate([x, h.astype(np.float32), mids, -mids, edge])
+    x = x[~np.isnan(x)]
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    got = oracle.f32_to_f16(x)
+    bad = np.nonzero(got != ref)[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first x={x[bad[0]]!r}"
+
+
+# ----------------------------------------------------------------------------- known answers
+def test_q8_0_known_answer(oracle):
+    """src/gguf/mod.rs:1681-1695: scale f16(0.5), q = i - 16."""
+    scale = np.array([0.5], np.float32).astype(np.float16).view(np.uint8)
+    block = np.concatenate([scale, (np.arange(32) - 16).astype(np.int8).view(np.uint8)])
+    v = oracle.dequantize(Q8_0, block, 32)
+    assert v.size == 32
+    assert v[0] == -8.0 and v[16] == 0.0 and v[31] == 7.5
+
+
+@pytest.mark.parametrize("fmt,tol,n", [(Q8_0, 0.03, 64), (Q4_0, 0.3, 64), (Q4_K, 0.4, 300)])
+def test_reference_roundtrip_tolerances(oracle, fmt, tol, n):
+    """src/quant/mod.rs:1287-1325 (Q8_0 / Q4_0 on i/16-2, Q4_K on i/31-4)."""
+    if fmt == Q4_K:
+        data = np.arange(n, dtype=np.float32) / np.float32(31.0) - np.float32(4.0)
+    else:
+        data = np.arange(n, dtype=np.float32) / np.float32(16.0) - np.float32(2.0)
+    q = oracle.quantize(fmt, data)
+    if fmt == Q4_K:
+        assert q.size == (n + 255) // 256 * 144  # src/quant/mod.rs:1318
+    dec = oracle.dequantize(fmt, q, n)
+    assert dec.size == n
+    assert np.all(np.abs(dec - data) < tol)
+
+
+def test_q4_k_ramp_sizes_match_gguf_test(oracle):
+    """src/gguf/mod.rs:1697-1714: Q4_K payload size and decoded length."""
+    data = np.arange(300, dtype=np.float32) / np.float32(31.0) - np.float32(4.0)
+    q = oracle.quantize(Q4_K, data)
+    assert q.size == 2 * 144
+    assert oracle.dequantize(Q4_K, q, 300).size == 300
+
+
+# ----------------------------------------------------------------------------- layouts
+def np_dequant(fmt, data, n):
+    """Independent vectorised statement of the three block layouts."""
+    f16 = lambda b: b.copy().view(np.float16).astype(np.float32).ravel()  # noqa: E731
+    np.seterr(invalid="ignore", over="ignore")
+    if fmt == Q8_0:
+        b = data.reshape(-1, 34)
+        d = f16(b[:, 0:2])
+        v = b[:, 2:].view(np.int8).astype(np.float32) * d[:, None]
+    elif fmt == Q4_0:
+        b = data.reshape(-1, 18)
+        d = f16(b[:, 0:2])
+        qs = b[:, 2:]
+        q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.int16) - 8
+        v = q.astype(np.float32) * d[:, None]
+    else:
+        b = data.reshape(-1, 144)
+        d, dmin = f16(b[:, 0:2]), f16(b[:, 2:4])
+        p = b[:, 4:16]
+        sc = np.concatenate([p[:, 0:4] & 63, (p[:, 8:12] & 15) | ((p[:, 0:4] >> 6) << 4)], axis=1)
+        mn = np.concatenate([p[:, 4:8] & 63, (p[:, 8:12] >> 4) | ((p[:, 4:8] >> 6) << 4)], axis=1)
+        qs = b[:, 16:]
+        q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.float32)  # element i, i+128
+        sub = np.arange(256) // 32
+        v = (d[:, None] * sc[:, sub].astype(np.float32)) * q - dmin[:, None] * mn[:, sub].astype(
+            np.float32)
+    return v.ravel()[:n]
+
+
+def crafted_blocks(fmt, nblocks, seed):
+    rng = np.random.default_rng(seed)
+    bs = {Q8_0: 34, Q4_0: 18, Q4_K: 144}[fmt]
+    data = rng.integers(0, 256, size=(nblocks, bs), dtype=np.uint8)
+    # scales: normal, subnormal, zero, negative zero, largest finite
+    special = np.array([0x3C00, 0x0001, 0x03FF, 0x0000, 0x8000, 0x7BFF, 0x2E66, 0x8123],
+                       np.uint16)
+    hdr = data[:, 0:2].copy().view(np.uint16).ravel()
+    hdr[: nblocks // 2] = special[np.arange(nblocks // 2) % special.size]
+    data[:, 0:2] = hdr.view(np.uint8).reshape(-1, 2)
+    if fmt == Q4_K:
+        dm = data[:, 2:4].copy().view(np.uint16).ravel()
+        dm[: nblocks // 2] = special[(np.arange(nblocks // 2) + 3) % special.size]
+        data[:, 2:4] = dm.view(np.uint8).reshape(-1, 2)
+        # walk every 6-bit scale/min value through every sub-block slot
+        for b in range(min(nblocks, 64)):
+            sc = np.full(8, b, np.uint8)
+            mn = np.full(8, 63 - b, np.uint8)
+            data[b, 4:16] = (np.array(
+                [(sc[i] & 63) | ((sc[i + 4] >> 4) << 6) for i in range(4)] +
+                [(mn[i] & 63) | ((mn[i + 4] >> 4) << 6) for i in range(4)] +
+                [(sc[i + 4] & 15) | ((mn[i + 4] & 15) << 4) for i in range(4)], np.uint8))
+    return data.ravel()
+
+
+@pytest.mark.parametrize("fmt", [Q8_0, Q4_0, Q4_K])
+def test_dequant_matches_layout_statement(oracle, fmt):
+    blk = {Q8_0: 32, Q4_0: 32, Q4_K: 256}[fmt]
+    data = crafted_blocks(fmt, 256, seed=fmt)
+    n = 256 * blk
+    got = oracle.dequantize(fmt, data, n)
+    ref = np_dequant(fmt, data, n)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    # output_len stops mid-block; a ragged byte tail is dropped like chunks_exact
+    got2 = oracle.dequantize(fmt, data[: data.size - 5], n - 7)
+    assert got2.size == (255 * blk if blk * 255 < n - 7 else n - 7)
+    assert np.array_equal(got2.view(np.uint32), ref[: got2.size].view(np.uint32))
+
+
+def test_q4k_every_code_and_scale(oracle):
+    """Brute force: every (sc, m) in [0,63]^2 and q in [0,15] for d = dmin = 1 and
+    for subnormal d/dmin: value = d*sc*q - dmin*m (products exact in f32)."""
+    for d_bits, m_bits in [(0x3C00, 0x3C00), (0x0001, 0x0003), (0x7BFF, 0x0400)]:
+        d = np.uint16(d_bits).view(np.float16).astype(np.float64)
+        dm = np.uint16(m_bits).view(np.float16).astype(np.float64)
+        blocks = []
+        expect = []
+        for s in range(64):
+            sc = np.full(8, s, np.uint8)
+            mn = (np.arange(8, dtype=np.uint8) * 9 + s) % 64
+            packed = oracle.pack_q4k_scales(sc, mn)
+            s2, m2 = oracle.unpack_q4k_scales(packed)
+            assert np.array_equal(s2, sc) and np.array_equal(m2, mn)
+            qs = (np.arange(128) % 16 | ((np.arange(128) * 7 % 16) << 4)).astype(np.uint8)
+            hdr = np.array([d_bits, m_bits], np.uint16).view(np.uint8)
+            blocks.append(np.concatenate([hdr, packed, qs]))
+            q = np.concatenate([qs & 15, qs >> 4]).astype(np.float64)
+            sub = np.arange(256) // 32
+            exact = d * sc[sub] * q - dm * mn[sub]
+            expect.append(exact.astype(np.float32))  # one rounding of the exact value
+        got = oracle.dequantize(Q4_K, np.concatenate(blocks), 64 * 256)
+        assert np.array_equal(got, np.concatenate(expect))
+
+
+def test_scale_pack_roundtrip_all_values(oracle):
+    for s in range(64):
+        for m in range(0, 64, 7):
+            sc = (np.arange(8) * 5 + s) % 64
+            mn = (np.arange(8) * 3 + m) % 64
+            s2, m2 = oracle.unpack_q4k_scales(oracle.pack_q4k_scales(sc, mn))
+            assert np.array_equal(s2, sc) and np.array_equal(m2, mn)
+
+
+# ----------------------------------------------------------------------------- quantizers
+@pytest.mark.parametrize("fmt", [Q8_0, Q4_0, Q4_K])
+def test_quantizer_error_bounds(oracle, fmt):
+    """|x - dq(q(x))| stays within each format's step bound on N(0, 0.02) data."""
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(256 * 64) * 0.02).astype(np.float32)
+    q = oracle.quantize(fmt, x)
+    dq = oracle.dequantize(fmt, q, x.size)
+    blk = {Q8_0: 32, Q4_0: 32, Q4_K: 256}[fmt]
+    xb = x.reshape(-1, blk)
+    err = np.abs(dq - x).reshape(-1, blk)
+    amax = np.abs(xb).max(axis=1, keepdims=True)
+    if fmt == Q8_0:
+        bound = amax / 127 * 0.5 * 1.01 + amax * 2.0**-11
+    elif fmt == Q4_0:
+        bound = amax / 7 * 0.5 * 1.01 + amax * 2.0**-11 * 8
+    else:
+        bound = (xb.max(axis=1, keepdims=True) - xb.min(axis=1, keepdims=True)) / 15 * 1.2
+    assert np.all(err <= bound)
+
+
+def test_quantizer_thread_invariance(oracle):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(256 * 97) * 0.02).astype(np.float32)
+    for fmt in (Q8_0, Q4_0, Q4_K):
+        a = oracle.quantize(fmt, x, nthreads=1)
+        b = oracle.quantize(fmt, x, nthreads=7)
+        assert np.array_equal(a, b)
+
+
+def test_q8_0_hand_block(oracle):
+    """One block worked by hand: x = (i-16)/2 -> max 8, scale 8/127 (f32), q = round(x/scale)."""
+    x = ((np.arange(32) - 16) * 0.5).astype(np.float32)
+    q = oracle.quantize(Q8_0, x)
+    scale32 = np.float32(8.0) / np.float32(127.0)
+    assert q[0:2].view(np.uint16)[0] == np.float32(scale32).astype(np.float16).view(np.uint16)
+    codes = q[2:].view(np.int8).astype(np.int32)
+    expect = [int(np.sign(v) * np.floor(abs(v) + 0.5)) for v in (x / scale32).astype(np.float32)]
+    assert codes.tolist() == expect
+    assert codes[0] == -127 and codes[16] == 0
+
+
+def test_q4_k_hand_block(oracle):
+    """A block whose sub-blocks are exact ramps 0..15 scaled by 2^-4: d = 1/63*(15/16)/15...
+    every value must survive the round trip exactly when scales are representable."""
+    x = np.zeros(256, np.float32)
+    x[:] = (np.arange(256) % 16).astype(np.float32)  # each sub-block: 0..15, twice
+    q = oracle.quantize(Q4_K, x)
+    dq = oracle.dequantize(Q4_K, q, 256)
+    # scale per sub-block = 15/15 = 1, d = 1/63 -> f16; sc = 63; offsets 0 -> dmin = 0
+    d16 = np.float32(np.float32(1.0) / np.float32(63.0)).astype(np.float16).astype(np.float32)
+    assert q[2:4].view(np.uint16)[0] == 0  # dmin == 0
+    s, m = oracle.unpack_q4k_scales(q[4:16])
+    assert s.tolist() == [63] * 8 and m.tolist() == [0] * 8
+    assert np.array_equal(dq, (d16 * np.float32(63.0)) * x)
