@@ -1,0 +1,232 @@
+"""Benchmark: Mixtral-8x7B-shaped MoE layer (Q4_K experts) on one MI355X.
+
+One step = one pass of the MoE layer (router -> permutation -> gate/up GEMV
+with fused SwiGLU -> down GEMV -> combine) over one batch of synthetic tokens
+whose activations, router logits and quantized experts are already resident
+in HBM.  Weights ~N(0, 0.02) are quantized to Q4_K on the device by the
+library's quantizer; activations ~N(0, 1); logits = x . W_r^T with
+W_r ~N(0, 0.02).  Several replicas of the expert set (more than twice the
+~256 MB Infinity Cache in the bytes a step touches) are rotated step by step
+so the weight bytes come from HBM.
+
+Prints one JSON line (rank 0, N=1).  `value` = tokens/s of the whole layer.
+`roofline` is for the dominant kernel (the gate/up GEMV): algorithmic bytes
+= quantized weight bytes of the experts the step activates, divided by the
+kernel's mean duration from HIP events on the stream it runs on.
+`cpu_baseline` times the CPU oracle (single-threaded restatement of
+InferenceEngine::dispatch_moe_ffn, f32 weights dequantized beforehand) on a
+bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer tokens/sec + effective HBM GB/s (Mixtral-shape Q4_K), 1 GPU"
+HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+Q4K_BYTES_PER_WEIGHT = 144.0 / 256.0
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--tokens", type=int, default=1)
+    p.add_argument("--replicas", type=int, default=4)
+    p.add_argument("--path", default="gemv", choices=["auto", "gemv", "mfma_f16", "mfma_bf16"])
+    p.add_argument("--cpu-tokens", type=int, default=16, help="tokens in the CPU-baseline sample")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--seed", type=int, default=0)
+    return p.parse_args()
+
+
+def make_expert_sets(nx, ctx, torch, fmt, E, H, F, replicas, seed):
+    """Quantized expert sets generated on the device (N(0, 0.02) -> fmt)."""
+    dev = torch.device("cuda", 0)
+    sets = []
+    qbuf = None
+    for rep in range(replicas):
+        ex = nx.Experts(ctx, fmt, E, H, F)
+        for e in range(E):
+            for role, (r, c) in ((nx.ROLE_GATE, (F, H)), (nx.ROLE_UP, (F, H)), (nx.ROLE_DOWN, (H, F))):
+                g = torch.Generator(device=dev)
+                g.manual_seed(seed * 1000003 + rep * 10007 + e * 101 + role)
+                w = torch.randn((r, c), generator=g, device=dev, dtype=torch.float32) * 0.02
+                nb = nx.quant_bytes(fmt, r * c)
+                if qbuf is None or qbuf.numel() < nb:
+                    qbuf = torch.empty(nb, dtype=torch.uint8, device=dev)
+                ctx.quantize_dev(fmt, w.data_ptr(), r * c, qbuf.data_ptr(), nb)
+                ex.load_dev(e, role, qbuf.data_ptr(), nb)
+                del w
+        sets.append(ex)
+    torch.cuda.synchronize()
+    return sets
+
+
+def cpu_baseline(nx, ctx, torch, x, logits, E, H, F, k, seed, ntok):
+    """Single-threaded oracle dispatch_moe_ffn on `ntok` tokens (f32 weights
+    dequantized from the same Q4_K payloads outside the timed region)."""
+    import numpy as np
+
+    import oracle
+
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed + 77)
+    xs = torch.randn((ntok, H), generator=gen, device=dev, dtype=torch.float32)
+    rw = logits["router"]
+    lg = (xs @ rw.t()).contiguous()
+    xs_h, lg_h = xs.cpu().numpy(), lg.cpu().numpy()
+    ex_ids, _, cnt, _ = oracle.route(lg_h, ntok, E, k)
+    need = sorted({int(e) for t in range(ntok) for e in ex_ids[t, :cnt[t]]})
+    mats = {0: [None] * E, 1: [None] * E, 2: [None] * E}
+    for e in need:
+        for role, (r, c) in ((0, (F, H)), (1, (F, H)), (2, (H, F))):
+            g = torch.Generator(device=dev)
+            g.manual_seed(seed * 1000003 + 0 * 10007 + e * 101 + role)  # replica 0
+            w = torch.randn((r, c), generator=g, device=dev, dtype=torch.float32) * 0.02
+            nb = nx.quant_bytes(nx.Q4_K, r * c)
+            qb = torch.empty(nb, dtype=torch.uint8, device=dev)
+            ctx.quantize_dev(nx.Q4_K, w.data_ptr(), r * c, qb.data_ptr(), nb)
+            torch.cuda.synchronize()
+            mats[role][e] = oracle.dequantize(oracle.Q4_K, qb.cpu().numpy(), r * c)
+            del w, qb
+    t0 = time.perf_counter()
+    for t in range(ntok):
+        oracle.dispatch_moe_ffn(xs_h[t], lg_h[t], mats[0], mats[1], mats[2], k, H, F)
+    dt = time.perf_counter() - t0
+    return {"value": ntok / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{ntok} tokens of the same Mixtral Q4_K layer through the oracle's "
+                      f"single-threaded dispatch_moe_ffn (f32 weights dequantized from the "
+                      f"Q4_K payloads outside the timed region), {dt:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import nexus_amd as nx
+
+    E, H, F, k, T = 8, 4096, 14336, 2, args.tokens
+    path = {"auto": nx.PATH_AUTO, "gemv": nx.PATH_GEMV, "mfma_f16": nx.PATH_MFMA_F16,
+            "mfma_bf16": nx.PATH_MFMA_BF16}[args.path]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    ctx = nx.Context(0)
+    # torch and the library share one explicit stream, so every launch is
+    # ordered after the tensors it reads (torch's default is the null stream)
+    stream = torch.cuda.Stream(device=dev)
+    torch.cuda.set_stream(stream)
+    ctx.set_stream(stream.cuda_stream)
+
+    print(f"bench: building {args.replicas} Q4_K expert replicas (E={E} H={H} F={F})",
+          file=sys.stderr, flush=True)
+    sets = make_expert_sets(nx, ctx, torch, nx.Q4_K, E, H, F, args.replicas, args.seed)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 1)
+    x = torch.randn((T, H), generator=g, device=dev, dtype=torch.float32)
+    router = torch.randn((E, H), generator=g, device=dev, dtype=torch.float32) * 0.02
+    logits = (x @ router.t()).contiguous()
+    out = torch.empty((T, H), device=dev, dtype=torch.float32)
+
+    # realised routing -> algorithmic bytes
+    ex_ids, w, cnt, _ = ctx.route_topk(logits.cpu().numpy(), T, E, k)
+    active = sorted({int(e) for t in range(T) for e in ex_ids[t, :cnt[t]]})
+    n_act = len(active)
+    gateup_bytes = n_act * 2 * F * H * Q4K_BYTES_PER_WEIGHT
+    down_bytes = n_act * H * F * Q4K_BYTES_PER_WEIGHT
+    step_bytes = gateup_bytes + down_bytes
+
+    def step(i):
+        sets[i % len(sets)].forward_dev(x.data_ptr(), logits.data_ptr(), T, k, out.data_ptr(),
+                                        path=path)
+
+    print("bench: warmup", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # timed region (value): K steps, no per-kernel events
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt * 1e3 / args.steps
+
+    # timed region (roofline): same K steps with HIP events around every launch
+    ctx.profile(True)
+    ctx.profile_reset()
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    stats = ctx.profile_stats()
+    ctx.profile(False)
+    kern = {name: ms / max(n, 1) for name, (n, ms) in stats.items()}
+    print("bench: per-kernel mean ms " + json.dumps({k_: round(v, 5) for k_, v in kern.items()}),
+          file=sys.stderr, flush=True)
+    gu_ms = kern.get("gemv_gateup", float("nan"))
+    dn_ms = kern.get("gemv_down", float("nan"))
+    achieved = gateup_bytes / (gu_ms * 1e-3) / 1e9
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemv_gateup_mixtral_q4k_t1_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get("bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu:
+        print(f"bench: cpu baseline on {args.cpu_tokens} tokens", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(nx, ctx, torch, x, {"router": router}, E, H, F, k, args.seed,
+                           args.cpu_tokens)
+
+    rec = {
+        "metric": METRIC,
+        "value": T / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "Mixtral-8x7B MoE layer, decode", "hidden": H, "ffn": F,
+                   "experts": E, "top_k": k, "tokens": T, "weights": "Q4_K",
+                   "path": args.path, "replicas_rotated": len(sets)},
+        "effective_GBps": step_bytes / (ms_per_step * 1e-3) / 1e9,
+        "layer_hbm_frac": step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        "kernels_ms": {k_: round(v, 5) for k_, v in kern.items()},
+        "roofline": {"bound": "hbm", "kernel": "gemv_gateup", "achieved": achieved,
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
+                     "traffic": traffic, "algorithmic_bytes": gateup_bytes},
+        "down_gemv_GBps": down_bytes / (dn_ms * 1e-3) / 1e9,
+        "cpu_baseline": cpu,
+    }
+    for s in sets:
+        s.close()
+    ctx.close()
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,160 @@
+/*
+ * nexus_hip.h — C ABI of libnexus_hip.so, the MI355X (gfx950) MoE routed-FFN
+ * path for Nexus.
+ *
+ * Plain C: pointers, sizes and int status codes only.  Every call returns
+ * NX_OK (0) or an NX_ERR_* code and, on failure, sets a thread-local message
+ * readable with nx_last_error().  Calls whose pointers are host pointers block
+ * until the result is in host memory (the reference path is synchronous);
+ * *_dev calls take device pointers and are asynchronous on the context's
+ * stream.  A context is not thread-safe: use one context per host thread.
+ *
+ * Reference interfaces replaced (paths relative to the Nexus repository):
+ *   nx_moe_forward / nx_moe_forward_dev
+ *       InferenceEngine::dispatch_moe_ffn   src/engine/mod.rs:969-1024
+ *       (row t of a batch == dispatch_moe_ffn on row t; the expert products
+ *        InferenceEngine::matvec src/engine/mod.rs:775-801 run on device)
+ *   nx_route_topk
+ *       InferenceEngine::route_moe_experts  src/engine/mod.rs:918-966
+ *   nx_permute
+ *       the per-token route loop             src/engine/mod.rs:994-1021
+ *   nx_dequant / nx_dequant_dev
+ *       GgufReader::tensor_bytes_to_f32 for Q4_0/Q8_0/Q4_K
+ *                                            src/gguf/mod.rs:962-1056
+ *       (== QuantEngine::dequantize          src/quant/mod.rs:643-849)
+ *   nx_quantize / nx_quantize_dev
+ *       QuantEngine::quantize_weights        src/quant/mod.rs:623-818
+ *   nx_experts_*
+ *       the load-time expert tensors of ModelWeights (src/engine/mod.rs:642),
+ *       kept quantized and resident in HBM instead of dequantized to f32
+ *   nx_device_count / nx_ctx_* / nx_sync / nx_mem_info
+ *       Backend::{is_available, memory_info, synchronize}
+ *                                            src/backend/mod.rs:74-96
+ *       for the HIP backend that replaces the CUDA placeholder
+ *                                            src/backend/mod.rs:206-212,221-230
+ */
+#ifndef NEXUS_HIP_H
+#define NEXUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define NX_OK 0
+#define NX_ERR_INVALID_ARG 1 /* null pointer, bad enum, negative size */
+#define NX_ERR_SHAPE 2       /* sizes inconsistent with each other */
+#define NX_ERR_UNSUPPORTED 3 /* valid request this build does not implement */
+#define NX_ERR_DEVICE 4      /* HIP runtime failure or no gfx950 device */
+#define NX_ERR_OOM 5         /* device allocation failed */
+#define NX_ERR_TRUNCATED 6   /* quantized payload shorter than its element count */
+#define NX_ERR_NO_ROUTES 7   /* router produced no route lists (k == 0, E == 0, ...) */
+
+/* weight formats: GGUF tensor type ids (src/gguf/mod.rs:106-118) */
+#define NX_FMT_F32 0
+#define NX_FMT_Q4_0 2
+#define NX_FMT_Q8_0 8
+#define NX_FMT_Q4_K 12
+
+/* router score modes */
+#define NX_SCORE_SOFTMAX 0 /* reference: softmax over the selected top-k logits */
+#define NX_SCORE_SIGMOID 1 /* extension: sigmoid scores renormalised over the top-k */
+
+/* expert-product paths */
+#define NX_PATH_AUTO 0      /* GEMV for few tokens per expert, MFMA otherwise */
+#define NX_PATH_GEMV 1      /* dequant-in-register GEMV, fp32 accumulate */
+#define NX_PATH_MFMA_F16 2  /* LDS-dequant grouped GEMM on fp16 MFMA, fp32 accumulate */
+#define NX_PATH_MFMA_BF16 3 /* same on bf16 MFMA */
+
+/* expert matrix roles */
+#define NX_ROLE_GATE 0 /* [ff_dim x hidden] */
+#define NX_ROLE_UP 1   /* [ff_dim x hidden] */
+#define NX_ROLE_DOWN 2 /* [hidden x ff_dim] */
+#define NX_EXPERT_SHARED (-1)
+
+typedef struct nx_ctx nx_ctx;
+typedef struct nx_experts nx_experts;
+
+/* ---------------------------------------------------------------- runtime */
+const char *nx_last_error(void);
+int nx_version(void);
+/* Number of visible gfx950 devices (Backend::is_available). */
+int nx_device_count(int *count);
+int nx_ctx_create(int device, nx_ctx **out);
+int nx_ctx_destroy(nx_ctx *ctx);
+/* Use a caller-owned hipStream_t (NULL restores the context's own stream). */
+int nx_ctx_set_stream(nx_ctx *ctx, void *hip_stream);
+int nx_ctx_get_stream(nx_ctx *ctx, void **hip_stream);
+int nx_sync(nx_ctx *ctx);
+int nx_mem_info(nx_ctx *ctx, size_t *free_bytes, size_t *total_bytes);
+/* Per-kernel HIP-event timing of *_dev launches (0 = off).  Stats accumulate
+ * until reset; index runs over the kernels launched so far. */
+int nx_profile_enable(nx_ctx *ctx, int enable);
+int nx_profile_reset(nx_ctx *ctx);
+int nx_profile_count(nx_ctx *ctx, int *n_kernels);
+int nx_profile_get(nx_ctx *ctx, int index, char *name, size_t name_cap, int *launches,
+                   double *total_ms);
+
+/* ---------------------------------------------------------------- quant */
+/* Payload bytes of n elements (src/gguf/mod.rs:249-293). */
+int nx_quant_bytes(int fmt, size_t n_elems, size_t *bytes);
+/* Bit-exact dequantization of a GGUF payload; n_elems = output_len. */
+int nx_dequant(nx_ctx *ctx, int fmt, const void *src, size_t src_bytes, size_t n_elems,
+               float *dst);
+int nx_dequant_dev(nx_ctx *ctx, int fmt, const void *d_src, size_t src_bytes, size_t n_elems,
+                   float *d_dst);
+/* Bit-exact restatement of the reference quantizer on device. */
+int nx_quantize(nx_ctx *ctx, int fmt, const float *src, size_t n_elems, void *dst,
+                size_t dst_bytes);
+int nx_quantize_dev(nx_ctx *ctx, int fmt, const float *d_src, size_t n_elems, void *d_dst,
+                    size_t dst_bytes);
+
+/* ---------------------------------------------------------------- routing */
+/* Top-k routing of [num_tokens x num_experts] logits.  Outputs are
+ * [num_tokens x top_k] (expert -1 / weight 0 padding) and counts[num_tokens].
+ * *lists is the number of route lists produced (tokens whose logits lie
+ * wholly inside logits_len, as in the reference). */
+int nx_route_topk(nx_ctx *ctx, const float *logits, size_t logits_len, int num_tokens,
+                  int num_experts, int top_k, int score_mode, int32_t *experts, float *weights,
+                  int32_t *counts, int *lists);
+/* Stable counting sort of (token, slot) pairs by expert: expert_counts[E],
+ * offsets[E+1], perm_token/perm_slot[sum(counts)], inv_pos[T x k] (-1 pad). */
+int nx_permute(nx_ctx *ctx, const int32_t *experts, const int32_t *counts, int num_tokens,
+               int top_k, int num_experts, int32_t *expert_counts, int32_t *offsets,
+               int32_t *perm_token, int32_t *perm_slot, int32_t *inv_pos);
+
+/* ---------------------------------------------------------------- experts */
+/* A device-resident expert set: E routed experts of [ff_dim x hidden] gate and
+ * up and [hidden x ff_dim] down in one format.  Quantized formats need the
+ * row length (hidden for gate/up, ff_dim for down) to be a whole number of
+ * blocks (256 for Q4_K, 32 for Q8_0/Q4_0). */
+int nx_experts_create(nx_ctx *ctx, int fmt, int num_experts, int hidden, int ff_dim,
+                      nx_experts **out);
+/* Adds one always-on shared expert of shared_ff_dim (weight 1, added after
+ * the routed experts). */
+int nx_experts_add_shared(nx_ctx *ctx, nx_experts *ex, int shared_ff_dim);
+/* Loads one matrix from a GGUF payload (host or device memory) into the
+ * resident layout.  expert = 0..E-1 or NX_EXPERT_SHARED. */
+int nx_experts_load(nx_ctx *ctx, nx_experts *ex, int expert, int role, const void *src,
+                    size_t src_bytes, int src_on_device);
+int nx_experts_info(const nx_experts *ex, int *fmt, int *num_experts, int *hidden, int *ff_dim,
+                    int *shared_ff_dim, size_t *device_bytes);
+int nx_experts_destroy(nx_experts *ex);
+
+/* ---------------------------------------------------------------- forward */
+/* The MoE layer for a batch: out[t] = sum_r w[t,r] * FFN_{e[t,r]}(x[t])
+ * (+ shared FFN(x[t])).  x [T x hidden], logits [T x E], out [T x hidden],
+ * fp32.  Row t equals dispatch_moe_ffn(x[t], logits[t]). */
+int nx_moe_forward(nx_ctx *ctx, const nx_experts *ex, const float *x, const float *logits,
+                   int num_tokens, int top_k, int score_mode, int path, float *out);
+int nx_moe_forward_dev(nx_ctx *ctx, const nx_experts *ex, const float *d_x,
+                       const float *d_logits, int num_tokens, int top_k, int score_mode,
+                       int path, float *d_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,292 @@
+"""nexus_amd — MI355X (gfx950) MoE routed-FFN path for Nexus.
+
+The product is ``libnexus_hip.so`` (HIP kernels behind the C ABI declared in
+``include/nexus_hip.h``).  This module is a thin ctypes binding over that ABI
+for Python callers, tests and the benchmark.  There is no CPU fallback: if the
+library is missing, ``lib()`` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libnexus_hip.so")
+ROOT = os.path.dirname(_HERE)
+
+# status codes / enums (include/nexus_hip.h)
+NX_OK = 0
+NX_ERR_INVALID_ARG, NX_ERR_SHAPE, NX_ERR_UNSUPPORTED, NX_ERR_DEVICE = 1, 2, 3, 4
+NX_ERR_OOM, NX_ERR_TRUNCATED, NX_ERR_NO_ROUTES = 5, 6, 7
+F32, Q4_0, Q8_0, Q4_K = 0, 2, 8, 12
+SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
+PATH_AUTO, PATH_GEMV, PATH_MFMA_F16, PATH_MFMA_BF16 = 0, 1, 2, 3
+ROLE_GATE, ROLE_UP, ROLE_DOWN = 0, 1, 2
+EXPERT_SHARED = -1
+FORMAT_NAMES = {F32: "F32", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K"}
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), F32: (1, 4)}
+
+# every symbol the header declares (checked by the CPU test suite)
+EXPORTS = [
+    "nx_last_error", "nx_version", "nx_device_count", "nx_ctx_create", "nx_ctx_destroy",
+    "nx_ctx_set_stream", "nx_ctx_get_stream", "nx_sync", "nx_mem_info", "nx_profile_enable",
+    "nx_profile_reset", "nx_profile_count", "nx_profile_get", "nx_quant_bytes", "nx_dequant",
+    "nx_dequant_dev", "nx_quantize", "nx_quantize_dev", "nx_route_topk", "nx_permute",
+    "nx_experts_create", "nx_experts_add_shared", "nx_experts_load", "nx_experts_info",
+    "nx_experts_destroy", "nx_moe_forward", "nx_moe_forward_dev",
+]
+
+_lib = None
+_vp = C.c_void_p
+_fp = C.POINTER(C.c_float)
+_i32p = C.POINTER(C.c_int32)
+_ip = C.POINTER(C.c_int)
+
+
+class NexusError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+def build(verbose: bool = False) -> None:
+    """Compile libnexus_hip.so for gfx950 with hipcc (always rebuilds)."""
+    cmd = ["make", "-B", "-j8", "-C", os.path.join(_HERE, "csrc")]
+    out = subprocess.run(cmd, capture_output=not verbose, text=True)
+    if out.returncode != 0:
+        raise RuntimeError("libnexus_hip.so build failed:\n" + (out.stdout or "") + (out.stderr or ""))
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: run nexus_amd.build() (there is no CPU fallback)")
+    L = C.CDLL(LIB_PATH)
+    sig = {
+        "nx_last_error": ([], C.c_char_p),
+        "nx_version": ([], C.c_int),
+        "nx_device_count": ([_ip], C.c_int),
+        "nx_ctx_create": ([C.c_int, C.POINTER(_vp)], C.c_int),
+        "nx_ctx_destroy": ([_vp], C.c_int),
+        "nx_ctx_set_stream": ([_vp, _vp], C.c_int),
+        "nx_ctx_get_stream": ([_vp, C.POINTER(_vp)], C.c_int),
+        "nx_sync": ([_vp], C.c_int),
+        "nx_mem_info": ([_vp, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)], C.c_int),
+        "nx_profile_enable": ([_vp, C.c_int], C.c_int),
+        "nx_profile_reset": ([_vp], C.c_int),
+        "nx_profile_count": ([_vp, _ip], C.c_int),
+        "nx_profile_get": ([_vp, C.c_int, C.c_char_p, C.c_size_t, _ip, C.POINTER(C.c_double)], C.c_int),
+        "nx_quant_bytes": ([C.c_int, C.c_size_t, C.POINTER(C.c_size_t)], C.c_int),
+        "nx_dequant": ([_vp, C.c_int, _vp, C.c_size_t, C.c_size_t, _fp], C.c_int),
+        "nx_dequant_dev": ([_vp, C.c_int, _vp, C.c_size_t, C.c_size_t, _vp], C.c_int),
+        "nx_quantize": ([_vp, C.c_int, _fp, C.c_size_t, _vp, C.c_size_t], C.c_int),
+        "nx_quantize_dev": ([_vp, C.c_int, _vp, C.c_size_t, _vp, C.c_size_t], C.c_int),
+        "nx_route_topk": ([_vp, _fp, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_int, _i32p, _fp,
+                           _i32p, _ip], C.c_int),
+        "nx_permute": ([_vp, _i32p, _i32p, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _i32p, _i32p,
+                        _i32p], C.c_int),
+        "nx_experts_create": ([_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(_vp)], C.c_int),
+        "nx_experts_add_shared": ([_vp, _vp, C.c_int], C.c_int),
+        "nx_experts_load": ([_vp, _vp, C.c_int, C.c_int, _vp, C.c_size_t, C.c_int], C.c_int),
+        "nx_experts_info": ([_vp, _ip, _ip, _ip, _ip, _ip, C.POINTER(C.c_size_t)], C.c_int),
+        "nx_experts_destroy": ([_vp], C.c_int),
+        "nx_moe_forward": ([_vp, _vp, _fp, _fp, C.c_int, C.c_int, C.c_int, C.c_int, _fp], C.c_int),
+        "nx_moe_forward_dev": ([_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp],
+                               C.c_int),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = L
+    return L
+
+
+def check(rc: int) -> None:
+    if rc != NX_OK:
+        raise NexusError(rc, lib().nx_last_error().decode())
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(lib().nx_device_count(C.byref(n)))
+    return n.value
+
+
+def quant_bytes(fmt: int, n: int) -> int:
+    out = C.c_size_t(0)
+    check(lib().nx_quant_bytes(fmt, n, C.byref(out)))
+    return out.value
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Context:
+    """A device context (one HIP stream).  Not thread-safe."""
+
+    def __init__(self, device: int = 0):
+        h = _vp()
+        check(lib().nx_ctx_create(device, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().nx_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ----------------------------------------------------------- runtime
+    def sync(self):
+        check(lib().nx_sync(self.h))
+
+    def set_stream(self, stream_handle: int | None):
+        check(lib().nx_ctx_set_stream(self.h, _vp(stream_handle or 0)))
+
+    def mem_info(self):
+        f, t = C.c_size_t(0), C.c_size_t(0)
+        check(lib().nx_mem_info(self.h, C.byref(f), C.byref(t)))
+        return f.value, t.value
+
+    def profile(self, enable: bool):
+        check(lib().nx_profile_enable(self.h, 1 if enable else 0))
+
+    def profile_reset(self):
+        check(lib().nx_profile_reset(self.h))
+
+    def profile_stats(self) -> dict:
+        n = C.c_int(0)
+        check(lib().nx_profile_count(self.h, C.byref(n)))
+        out = {}
+        for i in range(n.value):
+            name = C.create_string_buffer(64)
+            cnt = C.c_int(0)
+            ms = C.c_double(0)
+            check(lib().nx_profile_get(self.h, i, name, 64, C.byref(cnt), C.byref(ms)))
+            out[name.value.decode()] = (cnt.value, ms.value)
+        return out
+
+    # ----------------------------------------------------------- quant
+    def dequant(self, fmt: int, data, n: int) -> np.ndarray:
+        data = np.ascontiguousarray(data, dtype=np.uint8).ravel()
+        out = np.empty(max(n, 1), np.float32)
+        check(lib().nx_dequant(self.h, fmt, _vp(data.ctypes.data), data.size, n, _p(out, _fp)))
+        return out[:n]
+
+    def quantize(self, fmt: int, x) -> np.ndarray:
+        x = _f32(x).ravel()
+        nb = quant_bytes(fmt, x.size)
+        out = np.empty(max(nb, 1), np.uint8)
+        check(lib().nx_quantize(self.h, fmt, _p(x, _fp), x.size, _vp(out.ctypes.data), nb))
+        return out[:nb]
+
+    def dequant_dev(self, fmt: int, src_ptr: int, src_bytes: int, n: int, dst_ptr: int):
+        check(lib().nx_dequant_dev(self.h, fmt, _vp(src_ptr), src_bytes, n, _vp(dst_ptr)))
+
+    def quantize_dev(self, fmt: int, src_ptr: int, n: int, dst_ptr: int, dst_bytes: int):
+        check(lib().nx_quantize_dev(self.h, fmt, _vp(src_ptr), n, _vp(dst_ptr), dst_bytes))
+
+    # ----------------------------------------------------------- routing
+    def route_topk(self, logits, num_tokens: int, num_experts: int, top_k: int,
+                   score_mode: int = SCORE_SOFTMAX):
+        lg = _f32(logits).ravel()
+        T, k = num_tokens, top_k
+        ex = np.full((max(T, 1), max(k, 1)), -1, np.int32)
+        w = np.zeros((max(T, 1), max(k, 1)), np.float32)
+        cnt = np.zeros(max(T, 1), np.int32)
+        lists = C.c_int(0)
+        check(lib().nx_route_topk(self.h, _p(lg, _fp), lg.size, T, num_experts, k, score_mode,
+                                  _p(ex, _i32p), _p(w, _fp), _p(cnt, _i32p), C.byref(lists)))
+        return ex[:T, :k], w[:T, :k], cnt[:T], lists.value
+
+    def permute(self, experts, counts, num_experts: int):
+        ex = np.ascontiguousarray(experts, dtype=np.int32)
+        cnt = np.ascontiguousarray(counts, dtype=np.int32)
+        T, k = ex.shape
+        P = max(int(cnt.sum()), 1)
+        ec = np.zeros(num_experts, np.int32)
+        off = np.zeros(num_experts + 1, np.int32)
+        pt = np.full(P, -1, np.int32)
+        ps = np.full(P, -1, np.int32)
+        inv = np.full((max(T, 1), max(k, 1)), -1, np.int32)
+        check(lib().nx_permute(self.h, _p(ex, _i32p), _p(cnt, _i32p), T, k, num_experts,
+                               _p(ec, _i32p), _p(off, _i32p), _p(pt, _i32p), _p(ps, _i32p),
+                               _p(inv, _i32p)))
+        n = int(off[-1])
+        return ec, off, pt[:n], ps[:n], inv[:T, :k]
+
+
+class Experts:
+    """A device-resident expert set (quantized payloads kept in HBM)."""
+
+    def __init__(self, ctx: Context, fmt: int, num_experts: int, hidden: int, ff_dim: int,
+                 shared_ff_dim: int = 0):
+        h = _vp()
+        check(lib().nx_experts_create(ctx.h, fmt, num_experts, hidden, ff_dim, C.byref(h)))
+        self.h = h
+        self.ctx = ctx
+        self.fmt, self.E, self.H, self.F, self.Fs = fmt, num_experts, hidden, ff_dim, 0
+        if shared_ff_dim:
+            check(lib().nx_experts_add_shared(ctx.h, h, shared_ff_dim))
+            self.Fs = shared_ff_dim
+
+    def load(self, expert: int, role: int, payload) -> None:
+        """Load one GGUF payload (numpy uint8 array in host memory)."""
+        data = np.ascontiguousarray(payload).view(np.uint8).ravel()
+        check(lib().nx_experts_load(self.ctx.h, self.h, expert, role, _vp(data.ctypes.data),
+                                    data.size, 0))
+
+    def load_dev(self, expert: int, role: int, ptr: int, nbytes: int) -> None:
+        check(lib().nx_experts_load(self.ctx.h, self.h, expert, role, _vp(ptr), nbytes, 1))
+
+    def device_bytes(self) -> int:
+        b = C.c_size_t(0)
+        check(lib().nx_experts_info(self.h, None, None, None, None, None, C.byref(b)))
+        return b.value
+
+    def close(self):
+        if self.h:
+            lib().nx_experts_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def forward(self, x, logits, top_k: int, score_mode: int = SCORE_SOFTMAX,
+                path: int = PATH_AUTO) -> np.ndarray:
+        x = _f32(x)
+        T = x.shape[0]
+        lg = _f32(logits)
+        out = np.empty((max(T, 1), self.H), np.float32)
+        check(lib().nx_moe_forward(self.ctx.h, self.h, _p(x, _fp), _p(lg, _fp), T, top_k,
+                                   score_mode, path, _p(out, _fp)))
+        return out[:T]
+
+    def forward_dev(self, x_ptr: int, logits_ptr: int, num_tokens: int, top_k: int,
+                    out_ptr: int, score_mode: int = SCORE_SOFTMAX, path: int = PATH_AUTO):
+        check(lib().nx_moe_forward_dev(self.ctx.h, self.h, _vp(x_ptr), _vp(logits_ptr),
+                                       num_tokens, top_k, score_mode, path, _vp(out_ptr)))

@@ -1,0 +1,644 @@
+// nx_api.hip — the extern "C" boundary of libnexus_hip.so (include/nexus_hip.h).
+//
+// Validation mirrors the reference where the reference validates
+// (src/engine/mod.rs:975-991, src/gguf/mod.rs:962-1030); every device launch
+// is preceded by host-side checks that the shapes match what the kernels and
+// their grids assume.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "nx_internal.hpp"
+
+namespace nx {
+
+static thread_local std::string g_err;
+
+int fail(int code, const std::string &msg) {
+  g_err = msg;
+  return code;
+}
+void clear_error() { g_err.clear(); }
+
+bool format_info(int fmt, FormatInfo *fi) {
+  switch (fmt) {
+  case NX_FMT_Q4_K: *fi = {fmt, 256, 144, 128, 16}; return true;
+  case NX_FMT_Q8_0: *fi = {fmt, 32, 34, 32, 2}; return true;
+  case NX_FMT_Q4_0: *fi = {fmt, 32, 18, 16, 2}; return true;
+  case NX_FMT_F32: *fi = {fmt, 4, 16, 16, 0}; return true;
+  }
+  return false;
+}
+
+static const char *fmt_name(int fmt) {
+  switch (fmt) {
+  case NX_FMT_Q4_K: return "Q4_K";
+  case NX_FMT_Q8_0: return "Q8_0";
+  case NX_FMT_Q4_0: return "Q4_0";
+  case NX_FMT_F32: return "F32";
+  }
+  return "?";
+}
+
+static size_t gguf_bytes(int fmt, size_t n) {
+  switch (fmt) {
+  case NX_FMT_Q4_K: return (n + 255) / 256 * 144;
+  case NX_FMT_Q8_0: return (n + 31) / 32 * 34;
+  case NX_FMT_Q4_0: return (n + 31) / 32 * 18;
+  case NX_FMT_F32: return n * 4;
+  }
+  return 0;
+}
+
+int ws_get(nx_ctx *c, int slot, size_t bytes, void **out) {
+  DevBuf &b = c->ws[slot];
+  if (bytes == 0) bytes = 256;
+  if (b.cap < bytes) {
+    if (b.ptr) {
+      NX_HIP(hipStreamSynchronize(c->stream));
+      NX_HIP(hipFree(b.ptr));
+      b.ptr = nullptr;
+      b.cap = 0;
+    }
+    size_t cap = bytes + bytes / 4;
+    cap = (cap + 255) / 256 * 256;
+    if (hipMalloc(&b.ptr, cap) != hipSuccess) {
+      (void)hipGetLastError();
+      b.ptr = nullptr;
+      return fail(NX_ERR_OOM, "device allocation of " + std::to_string(cap) + " bytes failed");
+    }
+    b.cap = cap;
+  }
+  *out = b.ptr;
+  return NX_OK;
+}
+
+template <typename T>
+static int ws(nx_ctx *c, int slot, size_t count, T **out) {
+  void *p = nullptr;
+  NX_TRY(ws_get(c, slot, count * sizeof(T), &p));
+  *out = static_cast<T *>(p);
+  return NX_OK;
+}
+
+static int get_event(nx_ctx *c, hipEvent_t *e) {
+  if (!c->event_pool.empty()) {
+    *e = c->event_pool.back();
+    c->event_pool.pop_back();
+    return NX_OK;
+  }
+  NX_HIP(hipEventCreate(e));
+  return NX_OK;
+}
+
+int begin_launch(nx_ctx *c, const char *name, int *stat_index) {
+  *stat_index = -1;
+  if (!c->profile) return NX_OK;
+  int si = -1;
+  for (size_t i = 0; i < c->stats.size(); ++i)
+    if (c->stats[i].name == name) si = (int)i;
+  if (si < 0) {
+    c->stats.push_back(KernelStat{name, 0, 0.0});
+    si = (int)c->stats.size() - 1;
+  }
+  PendingEvent pe{si, nullptr, nullptr};
+  NX_TRY(get_event(c, &pe.start));
+  NX_TRY(get_event(c, &pe.stop));
+  NX_HIP(hipEventRecord(pe.start, c->stream));
+  c->pending.push_back(pe);
+  *stat_index = (int)c->pending.size() - 1;
+  return NX_OK;
+}
+
+int end_launch(nx_ctx *c, int pending_index) {
+  if (pending_index < 0) return NX_OK;
+  NX_HIP(hipEventRecord(c->pending[pending_index].stop, c->stream));
+  return NX_OK;
+}
+
+static int collect_profile(nx_ctx *c) {
+  if (c->pending.empty()) return NX_OK;
+  NX_HIP(hipStreamSynchronize(c->stream));
+  for (auto &pe : c->pending) {
+    float ms = 0.f;
+    NX_HIP(hipEventElapsedTime(&ms, pe.start, pe.stop));
+    c->stats[pe.stat].launches += 1;
+    c->stats[pe.stat].total_ms += ms;
+    c->event_pool.push_back(pe.start);
+    c->event_pool.push_back(pe.stop);
+  }
+  c->pending.clear();
+  return NX_OK;
+}
+
+static int set_device(nx_ctx *c) {
+  NX_HIP(hipSetDevice(c->device));
+  return NX_OK;
+}
+
+// one dense device allocation, recorded for release with the expert set
+static int ex_alloc(nx_experts *ex, size_t bytes, uint8_t **out) {
+  void *p = nullptr;
+  if (bytes == 0) bytes = 256;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(NX_ERR_OOM, "device allocation of " + std::to_string(bytes) + " bytes failed");
+  }
+  ex->allocs.push_back(p);
+  ex->device_bytes += bytes;
+  *out = static_cast<uint8_t *>(p);
+  return NX_OK;
+}
+
+static int init_plane(nx_experts *ex, RolePlane &pl, int count, int rows, int cols) {
+  FormatInfo fi;
+  format_info(ex->fmt, &fi);
+  pl.rows = rows;
+  pl.cols = cols;
+  pl.nblocks = ex->fmt == NX_FMT_F32 ? (cols + 3) / 4 : cols / fi.block;
+  pl.qs_stride = (size_t)rows * pl.nblocks * fi.qs_bytes;
+  pl.meta_stride = (size_t)rows * pl.nblocks * fi.meta_bytes;
+  // round strides to 256 B so every expert's planes start aligned
+  pl.qs_stride = (pl.qs_stride + 255) / 256 * 256;
+  pl.meta_stride = (pl.meta_stride + 255) / 256 * 256;
+  NX_TRY(ex_alloc(ex, pl.qs_stride * count, &pl.qs));
+  if (fi.meta_bytes) NX_TRY(ex_alloc(ex, pl.meta_stride * count, &pl.meta));
+  return NX_OK;
+}
+
+static int check_ctx(nx_ctx *c) {
+  if (!c) return fail(NX_ERR_INVALID_ARG, "null context");
+  return set_device(c);
+}
+
+}  // namespace nx
+
+using namespace nx;
+
+extern "C" {
+
+const char *nx_last_error(void) { return g_err.c_str(); }
+
+int nx_version(void) { return 1; }
+
+int nx_device_count(int *count) {
+  if (!count) return fail(NX_ERR_INVALID_ARG, "null count");
+  *count = 0;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return NX_OK;
+  }
+  int good = 0;
+  for (int d = 0; d < n; ++d) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, d) == hipSuccess && std::strstr(prop.gcnArchName, "gfx950"))
+      ++good;
+  }
+  *count = good;
+  return NX_OK;
+}
+
+int nx_ctx_create(int device, nx_ctx **out) {
+  if (!out) return fail(NX_ERR_INVALID_ARG, "null output pointer");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return fail(NX_ERR_DEVICE, "no HIP device available");
+  }
+  if (device < 0 || device >= n) return fail(NX_ERR_INVALID_ARG, "device index out of range");
+  hipDeviceProp_t prop;
+  NX_HIP(hipGetDeviceProperties(&prop, device));
+  if (!std::strstr(prop.gcnArchName, "gfx950"))
+    return fail(NX_ERR_DEVICE, std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950");
+  NX_HIP(hipSetDevice(device));
+  nx_ctx *c = new nx_ctx();
+  c->device = device;
+  c->num_cu = prop.multiProcessorCount;
+  if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return fail(NX_ERR_DEVICE, "hipStreamCreateWithFlags failed");
+  }
+  c->stream = c->own_stream;
+  *out = c;
+  return NX_OK;
+}
+
+int nx_ctx_destroy(nx_ctx *c) {
+  if (!c) return NX_OK;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (auto &b : c->ws)
+    if (b.ptr) (void)hipFree(b.ptr);
+  if (c->host_stage.ptr) (void)hipHostFree(c->host_stage.ptr);
+  for (auto &pe : c->pending) {
+    (void)hipEventDestroy(pe.start);
+    (void)hipEventDestroy(pe.stop);
+  }
+  for (auto e : c->event_pool) (void)hipEventDestroy(e);
+  if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+  delete c;
+  return NX_OK;
+}
+
+int nx_ctx_set_stream(nx_ctx *c, void *s) {
+  NX_TRY(check_ctx(c));
+  c->stream = s ? static_cast<hipStream_t>(s) : c->own_stream;
+  return NX_OK;
+}
+
+int nx_ctx_get_stream(nx_ctx *c, void **s) {
+  NX_TRY(check_ctx(c));
+  if (!s) return fail(NX_ERR_INVALID_ARG, "null output pointer");
+  *s = c->stream;
+  return NX_OK;
+}
+
+int nx_sync(nx_ctx *c) {
+  NX_TRY(check_ctx(c));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}
+
+int nx_mem_info(nx_ctx *c, size_t *free_b, size_t *total_b) {
+  NX_TRY(check_ctx(c));
+  size_t f = 0, t = 0;
+  NX_HIP(hipMemGetInfo(&f, &t));
+  if (free_b) *free_b = f;
+  if (total_b) *total_b = t;
+  return NX_OK;
+}
+
+int nx_profile_enable(nx_ctx *c, int enable) {
+  NX_TRY(check_ctx(c));
+  c->profile = enable != 0;
+  return NX_OK;
+}
+
+int nx_profile_reset(nx_ctx *c) {
+  NX_TRY(check_ctx(c));
+  NX_TRY(collect_profile(c));
+  c->stats.clear();
+  return NX_OK;
+}
+
+int nx_profile_count(nx_ctx *c, int *n) {
+  NX_TRY(check_ctx(c));
+  NX_TRY(collect_profile(c));
+  if (n) *n = (int)c->stats.size();
+  return NX_OK;
+}
+
+int nx_profile_get(nx_ctx *c, int index, char *name, size_t cap, int *launches, double *total_ms) {
+  NX_TRY(check_ctx(c));
+  NX_TRY(collect_profile(c));
+  if (index < 0 || index >= (int)c->stats.size()) return fail(NX_ERR_INVALID_ARG, "profile index out of range");
+  const KernelStat &s = c->stats[index];
+  if (name && cap) {
+    std::strncpy(name, s.name.c_str(), cap - 1);
+    name[cap - 1] = 0;
+  }
+  if (launches) *launches = s.launches;
+  if (total_ms) *total_ms = s.total_ms;
+  return NX_OK;
+}
+
+// ------------------------------------------------------------------- quant
+int nx_quant_bytes(int fmt, size_t n, size_t *bytes) {
+  FormatInfo fi;
+  if (!format_info(fmt, &fi)) return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
+  if (!bytes) return fail(NX_ERR_INVALID_ARG, "null output pointer");
+  *bytes = gguf_bytes(fmt, n);
+  return NX_OK;
+}
+
+int nx_dequant_dev(nx_ctx *c, int fmt, const void *src, size_t src_bytes, size_t n, float *dst) {
+  NX_TRY(check_ctx(c));
+  FormatInfo fi;
+  if (!format_info(fmt, &fi)) return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
+  if (n == 0) return NX_OK;
+  if (!src || !dst) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  if (src_bytes < gguf_bytes(fmt, n))  // src/gguf/mod.rs:966-971 and siblings
+    return fail(NX_ERR_TRUNCATED, std::string(fmt_name(fmt)) + " tensor payload is truncated");
+  return launch_dequant(c, fmt, src, n, dst);
+}
+
+int nx_dequant(nx_ctx *c, int fmt, const void *src, size_t src_bytes, size_t n, float *dst) {
+  NX_TRY(check_ctx(c));
+  FormatInfo fi;
+  if (!format_info(fmt, &fi)) return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
+  if (n == 0) return NX_OK;
+  if (!src || !dst) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  const size_t need = gguf_bytes(fmt, n);
+  if (src_bytes < need) return fail(NX_ERR_TRUNCATED, std::string(fmt_name(fmt)) + " tensor payload is truncated");
+  uint8_t *d_src = nullptr;
+  float *d_dst = nullptr;
+  NX_TRY(ws(c, WS_XIN, need, &d_src));
+  NX_TRY(ws(c, WS_OUT, n, &d_dst));
+  NX_HIP(hipMemcpyAsync(d_src, src, need, hipMemcpyHostToDevice, c->stream));
+  NX_TRY(launch_dequant(c, fmt, d_src, n, d_dst));
+  NX_HIP(hipMemcpyAsync(dst, d_dst, n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}
+
+int nx_quantize_dev(nx_ctx *c, int fmt, const float *src, size_t n, void *dst, size_t dst_bytes) {
+  NX_TRY(check_ctx(c));
+  FormatInfo fi;
+  if (!format_info(fmt, &fi)) return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
+  if (n == 0) return NX_OK;
+  if (!src || !dst) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  if (dst_bytes < gguf_bytes(fmt, n)) return fail(NX_ERR_SHAPE, "destination smaller than the quantized payload");
+  return launch_quantize(c, fmt, src, n, dst);
+}
+
+int nx_quantize(nx_ctx *c, int fmt, const float *src, size_t n, void *dst, size_t dst_bytes) {
+  NX_TRY(check_ctx(c));
+  FormatInfo fi;
+  if (!format_info(fmt, &fi)) return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
+  if (n == 0) return NX_OK;
+  if (!src || !dst) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  const size_t need = gguf_bytes(fmt, n);
+  if (dst_bytes < need) return fail(NX_ERR_SHAPE, "destination smaller than the quantized payload");
+  float *d_src = nullptr;
+  uint8_t *d_dst = nullptr;
+  NX_TRY(ws(c, WS_XIN, n, &d_src));
+  NX_TRY(ws(c, WS_OUT, need, &d_dst));
+  NX_HIP(hipMemcpyAsync(d_src, src, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+  NX_TRY(launch_quantize(c, fmt, d_src, n, d_dst));
+  NX_HIP(hipMemcpyAsync(dst, d_dst, need, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}
+
+// ------------------------------------------------------------------- routing
+int nx_route_topk(nx_ctx *c, const float *logits, size_t logits_len, int T, int E, int k,
+                  int score_mode, int32_t *experts, float *weights, int32_t *counts, int *lists) {
+  NX_TRY(check_ctx(c));
+  if (T < 0 || E < 0 || k < 0) return fail(NX_ERR_INVALID_ARG, "negative size");
+  if (score_mode != NX_SCORE_SOFTMAX && score_mode != NX_SCORE_SIGMOID)
+    return fail(NX_ERR_INVALID_ARG, "unknown score mode");
+  if (T > 0 && k > 0 && (!experts || !weights || !counts))
+    return fail(NX_ERR_INVALID_ARG, "null output buffer");
+  for (size_t i = 0; i < (size_t)T * k; ++i) {
+    experts[i] = -1;
+    weights[i] = 0.0f;
+  }
+  for (int t = 0; t < T && counts; ++t) counts[t] = 0;
+  int n = 0;
+  if (T > 0 && E > 0 && k > 0) {  // src/engine/mod.rs:924-934
+    if (!logits) return fail(NX_ERR_INVALID_ARG, "null logits");
+    n = (int)std::min<size_t>((size_t)T, logits_len / (size_t)E);
+  }
+  if (lists) *lists = n;
+  if (n == 0) return NX_OK;
+  float *d_logits;
+  int32_t *d_exp, *d_cnt;
+  float *d_w;
+  NX_TRY(ws(c, WS_LOGITS, (size_t)n * E, &d_logits));
+  NX_TRY(ws(c, WS_ROUTE_EXPERT, (size_t)n * k, &d_exp));
+  NX_TRY(ws(c, WS_ROUTE_WEIGHT, (size_t)n * k, &d_w));
+  NX_TRY(ws(c, WS_ROUTE_COUNT, (size_t)n, &d_cnt));
+  NX_HIP(hipMemcpyAsync(d_logits, logits, (size_t)n * E * 4, hipMemcpyHostToDevice, c->stream));
+  NX_TRY(launch_route(c, d_logits, n, E, k, score_mode, d_exp, d_w, d_cnt));
+  NX_HIP(hipMemcpyAsync(experts, d_exp, (size_t)n * k * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipMemcpyAsync(weights, d_w, (size_t)n * k * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipMemcpyAsync(counts, d_cnt, (size_t)n * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}
+
+int nx_permute(nx_ctx *c, const int32_t *experts, const int32_t *counts, int T, int k, int E,
+               int32_t *ecount, int32_t *offsets, int32_t *ptok, int32_t *pslot, int32_t *inv) {
+  NX_TRY(check_ctx(c));
+  if (T < 0 || k < 0 || E <= 0) return fail(NX_ERR_INVALID_ARG, "invalid sizes");
+  if (E > 1024) return fail(NX_ERR_UNSUPPORTED, "permutation supports at most 1024 experts");
+  if (T > 0 && (!experts || !counts || !inv)) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  if (!ecount || !offsets) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  // host-side validation: every listed expert in range, at most once per token
+  size_t pairs = 0;
+  std::vector<int> seen(E, -1);
+  for (int t = 0; t < T; ++t) {
+    if (counts[t] < 0 || counts[t] > k) return fail(NX_ERR_INVALID_ARG, "route count out of range");
+    for (int r = 0; r < counts[t]; ++r) {
+      const int e = experts[(size_t)t * k + r];
+      if (e < 0 || e >= E) return fail(NX_ERR_INVALID_ARG, "expert index out of range");
+      if (seen[e] == t) return fail(NX_ERR_INVALID_ARG, "expert listed twice for one token");
+      seen[e] = t;
+    }
+    pairs += counts[t];
+  }
+  if (pairs > 0 && (!ptok || !pslot)) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  int32_t *d_exp, *d_cnt, *d_ec, *d_off, *d_pt, *d_ps, *d_inv, *d_act;
+  const size_t tk = std::max<size_t>((size_t)T * k, 1);
+  NX_TRY(ws(c, WS_ROUTE_EXPERT, tk, &d_exp));
+  NX_TRY(ws(c, WS_ROUTE_COUNT, std::max(T, 1), &d_cnt));
+  NX_TRY(ws(c, WS_EXPERT_COUNT, E, &d_ec));
+  NX_TRY(ws(c, WS_OFFSETS, E + 1, &d_off));
+  NX_TRY(ws(c, WS_PERM_TOKEN, tk, &d_pt));
+  NX_TRY(ws(c, WS_PERM_SLOT, tk, &d_ps));
+  NX_TRY(ws(c, WS_INV_POS, tk, &d_inv));
+  NX_TRY(ws(c, WS_ACTIVE, E + 1, &d_act));
+  if (T > 0) {
+    NX_HIP(hipMemcpyAsync(d_exp, experts, (size_t)T * k * 4, hipMemcpyHostToDevice, c->stream));
+    NX_HIP(hipMemcpyAsync(d_cnt, counts, (size_t)T * 4, hipMemcpyHostToDevice, c->stream));
+  }
+  NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act, nullptr));
+  NX_HIP(hipMemcpyAsync(ecount, d_ec, (size_t)E * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipMemcpyAsync(offsets, d_off, (size_t)(E + 1) * 4, hipMemcpyDeviceToHost, c->stream));
+  if (pairs > 0) {
+    NX_HIP(hipMemcpyAsync(ptok, d_pt, pairs * 4, hipMemcpyDeviceToHost, c->stream));
+    NX_HIP(hipMemcpyAsync(pslot, d_ps, pairs * 4, hipMemcpyDeviceToHost, c->stream));
+  }
+  if (T > 0 && k > 0)
+    NX_HIP(hipMemcpyAsync(inv, d_inv, (size_t)T * k * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}
+
+// ------------------------------------------------------------------- experts
+int nx_experts_create(nx_ctx *c, int fmt, int E, int H, int F, nx_experts **out) {
+  NX_TRY(check_ctx(c));
+  if (!out) return fail(NX_ERR_INVALID_ARG, "null output pointer");
+  *out = nullptr;
+  FormatInfo fi;
+  if (!format_info(fmt, &fi)) return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
+  if (E <= 0) return fail(NX_ERR_INVALID_ARG, "MoE expert weight lists must be non-empty and aligned");
+  if (H <= 0 || F <= 0) return fail(NX_ERR_INVALID_ARG, "hidden and ff_dim must be positive");
+  if (fmt != NX_FMT_F32 && (H % fi.block || F % fi.block))
+    return fail(NX_ERR_UNSUPPORTED, std::string(fmt_name(fmt)) + " experts need hidden and ff_dim to be multiples of " +
+                                        std::to_string(fi.block));
+  nx_experts *ex = new nx_experts();
+  ex->ctx = c;
+  ex->fmt = fmt;
+  ex->E = E;
+  ex->H = H;
+  ex->F = F;
+  int rc = init_plane(ex, ex->role[NX_ROLE_GATE], E, F, H);
+  if (!rc) rc = init_plane(ex, ex->role[NX_ROLE_UP], E, F, H);
+  if (!rc) rc = init_plane(ex, ex->role[NX_ROLE_DOWN], E, H, F);
+  if (rc) {
+    nx_experts_destroy(ex);
+    return rc;
+  }
+  *out = ex;
+  return NX_OK;
+}
+
+int nx_experts_add_shared(nx_ctx *c, nx_experts *ex, int Fs) {
+  NX_TRY(check_ctx(c));
+  if (!ex) return fail(NX_ERR_INVALID_ARG, "null expert set");
+  if (ex->Fs) return fail(NX_ERR_INVALID_ARG, "expert set already has a shared expert");
+  FormatInfo fi;
+  format_info(ex->fmt, &fi);
+  if (Fs <= 0) return fail(NX_ERR_INVALID_ARG, "shared ff_dim must be positive");
+  if (ex->fmt != NX_FMT_F32 && Fs % fi.block)
+    return fail(NX_ERR_UNSUPPORTED, "shared ff_dim must be a multiple of the block size");
+  NX_TRY(init_plane(ex, ex->shared[NX_ROLE_GATE], 1, Fs, ex->H));
+  NX_TRY(init_plane(ex, ex->shared[NX_ROLE_UP], 1, Fs, ex->H));
+  NX_TRY(init_plane(ex, ex->shared[NX_ROLE_DOWN], 1, ex->H, Fs));
+  ex->Fs = Fs;
+  return NX_OK;
+}
+
+int nx_experts_load(nx_ctx *c, nx_experts *ex, int expert, int role, const void *src,
+                    size_t src_bytes, int on_device) {
+  NX_TRY(check_ctx(c));
+  if (!ex || !src) return fail(NX_ERR_INVALID_ARG, "null argument");
+  if (role < 0 || role > 2) return fail(NX_ERR_INVALID_ARG, "unknown role");
+  RolePlane *pl;
+  size_t qoff = 0, moff = 0;
+  if (expert == NX_EXPERT_SHARED) {
+    if (!ex->Fs) return fail(NX_ERR_INVALID_ARG, "expert set has no shared expert");
+    pl = &ex->shared[role];
+  } else {
+    if (expert < 0 || expert >= ex->E) return fail(NX_ERR_INVALID_ARG, "expert index out of range");
+    pl = &ex->role[role];
+    qoff = pl->qs_stride * expert;
+    moff = pl->meta_stride * expert;
+  }
+  const size_t n = (size_t)pl->rows * pl->cols;
+  const size_t need = gguf_bytes(ex->fmt, n);
+  if (src_bytes < need) return fail(NX_ERR_TRUNCATED, std::string(fmt_name(ex->fmt)) + " tensor payload is truncated");
+  const void *d_src = src;
+  void *tmp = nullptr;
+  if (!on_device) {
+    if (hipMalloc(&tmp, need) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(NX_ERR_OOM, "staging allocation failed");
+    }
+    hipError_t e = hipMemcpyAsync(tmp, src, need, hipMemcpyHostToDevice, c->stream);
+    if (e != hipSuccess) {
+      (void)hipFree(tmp);
+      return fail(NX_ERR_DEVICE, std::string("hipMemcpyAsync: ") + hipGetErrorString(e));
+    }
+    d_src = tmp;
+  }
+  int rc = launch_repack(c, ex->fmt, d_src, pl->rows, pl->cols, pl->qs + qoff,
+                         pl->meta ? pl->meta + moff : nullptr);
+  hipError_t e = hipStreamSynchronize(c->stream);
+  if (tmp) (void)hipFree(tmp);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(NX_ERR_DEVICE, std::string("hipStreamSynchronize: ") + hipGetErrorString(e));
+  return NX_OK;
+}
+
+int nx_experts_info(const nx_experts *ex, int *fmt, int *E, int *H, int *F, int *Fs, size_t *bytes) {
+  if (!ex) return fail(NX_ERR_INVALID_ARG, "null expert set");
+  if (fmt) *fmt = ex->fmt;
+  if (E) *E = ex->E;
+  if (H) *H = ex->H;
+  if (F) *F = ex->F;
+  if (Fs) *Fs = ex->Fs;
+  if (bytes) *bytes = ex->device_bytes;
+  return NX_OK;
+}
+
+int nx_experts_destroy(nx_experts *ex) {
+  if (!ex) return NX_OK;
+  if (ex->ctx) {
+    (void)hipSetDevice(ex->ctx->device);
+    (void)hipStreamSynchronize(ex->ctx->stream);
+  }
+  for (void *p : ex->allocs) (void)hipFree(p);
+  delete ex;
+  return NX_OK;
+}
+
+// ------------------------------------------------------------------- forward
+int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const float *d_logits,
+                       int T, int k, int score_mode, int path, float *d_out) {
+  NX_TRY(check_ctx(c));
+  if (!ex) return fail(NX_ERR_INVALID_ARG, "null expert set");
+  if (ex->ctx != c) return fail(NX_ERR_INVALID_ARG, "expert set belongs to another context");
+  if (T < 0) return fail(NX_ERR_INVALID_ARG, "negative token count");
+  if (score_mode != NX_SCORE_SOFTMAX && score_mode != NX_SCORE_SIGMOID)
+    return fail(NX_ERR_INVALID_ARG, "unknown score mode");
+  if (path < NX_PATH_AUTO || path > NX_PATH_MFMA_BF16) return fail(NX_ERR_INVALID_ARG, "unknown path");
+  if (k <= 0) return fail(NX_ERR_NO_ROUTES, "MoE router produced no routes");  // src/engine/mod.rs:989-991
+  if (T == 0) return NX_OK;
+  if (!d_x || !d_logits || !d_out) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  const int E = ex->E, H = ex->H;
+  if (E > 1024) return fail(NX_ERR_UNSUPPORTED, "at most 1024 experts");
+  if (k > 64) return fail(NX_ERR_UNSUPPORTED, "top_k above 64");
+  const bool shared = ex->Fs > 0;
+  const size_t tk = (size_t)T * k;
+  const size_t pairs_total = tk + (shared ? (size_t)T : 0);
+
+  int32_t *d_exp, *d_cnt, *d_ec, *d_off, *d_pt, *d_ps, *d_inv, *d_act;
+  float *d_w, *d_ypair;
+  NX_TRY(ws(c, WS_ROUTE_EXPERT, tk, &d_exp));
+  NX_TRY(ws(c, WS_ROUTE_WEIGHT, tk, &d_w));
+  NX_TRY(ws(c, WS_ROUTE_COUNT, (size_t)T, &d_cnt));
+  NX_TRY(ws(c, WS_EXPERT_COUNT, (size_t)E, &d_ec));
+  NX_TRY(ws(c, WS_OFFSETS, (size_t)E + 1, &d_off));
+  NX_TRY(ws(c, WS_PERM_TOKEN, tk, &d_pt));
+  NX_TRY(ws(c, WS_PERM_SLOT, tk, &d_ps));
+  NX_TRY(ws(c, WS_INV_POS, tk, &d_inv));
+  NX_TRY(ws(c, WS_ACTIVE, (size_t)E + 1, &d_act));
+  NX_TRY(ws(c, WS_YPAIR, pairs_total * H, &d_ypair));
+
+  int use = path;
+  if (use == NX_PATH_AUTO) use = NX_PATH_GEMV;
+  if (use != NX_PATH_GEMV) return fail(NX_ERR_UNSUPPORTED, "MFMA path not available in this build");
+
+  NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
+  NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act, nullptr));
+
+  const int fmax = std::max(ex->F, ex->Fs);
+  const int act_stride = (fmax + 3) / 4 * 4;
+  float *d_actv;
+  NX_TRY(ws(c, WS_ACT, pairs_total * act_stride, &d_actv));
+  GemvPlan gp{ex, T, k, d_x, d_pt, d_off, d_act, d_actv, act_stride, d_ypair};
+  NX_TRY(launch_gemv_gateup(c, gp));
+  NX_TRY(launch_gemv_down(c, gp));
+  NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out));
+  return NX_OK;
+}
+
+int nx_moe_forward(nx_ctx *c, const nx_experts *ex, const float *x, const float *logits, int T,
+                   int k, int score_mode, int path, float *out) {
+  NX_TRY(check_ctx(c));
+  if (!ex) return fail(NX_ERR_INVALID_ARG, "null expert set");
+  if (k <= 0) return fail(NX_ERR_NO_ROUTES, "MoE router produced no routes");
+  if (T < 0) return fail(NX_ERR_INVALID_ARG, "negative token count");
+  if (T == 0) return NX_OK;
+  if (!x || !logits || !out) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  const size_t nx_ = (size_t)T * ex->H, nl = (size_t)T * ex->E;
+  float *d_x, *d_l, *d_o;
+  NX_TRY(ws(c, WS_XIN, nx_, &d_x));
+  NX_TRY(ws(c, WS_LOGITS, nl, &d_l));
+  NX_TRY(ws(c, WS_OUT, nx_, &d_o));
+  NX_HIP(hipMemcpyAsync(d_x, x, nx_ * 4, hipMemcpyHostToDevice, c->stream));
+  NX_HIP(hipMemcpyAsync(d_l, logits, nl * 4, hipMemcpyHostToDevice, c->stream));
+  NX_TRY(nx_moe_forward_dev(c, ex, d_x, d_l, T, k, score_mode, path, d_o));
+  NX_HIP(hipMemcpyAsync(out, d_o, nx_ * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,187 @@
+// nx_internal.hpp — host-side internals of libnexus_hip.so (context, resident
+// expert layout, workspace, launch helpers).  Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/nexus_hip.h"
+
+namespace nx {
+
+int fail(int code, const std::string &msg);
+void clear_error();
+
+#define NX_HIP(call)                                                                       \
+  do {                                                                                     \
+    hipError_t nx_e_ = (call);                                                             \
+    if (nx_e_ != hipSuccess)                                                               \
+      return ::nx::fail(NX_ERR_DEVICE, std::string(#call) + ": " + hipGetErrorString(nx_e_)); \
+  } while (0)
+
+#define NX_TRY(expr)        \
+  do {                      \
+    int nx_rc_ = (expr);    \
+    if (nx_rc_) return nx_rc_; \
+  } while (0)
+
+// Resident per-format layout.  A GGUF block of `block` elements and
+// `block_bytes` bytes is split into a code plane (qs_bytes per block) and a
+// scale plane (meta_bytes per block) so that code loads are dense 16-byte
+// vectors.  Q4_K: 144 B = 128 B codes + 16 B {d, dmin, scales12};
+// Q8_0: 34 B = 32 B codes + 2 B d; Q4_0: 18 B = 16 B codes + 2 B d;
+// F32: 4-element "blocks" of 16 B with no scale plane.
+struct FormatInfo {
+  int fmt;
+  int block;       // elements per block
+  int block_bytes; // GGUF bytes per block
+  int qs_bytes;    // code-plane bytes per block
+  int meta_bytes;  // scale-plane bytes per block
+};
+bool format_info(int fmt, FormatInfo *fi);
+
+// One matrix role (gate / up / down) for all experts of a set:
+// expert e's codes start at qs + e * qs_stride, scales at meta + e * meta_stride.
+struct RolePlane {
+  uint8_t *qs = nullptr;
+  uint8_t *meta = nullptr;
+  size_t qs_stride = 0;
+  size_t meta_stride = 0;
+  int rows = 0;
+  int cols = 0;     // logical columns
+  int nblocks = 0;  // blocks per row (F32: ceil(cols/4))
+};
+
+struct KernelStat {
+  std::string name;
+  int launches = 0;
+  double total_ms = 0.0;
+};
+
+struct PendingEvent {
+  int stat;
+  hipEvent_t start, stop;
+};
+
+// Device scratch owned by a context; grown on demand, never shrunk.
+struct DevBuf {
+  void *ptr = nullptr;
+  size_t cap = 0;
+};
+
+}  // namespace nx
+
+struct nx_ctx {
+  int device = 0;
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  int num_cu = 0;
+  // workspace
+  nx::DevBuf ws[16];
+  // host-visible staging for blocking calls
+  nx::DevBuf host_stage;
+  // profiling
+  bool profile = false;
+  std::vector<nx::KernelStat> stats;
+  std::vector<nx::PendingEvent> pending;
+  std::vector<hipEvent_t> event_pool;
+};
+
+struct nx_experts {
+  nx_ctx *ctx = nullptr;
+  int fmt = 0;
+  int E = 0, H = 0, F = 0, Fs = 0;
+  nx::RolePlane role[3];
+  nx::RolePlane shared[3];
+  size_t device_bytes = 0;
+  std::vector<void *> allocs;
+};
+
+namespace nx {
+
+// workspace slots
+enum WsSlot {
+  WS_ROUTE_EXPERT = 0,
+  WS_ROUTE_WEIGHT,
+  WS_ROUTE_COUNT,
+  WS_EXPERT_COUNT,
+  WS_OFFSETS,
+  WS_PERM_TOKEN,
+  WS_PERM_SLOT,
+  WS_INV_POS,
+  WS_ACTIVE,   // [E + 1]: active expert ids, then n_active at index E
+  WS_ACT,      // SwiGLU activations
+  WS_YPAIR,    // per-pair expert outputs
+  WS_XIN,      // device copy of inputs for blocking calls
+  WS_LOGITS,
+  WS_OUT,
+  WS_TILES,    // grouped-GEMM tile list
+  WS_XH,       // half-precision copy of activations for the MFMA path
+};
+
+int ws_get(nx_ctx *c, int slot, size_t bytes, void **out);
+
+// Launch bookkeeping: records HIP events around `launch` when profiling.
+int begin_launch(nx_ctx *c, const char *name, int *stat_index);
+int end_launch(nx_ctx *c, int stat_index);
+
+template <typename F>
+int launch(nx_ctx *c, const char *name, F &&fn) {
+  int si = -1;
+  NX_TRY(begin_launch(c, name, &si));
+  fn();
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NX_ERR_DEVICE, std::string("launch ") + name + ": " + hipGetErrorString(e));
+  return end_launch(c, si);
+}
+
+// ---- launchers implemented in the kernel files ----
+int launch_dequant(nx_ctx *c, int fmt, const void *d_src, size_t n, float *d_dst);
+int launch_quantize(nx_ctx *c, int fmt, const float *d_src, size_t n, void *d_dst);
+int launch_repack(nx_ctx *c, int fmt, const void *d_src, int rows, int cols, uint8_t *qs,
+                  uint8_t *meta);
+
+int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
+                 int32_t *d_expert, float *d_weight, int32_t *d_count);
+int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, int T, int k,
+                   int E, int tile_m, int32_t *d_ecount, int32_t *d_offsets, int32_t *d_ptok,
+                   int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles);
+int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
+                   const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out);
+
+struct GemvPlan {
+  const nx_experts *ex;
+  int T, k;
+  const float *x;            // [T][H]
+  const int32_t *perm_token;  // [pairs]
+  const int32_t *offsets;     // [E+1]
+  const int32_t *active;      // [E] ids then n_active at [E]
+  float *act;                 // [pairs_total][act_stride]
+  int act_stride;
+  float *ypair;               // [pairs_total][H]
+};
+int launch_gemv_gateup(nx_ctx *c, const GemvPlan &p);
+int launch_gemv_down(nx_ctx *c, const GemvPlan &p);
+
+struct GemmPlan {
+  const nx_experts *ex;
+  int T, k;
+  bool bf16;
+  const float *x;
+  const int32_t *perm_token;
+  const int32_t *offsets;
+  const int32_t *active;
+  const int32_t *tiles;  // tile list from the permutation kernel
+  void *act;             // [pairs_total][act_stride] half precision
+  int act_stride;
+  float *ypair;
+  void *xh;              // [T][H] half precision copy of x
+};
+int gemm_tile_m();
+int launch_gemm_gateup(nx_ctx *c, const GemmPlan &p);
+int launch_gemm_down(nx_ctx *c, const GemmPlan &p);
+
+}  // namespace nx

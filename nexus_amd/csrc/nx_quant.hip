@@ -1,0 +1,323 @@
+// nx_quant.hip — GGUF block formats on gfx950: bit-exact dequantization,
+// a device restatement of the reference quantizer, and the repack of GGUF
+// payloads into the resident split code/scale planes.
+//
+// Dequantization (src/gguf/mod.rs:962-1056 == src/quant/mod.rs:689-849):
+// every decoded value is an exact product (Q8_0 q*d, Q4_0 (q-8)*d) or the
+// single rounding of the difference of two exact products (Q4_K d*sc*q -
+// dmin*m), so the device result is bit-identical to the reference whatever
+// the contraction.  Quantization (src/quant/mod.rs:669-818) uses IEEE
+// division, roundf (half away from zero), minNum/maxNum and hardware RNE f16
+// conversion; contraction is switched off so each expression rounds as the
+// Rust f32 expression does.
+#include "nx_device.hpp"
+#include "nx_internal.hpp"
+
+namespace nx {
+
+namespace {
+
+__device__ __forceinline__ float ld_f16(const uint8_t *p) {
+  return h2f((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+}
+
+// ---------------------------------------------------------------- dequant
+template <int FMT>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ src, size_t n,
+                                                 float *__restrict__ dst) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    float v;
+    if constexpr (FMT == NX_FMT_Q8_0) {
+      const uint8_t *b = src + (i / 32) * 34;
+      v = (float)(int8_t)b[2 + i % 32] * ld_f16(b);
+    } else if constexpr (FMT == NX_FMT_Q4_0) {
+      const uint8_t *b = src + (i / 32) * 18;
+      const int j = (int)(i % 32);
+      const int q = j < 16 ? (b[2 + j] & 15) : (b[2 + j - 16] >> 4);
+      v = (float)(q - 8) * ld_f16(b);
+    } else {  // Q4_K
+      const uint8_t *b = src + (i / 256) * 144;
+      const int j = (int)(i % 256);
+      const int s = j / 32;
+      const uint8_t *p = b + 4;
+      uint32_t sc, mn;
+      if (s < 4) {
+        sc = p[s] & 63;
+        mn = p[s + 4] & 63;
+      } else {
+        sc = (p[s + 4] & 15) | ((p[s - 4] >> 6) << 4);
+        mn = (p[s + 4] >> 4) | ((p[s] >> 6) << 4);
+      }
+      const uint8_t packed = b[16 + (j & 127)];
+      const uint32_t q = j < 128 ? (packed & 15u) : (packed >> 4);
+      v = ld_f16(b) * (float)sc * (float)q - ld_f16(b + 2) * (float)mn;
+    }
+    dst[i] = v;
+  }
+}
+
+// ---------------------------------------------------------------- quantize
+#pragma clang fp contract(off)
+
+__device__ __forceinline__ void st_f16(uint8_t *p, float v) {
+  const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
+  p[0] = (uint8_t)(h & 0xFF);
+  p[1] = (uint8_t)(h >> 8);
+}
+// Rust `as u8` / `as i8` after clamp: saturating, NaN -> 0.
+__device__ __forceinline__ uint8_t sat_u8(float v) {
+  if (!(v > 0.0f)) return 0;
+  if (v >= 255.0f) return 255;
+  return (uint8_t)v;
+}
+__device__ __forceinline__ int8_t sat_i8(float v) {
+  if (v != v) return 0;
+  if (v <= -128.0f) return -128;
+  if (v >= 127.0f) return 127;
+  return (int8_t)v;
+}
+__device__ __forceinline__ float clampf(float v, float lo, float hi) {
+  if (v < lo) v = lo;
+  if (v > hi) v = hi;
+  return v;
+}
+
+// one thread per 32-element block (src/quant/mod.rs:669-687, 705-721, 747-754)
+template <int FMT>
+__global__ __launch_bounds__(256) void k_quant32(const float *__restrict__ src, size_t n,
+                                                 uint8_t *__restrict__ dst) {
+  const size_t nb = (n + 31) / 32;
+  for (size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x; b < nb;
+       b += (size_t)gridDim.x * blockDim.x) {
+    const size_t base = b * 32;
+    const int len = (int)(n - base < 32 ? n - base : 32);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = i < len ? src[base + i] : 0.0f;
+    float max_abs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i)
+      if (i < len) max_abs = fmaxf(max_abs, fabsf(v[i]));
+    if constexpr (FMT == NX_FMT_Q8_0) {
+      uint8_t *o = dst + b * 34;
+      const float scale = max_abs > 0.0f ? max_abs / 127.0f : 0.0f;
+      st_f16(o, scale);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        int8_t q = 0;
+        if (scale > 0.0f) q = sat_i8(clampf(roundf(v[i] / scale), -128.0f, 127.0f));
+        o[2 + i] = (uint8_t)q;
+      }
+    } else {
+      uint8_t *o = dst + b * 18;
+      const float scale = max_abs > 0.0f ? max_abs / 7.0f : 0.0f;
+      st_f16(o, scale);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        uint8_t lo = 8, hi = 8;
+        if (scale > 0.0f) {
+          const float ql = clampf(roundf(v[i] / scale), -8.0f, 7.0f);
+          const float qh = clampf(roundf(v[i + 16] / scale), -8.0f, 7.0f);
+          lo = (uint8_t)((ql != ql ? 0 : (int)ql) + 8);
+          hi = (uint8_t)((qh != qh ? 0 : (int)qh) + 8);
+        }
+        o[2 + i] = (uint8_t)((lo & 15) | ((hi & 15) << 4));
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ uint8_t quantize_u6(float value, float scale) {
+  if (scale > 0.0f && value > 0.0f) return sat_u8(clampf(roundf(value / scale), 1.0f, 63.0f));
+  return 0;
+}
+__device__ __forceinline__ uint8_t q4k_value(float value, float d, float dmin, uint32_t sq,
+                                             uint32_t mq) {
+  const float scale = d * (float)sq;
+  const float offset = dmin * (float)mq;
+  if (scale > 0.0f) return sat_u8(clampf(roundf((value + offset) / scale), 0.0f, 15.0f));
+  return 0;
+}
+
+// Q4_K (src/quant/mod.rs:756-818): eight lanes per 256-element block; lane j
+// owns sub-block j for the statistics, lanes 0..3 then write the 32 code
+// bytes holding sub-blocks j (low nibbles) and j+4 (high nibbles).
+__global__ __launch_bounds__(256) void k_quant_q4k(const float *__restrict__ src, size_t n,
+                                                   uint8_t *__restrict__ dst) {
+  const size_t nb = (n + 255) / 256;
+  const int j = threadIdx.x & 7;
+  const int lane = threadIdx.x & 63;
+  // each wave owns 8 consecutive blocks per step; the loop bound is uniform
+  // across the wave so the shuffles below always see all eight lanes of a block
+  const size_t wave_id = blockIdx.x * (size_t)(blockDim.x / 64) + (threadIdx.x >> 6);
+  const size_t wave_stride = (size_t)gridDim.x * (blockDim.x / 64) * 8;
+  for (size_t wb = wave_id * 8; wb < nb; wb += wave_stride) {
+    const size_t b = wb + (size_t)(lane >> 3);
+    const bool live = b < nb;
+    const size_t base = b * 256;
+    auto val = [&](int i) -> float {
+      const size_t idx = base + (size_t)i;
+      return (live && idx < n) ? src[idx] : 0.0f;
+    };
+    float mn = INFINITY, mx = -INFINITY;
+    for (int i = 0; i < 32; ++i) mn = fminf(mn, val(j * 32 + i));
+    for (int i = 0; i < 32; ++i) mx = fmaxf(mx, val(j * 32 + i));
+    const float offset = mn < 0.0f ? -mn : 0.0f;
+    const float scale = fmaxf((mx + offset) / 15.0f, 0.0f);
+    // neither value can be NaN, so the fold order of max does not matter
+    float max_scale = scale, max_offset = offset;
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+      max_scale = fmaxf(max_scale, __shfl_xor(max_scale, m, 64));
+      max_offset = fmaxf(max_offset, __shfl_xor(max_offset, m, 64));
+    }
+    max_scale = fmaxf(0.0f, max_scale);
+    max_offset = fmaxf(0.0f, max_offset);
+    const float d = max_scale > 0.0f ? max_scale / 63.0f : 0.0f;
+    const float dmin = max_offset > 0.0f ? max_offset / 63.0f : 0.0f;
+    const uint32_t sq = quantize_u6(scale, d);
+    const uint32_t mq = quantize_u6(offset, dmin);
+    // gather the eight (scale, min) codes of the block into every lane
+    uint32_t sc[8], mi[8];
+    const int lane0 = lane & ~7;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      sc[s] = __shfl(sq, lane0 + s, 64);
+      mi[s] = __shfl(mq, lane0 + s, 64);
+    }
+    if (live) {
+      uint8_t *o = dst + b * 144;
+      if (j == 0) {
+        st_f16(o, d);
+        st_f16(o + 2, dmin);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o[4 + i] = (uint8_t)((sc[i] & 0x3F) | ((sc[i + 4] >> 4) << 6));
+          o[8 + i] = (uint8_t)((mi[i] & 0x3F) | ((mi[i + 4] >> 4) << 6));
+          o[12 + i] = (uint8_t)((sc[i + 4] & 0x0F) | ((mi[i + 4] & 0x0F) << 4));
+        }
+      }
+      if (j < 4) {
+        for (int i = 0; i < 32; ++i) {
+          const int e = j * 32 + i;
+          const uint8_t lo = q4k_value(val(e), d, dmin, sc[j], mi[j]);
+          const uint8_t hi = q4k_value(val(e + 128), d, dmin, sc[j + 4], mi[j + 4]);
+          o[16 + e] = (uint8_t)((lo & 0x0F) | ((hi & 0x0F) << 4));
+        }
+      }
+    }
+  }
+}
+
+#pragma clang fp contract(on)
+
+// ---------------------------------------------------------------- repack
+// GGUF row-major blocks -> code plane [rows][nb][qs_bytes] + scale plane
+// [rows][nb][meta_bytes].  One thread per block.
+template <int QS, int META, int BB>
+__global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ src, size_t nblocks,
+                                                uint8_t *__restrict__ qs,
+                                                uint8_t *__restrict__ meta) {
+  for (size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x; b < nblocks;
+       b += (size_t)gridDim.x * blockDim.x) {
+    const uint8_t *s = src + b * BB;
+    uint8_t *m = meta + b * META;
+    uint8_t *q = qs + b * QS;
+    // Q4_K: meta = d, dmin, scales12 (16 B); Q8_0 / Q4_0: meta = d (2 B)
+#pragma unroll
+    for (int i = 0; i < META; ++i) m[i] = s[i];
+#pragma unroll
+    for (int i = 0; i < QS; ++i) q[i] = s[META + i];
+  }
+}
+
+// F32 rows padded to a multiple of 4 floats (zero fill).
+__global__ __launch_bounds__(256) void k_repack_f32(const float *__restrict__ src, int rows,
+                                                    int cols, int stride,
+                                                    float *__restrict__ dst) {
+  const size_t total = (size_t)rows * stride;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int r = (int)(i / stride), c = (int)(i % stride);
+    dst[i] = c < cols ? src[(size_t)r * cols + c] : 0.0f;
+  }
+}
+
+unsigned grid_for(size_t items, unsigned per_block) {
+  size_t g = (items + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > 65535u * 16u) g = 65535u * 16u;
+  return (unsigned)g;
+}
+
+}  // namespace
+
+int launch_dequant(nx_ctx *c, int fmt, const void *d_src, size_t n, float *d_dst) {
+  if (n == 0) return NX_OK;
+  const uint8_t *s = static_cast<const uint8_t *>(d_src);
+  const unsigned g = grid_for(n, 256);
+  switch (fmt) {
+  case NX_FMT_Q8_0:
+    return launch(c, "dequant_q8_0", [&] { k_dequant<NX_FMT_Q8_0><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
+  case NX_FMT_Q4_0:
+    return launch(c, "dequant_q4_0", [&] { k_dequant<NX_FMT_Q4_0><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
+  case NX_FMT_Q4_K:
+    return launch(c, "dequant_q4_k", [&] { k_dequant<NX_FMT_Q4_K><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
+  case NX_FMT_F32:
+    NX_HIP(hipMemcpyAsync(d_dst, d_src, n * 4, hipMemcpyDeviceToDevice, c->stream));
+    return NX_OK;
+  }
+  return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
+}
+
+int launch_quantize(nx_ctx *c, int fmt, const float *d_src, size_t n, void *d_dst) {
+  if (n == 0) return NX_OK;
+  uint8_t *d = static_cast<uint8_t *>(d_dst);
+  switch (fmt) {
+  case NX_FMT_Q8_0: {
+    const unsigned g = grid_for((n + 31) / 32, 256);
+    return launch(c, "quantize_q8_0", [&] { k_quant32<NX_FMT_Q8_0><<<g, 256, 0, c->stream>>>(d_src, n, d); });
+  }
+  case NX_FMT_Q4_0: {
+    const unsigned g = grid_for((n + 31) / 32, 256);
+    return launch(c, "quantize_q4_0", [&] { k_quant32<NX_FMT_Q4_0><<<g, 256, 0, c->stream>>>(d_src, n, d); });
+  }
+  case NX_FMT_Q4_K: {
+    const unsigned g = grid_for((n + 255) / 256, 32);
+    return launch(c, "quantize_q4_k", [&] { k_quant_q4k<<<g, 256, 0, c->stream>>>(d_src, n, d); });
+  }
+  case NX_FMT_F32:
+    NX_HIP(hipMemcpyAsync(d_dst, d_src, n * 4, hipMemcpyDeviceToDevice, c->stream));
+    return NX_OK;
+  }
+  return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
+}
+
+int launch_repack(nx_ctx *c, int fmt, const void *d_src, int rows, int cols, uint8_t *qs,
+                  uint8_t *meta) {
+  const uint8_t *s = static_cast<const uint8_t *>(d_src);
+  if (fmt == NX_FMT_F32) {
+    const int stride = (cols + 3) / 4 * 4;
+    const unsigned g = grid_for((size_t)rows * stride, 256);
+    return launch(c, "repack_f32", [&] {
+      k_repack_f32<<<g, 256, 0, c->stream>>>(reinterpret_cast<const float *>(s), rows, cols,
+                                             stride, reinterpret_cast<float *>(qs));
+    });
+  }
+  FormatInfo fi;
+  if (!format_info(fmt, &fi)) return fail(NX_ERR_INVALID_ARG, "unknown weight format");
+  const size_t nblocks = (size_t)rows * (cols / fi.block);
+  const unsigned g = grid_for(nblocks, 256);
+  switch (fmt) {
+  case NX_FMT_Q4_K:
+    return launch(c, "repack_q4_k", [&] { k_repack<128, 16, 144><<<g, 256, 0, c->stream>>>(s, nblocks, qs, meta); });
+  case NX_FMT_Q8_0:
+    return launch(c, "repack_q8_0", [&] { k_repack<32, 2, 34><<<g, 256, 0, c->stream>>>(s, nblocks, qs, meta); });
+  case NX_FMT_Q4_0:
+    return launch(c, "repack_q4_0", [&] { k_repack<16, 2, 18><<<g, 256, 0, c->stream>>>(s, nblocks, qs, meta); });
+  }
+  return fail(NX_ERR_INVALID_ARG, "unknown weight format");
+}
+
+}  // namespace nx

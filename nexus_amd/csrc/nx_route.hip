@@ -1,0 +1,304 @@
+// nx_route.hip — top-k router, token->expert permutation and weighted combine
+// on gfx950.
+//
+// Router (InferenceEngine::route_moe_experts, src/engine/mod.rs:918-966): one
+// wavefront per token.  Each finite logit becomes a 64-bit key
+// (total-order-sortable f32 bits << 32 | ~expert), so a wave-wide max picks
+// the largest logit and, among identical bit patterns, the lowest expert
+// index — exactly the order of the reference's stable descending sort by
+// f32::total_cmp (+0.0 above -0.0).  Non-finite logits get key 0 and are never
+// selected.  k rounds of arg-max give the top-k in order; the weights are
+// exp(l - l_max) (evaluated in double and rounded once, which agrees with
+// glibc expf to the last bit except where glibc's own error exceeds half an
+// ulp), summed sequentially in route order and divided as in the reference.
+//
+// Permutation (no reference counterpart; it reorders the per-token loop of
+// src/engine/mod.rs:994): a stable counting sort of the (token, slot) pairs by
+// expert in one workgroup — LDS histogram, workgroup scan, then per chunk of
+// tokens a bit matrix [expert][token] whose popcount prefix gives each pair
+// its rank among earlier tokens of the same expert.
+//
+// Combine (src/engine/mod.rs:1018-1020): out[t] = sum over routes in route
+// order of w * y, starting from 0, with no atomics (gather by inverse
+// permutation), so the result is deterministic.
+#include "nx_device.hpp"
+#include "nx_internal.hpp"
+
+namespace nx {
+
+namespace {
+
+__device__ __forceinline__ uint32_t sortable(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float unsortable(uint32_t s) {
+  return __uint_as_float((s & 0x80000000u) ? (s & 0x7FFFFFFFu) : ~s);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
+  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, int T, int E,
+                                               int k, int score_mode,
+                                               int32_t *__restrict__ rexp,
+                                               float *__restrict__ rw,
+                                               int32_t *__restrict__ rcnt) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // wave-uniform
+  const float *row = logits + (size_t)t * E;
+  uint64_t key[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    key[i] = 0;
+    if (e < E) {
+      const float l = row[e];
+      if (isfinite(l)) key[i] = ((uint64_t)sortable(l) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+    }
+  }
+  const int kk = k < E ? k : E;
+  uint64_t mine = 0;  // lane r keeps the r-th selection
+  int n = 0;
+  for (int r = 0; r < kk; ++r) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+      const uint64_t o = shfl_xor_u64(best, m);
+      best = o > best ? o : best;
+    }
+    if (best == 0) break;  // no finite logits left (uniform across the wave)
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (key[i] == best) key[i] = 0;
+    if (lane == r) mine = best;
+    ++n;
+  }
+  float l = 0.f, w = 0.f;
+  int e = -1;
+  if (lane < n) {
+    l = unsortable((uint32_t)(mine >> 32));
+    e = (int)(0xFFFFFFFFu - (uint32_t)mine);
+  }
+  const float l0 = __shfl(l, 0, 64);  // largest selected logit
+  if (lane < n) {
+    if (score_mode == NX_SCORE_SOFTMAX) {
+      w = (float)exp((double)(l - l0));
+    } else {
+      const float ex = (float)exp(-(double)l);
+      w = 1.0f / (1.0f + ex);
+    }
+  }
+  // sequential f32 sum in route order (Iterator::sum)
+  float sum = -0.0f;
+  for (int r = 0; r < n; ++r) sum = sum + __shfl(w, r, 64);
+  if (sum > 0.0f && lane < n) w = w / sum;
+  if (lane < k) {
+    rexp[(size_t)t * k + lane] = lane < n ? e : -1;
+    rw[(size_t)t * k + lane] = lane < n ? w : 0.0f;
+  }
+  if (lane == 0) rcnt[t] = n;
+}
+
+// exclusive scan of one value per thread over a 1024-thread workgroup
+__device__ int block_exclusive_scan(int v, int *wave_tot, int *total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) wave_tot[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+      const int s = wave_tot[w];
+      wave_tot[w] = run;
+      run += s;
+    }
+    *total = run;
+  }
+  __syncthreads();
+  const int r = x - v + wave_tot[wave];
+  __syncthreads();
+  return r;
+}
+
+constexpr int PERM_THREADS = 1024;
+constexpr int PERM_WORDS = 4096;  // LDS words per bit matrix
+
+__global__ __launch_bounds__(PERM_THREADS) void k_permute(
+    const int32_t *__restrict__ rexp, const int32_t *__restrict__ rcnt, int T, int k, int E,
+    int W, int tile_m, int32_t *__restrict__ ecount, int32_t *__restrict__ offsets,
+    int32_t *__restrict__ ptok, int32_t *__restrict__ pslot, int32_t *__restrict__ inv,
+    int32_t *__restrict__ active, int32_t *__restrict__ tiles) {
+  __shared__ int cnt[PERM_THREADS];
+  __shared__ int base[PERM_THREADS];
+  __shared__ int run[PERM_THREADS];
+  __shared__ uint32_t bits[PERM_WORDS];
+  __shared__ uint32_t pref[PERM_WORDS];
+  __shared__ int wave_tot[PERM_THREADS / 64];
+  __shared__ int total;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += PERM_THREADS) cnt[e] = 0;
+  __syncthreads();
+  const int pairs = T * k;
+  for (int i = tid; i < pairs; i += PERM_THREADS) {
+    const int t = i / k, r = i - t * k;
+    if (r < rcnt[t]) atomicAdd(&cnt[rexp[i]], 1);
+  }
+  __syncthreads();
+  // E <= PERM_THREADS: one expert per thread
+  const int c = tid < E ? cnt[tid] : 0;
+  const int b = block_exclusive_scan(c, wave_tot, &total);
+  const int npairs = total;
+  if (tid < E) {
+    base[tid] = b;
+    run[tid] = 0;
+    ecount[tid] = c;
+    offsets[tid] = b;
+  }
+  if (tid == 0) offsets[E] = npairs;
+  const int act = block_exclusive_scan(tid < E && c > 0 ? 1 : 0, wave_tot, &total);
+  const int n_active = total;
+  if (tid < E && c > 0) active[act] = tid;
+  if (tid == 0) active[E] = n_active;
+  // tile list for the grouped GEMM: (expert, first row) per tile_m rows
+  if (tiles != nullptr) {
+    const int nt = tid < E ? (c + tile_m - 1) / tile_m : 0;
+    const int tb = block_exclusive_scan(nt, wave_tot, &total);
+    const int ntiles = total;
+    for (int j = 0; j < nt; ++j) {
+      tiles[2 + 2 * (tb + j)] = tid;
+      tiles[2 + 2 * (tb + j) + 1] = j * tile_m;
+    }
+    if (tid == 0) {
+      tiles[0] = ntiles;
+      tiles[1] = 0;
+    }
+  }
+  __syncthreads();
+  // ranks: chunks of CT = 32*W tokens, one token per thread
+  const int CT = 32 * W;
+  for (int t0 = 0; t0 < T; t0 += CT) {
+    for (int i = tid; i < E * W; i += PERM_THREADS) bits[i] = 0;
+    __syncthreads();
+    const int tl = tid;
+    const int t = t0 + tl;
+    const bool mine = tl < CT && t < T;
+    int nr = 0;
+    if (mine) {
+      nr = rcnt[t];
+      for (int r = 0; r < nr; ++r) {
+        const int e = rexp[(size_t)t * k + r];
+        atomicOr(&bits[e * W + (tl >> 5)], 1u << (tl & 31));
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < E * W; i += PERM_THREADS) {
+      const int e = i / W, w = i - e * W;
+      uint32_t s = 0;
+      for (int j = 0; j < w; ++j) s += __popc(bits[e * W + j]);
+      pref[i] = s;
+    }
+    __syncthreads();
+    if (mine) {
+      for (int r = 0; r < k; ++r) {
+        if (r >= nr) {
+          inv[(size_t)t * k + r] = -1;
+          continue;
+        }
+        const int e = rexp[(size_t)t * k + r];
+        const int wi = e * W + (tl >> 5);
+        const int rank = (int)pref[wi] + __popc(bits[wi] & ((1u << (tl & 31)) - 1u));
+        const int pos = base[e] + run[e] + rank;
+        inv[(size_t)t * k + r] = pos;
+        ptok[pos] = t;
+        pslot[pos] = r;
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += PERM_THREADS)
+      run[e] += (int)pref[e * W + W - 1] + __popc(bits[e * W + W - 1]);
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair,
+                                                 const float *__restrict__ rw,
+                                                 const int32_t *__restrict__ rcnt,
+                                                 const int32_t *__restrict__ inv, int T, int k,
+                                                 int H, int shared, float *__restrict__ out) {
+  const size_t total = (size_t)T * H;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int t = (int)(i / H), h = (int)(i - (size_t)t * H);
+    const int n = rcnt[t];
+    float acc = 0.0f;
+    for (int r = 0; r < n; ++r) {
+      const int p = inv[(size_t)t * k + r];
+      acc = acc + __fmul_rn(rw[(size_t)t * k + r], ypair[(size_t)p * H + h]);
+    }
+    if (shared) acc = acc + ypair[((size_t)T * k + t) * H + h];
+    out[i] = acc;
+  }
+}
+
+}  // namespace
+
+int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
+                 int32_t *d_expert, float *d_weight, int32_t *d_count) {
+  if (T <= 0) return NX_OK;
+  if (E > 1024) return fail(NX_ERR_UNSUPPORTED, "router supports at most 1024 experts");
+  if (k > 64) return fail(NX_ERR_UNSUPPORTED, "router supports top_k <= 64");
+  const unsigned g = (unsigned)((T + 3) / 4);
+  const int epl = (E + 63) / 64;
+#define NX_ROUTE(N)                                                                        \
+  return launch(c, "route_topk", [&] {                                                     \
+    k_route<N><<<g, 256, 0, c->stream>>>(d_logits, T, E, k, score_mode, d_expert, d_weight, \
+                                         d_count);                                          \
+  })
+  if (epl <= 1) NX_ROUTE(1);
+  if (epl <= 2) NX_ROUTE(2);
+  if (epl <= 4) NX_ROUTE(4);
+  if (epl <= 8) NX_ROUTE(8);
+  NX_ROUTE(16);
+#undef NX_ROUTE
+}
+
+int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, int T, int k,
+                   int E, int tile_m, int32_t *d_ecount, int32_t *d_offsets, int32_t *d_ptok,
+                   int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles) {
+  if (E > PERM_THREADS) return fail(NX_ERR_UNSUPPORTED, "permutation supports at most 1024 experts");
+  int W = PERM_WORDS / (E > 0 ? E : 1);
+  if (W > PERM_THREADS / 32) W = PERM_THREADS / 32;
+  if (W < 1) W = 1;
+  return launch(c, "permute", [&] {
+    k_permute<<<1, PERM_THREADS, 0, c->stream>>>(d_expert, d_count, T, k, E, W,
+                                                 tile_m > 0 ? tile_m : 1, d_ecount, d_offsets,
+                                                 d_ptok, d_pslot, d_inv, d_active, d_tiles);
+  });
+}
+
+int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
+                   const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out) {
+  const size_t total = (size_t)T * H;
+  if (total == 0) return NX_OK;
+  size_t g = (total + 255) / 256;
+  if (g > 65536) g = 65536;
+  return launch(c, "combine", [&] {
+    k_combine<<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H,
+                                                  shared ? 1 : 0, d_out);
+  });
+}
+
+}  // namespace nx

@@ -1,0 +1,211 @@
+"""GPU parity of the HIP path against the oracle, through the C ABI.
+
+Bars: dequantized values, quantized bytes, router indices/counts and the
+permutation bit-exact; router weights within 1 ulp (device exp vs glibc
+expf); layer outputs within relative L2 1e-4 on the fp32-accumulate GEMV path.
+"""
+import numpy as np
+import pytest
+
+import nexus_amd as nx
+import oracle
+from moe_cases import F32, Q4_0, Q4_K, Q8_0, Layer, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = nx.Context(0)
+    yield c
+    c.close()
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+# ----------------------------------------------------------------------------- quant
+def crafted(fmt, nblocks, seed):
+    from test_oracle_quant import crafted_blocks
+    return crafted_blocks(fmt, nblocks, seed)
+
+
+@pytest.mark.parametrize("fmt", [Q8_0, Q4_0, Q4_K])
+def test_dequant_bit_exact_crafted(ctx, fmt):
+    say(f"dequant crafted fmt={fmt}")
+    blk = oracle.BLOCK[fmt][0]
+    data = crafted(fmt, 512, seed=fmt + 1)
+    n = 512 * blk - 3
+    got = ctx.dequant(fmt, data, n)
+    ref = oracle.dequantize(fmt, data, n)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", [Q8_0, Q4_0, Q4_K])
+def test_dequant_bit_exact_quantized_weights(ctx, fmt):
+    rng = np.random.default_rng(fmt)
+    w = (rng.standard_normal(4096 * 1024) * 0.02).astype(np.float32)
+    q = oracle.quantize(fmt, w)
+    say(f"dequant N(0,0.02) fmt={fmt} n={w.size}")
+    got = ctx.dequant(fmt, q, w.size)
+    assert np.array_equal(got, oracle.dequantize(fmt, q, w.size))
+
+
+def test_dequant_truncated_payload_error(ctx):
+    with pytest.raises(nx.NexusError, match="^Q4_K tensor payload is truncated$") as e:
+        ctx.dequant(Q4_K, np.zeros(143, np.uint8), 256)
+    assert e.value.code == nx.NX_ERR_TRUNCATED
+    # the Q8_0 known answer (src/gguf/mod.rs:1681-1695) on the device
+    scale = np.array([0.5], np.float32).astype(np.float16).view(np.uint8)
+    block = np.concatenate([scale, (np.arange(32) - 16).astype(np.int8).view(np.uint8)])
+    v = ctx.dequant(Q8_0, block, 32)
+    assert v[0] == -8.0 and v[16] == 0.0 and v[31] == 7.5
+
+
+@pytest.mark.parametrize("fmt", [Q8_0, Q4_0, Q4_K])
+def test_quantize_bit_exact(ctx, fmt):
+    rng = np.random.default_rng(10 + fmt)
+    parts = [
+        (rng.standard_normal(256 * 2048) * 0.02).astype(np.float32),
+        rng.standard_normal(256 * 512).astype(np.float32),
+        (rng.standard_normal(256 * 64) * 1e-6).astype(np.float32),  # subnormal f16 scales
+        np.arange(300, dtype=np.float32) / np.float32(31.0) - np.float32(4.0),
+        np.zeros(256, np.float32),
+        np.full(256, 3.0, np.float32),
+        (rng.standard_normal(256 * 16) * 1e5).astype(np.float32),  # f16 overflow of scales
+    ]
+    for x in parts:
+        x = np.concatenate([x, rng.standard_normal(77).astype(np.float32)])  # ragged tail
+        say(f"quantize fmt={fmt} n={x.size}")
+        assert np.array_equal(ctx.quantize(fmt, x), oracle.quantize(fmt, x))
+
+
+# ----------------------------------------------------------------------------- router
+def router_case(rng, T, E, special=0.0):
+    lg = rng.standard_normal(T * E).astype(np.float32)
+    if special:
+        pool = np.array([0.0, -0.0, 1.0, np.nan, np.inf, -np.inf, 0.5, -1.0], np.float32)
+        m = rng.random(T * E) < special
+        lg[m] = pool[rng.integers(0, pool.size, m.sum())]
+    return lg
+
+
+@pytest.mark.parametrize("T,E,k,special", [(1, 8, 2, 0), (64, 8, 2, 0.3), (512, 128, 8, 0),
+                                           (33, 128, 8, 0.5), (4096, 256, 8, 0),
+                                           (7, 256, 8, 0.9), (5, 1000, 16, 0.2),
+                                           (9, 3, 7, 0.4), (16, 64, 64, 0.1)])
+@pytest.mark.parametrize("score", [0, 1])
+def test_router_matches_reference_order(ctx, T, E, k, special, score):
+    rng = np.random.default_rng(T * 1000 + E + k)
+    lg = router_case(rng, T, E, special)
+    say(f"router T={T} E={E} k={k} special={special} score={score}")
+    ex, w, cnt, n = ctx.route_topk(lg, T, E, k, score)
+    rex, rw, rcnt, rn = oracle.route(lg, T, E, k, score)
+    assert n == rn
+    assert np.array_equal(cnt, rcnt)
+    assert np.array_equal(ex, rex)
+    ulp = np.abs(w.view(np.int32).astype(np.int64) - rw.view(np.int32).astype(np.int64))
+    assert ulp.max() <= 1, f"max ulp {ulp.max()}"
+
+
+def test_router_reference_case_and_short_logits(ctx):
+    ex, w, cnt, n = ctx.route_topk([0.1, 3.0, 1.0, 2.0, 0.5, 0.2], 2, 3, 2)
+    assert n == 2 and ex[0].tolist() == [1, 2] and abs(float(w[0].sum()) - 1) < 1e-6
+    ex, w, cnt, n = ctx.route_topk([0.1, 3.0, 1.0, 2.0, 0.5], 2, 3, 2)  # second row cut short
+    assert n == 1 and cnt.tolist() == [2, 0] and ex[1].tolist() == [-1, -1]
+    assert ctx.route_topk([1.0, 2.0], 1, 2, 0)[3] == 0
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (32, 8, 2), (2048, 8, 2), (512, 128, 8),
+                                   (4096, 256, 8), (3000, 1000, 5), (100, 3, 3)])
+def test_permutation_bit_exact(ctx, T, E, k):
+    rng = np.random.default_rng(T + E)
+    lg = router_case(rng, T, E, 0.05)
+    ex, w, cnt, _ = oracle.route(lg, T, E, k)
+    say(f"permute T={T} E={E} k={k}")
+    got = ctx.permute(ex, cnt, E)
+    ref = oracle.permute(ex, cnt, E)
+    for g, r in zip(got, ref):
+        assert np.array_equal(g, r)
+
+
+def test_permutation_rejects_bad_routes(ctx):
+    with pytest.raises(nx.NexusError):
+        ctx.permute(np.array([[0, 0]], np.int32), np.array([2], np.int32), 4)
+    with pytest.raises(nx.NexusError):
+        ctx.permute(np.array([[0, 9]], np.int32), np.array([2], np.int32), 4)
+
+
+# ----------------------------------------------------------------------------- layer
+def run_layer(ctx, L, path=nx.PATH_GEMV):
+    ex = L.upload(nx, ctx)
+    try:
+        return ex.forward(L.x, L.logits, L.k, L.score_mode, path)
+    finally:
+        ex.close()
+
+
+@pytest.mark.parametrize("fmt,E,H,F,k,T", [
+    (F32, 8, 512, 1024, 2, 16),    # tiny F32 layer
+    (Q4_K, 8, 512, 1024, 2, 16),
+    (Q8_0, 8, 512, 1024, 2, 16),
+    (Q4_0, 8, 512, 1024, 2, 16),
+    (Q4_K, 8, 1024, 768, 2, 1),
+    (Q4_K, 16, 256, 256, 4, 37),
+    (Q8_0, 128, 256, 768, 8, 9),
+    (F32, 4, 36, 20, 3, 5),        # row lengths that are not multiples of 4
+])
+def test_layer_gemv_parity(ctx, fmt, E, H, F, k, T):
+    L = Layer(fmt, E, H, F, k, T, seed=E * 7 + H + F + T)
+    say(f"layer gemv fmt={fmt} E={E} H={H} F={F} k={k} T={T}")
+    err = rel_l2(run_layer(ctx, L), L.oracle_out())
+    assert err <= GEMV_TOL, err
+
+
+def test_layer_sigmoid_and_shared_expert(ctx):
+    L = Layer(Q4_K, 32, 512, 512, 8, 6, seed=3, shared_F=512, score_mode=1)
+    say("layer sigmoid + shared expert")
+    assert rel_l2(run_layer(ctx, L), L.oracle_out()) <= GEMV_TOL
+
+
+def test_reference_dispatch_case(ctx):
+    """src/engine/mod.rs:1632-1656 on the device: [0.18395..] x 2."""
+    ex = nx.Experts(ctx, F32, 2, 2, 2)
+    eye = np.eye(2, dtype=np.float32).ravel()
+    for e, (g, u, d) in enumerate([(eye, eye, eye), (np.full(4, 0.5), np.full(4, 0.25),
+                                                      np.full(4, 0.1))]):
+        for role, m in enumerate((g, u, d)):
+            ex.load(e, role, np.asarray(m, np.float32))
+    out = ex.forward(np.array([[1.0, 2.0]]), np.array([[0.0, 4.0]]), 1)
+    ref = oracle.dispatch_moe_ffn([1.0, 2.0], [0.0, 4.0], [eye, np.full(4, 0.5)],
+                                  [eye, np.full(4, 0.25)], [eye, np.full(4, 0.1)], 1, 2, 2)
+    np.testing.assert_allclose(out[0], ref, rtol=1e-6)
+    # all-non-finite logits: the token has no routes and its output is zero
+    out = ex.forward(np.array([[1.0, 2.0]]), np.array([[np.nan, np.inf]]), 2)
+    assert out.tolist() == [[0.0, 0.0]]
+    with pytest.raises(nx.NexusError, match="^MoE router produced no routes$"):
+        ex.forward(np.array([[1.0, 2.0]]), np.array([[0.0, 4.0]]), 0)
+    ex.close()
+
+
+def test_run_to_run_bit_identical(ctx):
+    L = Layer(Q4_K, 8, 512, 1024, 2, 24, seed=99)
+    ex = L.upload(nx, ctx)
+    a = ex.forward(L.x, L.logits, 2, path=nx.PATH_GEMV)
+    b = ex.forward(L.x, L.logits, 2, path=nx.PATH_GEMV)
+    ex.close()
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.slow
+def test_mixtral_decode_full_size(ctx):
+    """Mixtral-shaped Q4_K layer at its real size, batch 1 (only the two routed
+    experts need f32 copies for the oracle)."""
+    L = Layer(Q4_K, 8, 4096, 14336, 2, 1, seed=2024)
+    say("mixtral Q4_K T=1 full size")
+    err = rel_l2(run_layer(ctx, L), L.oracle_out())
+    say(f"  rel L2 = {err:.2e}")
+    assert err <= GEMV_TOL
