@@ -154,18 +154,32 @@ static int ex_alloc(nx_experts *ex, size_t bytes, uint8_t **out) {
 }
 
 static int init_plane(nx_experts *ex, RolePlane &pl, int count, int rows, int cols) {
-  FormatInfo fi;
-  format_info(ex->fmt, &fi);
   pl.rows = rows;
   pl.cols = cols;
-  pl.nblocks = ex->fmt == NX_FMT_F32 ? (cols + 3) / 4 : cols / fi.block;
-  pl.qs_stride = (size_t)rows * pl.nblocks * fi.qs_bytes;
-  pl.meta_stride = (size_t)rows * pl.nblocks * fi.meta_bytes;
-  // round strides to 256 B so every expert's planes start aligned
-  pl.qs_stride = (pl.qs_stride + 255) / 256 * 256;
-  pl.meta_stride = (pl.meta_stride + 255) / 256 * 256;
+  switch (ex->fmt) {
+  case NX_FMT_Q4_K:
+    pl.nseg = cols / 256 * 4;
+    pl.row_meta = (uint32_t)(cols / 256 * 16);
+    break;
+  case NX_FMT_Q8_0:
+    pl.nseg = cols / 32;
+    pl.row_meta = (uint32_t)(cols / 32 * 2);
+    break;
+  case NX_FMT_Q4_0:
+    pl.nseg = (cols / 32 + 1) / 2;
+    pl.row_meta = (uint32_t)(pl.nseg * 4);
+    break;
+  default:  // F32
+    pl.nseg = (cols + 7) / 8;
+    pl.row_meta = 0;
+    break;
+  }
+  pl.row_qs = (uint32_t)pl.nseg * 32;
+  // strides rounded to 256 B so every expert's planes start aligned
+  pl.qs_stride = ((size_t)rows * pl.row_qs + 255) / 256 * 256;
+  pl.meta_stride = ((size_t)rows * pl.row_meta + 255) / 256 * 256;
   NX_TRY(ex_alloc(ex, pl.qs_stride * count, &pl.qs));
-  if (fi.meta_bytes) NX_TRY(ex_alloc(ex, pl.meta_stride * count, &pl.meta));
+  if (pl.row_meta) NX_TRY(ex_alloc(ex, pl.meta_stride * count, &pl.meta));
   return NX_OK;
 }
 
@@ -447,7 +461,8 @@ int nx_permute(nx_ctx *c, const int32_t *experts, const int32_t *counts, int T, 
     NX_HIP(hipMemcpyAsync(d_exp, experts, (size_t)T * k * 4, hipMemcpyHostToDevice, c->stream));
     NX_HIP(hipMemcpyAsync(d_cnt, counts, (size_t)T * 4, hipMemcpyHostToDevice, c->stream));
   }
-  NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act, nullptr));
+  NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act, nullptr,
+                        nullptr, 0));
   NX_HIP(hipMemcpyAsync(ecount, d_ec, (size_t)E * 4, hipMemcpyDeviceToHost, c->stream));
   NX_HIP(hipMemcpyAsync(offsets, d_off, (size_t)(E + 1) * 4, hipMemcpyDeviceToHost, c->stream));
   if (pairs > 0) {
@@ -538,7 +553,7 @@ int nx_experts_load(nx_ctx *c, nx_experts *ex, int expert, int role, const void 
     }
     d_src = tmp;
   }
-  int rc = launch_repack(c, ex->fmt, d_src, pl->rows, pl->cols, pl->qs + qoff,
+  int rc = launch_repack(c, ex->fmt, d_src, *pl, pl->qs + qoff,
                          pl->meta ? pl->meta + moff : nullptr);
   hipError_t e = hipStreamSynchronize(c->stream);
   if (tmp) (void)hipFree(tmp);
@@ -606,17 +621,23 @@ int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const 
   if (use == NX_PATH_AUTO) use = NX_PATH_GEMV;
   if (use != NX_PATH_GEMV) return fail(NX_ERR_UNSUPPORTED, "MFMA path not available in this build");
 
-  NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
-  NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act, nullptr));
+  if (route_permute_fusable(T, E, k)) {
+    NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
+                                d_pt, d_ps, d_inv, d_act, nullptr, 0));
+  } else {
+    NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
+    NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act,
+                          nullptr, nullptr, 0));
+  }
 
   const int fmax = std::max(ex->F, ex->Fs);
-  const int act_stride = (fmax + 3) / 4 * 4;
+  const int act_stride = (fmax + 7) / 8 * 8;
   float *d_actv;
   NX_TRY(ws(c, WS_ACT, pairs_total * act_stride, &d_actv));
-  GemvPlan gp{ex, T, k, d_x, d_pt, d_off, d_act, d_actv, act_stride, d_ypair};
+  GemvPlan gp{ex, T, k, d_x, d_pt, d_off, d_act, d_actv, act_stride, d_ypair,
+              d_w, d_cnt, d_inv, d_out};
   NX_TRY(launch_gemv_gateup(c, gp));
   NX_TRY(launch_gemv_down(c, gp));
-  NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out));
   return NX_OK;
 }
 

@@ -30,10 +30,10 @@ void clear_error();
 
 // Resident per-format layout.  A GGUF block of `block` elements and
 // `block_bytes` bytes is split into a code plane (qs_bytes per block) and a
-// scale plane (meta_bytes per block) so that code loads are dense 16-byte
-// vectors.  Q4_K: 144 B = 128 B codes + 16 B {d, dmin, scales12};
-// Q8_0: 34 B = 32 B codes + 2 B d; Q4_0: 18 B = 16 B codes + 2 B d;
-// F32: 4-element "blocks" of 16 B with no scale plane.
+// scale plane (meta_bytes per block); the code plane of each row is cut into
+// 32-byte segments stored half-interleaved (nx_device.hpp).  Q4_K: 144 B =
+// 128 B codes + 16 B {d, dmin, scales12}; Q8_0: 34 B = 32 B codes + 2 B d;
+// Q4_0: 18 B = 16 B codes + 2 B d; F32: rows padded to 8 floats, no scales.
 struct FormatInfo {
   int fmt;
   int block;       // elements per block
@@ -48,11 +48,13 @@ bool format_info(int fmt, FormatInfo *fi);
 struct RolePlane {
   uint8_t *qs = nullptr;
   uint8_t *meta = nullptr;
-  size_t qs_stride = 0;
-  size_t meta_stride = 0;
+  size_t qs_stride = 0;    // bytes per expert (code plane)
+  size_t meta_stride = 0;  // bytes per expert (scale plane)
   int rows = 0;
-  int cols = 0;     // logical columns
-  int nblocks = 0;  // blocks per row (F32: ceil(cols/4))
+  int cols = 0;        // logical columns
+  int nseg = 0;        // 32-byte code segments per row
+  uint32_t row_qs = 0;    // code-plane bytes per row (nseg * 32)
+  uint32_t row_meta = 0;  // scale-plane bytes per row
 };
 
 struct KernelStat {
@@ -80,7 +82,7 @@ struct nx_ctx {
   hipStream_t stream = nullptr;
   int num_cu = 0;
   // workspace
-  nx::DevBuf ws[16];
+  nx::DevBuf ws[24];
   // host-visible staging for blocking calls
   nx::DevBuf host_stage;
   // profiling
@@ -141,14 +143,21 @@ int launch(nx_ctx *c, const char *name, F &&fn) {
 // ---- launchers implemented in the kernel files ----
 int launch_dequant(nx_ctx *c, int fmt, const void *d_src, size_t n, float *d_dst);
 int launch_quantize(nx_ctx *c, int fmt, const float *d_src, size_t n, void *d_dst);
-int launch_repack(nx_ctx *c, int fmt, const void *d_src, int rows, int cols, uint8_t *qs,
+int launch_repack(nx_ctx *c, int fmt, const void *d_src, const RolePlane &pl, uint8_t *qs,
                   uint8_t *meta);
 
 int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
                  int32_t *d_expert, float *d_weight, int32_t *d_count);
 int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, int T, int k,
                    int E, int tile_m, int32_t *d_ecount, int32_t *d_offsets, int32_t *d_ptok,
-                   int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles);
+                   int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles,
+                   int *d_counters, int n_counters);
+// router + permutation in one workgroup, for small batches
+bool route_permute_fusable(int T, int E, int k);
+int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
+                         int32_t *d_expert, float *d_weight, int32_t *d_count, int32_t *d_ecount,
+                         int32_t *d_offsets, int32_t *d_ptok, int32_t *d_pslot, int32_t *d_inv,
+                         int32_t *d_active, int *d_counters, int n_counters);
 int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
                    const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out);
 
@@ -162,6 +171,11 @@ struct GemvPlan {
   float *act;                 // [pairs_total][act_stride]
   int act_stride;
   float *ypair;               // [pairs_total][H]
+  // combine inputs for the down projection
+  const float *rw;
+  const int32_t *rcnt;
+  const int32_t *inv;
+  float *out;
 };
 int launch_gemv_gateup(nx_ctx *c, const GemvPlan &p);
 int launch_gemv_down(nx_ctx *c, const GemvPlan &p);

@@ -213,34 +213,67 @@ __global__ __launch_bounds__(256) void k_quant_q4k(const float *__restrict__ src
 #pragma clang fp contract(on)
 
 // ---------------------------------------------------------------- repack
-// GGUF row-major blocks -> code plane [rows][nb][qs_bytes] + scale plane
-// [rows][nb][meta_bytes].  One thread per block.
-template <int QS, int META, int BB>
-__global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ src, size_t nblocks,
-                                                uint8_t *__restrict__ qs,
-                                                uint8_t *__restrict__ meta) {
-  for (size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x; b < nblocks;
-       b += (size_t)gridDim.x * blockDim.x) {
-    const uint8_t *s = src + b * BB;
-    uint8_t *m = meta + b * META;
-    uint8_t *q = qs + b * QS;
-    // Q4_K: meta = d, dmin, scales12 (16 B); Q8_0 / Q4_0: meta = d (2 B)
+// GGUF row-major blocks -> resident planes (nx_device.hpp): the code plane is
+// written as 16-byte halves of 32-byte segments at their half-interleaved
+// offsets, the scale plane as {d, dmin, scales12} (Q4_K) or d (Q8_0, Q4_0).
+// One thread per 16-byte code half; byte copies because GGUF blocks are not
+// 4-byte aligned.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_repack_codes(const uint8_t *__restrict__ src, int rows,
+                                                      int cols, int nseg, uint32_t row_qs,
+                                                      uint8_t *__restrict__ qs) {
+  const size_t total = (size_t)rows * nseg * 2;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int h = (int)(i & 1);
+    const size_t rj = i >> 1;
+    const int r = (int)(rj / nseg), j = (int)(rj - (size_t)r * nseg);
+    uint8_t *dst = qs + (size_t)r * row_qs + seg_off(j, h, nseg);
+    if constexpr (FMT == NX_FMT_F32) {
+      const float *sf = reinterpret_cast<const float *>(src) + (size_t)r * cols;
+      float *df = reinterpret_cast<float *>(dst);
 #pragma unroll
-    for (int i = 0; i < META; ++i) m[i] = s[i];
+      for (int v = 0; v < 4; ++v) {
+        const int c = 8 * j + 4 * h + v;
+        df[v] = c < cols ? sf[c] : 0.0f;
+      }
+    } else {
+      const uint8_t *b = nullptr;
+      if constexpr (FMT == NX_FMT_Q4_K) {
+        const int nb = cols / 256;
+        b = src + ((size_t)r * nb + (j >> 2)) * 144 + 16 + (j & 3) * 32 + h * 16;
+      } else if constexpr (FMT == NX_FMT_Q8_0) {
+        const int nb = cols / 32;
+        b = src + ((size_t)r * nb + j) * 34 + 2 + h * 16;
+      } else {  // Q4_0: segment j = blocks 2j, 2j+1
+        const int nb = cols / 32;
+        const int blk = 2 * j + h;
+        if (blk < nb) b = src + ((size_t)r * nb + blk) * 18 + 2;
+      }
 #pragma unroll
-    for (int i = 0; i < QS; ++i) q[i] = s[META + i];
+      for (int v = 0; v < 16; ++v) dst[v] = b ? b[v] : (uint8_t)0;
+    }
   }
 }
 
-// F32 rows padded to a multiple of 4 floats (zero fill).
-__global__ __launch_bounds__(256) void k_repack_f32(const float *__restrict__ src, int rows,
-                                                    int cols, int stride,
-                                                    float *__restrict__ dst) {
-  const size_t total = (size_t)rows * stride;
+template <int FMT>
+__global__ __launch_bounds__(256) void k_repack_meta(const uint8_t *__restrict__ src, int rows,
+                                                     int cols, int nseg, uint32_t row_meta,
+                                                     uint8_t *__restrict__ meta) {
+  constexpr int BLK = FMT == NX_FMT_Q4_K ? 256 : 32;
+  constexpr int BB = FMT == NX_FMT_Q4_K ? 144 : (FMT == NX_FMT_Q8_0 ? 34 : 18);
+  constexpr int MB = FMT == NX_FMT_Q4_K ? 16 : 2;
+  const int nb = cols / BLK;
+  // Q4_0 rows are padded to an even block count (two blocks per segment)
+  const int slots = FMT == NX_FMT_Q4_0 ? 2 * nseg : nb;
+  const size_t total = (size_t)rows * slots;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
-    const int r = (int)(i / stride), c = (int)(i % stride);
-    dst[i] = c < cols ? src[(size_t)r * cols + c] : 0.0f;
+    const int r = (int)(i / slots), b = (int)(i - (size_t)r * slots);
+    uint8_t *dst = meta + (size_t)r * row_meta + (size_t)b * MB;
+    const uint8_t *s = b < nb ? src + ((size_t)r * nb + b) * BB : nullptr;
+#pragma unroll
+    for (int v = 0; v < MB; ++v) dst[v] = s ? s[v] : (uint8_t)0;
   }
 }
 
@@ -294,29 +327,30 @@ int launch_quantize(nx_ctx *c, int fmt, const float *d_src, size_t n, void *d_ds
   return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
 }
 
-int launch_repack(nx_ctx *c, int fmt, const void *d_src, int rows, int cols, uint8_t *qs,
+int launch_repack(nx_ctx *c, int fmt, const void *d_src, const RolePlane &pl, uint8_t *qs,
                   uint8_t *meta) {
   const uint8_t *s = static_cast<const uint8_t *>(d_src);
-  if (fmt == NX_FMT_F32) {
-    const int stride = (cols + 3) / 4 * 4;
-    const unsigned g = grid_for((size_t)rows * stride, 256);
-    return launch(c, "repack_f32", [&] {
-      k_repack_f32<<<g, 256, 0, c->stream>>>(reinterpret_cast<const float *>(s), rows, cols,
-                                             stride, reinterpret_cast<float *>(qs));
-    });
-  }
-  FormatInfo fi;
-  if (!format_info(fmt, &fi)) return fail(NX_ERR_INVALID_ARG, "unknown weight format");
-  const size_t nblocks = (size_t)rows * (cols / fi.block);
-  const unsigned g = grid_for(nblocks, 256);
+  const unsigned gc = grid_for((size_t)pl.rows * pl.nseg * 2, 256);
+  const unsigned gm = grid_for((size_t)pl.rows * (size_t)(pl.row_meta ? pl.row_meta : 1), 256);
+#define NX_RP(F, NAME)                                                                          \
+  do {                                                                                          \
+    NX_TRY(launch(c, NAME, [&] {                                                                \
+      k_repack_codes<F><<<gc, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_qs, qs); \
+    }));                                                                                        \
+    if (F != NX_FMT_F32)                                                                        \
+      NX_TRY(launch(c, NAME, [&] {                                                              \
+        k_repack_meta<F><<<gm, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_meta, \
+                                                    meta);                                      \
+      }));                                                                                      \
+    return NX_OK;                                                                               \
+  } while (0)
   switch (fmt) {
-  case NX_FMT_Q4_K:
-    return launch(c, "repack_q4_k", [&] { k_repack<128, 16, 144><<<g, 256, 0, c->stream>>>(s, nblocks, qs, meta); });
-  case NX_FMT_Q8_0:
-    return launch(c, "repack_q8_0", [&] { k_repack<32, 2, 34><<<g, 256, 0, c->stream>>>(s, nblocks, qs, meta); });
-  case NX_FMT_Q4_0:
-    return launch(c, "repack_q4_0", [&] { k_repack<16, 2, 18><<<g, 256, 0, c->stream>>>(s, nblocks, qs, meta); });
+  case NX_FMT_Q4_K: NX_RP(NX_FMT_Q4_K, "repack_q4_k");
+  case NX_FMT_Q8_0: NX_RP(NX_FMT_Q8_0, "repack_q8_0");
+  case NX_FMT_Q4_0: NX_RP(NX_FMT_Q4_0, "repack_q4_0");
+  case NX_FMT_F32: NX_RP(NX_FMT_F32, "repack_f32");
   }
+#undef NX_RP
   return fail(NX_ERR_INVALID_ARG, "unknown weight format");
 }
 

@@ -42,16 +42,12 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// Routes one token with one wavefront.  On return lane r < *n holds the r-th
+// route (expert *e, weight *w); lanes >= *n hold e = -1, w = 0.
 template <int EPL>
-__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, int T, int E,
-                                               int k, int score_mode,
-                                               int32_t *__restrict__ rexp,
-                                               float *__restrict__ rw,
-                                               int32_t *__restrict__ rcnt) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;  // wave-uniform
-  const float *row = logits + (size_t)t * E;
+__device__ __forceinline__ void route_one(const float *__restrict__ row, int E, int k,
+                                          int score_mode, int lane, int *e_out, float *w_out,
+                                          int *n_out) {
   uint64_t key[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
@@ -100,9 +96,26 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
   float sum = -0.0f;
   for (int r = 0; r < n; ++r) sum = sum + __shfl(w, r, 64);
   if (sum > 0.0f && lane < n) w = w / sum;
+  *e_out = e;
+  *w_out = w;
+  *n_out = n;
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits, int T, int E,
+                                               int k, int score_mode,
+                                               int32_t *__restrict__ rexp,
+                                               float *__restrict__ rw,
+                                               int32_t *__restrict__ rcnt) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // wave-uniform
+  int e, n;
+  float w;
+  route_one<EPL>(logits + (size_t)t * E, E, k, score_mode, lane, &e, &w, &n);
   if (lane < k) {
-    rexp[(size_t)t * k + lane] = lane < n ? e : -1;
-    rw[(size_t)t * k + lane] = lane < n ? w : 0.0f;
+    rexp[(size_t)t * k + lane] = e;
+    rw[(size_t)t * k + lane] = w;
   }
   if (lane == 0) rcnt[t] = n;
 }
@@ -140,7 +153,8 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
     const int32_t *__restrict__ rexp, const int32_t *__restrict__ rcnt, int T, int k, int E,
     int W, int tile_m, int32_t *__restrict__ ecount, int32_t *__restrict__ offsets,
     int32_t *__restrict__ ptok, int32_t *__restrict__ pslot, int32_t *__restrict__ inv,
-    int32_t *__restrict__ active, int32_t *__restrict__ tiles) {
+    int32_t *__restrict__ active, int32_t *__restrict__ tiles, int *__restrict__ counters,
+    int n_counters) {
   __shared__ int cnt[PERM_THREADS];
   __shared__ int base[PERM_THREADS];
   __shared__ int run[PERM_THREADS];
@@ -149,6 +163,7 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
   __shared__ int wave_tot[PERM_THREADS / 64];
   __shared__ int total;
   const int tid = threadIdx.x;
+  for (int i = tid; i < n_counters; i += PERM_THREADS) counters[i] = 0;
   for (int e = tid; e < E; e += PERM_THREADS) cnt[e] = 0;
   __syncthreads();
   const int pairs = T * k;
@@ -233,6 +248,70 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
   }
 }
 
+// Router and permutation in one workgroup of 256 threads for small batches
+// (T*k <= 256, E <= 256): each wave routes tokens wave, wave+4, ...; then
+// thread e counts expert e's pairs, the workgroup scans the counts, and
+// thread e assigns its pairs their positions in (token, slot) order.
+constexpr int RP_MAX_PAIRS = 256;
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_route_permute(
+    const float *__restrict__ logits, int T, int E, int k, int score_mode,
+    int32_t *__restrict__ rexp, float *__restrict__ rw, int32_t *__restrict__ rcnt,
+    int32_t *__restrict__ ecount, int32_t *__restrict__ offsets, int32_t *__restrict__ ptok,
+    int32_t *__restrict__ pslot, int32_t *__restrict__ inv, int32_t *__restrict__ active,
+    int *__restrict__ counters, int n_counters) {
+  __shared__ int s_exp[RP_MAX_PAIRS];
+  __shared__ int s_cnt[RP_MAX_PAIRS];
+  __shared__ int wave_tot[PERM_THREADS / 64];
+  __shared__ int total;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i < n_counters; i += 256) counters[i] = 0;
+  for (int t = wave; t < T; t += 4) {
+    int e, n;
+    float w;
+    route_one<EPL>(logits + (size_t)t * E, E, k, score_mode, lane, &e, &w, &n);
+    if (lane < k) {
+      rexp[(size_t)t * k + lane] = e;
+      rw[(size_t)t * k + lane] = w;
+      s_exp[t * k + lane] = e;
+      inv[(size_t)t * k + lane] = -1;
+    }
+    if (lane == 0) {
+      rcnt[t] = n;
+      s_cnt[t] = n;
+    }
+  }
+  __syncthreads();
+  int c = 0;
+  if (tid < E) {
+    for (int t = 0; t < T; ++t)
+      for (int r = 0; r < s_cnt[t]; ++r) c += s_exp[t * k + r] == tid;
+  }
+  const int b = block_exclusive_scan(c, wave_tot, &total);
+  const int npairs = total;
+  const int act = block_exclusive_scan(tid < E && c > 0 ? 1 : 0, wave_tot, &total);
+  const int n_active = total;
+  if (tid < E) {
+    ecount[tid] = c;
+    offsets[tid] = b;
+    if (c > 0) active[act] = tid;
+    int pos = b;
+    for (int t = 0; t < T && pos < b + c; ++t)
+      for (int r = 0; r < s_cnt[t]; ++r)
+        if (s_exp[t * k + r] == tid) {
+          ptok[pos] = t;
+          pslot[pos] = r;
+          inv[(size_t)t * k + r] = pos;
+          ++pos;
+        }
+  }
+  if (tid == 0) {
+    offsets[E] = npairs;
+    active[E] = n_active;
+  }
+}
+
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair,
                                                  const float *__restrict__ rw,
                                                  const int32_t *__restrict__ rcnt,
@@ -277,7 +356,8 @@ int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int scor
 
 int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, int T, int k,
                    int E, int tile_m, int32_t *d_ecount, int32_t *d_offsets, int32_t *d_ptok,
-                   int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles) {
+                   int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles,
+                   int *d_counters, int n_counters) {
   if (E > PERM_THREADS) return fail(NX_ERR_UNSUPPORTED, "permutation supports at most 1024 experts");
   int W = PERM_WORDS / (E > 0 ? E : 1);
   if (W > PERM_THREADS / 32) W = PERM_THREADS / 32;
@@ -285,8 +365,32 @@ int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, i
   return launch(c, "permute", [&] {
     k_permute<<<1, PERM_THREADS, 0, c->stream>>>(d_expert, d_count, T, k, E, W,
                                                  tile_m > 0 ? tile_m : 1, d_ecount, d_offsets,
-                                                 d_ptok, d_pslot, d_inv, d_active, d_tiles);
+                                                 d_ptok, d_pslot, d_inv, d_active, d_tiles,
+                                                 d_counters, d_counters ? n_counters : 0);
   });
+}
+
+bool route_permute_fusable(int T, int E, int k) {
+  return T >= 1 && (long)T * k <= RP_MAX_PAIRS && E <= 256 && k <= 64;
+}
+
+int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
+                         int32_t *d_expert, float *d_weight, int32_t *d_count, int32_t *d_ecount,
+                         int32_t *d_offsets, int32_t *d_ptok, int32_t *d_pslot, int32_t *d_inv,
+                         int32_t *d_active, int *d_counters, int n_counters) {
+  if (!route_permute_fusable(T, E, k)) return fail(NX_ERR_UNSUPPORTED, "batch too large for the fused router");
+  const int epl = (E + 63) / 64;
+  const int nc = d_counters ? n_counters : 0;
+#define NX_RP(N)                                                                              \
+  return launch(c, "route_permute", [&] {                                                     \
+    k_route_permute<N><<<1, 256, 0, c->stream>>>(d_logits, T, E, k, score_mode, d_expert,     \
+                                                 d_weight, d_count, d_ecount, d_offsets, d_ptok, \
+                                                 d_pslot, d_inv, d_active, d_counters, nc);    \
+  })
+  if (epl <= 1) NX_RP(1);
+  if (epl <= 2) NX_RP(2);
+  NX_RP(4);
+#undef NX_RP
 }
 
 int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,

@@ -81,3 +81,17 @@ def rel_l2(got, ref) -> float:
     ref = np.asarray(ref, np.float64)
     den = np.linalg.norm(ref)
     return float(np.linalg.norm(got - ref) / (den if den > 0 else 1.0))
+
+
+def assert_same_bits(got, ref):
+    """Bit-for-bit equality of every non-NaN value and identical NaN positions.
+    NaN payloads are not compared: x86 and gfx950 differ in the payload they
+    give an invalid operation (x86's default NaN has the sign bit set)."""
+    got = np.asarray(got, np.float32).ravel()
+    ref = np.asarray(ref, np.float32).ravel()
+    assert got.shape == ref.shape
+    gn, rn = np.isnan(got), np.isnan(ref)
+    assert np.array_equal(gn, rn), f"NaN positions differ at {np.nonzero(gn != rn)[0][:8]}"
+    bad = np.nonzero(got[~gn].view(np.uint32) != ref[~rn].view(np.uint32))[0]
+    assert bad.size == 0, (f"{bad.size} values differ; first at {bad[:4]}: "
+                           f"{got[~gn][bad[:4]]} vs {ref[~rn][bad[:4]]}")

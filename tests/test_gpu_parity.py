@@ -1,7 +1,7 @@
 """GPU parity of the HIP path against the oracle, through the C ABI.
 
 Bars: dequantized values, quantized bytes, router indices/counts and the
-permutation bit-exact; router weights within 1 ulp (device exp vs glibc
+permutation bit-exact; router weights within 2 ulp (device exp vs glibc
 expf); layer outputs within relative L2 1e-4 on the fp32-accumulate GEMV path.
 """
 import numpy as np
@@ -9,7 +9,7 @@ import pytest
 
 import nexus_amd as nx
 import oracle
-from moe_cases import F32, Q4_0, Q4_K, Q8_0, Layer, rel_l2
+from moe_cases import F32, Q4_0, Q4_K, Q8_0, Layer, assert_same_bits, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -41,7 +41,7 @@ def test_dequant_bit_exact_crafted(ctx, fmt):
     n = 512 * blk - 3
     got = ctx.dequant(fmt, data, n)
     ref = oracle.dequantize(fmt, data, n)
-    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert_same_bits(got, ref)
 
 
 @pytest.mark.parametrize("fmt", [Q8_0, Q4_0, Q4_K])
@@ -51,7 +51,7 @@ def test_dequant_bit_exact_quantized_weights(ctx, fmt):
     q = oracle.quantize(fmt, w)
     say(f"dequant N(0,0.02) fmt={fmt} n={w.size}")
     got = ctx.dequant(fmt, q, w.size)
-    assert np.array_equal(got, oracle.dequantize(fmt, q, w.size))
+    assert_same_bits(got, oracle.dequantize(fmt, q, w.size))
 
 
 def test_dequant_truncated_payload_error(ctx):
@@ -107,8 +107,11 @@ def test_router_matches_reference_order(ctx, T, E, k, special, score):
     assert n == rn
     assert np.array_equal(cnt, rcnt)
     assert np.array_equal(ex, rex)
+    # weights: exp() on the device is not glibc's expf; a 1-ulp difference in
+    # one exp also moves the sum, so each normalised weight is within 2 ulp
     ulp = np.abs(w.view(np.int32).astype(np.int64) - rw.view(np.int32).astype(np.int64))
-    assert ulp.max() <= 1, f"max ulp {ulp.max()}"
+    assert ulp.max() <= 2, f"max ulp {ulp.max()}"
+    assert np.count_nonzero(ulp) <= max(2, 0.02 * ulp.size)
 
 
 def test_router_reference_case_and_short_logits(ctx):
