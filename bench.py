@@ -44,6 +44,13 @@ def parse():
     p.add_argument("--path", default="gemv", choices=["auto", "gemv", "mfma_f16", "mfma_bf16"])
     p.add_argument("--cpu-tokens", type=int, default=16, help="tokens in the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-extra", action="store_true",
+                   help="skip the 32-token decode and 2048-token prefill measurements")
+    p.add_argument("--prefill-steps", type=int, default=20)
+    p.add_argument("--prefill-path", default="mfma_f16", choices=["mfma_f16", "mfma_bf16"])
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="run one device-to-device copy of this size first (calibrates HBM "
+                        "byte counters under rocprofv3 --pmc)")
     p.add_argument("--seed", type=int, default=0)
     return p.parse_args()
 
@@ -109,12 +116,80 @@ def cpu_baseline(nx, ctx, torch, x, logits, E, H, F, k, seed, ntok):
                       f"Q4_K payloads outside the timed region), {dt:.1f} s"}
 
 
+def time_steps(torch, fn, steps, warmup):
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def kernel_means(ctx, torch, fn, steps):
+    """Mean duration per kernel (HIP events on the launch stream) over `steps` steps."""
+    ctx.profile(True)
+    ctx.profile_reset()
+    torch.cuda.synchronize()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    stats = ctx.profile_stats()
+    ctx.profile(False)
+    return {name: ms / max(n, 1) for name, (n, ms) in stats.items()}
+
+
+def active_experts(ctx, logits_np, T, E, k):
+    ex_ids, _, cnt, _ = ctx.route_topk(logits_np, T, E, k)
+    counts = [0] * E
+    for t in range(T):
+        for e in ex_ids[t, :cnt[t]]:
+            counts[int(e)] += 1
+    return counts
+
+
+def prefill(nx, ctx, torch, args):
+    """Mixtral-shaped Q8_0 layer, 2048 tokens, Zipf(1.2)-biased router, MFMA path."""
+    import math
+    E, H, F, k, T = 8, 4096, 14336, 2, 2048
+    dev = torch.device("cuda", 0)
+    ex = make_expert_sets(nx, ctx, torch, nx.Q8_0, E, H, F, 1, args.seed + 7)[0]
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 11)
+    x = torch.randn((T, H), generator=g, device=dev, dtype=torch.float32)
+    router = torch.randn((E, H), generator=g, device=dev, dtype=torch.float32) * 0.02
+    p = torch.tensor([(e + 1) ** -1.2 for e in range(E)], device=dev, dtype=torch.float64)
+    bias = torch.log(p / p.sum()).to(torch.float32)
+    logits = (x @ router.t() + bias[None, :]).contiguous()
+    out = torch.empty((T, H), device=dev, dtype=torch.float32)
+    counts = active_experts(ctx, logits.cpu().numpy(), T, E, k)
+    flops = 2.0 * 3 * H * F * sum(counts)
+    path = nx.PATH_MFMA_F16 if args.prefill_path == "mfma_f16" else nx.PATH_MFMA_BF16
+
+    def step(i):
+        ex.forward_dev(x.data_ptr(), logits.data_ptr(), T, k, out.data_ptr(), path=path)
+
+    ms = time_steps(torch, step, args.prefill_steps, 3)
+    kern = kernel_means(ctx, torch, step, args.prefill_steps)
+    gemm_ms = kern.get("gemm_gateup", 0.0) + kern.get("gemm_down", 0.0)
+    ex.close()
+    return {
+        "workload": "Mixtral-8x7B MoE layer, prefill, Q8_0, Zipf(1.2) router",
+        "tokens": T, "path": args.prefill_path, "expert_tokens": counts,
+        "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
+        "layer_TFLOPs": flops / (ms * 1e-3) / 1e12,
+        "gemm_TFLOPs": flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None,
+        "gemm_frac_of_fp16_peak": flops / (gemm_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS if gemm_ms else None,
+        "kernels_ms": {k_: round(v, 4) for k_, v in kern.items()},
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
         sys.exit(2)
-    import numpy as np
     import torch
 
     import nexus_amd as nx
@@ -131,57 +206,60 @@ def main():
     torch.cuda.set_stream(stream)
     ctx.set_stream(stream.cuda_stream)
 
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     print(f"bench: building {args.replicas} Q4_K expert replicas (E={E} H={H} F={F})",
           file=sys.stderr, flush=True)
     sets = make_expert_sets(nx, ctx, torch, nx.Q4_K, E, H, F, args.replicas, args.seed)
     g = torch.Generator(device=dev)
     g.manual_seed(args.seed + 1)
-    x = torch.randn((T, H), generator=g, device=dev, dtype=torch.float32)
+    x = torch.randn((max(T, 32), H), generator=g, device=dev, dtype=torch.float32)
     router = torch.randn((E, H), generator=g, device=dev, dtype=torch.float32) * 0.02
     logits = (x @ router.t()).contiguous()
-    out = torch.empty((T, H), device=dev, dtype=torch.float32)
+    out = torch.empty((max(T, 32), H), device=dev, dtype=torch.float32)
 
-    # realised routing -> algorithmic bytes
-    ex_ids, w, cnt, _ = ctx.route_topk(logits.cpu().numpy(), T, E, k)
-    active = sorted({int(e) for t in range(T) for e in ex_ids[t, :cnt[t]]})
-    n_act = len(active)
-    gateup_bytes = n_act * 2 * F * H * Q4K_BYTES_PER_WEIGHT
-    down_bytes = n_act * H * F * Q4K_BYTES_PER_WEIGHT
+    def decode_case(ntok, pth):
+        counts = active_experts(ctx, logits[:ntok].cpu().numpy(), ntok, E, k)
+        n_act = sum(1 for c in counts if c)
+        gu_bytes = n_act * 2 * F * H * Q4K_BYTES_PER_WEIGHT
+        dn_bytes = n_act * H * F * Q4K_BYTES_PER_WEIGHT
+
+        def step(i):
+            sets[i % len(sets)].forward_dev(x.data_ptr(), logits.data_ptr(), ntok, k,
+                                            out.data_ptr(), path=pth)
+
+        ms = time_steps(torch, step, args.steps, args.warmup)
+        kern = kernel_means(ctx, torch, step, args.steps)
+        return ms, kern, gu_bytes, dn_bytes
+
+    print("bench: decode", file=sys.stderr, flush=True)
+    ms_per_step, kern, gateup_bytes, down_bytes = decode_case(T, path)
     step_bytes = gateup_bytes + down_bytes
-
-    def step(i):
-        sets[i % len(sets)].forward_dev(x.data_ptr(), logits.data_ptr(), T, k, out.data_ptr(),
-                                        path=path)
-
-    print("bench: warmup", file=sys.stderr, flush=True)
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # timed region (value): K steps, no per-kernel events
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    ms_per_step = dt * 1e3 / args.steps
-
-    # timed region (roofline): same K steps with HIP events around every launch
-    ctx.profile(True)
-    ctx.profile_reset()
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        step(i)
-    torch.cuda.synchronize()
-    stats = ctx.profile_stats()
-    ctx.profile(False)
-    kern = {name: ms / max(n, 1) for name, (n, ms) in stats.items()}
     print("bench: per-kernel mean ms " + json.dumps({k_: round(v, 5) for k_, v in kern.items()}),
           file=sys.stderr, flush=True)
     gu_ms = kern.get("gemv_gateup", float("nan"))
-    dn_ms = kern.get("gemv_down", float("nan"))
+    dn_ms = kern.get("gemv_down_combine", float("nan"))
     achieved = gateup_bytes / (gu_ms * 1e-3) / 1e9
+
+    extra = {}
+    if not args.no_extra:
+        print("bench: decode, 32 tokens", file=sys.stderr, flush=True)
+        ms32, kern32, gu32, dn32 = decode_case(32, nx.PATH_AUTO)
+        extra["decode_32_tokens"] = {
+            "ms_per_step": ms32, "tokens_per_s": 32 / (ms32 * 1e-3),
+            "effective_GBps": (gu32 + dn32) / (ms32 * 1e-3) / 1e9, "path": "auto",
+            "kernels_ms": {k_: round(v, 4) for k_, v in kern32.items()}}
+    for s_ in sets:
+        s_.close()
+    if not args.no_extra:
+        print("bench: prefill", file=sys.stderr, flush=True)
+        extra["prefill_2048_tokens"] = prefill(nx, ctx, torch, args)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "gemv_gateup_mixtral_q4k_t1_traffic.json")
@@ -222,8 +300,7 @@ def main():
         "down_gemv_GBps": down_bytes / (dn_ms * 1e-3) / 1e9,
         "cpu_baseline": cpu,
     }
-    for s in sets:
-        s.close()
+    rec.update(extra)
     ctx.close()
     print(json.dumps(rec), flush=True)
 

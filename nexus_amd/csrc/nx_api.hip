@@ -462,7 +462,7 @@ int nx_permute(nx_ctx *c, const int32_t *experts, const int32_t *counts, int T, 
     NX_HIP(hipMemcpyAsync(d_cnt, counts, (size_t)T * 4, hipMemcpyHostToDevice, c->stream));
   }
   NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act, nullptr,
-                        nullptr, 0));
+                        0));
   NX_HIP(hipMemcpyAsync(ecount, d_ec, (size_t)E * 4, hipMemcpyDeviceToHost, c->stream));
   NX_HIP(hipMemcpyAsync(offsets, d_off, (size_t)(E + 1) * 4, hipMemcpyDeviceToHost, c->stream));
   if (pairs > 0) {
@@ -618,26 +618,57 @@ int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const 
   NX_TRY(ws(c, WS_YPAIR, pairs_total * H, &d_ypair));
 
   int use = path;
-  if (use == NX_PATH_AUTO) use = NX_PATH_GEMV;
-  if (use != NX_PATH_GEMV) return fail(NX_ERR_UNSUPPORTED, "MFMA path not available in this build");
-
-  if (route_permute_fusable(T, E, k)) {
-    NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
-                                d_pt, d_ps, d_inv, d_act, nullptr, 0));
-  } else {
-    NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
-    NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act,
-                          nullptr, nullptr, 0));
+  if (use == NX_PATH_AUTO) {
+    // MFMA once experts see enough tokens on average to amortize the tile
+    // dequantization; below that the GEMV streams each weight fewer times
+    const long active_max = std::min<long>(E, (long)T * k);
+    use = ((long)T * k >= 32 * active_max) ? NX_PATH_MFMA_F16 : NX_PATH_GEMV;
   }
 
+  if (use == NX_PATH_GEMV) {
+    if (route_permute_fusable(T, E, k)) {
+      NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
+                                  d_pt, d_ps, d_inv, d_act, nullptr, 0));
+    } else {
+      NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
+      NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act,
+                            nullptr, 0));
+    }
+    const int fmax = std::max(ex->F, ex->Fs);
+    const int act_stride = (fmax + 7) / 8 * 8;
+    float *d_actv;
+    NX_TRY(ws(c, WS_ACT, pairs_total * act_stride, &d_actv));
+    GemvPlan gp{ex, T, k, d_x, d_pt, d_off, d_act, d_actv, act_stride, d_ypair,
+                d_w, d_cnt, d_inv, d_out};
+    NX_TRY(launch_gemv_gateup(c, gp));
+    NX_TRY(launch_gemv_down(c, gp));
+    return NX_OK;
+  }
+
+  // grouped GEMM on MFMA
+  const bool bf16 = use == NX_PATH_MFMA_BF16;
+  const int tm = gemm_tile_m();
+  const long active_max = std::min<long>(E, (long)T * k);
+  const int max_tiles = (int)(((long)T * k + tm - 1) / tm + active_max +
+                              (shared ? ((long)T + tm - 1) / tm : 0));
+  int32_t *d_tiles;
+  NX_TRY(ws(c, WS_TILES, 2 + 2 * (size_t)max_tiles, &d_tiles));
+  NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
+  NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, tm, d_ec, d_off, d_pt, d_ps, d_inv, d_act,
+                        d_tiles, shared ? T : 0));
+  void *d_xh, *d_acth;
+  NX_TRY(ws_get(c, WS_XH, (size_t)T * H * 2, &d_xh));
+  NX_TRY(launch_to_half(c, d_x, (size_t)T * H, bf16, d_xh));
   const int fmax = std::max(ex->F, ex->Fs);
   const int act_stride = (fmax + 7) / 8 * 8;
-  float *d_actv;
-  NX_TRY(ws(c, WS_ACT, pairs_total * act_stride, &d_actv));
-  GemvPlan gp{ex, T, k, d_x, d_pt, d_off, d_act, d_actv, act_stride, d_ypair,
-              d_w, d_cnt, d_inv, d_out};
-  NX_TRY(launch_gemv_gateup(c, gp));
-  NX_TRY(launch_gemv_down(c, gp));
+  NX_TRY(ws_get(c, WS_ACT, pairs_total * act_stride * 2, &d_acth));
+  if ((size_t)T * H * 2 >= (1u << 31) || pairs_total * act_stride * 2 >= (1u << 31))
+    return fail(NX_ERR_UNSUPPORTED, "activation buffers above 2 GiB");
+  GemmPlan mp{ex, T, k, bf16, d_x, d_pt, d_off, d_act, d_tiles, max_tiles, d_acth, act_stride,
+              d_ypair, d_xh, pairs_total};
+  NX_TRY(launch_gemm_gateup(c, mp));
+  NX_TRY(launch_gemm_down(c, mp));
+  NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out));
   return NX_OK;
 }
 

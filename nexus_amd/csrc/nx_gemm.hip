@@ -1,9 +1,472 @@
-// nx_gemm.hip — prefill path: grouped GEMM on MFMA (placeholder until the
-// LDS-dequant kernels land; the launchers report the path as unsupported).
+// nx_gemm.hip — prefill path: grouped GEMM over the resident quantized
+// experts on CDNA4 MFMA (fp16 or bf16 operands, fp32 accumulate).
+//
+// Replaces, for many tokens per expert, the matvec/SwiGLU/matvec sequence of
+// dispatch_moe_ffn (src/engine/mod.rs:994-1017) applied token by token:
+//   gate/up: act[p] = silu(W_gate . x[tok(p)]) * (W_up . x[tok(p)])  for the
+//            pairs p of each expert, written as fp16/bf16;
+//   down:    y[p] = W_down . act[p]  (fp32), then the route-weighted combine.
+//
+// Work decomposition.  The permutation kernel lists M-tiles (expert, first
+// pair) of 128 pairs; grid.y walks that list (extra workgroups exit), grid.x
+// walks 128-row N-tiles of the weight matrices, so consecutive workgroups of
+// one N-tile column share weights.  A workgroup of 4 waves owns a 128x128
+// output tile (gate/up: two of them, for the gate and the up rows), each
+// wave a 64x64 quarter made of 2x2 v_mfma_f32_32x32x16 tiles.
+//
+// K loop, 64 elements per step (one Q4_K segment = sub-blocks s and s+4 of a
+// block, two Q8_0 / Q4_0 blocks, or 64 F32 values): the weight codes and
+// scales of the next step are fetched into registers while the MFMAs consume
+// the current step from LDS; each thread then dequantizes its 32 weights
+// (bit-exact f32 value, rounded once to the operand type) into LDS.  The
+// activation tile is gathered row by row through the permutation.
+#include "nx_device.hpp"
 #include "nx_internal.hpp"
 
 namespace nx {
-int gemm_tile_m() { return 128; }
-int launch_gemm_gateup(nx_ctx *, const GemmPlan &) { return fail(NX_ERR_UNSUPPORTED, "MFMA path not built"); }
-int launch_gemm_down(nx_ctx *, const GemmPlan &) { return fail(NX_ERR_UNSUPPORTED, "MFMA path not built"); }
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128;   // pairs per tile
+constexpr int BN = 128;   // weight rows per tile
+constexpr int BK = 64;    // K elements per step
+constexpr int LDK = BK + 8;  // LDS row stride in elements (16-byte pad)
+
+template <bool BF16>
+struct OpT;
+template <>
+struct OpT<false> {
+  using T = _Float16;
+  using V8 = f16x8;
+  __device__ __forceinline__ static uint16_t bits(float v) {
+    return __builtin_bit_cast(uint16_t, (_Float16)v);
+  }
+  __device__ __forceinline__ static f32x16 mfma(const V8 &a, const V8 &b, const f32x16 &c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct OpT<true> {
+  using T = __bf16;
+  using V8 = bf16x8;
+  __device__ __forceinline__ static uint16_t bits(float v) {
+    return __builtin_bit_cast(uint16_t, (__bf16)v);
+  }
+  __device__ __forceinline__ static f32x16 mfma(const V8 &a, const V8 &b, const f32x16 &c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+struct GemmArgs {
+  // weights: role bases (gate, up) or (down, -), per-expert strides, row bytes
+  const uint8_t *qs0, *qs1, *meta0, *meta1;
+  size_t qs_stride, meta_stride;
+  uint32_t row_qs, row_meta;
+  int rows, cols, nseg;
+  const uint8_t *sqs0, *sqs1, *smeta0, *smeta1;
+  uint32_t srow_qs, srow_meta;
+  int srows, scols, snseg;
+  // activations (operand type), [rows][a_stride]; a_bytes = size of the buffer
+  const uint16_t *a;
+  int a_stride;
+  uint32_t a_bytes;
+  const int32_t *perm_token;  // gate/up: pair -> token row of `a`; down: null (a is per pair)
+  const int32_t *offsets;
+  const int32_t *tiles;  // [0] = count, then (expert, first pair) pairs; expert E = shared
+  int E, T, k, has_shared;
+  // outputs
+  uint16_t *act;  // gate/up: [pairs][act_stride] operand type
+  int act_stride;
+  float *y;       // down: [pairs][H]
+  int y_stride;
+};
+
+// One thread's share of a weight tile: row = tid / 2, half h = tid % 2 of the
+// 64-element K step, dequantized to 32 floats in K order.
+template <int FMT>
+struct WLoad {
+  uint4 q[2];  // codes (Q4_K / Q4_0: q[0] only; F32: 8 floats in q[0..1]x... see below)
+  uint4 f[6];  // F32 only: 32 floats = 8 x uint4 with q[0..1]
+  uint4 m;     // scales
+};
+
+template <int FMT>
+__device__ __forceinline__ void w_fetch(WLoad<FMT> &w, __amdgpu_buffer_rsrc_t rq,
+                                        __amdgpu_buffer_rsrc_t rm, uint32_t row_off_q,
+                                        uint32_t row_off_m, int ks, int h, int nseg, bool valid) {
+  if constexpr (FMT == NX_FMT_Q4_K) {
+    // segment ks, half h: 16 code bytes -> 16 low-nibble (sub-block s) and
+    // 16 high-nibble (sub-block s+4) weights
+    const uint32_t o = valid ? row_off_q + seg_off(ks, h, nseg) : OOB;
+    w.q[0] = bload16(rq, o);
+    w.m = bload16(rm, valid ? row_off_m + (uint32_t)(ks >> 2) * 16u : OOB);
+  } else if constexpr (FMT == NX_FMT_Q8_0) {
+    // blocks 2ks + h (segment = block): 32 codes
+    const int j = 2 * ks + h;
+    const bool v = valid && j < nseg;
+    w.q[0] = bload16(rq, v ? row_off_q + seg_off(j, 0, nseg) : OOB);
+    w.q[1] = bload16(rq, v ? row_off_q + seg_off(j, 1, nseg) : OOB);
+    const uint32_t mo = v ? row_off_m + (uint32_t)j * 2u : OOB;
+    const uint32_t mw = bload4(rm, mo == OOB ? OOB : (mo & ~3u));
+    w.m.x = (mo & 2u) ? (mw >> 16) : (mw & 0xFFFFu);
+  } else if constexpr (FMT == NX_FMT_Q4_0) {
+    // segment ks holds blocks 2ks (half 0) and 2ks+1 (half 1)
+    w.q[0] = bload16(rq, valid ? row_off_q + seg_off(ks, h, nseg) : OOB);
+    const uint32_t mw = bload4(rm, valid ? row_off_m + (uint32_t)ks * 4u : OOB);
+    w.m.x = h ? (mw >> 16) : (mw & 0xFFFFu);
+  } else {  // F32: segments 8ks + 4h .. +3 (8 floats each)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 8 * ks + 4 * h + i;
+      const bool v = valid && j < nseg;
+      const uint4 a = bload16(rq, v ? row_off_q + seg_off(j, 0, nseg) : OOB);
+      const uint4 b = bload16(rq, v ? row_off_q + seg_off(j, 1, nseg) : OOB);
+      if (i == 0) {
+        w.q[0] = a;
+        w.q[1] = b;
+      } else {
+        w.f[2 * (i - 1)] = a;
+        w.f[2 * (i - 1) + 1] = b;
+      }
+    }
+  }
+}
+
+// dequantize to 32 floats in the K order of the step (positions 32h .. 32h+31
+// of the 64-element step, except Q4_K whose halves interleave: low nibbles go
+// to positions 16h + i, high nibbles to 32 + 16h + i)
+template <int FMT>
+__device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, float *v) {
+  if constexpr (FMT == NX_FMT_Q4_K) {
+    const float d = h2f(w.m.x & 0xFFFFu), dmin = h2f(w.m.x >> 16);
+    const int s = ks & 3;
+    const uint32_t b0 = (w.m.y >> (8 * s)) & 0xFFu;
+    const uint32_t b4 = (w.m.z >> (8 * s)) & 0xFFu;
+    const uint32_t b8 = (w.m.w >> (8 * s)) & 0xFFu;
+    const float sl = (float)(b0 & 63u), ml = (float)(b4 & 63u);
+    const float sh = (float)((b8 & 15u) | ((b0 >> 6) << 4));
+    const float mh = (float)((b8 >> 4) | ((b4 >> 6) << 4));
+    const uint32_t ws[4] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t byte = (ws[j] >> (8 * i)) & 0xFFu;
+        // src/quant/mod.rs:841: d * sc * q - dmin * m (exact products)
+        v[4 * j + i] = d * sl * (float)(byte & 15u) - dmin * ml;
+        v[16 + 4 * j + i] = d * sh * (float)(byte >> 4) - dmin * mh;
+      }
+  } else if constexpr (FMT == NX_FMT_Q8_0) {
+    const float d = h2f(w.m.x);
+    const uint32_t ws[8] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w,
+                            w.q[1].x, w.q[1].y, w.q[1].z, w.q[1].w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[4 * j + i] = (float)(int32_t)(int8_t)((ws[j] >> (8 * i)) & 0xFFu) * d;
+  } else if constexpr (FMT == NX_FMT_Q4_0) {
+    const float d = h2f(w.m.x);
+    const uint32_t ws[4] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t byte = (ws[j] >> (8 * i)) & 0xFFu;
+        v[4 * j + i] = (float)((int)(byte & 15u) - 8) * d;
+        v[16 + 4 * j + i] = (float)((int)(byte >> 4) - 8) * d;
+      }
+  } else {
+    const uint4 all[8] = {w.q[0], w.q[1], w.f[0], w.f[1], w.f[2], w.f[3], w.f[4], w.f[5]};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[4 * j] = __uint_as_float(all[j].x);
+      v[4 * j + 1] = __uint_as_float(all[j].y);
+      v[4 * j + 2] = __uint_as_float(all[j].z);
+      v[4 * j + 3] = __uint_as_float(all[j].w);
+    }
+  }
+}
+
+// LDS position (within the 64-element step) of decoded value i of half h
+template <int FMT>
+__device__ __forceinline__ int w_pos(int h, int i) {
+  if constexpr (FMT == NX_FMT_Q4_K) return i < 16 ? 16 * h + i : 32 + 16 * h + (i - 16);
+  return 32 * h + i;
+}
+
+// element index (within the activation row) of K position p of step ks
+template <int FMT>
+__device__ __forceinline__ int a_elem(int ks, int p) {
+  if constexpr (FMT == NX_FMT_Q4_K)
+    return (ks >> 2) * 256 + (ks & 3) * 32 + (p & 31) + ((p >> 5) << 7);
+  return ks * 64 + p;
+}
+
+template <int FMT, bool BF16, bool GATEUP>
+__global__ __launch_bounds__(256, 2) void k_gemm(const GemmArgs g) {
+  using Op = OpT<BF16>;
+  using V8 = typename Op::V8;
+  constexpr int NMAT = GATEUP ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[NMAT][BN * LDK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tile = blockIdx.y;
+  if (tile >= g.tiles[0]) return;  // workgroup-uniform
+  const int e = g.tiles[2 + 2 * tile], m0 = g.tiles[3 + 2 * tile];
+  const bool routed = e < g.E;
+  const int pair0 = routed ? g.offsets[e] : g.T * g.k;
+  const int count = routed ? g.offsets[e + 1] - pair0 : g.T;
+  const int rows = routed ? g.rows : g.srows;
+  const int cols = routed ? g.cols : g.scols;
+  const int nseg = routed ? g.nseg : g.snseg;
+  const uint32_t rq = routed ? g.row_qs : g.srow_qs;
+  const uint32_t rm = routed ? g.row_meta : g.srow_meta;
+  const int n0 = blockIdx.x * BN;
+  if (n0 >= rows) return;
+  const int mrows = min(BM, count - m0);
+
+  const uint8_t *q0p = routed ? g.qs0 + (size_t)e * g.qs_stride : g.sqs0;
+  const uint8_t *q1p = routed ? g.qs1 + (size_t)e * g.qs_stride : g.sqs1;
+  const uint8_t *m0p = routed ? g.meta0 + (size_t)e * g.meta_stride : g.smeta0;
+  const uint8_t *m1p = routed ? g.meta1 + (size_t)e * g.meta_stride : g.smeta1;
+  const __amdgpu_buffer_rsrc_t rq0 = make_rsrc(q0p, (uint32_t)rows * rq);
+  const __amdgpu_buffer_rsrc_t rq1 = make_rsrc(q1p, (uint32_t)rows * rq);
+  const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(m0p, (uint32_t)rows * rm);
+  const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(m1p, (uint32_t)rows * rm);
+
+  // ---- this thread's load assignment: row r = tid / 2, half h = tid % 2
+  const int lr = tid >> 1, lh = tid & 1;
+  // activation row (gathered through the permutation for gate/up)
+  const bool arow_ok = lr < mrows;
+  int arow = 0;
+  if (arow_ok) {
+    const int p = pair0 + m0 + lr;
+    arow = GATEUP ? (routed ? g.perm_token[p] : (m0 + lr)) : p;
+  }
+  // one wave-uniform resource over the whole activation buffer; per-lane
+  // offsets select the row, and absent rows / columns past the row read zero
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.a, g.a_bytes);
+  const uint32_t arow_off = (uint32_t)arow * (uint32_t)g.a_stride * 2u;
+  // weight row of this thread
+  const int wrow = n0 + lr;
+  const bool wrow_ok = wrow < rows;
+  const uint32_t wq_off = (uint32_t)wrow * rq, wm_off = (uint32_t)wrow * rm;
+
+  // number of 64-element K steps
+  const int nks = FMT == NX_FMT_Q4_K ? nseg : (FMT == NX_FMT_F32 ? (nseg + 7) / 8 : (FMT == NX_FMT_Q8_0 ? (nseg + 1) / 2 : nseg));
+
+  // ---- register prefetch buffers
+  uint4 abuf[4];
+  WLoad<FMT> wb[NMAT];
+  auto fetch = [&](int ks) {
+    // activations: 32 elements = two 16-element runs (contiguous in the row)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = 32 * lh + 8 * i;  // K position of this 8-element piece
+      const int el = a_elem<FMT>(ks, p);
+      abuf[i] = bload16(ra, (arow_ok && el < cols) ? arow_off + (uint32_t)el * 2u : OOB);
+    }
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+      w_fetch<FMT>(wb[mt], mt == 0 ? rq0 : rq1, mt == 0 ? rm0 : rm1, wq_off, wm_off, ks, lh, nseg,
+                   wrow_ok);
+  };
+  auto stash = [&](int ks) {
+    // activation piece i of this thread covers K positions:
+    //   Q4_K: half 0 -> low-nibble positions 0..31 (8i..8i+7), half 1 -> 32..63
+    //   others: 32h + 8i
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = FMT == NX_FMT_Q4_K ? (lh == 0 ? 8 * i : 32 + 8 * i) : 32 * lh + 8 * i;
+      *reinterpret_cast<uint4 *>(&As[lr * LDK + p]) = abuf[i];
+    }
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) {
+      float v[32];
+      w_decode<FMT>(wb[mt], ks, v);
+#pragma unroll
+      for (int i = 0; i < 32; i += 2) {
+        const uint32_t pk = (uint32_t)Op::bits(v[i]) | ((uint32_t)Op::bits(v[i + 1]) << 16);
+        *reinterpret_cast<uint32_t *>(&Bs[mt][lr * LDK + w_pos<FMT>(lh, i)]) = pk;
+      }
+    }
+  };
+
+  // ---- accumulators: wave (wm, wn) owns rows wm*64.., cols wn*64..
+  const int wm = wave >> 1, wn = wave & 1;
+  f32x16 acc[NMAT][2][2];
+#pragma unroll
+  for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mt][i][j][r] = 0.f;
+
+  fetch(0);
+  for (int ks = 0; ks < nks; ++ks) {
+    __syncthreads();  // previous step's MFMAs are done with the LDS tiles
+    stash(ks);
+    __syncthreads();
+    if (ks + 1 < nks) fetch(ks + 1);
+    // MFMA over the 64-element step: 4 sub-steps of 16
+    const int l32 = lane & 31, kh = lane >> 5;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      V8 af[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const V8 *>(&As[(wm * 64 + i * 32 + l32) * LDK + kk * 16 + kh * 8]);
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt) {
+        V8 bf[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          bf[j] = *reinterpret_cast<const V8 *>(&Bs[mt][(wn * 64 + j * 32 + l32) * LDK + kk * 16 + kh * 8]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) acc[mt][i][j] = Op::mfma(af[i], bf[j], acc[mt][i][j]);
+      }
+    }
+  }
+
+  // ---- epilogue.  32x32 accumulator layout: lane holds column (lane % 32),
+  // register r holds row (r / 4) * 8 + (lane / 32) * 4 + r % 4.
+  const int col_l = lane & 31, rq4 = (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 64 + j * 32 + col_l;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wm * 64 + i * 32 + (r >> 2) * 8 + rq4 + (r & 3);
+        if (row < mrows && col < rows) {
+          const size_t p = (size_t)(pair0 + m0 + row);
+          if constexpr (GATEUP) {
+            const float v = silu_mul(acc[0][i][j][r], acc[1][i][j][r]);
+            g.act[p * g.act_stride + col] = Op::bits(v);
+          } else {
+            g.y[p * g.y_stride + col] = acc[0][i][j][r];
+          }
+        }
+      }
+    }
+}
+
+// f32 activations -> operand type (one row per token)
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_to_half(const float *__restrict__ x, size_t n,
+                                                 uint16_t *__restrict__ out) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = OpT<BF16>::bits(x[i]);
+}
+
+using GemmFn = void (*)(GemmArgs);
+
+template <bool BF16, bool GATEUP>
+GemmFn pick_fmt(int fmt) {
+  switch (fmt) {
+  case NX_FMT_Q4_K: return k_gemm<NX_FMT_Q4_K, BF16, GATEUP>;
+  case NX_FMT_Q8_0: return k_gemm<NX_FMT_Q8_0, BF16, GATEUP>;
+  case NX_FMT_Q4_0: return k_gemm<NX_FMT_Q4_0, BF16, GATEUP>;
+  case NX_FMT_F32: return k_gemm<NX_FMT_F32, BF16, GATEUP>;
+  }
+  return nullptr;
+}
+
+GemmFn pick(int fmt, bool bf16, bool gateup) {
+  if (bf16) return gateup ? pick_fmt<true, true>(fmt) : pick_fmt<true, false>(fmt);
+  return gateup ? pick_fmt<false, true>(fmt) : pick_fmt<false, false>(fmt);
+}
+
+void fill_weights(GemmArgs &a, const nx_experts *ex, bool gateup) {
+  const RolePlane &R0 = ex->role[gateup ? NX_ROLE_GATE : NX_ROLE_DOWN];
+  const RolePlane &R1 = ex->role[gateup ? NX_ROLE_UP : NX_ROLE_DOWN];
+  a.qs0 = R0.qs;
+  a.qs1 = R1.qs;
+  a.meta0 = R0.meta;
+  a.meta1 = R1.meta;
+  a.qs_stride = R0.qs_stride;
+  a.meta_stride = R0.meta_stride;
+  a.row_qs = R0.row_qs;
+  a.row_meta = R0.row_meta;
+  a.rows = R0.rows;
+  a.cols = R0.cols;
+  a.nseg = R0.nseg;
+  if (ex->Fs > 0) {
+    const RolePlane &S0 = ex->shared[gateup ? NX_ROLE_GATE : NX_ROLE_DOWN];
+    const RolePlane &S1 = ex->shared[gateup ? NX_ROLE_UP : NX_ROLE_DOWN];
+    a.sqs0 = S0.qs;
+    a.sqs1 = S1.qs;
+    a.smeta0 = S0.meta;
+    a.smeta1 = S1.meta;
+    a.srow_qs = S0.row_qs;
+    a.srow_meta = S0.row_meta;
+    a.srows = S0.rows;
+    a.scols = S0.cols;
+    a.snseg = S0.nseg;
+  }
+}
+
+int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
+  const nx_experts *ex = p.ex;
+  GemmArgs a{};
+  fill_weights(a, ex, gateup);
+  a.offsets = p.offsets;
+  a.tiles = p.tiles;
+  a.E = ex->E;
+  a.T = p.T;
+  a.k = p.k;
+  a.has_shared = ex->Fs > 0 ? 1 : 0;
+  if (gateup) {
+    a.a = static_cast<const uint16_t *>(p.xh);
+    a.a_stride = ex->H;
+    a.a_bytes = (uint32_t)((size_t)p.T * ex->H * 2);
+    a.perm_token = p.perm_token;
+    a.act = static_cast<uint16_t *>(p.act);
+    a.act_stride = p.act_stride;
+  } else {
+    a.a = static_cast<const uint16_t *>(p.act);
+    a.a_stride = p.act_stride;
+    a.a_bytes = (uint32_t)(p.pairs_total * p.act_stride * 2);
+    a.perm_token = nullptr;
+    a.y = p.ypair;
+    a.y_stride = ex->H;
+  }
+  const int rows = a.rows > a.srows ? a.rows : a.srows;
+  const unsigned gx = (unsigned)((rows + BN - 1) / BN);
+  const unsigned gy = (unsigned)p.max_tiles;
+  GemmFn fn = pick(ex->fmt, p.bf16, gateup);
+  if (!fn) return fail(NX_ERR_UNSUPPORTED, "no grouped-GEMM kernel for this format");
+  const char *name = gateup ? "gemm_gateup" : "gemm_down";
+  return launch(c, name, [&] { hipLaunchKernelGGL(fn, dim3(gx, gy), dim3(256), 0, c->stream, a); });
+}
+
+}  // namespace
+
+int gemm_tile_m() { return BM; }
+
+int launch_to_half(nx_ctx *c, const float *x, size_t n, bool bf16, void *out) {
+  if (n == 0) return NX_OK;
+  size_t gblocks = (n + 255) / 256;
+  if (gblocks > 65536) gblocks = 65536;
+  uint16_t *o = static_cast<uint16_t *>(out);
+  if (bf16)
+    return launch(c, "to_bf16", [&] { k_to_half<true><<<(unsigned)gblocks, 256, 0, c->stream>>>(x, n, o); });
+  return launch(c, "to_f16", [&] { k_to_half<false><<<(unsigned)gblocks, 256, 0, c->stream>>>(x, n, o); });
+}
+
+int launch_gemm_gateup(nx_ctx *c, const GemmPlan &p) { return run(c, p, true); }
+int launch_gemm_down(nx_ctx *c, const GemmPlan &p) { return run(c, p, false); }
+
 }  // namespace nx

@@ -148,10 +148,13 @@ int launch_repack(nx_ctx *c, int fmt, const void *d_src, const RolePlane &pl, ui
 
 int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
                  int32_t *d_expert, float *d_weight, int32_t *d_count);
+// d_tiles (optional): [0] = tile count, then (expert, first pair) per tile
+// of tile_m pairs; shared_T > 0 appends ceil(shared_T / tile_m) tiles of the
+// shared expert (expert id E)
 int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, int T, int k,
                    int E, int tile_m, int32_t *d_ecount, int32_t *d_offsets, int32_t *d_ptok,
                    int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles,
-                   int *d_counters, int n_counters);
+                   int shared_T);
 // router + permutation in one workgroup, for small batches
 bool route_permute_fusable(int T, int E, int k);
 int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
@@ -189,12 +192,15 @@ struct GemmPlan {
   const int32_t *offsets;
   const int32_t *active;
   const int32_t *tiles;  // tile list from the permutation kernel
+  int max_tiles;         // grid bound for the tile list
   void *act;             // [pairs_total][act_stride] half precision
   int act_stride;
   float *ypair;
   void *xh;              // [T][H] half precision copy of x
+  size_t pairs_total;    // rows of act / ypair
 };
 int gemm_tile_m();
+int launch_to_half(nx_ctx *c, const float *x, size_t n, bool bf16, void *out);
 int launch_gemm_gateup(nx_ctx *c, const GemmPlan &p);
 int launch_gemm_down(nx_ctx *c, const GemmPlan &p);
 

@@ -153,8 +153,7 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
     const int32_t *__restrict__ rexp, const int32_t *__restrict__ rcnt, int T, int k, int E,
     int W, int tile_m, int32_t *__restrict__ ecount, int32_t *__restrict__ offsets,
     int32_t *__restrict__ ptok, int32_t *__restrict__ pslot, int32_t *__restrict__ inv,
-    int32_t *__restrict__ active, int32_t *__restrict__ tiles, int *__restrict__ counters,
-    int n_counters) {
+    int32_t *__restrict__ active, int32_t *__restrict__ tiles, int shared_T) {
   __shared__ int cnt[PERM_THREADS];
   __shared__ int base[PERM_THREADS];
   __shared__ int run[PERM_THREADS];
@@ -163,7 +162,6 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
   __shared__ int wave_tot[PERM_THREADS / 64];
   __shared__ int total;
   const int tid = threadIdx.x;
-  for (int i = tid; i < n_counters; i += PERM_THREADS) counters[i] = 0;
   for (int e = tid; e < E; e += PERM_THREADS) cnt[e] = 0;
   __syncthreads();
   const int pairs = T * k;
@@ -196,8 +194,13 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
       tiles[2 + 2 * (tb + j)] = tid;
       tiles[2 + 2 * (tb + j) + 1] = j * tile_m;
     }
+    const int nshared = (shared_T + tile_m - 1) / tile_m;
+    for (int j = tid; j < nshared; j += PERM_THREADS) {
+      tiles[2 + 2 * (ntiles + j)] = E;
+      tiles[2 + 2 * (ntiles + j) + 1] = j * tile_m;
+    }
     if (tid == 0) {
-      tiles[0] = ntiles;
+      tiles[0] = ntiles + nshared;
       tiles[1] = 0;
     }
   }
@@ -357,7 +360,7 @@ int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int scor
 int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, int T, int k,
                    int E, int tile_m, int32_t *d_ecount, int32_t *d_offsets, int32_t *d_ptok,
                    int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles,
-                   int *d_counters, int n_counters) {
+                   int shared_T) {
   if (E > PERM_THREADS) return fail(NX_ERR_UNSUPPORTED, "permutation supports at most 1024 experts");
   int W = PERM_WORDS / (E > 0 ? E : 1);
   if (W > PERM_THREADS / 32) W = PERM_THREADS / 32;
@@ -366,7 +369,7 @@ int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, i
     k_permute<<<1, PERM_THREADS, 0, c->stream>>>(d_expert, d_count, T, k, E, W,
                                                  tile_m > 0 ? tile_m : 1, d_ecount, d_offsets,
                                                  d_ptok, d_pslot, d_inv, d_active, d_tiles,
-                                                 d_counters, d_counters ? n_counters : 0);
+                                                 shared_T);
   });
 }
 

@@ -212,3 +212,43 @@ def test_mixtral_decode_full_size(ctx):
     err = rel_l2(run_layer(ctx, L), L.oracle_out())
     say(f"  rel L2 = {err:.2e}")
     assert err <= GEMV_TOL
+
+
+# ----------------------------------------------------------------------------- MFMA path
+MFMA_TOL = 1e-2
+
+
+@pytest.mark.parametrize("path", [nx.PATH_MFMA_F16, nx.PATH_MFMA_BF16])
+@pytest.mark.parametrize("fmt,E,H,F,k,T,zipf", [
+    (Q8_0, 8, 512, 1024, 2, 300, 1.2),   # Zipf-imbalanced expert popularity
+    (Q4_K, 8, 512, 768, 2, 200, None),
+    (Q4_0, 8, 256, 512, 2, 130, None),
+    (F32, 8, 512, 1024, 2, 64, None),
+    (Q4_K, 32, 256, 512, 4, 77, None),
+    (Q8_0, 4, 256, 320, 1, 129, None),   # F not a multiple of the 128-row tile
+])
+def test_layer_mfma_parity(ctx, path, fmt, E, H, F, k, T, zipf):
+    L = Layer(fmt, E, H, F, k, T, seed=3 * E + H + F + T, zipf=zipf)
+    say(f"layer mfma path={path} fmt={fmt} E={E} H={H} F={F} k={k} T={T} zipf={zipf}")
+    err = rel_l2(run_layer(ctx, L, path), L.oracle_out())
+    say(f"  rel L2 = {err:.2e}")
+    assert err <= MFMA_TOL, err
+
+
+def test_layer_mfma_shared_expert_sigmoid(ctx):
+    L = Layer(Q4_K, 16, 512, 512, 4, 96, seed=5, shared_F=512, score_mode=1)
+    say("layer mfma shared + sigmoid")
+    assert rel_l2(run_layer(ctx, L, nx.PATH_MFMA_F16), L.oracle_out()) <= MFMA_TOL
+
+
+def test_auto_path_picks_mfma_for_prefill(ctx):
+    L = Layer(Q8_0, 8, 512, 512, 2, 256, seed=8)
+    ex = L.upload(nx, ctx)
+    ctx.profile(True)
+    ctx.profile_reset()
+    out = ex.forward(L.x, L.logits, L.k, path=nx.PATH_AUTO)
+    stats = ctx.profile_stats()
+    ctx.profile(False)
+    ex.close()
+    assert "gemm_gateup" in stats and "gemm_down" in stats
+    assert rel_l2(out, L.oracle_out()) <= MFMA_TOL
