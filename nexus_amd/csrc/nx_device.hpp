@@ -4,13 +4,16 @@
 // Resident code-plane layout.  Each matrix row is cut into 32-byte
 // "segments" of its code plane:
 //   Q4_K (src/quant/mod.rs:820-849): segment j = block b = j/4, sub-block pair
-//        s = j%4: qs bytes [32s, 32s+32) of the block.  Byte i holds element
-//        b*256 + 32s + i (low nibble, sub-block s) and b*256 + 128 + 32s + i
-//        (high nibble, sub-block s+4); y = d*sc*q - dmin*m.
-//   Q8_0 (src/quant/mod.rs:689-703): segment j = block j, y = (int8)q * d.
-//   Q4_0 (src/quant/mod.rs:723-745): segment j = blocks 2j and 2j+1 (16 B
-//        each); byte i of block c holds c*32 + i (low) and c*32 + 16 + i
-//        (high), y = (q - 8) * d.
+//        s = j%4: half 0 holds the 32 codes of sub-block s (block elements
+//        32s ..), half 1 those of sub-block s+4 (elements 128 + 32s ..);
+//        y = d*sc*q - dmin*m.
+//   Q4_0 (src/quant/mod.rs:723-745): segment j = blocks 2j (half 0) and 2j+1
+//        (half 1); y = (q - 8) * d.
+//   In both 4-bit formats the 16 bytes of a half hold one 32-element
+//   sub-block: byte 4k+i has element 8k+i in its low nibble and element
+//   8k+4+i in its high nibble.
+//   Q8_0 (src/quant/mod.rs:689-703): segment j = block j in element order,
+//        y = (int8)q * d.
 //   F32: segment j = floats 8j .. 8j+7.
 // Segments are stored half-interleaved per group of 64: half h (16 B) of
 // segment j lives at (j/64)*2048 + h*G*16 + (j%64)*16 with G the group's
@@ -31,23 +34,6 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
   return (float)h;
 }
 
-// Nibble masks reach the kernels as arguments (GemvArgs::mask_lo/mask_hi):
-// with compile-time masks the compiler folds mask-then-convert into a 4-bit
-// field extract plus a convert; with opaque masks each byte of the masked
-// word converts with a single v_cvt_f32_ubyteN.
-__device__ __forceinline__ float ub0(uint32_t w) { return (float)(w & 0xFFu); }
-__device__ __forceinline__ float ub1(uint32_t w) { return (float)((w >> 8) & 0xFFu); }
-__device__ __forceinline__ float ub2(uint32_t w) { return (float)((w >> 16) & 0xFFu); }
-__device__ __forceinline__ float ub3(uint32_t w) { return (float)(w >> 24); }
-
-// sum_i byte_i(w) * x[i] for the four bytes of w
-__device__ __forceinline__ float dot4u(uint32_t w, const float *x, float acc) {
-  acc = fmaf(ub0(w), x[0], acc);
-  acc = fmaf(ub1(w), x[1], acc);
-  acc = fmaf(ub2(w), x[2], acc);
-  acc = fmaf(ub3(w), x[3], acc);
-  return acc;
-}
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // Raw buffer resources: 32-bit byte offsets, and any load at or beyond
@@ -80,14 +66,123 @@ __device__ __forceinline__ uint32_t seg_off(int j, int h, int nseg) {
   return (uint32_t)(g * 2048 + h * gsz * 16 + (j & 63) * 16);
 }
 
+// ---- Integer-dot GEMV operands.
+//
+// The decode GEMV computes sum_i q_i x_i with exact integer dot products.  A
+// lane's activations over one segment are put in 24-bit block fixed point:
+// with E the binary exponent of max|x| (max|x| < 2^E), X_i = round(x_i *
+// 2^(22-E)) is an integer in [-2^22, 2^22] and x_i = X_i * 2^(E-22) up to
+// half a unit of 2^(E-22) (relative precision 2^-23 of the block maximum).
+// X is computed with the 1.5*2^23 rounding constant: the bits of
+// fma(x, 2^(22-E), 1.5*2^23) are 0x4B400000 + X.
+//
+// 4-bit codes (Q4_K, Q4_0): Y = X + 2^23 lies in [0, 2^24) and is split into
+// six 4-bit digits.  The repacked code dword k of a 32-element sub-block holds
+// elements 8k+i (low nibble of byte i) and 8k+4+i (high nibble); digit plane
+// d holds digit d of the same elements at the same nibble positions, so one
+// v_dot8_u32_u4 per digit gives sum_i q_i * digit_d(Y_i), and one more with
+// 0x11111111 gives sum_i q_i.  Then sum_i q_i X_i = L + 4096 * H with
+// L = a0 + 16 a1 + 256 a2 and H = a3 + 16 a4 + 256 a5 - 2048 * sum q (all
+// exact in 32-bit integers), rounded once to float.
+//
+// Q8_0: Z = X + 0x808080 has base-256 digits z_d in [0, 256); z_d - 128 =
+// (z_d ^ 0x80) as a signed byte is a balanced digit D_d with X = D0 + 256 D1 +
+// 65536 D2, so three v_dot4_i32_i8 per code dword give the sums exactly.
+//
+// Non-finite activations give NaN for the whole segment.
+
+// binary exponent of m (m < 2^E), clamped so that both 2^(22-E) and
+// 2^(E-22) stay normal floats
+__device__ __forceinline__ int blk_exp(float m) {
+  const int e = __builtin_amdgcn_frexp_expf(m);
+  return e < -100 ? -100 : (e > 128 ? 128 : e);
+}
+
+__device__ __forceinline__ float abs_max(const float *x, int n) {
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < n; ++i) m = fmaxf(m, fabsf(x[i]));
+  return m;
+}
+
+// bytes b of four words -> one word (b in 0..1 pairs, b = 2 alone)
+__device__ __forceinline__ void byte_transpose4(const uint32_t *y, uint32_t &b0, uint32_t &b1,
+                                                uint32_t &b2) {
+  const uint32_t t01 = __builtin_amdgcn_perm(y[1], y[0], 0x05010400u);
+  const uint32_t t23 = __builtin_amdgcn_perm(y[3], y[2], 0x05010400u);
+  b0 = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+  b1 = __builtin_amdgcn_perm(t23, t01, 0x07060302u);
+  const uint32_t u01 = __builtin_amdgcn_perm(y[1], y[0], 0x0C0C0602u);
+  const uint32_t u23 = __builtin_amdgcn_perm(y[3], y[2], 0x0C0C0602u);
+  b2 = __builtin_amdgcn_perm(u23, u01, 0x05040100u);
+}
+
+// 32 activations of one 4-bit sub-block -> digit planes p[digit][dword]
+__device__ __forceinline__ void planes4(const float *x, float sc, uint32_t (&p)[6][4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      y[i] = __float_as_uint(fmaf(x[8 * k + i], sc, 12582912.0f)) - 0x4AC00000u;
+    uint32_t lo[3], hi[3];
+    byte_transpose4(y, lo[0], lo[1], lo[2]);
+    byte_transpose4(y + 4, hi[0], hi[1], hi[2]);
+    constexpr uint32_t M = 0x0F0F0F0Fu;
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+      p[2 * b][k] = (lo[b] & M) | ((hi[b] << 4) & ~M);
+      p[2 * b + 1][k] = ((lo[b] >> 4) & M) | (hi[b] & ~M);
+    }
+  }
+}
+
+// sum_i q_i X_i over one 4-bit sub-block (codes w, planes p)
+__device__ __forceinline__ float sumqx4(const uint4 &w, const uint32_t (&p)[6][4]) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  uint32_t a[6] = {0, 0, 0, 0, 0, 0}, sq = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+#pragma unroll
+    for (int d = 0; d < 6; ++d) a[d] = __builtin_amdgcn_udot8(ws[k], p[d][k], a[d], false);
+    sq = __builtin_amdgcn_udot8(ws[k], 0x11111111u, sq, false);
+  }
+  const int32_t L = (int32_t)(a[0] + (a[1] << 4) + (a[2] << 8));
+  const int32_t H = (int32_t)(a[3] + (a[4] << 4) + (a[5] << 8)) - (int32_t)(sq << 11);
+  return fmaf((float)H, 4096.0f, (float)L);
+}
+
+// activations of one 64-element 4-bit segment (two sub-blocks)
+struct X4 {
+  uint32_t p[2][6][4];
+  float post;  // 2^(E-22), or NaN for non-finite activations
+  float s[2];  // sub-block sums of x
+};
+
+__device__ __forceinline__ void prep4(const float *x, X4 &o) {
+  float a = 0.f, b = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) a += x[i];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) b += x[32 + i];
+  o.s[0] = a;
+  o.s[1] = b;
+  const int e = blk_exp(abs_max(x, 64));
+  const float sc = __builtin_amdgcn_ldexpf(1.0f, 22 - e);
+  o.post = fabsf(a + b) <= 3.4e38f ? __builtin_amdgcn_ldexpf(1.0f, e - 22) : __builtin_nanf("");
+  planes4(x, sc, o.p[0]);
+  planes4(x + 32, sc, o.p[1]);
+}
+
 template <int FMT>
 struct Seg;
 
 template <>
 struct Seg<NX_FMT_Q4_K> {
   static constexpr int EPS = 64;  // elements per segment
-  static constexpr int NXS = 2;   // x partial sums kept per segment
   using Meta = uint4;
+  using X = X4;
+  // segment element v: sub-block s = j%4 (v < 32), sub-block s+4 (v >= 32)
   __device__ __forceinline__ static int xidx(int j, int v) {
     return (j >> 2) * 256 + (j & 3) * 32 + (v & 31) + ((v >> 5) << 7);
   }
@@ -98,56 +193,39 @@ struct Seg<NX_FMT_Q4_K> {
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return bload16(r, off);
   }
-  __device__ __forceinline__ static void xsums(const float *x, float *xs) {
-    float a = 0.f, b = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) a += x[i];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) b += x[32 + i];
-    xs[0] = a;
-    xs[1] = b;
-  }
-  // sum over the segment of w*x for NT tokens
+  __device__ __forceinline__ static void prep(const float *x, X &o) { prep4(x, o); }
+  // sum over the segment of w*x for NT tokens; src/quant/mod.rs:841 gives
+  // w = d*sc*q - dmin*m per element, summed here as
+  // d*(sc_a*sum q x + sc_b*sum q x) - dmin*(m_a*sum x + m_b*sum x)
   template <int NT>
   __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m,
-                                             int j, const float (*x)[EPS],
-                                             const float (*xs)[NXS], float *acc, uint32_t mlo,
-                                             uint32_t mhi) {
+                                             int j, const X *xv, float *acc) {
     const float d = h2f(m.x & 0xFFFFu), dmin = h2f(m.x >> 16);
     const int s = j & 3;
     const uint32_t b0 = (m.y >> (8 * s)) & 0xFFu;  // scales12[s]
     const uint32_t b4 = (m.z >> (8 * s)) & 0xFFu;  // scales12[s+4]
     const uint32_t b8 = (m.w >> (8 * s)) & 0xFFu;  // scales12[s+8]
-    const float s_lo = d * (float)(b0 & 63u);
-    const float m_lo = dmin * (float)(b4 & 63u);
-    // high nibbles are converted in place (16*q), so their scale carries 1/16
-    const float s_hi = d * (float)((b8 & 15u) | ((b0 >> 6) << 4)) * 0.0625f;
-    const float m_hi = dmin * (float)((b8 >> 4) | ((b4 >> 6) << 4));
-    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    float lo[NT], hi[NT];
+    const float sa = (float)(b0 & 63u), ma = (float)(b4 & 63u);
+    const float sb = (float)((b8 & 15u) | ((b0 >> 6) << 4));
+    const float mb = (float)((b8 >> 4) | ((b4 >> 6) << 4));
 #pragma unroll
-    for (int t = 0; t < NT; ++t) lo[t] = hi[t] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t l = w[i] & mlo;
-      const uint32_t h = w[i] & mhi;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        lo[t] = dot4u(l, &x[t][4 * i], lo[t]);
-        hi[t] = dot4u(h, &x[t][32 + 4 * i], hi[t]);
-      }
+    for (int t = 0; t < NT; ++t) {
+      const float fa = sumqx4(q0, xv[t].p[0]);
+      const float fb = sumqx4(q1, xv[t].p[1]);
+      const float qx = fmaf(sa, fa, sb * fb) * d * xv[t].post;
+      acc[t] += qx - dmin * fmaf(ma, xv[t].s[0], mb * xv[t].s[1]);
     }
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-      acc[t] += (s_lo * lo[t] - m_lo * xs[t][0]) + (s_hi * hi[t] - m_hi * xs[t][1]);
   }
 };
 
 template <>
 struct Seg<NX_FMT_Q8_0> {
   static constexpr int EPS = 32;
-  static constexpr int NXS = 1;
   using Meta = uint32_t;
+  struct X {
+    uint32_t p[3][8];
+    float post;
+  };
   __device__ __forceinline__ static int xidx(int j, int v) { return j * 32 + v; }
   __device__ __forceinline__ static uint32_t meta_off(int j, bool valid) {
     return valid ? (uint32_t)(j * 2) : OOB;
@@ -157,29 +235,39 @@ struct Seg<NX_FMT_Q8_0> {
     const uint32_t w = bload4(r, off & ~3u);
     return (off & 2u) ? (w >> 16) : (w & 0xFFFFu);
   }
-  __device__ __forceinline__ static void xsums(const float *x, float *xs) {
+  __device__ __forceinline__ static void prep(const float *x, X &o) {
     float a = 0.f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) a += x[i];
-    xs[0] = a;
+    const int e = blk_exp(abs_max(x, 32));
+    const float sc = __builtin_amdgcn_ldexpf(1.0f, 22 - e);
+    o.post = fabsf(a) <= 3.4e38f ? __builtin_amdgcn_ldexpf(1.0f, e - 22) : __builtin_nanf("");
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      uint32_t z[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        z[i] = (__float_as_uint(fmaf(x[4 * k + i], sc, 12582912.0f)) - (0x4B400000u - 0x808080u)) ^
+               0x808080u;
+      byte_transpose4(z, o.p[0][k], o.p[1][k], o.p[2][k]);
+    }
   }
-  // signed codes are read as unsigned q + 128 (byte xor 0x80): sum (q+128) x - 128 sum x
+  // src/quant/mod.rs:689-703: w = (int8)q * d
   template <int NT>
-  __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m,
-                                             int, const float (*x)[EPS],
-                                             const float (*xs)[NXS], float *acc, uint32_t,
-                                             uint32_t mflip) {
+  __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m, int,
+                                             const X *xv, float *acc) {
     const float d = h2f(m);
     const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    uint32_t u[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) u[i] = w[i] ^ mflip;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      float a = 0.f;
+      int32_t a[3] = {0, 0, 0};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a = dot4u(u[i], &x[t][4 * i], a);
-      acc[t] += d * (a - 128.f * xs[t][0]);
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int dg = 0; dg < 3; ++dg)
+          a[dg] = __builtin_amdgcn_sdot4((int)w[k], (int)xv[t].p[dg][k], a[dg], false);
+      const float f = fmaf((float)a[2], 65536.0f, (float)(a[0] + (a[1] << 8)));
+      acc[t] += f * d * xv[t].post;
     }
   }
 };
@@ -187,8 +275,8 @@ struct Seg<NX_FMT_Q8_0> {
 template <>
 struct Seg<NX_FMT_Q4_0> {
   static constexpr int EPS = 64;
-  static constexpr int NXS = 2;
   using Meta = uint32_t;  // two f16 scales (blocks 2j, 2j+1)
+  using X = X4;
   __device__ __forceinline__ static int xidx(int j, int v) { return j * 64 + v; }
   __device__ __forceinline__ static uint32_t meta_off(int j, bool valid) {
     return valid ? (uint32_t)(j * 4) : OOB;
@@ -196,35 +284,18 @@ struct Seg<NX_FMT_Q4_0> {
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return bload4(r, off);
   }
-  __device__ __forceinline__ static void xsums(const float *x, float *xs) {
-    float a = 0.f, b = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) a += x[i];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) b += x[32 + i];
-    xs[0] = a;
-    xs[1] = b;
-  }
+  __device__ __forceinline__ static void prep(const float *x, X &o) { prep4(x, o); }
+  // src/quant/mod.rs:723-745: w = (q - 8) * d per block
   template <int NT>
-  __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m,
-                                             int, const float (*x)[EPS],
-                                             const float (*xs)[NXS], float *acc, uint32_t mlo,
-                                             uint32_t mhi) {
+  __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m, int,
+                                             const X *xv, float *acc) {
     const float d0 = h2f(m & 0xFFFFu), d1 = h2f(m >> 16);
-    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      float a0 = 0.f, b0 = 0.f, a1 = 0.f, b1 = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t l0 = w[i] & mlo, h0 = w[i] & mhi;
-        const uint32_t l1 = w[4 + i] & mlo, h1 = w[4 + i] & mhi;
-        a0 = dot4u(l0, &x[t][4 * i], a0);
-        b0 = dot4u(h0, &x[t][16 + 4 * i], b0);
-        a1 = dot4u(l1, &x[t][32 + 4 * i], a1);
-        b1 = dot4u(h1, &x[t][48 + 4 * i], b1);
-      }
-      acc[t] += d0 * (a0 + 0.0625f * b0 - 8.f * xs[t][0]) + d1 * (a1 + 0.0625f * b1 - 8.f * xs[t][1]);
+      const float fa = sumqx4(q0, xv[t].p[0]);
+      const float fb = sumqx4(q1, xv[t].p[1]);
+      const float qx = fmaf(d0, fa, d1 * fb) * xv[t].post;
+      acc[t] += qx - 8.0f * fmaf(d0, xv[t].s[0], d1 * xv[t].s[1]);
     }
   }
 };
@@ -232,22 +303,26 @@ struct Seg<NX_FMT_Q4_0> {
 template <>
 struct Seg<NX_FMT_F32> {
   static constexpr int EPS = 8;
-  static constexpr int NXS = 1;
   using Meta = uint32_t;
+  struct X {
+    float x[8];
+  };
   __device__ __forceinline__ static int xidx(int j, int v) { return j * 8 + v; }
   __device__ __forceinline__ static uint32_t meta_off(int, bool) { return 0; }
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t, uint32_t) { return 0; }
-  __device__ __forceinline__ static void xsums(const float *, float *xs) { xs[0] = 0.f; }
+  __device__ __forceinline__ static void prep(const float *x, X &o) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o.x[i] = x[i];
+  }
   template <int NT>
   __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &, int,
-                                             const float (*x)[EPS], const float (*)[NXS],
-                                             float *acc, uint32_t, uint32_t) {
+                                             const X *xv, float *acc) {
     const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       float a = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a = fmaf(__uint_as_float(w[i]), x[t][i], a);
+      for (int i = 0; i < 8; ++i) a = fmaf(__uint_as_float(w[i]), xv[t].x[i], a);
       acc[t] += a;
     }
   }

@@ -99,8 +99,7 @@ __device__ __forceinline__ void w_fetch(WLoad<FMT> &w, __amdgpu_buffer_rsrc_t rq
                                         __amdgpu_buffer_rsrc_t rm, uint32_t row_off_q,
                                         uint32_t row_off_m, int ks, int h, int nseg, bool valid) {
   if constexpr (FMT == NX_FMT_Q4_K) {
-    // segment ks, half h: 16 code bytes -> 16 low-nibble (sub-block s) and
-    // 16 high-nibble (sub-block s+4) weights
+    // segment ks, half h: the 32 codes of sub-block s (h = 0) or s+4 (h = 1)
     const uint32_t o = valid ? row_off_q + seg_off(ks, h, nseg) : OOB;
     w.q[0] = bload16(rq, o);
     w.m = bload16(rm, valid ? row_off_m + (uint32_t)(ks >> 2) * 16u : OOB);
@@ -136,29 +135,28 @@ __device__ __forceinline__ void w_fetch(WLoad<FMT> &w, __amdgpu_buffer_rsrc_t rq
   }
 }
 
-// dequantize to 32 floats in the K order of the step (positions 32h .. 32h+31
-// of the 64-element step, except Q4_K whose halves interleave: low nibbles go
-// to positions 16h + i, high nibbles to 32 + 16h + i)
+// dequantize this thread's 32 weights (half h of the 64-element step) to
+// floats in K order: positions 32h .. 32h+31 of the step
 template <int FMT>
-__device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, float *v) {
+__device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, int h, float *v) {
   if constexpr (FMT == NX_FMT_Q4_K) {
+    // half 0: sub-block s = ks%4, half 1: sub-block s+4
     const float d = h2f(w.m.x & 0xFFFFu), dmin = h2f(w.m.x >> 16);
     const int s = ks & 3;
     const uint32_t b0 = (w.m.y >> (8 * s)) & 0xFFu;
     const uint32_t b4 = (w.m.z >> (8 * s)) & 0xFFu;
     const uint32_t b8 = (w.m.w >> (8 * s)) & 0xFFu;
-    const float sl = (float)(b0 & 63u), ml = (float)(b4 & 63u);
-    const float sh = (float)((b8 & 15u) | ((b0 >> 6) << 4));
-    const float mh = (float)((b8 >> 4) | ((b4 >> 6) << 4));
+    const float sc = h ? (float)((b8 & 15u) | ((b0 >> 6) << 4)) : (float)(b0 & 63u);
+    const float mn = h ? (float)((b8 >> 4) | ((b4 >> 6) << 4)) : (float)(b4 & 63u);
     const uint32_t ws[4] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t byte = (ws[j] >> (8 * i)) & 0xFFu;
+        const uint32_t byte = (ws[k] >> (8 * i)) & 0xFFu;
         // src/quant/mod.rs:841: d * sc * q - dmin * m (exact products)
-        v[4 * j + i] = d * sl * (float)(byte & 15u) - dmin * ml;
-        v[16 + 4 * j + i] = d * sh * (float)(byte >> 4) - dmin * mh;
+        v[8 * k + i] = d * sc * (float)(byte & 15u) - dmin * mn;
+        v[8 * k + 4 + i] = d * sc * (float)(byte >> 4) - dmin * mn;
       }
   } else if constexpr (FMT == NX_FMT_Q8_0) {
     const float d = h2f(w.m.x);
@@ -173,12 +171,12 @@ __device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, float *v) 
     const float d = h2f(w.m.x);
     const uint32_t ws[4] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t byte = (ws[j] >> (8 * i)) & 0xFFu;
-        v[4 * j + i] = (float)((int)(byte & 15u) - 8) * d;
-        v[16 + 4 * j + i] = (float)((int)(byte >> 4) - 8) * d;
+        const uint32_t byte = (ws[k] >> (8 * i)) & 0xFFu;
+        v[8 * k + i] = (float)((int)(byte & 15u) - 8) * d;
+        v[8 * k + 4 + i] = (float)((int)(byte >> 4) - 8) * d;
       }
   } else {
     const uint4 all[8] = {w.q[0], w.q[1], w.f[0], w.f[1], w.f[2], w.f[3], w.f[4], w.f[5]};
@@ -190,13 +188,6 @@ __device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, float *v) 
       v[4 * j + 3] = __uint_as_float(all[j].w);
     }
   }
-}
-
-// LDS position (within the 64-element step) of decoded value i of half h
-template <int FMT>
-__device__ __forceinline__ int w_pos(int h, int i) {
-  if constexpr (FMT == NX_FMT_Q4_K) return i < 16 ? 16 * h + i : 32 + 16 * h + (i - 16);
-  return 32 * h + i;
 }
 
 // element index (within the activation row) of K position p of step ks
@@ -278,22 +269,19 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const GemmArgs g) {
                    wrow_ok);
   };
   auto stash = [&](int ks) {
-    // activation piece i of this thread covers K positions:
-    //   Q4_K: half 0 -> low-nibble positions 0..31 (8i..8i+7), half 1 -> 32..63
-    //   others: 32h + 8i
+    // activation piece i and weight value i of this thread sit at K
+    // positions 32h + 8i and 32h + i of the step
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = FMT == NX_FMT_Q4_K ? (lh == 0 ? 8 * i : 32 + 8 * i) : 32 * lh + 8 * i;
-      *reinterpret_cast<uint4 *>(&As[lr * LDK + p]) = abuf[i];
-    }
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<uint4 *>(&As[lr * LDK + 32 * lh + 8 * i]) = abuf[i];
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) {
       float v[32];
-      w_decode<FMT>(wb[mt], ks, v);
+      w_decode<FMT>(wb[mt], ks, lh, v);
 #pragma unroll
       for (int i = 0; i < 32; i += 2) {
         const uint32_t pk = (uint32_t)Op::bits(v[i]) | ((uint32_t)Op::bits(v[i + 1]) << 16);
-        *reinterpret_cast<uint32_t *>(&Bs[mt][lr * LDK + w_pos<FMT>(lh, i)]) = pk;
+        *reinterpret_cast<uint32_t *>(&Bs[mt][lr * LDK + 32 * lh + i]) = pk;
       }
     }
   };

@@ -3,20 +3,26 @@
 //
 // Replaces the three InferenceEngine::matvec calls, the SwiGLU and the
 // weighted accumulate of dispatch_moe_ffn (src/engine/mod.rs:994-1021,
-// 775-801) for the tokens routed to each expert.  Gate/up grid: x = row
-// blocks, y = expert slot (the i-th active expert from the permutation, then
-// one slot for the shared expert).  Down grid: row blocks only; each
-// workgroup runs every slot over its rows and then combines them.
+// 775-801) for the tokens routed to each expert.
 //
 // A row group of L = LPR * KSPLIT lanes owns a run of rows.  Lane i of the
 // group owns segments i, i+L, ... of every row (see nx_device.hpp), so the
 // activations it needs are loaded into registers once per token group and
 // reused for all rows.  Rows are processed U at a time in a two-stage
 // software pipeline: the code and scale loads of the next U rows are issued
-// before the current U rows are decoded and reduced (DPP adds within the
-// group, an LDS sum across waves when KSPLIT > 1).
+// before the current U rows are decoded and reduced (DPP adds within a
+// wave's row group).
 //
-// The down projection writes each pair's output rows, then the same
+// Gate/up (k_gemv_gateup): grid x = row blocks, y = expert slot (the i-th
+// active expert from the permutation, then one slot for the shared expert);
+// the epilogue applies SwiGLU and stores the activation row of each pair.
+//
+// Down + combine (k_gemv_down): grid x = row blocks only.  Each half of a
+// 512-thread workgroup walks every (slot, token group, row stage) of its
+// slots over the workgroup's rows as one continuous pipeline, so the weight
+// stream does not drain between experts.  Each wave
+// leaves its per-row partial sums in LDS (or, for very many pairs, in a
+// global scratch area private to the workgroup); after one barrier the
 // workgroup forms out[t] = sum_r w[t,r] * y[pair(t,r)] (+ shared) for its
 // rows in route order — the reference's accumulation order, with no atomics
 // and no communication between workgroups.
@@ -44,102 +50,95 @@ struct GemvArgs {
   float *out;
   int out_stride;
   int rows_per_group;
-  uint32_t mask_lo, mask_hi;  // 0x0F0F0F0F / 0xF0F0F0F0 (Q8_0: 0x80808080 in mask_hi)
-  // combine (down projection)
+  // down projection: combine inputs, pair count, global partial-sum area
   const float *rw;
   const int32_t *rcnt;
   const int32_t *inv;
   float *final_out;
+  int npairs;
+  float *gpart;
 };
 
-template <int FMT, int LPR, int KSPLIT, int SPL, int NT, bool GATEUP>
-__global__ __launch_bounds__(256, 2) void k_gemv(const GemvArgs a) {
-  using S = Seg<FMT>;
-  using Meta = typename S::Meta;
-  constexpr int EPS = S::EPS, NXS = S::NXS;
-  constexpr int NMAT = GATEUP ? 2 : 1;
-  constexpr int L = LPR * KSPLIT;
-  constexpr int GROUPS = 256 / L;
-  constexpr int U = GATEUP ? 2 : 4;  // rows per pipeline stage
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int li = KSPLIT == 1 ? (lane % LPR) : tid;
-  const int grp = KSPLIT == 1 ? (tid / LPR) : 0;
-
-  const int n_active = a.active[a.E];
-  const int n_slots = n_active + (a.has_shared ? 1 : 0);
-  if (GATEUP && (int)blockIdx.y >= n_slots) return;  // workgroup-uniform
-  __shared__ float red[KSPLIT > 1 ? 4 * U * NMAT * NT : 1];
-
-  // gate/up: one slot per workgroup row; down: every slot, in order
-  for (int si = 0; si < (GATEUP ? 1 : n_slots); ++si) {
-  const int slot = GATEUP ? (int)blockIdx.y : si;
-  // ---- slot -> expert, pair range, matrix bases (workgroup-uniform)
+// Workgroup-uniform description of one expert slot.
+struct SlotView {
   int pair0, count, rows, cols, nseg;
-  const uint8_t *q0p, *q1p, *m0p, *m1p;
+  const uint8_t *q0, *q1, *m0, *m1;
   uint32_t rq, rm;
   bool routed;
+};
+
+__device__ __forceinline__ SlotView slot_view(const GemvArgs &a, int slot, int n_active) {
+  SlotView v;
   if (slot < n_active) {
     const int e = a.active[slot];
-    pair0 = a.offsets[e];
-    count = a.offsets[e + 1] - pair0;
-    rows = a.rows;
-    cols = a.cols;
-    nseg = a.nseg;
-    q0p = a.qs0 + (size_t)e * a.qs_stride;
-    q1p = a.qs1 + (size_t)e * a.qs_stride;
-    m0p = a.meta0 + (size_t)e * a.meta_stride;
-    m1p = a.meta1 + (size_t)e * a.meta_stride;
-    rq = a.row_qs;
-    rm = a.row_meta;
-    routed = true;
+    v.pair0 = a.offsets[e];
+    v.count = a.offsets[e + 1] - v.pair0;
+    v.rows = a.rows;
+    v.cols = a.cols;
+    v.nseg = a.nseg;
+    v.q0 = a.qs0 + (size_t)e * a.qs_stride;
+    v.q1 = a.qs1 + (size_t)e * a.qs_stride;
+    v.m0 = a.meta0 + (size_t)e * a.meta_stride;
+    v.m1 = a.meta1 + (size_t)e * a.meta_stride;
+    v.rq = a.row_qs;
+    v.rm = a.row_meta;
+    v.routed = true;
   } else {
-    pair0 = a.T * a.k;
-    count = a.T;
-    rows = a.srows;
-    cols = a.scols;
-    nseg = a.snseg;
-    q0p = a.sqs0;
-    q1p = a.sqs1;
-    m0p = a.smeta0;
-    m1p = a.smeta1;
-    rq = a.srow_qs;
-    rm = a.srow_meta;
-    routed = false;
+    v.pair0 = a.T * a.k;
+    v.count = a.T;
+    v.rows = a.srows;
+    v.cols = a.scols;
+    v.nseg = a.snseg;
+    v.q0 = a.sqs0;
+    v.q1 = a.sqs1;
+    v.m0 = a.smeta0;
+    v.m1 = a.smeta1;
+    v.rq = a.srow_qs;
+    v.rm = a.srow_meta;
+    v.routed = false;
   }
-  const int row_begin = (blockIdx.x * GROUPS + grp) * a.rows_per_group;
-  const int row_end = min(rows, row_begin + a.rows_per_group);
+  return v;
+}
 
-  // buffer resources over this expert's matrices (loads past the end read 0)
-  const __amdgpu_buffer_rsrc_t rq0 = make_rsrc(q0p, (uint32_t)rows * rq);
-  const __amdgpu_buffer_rsrc_t rq1 = make_rsrc(q1p, (uint32_t)rows * rq);
-  const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(m0p, (uint32_t)rows * rm);
-  const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(m1p, (uint32_t)rows * rm);
-
-  // this lane's segments and their byte offsets inside a row (OOB if none)
-  int jseg[SPL];
-  bool jv[SPL];
-  uint32_t off0[SPL], off1[SPL], moff[SPL];
-#pragma unroll
-  for (int m = 0; m < SPL; ++m) {
-    jseg[m] = li + m * L;
-    jv[m] = jseg[m] < nseg;
-    off0[m] = jv[m] ? seg_off(jseg[m], 0, nseg) : OOB;
-    off1[m] = jv[m] ? seg_off(jseg[m], 1, nseg) : OOB;
-    moff[m] = S::meta_off(jseg[m], jv[m]);
-  }
+// Register-resident pieces of one row group's work: its segments of a row,
+// the activations for NT tokens over those segments, and U rows of codes and
+// scales for NMAT matrices.
+template <int FMT, int L, int SPL, int NT, int U, int NMAT>
+struct RowGroup {
+  using S = Seg<FMT>;
+  using Meta = typename S::Meta;
+  using XS = typename S::X;
+  static constexpr int EPS = S::EPS;
 
   struct Stage {
     uint4 q[U][NMAT][SPL][2];
     Meta m[U][NMAT][SPL];
   };
-  // rows past row_end load zeros (their offsets are out of range) and are
-  // never stored
-  auto load = [&](Stage &st, int r0) {
+
+  int li;      // lane index within the row group
+  XS xv[SPL][NT];  // activations of this lane's segments, per token
+
+  // Issue the loads of rows r0 .. r0+U-1 of view v; rows at or past row_end
+  // (and absent segments) get out-of-range offsets and read as zero.
+  __device__ __forceinline__ void load(Stage &st, const SlotView &v, int r0, int row_end) const {
+    const __amdgpu_buffer_rsrc_t rq0 = make_rsrc(v.q0, (uint32_t)v.rows * v.rq);
+    const __amdgpu_buffer_rsrc_t rq1 = make_rsrc(v.q1, (uint32_t)v.rows * v.rq);
+    const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(v.m0, (uint32_t)v.rows * v.rm);
+    const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(v.m1, (uint32_t)v.rows * v.rm);
+    uint32_t off0[SPL], off1[SPL], moff[SPL];
+#pragma unroll
+    for (int m = 0; m < SPL; ++m) {
+      const int j = li + m * L;
+      const bool jv = j < v.nseg;
+      off0[m] = jv ? seg_off(j, 0, v.nseg) : OOB;
+      off1[m] = jv ? seg_off(j, 1, v.nseg) : OOB;
+      moff[m] = S::meta_off(j, jv);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool rv = r0 + u < row_end;
-      const uint32_t rqo = rv ? (uint32_t)(r0 + u) * rq : OOB;
-      const uint32_t rmo = rv ? (uint32_t)(r0 + u) * rm : OOB;
+      const uint32_t rqo = rv ? (uint32_t)(r0 + u) * v.rq : OOB;
+      const uint32_t rmo = rv ? (uint32_t)(r0 + u) * v.rm : OOB;
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt) {
 #pragma unroll
@@ -150,76 +149,112 @@ __global__ __launch_bounds__(256, 2) void k_gemv(const GemvArgs a) {
         }
       }
     }
-  };
+  }
 
-  for (int t0 = 0; t0 < count; t0 += NT) {
-    // ---- activations of NT tokens for this lane's segments
-    float x[SPL][NT][EPS];
-    float xs[SPL][NT][NXS];
+  // Activations of tokens t0 .. t0+NT-1 of view v over this lane's segments.
+  // row_of(t) gives the row of the activation matrix for token t of the slot;
+  // one buffer resource per row, sized to the row, so columns past the row
+  // (padding, absent segments) and absent tokens read as zero.
+  template <class RowOf>
+  __device__ __forceinline__ void load_x(const float *xbase, int xstride, const SlotView &v, int t0,
+                                         RowOf row_of) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      // one buffer resource per token row, sized to the row: columns past
-      // the row (padding, absent segments) and absent tokens read as zero
-      const bool tv = t0 + t < count;
-      const float *xrow = a.x;
-      if (tv) {
-        const int p = pair0 + t0 + t;
-        const int row = GATEUP ? (routed ? a.perm_token[p] : (t0 + t)) : p;
-        xrow = a.x + (size_t)row * a.x_stride;
-      }
-      const __amdgpu_buffer_rsrc_t xr = make_rsrc(xrow, tv ? (uint32_t)cols * 4u : 0u);
+      const bool tv = t0 + t < v.count;
+      const float *xrow = xbase;
+      if (tv) xrow = xbase + (size_t)row_of(t0 + t) * xstride;
+      const __amdgpu_buffer_rsrc_t xr = make_rsrc(xrow, tv ? (uint32_t)v.cols * 4u : 0u);
 #pragma unroll
       for (int m = 0; m < SPL; ++m) {
+        const int j = li + m * L;
+        const bool jv = j < v.nseg;
+        float x[EPS];
 #pragma unroll
-        for (int v = 0; v < EPS; v += 4) {
-          const uint32_t xo = jv[m] ? (uint32_t)S::xidx(jseg[m], v) * 4u : OOB;
+        for (int e = 0; e < EPS; e += 4) {
+          const uint32_t xo = jv ? (uint32_t)S::xidx(j, e) * 4u : OOB;
           if constexpr (FMT == NX_FMT_F32) {
             // rows of odd length: element-wise so that each load is wholly in or out
 #pragma unroll
-            for (int e = 0; e < 4; ++e) x[m][t][v + e] = __uint_as_float(bload4(xr, xo + 4u * e));
+            for (int i = 0; i < 4; ++i) x[e + i] = __uint_as_float(bload4(xr, xo + 4u * i));
           } else {
             const uint4 f = bload16(xr, xo);
-            x[m][t][v] = __uint_as_float(f.x);
-            x[m][t][v + 1] = __uint_as_float(f.y);
-            x[m][t][v + 2] = __uint_as_float(f.z);
-            x[m][t][v + 3] = __uint_as_float(f.w);
+            x[e] = __uint_as_float(f.x);
+            x[e + 1] = __uint_as_float(f.y);
+            x[e + 2] = __uint_as_float(f.z);
+            x[e + 3] = __uint_as_float(f.w);
           }
         }
-        S::xsums(x[m][t], xs[m][t]);
+        S::prep(x, xv[m][t]);
       }
     }
+  }
 
-    auto compute = [&](const Stage &st, int r0) {
-      float acc[U][NMAT][NT];
+  // Dot products of the staged rows with the activations, summed over the
+  // row group's LPR lanes (the total lands in the group's last lane).
+  template <int LPR>
+  __device__ __forceinline__ void compute(const Stage &st, float (&acc)[U][NMAT][NT]) const {
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int mt = 0; mt < NMAT; ++mt)
+      for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-          for (int t = 0; t < NT; ++t) acc[u][mt][t] = 0.f;
+        for (int t = 0; t < NT; ++t) acc[u][mt][t] = 0.f;
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int mt = 0; mt < NMAT; ++mt)
+      for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-          for (int m = 0; m < SPL; ++m)
-          {
-            S::template dot<NT>(st.q[u][mt][m][0], st.q[u][mt][m][1], st.m[u][mt][m], jseg[m],
-                                x[m], xs[m], acc[u][mt], a.mask_lo, a.mask_hi);
-            // keep each segment's decode local: without this the scheduler
-            // hoists every byte conversion of the stage and runs out of registers
-            __builtin_amdgcn_sched_barrier(0);
-          }
-      group_sum_n<LPR, U * NMAT * NT>(&acc[0][0][0]);
-      bool writer = (li % LPR) == LPR - 1;
+        for (int m = 0; m < SPL; ++m) {
+          S::template dot<NT>(st.q[u][mt][m][0], st.q[u][mt][m][1], st.m[u][mt][m], li + m * L,
+                              xv[m], acc[u][mt]);
+          // keep each segment's decode local: without this the scheduler
+          // hoists the work of the whole stage and runs out of registers
+          __builtin_amdgcn_sched_barrier(0);
+        }
+    group_sum_n<LPR, U * NMAT * NT>(&acc[0][0][0]);
+  }
+};
+
+template <int FMT, int LPR, int KSPLIT, int SPL, int NT>
+__global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
+  constexpr int L = LPR * KSPLIT;
+  constexpr int GROUPS = 256 / L;
+  constexpr int U = 2;  // rows per pipeline stage
+  using RG = RowGroup<FMT, L, SPL, NT, U, 2>;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = KSPLIT == 1 ? (tid / LPR) : 0;
+
+  const int n_active = a.active[a.E];
+  const int n_slots = n_active + (a.has_shared ? 1 : 0);
+  const int slot = blockIdx.y;
+  if (slot >= n_slots) return;  // workgroup-uniform
+  __shared__ float red[KSPLIT > 1 ? 4 * U * 2 * NT : 1];
+
+  const SlotView v = slot_view(a, slot, n_active);
+  const int row_begin = (blockIdx.x * GROUPS + grp) * a.rows_per_group;
+  const int row_end = min(v.rows, row_begin + a.rows_per_group);
+  RG g;
+  g.li = KSPLIT == 1 ? (lane % LPR) : tid;
+
+  typename RG::Stage A, B;
+  for (int t0 = 0; t0 < v.count; t0 += NT) {
+    // the first weight stage does not depend on the activations: issue it first
+    g.load(A, v, row_begin, row_end);
+    g.load_x(a.x, a.x_stride, v, t0,
+             [&](int t) { return v.routed ? a.perm_token[v.pair0 + t] : t; });
+
+    auto finish = [&](const typename RG::Stage &st, int r0) {
+      float acc[U][2][NT];
+      g.template compute<LPR>(st, acc);
+      bool writer = (g.li % LPR) == LPR - 1;
       if constexpr (KSPLIT > 1) {
         if (lane == 63) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int mt = 0; mt < NMAT; ++mt)
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-              for (int t = 0; t < NT; ++t) red[((wave * U + u) * NMAT + mt) * NT + t] = acc[u][mt][t];
+              for (int t = 0; t < NT; ++t) red[((wave * U + u) * 2 + mt) * NT + t] = acc[u][mt][t];
         }
         __syncthreads();
         writer = tid == 255;
@@ -227,12 +262,12 @@ __global__ __launch_bounds__(256, 2) void k_gemv(const GemvArgs a) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int mt = 0; mt < NMAT; ++mt)
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
               for (int t = 0; t < NT; ++t) {
                 float s = 0.f;
 #pragma unroll
-                for (int w = 0; w < KSPLIT; ++w) s += red[((w * U + u) * NMAT + mt) * NT + t];
+                for (int w = 0; w < KSPLIT; ++w) s += red[((w * U + u) * 2 + mt) * NT + t];
                 acc[u][mt][t] = s;
               }
         }
@@ -245,43 +280,145 @@ __global__ __launch_bounds__(256, 2) void k_gemv(const GemvArgs a) {
           if (r >= row_end) continue;
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
-            if (t0 + t >= count) continue;
-            const float v = GATEUP ? silu_mul(acc[u][0][t], acc[u][NMAT - 1][t]) : acc[u][0][t];
-            a.out[(size_t)(pair0 + t0 + t) * a.out_stride + r] = v;
+            if (t0 + t >= v.count) continue;
+            a.out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
+                silu_mul(acc[u][0][t], acc[u][1][t]);
           }
         }
       }
     };
 
-    Stage A, B;
-    load(A, row_begin);
+    // with KSPLIT > 1 the whole workgroup is one row group, so the trip
+    // count (and every barrier in finish) is workgroup-uniform
     for (int r = row_begin; r < row_end; r += 2 * U) {
-      load(B, r + U);
-      compute(A, r);
-      load(A, r + 2 * U);
-      compute(B, r + U);
+      g.load(B, v, r + U, row_end);
+      finish(A, r);
+      if (r + U >= row_end) break;
+      g.load(A, v, r + 2 * U, row_end);
+      finish(B, r + U);
+    }
+  }
+}
+
+// Down projection of every pair over this workgroup's rows, then the combine.
+// The workgroup is DOWN_SG halves of 256 threads; half h runs slots h,
+// h + DOWN_SG, ... over the same rows, so the experts of a token are
+// streamed side by side.  YLDS: partial sums in LDS (dynamic,
+// [KSPLIT][npairs][wg_rows]); otherwise in a.gpart at this workgroup's own
+// offset.
+constexpr int DOWN_SG = 2;
+
+template <int FMT, int LPR, int KSPLIT, int SPL, int NT, bool YLDS>
+__global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a) {
+  constexpr int L = LPR * KSPLIT;
+  constexpr int GROUPS = 256 / L;
+  constexpr int U = NT == 1 ? 4 : 2;  // rows per pipeline stage
+  using RG = RowGroup<FMT, L, SPL, NT, U, 1>;
+  extern __shared__ float ypart_lds[];
+  const int tid = threadIdx.x, half = tid >> 8, tl = tid & 255;
+  const int lane = tl & 63, wave = tl >> 6;
+  const int grp = KSPLIT == 1 ? (tl / LPR) : 0;
+  const int kpart = KSPLIT == 1 ? 0 : wave;  // which partial this wave leaves
+
+  const int n_active = a.active[a.E];
+  const int n_slots = n_active + (a.has_shared ? 1 : 0);
+  const int npairs = a.npairs;
+  const int wg_rows = GROUPS * a.rows_per_group;
+  const int rb0 = blockIdx.x * wg_rows;
+  const int nr = min(a.rows, rb0 + wg_rows) - rb0;
+  const int row_begin = rb0 + grp * a.rows_per_group;
+  const int row_end = min(a.rows, row_begin + a.rows_per_group);
+  float *ybuf = YLDS ? ypart_lds : a.gpart + (size_t)blockIdx.x * KSPLIT * npairs * wg_rows;
+
+  RG g;
+  g.li = KSPLIT == 1 ? (lane % LPR) : tl;
+  const bool writer = (g.li % LPR) == LPR - 1;
+
+  // Stage positions: (slot, first token of the group, first row).  The
+  // sequence runs over rows fastest, then token groups, then this half's
+  // slots.
+  struct Pos {
+    int si, t0, r;
+  };
+  auto advance = [&](Pos &p, SlotView &v) {
+    p.r += U;
+    if (p.r >= row_end) {
+      p.r = row_begin;
+      p.t0 += NT;
+      if (p.t0 >= v.count) {
+        p.t0 = 0;
+        p.si += DOWN_SG;
+        if (p.si < n_slots) v = slot_view(a, p.si, n_active);
+      }
+    }
+  };
+  auto finish = [&](const typename RG::Stage &st, const SlotView &v, const Pos &p) {
+    float acc[U][1][NT];
+    g.template compute<LPR>(st, acc);
+    if (writer) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = p.r + u;
+        if (r >= row_end) continue;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if (p.t0 + t >= v.count) continue;
+          ybuf[((size_t)kpart * npairs + v.pair0 + p.t0 + t) * wg_rows + (r - rb0)] = acc[u][0][t];
+        }
+      }
+    }
+  };
+
+  if (row_begin < row_end && half < n_slots) {  // uniform within the row group
+    Pos pc{half, 0, row_begin};
+    SlotView vc = slot_view(a, half, n_active);
+    Pos pl = pc;
+    SlotView vl = vc;
+    typename RG::Stage A, B;
+    g.load(A, vc, pc.r, row_end);
+    while (true) {
+      // activations of a new token group go out before the next stage's
+      // loads, so waiting for them does not wait for that stage
+      if (pc.r == row_begin)
+        g.load_x(a.x, a.x_stride, vc, pc.t0, [&](int t) { return vc.pair0 + t; });
+      advance(pl, vl);
+      if (pl.si < n_slots) g.load(B, vl, pl.r, row_end);
+      finish(A, vc, pc);
+      if (pl.si >= n_slots) break;
+      pc = pl;
+      vc = vl;
+
+      if (pc.r == row_begin)
+        g.load_x(a.x, a.x_stride, vc, pc.t0, [&](int t) { return vc.pair0 + t; });
+      advance(pl, vl);
+      if (pl.si < n_slots) g.load(A, vl, pl.r, row_end);
+      finish(B, vc, pc);
+      if (pl.si >= n_slots) break;
+      pc = pl;
+      vc = vl;
     }
   }
 
-  }  // slot loop
-
-  if constexpr (!GATEUP) {
-    // combine this workgroup's rows: out[t][h] = sum_r w[t,r] * y[pair(t,r)][h]
-    // (+ shared), in route order; the y rows were written by this workgroup
-    __syncthreads();
-    const int rb0 = blockIdx.x * GROUPS * a.rows_per_group;
-    const int nr = min(a.rows, rb0 + GROUPS * a.rows_per_group) - rb0;
-    for (int i = tid; i < nr * a.T; i += 256) {
-      const int t = i / nr, h = rb0 + (i - t * nr);
-      const int n = a.rcnt[t];
-      float acc = 0.0f;
-      for (int r = 0; r < n; ++r) {
-        const int p = a.inv[(size_t)t * a.k + r];
-        acc = acc + __fmul_rn(a.rw[(size_t)t * a.k + r], a.out[(size_t)p * a.out_stride + h]);
-      }
-      if (a.has_shared) acc = acc + a.out[((size_t)a.T * a.k + t) * a.out_stride + h];
-      a.final_out[(size_t)t * a.rows + h] = acc;
+  // combine this workgroup's rows: out[t][h] = sum_r w[t,r] * y[pair(t,r)][h]
+  // (+ shared), in route order; y = the KSPLIT partials summed in wave order
+  __syncthreads();
+  const int T = a.T;
+  for (int i = tid; i < nr * T; i += 256 * DOWN_SG) {
+    const int t = i / nr, hl = i - t * nr;
+    auto y = [&](int p) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < KSPLIT; ++w) s += ybuf[((size_t)w * npairs + p) * wg_rows + hl];
+      return s;
+    };
+    const int n = a.rcnt[t];
+    float acc = 0.0f;
+    for (int r = 0; r < n; ++r) {
+      const int p = a.inv[(size_t)t * a.k + r];
+      acc = acc + __fmul_rn(a.rw[(size_t)t * a.k + r], y(p));
     }
+    if (a.has_shared) acc = acc + y(T * a.k + t);
+    a.final_out[(size_t)t * a.rows + rb0 + hl] = acc;
   }
 }
 
@@ -291,32 +428,43 @@ struct Shape {
   int lpr, ksplit, spl;
 };
 
-template <int FMT, bool GATEUP, int NT>
-KernelFn pick_shape(const Shape &s) {
+// kernel instance for (format, tokens per group, shape, role, partials in LDS)
+template <int FMT, int NT, int LPR, int KSPLIT, int SPL>
+KernelFn inst(bool gateup, bool ylds) {
+  if (gateup) return k_gemv_gateup<FMT, LPR, KSPLIT, SPL, NT>;
+  return ylds ? k_gemv_down<FMT, LPR, KSPLIT, SPL, NT, true>
+              : k_gemv_down<FMT, LPR, KSPLIT, SPL, NT, false>;
+}
+
+template <int FMT, int NT>
+KernelFn pick_shape(bool gateup, bool ylds, const Shape &s) {
+  // two segments per lane exist only where choose_shape allows them
+  constexpr bool two = 2 * Seg<FMT>::EPS * NT <= 64;
   if (s.ksplit == 1) {
-    if (s.lpr == 16 && s.spl == 1) return k_gemv<FMT, 16, 1, 1, NT, GATEUP>;
-    if (s.lpr == 32 && s.spl == 1) return k_gemv<FMT, 32, 1, 1, NT, GATEUP>;
-    if (s.lpr == 64 && s.spl == 1) return k_gemv<FMT, 64, 1, 1, NT, GATEUP>;
-    if (s.lpr == 64 && s.spl == 2) return k_gemv<FMT, 64, 1, 2, NT, GATEUP>;
+    if (s.lpr == 16 && s.spl == 1) return inst<FMT, NT, 16, 1, 1>(gateup, ylds);
+    if (s.lpr == 32 && s.spl == 1) return inst<FMT, NT, 32, 1, 1>(gateup, ylds);
+    if (s.lpr == 64 && s.spl == 1) return inst<FMT, NT, 64, 1, 1>(gateup, ylds);
+    if constexpr (two)
+      if (s.lpr == 64 && s.spl == 2) return inst<FMT, NT, 64, 1, 2>(gateup, ylds);
   } else {
-    if (s.spl == 1) return k_gemv<FMT, 64, 4, 1, NT, GATEUP>;
-    if (s.spl == 2) return k_gemv<FMT, 64, 4, 2, NT, GATEUP>;
+    if (s.spl == 1) return inst<FMT, NT, 64, 4, 1>(gateup, ylds);
+    if constexpr (two)
+      if (s.spl == 2) return inst<FMT, NT, 64, 4, 2>(gateup, ylds);
   }
   return nullptr;
 }
 
 template <int FMT>
-KernelFn pick_fmt(bool gateup, int nt, const Shape &s) {
-  if (gateup) return nt == 1 ? pick_shape<FMT, true, 1>(s) : pick_shape<FMT, true, 2>(s);
-  return nt == 1 ? pick_shape<FMT, false, 1>(s) : pick_shape<FMT, false, 2>(s);
+KernelFn pick_fmt(bool gateup, bool ylds, int nt, const Shape &s) {
+  return nt == 1 ? pick_shape<FMT, 1>(gateup, ylds, s) : pick_shape<FMT, 2>(gateup, ylds, s);
 }
 
-KernelFn pick(int fmt, bool gateup, int nt, const Shape &s) {
+KernelFn pick(int fmt, bool gateup, bool ylds, int nt, const Shape &s) {
   switch (fmt) {
-  case NX_FMT_Q4_K: return pick_fmt<NX_FMT_Q4_K>(gateup, nt, s);
-  case NX_FMT_Q8_0: return pick_fmt<NX_FMT_Q8_0>(gateup, nt, s);
-  case NX_FMT_Q4_0: return pick_fmt<NX_FMT_Q4_0>(gateup, nt, s);
-  case NX_FMT_F32: return pick_fmt<NX_FMT_F32>(gateup, nt, s);
+  case NX_FMT_Q4_K: return pick_fmt<NX_FMT_Q4_K>(gateup, ylds, nt, s);
+  case NX_FMT_Q8_0: return pick_fmt<NX_FMT_Q8_0>(gateup, ylds, nt, s);
+  case NX_FMT_Q4_0: return pick_fmt<NX_FMT_Q4_0>(gateup, ylds, nt, s);
+  case NX_FMT_F32: return pick_fmt<NX_FMT_F32>(gateup, ylds, nt, s);
   }
   return nullptr;
 }
@@ -344,6 +492,9 @@ bool choose_shape(int nseg, int eps, int nt, Shape *s) {
   else return false;
   return true;
 }
+
+// partial sums of the down kernel stay in LDS up to this size per workgroup
+constexpr size_t kDownLdsMax = 64 * 1024;
 
 int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const nx_experts *ex = p.ex;
@@ -391,8 +542,6 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   } else {
     a.x = p.act;
     a.x_stride = p.act_stride;
-    a.out = p.ypair;
-    a.out_stride = ex->H;
   }
 
   const int nseg = a.nseg > a.snseg ? a.nseg : a.snseg;
@@ -404,38 +553,51 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const int groups_per_wg = 256 / L;
   const int slots_max = (ex->E < p.T * p.k ? ex->E : p.T * p.k) + (has_shared ? 1 : 0);
   const int rows = a.rows > a.srows ? a.rows : a.srows;
-  KernelFn fn = pick(ex->fmt, gateup, nt, sh);
-  if (!fn) return fail(NX_ERR_UNSUPPORTED, "no GEMV kernel instance for this shape");
+  // residency is register-bound (eight waves per CU by launch bounds)
+  const int threads = gateup ? 256 : 256 * DOWN_SG;
+  KernelFn probe = pick(ex->fmt, gateup, true, nt, sh);
+  if (!probe) return fail(NX_ERR_UNSUPPORTED, "no GEMV kernel instance for this shape");
   int wg_per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wg_per_cu, reinterpret_cast<const void *>(fn),
-                                                   256, 0) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wg_per_cu, reinterpret_cast<const void *>(probe),
+                                                   threads, 0) != hipSuccess ||
       wg_per_cu < 1) {
     (void)hipGetLastError();
     wg_per_cu = 1;
   }
   // gate/up spreads slots over grid.y; down runs all slots inside each
-  // workgroup.  Size the row runs so the launch is about one round of
-  // resident workgroups, each with a long software pipeline.
+  // workgroup.  Size the row runs so the launch is one round of resident
+  // workgroups with equal work each.
   const long work_rows = gateup ? (long)rows * slots_max : (long)rows;
-  const int step = gateup ? 4 : 8;  // rows per pipeline round (2 stages x U)
   const long groups = (long)c->num_cu * wg_per_cu * groups_per_wg;
   long rpg = (work_rows + groups - 1) / groups;
-  rpg = (rpg + step - 1) / step * step;
-  if (rpg < step) rpg = step;
+  if (rpg < 1) rpg = 1;
   a.rows_per_group = (int)rpg;
-  a.mask_lo = 0x0F0F0F0Fu;
-  a.mask_hi = ex->fmt == NX_FMT_Q8_0 ? 0x80808080u : 0xF0F0F0F0u;
   const long rows_per_wg = rpg * groups_per_wg;
   const unsigned gx = (unsigned)((rows + rows_per_wg - 1) / rows_per_wg);
-  if (!gateup) {
-    a.rw = p.rw;
-    a.rcnt = p.rcnt;
-    a.inv = p.inv;
-    a.final_out = p.out;
+
+  if (gateup) {
+    const dim3 grid(gx, (unsigned)slots_max);
+    return launch(c, "gemv_gateup",
+                  [&] { hipLaunchKernelGGL(probe, grid, dim3(256), 0, c->stream, a); });
   }
-  const char *name = gateup ? "gemv_gateup" : "gemv_down_combine";
-  const dim3 grid(gx, gateup ? (unsigned)slots_max : 1u);
-  return launch(c, name, [&] { hipLaunchKernelGGL(fn, grid, dim3(256), 0, c->stream, a); });
+
+  a.rw = p.rw;
+  a.rcnt = p.rcnt;
+  a.inv = p.inv;
+  a.final_out = p.out;
+  a.npairs = (int)((long)p.T * p.k + (has_shared ? p.T : 0));
+  const size_t part_bytes = (size_t)sh.ksplit * a.npairs * rows_per_wg * sizeof(float);
+  const bool ylds = part_bytes <= kDownLdsMax;
+  KernelFn fn = pick(ex->fmt, false, ylds, nt, sh);
+  if (!fn) return fail(NX_ERR_UNSUPPORTED, "no GEMV kernel instance for this shape");
+  if (!ylds) {
+    void *gp = nullptr;
+    NX_TRY(ws_get(c, WS_YPAIR, part_bytes * gx, &gp));
+    a.gpart = static_cast<float *>(gp);
+  }
+  const unsigned lds = ylds ? (unsigned)part_bytes : 0u;
+  return launch(c, "gemv_down_combine",
+                [&] { hipLaunchKernelGGL(fn, dim3(gx), dim3(threads), lds, c->stream, a); });
 }
 
 }  // namespace

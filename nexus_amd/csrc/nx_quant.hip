@@ -237,21 +237,35 @@ __global__ __launch_bounds__(256) void k_repack_codes(const uint8_t *__restrict_
         const int c = 8 * j + 4 * h + v;
         df[v] = c < cols ? sf[c] : 0.0f;
       }
+    } else if constexpr (FMT == NX_FMT_Q8_0) {
+      const int nb = cols / 32;
+      const uint8_t *b = src + ((size_t)r * nb + j) * 34 + 2 + h * 16;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) dst[v] = b[v];
     } else {
-      const uint8_t *b = nullptr;
+      // the 32 codes of one sub-block in element order ...
+      uint8_t q[32];
       if constexpr (FMT == NX_FMT_Q4_K) {
+        // qs byte 32s + i: element 32s + i (low nibble), 128 + 32s + i (high)
         const int nb = cols / 256;
-        b = src + ((size_t)r * nb + (j >> 2)) * 144 + 16 + (j & 3) * 32 + h * 16;
-      } else if constexpr (FMT == NX_FMT_Q8_0) {
-        const int nb = cols / 32;
-        b = src + ((size_t)r * nb + j) * 34 + 2 + h * 16;
-      } else {  // Q4_0: segment j = blocks 2j, 2j+1
+        const uint8_t *b = src + ((size_t)r * nb + (j >> 2)) * 144 + 16 + (j & 3) * 32;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) q[i] = h ? (b[i] >> 4) : (b[i] & 15);
+      } else {  // Q4_0: segment j = blocks 2j, 2j+1; byte i: element i (low), 16 + i (high)
         const int nb = cols / 32;
         const int blk = 2 * j + h;
-        if (blk < nb) b = src + ((size_t)r * nb + blk) * 18 + 2;
-      }
+        const uint8_t *b = blk < nb ? src + ((size_t)r * nb + blk) * 18 + 2 : nullptr;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) dst[v] = b ? b[v] : (uint8_t)0;
+        for (int i = 0; i < 16; ++i) {
+          q[i] = b ? (b[i] & 15) : 0;
+          q[16 + i] = b ? (b[i] >> 4) : 0;
+        }
+      }
+      // ... stored as byte 4k+i = element 8k+i | element 8k+4+i << 4
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[4 * k + i] = (uint8_t)(q[8 * k + i] | (q[8 * k + 4 + i] << 4));
     }
   }
 }
