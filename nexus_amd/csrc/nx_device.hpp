@@ -11,7 +11,8 @@
 //        (half 1); y = (q - 8) * d.
 //   In both 4-bit formats the 16 bytes of a half hold one 32-element
 //   sub-block: byte 4k+i has element 8k+i in its low nibble and element
-//   8k+4+i in its high nibble.
+//   8k+4+i in its high nibble, each stored as q ^ 8 (the two's-complement
+//   4-bit form of q - 8).
 //   Q8_0 (src/quant/mod.rs:689-703): segment j = block j in element order,
 //        y = (int8)q * d.
 //   F32: segment j = floats 8j .. 8j+7.
@@ -76,14 +77,14 @@ __device__ __forceinline__ uint32_t seg_off(int j, int h, int nseg) {
 // X is computed with the 1.5*2^23 rounding constant: the bits of
 // fma(x, 2^(22-E), 1.5*2^23) are 0x4B400000 + X.
 //
-// 4-bit codes (Q4_K, Q4_0): Y = X + 2^23 lies in [0, 2^24) and is split into
-// six 4-bit digits.  The repacked code dword k of a 32-element sub-block holds
-// elements 8k+i (low nibble of byte i) and 8k+4+i (high nibble); digit plane
-// d holds digit d of the same elements at the same nibble positions, so one
-// v_dot8_u32_u4 per digit gives sum_i q_i * digit_d(Y_i), and one more with
-// 0x11111111 gives sum_i q_i.  Then sum_i q_i X_i = L + 4096 * H with
-// L = a0 + 16 a1 + 256 a2 and H = a3 + 16 a4 + 256 a5 - 2048 * sum q (all
-// exact in 32-bit integers), rounded once to float.
+// 4-bit codes (Q4_K, Q4_0) are stored as signed nibbles c = q - 8.  X is
+// split into six balanced 4-bit digits D_d in [-8, 8): Z = X + 0x888888 lies
+// in [0, 2^24) and D_d = digit_d(Z) - 8, the signed nibble digit_d(Z) ^ 8.
+// The repacked code dword k of a 32-element sub-block holds elements 8k+i
+// (low nibble of byte i) and 8k+4+i (high nibble); digit plane d holds D_d of
+// the same elements at the same nibble positions, so one v_dot8_i32_i4 per
+// digit gives a_d = sum_i c_i D_d,i, and sum_i c_i X_i = sum_d 16^d a_d is
+// exact in 32 bits; then sum_i q_i x_i = 2^(E-22) * that + 8 * sum_i x_i.
 //
 // Q8_0: Z = X + 0x808080 has base-256 digits z_d in [0, 256); z_d - 128 =
 // (z_d ^ 0x80) as a signed byte is a balanced digit D_d with X = D0 + 256 D1 +
@@ -117,39 +118,73 @@ __device__ __forceinline__ void byte_transpose4(const uint32_t *y, uint32_t &b0,
   b2 = __builtin_amdgcn_perm(u23, u01, 0x05040100u);
 }
 
+// 8 activations (one code dword) -> their six 4-bit digit-plane dwords
+__device__ __forceinline__ void plane4_dword(const float *x, float sc, uint32_t (&o)[6]) {
+  uint32_t y[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    y[i] = (__float_as_uint(fmaf(x[i], sc, 12582912.0f)) - (0x4B400000u - 0x888888u)) ^ 0x888888u;
+  uint32_t lo[3], hi[3];
+  byte_transpose4(y, lo[0], lo[1], lo[2]);
+  byte_transpose4(y + 4, hi[0], hi[1], hi[2]);
+  constexpr uint32_t M = 0x0F0F0F0Fu;
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    o[2 * b] = (lo[b] & M) | ((hi[b] << 4) & ~M);
+    o[2 * b + 1] = ((lo[b] >> 4) & M) | (hi[b] & ~M);
+  }
+}
+
 // 32 activations of one 4-bit sub-block -> digit planes p[digit][dword]
 __device__ __forceinline__ void planes4(const float *x, float sc, uint32_t (&p)[6][4]) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    uint32_t y[8];
+    uint32_t o[6];
+    plane4_dword(x + 8 * k, sc, o);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      y[i] = __float_as_uint(fmaf(x[8 * k + i], sc, 12582912.0f)) - 0x4AC00000u;
-    uint32_t lo[3], hi[3];
-    byte_transpose4(y, lo[0], lo[1], lo[2]);
-    byte_transpose4(y + 4, hi[0], hi[1], hi[2]);
-    constexpr uint32_t M = 0x0F0F0F0Fu;
-#pragma unroll
-    for (int b = 0; b < 3; ++b) {
-      p[2 * b][k] = (lo[b] & M) | ((hi[b] << 4) & ~M);
-      p[2 * b + 1][k] = ((lo[b] >> 4) & M) | (hi[b] & ~M);
-    }
+    for (int d = 0; d < 6; ++d) p[d][k] = o[d];
   }
 }
 
-// sum_i q_i X_i over one 4-bit sub-block (codes w, planes p)
-__device__ __forceinline__ float sumqx4(const uint4 &w, const uint32_t (&p)[6][4]) {
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-  uint32_t a[6] = {0, 0, 0, 0, 0, 0}, sq = 0;
+// 4 activations (one Q8_0 code dword) -> their three byte-digit plane dwords
+__device__ __forceinline__ void plane8_dword(const float *x, float sc, uint32_t &p0, uint32_t &p1,
+                                             uint32_t &p2) {
+  uint32_t z[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int i = 0; i < 4; ++i)
+    z[i] = (__float_as_uint(fmaf(x[i], sc, 12582912.0f)) - (0x4B400000u - 0x808080u)) ^ 0x808080u;
+  byte_transpose4(z, p0, p1, p2);
+}
+
+// Per-token accumulator state of the integer dot.  The signed dot
+// instructions of gfx950 accumulate in place (v_dot8c / v_dot4c).
+//   4-bit: each sub-block's digits are accumulated Horner-style into one
+//     register, acc = 16 * acc + sum_i c_i D_d,i for d = 5 .. 0, which ends as
+//     sum_i c_i X_i exactly (|sum| <= 32 * 8 * 2^22 < 2^31).
+//   Q8_0: the sum does not fit in 32 bits, so D1 and D0 share one register
+//     (256 * a1 + a0, < 2^28) and D2 has its own; these run for the whole
+//     kernel and each segment's sums are differences of snapshots taken
+//     modulo 2^32 (exact, since one segment's true sums fit).
+struct Run4 {};
+struct Run8 {
+  int32_t i, a2;
+  uint32_t si, sa2;  // last snapshot
+};
+template <class R>
+__device__ __forceinline__ void run_init(R &) {}
+__device__ __forceinline__ void run_init(Run8 &r) { r.i = r.a2 = 0, r.si = r.sa2 = 0; }
+
+// sum_i c_i X_i over one 4-bit sub-block (signed codes w, planes p)
+__device__ __forceinline__ float sumcx4(const uint4 &w, const uint32_t (&p)[6][4], Run4 &) {
+  const int ws[4] = {(int)w.x, (int)w.y, (int)w.z, (int)w.w};
+  int32_t acc = 0;
 #pragma unroll
-    for (int d = 0; d < 6; ++d) a[d] = __builtin_amdgcn_udot8(ws[k], p[d][k], a[d], false);
-    sq = __builtin_amdgcn_udot8(ws[k], 0x11111111u, sq, false);
+  for (int d = 5; d >= 0; --d) {
+    if (d < 5) acc = (int32_t)((uint32_t)acc << 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_sdot8(ws[k], (int)p[d][k], acc, false);
   }
-  const int32_t L = (int32_t)(a[0] + (a[1] << 4) + (a[2] << 8));
-  const int32_t H = (int32_t)(a[3] + (a[4] << 4) + (a[5] << 8)) - (int32_t)(sq << 11);
-  return fmaf((float)H, 4096.0f, (float)L);
+  return (float)acc;
 }
 
 // activations of one 64-element 4-bit segment (two sub-blocks)
@@ -158,6 +193,43 @@ struct X4 {
   float post;  // 2^(E-22), or NaN for non-finite activations
   float s[2];  // sub-block sums of x
 };
+
+// ---- Quad-cooperative preparation: the lanes 4i .. 4i+3 of a wave build one
+// segment's operand together, lane q from the q-th quarter of its elements
+// (EPS/4 consecutive values of the segment order); the block exponent and the
+// sums come from quad DPP reductions.  o points into LDS.
+__device__ __forceinline__ float quad_max(float m) {
+  m = fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0xB1, 0xF, 0xF, true)));
+  return fmaxf(m, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(m), 0x4E, 0xF, 0xF, true)));
+}
+__device__ __forceinline__ float quad_pair_sum(float v) {  // lanes (0,1), (2,3)
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float quad_swap_halves(float v) {  // lanes (0,1) <-> (2,3)
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
+}
+
+// quarter q of a 4-bit segment = dwords 2(q&1), 2(q&1)+1 of sub-block q>>1
+__device__ __forceinline__ void prep4_quarter(const float *x, int q, X4 *o) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s += x[i];
+  const float sp = quad_pair_sum(s);        // this sub-block
+  const float sa = sp + quad_swap_halves(sp);  // the segment
+  const int e = blk_exp(quad_max(abs_max(x, 16)));
+  const float sc = __builtin_amdgcn_ldexpf(1.0f, 22 - e);
+  const int h = q >> 1, k0 = (q & 1) * 2;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    uint32_t pd[6];
+    plane4_dword(x + 8 * kk, sc, pd);
+#pragma unroll
+    for (int d = 0; d < 6; ++d) o->p[h][d][k0 + kk] = pd[d];
+  }
+  if ((q & 1) == 0) o->s[h] = sp;
+  if (q == 0)
+    o->post = fabsf(sa) <= 3.4e38f ? __builtin_amdgcn_ldexpf(1.0f, e - 22) : __builtin_nanf("");
+}
 
 __device__ __forceinline__ void prep4(const float *x, X4 &o) {
   float a = 0.f, b = 0.f;
@@ -182,6 +254,7 @@ struct Seg<NX_FMT_Q4_K> {
   static constexpr int EPS = 64;  // elements per segment
   using Meta = uint4;
   using X = X4;
+  using Run = Run4;
   // segment element v: sub-block s = j%4 (v < 32), sub-block s+4 (v >= 32)
   __device__ __forceinline__ static int xidx(int j, int v) {
     return (j >> 2) * 256 + (j & 3) * 32 + (v & 31) + ((v >> 5) << 7);
@@ -194,12 +267,15 @@ struct Seg<NX_FMT_Q4_K> {
     return bload16(r, off);
   }
   __device__ __forceinline__ static void prep(const float *x, X &o) { prep4(x, o); }
+  __device__ __forceinline__ static void prep_quarter(const float *x, int q, X *o) {
+    prep4_quarter(x, q, o);
+  }
   // sum over the segment of w*x for NT tokens; src/quant/mod.rs:841 gives
-  // w = d*sc*q - dmin*m per element, summed here as
-  // d*(sc_a*sum q x + sc_b*sum q x) - dmin*(m_a*sum x + m_b*sum x)
+  // w = d*sc*q - dmin*m per element, summed here with q = c + 8 as
+  // d*(sc_a*sum c x + sc_b*sum c x) + (8*d*sc - dmin*m) * sum x per sub-block
   template <int NT>
   __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m,
-                                             int j, const X *xv, float *acc) {
+                                             int j, const X *xv, Run *run, float *acc) {
     const float d = h2f(m.x & 0xFFFFu), dmin = h2f(m.x >> 16);
     const int s = j & 3;
     const uint32_t b0 = (m.y >> (8 * s)) & 0xFFu;  // scales12[s]
@@ -208,12 +284,13 @@ struct Seg<NX_FMT_Q4_K> {
     const float sa = (float)(b0 & 63u), ma = (float)(b4 & 63u);
     const float sb = (float)((b8 & 15u) | ((b0 >> 6) << 4));
     const float mb = (float)((b8 >> 4) | ((b4 >> 6) << 4));
+    const float ka = 8.0f * d * sa - dmin * ma, kb = 8.0f * d * sb - dmin * mb;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const float fa = sumqx4(q0, xv[t].p[0]);
-      const float fb = sumqx4(q1, xv[t].p[1]);
-      const float qx = fmaf(sa, fa, sb * fb) * d * xv[t].post;
-      acc[t] += qx - dmin * fmaf(ma, xv[t].s[0], mb * xv[t].s[1]);
+      const float fa = sumcx4(q0, xv[t].p[0], run[t]);
+      const float fb = sumcx4(q1, xv[t].p[1], run[t]);
+      const float cx = fmaf(sa, fa, sb * fb) * (d * xv[t].post);
+      acc[t] += cx + fmaf(ka, xv[t].s[0], kb * xv[t].s[1]);
     }
   }
 };
@@ -222,6 +299,7 @@ template <>
 struct Seg<NX_FMT_Q8_0> {
   static constexpr int EPS = 32;
   using Meta = uint32_t;
+  using Run = Run8;
   struct X {
     uint32_t p[3][8];
     float post;
@@ -243,30 +321,53 @@ struct Seg<NX_FMT_Q8_0> {
     const float sc = __builtin_amdgcn_ldexpf(1.0f, 22 - e);
     o.post = fabsf(a) <= 3.4e38f ? __builtin_amdgcn_ldexpf(1.0f, e - 22) : __builtin_nanf("");
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      uint32_t z[4];
+    for (int k = 0; k < 8; ++k) plane8_dword(x + 4 * k, sc, o.p[0][k], o.p[1][k], o.p[2][k]);
+  }
+  // quarter q = dwords 2q, 2q+1
+  __device__ __forceinline__ static void prep_quarter(const float *x, int q, X *o) {
+    float s = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        z[i] = (__float_as_uint(fmaf(x[4 * k + i], sc, 12582912.0f)) - (0x4B400000u - 0x808080u)) ^
-               0x808080u;
-      byte_transpose4(z, o.p[0][k], o.p[1][k], o.p[2][k]);
+    for (int i = 0; i < 8; ++i) s += x[i];
+    const float sa = quad_pair_sum(s) + quad_swap_halves(quad_pair_sum(s));
+    const int e = blk_exp(quad_max(abs_max(x, 8)));
+    const float sc = __builtin_amdgcn_ldexpf(1.0f, 22 - e);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      uint32_t a, b, c;
+      plane8_dword(x + 4 * kk, sc, a, b, c);
+      o->p[0][2 * q + kk] = a;
+      o->p[1][2 * q + kk] = b;
+      o->p[2][2 * q + kk] = c;
     }
+    if (q == 0)
+      o->post = fabsf(sa) <= 3.4e38f ? __builtin_amdgcn_ldexpf(1.0f, e - 22) : __builtin_nanf("");
   }
   // src/quant/mod.rs:689-703: w = (int8)q * d
   template <int NT>
   __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m, int,
-                                             const X *xv, float *acc) {
+                                             const X *xv, Run *run, float *acc) {
     const float d = h2f(m);
     const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      int32_t a[3] = {0, 0, 0};
+      Run8 &r = run[t];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        r.a2 = __builtin_amdgcn_sdot4((int)w[k], (int)xv[t].p[2][k], r.a2, false);
+        r.i = __builtin_amdgcn_sdot4((int)w[k], (int)xv[t].p[1][k], r.i, false);
+      }
+      // the shared register holds 256 * (sum over D1) + (sum over D0)
+      r.i = (int32_t)((uint32_t)r.i << 8);
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-#pragma unroll
-        for (int dg = 0; dg < 3; ++dg)
-          a[dg] = __builtin_amdgcn_sdot4((int)w[k], (int)xv[t].p[dg][k], a[dg], false);
-      const float f = fmaf((float)a[2], 65536.0f, (float)(a[0] + (a[1] << 8)));
+        r.i = __builtin_amdgcn_sdot4((int)w[k], (int)xv[t].p[0][k], r.i, false);
+      // this segment's sums (the shift also scaled the previous value P by
+      // 256): |256 * D1 part + D0 part| < 2^28, |D2 part| < 2^19
+      const int32_t di = (int32_t)((uint32_t)r.i - (r.si << 8));
+      const int32_t d2 = (int32_t)((uint32_t)r.a2 - r.sa2);
+      r.si = (uint32_t)r.i;
+      r.sa2 = (uint32_t)r.a2;
+      const float f = fmaf((float)d2, 65536.0f, (float)di);
       acc[t] += f * d * xv[t].post;
     }
   }
@@ -277,6 +378,7 @@ struct Seg<NX_FMT_Q4_0> {
   static constexpr int EPS = 64;
   using Meta = uint32_t;  // two f16 scales (blocks 2j, 2j+1)
   using X = X4;
+  using Run = Run4;
   __device__ __forceinline__ static int xidx(int j, int v) { return j * 64 + v; }
   __device__ __forceinline__ static uint32_t meta_off(int j, bool valid) {
     return valid ? (uint32_t)(j * 4) : OOB;
@@ -285,17 +387,19 @@ struct Seg<NX_FMT_Q4_0> {
     return bload4(r, off);
   }
   __device__ __forceinline__ static void prep(const float *x, X &o) { prep4(x, o); }
-  // src/quant/mod.rs:723-745: w = (q - 8) * d per block
+  __device__ __forceinline__ static void prep_quarter(const float *x, int q, X *o) {
+    prep4_quarter(x, q, o);
+  }
+  // src/quant/mod.rs:723-745: w = (q - 8) * d per block, and c = q - 8
   template <int NT>
   __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m, int,
-                                             const X *xv, float *acc) {
+                                             const X *xv, Run *run, float *acc) {
     const float d0 = h2f(m & 0xFFFFu), d1 = h2f(m >> 16);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const float fa = sumqx4(q0, xv[t].p[0]);
-      const float fb = sumqx4(q1, xv[t].p[1]);
-      const float qx = fmaf(d0, fa, d1 * fb) * xv[t].post;
-      acc[t] += qx - 8.0f * fmaf(d0, xv[t].s[0], d1 * xv[t].s[1]);
+      const float fa = sumcx4(q0, xv[t].p[0], run[t]);
+      const float fb = sumcx4(q1, xv[t].p[1], run[t]);
+      acc[t] += fmaf(d0, fa, d1 * fb) * xv[t].post;
     }
   }
 };
@@ -304,6 +408,7 @@ template <>
 struct Seg<NX_FMT_F32> {
   static constexpr int EPS = 8;
   using Meta = uint32_t;
+  struct Run {};
   struct X {
     float x[8];
   };
@@ -314,9 +419,10 @@ struct Seg<NX_FMT_F32> {
 #pragma unroll
     for (int i = 0; i < 8; ++i) o.x[i] = x[i];
   }
+  __device__ __forceinline__ static void prep_quarter(const float *, int, X *) {}
   template <int NT>
   __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &, int,
-                                             const X *xv, float *acc) {
+                                             const X *xv, Run *, float *acc) {
     const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -374,8 +480,12 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// SwiGLU: silu(g) * u = g * u / (1 + e^-g), with the hardware exp2 and
+// reciprocal (about 1 ulp each); g -> -inf gives g*u*0 (NaN for infinite g,
+// as the quotient form does)
 __device__ __forceinline__ float silu_mul(float g, float u) {
-  return (g / (1.0f + expf(-g))) * u;
+  const float e = __builtin_amdgcn_exp2f(-1.4426950408889634f * g);
+  return (g * u) * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 }  // namespace nx

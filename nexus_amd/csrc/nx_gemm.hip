@@ -153,7 +153,8 @@ __device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, int h, flo
     for (int k = 0; k < 4; ++k)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t byte = (ws[k] >> (8 * i)) & 0xFFu;
+        // stored nibbles are q ^ 8
+        const uint32_t byte = ((ws[k] >> (8 * i)) & 0xFFu) ^ 0x88u;
         // src/quant/mod.rs:841: d * sc * q - dmin * m (exact products)
         v[8 * k + i] = d * sc * (float)(byte & 15u) - dmin * mn;
         v[8 * k + 4 + i] = d * sc * (float)(byte >> 4) - dmin * mn;
@@ -174,7 +175,7 @@ __device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, int h, flo
     for (int k = 0; k < 4; ++k)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t byte = (ws[k] >> (8 * i)) & 0xFFu;
+        const uint32_t byte = ((ws[k] >> (8 * i)) & 0xFFu) ^ 0x88u;  // stored nibbles are q ^ 8
         v[8 * k + i] = (float)((int)(byte & 15u) - 8) * d;
         v[8 * k + 4 + i] = (float)((int)(byte >> 4) - 8) * d;
       }

@@ -117,14 +117,21 @@ struct RowGroup {
 
   int li;      // lane index within the row group
   XS xv[SPL][NT];  // activations of this lane's segments, per token
+  typename S::Run run[NT];  // running integer dot sums, per token
+
+  __device__ __forceinline__ void init(int lane_index) {
+    li = lane_index;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) run_init(run[t]);
+  }
 
   // Issue the loads of rows r0 .. r0+U-1 of view v; rows at or past row_end
-  // (and absent segments) get out-of-range offsets and read as zero.
+  // (and absent segments) read as zero.  When a row group spans whole waves
+  // (L >= 64) the rows are wave-uniform: each row gets its own buffer
+  // resource (size 0 past row_end), built on the scalar unit, and the lane
+  // offsets stay constant.  Otherwise rows differ within a wave and the row
+  // offset is added per lane.
   __device__ __forceinline__ void load(Stage &st, const SlotView &v, int r0, int row_end) const {
-    const __amdgpu_buffer_rsrc_t rq0 = make_rsrc(v.q0, (uint32_t)v.rows * v.rq);
-    const __amdgpu_buffer_rsrc_t rq1 = make_rsrc(v.q1, (uint32_t)v.rows * v.rq);
-    const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(v.m0, (uint32_t)v.rows * v.rm);
-    const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(v.m1, (uint32_t)v.rows * v.rm);
     uint32_t off0[SPL], off1[SPL], moff[SPL];
 #pragma unroll
     for (int m = 0; m < SPL; ++m) {
@@ -134,18 +141,44 @@ struct RowGroup {
       off1[m] = jv ? seg_off(j, 1, v.nseg) : OOB;
       moff[m] = S::meta_off(j, jv);
     }
+    if constexpr (L >= 64) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool rv = r0 + u < row_end;
-      const uint32_t rqo = rv ? (uint32_t)(r0 + u) * v.rq : OOB;
-      const uint32_t rmo = rv ? (uint32_t)(r0 + u) * v.rm : OOB;
+      for (int u = 0; u < U; ++u) {
+        const int r = r0 + u;
+        const bool rv = r < row_end;
+        const uint32_t nq = rv ? v.rq : 0u, nm = rv ? v.rm : 0u;
+        const __amdgpu_buffer_rsrc_t rq0 = make_rsrc(v.q0 + (size_t)r * v.rq, nq);
+        const __amdgpu_buffer_rsrc_t rq1 = make_rsrc(v.q1 + (size_t)r * v.rq, nq);
+        const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(v.m0 + (size_t)r * v.rm, nm);
+        const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(v.m1 + (size_t)r * v.rm, nm);
 #pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) {
+        for (int mt = 0; mt < NMAT; ++mt) {
 #pragma unroll
-        for (int m = 0; m < SPL; ++m) {
-          st.q[u][mt][m][0] = bload16(mt == 0 ? rq0 : rq1, rqo + off0[m]);
-          st.q[u][mt][m][1] = bload16(mt == 0 ? rq0 : rq1, rqo + off1[m]);
-          st.m[u][mt][m] = S::load_meta(mt == 0 ? rm0 : rm1, rmo + moff[m]);
+          for (int m = 0; m < SPL; ++m) {
+            st.q[u][mt][m][0] = bload16(mt == 0 ? rq0 : rq1, off0[m]);
+            st.q[u][mt][m][1] = bload16(mt == 0 ? rq0 : rq1, off1[m]);
+            st.m[u][mt][m] = S::load_meta(mt == 0 ? rm0 : rm1, moff[m]);
+          }
+        }
+      }
+    } else {
+      const __amdgpu_buffer_rsrc_t rq0 = make_rsrc(v.q0, (uint32_t)v.rows * v.rq);
+      const __amdgpu_buffer_rsrc_t rq1 = make_rsrc(v.q1, (uint32_t)v.rows * v.rq);
+      const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(v.m0, (uint32_t)v.rows * v.rm);
+      const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(v.m1, (uint32_t)v.rows * v.rm);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool rv = r0 + u < row_end;
+        const uint32_t rqo = rv ? (uint32_t)(r0 + u) * v.rq : OOB;
+        const uint32_t rmo = rv ? (uint32_t)(r0 + u) * v.rm : OOB;
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt) {
+#pragma unroll
+          for (int m = 0; m < SPL; ++m) {
+            st.q[u][mt][m][0] = bload16(mt == 0 ? rq0 : rq1, rqo + off0[m]);
+            st.q[u][mt][m][1] = bload16(mt == 0 ? rq0 : rq1, rqo + off1[m]);
+            st.m[u][mt][m] = S::load_meta(mt == 0 ? rm0 : rm1, rmo + moff[m]);
+          }
         }
       }
     }
@@ -189,10 +222,52 @@ struct RowGroup {
     }
   }
 
+  // Workgroup-cooperative activations, for row groups of one whole wave
+  // (L == 64, SPL == 1): every wave of the workgroup owns the same 64
+  // segments, so the workgroup builds each segment's operand once in LDS.
+  // Thread tid loads quarter tid%4 of segment tid/4 (coop_issue, before the
+  // weight loads so that its loads are not queued behind them), then the
+  // quads build the operands (coop_finish) and every lane copies its own.
+  static constexpr int XQ = EPS / 4;                        // values per quarter
+  static constexpr int XW = (int)((sizeof(XS) + 15) / 16);  // 16-byte words per operand
+
+  template <class RowOf>
+  __device__ __forceinline__ void coop_issue(float (&xq)[NT][XQ], const float *xbase, int xstride,
+                                             const SlotView &v, int t0, RowOf row_of,
+                                             int tid) const {
+    const int sgm = tid >> 2, q = tid & 3;
+    const bool jv = sgm < v.nseg;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const bool tv = t0 + t < v.count;
+      const float *xrow = xbase;
+      if (tv) xrow = xbase + (size_t)row_of(t0 + t) * xstride;
+      const __amdgpu_buffer_rsrc_t xr = make_rsrc(xrow, tv ? (uint32_t)v.cols * 4u : 0u);
+#pragma unroll
+      for (int e = 0; e < XQ; e += 4) {
+        const uint4 f = bload16(xr, jv ? (uint32_t)S::xidx(sgm, q * XQ + e) * 4u : OOB);
+        xq[t][e] = __uint_as_float(f.x);
+        xq[t][e + 1] = __uint_as_float(f.y);
+        xq[t][e + 2] = __uint_as_float(f.z);
+        xq[t][e + 3] = __uint_as_float(f.w);
+      }
+    }
+  }
+  __device__ __forceinline__ void coop_finish(const float (&xq)[NT][XQ], uint4 *xsh, int tid) {
+    const int sgm = tid >> 2, q = tid & 3;
+    __syncthreads();  // the previous token group's operands have been copied
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      S::prep_quarter(xq[t], q, reinterpret_cast<XS *>(xsh + (t * 64 + sgm) * XW));
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) xv[0][t] = *reinterpret_cast<const XS *>(xsh + (t * 64 + li) * XW);
+  }
+
   // Dot products of the staged rows with the activations, summed over the
   // row group's LPR lanes (the total lands in the group's last lane).
   template <int LPR>
-  __device__ __forceinline__ void compute(const Stage &st, float (&acc)[U][NMAT][NT]) const {
+  __device__ __forceinline__ void compute(const Stage &st, float (&acc)[U][NMAT][NT]) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -206,7 +281,7 @@ struct RowGroup {
 #pragma unroll
         for (int m = 0; m < SPL; ++m) {
           S::template dot<NT>(st.q[u][mt][m][0], st.q[u][mt][m][1], st.m[u][mt][m], li + m * L,
-                              xv[m], acc[u][mt]);
+                              xv[m], run, acc[u][mt]);
           // keep each segment's decode local: without this the scheduler
           // hoists the work of the whole stage and runs out of registers
           __builtin_amdgcn_sched_barrier(0);
@@ -220,9 +295,12 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   constexpr int L = LPR * KSPLIT;
   constexpr int GROUPS = 256 / L;
   constexpr int U = 2;  // rows per pipeline stage
+  constexpr int S = 2;  // stages (S - 1 of them in flight while one is decoded)
   using RG = RowGroup<FMT, L, SPL, NT, U, 2>;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int grp = KSPLIT == 1 ? (tid / LPR) : 0;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // wave index, known to the compiler as wave-uniform
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = KSPLIT > 1 ? 0 : (LPR == 64 ? wave : tid / LPR);
 
   const int n_active = a.active[a.E];
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
@@ -230,18 +308,31 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   if (slot >= n_slots) return;  // workgroup-uniform
   __shared__ float red[KSPLIT > 1 ? 4 * U * 2 * NT : 1];
 
+  // one wave per row group: the workgroup shares the activation operands
+  constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32;
+  __shared__ uint4 xsh[COOP ? NT * 64 * RG::XW : 1];
+
   const SlotView v = slot_view(a, slot, n_active);
   const int row_begin = (blockIdx.x * GROUPS + grp) * a.rows_per_group;
   const int row_end = min(v.rows, row_begin + a.rows_per_group);
   RG g;
-  g.li = KSPLIT == 1 ? (lane % LPR) : tid;
+  g.init(KSPLIT == 1 ? (lane % LPR) : tid);
+  auto row_of = [&](int t) { return v.routed ? a.perm_token[v.pair0 + t] : t; };
 
-  typename RG::Stage A, B;
+  typename RG::Stage st[S];
   for (int t0 = 0; t0 < v.count; t0 += NT) {
-    // the first weight stage does not depend on the activations: issue it first
-    g.load(A, v, row_begin, row_end);
-    g.load_x(a.x, a.x_stride, v, t0,
-             [&](int t) { return v.routed ? a.perm_token[v.pair0 + t] : t; });
+    if constexpr (COOP) {
+      float xq[NT][RG::XQ];
+      g.coop_issue(xq, a.x, a.x_stride, v, t0, row_of, tid);
+#pragma unroll
+      for (int i = 0; i < S - 1; ++i) g.load(st[i], v, row_begin + i * U, row_end);
+      g.coop_finish(xq, xsh, tid);
+    } else {
+      // the weight stages do not depend on the activations: issue them first
+#pragma unroll
+      for (int i = 0; i < S - 1; ++i) g.load(st[i], v, row_begin + i * U, row_end);
+      g.load_x(a.x, a.x_stride, v, t0, row_of);
+    }
 
     auto finish = [&](const typename RG::Stage &st, int r0) {
       float acc[U][2][NT];
@@ -290,12 +381,14 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
 
     // with KSPLIT > 1 the whole workgroup is one row group, so the trip
     // count (and every barrier in finish) is workgroup-uniform
-    for (int r = row_begin; r < row_end; r += 2 * U) {
-      g.load(B, v, r + U, row_end);
-      finish(A, r);
-      if (r + U >= row_end) break;
-      g.load(A, v, r + 2 * U, row_end);
-      finish(B, r + U);
+    for (int r = row_begin; r < row_end; r += S * U) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        const int rr = r + i * U;
+        if (rr >= row_end) break;
+        g.load(st[(i + S - 1) % S], v, rr + (S - 1) * U, row_end);
+        finish(st[i], rr);
+      }
     }
   }
 }
@@ -315,9 +408,11 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
   constexpr int U = NT == 1 ? 4 : 2;  // rows per pipeline stage
   using RG = RowGroup<FMT, L, SPL, NT, U, 1>;
   extern __shared__ float ypart_lds[];
-  const int tid = threadIdx.x, half = tid >> 8, tl = tid & 255;
-  const int lane = tl & 63, wave = tl >> 6;
-  const int grp = KSPLIT == 1 ? (tl / LPR) : 0;
+  const int tid = threadIdx.x, tl = tid & 255, lane = tl & 63;
+  // half and wave index, known to the compiler as wave-uniform
+  const int half = __builtin_amdgcn_readfirstlane(tid >> 8);
+  const int wave = __builtin_amdgcn_readfirstlane(tl >> 6);
+  const int grp = KSPLIT > 1 ? 0 : (LPR == 64 ? wave : tl / LPR);
   const int kpart = KSPLIT == 1 ? 0 : wave;  // which partial this wave leaves
 
   const int n_active = a.active[a.E];
@@ -331,7 +426,7 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
   float *ybuf = YLDS ? ypart_lds : a.gpart + (size_t)blockIdx.x * KSPLIT * npairs * wg_rows;
 
   RG g;
-  g.li = KSPLIT == 1 ? (lane % LPR) : tl;
+  g.init(KSPLIT == 1 ? (lane % LPR) : tl);
   const bool writer = (g.li % LPR) == LPR - 1;
 
   // Stage positions: (slot, first token of the group, first row).  The
@@ -375,12 +470,15 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
     Pos pl = pc;
     SlotView vl = vc;
     typename RG::Stage A, B;
+    // activations go out before weight loads issued at the same time, so
+    // waiting for them does not wait for those weights
+    g.load_x(a.x, a.x_stride, vc, pc.t0, [&](int t) { return vc.pair0 + t; });
     g.load(A, vc, pc.r, row_end);
+    bool first = true;
     while (true) {
-      // activations of a new token group go out before the next stage's
-      // loads, so waiting for them does not wait for that stage
-      if (pc.r == row_begin)
+      if (pc.r == row_begin && !first)
         g.load_x(a.x, a.x_stride, vc, pc.t0, [&](int t) { return vc.pair0 + t; });
+      first = false;
       advance(pl, vl);
       if (pl.si < n_slots) g.load(B, vl, pl.r, row_end);
       finish(A, vc, pc);

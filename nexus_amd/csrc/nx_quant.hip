@@ -261,11 +261,13 @@ __global__ __launch_bounds__(256) void k_repack_codes(const uint8_t *__restrict_
           q[16 + i] = b ? (b[i] >> 4) : 0;
         }
       }
-      // ... stored as byte 4k+i = element 8k+i | element 8k+4+i << 4
+      // ... stored as signed nibbles q ^ 8 = q - 8: byte 4k+i = element 8k+i
+      // (low) | element 8k+4+i (high)
 #pragma unroll
       for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[4 * k + i] = (uint8_t)(q[8 * k + i] | (q[8 * k + 4 + i] << 4));
+        for (int i = 0; i < 4; ++i)
+          dst[4 * k + i] = (uint8_t)(((q[8 * k + i] ^ 8) | ((q[8 * k + 4 + i] ^ 8) << 4)) & 0xFF);
     }
   }
 }
