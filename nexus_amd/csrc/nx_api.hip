@@ -233,6 +233,7 @@ int nx_ctx_create(int device, nx_ctx **out) {
   nx_ctx *c = new nx_ctx();
   c->device = device;
   c->num_cu = prop.multiProcessorCount;
+  c->lds_per_cu = prop.maxSharedMemoryPerMultiProcessor;
   if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
     delete c;
     return fail(NX_ERR_DEVICE, "hipStreamCreateWithFlags failed");

@@ -8,18 +8,22 @@
 //   down:    y[p] = W_down . act[p]  (fp32), then the route-weighted combine.
 //
 // Work decomposition.  The permutation kernel lists M-tiles (expert, first
-// pair) of 128 pairs; grid.y walks that list (extra workgroups exit), grid.x
-// walks 128-row N-tiles of the weight matrices, so consecutive workgroups of
-// one N-tile column share weights.  A workgroup of 4 waves owns a 128x128
-// output tile (gate/up: two of them, for the gate and the up rows), each
-// wave a 64x64 quarter made of 2x2 v_mfma_f32_32x32x16 tiles.
+// pair) of 128 pairs; the 1-D grid covers (M-tile, 128-row N-tile) pairs in
+// an XCD-aware order (see k_gemm; extra workgroups exit).  A workgroup of 4 waves owns
+// a 128x128 output tile (gate/up: two of them, for the gate and the up rows);
+// wave w owns weight rows 32w .. 32w+31 of the tile for all 128 pairs, as
+// 4 v_mfma_f32_32x32x16 tiles per matrix.
 //
 // K loop, 64 elements per step (one Q4_K segment = sub-blocks s and s+4 of a
-// block, two Q8_0 / Q4_0 blocks, or 64 F32 values): the weight codes and
-// scales of the next step are fetched into registers while the MFMAs consume
-// the current step from LDS; each thread then dequantizes its 32 weights
-// (bit-exact f32 value, rounded once to the operand type) into LDS.  The
-// activation tile is gathered row by row through the permutation.
+// block, two Q8_0 / Q4_0 blocks, or 64 F32 values).  The activation tile is
+// gathered row by row through the permutation into LDS, shared by the four
+// waves.  The weights never pass through LDS: lane l of wave w dequantizes
+// half l/32 of the step for weight row 32w + l%32 (32 values, bit-exact f32,
+// rounded once to the operand type) straight into its MFMA B operands.  Within
+// a step, MFMA sub-step kk uses, for lane half h, the K positions
+// 32h + 8kk .. 32h + 8kk + 7; the A operands read the same positions from LDS.
+// The codes and scales of the next step are fetched while the MFMAs of the
+// current step run.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 
@@ -83,6 +87,8 @@ struct GemmArgs {
   int act_stride;
   float *y;       // down: [pairs][H]
   int y_stride;
+  // grid decomposition (see k_gemm): N-tiles and the tile order
+  int n_tiles, xcd_split;
 };
 
 // One thread's share of a weight tile: row = tid / 2, half h = tid % 2 of the
@@ -191,6 +197,46 @@ __device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, int h, flo
   }
 }
 
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// The 32 weights of this lane's half step as MFMA B operands b[kk] (values
+// 8kk .. 8kk+7 of the half).
+template <int FMT, bool BF16>
+__device__ __forceinline__ void w_operands(const WLoad<FMT> &w, int ks, int h,
+                                           typename OpT<BF16>::V8 (&b)[4]) {
+  if constexpr (FMT == NX_FMT_Q8_0 && !BF16) {
+    // fp16 without a float detour: byte u = q ^ 0x80 becomes the f16 1024 + u
+    // (exponent byte 0x64 above it), minus 1152 gives q exactly, and the f16
+    // product with the f16 scale is q * d rounded once, as from the exact value
+#pragma clang fp contract(off)
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)w.m.x);
+    const h2 dd = {d, d}, off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t ws[8] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w,
+                            w.q[1].x, w.q[1].y, w.q[1].z, w.q[1].w};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      h2 r[4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t u = ws[2 * kk + j] ^ 0x80808080u;
+        const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
+        const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
+        r[2 * j] = (lo - off) * dd;
+        r[2 * j + 1] = (hi - off) * dd;
+      }
+      b[kk] = typename OpT<BF16>::V8{r[0][0], r[0][1], r[1][0], r[1][1],
+                                     r[2][0], r[2][1], r[3][0], r[3][1]};
+    }
+  } else {
+    float v[32];
+    w_decode<FMT>(w, ks, h, v);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b[kk][i] = (typename OpT<BF16>::T)v[8 * kk + i];
+  }
+}
+
 // element index (within the activation row) of K position p of step ks
 template <int FMT>
 __device__ __forceinline__ int a_elem(int ks, int p) {
@@ -199,17 +245,36 @@ __device__ __forceinline__ int a_elem(int ks, int p) {
   return ks * 64 + p;
 }
 
+// F32 weights keep 64 floats of codes in flight per lane: one workgroup per CU
 template <int FMT, bool BF16, bool GATEUP>
-__global__ __launch_bounds__(256, 2) void k_gemm(const GemmArgs g) {
+__global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const GemmArgs g) {
   using Op = OpT<BF16>;
   using V8 = typename Op::V8;
   constexpr int NMAT = GATEUP ? 2 : 1;
   __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[NMAT][BN * LDK];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tile = blockIdx.y;
-  if (tile >= g.tiles[0]) return;  // workgroup-uniform
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Tile order.  xcd_split (gate/up): workgroup L runs on XCD L % 8; XCD x
+  // owns N-tiles [x * npx, (x+1) * npx) and walks them with the M-tile list
+  // fastest, so the M-tiles of one expert take each weight tile from the same
+  // L2 back to back.  Otherwise (down, whose activation tiles span K = the
+  // expert width and are the larger operand): N-tiles fastest, so the N-tiles
+  // of one activation tile run together.
+  const int L = blockIdx.x;
+  const int mcount = g.tiles[0];
+  if (mcount <= 0) return;
+  int tile, ntile;
+  if (g.xcd_split) {
+    const int xcd = L & 7, j = L >> 3, npx = (g.n_tiles + 7) >> 3;
+    tile = j % mcount;
+    ntile = xcd * npx + j / mcount;
+    if (ntile >= min(g.n_tiles, (xcd + 1) * npx)) return;  // workgroup-uniform
+  } else {
+    tile = L / g.n_tiles;
+    ntile = L - tile * g.n_tiles;
+    if (tile >= mcount) return;  // workgroup-uniform
+  }
   const int e = g.tiles[2 + 2 * tile], m0 = g.tiles[3 + 2 * tile];
   const bool routed = e < g.E;
   const int pair0 = routed ? g.offsets[e] : g.T * g.k;
@@ -219,7 +284,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const GemmArgs g) {
   const int nseg = routed ? g.nseg : g.snseg;
   const uint32_t rq = routed ? g.row_qs : g.srow_qs;
   const uint32_t rm = routed ? g.row_meta : g.srow_meta;
-  const int n0 = blockIdx.x * BN;
+  const int n0 = ntile * BN;
   if (n0 >= rows) return;
   const int mrows = min(BM, count - m0);
 
@@ -232,7 +297,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const GemmArgs g) {
   const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(m0p, (uint32_t)rows * rm);
   const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(m1p, (uint32_t)rows * rm);
 
-  // ---- this thread's load assignment: row r = tid / 2, half h = tid % 2
+  // ---- activation loads: row lr = tid / 2, half lh = tid % 2 of the step
   const int lr = tid >> 1, lh = tid & 1;
   // activation row (gathered through the permutation for gate/up)
   const bool arow_ok = lr < mrows;
@@ -245,8 +310,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const GemmArgs g) {
   // offsets select the row, and absent rows / columns past the row read zero
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.a, g.a_bytes);
   const uint32_t arow_off = (uint32_t)arow * (uint32_t)g.a_stride * 2u;
-  // weight row of this thread
-  const int wrow = n0 + lr;
+
+  // ---- weight loads: row n0 + 32 * wave + lane % 32, half lane / 32
+  const int l32 = lane & 31, kh = lane >> 5;
+  const int wrow = n0 + 32 * wave + l32;
   const bool wrow_ok = wrow < rows;
   const uint32_t wq_off = (uint32_t)wrow * rq, wm_off = (uint32_t)wrow * rm;
 
@@ -266,86 +333,59 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const GemmArgs g) {
     }
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
-      w_fetch<FMT>(wb[mt], mt == 0 ? rq0 : rq1, mt == 0 ? rm0 : rm1, wq_off, wm_off, ks, lh, nseg,
+      w_fetch<FMT>(wb[mt], mt == 0 ? rq0 : rq1, mt == 0 ? rm0 : rm1, wq_off, wm_off, ks, kh, nseg,
                    wrow_ok);
   };
-  auto stash = [&](int ks) {
-    // activation piece i and weight value i of this thread sit at K
-    // positions 32h + 8i and 32h + i of the step
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4 *>(&As[lr * LDK + 32 * lh + 8 * i]) = abuf[i];
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) {
-      float v[32];
-      w_decode<FMT>(wb[mt], ks, lh, v);
-#pragma unroll
-      for (int i = 0; i < 32; i += 2) {
-        const uint32_t pk = (uint32_t)Op::bits(v[i]) | ((uint32_t)Op::bits(v[i + 1]) << 16);
-        *reinterpret_cast<uint32_t *>(&Bs[mt][lr * LDK + 32 * lh + i]) = pk;
-      }
-    }
-  };
 
-  // ---- accumulators: wave (wm, wn) owns rows wm*64.., cols wn*64..
-  const int wm = wave >> 1, wn = wave & 1;
-  f32x16 acc[NMAT][2][2];
+  // ---- accumulators: acc[mt][mi] = pairs 32mi .. 32mi+31 x this wave's 32 rows
+  f32x16 acc[NMAT][4];
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[mt][i][j][r] = 0.f;
+      for (int r = 0; r < 16; ++r) acc[mt][i][r] = 0.f;
 
   fetch(0);
   for (int ks = 0; ks < nks; ++ks) {
-    __syncthreads();  // previous step's MFMAs are done with the LDS tiles
-    stash(ks);
+    __syncthreads();  // previous step's A reads are done
+    // activation piece i of this thread sits at K positions 32 lh + 8i
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<uint4 *>(&As[lr * LDK + 32 * lh + 8 * i]) = abuf[i];
+    V8 bf[NMAT][4];
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) w_operands<FMT, BF16>(wb[mt], ks, kh, bf[mt]);
     __syncthreads();
     if (ks + 1 < nks) fetch(ks + 1);
-    // MFMA over the 64-element step: 4 sub-steps of 16
-    const int l32 = lane & 31, kh = lane >> 5;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      V8 af[2];
+      V8 af[4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const V8 *>(&As[(wm * 64 + i * 32 + l32) * LDK + kk * 16 + kh * 8]);
+      for (int i = 0; i < 4; ++i)
+        af[i] = *reinterpret_cast<const V8 *>(&As[(i * 32 + l32) * LDK + 32 * kh + 8 * kk]);
 #pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) {
-        V8 bf[2];
+      for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          bf[j] = *reinterpret_cast<const V8 *>(&Bs[mt][(wn * 64 + j * 32 + l32) * LDK + kk * 16 + kh * 8]);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j) acc[mt][i][j] = Op::mfma(af[i], bf[j], acc[mt][i][j]);
-      }
+        for (int i = 0; i < 4; ++i) acc[mt][i] = Op::mfma(af[i], bf[mt][kk], acc[mt][i]);
     }
   }
 
   // ---- epilogue.  32x32 accumulator layout: lane holds column (lane % 32),
   // register r holds row (r / 4) * 8 + (lane / 32) * 4 + r % 4.
-  const int col_l = lane & 31, rq4 = (lane >> 5) * 4;
+  const int col = n0 + 32 * wave + l32, rq4 = kh * 4;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn * 64 + j * 32 + col_l;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = wm * 64 + i * 32 + (r >> 2) * 8 + rq4 + (r & 3);
-        if (row < mrows && col < rows) {
-          const size_t p = (size_t)(pair0 + m0 + row);
-          if constexpr (GATEUP) {
-            const float v = silu_mul(acc[0][i][j][r], acc[1][i][j][r]);
-            g.act[p * g.act_stride + col] = Op::bits(v);
-          } else {
-            g.y[p * g.y_stride + col] = acc[0][i][j][r];
-          }
+    for (int r = 0; r < 16; ++r) {
+      const int row = i * 32 + (r >> 2) * 8 + rq4 + (r & 3);
+      if (row < mrows && col < rows) {
+        const size_t p = (size_t)(pair0 + m0 + row);
+        if constexpr (GATEUP) {
+          const float v = silu_mul(acc[0][i][r], acc[1][i][r]);
+          g.act[p * g.act_stride + col] = Op::bits(v);
+        } else {
+          g.y[p * g.y_stride + col] = acc[0][i][r];
         }
       }
     }
@@ -433,12 +473,26 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
     a.y_stride = ex->H;
   }
   const int rows = a.rows > a.srows ? a.rows : a.srows;
-  const unsigned gx = (unsigned)((rows + BN - 1) / BN);
-  const unsigned gy = (unsigned)p.max_tiles;
+  a.n_tiles = (rows + BN - 1) / BN;
+  a.xcd_split = gateup ? 1 : 0;
+  // enough workgroups for either order at the largest M-tile count
+  const long wgs = a.xcd_split ? 8L * ((a.n_tiles + 7) / 8) * p.max_tiles
+                               : (long)a.n_tiles * p.max_tiles;
+  if (wgs > 0x7FFFFFFFL) return fail(NX_ERR_UNSUPPORTED, "grouped GEMM grid too large");
   GemmFn fn = pick(ex->fmt, p.bf16, gateup);
   if (!fn) return fail(NX_ERR_UNSUPPORTED, "no grouped-GEMM kernel for this format");
   const char *name = gateup ? "gemm_gateup" : "gemm_down";
-  return launch(c, name, [&] { hipLaunchKernelGGL(fn, dim3(gx, gy), dim3(256), 0, c->stream, a); });
+  // The down projection needs few registers, so up to four workgroups could
+  // share a CU; their activation tiles (K = the expert width) then overflow
+  // L2.  Reserving LDS keeps it at three per CU.
+  size_t lds = 0;
+  if (!gateup && c->lds_per_cu > 0) {
+    const size_t per_wg = c->lds_per_cu / 3, fixed = sizeof(uint16_t) * BM * LDK;
+    lds = per_wg > fixed + 1024 ? per_wg - fixed - 1024 : 0;
+  }
+  return launch(c, name, [&] {
+    hipLaunchKernelGGL(fn, dim3((unsigned)wgs), dim3(256), (unsigned)lds, c->stream, a);
+  });
 }
 
 }  // namespace

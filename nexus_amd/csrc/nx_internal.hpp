@@ -81,6 +81,7 @@ struct nx_ctx {
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
   int num_cu = 0;
+  size_t lds_per_cu = 0;  // bytes of LDS per CU
   // workspace
   nx::DevBuf ws[24];
   // host-visible staging for blocking calls
