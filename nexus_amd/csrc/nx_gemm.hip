@@ -24,6 +24,8 @@
 // 32h + 8kk .. 32h + 8kk + 7; the A operands read the same positions from LDS.
 // The codes and scales of the next step are fetched while the MFMAs of the
 // current step run.
+#include <type_traits>
+
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 
@@ -38,7 +40,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int BM = 128;   // pairs per tile
 constexpr int BN = 128;   // weight rows per tile
 constexpr int BK = 64;    // K elements per step
-constexpr int LDK = BK + 8;  // LDS row stride in elements (16-byte pad)
 
 template <bool BF16>
 struct OpT;
@@ -115,14 +116,16 @@ __device__ __forceinline__ void w_fetch(WLoad<FMT> &w, __amdgpu_buffer_rsrc_t rq
     const bool v = valid && j < nseg;
     w.q[0] = bload16(rq, v ? row_off_q + seg_off(j, 0, nseg) : OOB);
     w.q[1] = bload16(rq, v ? row_off_q + seg_off(j, 1, nseg) : OOB);
-    const uint32_t mo = v ? row_off_m + (uint32_t)j * 2u : OOB;
-    const uint32_t mw = bload4(rm, mo == OOB ? OOB : (mo & ~3u));
-    w.m.x = (mo & 2u) ? (mw >> 16) : (mw & 0xFFFFu);
+    // the scale's dword, and where in it the scale sits: the selection is
+    // left to the decode, so that nothing waits for the load here
+    const uint32_t mo = row_off_m + (uint32_t)j * 2u;
+    w.m.x = bload4(rm, v ? (mo & ~3u) : OOB);
+    w.m.y = (mo & 2u) * 8u;
   } else if constexpr (FMT == NX_FMT_Q4_0) {
     // segment ks holds blocks 2ks (half 0) and 2ks+1 (half 1)
     w.q[0] = bload16(rq, valid ? row_off_q + seg_off(ks, h, nseg) : OOB);
-    const uint32_t mw = bload4(rm, valid ? row_off_m + (uint32_t)ks * 4u : OOB);
-    w.m.x = h ? (mw >> 16) : (mw & 0xFFFFu);
+    // both blocks' scales; half h takes its own at decode time
+    w.m.x = bload4(rm, valid ? row_off_m + (uint32_t)ks * 4u : OOB);
   } else {  // F32: segments 8ks + 4h .. +3 (8 floats each)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -166,7 +169,7 @@ __device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, int h, flo
         v[8 * k + 4 + i] = d * sc * (float)(byte >> 4) - dmin * mn;
       }
   } else if constexpr (FMT == NX_FMT_Q8_0) {
-    const float d = h2f(w.m.x);
+    const float d = h2f((w.m.x >> w.m.y) & 0xFFFFu);
     const uint32_t ws[8] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w,
                             w.q[1].x, w.q[1].y, w.q[1].z, w.q[1].w};
 #pragma unroll
@@ -175,7 +178,7 @@ __device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, int h, flo
       for (int i = 0; i < 4; ++i)
         v[4 * j + i] = (float)(int32_t)(int8_t)((ws[j] >> (8 * i)) & 0xFFu) * d;
   } else if constexpr (FMT == NX_FMT_Q4_0) {
-    const float d = h2f(w.m.x);
+    const float d = h2f((w.m.x >> (16 * h)) & 0xFFFFu);
     const uint32_t ws[4] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w};
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -209,7 +212,7 @@ __device__ __forceinline__ void w_operands(const WLoad<FMT> &w, int ks, int h,
     // (exponent byte 0x64 above it), minus 1152 gives q exactly, and the f16
     // product with the f16 scale is q * d rounded once, as from the exact value
 #pragma clang fp contract(off)
-    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)w.m.x);
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(w.m.x >> w.m.y));
     const h2 dd = {d, d}, off = {(_Float16)1152.0f, (_Float16)1152.0f};
     const uint32_t ws[8] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w,
                             w.q[1].x, w.q[1].y, w.q[1].z, w.q[1].w};
@@ -245,13 +248,43 @@ __device__ __forceinline__ int a_elem(int ks, int p) {
   return ks * 64 + p;
 }
 
-// F32 weights keep 64 floats of codes in flight per lane: one workgroup per CU
+// LDS ring of activation stages: stage = the 128 x 64 activation tile of one
+// K step as 128 rows of eight 16-byte chunks; chunk c of row r is stored at
+// slot c ^ (r & 7), so the MFMA reads of eight consecutive rows hit eight
+// different bank groups.  Distinct arrays per stage let the compiler track
+// each stage's direct-to-LDS loads separately.
+constexpr int RING = 4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int S>
+__device__ __forceinline__ uint4 *ring_stage(uint4 *r0, uint4 *r1, uint4 *r2, uint4 *r3) {
+  if constexpr (S == 0) return r0;
+  else if constexpr (S == 1) return r1;
+  else if constexpr (S == 2) return r2;
+  else return r3;
+}
+
+// s_waitcnt vmcnt(n) (other counters unconstrained), n a compile-time constant
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// F32 weights keep 64 floats of codes per stage per lane: one workgroup per CU
 template <int FMT, bool BF16, bool GATEUP>
 __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const GemmArgs g) {
   using Op = OpT<BF16>;
   using V8 = typename Op::V8;
   constexpr int NMAT = GATEUP ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDK];
+  // vector-memory instructions per K step: 4 activation chunks, and per
+  // matrix the weight codes and scales
+  constexpr int NWM = FMT == NX_FMT_F32 ? 8 : (FMT == NX_FMT_Q8_0 ? 3 : 2);
+  constexpr int NA = 4, NW = NMAT * NWM;
+  __shared__ __attribute__((aligned(16))) uint4 ring0[BM * 8];
+  __shared__ __attribute__((aligned(16))) uint4 ring1[BM * 8];
+  __shared__ __attribute__((aligned(16))) uint4 ring2[BM * 8];
+  __shared__ __attribute__((aligned(16))) uint4 ring3[BM * 8];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -297,21 +330,31 @@ __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const G
   const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(m0p, (uint32_t)rows * rm);
   const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(m1p, (uint32_t)rows * rm);
 
-  // ---- activation loads: row lr = tid / 2, half lh = tid % 2 of the step
-  const int lr = tid >> 1, lh = tid & 1;
-  // activation row (gathered through the permutation for gate/up)
-  const bool arow_ok = lr < mrows;
-  int arow = 0;
-  if (arow_ok) {
-    const int p = pair0 + m0 + lr;
-    arow = GATEUP ? (routed ? g.perm_token[p] : (m0 + lr)) : p;
-  }
-  // one wave-uniform resource over the whole activation buffer; per-lane
-  // offsets select the row, and absent rows / columns past the row read zero
+  // ---- activation chunks: instruction q of this wave fills stage chunks
+  // (4 * wave + q) * 64 + lane, i.e. row r_q = (4 * wave + q) * 8 + lane / 8,
+  // slot lane % 8, which holds K chunk (lane % 8) ^ (r_q & 7) of that row
+  // (gathered through the permutation for gate/up).  One wave-uniform
+  // resource spans the activation buffer; absent rows read zero.
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.a, g.a_bytes);
-  const uint32_t arow_off = (uint32_t)arow * (uint32_t)g.a_stride * 2u;
+  uint32_t aoff[NA];
+  int achunk[NA];
+  int arow[NA];
+#pragma unroll
+  for (int q = 0; q < NA; ++q) {
+    const int r = (4 * wave + q) * 8 + (lane >> 3);
+    achunk[q] = (lane & 7) ^ (r & 7);
+    // absent rows look up the tile's first pair (always present) and are
+    // masked below, so the four lookups go out together
+    const int p = pair0 + m0 + (r < mrows ? r : 0);
+    arow[q] = GATEUP ? (routed ? g.perm_token[p] : p - pair0) : p;
+  }
+#pragma unroll
+  for (int q = 0; q < NA; ++q) {
+    const int r = (4 * wave + q) * 8 + (lane >> 3);
+    aoff[q] = r < mrows ? (uint32_t)arow[q] * (uint32_t)g.a_stride * 2u : OOB;
+  }
 
-  // ---- weight loads: row n0 + 32 * wave + lane % 32, half lane / 32
+  // ---- weights: row n0 + 32 * wave + lane % 32, half lane / 32 of the step
   const int l32 = lane & 31, kh = lane >> 5;
   const int wrow = n0 + 32 * wave + l32;
   const bool wrow_ok = wrow < rows;
@@ -320,21 +363,24 @@ __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const G
   // number of 64-element K steps
   const int nks = FMT == NX_FMT_Q4_K ? nseg : (FMT == NX_FMT_F32 ? (nseg + 7) / 8 : (FMT == NX_FMT_Q8_0 ? (nseg + 1) / 2 : nseg));
 
-  // ---- register prefetch buffers
-  uint4 abuf[4];
-  WLoad<FMT> wb[NMAT];
-  auto fetch = [&](int ks) {
-    // activations: 32 elements = two 16-element runs (contiguous in the row)
+  auto issue_a = [&](auto stage, int ks) {
+    constexpr int S = decltype(stage)::value;
+    uint4 *dst = ring_stage<S>(ring0, ring1, ring2, ring3);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = 32 * lh + 8 * i;  // K position of this 8-element piece
-      const int el = a_elem<FMT>(ks, p);
-      abuf[i] = bload16(ra, (arow_ok && el < cols) ? arow_off + (uint32_t)el * 2u : OOB);
+    for (int q = 0; q < NA; ++q) {
+      const int el = a_elem<FMT>(ks, 8 * achunk[q]);
+      const uint32_t off = (aoff[q] != OOB && el < cols) ? aoff[q] + (uint32_t)el * 2u : OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(dst + (4 * wave + q) * 64), 16, off,
+                                               0, 0, 0);
     }
+  };
+  WLoad<FMT> wbuf[2][NMAT];
+  auto issue_w = [&](WLoad<FMT>(&wb)[NMAT], int ks) {
+    // steps past the end read zeros (their activations are zero too)
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
       w_fetch<FMT>(wb[mt], mt == 0 ? rq0 : rq1, mt == 0 ? rm0 : rm1, wq_off, wm_off, ks, kh, nseg,
-                   wrow_ok);
+                   wrow_ok && ks < nks);
   };
 
   // ---- accumulators: acc[mt][mi] = pairs 32mi .. 32mi+31 x this wave's 32 rows
@@ -346,30 +392,70 @@ __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const G
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mt][i][r] = 0.f;
 
-  fetch(0);
-  for (int ks = 0; ks < nks; ++ks) {
-    __syncthreads();  // previous step's A reads are done
-    // activation piece i of this thread sits at K positions 32 lh + 8i
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4 *>(&As[lr * LDK + 32 * lh + 8 * i]) = abuf[i];
-    V8 bf[NMAT][4];
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) w_operands<FMT, BF16>(wb[mt], ks, kh, bf[mt]);
-    __syncthreads();
-    if (ks + 1 < nks) fetch(ks + 1);
+  // Software pipeline over a whole number of ring rounds (steps past nks load
+  // zeros and add nothing).  Step ks: wait until this wave's loads of
+  // activation stage ks and weights ks have landed, barrier (every wave's
+  // share of the stage is in LDS, and every wave is done reading stage ks-1's
+  // slot), issue activation stage ks+3 into that slot and weights ks+2, decode
+  // weights ks into B operands, run the step's MFMAs.  Every step issues the
+  // same loads, unconditionally (a conditional load would make the compiler
+  // copy its registers, waiting for all loads in flight): A(ks) at step ks-3,
+  // W(ks) at step ks-2 after A(ks+1), so after W(ks) come exactly A(ks+2) and
+  // W(ks+1), and vmcnt <= NA + NW completes both.
+  auto wait_step = [&]() {
+    wait_vm<NA + NW>();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto compute = [&](auto stage, const V8 (&bf)[NMAT][4]) {
+    constexpr int S = decltype(stage)::value;
+    const uint4 *src = ring_stage<S>(ring0, ring1, ring2, ring3);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
+      const int c = 4 * kh + kk;
       V8 af[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const V8 *>(&As[(i * 32 + l32) * LDK + 32 * kh + 8 * kk]);
+      for (int i = 0; i < 4; ++i) {
+        const int r = 32 * i + l32;
+        af[i] = __builtin_bit_cast(V8, src[r * 8 + (c ^ (r & 7))]);
+      }
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[mt][i] = Op::mfma(af[i], bf[mt][kk], acc[mt][i]);
     }
+  };
+  auto step = [&](auto stage, auto buf, int ks) {
+    constexpr int S = decltype(stage)::value, B = decltype(buf)::value;
+    wait_step();
+    issue_a(std::integral_constant<int, (S + 3) % RING>{}, ks + 3);
+    V8 bf[NMAT][4];
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) w_operands<FMT, BF16>(wbuf[B][mt], ks, kh, bf[mt]);
+    issue_w(wbuf[B], ks + 2);
+    compute(stage, bf);
+    // keep each step's work in its step (register pressure)
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  issue_a(I0{}, 0);
+  issue_a(I1{}, 1);
+  issue_w(wbuf[0], 0);
+  issue_a(I2{}, 2);
+  issue_w(wbuf[1], 1);
+  for (int ks = 0; ks < nks; ks += RING) {
+    step(I0{}, I0{}, ks);
+    step(I1{}, I1{}, ks + 1);
+    step(I2{}, I0{}, ks + 2);
+    step(I3{}, I1{}, ks + 3);
   }
+  // no direct-to-LDS write may land after the workgroup has ended
+  wait_vm<0>();
 
   // ---- epilogue.  32x32 accumulator layout: lane holds column (lane % 32),
   // register r holds row (r / 4) * 8 + (lane / 32) * 4 + r % 4.
@@ -482,17 +568,10 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   GemmFn fn = pick(ex->fmt, p.bf16, gateup);
   if (!fn) return fail(NX_ERR_UNSUPPORTED, "no grouped-GEMM kernel for this format");
   const char *name = gateup ? "gemm_gateup" : "gemm_down";
-  // The down projection needs few registers, so up to four workgroups could
-  // share a CU; their activation tiles (K = the expert width) then overflow
-  // L2.  Reserving LDS keeps it at three per CU.
-  size_t lds = 0;
-  if (!gateup && c->lds_per_cu > 0) {
-    const size_t per_wg = c->lds_per_cu / 3, fixed = sizeof(uint16_t) * BM * LDK;
-    lds = per_wg > fixed + 1024 ? per_wg - fixed - 1024 : 0;
-  }
-  return launch(c, name, [&] {
-    hipLaunchKernelGGL(fn, dim3((unsigned)wgs), dim3(256), (unsigned)lds, c->stream, a);
-  });
+  // (the 64 KB activation ring keeps at most two workgroups per CU, which
+  // also bounds the L2 footprint of the down projection's long K)
+  return launch(c, name,
+                [&] { hipLaunchKernelGGL(fn, dim3((unsigned)wgs), dim3(256), 0, c->stream, a); });
 }
 
 }  // namespace
