@@ -147,6 +147,13 @@ static int ex_alloc(nx_experts *ex, size_t bytes, uint8_t **out) {
     (void)hipGetLastError();
     return fail(NX_ERR_OOM, "device allocation of " + std::to_string(bytes) + " bytes failed");
   }
+  // padding between rows and past the last row is read (times zero
+  // activations) by the grouped GEMM's wide scale loads: keep it finite
+  if (hipMemsetAsync(p, 0, bytes, ex->ctx->stream) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(p);
+    return fail(NX_ERR_DEVICE, "clearing a device allocation failed");
+  }
   ex->allocs.push_back(p);
   ex->device_bytes += bytes;
   *out = static_cast<uint8_t *>(p);
@@ -163,7 +170,8 @@ static int init_plane(nx_experts *ex, RolePlane &pl, int count, int rows, int co
     break;
   case NX_FMT_Q8_0:
     pl.nseg = cols / 32;
-    pl.row_meta = (uint32_t)(cols / 32 * 2);
+    // whole dwords per row: the grouped GEMM loads two blocks' scales at once
+    pl.row_meta = (uint32_t)((cols / 32 * 2 + 3) / 4 * 4);
     break;
   case NX_FMT_Q4_0:
     pl.nseg = (cols / 32 + 1) / 2;
@@ -658,15 +666,16 @@ int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const 
   NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, tm, d_ec, d_off, d_pt, d_ps, d_inv, d_act,
                         d_tiles, shared ? T : 0));
   void *d_xh, *d_acth;
-  NX_TRY(ws_get(c, WS_XH, (size_t)T * H * 2, &d_xh));
-  NX_TRY(launch_to_half(c, d_x, (size_t)T * H, bf16, d_xh));
-  const int fmax = std::max(ex->F, ex->Fs);
-  const int act_stride = (fmax + 7) / 8 * 8;
-  NX_TRY(ws_get(c, WS_ACT, pairs_total * act_stride * 2, &d_acth));
-  if ((size_t)T * H * 2 >= (1u << 31) || pairs_total * act_stride * 2 >= (1u << 31))
+  // operands in the kernels' K order, rows padded to whole scale windows
+  const int x_stride = gemm_kpad(ex->fmt, H);
+  const int act_stride = gemm_kpad(ex->fmt, std::max(ex->F, ex->Fs));
+  if ((size_t)T * x_stride * 2 >= (1u << 31) || pairs_total * act_stride * 2 >= (1u << 31))
     return fail(NX_ERR_UNSUPPORTED, "activation buffers above 2 GiB");
+  NX_TRY(ws_get(c, WS_XH, (size_t)T * x_stride * 2, &d_xh));
+  NX_TRY(launch_to_half(c, ex->fmt, d_x, T, H, x_stride, bf16, d_xh));
+  NX_TRY(ws_get(c, WS_ACT, pairs_total * act_stride * 2, &d_acth));
   GemmPlan mp{ex, T, k, bf16, d_x, d_pt, d_off, d_act, d_tiles, max_tiles, d_acth, act_stride,
-              d_ypair, d_xh, pairs_total};
+              d_ypair, d_xh, x_stride, pairs_total};
   NX_TRY(launch_gemm_gateup(c, mp));
   NX_TRY(launch_gemm_down(c, mp));
   NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out));

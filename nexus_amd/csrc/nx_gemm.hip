@@ -9,21 +9,28 @@
 //
 // Work decomposition.  The permutation kernel lists M-tiles (expert, first
 // pair) of 128 pairs; the 1-D grid covers (M-tile, 128-row N-tile) pairs in
-// an XCD-aware order (see k_gemm; extra workgroups exit).  A workgroup of 4 waves owns
-// a 128x128 output tile (gate/up: two of them, for the gate and the up rows);
-// wave w owns weight rows 32w .. 32w+31 of the tile for all 128 pairs, as
-// 4 v_mfma_f32_32x32x16 tiles per matrix.
+// an XCD-aware order (see k_gemm; extra workgroups exit).  A workgroup of 4
+// waves owns a 128x128 output tile (gate/up: two of them, for the gate and
+// the up rows); wave w owns weight rows 32w .. 32w+31 of the tile for all 128
+// pairs, as 2 x 8 v_mfma_f32_16x16x32 tiles per matrix.
 //
-// K loop, 64 elements per step (one Q4_K segment = sub-blocks s and s+4 of a
-// block, two Q8_0 / Q4_0 blocks, or 64 F32 values).  The activation tile is
-// gathered row by row through the permutation into LDS, shared by the four
-// waves.  The weights never pass through LDS: lane l of wave w dequantizes
-// half l/32 of the step for weight row 32w + l%32 (32 values, bit-exact f32,
-// rounded once to the operand type) straight into its MFMA B operands.  Within
-// a step, MFMA sub-step kk uses, for lane half h, the K positions
-// 32h + 8kk .. 32h + 8kk + 7; the A operands read the same positions from LDS.
-// The codes and scales of the next step are fetched while the MFMAs of the
-// current step run.
+// Operand order.  The K loop takes 64 positions per step.  Position
+// j = 64 ks + 16 q + i is value i of the lanes of quarter q (lanes 16q ..
+// 16q+15) at step ks: with the 16x16x32 MFMA, the four lanes of a weight row
+// (one per quarter) cover 64 consecutive operand positions, and the order is
+// chosen per format so that those four lanes read 32-64 contiguous bytes of
+// one 128-byte line of the resident code plane, and so that a lane's scales
+// for several steps sit in one load (kpos below).  The activations are
+// written in the same order by their producers (k_to_half for x, the gate/up
+// epilogue for act), so the activation tile of a step is still one
+// contiguous 128-byte run per row.
+//
+// Pipeline.  The activation tile of a step goes into a 4-stage LDS ring by
+// direct-to-LDS loads, shared by the four waves.  The weights never pass
+// through LDS: each lane dequantizes its 16 values of each of its two rows
+// (bit-exact f32, rounded once to the operand type) straight into its MFMA B
+// operands.  Codes are fetched two steps ahead, scales once per window of
+// steps, activations three steps ahead.
 #include <type_traits>
 
 #include "nx_device.hpp"
@@ -35,11 +42,12 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128;   // pairs per tile
 constexpr int BN = 128;   // weight rows per tile
-constexpr int BK = 64;    // K elements per step
+constexpr int BK = 64;    // K positions per step
 
 template <bool BF16>
 struct OpT;
@@ -50,8 +58,8 @@ struct OpT<false> {
   __device__ __forceinline__ static uint16_t bits(float v) {
     return __builtin_bit_cast(uint16_t, (_Float16)v);
   }
-  __device__ __forceinline__ static f32x16 mfma(const V8 &a, const V8 &b, const f32x16 &c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  __device__ __forceinline__ static f32x4 mfma(const V8 &a, const V8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
 template <>
@@ -61,10 +69,69 @@ struct OpT<true> {
   __device__ __forceinline__ static uint16_t bits(float v) {
     return __builtin_bit_cast(uint16_t, (__bf16)v);
   }
-  __device__ __forceinline__ static f32x16 mfma(const V8 &a, const V8 &b, const f32x16 &c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  __device__ __forceinline__ static f32x4 mfma(const V8 &a, const V8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
 };
+
+// ---- operand order --------------------------------------------------------
+//
+// Window = the K positions whose scales one lane loads at once.  Within a
+// window of format FMT, operand position j (step s = (j / 64) % steps, lane
+// quarter q = (j / 16) % 4, value i = j % 16) holds activation element
+// kpos(j):
+//   Q8_0 (window 256 = blocks 8u .. 8u+7, 4 steps): quarter q takes blocks
+//        8u+2q (steps 0, 1) and 8u+2q+1 (steps 2, 3), code-plane half s%2,
+//        so e = 256u + 64q + 16s + i (a transpose of 16-element pieces); its
+//        two scales are one dword.
+//   Q4_K (window 512 = blocks 2u, 2u+1, 8 steps): quarter q takes block
+//        2u + q/2, sub-block (s%4) + 4(s/4), bytes 8(q%2) .. +7 of its
+//        16-byte half: e = 512u + 256(q/2) + 128(s/4) + 32(s%4) + 16(q%2) + i;
+//        its scales are the block's 16 bytes.
+//   Q4_0 (window 512 = segments 8u .. 8u+7, 8 steps): quarter q takes
+//        segment 8u + 4(q/2) + s%4, block half s/4 (block 2*segment + s/4),
+//        bytes 8(q%2) .. +7: e = 512u + 256(q/2) + 64(s%4) + 32(s/4) +
+//        16(q%2) + i; its scales are 16 bytes (4 segments).
+//   F32 (window 64): e = j.
+template <int FMT>
+__host__ __device__ constexpr int kwin() {
+  return FMT == NX_FMT_Q8_0 ? 256 : (FMT == NX_FMT_F32 ? 64 : 512);
+}
+
+template <int FMT>
+__host__ __device__ __forceinline__ int kpos(int j) {
+  if constexpr (FMT == NX_FMT_Q8_0) {
+    return (j & ~255) | ((j & 48) << 2) | ((j >> 2) & 48) | (j & 15);
+  } else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) {
+    const int s = (j >> 6) & 7, q = (j >> 4) & 3;
+    const int p = s >> 2, t = s & 3;
+    const int mid = FMT == NX_FMT_Q4_K ? 128 * p + 32 * t : 64 * t + 32 * p;
+    return (j & ~511) + 256 * (q >> 1) + mid + 16 * (q & 1) + (j & 15);
+  } else {
+    return j;
+  }
+}
+
+// inverse of kpos: operand position of activation element e
+template <int FMT>
+__host__ __device__ __forceinline__ int kslot(int e) {
+  if constexpr (FMT == NX_FMT_Q8_0) {
+    return kpos<FMT>(e);
+  } else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) {
+    const int a = (e >> 8) & 1, b = (e >> 4) & 1;
+    const int p = FMT == NX_FMT_Q4_K ? (e >> 7) & 1 : (e >> 5) & 1;
+    const int t = FMT == NX_FMT_Q4_K ? (e >> 5) & 3 : (e >> 6) & 3;
+    return (e & ~511) + 64 * (4 * p + t) + 16 * (2 * a + b) + (e & 15);
+  } else {
+    return e;
+  }
+}
+
+int kpad_of(int fmt, int cols) {
+  const int w = fmt == NX_FMT_Q8_0 ? kwin<NX_FMT_Q8_0>()
+                                   : (fmt == NX_FMT_F32 ? kwin<NX_FMT_F32>() : kwin<NX_FMT_Q4_K>());
+  return (cols + w - 1) / w * w;
+}
 
 struct GemmArgs {
   // weights: role bases (gate, up) or (down, -), per-expert strides, row bytes
@@ -75,7 +142,8 @@ struct GemmArgs {
   const uint8_t *sqs0, *sqs1, *smeta0, *smeta1;
   uint32_t srow_qs, srow_meta;
   int srows, scols, snseg;
-  // activations (operand type), [rows][a_stride]; a_bytes = size of the buffer
+  // activations (operand type, operand order), [rows][a_stride]; a_bytes =
+  // size of the buffer
   const uint16_t *a;
   int a_stride;
   uint32_t a_bytes;
@@ -84,7 +152,7 @@ struct GemmArgs {
   const int32_t *tiles;  // [0] = count, then (expert, first pair) pairs; expert E = shared
   int E, T, k, has_shared;
   // outputs
-  uint16_t *act;  // gate/up: [pairs][act_stride] operand type
+  uint16_t *act;  // gate/up: [pairs][act_stride] operand type, operand order
   int act_stride;
   float *y;       // down: [pairs][H]
   int y_stride;
@@ -92,167 +160,206 @@ struct GemmArgs {
   int n_tiles, xcd_split;
 };
 
-// One thread's share of a weight tile: row = tid / 2, half h = tid % 2 of the
-// 64-element K step, dequantized to 32 floats in K order.
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return make_uint2(v[0], v[1]);
+}
+
+// ---- weights: one lane's codes of one step, and scales of one window ------
+//
+// A lane holds weight rows n0 + 32w + l%16 and that + 16 (index n = 0, 1).
 template <int FMT>
-struct WLoad {
-  uint4 q[2];  // codes (Q4_K / Q4_0: q[0] only; F32: 8 floats in q[0..1]x... see below)
-  uint4 f[6];  // F32 only: 32 floats = 8 x uint4 with q[0..1]
-  uint4 m;     // scales
+struct WCodes {
+  uint4 c[2];
 };
-
+template <>
+struct WCodes<NX_FMT_Q4_K> {
+  uint2 c[2];
+};
+template <>
+struct WCodes<NX_FMT_Q4_0> {
+  uint2 c[2];
+};
+template <>
+struct WCodes<NX_FMT_F32> {
+  uint4 c[2][4];
+};
 template <int FMT>
-__device__ __forceinline__ void w_fetch(WLoad<FMT> &w, __amdgpu_buffer_rsrc_t rq,
-                                        __amdgpu_buffer_rsrc_t rm, uint32_t row_off_q,
-                                        uint32_t row_off_m, int ks, int h, int nseg, bool valid) {
-  if constexpr (FMT == NX_FMT_Q4_K) {
-    // segment ks, half h: the 32 codes of sub-block s (h = 0) or s+4 (h = 1)
-    const uint32_t o = valid ? row_off_q + seg_off(ks, h, nseg) : OOB;
-    w.q[0] = bload16(rq, o);
-    w.m = bload16(rm, valid ? row_off_m + (uint32_t)(ks >> 2) * 16u : OOB);
-  } else if constexpr (FMT == NX_FMT_Q8_0) {
-    // blocks 2ks + h (segment = block): 32 codes
-    const int j = 2 * ks + h;
-    const bool v = valid && j < nseg;
-    w.q[0] = bload16(rq, v ? row_off_q + seg_off(j, 0, nseg) : OOB);
-    w.q[1] = bload16(rq, v ? row_off_q + seg_off(j, 1, nseg) : OOB);
-    // the scale's dword, and where in it the scale sits: the selection is
-    // left to the decode, so that nothing waits for the load here
-    const uint32_t mo = row_off_m + (uint32_t)j * 2u;
-    w.m.x = bload4(rm, v ? (mo & ~3u) : OOB);
-    w.m.y = (mo & 2u) * 8u;
-  } else if constexpr (FMT == NX_FMT_Q4_0) {
-    // segment ks holds blocks 2ks (half 0) and 2ks+1 (half 1)
-    w.q[0] = bload16(rq, valid ? row_off_q + seg_off(ks, h, nseg) : OOB);
-    // both blocks' scales; half h takes its own at decode time
-    w.m.x = bload4(rm, valid ? row_off_m + (uint32_t)ks * 4u : OOB);
-  } else {  // F32: segments 8ks + 4h .. +3 (8 floats each)
+struct WMeta {
+  uint4 m[2];
+};
+template <>
+struct WMeta<NX_FMT_Q8_0> {
+  uint32_t m[2];
+};
+template <>
+struct WMeta<NX_FMT_F32> {};
+
+// code loads per matrix per step, scale loads per matrix per window
+template <int FMT>
+constexpr int n_code_loads() {
+  return FMT == NX_FMT_F32 ? 8 : 2;
+}
+template <int FMT>
+constexpr int n_meta_loads() {
+  return FMT == NX_FMT_F32 ? 0 : 2;
+}
+// steps per window
+template <int FMT>
+constexpr int win_steps() {
+  return kwin<FMT>() / BK;
+}
+// steps over a row of `cols` activations padded to whole windows
+template <int FMT>
+__device__ __forceinline__ int kpad_steps(int cols) {
+  return (cols + kwin<FMT>() - 1) / kwin<FMT>() * win_steps<FMT>();
+}
+
+// Weight addressing.  A lane's loads of row n are at lane base lq[n] (row
+// offset plus the lane quarter's place in the line) + a wave-uniform part
+// (group, plane half and line of the step's window) + a constant.  Every
+// part goes into the range-checked offset, so rows past the matrix read zero;
+// blocks past a row's end (last partial window only) read finite neighbours,
+// which meet zero activations.
+template <int FMT>
+__device__ __forceinline__ uint32_t code_lane_off(uint32_t row_off, int q) {
+  if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0)
+    return row_off + 64u * (q >> 1) + 8u * (q & 1);
+  return row_off + 32u * q;  // Q8_0: blocks 8u + 2q (+1); F32: segments 8u + 2q (+1)
+}
+template <int FMT>
+__device__ __forceinline__ uint32_t meta_lane_off(uint32_t row_off, int q) {
+  if constexpr (FMT == NX_FMT_Q8_0) return row_off + 4u * q;
+  return row_off + 16u * (q >> 1);
+}
+// uniform part of window win, code-plane half p: group (64 segments), half,
+// 8-segment line
+__device__ __forceinline__ uint32_t code_win_off(int win, int p, int nseg) {
+  const int g = win >> 3;
+  const int gsz = min(64, nseg - 64 * g);
+  return (uint32_t)(g * 2048 + p * gsz * 16 + (win & 7) * 128);
+}
+
+// codes of step S of window win
+template <int FMT, int S>
+__device__ __forceinline__ void fetch_codes(WCodes<FMT> &w, __amdgpu_buffer_rsrc_t rq,
+                                            const uint32_t (&lq)[2], int win, int nseg) {
+  if constexpr (FMT == NX_FMT_Q8_0) {
+    const uint32_t u = code_win_off(win, S & 1, nseg);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 8 * ks + 4 * h + i;
-      const bool v = valid && j < nseg;
-      const uint4 a = bload16(rq, v ? row_off_q + seg_off(j, 0, nseg) : OOB);
-      const uint4 b = bload16(rq, v ? row_off_q + seg_off(j, 1, nseg) : OOB);
-      if (i == 0) {
-        w.q[0] = a;
-        w.q[1] = b;
-      } else {
-        w.f[2 * (i - 1)] = a;
-        w.f[2 * (i - 1) + 1] = b;
-      }
-    }
+    for (int n = 0; n < 2; ++n) w.c[n] = bload16(rq, lq[n] + u + 16u * (S >> 1));
+  } else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) {
+    const uint32_t u = code_win_off(win, S >> 2, nseg);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) w.c[n] = bload8(rq, lq[n] + u + 16u * (S & 3));
+  } else {  // F32: segments 8 win + 2q (+1), both halves: floats 64 win + 16q ..
+    const uint32_t u0 = code_win_off(win, 0, nseg), u1 = code_win_off(win, 1, nseg);
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w.c[n][k] = bload16(rq, lq[n] + ((k & 1) ? u1 : u0) + 16u * (k >> 1));
   }
 }
 
-// dequantize this thread's 32 weights (half h of the 64-element step) to
-// floats in K order: positions 32h .. 32h+31 of the step
+// scales of window win: Q8_0 blocks 8 win + 2q, +1 (one dword, rows padded
+// to whole dwords); Q4_K block 2 win + q/2; Q4_0 segments 8 win + 4(q/2) .. +3
 template <int FMT>
-__device__ __forceinline__ void w_decode(const WLoad<FMT> &w, int ks, int h, float *v) {
-  if constexpr (FMT == NX_FMT_Q4_K) {
-    // half 0: sub-block s = ks%4, half 1: sub-block s+4
-    const float d = h2f(w.m.x & 0xFFFFu), dmin = h2f(w.m.x >> 16);
-    const int s = ks & 3;
-    const uint32_t b0 = (w.m.y >> (8 * s)) & 0xFFu;
-    const uint32_t b4 = (w.m.z >> (8 * s)) & 0xFFu;
-    const uint32_t b8 = (w.m.w >> (8 * s)) & 0xFFu;
-    const float sc = h ? (float)((b8 & 15u) | ((b0 >> 6) << 4)) : (float)(b0 & 63u);
-    const float mn = h ? (float)((b8 >> 4) | ((b4 >> 6) << 4)) : (float)(b4 & 63u);
-    const uint32_t ws[4] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w};
+__device__ __forceinline__ void fetch_meta(WMeta<FMT> &m, __amdgpu_buffer_rsrc_t rm,
+                                           const uint32_t (&lm)[2], int win) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        // stored nibbles are q ^ 8
-        const uint32_t byte = ((ws[k] >> (8 * i)) & 0xFFu) ^ 0x88u;
-        // src/quant/mod.rs:841: d * sc * q - dmin * m (exact products)
-        v[8 * k + i] = d * sc * (float)(byte & 15u) - dmin * mn;
-        v[8 * k + 4 + i] = d * sc * (float)(byte >> 4) - dmin * mn;
-      }
-  } else if constexpr (FMT == NX_FMT_Q8_0) {
-    const float d = h2f((w.m.x >> w.m.y) & 0xFFFFu);
-    const uint32_t ws[8] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w,
-                            w.q[1].x, w.q[1].y, w.q[1].z, w.q[1].w};
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        v[4 * j + i] = (float)(int32_t)(int8_t)((ws[j] >> (8 * i)) & 0xFFu) * d;
-  } else if constexpr (FMT == NX_FMT_Q4_0) {
-    const float d = h2f((w.m.x >> (16 * h)) & 0xFFFFu);
-    const uint32_t ws[4] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t byte = ((ws[k] >> (8 * i)) & 0xFFu) ^ 0x88u;  // stored nibbles are q ^ 8
-        v[8 * k + i] = (float)((int)(byte & 15u) - 8) * d;
-        v[8 * k + 4 + i] = (float)((int)(byte >> 4) - 8) * d;
-      }
-  } else {
-    const uint4 all[8] = {w.q[0], w.q[1], w.f[0], w.f[1], w.f[2], w.f[3], w.f[4], w.f[5]};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      v[4 * j] = __uint_as_float(all[j].x);
-      v[4 * j + 1] = __uint_as_float(all[j].y);
-      v[4 * j + 2] = __uint_as_float(all[j].z);
-      v[4 * j + 3] = __uint_as_float(all[j].w);
-    }
+  for (int n = 0; n < 2; ++n) {
+    if constexpr (FMT == NX_FMT_Q8_0) m.m[n] = bload4(rm, lm[n] + 16u * win);
+    else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) m.m[n] = bload16(rm, lm[n] + 32u * win);
   }
 }
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-
-// The 32 weights of this lane's half step as MFMA B operands b[kk] (values
-// 8kk .. 8kk+7 of the half).
-template <int FMT, bool BF16>
-__device__ __forceinline__ void w_operands(const WLoad<FMT> &w, int ks, int h,
-                                           typename OpT<BF16>::V8 (&b)[4]) {
+// values 8M .. 8M+7 of the 16 of row n at step S of the window, as a B operand
+template <int FMT, bool BF16, int S, int M>
+__device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WCodes<FMT> &w,
+                                                           const WMeta<FMT> &mt, int n) {
+  using Op = OpT<BF16>;
   if constexpr (FMT == NX_FMT_Q8_0 && !BF16) {
     // fp16 without a float detour: byte u = q ^ 0x80 becomes the f16 1024 + u
     // (exponent byte 0x64 above it), minus 1152 gives q exactly, and the f16
     // product with the f16 scale is q * d rounded once, as from the exact value
 #pragma clang fp contract(off)
-    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(w.m.x >> w.m.y));
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(mt.m[n] >> (16 * (S >> 1))));
     const h2 dd = {d, d}, off = {(_Float16)1152.0f, (_Float16)1152.0f};
-    const uint32_t ws[8] = {w.q[0].x, w.q[0].y, w.q[0].z, w.q[0].w,
-                            w.q[1].x, w.q[1].y, w.q[1].z, w.q[1].w};
+    const uint32_t ws[2] = {M ? w.c[n].z : w.c[n].x, M ? w.c[n].w : w.c[n].y};
+    h2 r[4];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      h2 r[4];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const uint32_t u = ws[2 * kk + j] ^ 0x80808080u;
-        const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
-        const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
-        r[2 * j] = (lo - off) * dd;
-        r[2 * j + 1] = (hi - off) * dd;
-      }
-      b[kk] = typename OpT<BF16>::V8{r[0][0], r[0][1], r[1][0], r[1][1],
-                                     r[2][0], r[2][1], r[3][0], r[3][1]};
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t u = ws[j] ^ 0x80808080u;
+      const h2 lo = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
+      const h2 hi = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
+      r[2 * j] = (lo - off) * dd;
+      r[2 * j + 1] = (hi - off) * dd;
     }
+    return typename Op::V8{r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
   } else {
-    float v[32];
-    w_decode<FMT>(w, ks, h, v);
+    float v[8];
+    if constexpr (FMT == NX_FMT_Q8_0) {
+      const float d = h2f((mt.m[n] >> (16 * (S >> 1))) & 0xFFFFu);
+      const uint32_t ws[2] = {M ? w.c[n].z : w.c[n].x, M ? w.c[n].w : w.c[n].y};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+      for (int k = 0; k < 2; ++k)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) b[kk][i] = (typename OpT<BF16>::T)v[8 * kk + i];
+        for (int i = 0; i < 4; ++i)
+          v[4 * k + i] = (float)(int32_t)(int8_t)((ws[k] >> (8 * i)) & 0xFFu) * d;
+    } else if constexpr (FMT == NX_FMT_Q4_K) {
+      // sub-block t + 4p of the block; src/quant/mod.rs:841: d * sc * q - dmin * m
+      constexpr int t = S & 3, p = S >> 2;
+      const uint4 Q = mt.m[n];
+      const float d = h2f(Q.x & 0xFFFFu), dmin = h2f(Q.x >> 16);
+      const uint32_t b0 = (Q.y >> (8 * t)) & 0xFFu;
+      const uint32_t b4 = (Q.z >> (8 * t)) & 0xFFu;
+      const uint32_t b8 = (Q.w >> (8 * t)) & 0xFFu;
+      const float sc = p ? (float)((b8 & 15u) | ((b0 >> 6) << 4)) : (float)(b0 & 63u);
+      const float mn = p ? (float)((b8 >> 4) | ((b4 >> 6) << 4)) : (float)(b4 & 63u);
+      const uint32_t ws = M ? w.c[n].y : w.c[n].x;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t byte = ((ws >> (8 * i)) & 0xFFu) ^ 0x88u;  // stored nibbles are q ^ 8
+        v[i] = d * sc * (float)(byte & 15u) - dmin * mn;
+        v[4 + i] = d * sc * (float)(byte >> 4) - dmin * mn;
+      }
+    } else if constexpr (FMT == NX_FMT_Q4_0) {
+      // segment 8u + 4(q/2) + t: dword t of the scales, block half p
+      constexpr int t = S & 3, p = S >> 2;
+      const uint32_t mw = t == 0 ? mt.m[n].x : (t == 1 ? mt.m[n].y : (t == 2 ? mt.m[n].z : mt.m[n].w));
+      const float d = h2f((mw >> (16 * p)) & 0xFFFFu);
+      const uint32_t ws = M ? w.c[n].y : w.c[n].x;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t byte = ((ws >> (8 * i)) & 0xFFu) ^ 0x88u;
+        v[i] = (float)((int)(byte & 15u) - 8) * d;
+        v[4 + i] = (float)((int)(byte >> 4) - 8) * d;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const uint4 c = w.c[n][2 * M + k];
+        v[4 * k] = __uint_as_float(c.x);
+        v[4 * k + 1] = __uint_as_float(c.y);
+        v[4 * k + 2] = __uint_as_float(c.z);
+        v[4 * k + 3] = __uint_as_float(c.w);
+      }
+    }
+    typename Op::V8 b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = (typename Op::T)v[i];
+    return b;
   }
 }
 
-// element index (within the activation row) of K position p of step ks
-template <int FMT>
-__device__ __forceinline__ int a_elem(int ks, int p) {
-  if constexpr (FMT == NX_FMT_Q4_K)
-    return (ks >> 2) * 256 + (ks & 3) * 32 + (p & 31) + ((p >> 5) << 7);
-  return ks * 64 + p;
-}
-
 // LDS ring of activation stages: stage = the 128 x 64 activation tile of one
-// K step as 128 rows of eight 16-byte chunks; chunk c of row r is stored at
-// slot c ^ (r & 7), so the MFMA reads of eight consecutive rows hit eight
-// different bank groups.  Distinct arrays per stage let the compiler track
-// each stage's direct-to-LDS loads separately.
+// K step as 128 rows of eight 16-byte chunks (chunk c = operand positions
+// 8c .. 8c+7 of the step); chunk c of row r is stored at slot
+// c ^ ((r / 2) % 8).  A 16-lane group of an MFMA operand read takes one chunk
+// of 16 consecutive rows: rows 2k and 2k+1 fall in the two halves of the
+// 64 banks, and the swizzle spreads the eight row pairs over eight slots, so
+// the read is free of bank conflicts.  Distinct arrays per stage let the
+// compiler track each stage's direct-to-LDS loads separately.
 constexpr int RING = 4;
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -271,16 +378,31 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
-// F32 weights keep 64 floats of codes per stage per lane: one workgroup per CU
+template <int V>
+using IC = std::integral_constant<int, V>;
+
+// compile-time loop: f(IC<I>{}), ..., f(IC<N-1>{})
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (I < N) {
+    f(IC<I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// F32 weights keep 2 x 64 floats of codes per step per lane: one workgroup per CU
 template <int FMT, bool BF16, bool GATEUP>
 __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const GemmArgs g) {
   using Op = OpT<BF16>;
   using V8 = typename Op::V8;
   constexpr int NMAT = GATEUP ? 2 : 1;
-  // vector-memory instructions per K step: 4 activation chunks, and per
-  // matrix the weight codes and scales
-  constexpr int NWM = FMT == NX_FMT_F32 ? 8 : (FMT == NX_FMT_Q8_0 ? 3 : 2);
-  constexpr int NA = 4, NW = NMAT * NWM;
+  constexpr int WS = win_steps<FMT>();
+  // steps per loop body: two scale windows (static double buffering of the
+  // scales), and whole rounds of the ring and of the two code buffers
+  constexpr int NB = WS >= 2 ? 2 * WS : RING;
+  static_assert(NB % RING == 0, "loop body must cover whole ring rounds");
+  constexpr int NA = 4;
+  constexpr int IG = GATEUP ? 2 : 4;  // M-tiles per scheduling group
   __shared__ __attribute__((aligned(16))) uint4 ring0[BM * 8];
   __shared__ __attribute__((aligned(16))) uint4 ring1[BM * 8];
   __shared__ __attribute__((aligned(16))) uint4 ring2[BM * 8];
@@ -330,160 +452,224 @@ __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const G
   const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(m0p, (uint32_t)rows * rm);
   const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(m1p, (uint32_t)rows * rm);
 
-  // ---- activation chunks: instruction q of this wave fills stage chunks
-  // (4 * wave + q) * 64 + lane, i.e. row r_q = (4 * wave + q) * 8 + lane / 8,
-  // slot lane % 8, which holds K chunk (lane % 8) ^ (r_q & 7) of that row
+  // ---- activation chunks: instruction i of this wave fills stage chunks
+  // (4 * wave + i) * 64 + lane, i.e. row r_i = (4 * wave + i) * 8 + lane / 8,
+  // slot lane % 8, which holds chunk (lane % 8) ^ ((r_i / 2) % 8) of that row
   // (gathered through the permutation for gate/up).  One wave-uniform
-  // resource spans the activation buffer; absent rows read zero.
+  // resource spans the activation buffer; absent rows, and every step past
+  // the padded width, read zero (rows are zero between the width and the
+  // padded width).
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.a, g.a_bytes);
-  uint32_t aoff[NA];
-  int achunk[NA];
+  uint32_t abase[NA];
   int arow[NA];
 #pragma unroll
-  for (int q = 0; q < NA; ++q) {
-    const int r = (4 * wave + q) * 8 + (lane >> 3);
-    achunk[q] = (lane & 7) ^ (r & 7);
+  for (int i = 0; i < NA; ++i) {
+    const int r = (4 * wave + i) * 8 + (lane >> 3);
     // absent rows look up the tile's first pair (always present) and are
     // masked below, so the four lookups go out together
     const int p = pair0 + m0 + (r < mrows ? r : 0);
-    arow[q] = GATEUP ? (routed ? g.perm_token[p] : p - pair0) : p;
+    arow[i] = GATEUP ? (routed ? g.perm_token[p] : p - pair0) : p;
   }
 #pragma unroll
-  for (int q = 0; q < NA; ++q) {
-    const int r = (4 * wave + q) * 8 + (lane >> 3);
-    aoff[q] = r < mrows ? (uint32_t)arow[q] * (uint32_t)g.a_stride * 2u : OOB;
+  for (int i = 0; i < NA; ++i) {
+    const int r = (4 * wave + i) * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+    abase[i] = r < mrows ? (uint32_t)arow[i] * (uint32_t)g.a_stride * 2u + 16u * chunk : OOB;
   }
+  // steps holding data (the padded width), and the steps run: whole loop
+  // bodies (the steps past the padded width load zeros and add nothing)
+  const int nk_data = kpad_steps<FMT>(cols);
+  const int nks = (nk_data + NB - 1) / NB * NB;
 
-  // ---- weights: row n0 + 32 * wave + lane % 32, half lane / 32 of the step
-  const int l32 = lane & 31, kh = lane >> 5;
-  const int wrow = n0 + 32 * wave + l32;
-  const bool wrow_ok = wrow < rows;
-  const uint32_t wq_off = (uint32_t)wrow * rq, wm_off = (uint32_t)wrow * rm;
-
-  // number of 64-element K steps
-  const int nks = FMT == NX_FMT_Q4_K ? nseg : (FMT == NX_FMT_F32 ? (nseg + 7) / 8 : (FMT == NX_FMT_Q8_0 ? (nseg + 1) / 2 : nseg));
+  // ---- weights: rows n0 + 32 * wave + 16 n + lane % 16, quarter lane / 16
+  const int l16 = lane & 15, q = lane >> 4;
+  uint32_t lq[2], lm[2];
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    const uint32_t wrow = (uint32_t)(n0 + 32 * wave + 16 * n + l16);
+    lq[n] = code_lane_off<FMT>(wrow * rq, q);
+    lm[n] = meta_lane_off<FMT>(wrow * rm, q);
+  }
 
   auto issue_a = [&](auto stage, int ks) {
     constexpr int S = decltype(stage)::value;
     uint4 *dst = ring_stage<S>(ring0, ring1, ring2, ring3);
+    // wave-uniform step offset; past the padded width it pushes every lane
+    // out of range (bases stay below 2^31, so the sum does not wrap)
+    const uint32_t koff = ks < nk_data ? (uint32_t)ks * (2u * BK) : OOB;
 #pragma unroll
-    for (int q = 0; q < NA; ++q) {
-      const int el = a_elem<FMT>(ks, 8 * achunk[q]);
-      const uint32_t off = (aoff[q] != OOB && el < cols) ? aoff[q] + (uint32_t)el * 2u : OOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(dst + (4 * wave + q) * 64), 16, off,
+    for (int i = 0; i < NA; ++i) {
+      const uint32_t off = abase[i] + koff;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(dst + (4 * wave + i) * 64), 16, off,
                                                0, 0, 0);
     }
   };
-  WLoad<FMT> wbuf[2][NMAT];
-  auto issue_w = [&](WLoad<FMT>(&wb)[NMAT], int ks) {
-    // steps past the end read zeros (their activations are zero too)
+  // Scales: Q8_0 (one dword per row) double-buffers them, loaded with the
+  // codes of a window's first step; the 16-byte scales of the 4-bit formats
+  // have one buffer, reloaded right after the last decode of a window.
+  constexpr bool META2 = FMT == NX_FMT_Q8_0;
+  constexpr int NMB = META2 ? 2 : 1;
+  WCodes<FMT> wbuf[2][NMAT];
+  WMeta<FMT> mbuf[NMB][NMAT];
+  // loads of the weights of step P of a loop body (P may reach into the next
+  // body) whose first window is wbase
+  auto issue_w = [&](auto pos, int wbase) {
+    constexpr int P = decltype(pos)::value;
+    constexpr int S = P % WS;
+    const int win = wbase + P / WS;
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
-      w_fetch<FMT>(wb[mt], mt == 0 ? rq0 : rq1, mt == 0 ? rm0 : rm1, wq_off, wm_off, ks, kh, nseg,
-                   wrow_ok && ks < nks);
+      fetch_codes<FMT, S>(wbuf[P % 2][mt], mt == 0 ? rq0 : rq1, lq, win, nseg);
+    if constexpr (META2 && S == 0) {
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+        fetch_meta<FMT>(mbuf[(P / WS) % NMB][mt], mt == 0 ? rm0 : rm1, lm, win);
+    }
+  };
+  // single-buffered scales of the window that starts at step P
+  auto issue_meta1 = [&](auto pos, int wbase) {
+    constexpr int P = decltype(pos)::value;
+    if constexpr (!META2 && n_meta_loads<FMT>() > 0) {
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+        fetch_meta<FMT>(mbuf[0][mt], mt == 0 ? rm0 : rm1, lm, wbase + P / WS);
+    }
   };
 
-  // ---- accumulators: acc[mt][mi] = pairs 32mi .. 32mi+31 x this wave's 32 rows
-  f32x16 acc[NMAT][4];
+  // ---- accumulators: acc[mt][n][i] = pairs 16i .. 16i+15 x rows 16n .. of this wave
+  f32x4 acc[NMAT][2][8];
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[mt][i][r] = 0.f;
+      for (int i = 0; i < 8; ++i) acc[mt][n][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Software pipeline over a whole number of ring rounds (steps past nks load
-  // zeros and add nothing).  Step ks: wait until this wave's loads of
-  // activation stage ks and weights ks have landed, barrier (every wave's
-  // share of the stage is in LDS, and every wave is done reading stage ks-1's
-  // slot), issue activation stage ks+3 into that slot and weights ks+2, decode
-  // weights ks into B operands, run the step's MFMAs.  Every step issues the
-  // same loads, unconditionally (a conditional load would make the compiler
-  // copy its registers, waiting for all loads in flight): A(ks) at step ks-3,
-  // W(ks) at step ks-2 after A(ks+1), so after W(ks) come exactly A(ks+2) and
-  // W(ks+1), and vmcnt <= NA + NW completes both.
-  auto wait_step = [&]() {
-    wait_vm<NA + NW>();
+  // Software pipeline.  Step ks: wait until this wave's loads of activation
+  // stage ks and weights ks have landed, barrier (every wave's share of the
+  // stage is in LDS, and every wave is done reading stage ks-1's slot), issue
+  // activation stage ks+3 into that slot, decode weights ks into B operands
+  // and run the step's MFMAs, half by half, issuing weights ks+2 (and, for
+  // single-buffered scales at a window's last step, the next window's
+  // scales before them) after the last decode.  Every step issues its loads
+  // unconditionally (a conditional load would make the compiler copy its
+  // registers, waiting for all loads in flight).  So after W(ks) (issued in
+  // step ks-2) come A(ks+2), the scales of a window starting at ks+1, and
+  // W(ks+1); a window starting at ks has its scales issued after A(ks+2).
+  const int sw = (l16 >> 1) & 7;
+  constexpr int NCW = NMAT * n_code_loads<FMT>();
+  constexpr int NMW = NMAT * n_meta_loads<FMT>();
+  auto step = [&](auto pos, int ks0, int wbase) {
+    constexpr int P = decltype(pos)::value;
+    constexpr int S = P % WS;
+    constexpr bool wstart = P % WS == 0, wnext = (P + 1) % WS == 0;
+    constexpr int NOUT = META2 ? NA + NCW + (wnext ? NMW : 0)
+                               : (wstart ? NCW : NA + NCW + (wnext ? NMW : 0));
+    wait_vm<NOUT>();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-  };
-  auto compute = [&](auto stage, const V8 (&bf)[NMAT][4]) {
-    constexpr int S = decltype(stage)::value;
-    const uint4 *src = ring_stage<S>(ring0, ring1, ring2, ring3);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int c = 4 * kh + kk;
-      V8 af[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 32 * i + l32;
-        af[i] = __builtin_bit_cast(V8, src[r * 8 + (c ^ (r & 7))]);
-      }
+    issue_a(IC<(P + 3) % RING>{}, ks0 + P + 3);
+    const uint4 *src = ring_stage<P % RING>(ring0, ring1, ring2, ring3);
+    // two halves of 32 K positions: B operands of the half, then its MFMAs
+    // (a scheduling fence between the halves bounds the live operands).  The
+    // code buffer of this step takes step P+2's loads once both halves are
+    // decoded.
+    static_for<0, 2>([&](auto half) {
+      constexpr int M = decltype(half)::value;
+      V8 bf[NMAT][2];
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mt][i] = Op::mfma(af[i], bf[mt][kk], acc[mt][i]);
-    }
-  };
-  auto step = [&](auto stage, auto buf, int ks) {
-    constexpr int S = decltype(stage)::value, B = decltype(buf)::value;
-    wait_step();
-    issue_a(std::integral_constant<int, (S + 3) % RING>{}, ks + 3);
-    V8 bf[NMAT][4];
+        for (int n = 0; n < 2; ++n) {
+          bf[mt][n] = w_operand<FMT, BF16, S, M>(wbuf[P % 2][mt], mbuf[(P / WS) % NMB][mt], n);
+          // float decodes: one operand's temporaries at a time
+          if constexpr (!(FMT == NX_FMT_Q8_0 && !BF16)) __builtin_amdgcn_sched_barrier(0);
+        }
+      if constexpr (M == 1) {
+        if constexpr (wnext) issue_meta1(IC<P + 1>{}, wbase);
+        issue_w(IC<P + 2>{}, wbase);
+      }
+      // M-tiles in groups (bounds the A operands read ahead)
 #pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) w_operands<FMT, BF16>(wbuf[B][mt], ks, kh, bf[mt]);
-    issue_w(wbuf[B], ks + 2);
-    compute(stage, bf);
-    // keep each step's work in its step (register pressure)
-    __builtin_amdgcn_sched_barrier(0);
+      for (int ig = 0; ig < 8 / IG; ++ig) {
+#pragma unroll
+        for (int i = IG * ig; i < IG * ig + IG; ++i) {
+          const V8 af = __builtin_bit_cast(V8, src[(16 * i + l16) * 8 + ((2 * q + M) ^ sw)]);
+#pragma unroll
+          for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+            for (int n = 0; n < 2; ++n) acc[mt][n][i] = Op::mfma(af, bf[mt][n], acc[mt][n][i]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    });
   };
 
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  issue_a(I0{}, 0);
-  issue_a(I1{}, 1);
-  issue_w(wbuf[0], 0);
-  issue_a(I2{}, 2);
-  issue_w(wbuf[1], 1);
-  for (int ks = 0; ks < nks; ks += RING) {
-    step(I0{}, I0{}, ks);
-    step(I1{}, I1{}, ks + 1);
-    step(I2{}, I0{}, ks + 2);
-    step(I3{}, I1{}, ks + 3);
-  }
+  issue_a(IC<0>{}, 0);
+  issue_a(IC<1>{}, 1);
+  issue_meta1(IC<0>{}, 0);
+  issue_w(IC<0>{}, 0);
+  issue_a(IC<2>{}, 2);
+  issue_w(IC<1>{}, 0);
+  for (int ks0 = 0, wbase = 0; ks0 < nks; ks0 += NB, wbase += NB / WS)
+    static_for<0, NB>([&](auto pos) { step(pos, ks0, wbase); });
   // no direct-to-LDS write may land after the workgroup has ended
   wait_vm<0>();
 
-  // ---- epilogue.  32x32 accumulator layout: lane holds column (lane % 32),
-  // register r holds row (r / 4) * 8 + (lane / 32) * 4 + r % 4.
-  const int col = n0 + 32 * wave + l32, rq4 = kh * 4;
+  // ---- epilogue.  16x16 accumulator layout: lane holds column (lane % 16),
+  // register j holds row 4 * (lane / 16) + j.
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int n = 0; n < 2; ++n) {
+    const int col = n0 + 32 * wave + 16 * n + l16;
+    if (col >= rows) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = i * 32 + (r >> 2) * 8 + rq4 + (r & 3);
-      if (row < mrows && col < rows) {
-        const size_t p = (size_t)(pair0 + m0 + row);
-        if constexpr (GATEUP) {
-          const float v = silu_mul(acc[0][i][r], acc[1][i][r]);
-          g.act[p * g.act_stride + col] = Op::bits(v);
-        } else {
-          g.y[p * g.y_stride + col] = acc[0][i][r];
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = 16 * i + 4 * q + j;
+        if (row < mrows) {
+          const size_t p = (size_t)(pair0 + m0 + row);
+          if constexpr (GATEUP) {
+            const float v = silu_mul(acc[0][n][i][j], acc[1][n][i][j]);
+            g.act[p * g.act_stride + kslot<FMT>(col)] = Op::bits(v);
+          } else {
+            g.y[p * g.y_stride + col] = acc[0][n][i][j];
+          }
         }
       }
-    }
+  }
 }
 
-// f32 activations -> operand type (one row per token)
-template <bool BF16>
-__global__ __launch_bounds__(256) void k_to_half(const float *__restrict__ x, size_t n,
+// f32 activations [T][H] -> operand type in operand order [T][kpad]
+// (positions past H are zero)
+template <int FMT, bool BF16>
+__global__ __launch_bounds__(256) void k_to_half(const float *__restrict__ x, int T, int H, int kpad,
                                                  uint16_t *__restrict__ out) {
+  const size_t n = (size_t)T * kpad;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-       i += (size_t)gridDim.x * blockDim.x)
-    out[i] = OpT<BF16>::bits(x[i]);
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t t = i / (size_t)kpad;
+    const int e = kpos<FMT>((int)(i - t * kpad));
+    out[i] = e < H ? OpT<BF16>::bits(x[t * H + e]) : (uint16_t)0;
+  }
+}
+
+// zero act's operand positions of elements width(p) .. kpad-1 (width F for
+// routed pairs, Fs for the shared expert's pairs p >= routed)
+template <int FMT>
+__global__ __launch_bounds__(256) void k_zero_pad(uint16_t *__restrict__ act, int stride,
+                                                  size_t routed, size_t pairs, int F, int Fs,
+                                                  int kpad) {
+  const int wmin = min(F, Fs > 0 ? Fs : F);
+  const int span = kpad - wmin;
+  const size_t n = pairs * (size_t)span;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t p = i / (size_t)span;
+    const int e = wmin + (int)(i - p * span);
+    if (e >= (p < routed ? F : Fs)) act[p * stride + kslot<FMT>(e)] = 0;
+  }
 }
 
 using GemmFn = void (*)(GemmArgs);
@@ -545,8 +731,8 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   a.has_shared = ex->Fs > 0 ? 1 : 0;
   if (gateup) {
     a.a = static_cast<const uint16_t *>(p.xh);
-    a.a_stride = ex->H;
-    a.a_bytes = (uint32_t)((size_t)p.T * ex->H * 2);
+    a.a_stride = p.x_stride;
+    a.a_bytes = (uint32_t)((size_t)p.T * p.x_stride * 2);
     a.perm_token = p.perm_token;
     a.act = static_cast<uint16_t *>(p.act);
     a.act_stride = p.act_stride;
@@ -574,21 +760,65 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
                 [&] { hipLaunchKernelGGL(fn, dim3((unsigned)wgs), dim3(256), 0, c->stream, a); });
 }
 
+template <int FMT>
+int to_half_fmt(nx_ctx *c, const float *x, int T, int H, int kpad, bool bf16, uint16_t *o) {
+  size_t gblocks = ((size_t)T * kpad + 255) / 256;
+  if (gblocks > 65536) gblocks = 65536;
+  const unsigned gb = (unsigned)gblocks;
+  if (bf16)
+    return launch(c, "to_bf16",
+                  [&] { k_to_half<FMT, true><<<gb, 256, 0, c->stream>>>(x, T, H, kpad, o); });
+  return launch(c, "to_f16",
+                [&] { k_to_half<FMT, false><<<gb, 256, 0, c->stream>>>(x, T, H, kpad, o); });
+}
+
 }  // namespace
 
 int gemm_tile_m() { return BM; }
 
-int launch_to_half(nx_ctx *c, const float *x, size_t n, bool bf16, void *out) {
-  if (n == 0) return NX_OK;
-  size_t gblocks = (n + 255) / 256;
-  if (gblocks > 65536) gblocks = 65536;
+int gemm_kpad(int fmt, int cols) { return kpad_of(fmt, cols); }
+
+int launch_to_half(nx_ctx *c, int fmt, const float *x, int T, int H, int kpad, bool bf16,
+                   void *out) {
+  if (T == 0) return NX_OK;
   uint16_t *o = static_cast<uint16_t *>(out);
-  if (bf16)
-    return launch(c, "to_bf16", [&] { k_to_half<true><<<(unsigned)gblocks, 256, 0, c->stream>>>(x, n, o); });
-  return launch(c, "to_f16", [&] { k_to_half<false><<<(unsigned)gblocks, 256, 0, c->stream>>>(x, n, o); });
+  switch (fmt) {
+  case NX_FMT_Q4_K: return to_half_fmt<NX_FMT_Q4_K>(c, x, T, H, kpad, bf16, o);
+  case NX_FMT_Q8_0: return to_half_fmt<NX_FMT_Q8_0>(c, x, T, H, kpad, bf16, o);
+  case NX_FMT_Q4_0: return to_half_fmt<NX_FMT_Q4_0>(c, x, T, H, kpad, bf16, o);
+  case NX_FMT_F32: return to_half_fmt<NX_FMT_F32>(c, x, T, H, kpad, bf16, o);
+  }
+  return fail(NX_ERR_UNSUPPORTED, "no operand conversion for this format");
 }
 
-int launch_gemm_gateup(nx_ctx *c, const GemmPlan &p) { return run(c, p, true); }
+int launch_gemm_gateup(nx_ctx *c, const GemmPlan &p) {
+  // act rows hold zeros between each expert's width and the padded width
+  const nx_experts *ex = p.ex;
+  const int wmin = ex->Fs > 0 ? std::min(ex->F, ex->Fs) : ex->F;
+  if (p.act_stride > wmin) {
+    const size_t routed = (size_t)p.T * p.k;
+    const size_t n = p.pairs_total * (size_t)(p.act_stride - wmin);
+    const unsigned gb = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
+    uint16_t *act = static_cast<uint16_t *>(p.act);
+    const int F = ex->F, Fs = ex->Fs, st = p.act_stride;
+    int rc = NX_OK;
+    switch (ex->fmt) {
+#define NX_ZP(F_)                                                                            \
+  case F_:                                                                                   \
+    rc = launch(c, "zero_pad", [&] {                                                         \
+      k_zero_pad<F_><<<gb, 256, 0, c->stream>>>(act, st, routed, p.pairs_total, F, Fs, st); \
+    });                                                                                      \
+    break;
+      NX_ZP(NX_FMT_Q4_K)
+      NX_ZP(NX_FMT_Q8_0)
+      NX_ZP(NX_FMT_Q4_0)
+      NX_ZP(NX_FMT_F32)
+#undef NX_ZP
+    }
+    NX_TRY(rc);
+  }
+  return run(c, p, true);
+}
 int launch_gemm_down(nx_ctx *c, const GemmPlan &p) { return run(c, p, false); }
 
 }  // namespace nx

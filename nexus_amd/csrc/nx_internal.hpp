@@ -197,11 +197,14 @@ struct GemmPlan {
   void *act;             // [pairs_total][act_stride] half precision
   int act_stride;
   float *ypair;
-  void *xh;              // [T][H] half precision copy of x
+  void *xh;              // [T][x_stride] half precision copy of x, operand order
+  int x_stride;
   size_t pairs_total;    // rows of act / ypair
 };
 int gemm_tile_m();
-int launch_to_half(nx_ctx *c, const float *x, size_t n, bool bf16, void *out);
+// width of a row of GEMM operands (operand order pads to whole scale windows)
+int gemm_kpad(int fmt, int cols);
+int launch_to_half(nx_ctx *c, int fmt, const float *x, int T, int H, int kpad, bool bf16, void *out);
 int launch_gemm_gateup(nx_ctx *c, const GemmPlan &p);
 int launch_gemm_down(nx_ctx *c, const GemmPlan &p);
 
