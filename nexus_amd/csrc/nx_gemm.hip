@@ -411,20 +411,35 @@ __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const G
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // Tile order.  xcd_split (gate/up): workgroup L runs on XCD L % 8; XCD x
-  // owns N-tiles [x * npx, (x+1) * npx) and walks them with the M-tile list
-  // fastest, so the M-tiles of one expert take each weight tile from the same
-  // L2 back to back.  Otherwise (down, whose activation tiles span K = the
-  // expert width and are the larger operand): N-tiles fastest, so the N-tiles
-  // of one activation tile run together.
+  // owns N-tiles [x * npx, (x+1) * npx) and takes the experts in tile-list
+  // order, each as a block of (its m_e M-tiles) x (the XCD's N-tiles), in
+  // groups of g_e = XCD_WGS / m_e N-tiles with the M-tiles fastest: about
+  // XCD_WGS workgroups, as many as an XCD runs at once, share g_e weight
+  // tiles and m_e activation tiles through the XCD's L2.  Otherwise (down,
+  // whose activation tiles span K = the expert width and are the larger
+  // operand): N-tiles fastest, so the N-tiles of one activation tile run
+  // together.
+  constexpr int XCD_WGS = 64;  // 32 CUs x 2 workgroups
   const int L = blockIdx.x;
   const int mcount = g.tiles[0];
   if (mcount <= 0) return;
   int tile, ntile;
   if (g.xcd_split) {
     const int xcd = L & 7, j = L >> 3, npx = (g.n_tiles + 7) >> 3;
-    tile = j % mcount;
-    ntile = xcd * npx + j / mcount;
-    if (ntile >= min(g.n_tiles, (xcd + 1) * npx)) return;  // workgroup-uniform
+    // the expert's block: tiles of one expert are consecutive, first rows
+    // 0, BM, 2 BM, ...
+    const int tg = j / npx;
+    if (tg >= mcount) return;  // workgroup-uniform
+    const int eg = g.tiles[2 + 2 * tg];
+    const int te = tg - g.tiles[3 + 2 * tg] / BM;
+    const int cnt = eg < g.E ? g.offsets[eg + 1] - g.offsets[eg] : g.T;
+    const int me = (cnt + BM - 1) / BM;
+    const int ge = max(1, XCD_WGS / me);
+    const int r = j - te * npx;
+    const int grp = r / (ge * me), r2 = r - grp * ge * me;
+    tile = te + r2 % me;
+    ntile = xcd * npx + grp * ge + r2 / me;
+    if (ntile >= g.n_tiles) return;  // workgroup-uniform
   } else {
     tile = L / g.n_tiles;
     ntile = L - tile * g.n_tiles;
