@@ -624,7 +624,6 @@ int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const 
   NX_TRY(ws(c, WS_PERM_SLOT, tk, &d_ps));
   NX_TRY(ws(c, WS_INV_POS, tk, &d_inv));
   NX_TRY(ws(c, WS_ACTIVE, (size_t)E + 1, &d_act));
-  NX_TRY(ws(c, WS_YPAIR, pairs_total * H, &d_ypair));
 
   int use = path;
   if (use == NX_PATH_AUTO) {
@@ -635,6 +634,7 @@ int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const 
   }
 
   if (use == NX_PATH_GEMV) {
+    NX_TRY(ws(c, WS_YPAIR, pairs_total * H, &d_ypair));
     if (route_permute_fusable(T, E, k)) {
       NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
                                   d_pt, d_ps, d_inv, d_act, nullptr, 0));
@@ -674,11 +674,16 @@ int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const 
   NX_TRY(ws_get(c, WS_XH, (size_t)T * x_stride * 2, &d_xh));
   NX_TRY(launch_to_half(c, ex->fmt, d_x, T, H, x_stride, bf16, d_xh));
   NX_TRY(ws_get(c, WS_ACT, pairs_total * act_stride * 2, &d_acth));
+  // the down pass splits K when that fills the CUs' rounds better; each
+  // split writes its own partial sums, added by the combine
+  const int ksplit = gemm_down_ksplit(ex->fmt, std::max(ex->F, ex->Fs), H, max_tiles, 2 * c->num_cu);
+  NX_TRY(ws(c, WS_YPAIR, (size_t)ksplit * pairs_total * H, &d_ypair));
   GemmPlan mp{ex, T, k, bf16, d_x, d_pt, d_off, d_act, d_tiles, max_tiles, d_acth, act_stride,
-              d_ypair, d_xh, x_stride, pairs_total};
+              d_ypair, d_xh, x_stride, pairs_total, ksplit};
   NX_TRY(launch_gemm_gateup(c, mp));
   NX_TRY(launch_gemm_down(c, mp));
-  NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out));
+  NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out, ksplit,
+                        pairs_total * (size_t)H));
   return NX_OK;
 }
 

@@ -10,9 +10,10 @@
 // Work decomposition.  The permutation kernel lists M-tiles (expert, first
 // pair) of 128 pairs; the 1-D grid covers (M-tile, 128-row N-tile) pairs in
 // an XCD-aware order (see k_gemm; extra workgroups exit).  A workgroup of 4
-// waves owns a 128x128 output tile (gate/up: two of them, for the gate and
-// the up rows); wave w owns weight rows 32w .. 32w+31 of the tile for all 128
-// pairs, as 2 x 8 v_mfma_f32_16x16x32 tiles per matrix.
+// waves owns a 128 x 64NT output tile (gate/up: two of them, for the gate
+// and the up rows); wave w owns weight rows 16NT w .. 16NT w + 16NT - 1 of
+// the tile for all 128 pairs, as NT x 8 v_mfma_f32_16x16x32 tiles per
+// matrix (NT = 4 for gate/up, 2 for down; see GemmShape).
 //
 // Operand order.  The K loop takes 64 positions per step.  Position
 // j = 64 ks + 16 q + i is value i of the lanes of quarter q (lanes 16q ..
@@ -34,6 +35,9 @@
 #include <type_traits>
 
 #include "nx_device.hpp"
+#ifndef WDIST_CFG
+#define WDIST_CFG 2
+#endif
 #include "nx_internal.hpp"
 
 namespace nx {
@@ -46,7 +50,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128;   // pairs per tile
-constexpr int BN = 128;   // weight rows per tile
 constexpr int BK = 64;    // K positions per step
 
 template <bool BF16>
@@ -80,10 +83,10 @@ struct OpT<true> {
 // window of format FMT, operand position j (step s = (j / 64) % steps, lane
 // quarter q = (j / 16) % 4, value i = j % 16) holds activation element
 // kpos(j):
-//   Q8_0 (window 256 = blocks 8u .. 8u+7, 4 steps): quarter q takes blocks
-//        8u+2q (steps 0, 1) and 8u+2q+1 (steps 2, 3), code-plane half s%2,
-//        so e = 256u + 64q + 16s + i (a transpose of 16-element pieces); its
-//        two scales are one dword.
+//   Q8_0 (window 256 = blocks 8u .. 8u+7, 4 steps): quarter q takes block
+//        8u + 2q + s%2, code-plane half s/2, so e = 256u + 64q + 32(s%2) +
+//        16(s/2) + i; its two scales are one dword, and steps 2k, 2k+1 read
+//        the two halves of the same 128-byte lines.
 //   Q4_K (window 512 = blocks 2u, 2u+1, 8 steps): quarter q takes block
 //        2u + q/2, sub-block (s%4) + 4(s/4), bytes 8(q%2) .. +7 of its
 //        16-byte half: e = 512u + 256(q/2) + 128(s/4) + 32(s%4) + 16(q%2) + i;
@@ -101,7 +104,8 @@ __host__ __device__ constexpr int kwin() {
 template <int FMT>
 __host__ __device__ __forceinline__ int kpos(int j) {
   if constexpr (FMT == NX_FMT_Q8_0) {
-    return (j & ~255) | ((j & 48) << 2) | ((j >> 2) & 48) | (j & 15);
+    const int s = (j >> 6) & 3, q = (j >> 4) & 3;
+    return (j & ~255) | (q << 6) | ((s & 1) << 5) | ((s >> 1) << 4) | (j & 15);
   } else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) {
     const int s = (j >> 6) & 7, q = (j >> 4) & 3;
     const int p = s >> 2, t = s & 3;
@@ -116,7 +120,8 @@ __host__ __device__ __forceinline__ int kpos(int j) {
 template <int FMT>
 __host__ __device__ __forceinline__ int kslot(int e) {
   if constexpr (FMT == NX_FMT_Q8_0) {
-    return kpos<FMT>(e);
+    const int q = (e >> 6) & 3, s = ((e >> 5) & 1) | (((e >> 4) & 1) << 1);
+    return (e & ~255) | (s << 6) | (q << 4) | (e & 15);
   } else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) {
     const int a = (e >> 8) & 1, b = (e >> 4) & 1;
     const int p = FMT == NX_FMT_Q4_K ? (e >> 7) & 1 : (e >> 5) & 1;
@@ -154,10 +159,12 @@ struct GemmArgs {
   // outputs
   uint16_t *act;  // gate/up: [pairs][act_stride] operand type, operand order
   int act_stride;
-  float *y;       // down: [pairs][H]
+  float *y;       // down: [ksplit][pairs][H], one partial sum per K split
   int y_stride;
-  // grid decomposition (see k_gemm): N-tiles and the tile order
-  int n_tiles, xcd_split;
+  size_t y_split;  // floats between the K splits' partial sums
+  // grid decomposition (see k_gemm): N-tiles, the tile order, and (down)
+  // the K splits, each over wg_per_split workgroups
+  int n_tiles, xcd_split, ksplit, wg_per_split;
 };
 
 __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -167,42 +174,42 @@ __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 
 // ---- weights: one lane's codes of one step, and scales of one window ------
 //
-// A lane holds weight rows n0 + 32w + l%16 and that + 16 (index n = 0, 1).
-template <int FMT>
+// A lane holds weight rows n0 + 16 NT w + 16 n + l%16, n = 0 .. NT-1.
+template <int FMT, int NT>
 struct WCodes {
-  uint4 c[2];
+  uint4 c[NT];
 };
-template <>
-struct WCodes<NX_FMT_Q4_K> {
-  uint2 c[2];
+template <int NT>
+struct WCodes<NX_FMT_Q4_K, NT> {
+  uint2 c[NT];
 };
-template <>
-struct WCodes<NX_FMT_Q4_0> {
-  uint2 c[2];
+template <int NT>
+struct WCodes<NX_FMT_Q4_0, NT> {
+  uint2 c[NT];
 };
-template <>
-struct WCodes<NX_FMT_F32> {
-  uint4 c[2][4];
+template <int NT>
+struct WCodes<NX_FMT_F32, NT> {
+  uint4 c[NT][4];
 };
-template <int FMT>
+template <int FMT, int NT>
 struct WMeta {
-  uint4 m[2];
+  uint4 m[NT];
 };
-template <>
-struct WMeta<NX_FMT_Q8_0> {
-  uint32_t m[2];
+template <int NT>
+struct WMeta<NX_FMT_Q8_0, NT> {
+  uint32_t m[NT];
 };
-template <>
-struct WMeta<NX_FMT_F32> {};
+template <int NT>
+struct WMeta<NX_FMT_F32, NT> {};
 
-// code loads per matrix per step, scale loads per matrix per window
+// code loads per matrix row set per step, scale loads per row set per window
 template <int FMT>
 constexpr int n_code_loads() {
-  return FMT == NX_FMT_F32 ? 8 : 2;
+  return FMT == NX_FMT_F32 ? 4 : 1;
 }
 template <int FMT>
 constexpr int n_meta_loads() {
-  return FMT == NX_FMT_F32 ? 0 : 2;
+  return FMT == NX_FMT_F32 ? 0 : 1;
 }
 // steps per window
 template <int FMT>
@@ -241,21 +248,21 @@ __device__ __forceinline__ uint32_t code_win_off(int win, int p, int nseg) {
 }
 
 // codes of step S of window win
-template <int FMT, int S>
-__device__ __forceinline__ void fetch_codes(WCodes<FMT> &w, __amdgpu_buffer_rsrc_t rq,
-                                            const uint32_t (&lq)[2], int win, int nseg) {
+template <int FMT, int S, int NT>
+__device__ __forceinline__ void fetch_codes(WCodes<FMT, NT> &w, __amdgpu_buffer_rsrc_t rq,
+                                            const uint32_t (&lq)[NT], int win, int nseg) {
   if constexpr (FMT == NX_FMT_Q8_0) {
-    const uint32_t u = code_win_off(win, S & 1, nseg);
+    const uint32_t u = code_win_off(win, S >> 1, nseg);
 #pragma unroll
-    for (int n = 0; n < 2; ++n) w.c[n] = bload16(rq, lq[n] + u + 16u * (S >> 1));
+    for (int n = 0; n < NT; ++n) w.c[n] = bload16(rq, lq[n] + u + 16u * (S & 1));
   } else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) {
     const uint32_t u = code_win_off(win, S >> 2, nseg);
 #pragma unroll
-    for (int n = 0; n < 2; ++n) w.c[n] = bload8(rq, lq[n] + u + 16u * (S & 3));
+    for (int n = 0; n < NT; ++n) w.c[n] = bload8(rq, lq[n] + u + 16u * (S & 3));
   } else {  // F32: segments 8 win + 2q (+1), both halves: floats 64 win + 16q ..
     const uint32_t u0 = code_win_off(win, 0, nseg), u1 = code_win_off(win, 1, nseg);
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
+    for (int n = 0; n < NT; ++n)
 #pragma unroll
       for (int k = 0; k < 4; ++k) w.c[n][k] = bload16(rq, lq[n] + ((k & 1) ? u1 : u0) + 16u * (k >> 1));
   }
@@ -263,27 +270,26 @@ __device__ __forceinline__ void fetch_codes(WCodes<FMT> &w, __amdgpu_buffer_rsrc
 
 // scales of window win: Q8_0 blocks 8 win + 2q, +1 (one dword, rows padded
 // to whole dwords); Q4_K block 2 win + q/2; Q4_0 segments 8 win + 4(q/2) .. +3
-template <int FMT>
-__device__ __forceinline__ void fetch_meta(WMeta<FMT> &m, __amdgpu_buffer_rsrc_t rm,
-                                           const uint32_t (&lm)[2], int win) {
+template <int FMT, int NT>
+__device__ __forceinline__ void fetch_meta(WMeta<FMT, NT> &m, __amdgpu_buffer_rsrc_t rm,
+                                           const uint32_t (&lm)[NT], int win) {
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
+  for (int n = 0; n < NT; ++n) {
     if constexpr (FMT == NX_FMT_Q8_0) m.m[n] = bload4(rm, lm[n] + 16u * win);
     else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) m.m[n] = bload16(rm, lm[n] + 32u * win);
   }
 }
 
 // values 8M .. 8M+7 of the 16 of row n at step S of the window, as a B operand
-template <int FMT, bool BF16, int S, int M>
-__device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WCodes<FMT> &w,
-                                                           const WMeta<FMT> &mt, int n) {
+template <int FMT, bool BF16, int S, int M, typename WC, typename WM>
+__device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WC &w, const WM &mt, int n) {
   using Op = OpT<BF16>;
   if constexpr (FMT == NX_FMT_Q8_0 && !BF16) {
     // fp16 without a float detour: byte u = q ^ 0x80 becomes the f16 1024 + u
     // (exponent byte 0x64 above it), minus 1152 gives q exactly, and the f16
     // product with the f16 scale is q * d rounded once, as from the exact value
 #pragma clang fp contract(off)
-    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(mt.m[n] >> (16 * (S >> 1))));
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(mt.m[n] >> (16 * (S & 1))));
     const h2 dd = {d, d}, off = {(_Float16)1152.0f, (_Float16)1152.0f};
     const uint32_t ws[2] = {M ? w.c[n].z : w.c[n].x, M ? w.c[n].w : w.c[n].y};
     h2 r[4];
@@ -299,7 +305,7 @@ __device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WCodes<FMT> &w
   } else {
     float v[8];
     if constexpr (FMT == NX_FMT_Q8_0) {
-      const float d = h2f((mt.m[n] >> (16 * (S >> 1))) & 0xFFFFu);
+      const float d = h2f((mt.m[n] >> (16 * (S & 1))) & 0xFFFFu);
       const uint32_t ws[2] = {M ? w.c[n].z : w.c[n].x, M ? w.c[n].w : w.c[n].y};
 #pragma unroll
       for (int k = 0; k < 2; ++k)
@@ -390,19 +396,92 @@ __device__ __forceinline__ void static_for(F &&f) {
   }
 }
 
-// F32 weights keep 2 x 64 floats of codes per step per lane: one workgroup per CU
+// Kernel shape per format and pass.  NT = 16-row weight sets per wave
+// (the tile has 64 NT weight rows), PAIR = code loads of steps 2k and 2k+1
+// issued back to back (both halves of the same lines, the second load hits
+// the cache), OCC = workgroups per CU.  Gate/up waves own 64 rows (their 256
+// accumulators fill the AGPRs, one workgroup per CU), so each activation
+// stage meets twice the weights; the down pass keeps 32 rows per wave and
+// two workgroups per CU; F32 codes take 4 loads per row per step and are not
+// paired.
+template <int FMT, bool GATEUP>
+struct GemmShape {
+  static constexpr int NT = 2;
+  static constexpr bool PAIR = false;
+  static constexpr int WDIST = WDIST_CFG;  // steps the codes are fetched ahead
+  static constexpr int OCC = (NT == 4 || FMT == NX_FMT_F32) ? 1 : 2;
+};
+int gemm_bn(int fmt, bool gateup) {
+  (void)fmt;
+  (void)gateup;
+  return 128;
+}
+
+// Load schedule of the K loop (body positions; it repeats every body).
+// Step t issues, in this order: at its start the activation stage
+// t + RING - 1; after its last decode, for single-buffered scales the
+// scales of a window starting at t+1, then the codes of the steps it
+// prefetches (t+2 and t+3 at even t when paired, else t+2), each window's
+// first step preceded by that window's double-buffered scales.  The wait at
+// step P lets through the loads issued after the last one P needs (its
+// activation stage, its codes, its window's scales).
+struct LoadSchedule {
+  int ring, ws, na, ncw, nmw, wdist;
+  bool pair, meta2;
+  static constexpr int mod(int x, int m) { return ((x % m) + m) % m; }
+  constexpr int outstanding(int P) const {
+    const int wstart = P - mod(P, ws);
+    int after = 0;
+    for (int t = P - 32; t < P; ++t) {
+      after += na;
+      if (t + ring - 1 == P) after = 0;
+      if (!meta2 && nmw > 0 && mod(t + 1, ws) == 0) {
+        after += nmw;
+        if (t + 1 == wstart) after = 0;
+      }
+      const int nj = pair ? (mod(t, 2) == 0 ? 2 : 0) : 1;
+      for (int k = 0; k < nj; ++k) {
+        const int j = t + (pair ? 2 : wdist) + k;
+        if (meta2 && nmw > 0 && mod(j, ws) == 0) {
+          after += nmw;
+          if (j == wstart) after = 0;
+        }
+        after += ncw;
+        if (j == P) after = 0;
+      }
+    }
+    return after;
+  }
+};
+
 template <int FMT, bool BF16, bool GATEUP>
-__global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const GemmArgs g) {
+__global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(const GemmArgs g) {
   using Op = OpT<BF16>;
   using V8 = typename Op::V8;
+  using Shape = GemmShape<FMT, GATEUP>;
+  constexpr int NT = Shape::NT;
+  constexpr bool PAIR = Shape::PAIR;
+  constexpr int BN = 64 * NT;
   constexpr int NMAT = GATEUP ? 2 : 1;
   constexpr int WS = win_steps<FMT>();
-  // steps per loop body: two scale windows (static double buffering of the
-  // scales), and whole rounds of the ring and of the two code buffers
-  constexpr int NB = WS >= 2 ? 2 * WS : RING;
-  static_assert(NB % RING == 0, "loop body must cover whole ring rounds");
+  // Scales: Q8_0 (one dword per row) double-buffers them, loaded just before
+  // the codes of a window's first step; the 16-byte scales of the 4-bit
+  // formats have one buffer, reloaded right after the last decode of a
+  // window.
+  constexpr bool META2 = FMT == NX_FMT_Q8_0;
+  constexpr int NMB = META2 ? 2 : 1;
+  constexpr int WDIST = Shape::WDIST;
+  constexpr int NBUF = (PAIR || WDIST > 2) ? 4 : 2;  // code buffers (steps mod NBUF)
+  static_assert(PAIR || WDIST <= NBUF, "code buffers");  // issued after the decode
+  // steps per loop body: whole rounds of the ring, of the code buffers and
+  // of the scale buffers
+  constexpr int NB0 = RING > NBUF ? RING : NBUF, NB1 = META2 ? 2 * WS : WS;
+  constexpr int NB = NB0 > NB1 ? NB0 : NB1;
+  static_assert(NB % RING == 0 && NB % NBUF == 0 && NB % (NMB * WS) == 0, "loop body");
   constexpr int NA = 4;
   constexpr int IG = GATEUP ? 2 : 4;  // M-tiles per scheduling group
+  constexpr LoadSchedule sched{RING, WS, NA, NMAT * NT * n_code_loads<FMT>(),
+                               NMAT * NT * n_meta_loads<FMT>(), WDIST, PAIR, META2};
   __shared__ __attribute__((aligned(16))) uint4 ring0[BM * 8];
   __shared__ __attribute__((aligned(16))) uint4 ring1[BM * 8];
   __shared__ __attribute__((aligned(16))) uint4 ring2[BM * 8];
@@ -419,8 +498,11 @@ __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const G
   // whose activation tiles span K = the expert width and are the larger
   // operand): N-tiles fastest, so the N-tiles of one activation tile run
   // together.
-  constexpr int XCD_WGS = 64;  // 32 CUs x 2 workgroups
-  const int L = blockIdx.x;
+  constexpr int XCD_WGS = 32 * Shape::OCC;  // 32 CUs x OCC workgroups
+  int L = blockIdx.x;
+  // down: K split `split` of ksplit (whole loop bodies each)
+  const int split = g.ksplit > 1 ? L / g.wg_per_split : 0;
+  L -= split * g.wg_per_split;
   const int mcount = g.tiles[0];
   if (mcount <= 0) return;
   int tile, ntile;
@@ -491,143 +573,192 @@ __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const G
     const int chunk = (lane & 7) ^ ((r >> 1) & 7);
     abase[i] = r < mrows ? (uint32_t)arow[i] * (uint32_t)g.a_stride * 2u + 16u * chunk : OOB;
   }
-  // steps holding data (the padded width), and the steps run: whole loop
-  // bodies (the steps past the padded width load zeros and add nothing)
+  // steps holding data (the padded width), and this workgroup's steps:
+  // its split's share of the whole loop bodies (the steps past the padded
+  // width load zeros and add nothing)
   const int nk_data = kpad_steps<FMT>(cols);
-  const int nks = (nk_data + NB - 1) / NB * NB;
+  const int nbody = (nk_data + NB - 1) / NB;
+  const int ks_begin = split * nbody / g.ksplit * NB;
+  const int ks_end = (split + 1) * nbody / g.ksplit * NB;
 
-  // ---- weights: rows n0 + 32 * wave + 16 n + lane % 16, quarter lane / 16
+  // ---- weights: rows n0 + 16 NT wave + 16 n + lane % 16, quarter lane / 16
   const int l16 = lane & 15, q = lane >> 4;
-  uint32_t lq[2], lm[2];
+  uint32_t lq[NT], lm[NT];
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
-    const uint32_t wrow = (uint32_t)(n0 + 32 * wave + 16 * n + l16);
+  for (int n = 0; n < NT; ++n) {
+    const uint32_t wrow = (uint32_t)(n0 + 16 * NT * wave + 16 * n + l16);
     lq[n] = code_lane_off<FMT>(wrow * rq, q);
     lm[n] = meta_lane_off<FMT>(wrow * rm, q);
   }
 
-  auto issue_a = [&](auto stage, int ks) {
+  // activation loads I0 .. I1-1 of stage ks
+  auto issue_a_part = [&](auto stage, int ks, auto i0, auto i1) {
     constexpr int S = decltype(stage)::value;
     uint4 *dst = ring_stage<S>(ring0, ring1, ring2, ring3);
     // wave-uniform step offset; past the padded width it pushes every lane
     // out of range (bases stay below 2^31, so the sum does not wrap)
     const uint32_t koff = ks < nk_data ? (uint32_t)ks * (2u * BK) : OOB;
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
+    for (int i = decltype(i0)::value; i < decltype(i1)::value; ++i) {
       const uint32_t off = abase[i] + koff;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(dst + (4 * wave + i) * 64), 16, off,
                                                0, 0, 0);
     }
   };
-  // Scales: Q8_0 (one dword per row) double-buffers them, loaded with the
-  // codes of a window's first step; the 16-byte scales of the 4-bit formats
-  // have one buffer, reloaded right after the last decode of a window.
-  constexpr bool META2 = FMT == NX_FMT_Q8_0;
-  constexpr int NMB = META2 ? 2 : 1;
-  WCodes<FMT> wbuf[2][NMAT];
-  WMeta<FMT> mbuf[NMB][NMAT];
-  // loads of the weights of step P of a loop body (P may reach into the next
-  // body) whose first window is wbase
+  auto issue_a = [&](auto stage, int ks) { issue_a_part(stage, ks, IC<0>{}, IC<NA>{}); };
+  WCodes<FMT, NT> wbuf[NBUF][NMAT];
+  WMeta<FMT, NT> mbuf[NMB][NMAT];
+  // codes (and double-buffered scales) of step J of a loop body (J may reach
+  // into the next body) whose first window is wbase
   auto issue_w = [&](auto pos, int wbase) {
-    constexpr int P = decltype(pos)::value;
-    constexpr int S = P % WS;
-    const int win = wbase + P / WS;
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt)
-      fetch_codes<FMT, S>(wbuf[P % 2][mt], mt == 0 ? rq0 : rq1, lq, win, nseg);
+    constexpr int J = decltype(pos)::value;
+    constexpr int S = J % WS;
+    const int win = wbase + J / WS;
     if constexpr (META2 && S == 0) {
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
-        fetch_meta<FMT>(mbuf[(P / WS) % NMB][mt], mt == 0 ? rm0 : rm1, lm, win);
+        fetch_meta<FMT, NT>(mbuf[(J / WS) % NMB][mt], mt == 0 ? rm0 : rm1, lm, win);
     }
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+      fetch_codes<FMT, S, NT>(wbuf[J % NBUF][mt], mt == 0 ? rq0 : rq1, lq, win, nseg);
   };
-  // single-buffered scales of the window that starts at step P
+  // single-buffered scales of the window that starts at step J
   auto issue_meta1 = [&](auto pos, int wbase) {
-    constexpr int P = decltype(pos)::value;
+    constexpr int J = decltype(pos)::value;
     if constexpr (!META2 && n_meta_loads<FMT>() > 0) {
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
-        fetch_meta<FMT>(mbuf[0][mt], mt == 0 ? rm0 : rm1, lm, wbase + P / WS);
+        fetch_meta<FMT, NT>(mbuf[0][mt], mt == 0 ? rm0 : rm1, lm, wbase + J / WS);
+    }
+  };
+  // the late issues of step T (see LoadSchedule)
+  auto issue_late = [&](auto pos, int wbase) {
+    constexpr int T = decltype(pos)::value;
+    if constexpr ((T + 1) % WS == 0) issue_meta1(IC<T + 1>{}, wbase);
+    if constexpr (PAIR) {
+      if constexpr (T % 2 == 0) {
+        issue_w(IC<T + 2>{}, wbase);
+        issue_w(IC<T + 3>{}, wbase);
+      }
+    } else {
+      issue_w(IC<T + WDIST>{}, wbase);
     }
   };
 
   // ---- accumulators: acc[mt][n][i] = pairs 16i .. 16i+15 x rows 16n .. of this wave
-  f32x4 acc[NMAT][2][8];
+  f32x4 acc[NMAT][NT][8];
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
+    for (int n = 0; n < NT; ++n)
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[mt][n][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Software pipeline.  Step ks: wait until this wave's loads of activation
-  // stage ks and weights ks have landed, barrier (every wave's share of the
-  // stage is in LDS, and every wave is done reading stage ks-1's slot), issue
-  // activation stage ks+3 into that slot, decode weights ks into B operands
-  // and run the step's MFMAs, half by half, issuing weights ks+2 (and, for
-  // single-buffered scales at a window's last step, the next window's
-  // scales before them) after the last decode.  Every step issues its loads
-  // unconditionally (a conditional load would make the compiler copy its
-  // registers, waiting for all loads in flight).  So after W(ks) (issued in
-  // step ks-2) come A(ks+2), the scales of a window starting at ks+1, and
-  // W(ks+1); a window starting at ks has its scales issued after A(ks+2).
+  // stage ks, codes ks and its window's scales have landed (the loads issued
+  // after them may stay in flight), barrier (every wave's share of the stage
+  // is in LDS, and every wave is done reading stage ks-1's slot), issue
+  // activation stage ks+3 into that slot, decode the codes into B operands
+  // and run the step's MFMAs, half by half, with the step's late loads
+  // after the last decode.  Every step issues its loads unconditionally (a
+  // conditional load would make the compiler copy its registers, waiting for
+  // all loads in flight).
   const int sw = (l16 >> 1) & 7;
-  constexpr int NCW = NMAT * n_code_loads<FMT>();
-  constexpr int NMW = NMAT * n_meta_loads<FMT>();
   auto step = [&](auto pos, int ks0, int wbase) {
     constexpr int P = decltype(pos)::value;
     constexpr int S = P % WS;
-    constexpr bool wstart = P % WS == 0, wnext = (P + 1) % WS == 0;
-    constexpr int NOUT = META2 ? NA + NCW + (wnext ? NMW : 0)
-                               : (wstart ? NCW : NA + NCW + (wnext ? NMW : 0));
-    wait_vm<NOUT>();
+    wait_vm<sched.outstanding(P)>();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue_a(IC<(P + 3) % RING>{}, ks0 + P + 3);
     const uint4 *src = ring_stage<P % RING>(ring0, ring1, ring2, ring3);
     // two halves of 32 K positions: B operands of the half, then its MFMAs
-    // (a scheduling fence between the halves bounds the live operands).  The
-    // code buffer of this step takes step P+2's loads once both halves are
-    // decoded.
-    static_for<0, 2>([&](auto half) {
-      constexpr int M = decltype(half)::value;
-      V8 bf[NMAT][2];
+    // in groups of IG M-tiles (scheduling fences between the groups bound
+    // the live operands).  The step's loads go between MFMA groups, so that
+    // a wave held up issuing a load (memory pipeline full) still has MFMAs
+    // queued: the activation loads after the first-half groups, the late
+    // loads after the first second-half group.
+    constexpr int NG = 8 / IG;          // groups per half
+    constexpr int APG = (NA + NG - 1) / NG;  // activation loads per group
+    // A operands are read one group ahead (across the halves too), so each
+    // group's MFMAs cover the LDS latency of the next group's reads
+    auto read_a = [&](auto grp, V8 (&af)[IG]) {
+      constexpr int G2 = decltype(grp)::value, M = G2 / NG, G = G2 % NG;
 #pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-        for (int n = 0; n < 2; ++n) {
-          bf[mt][n] = w_operand<FMT, BF16, S, M>(wbuf[P % 2][mt], mbuf[(P / WS) % NMB][mt], n);
-          // float decodes: one operand's temporaries at a time
-          if constexpr (!(FMT == NX_FMT_Q8_0 && !BF16)) __builtin_amdgcn_sched_barrier(0);
-        }
-      if constexpr (M == 1) {
-        if constexpr (wnext) issue_meta1(IC<P + 1>{}, wbase);
-        issue_w(IC<P + 2>{}, wbase);
+      for (int k = 0; k < IG; ++k) {
+        const int i = IG * G + k;
+        af[k] = __builtin_bit_cast(V8, src[(16 * i + l16) * 8 + ((2 * q + M) ^ sw)]);
       }
-      // M-tiles in groups (bounds the A operands read ahead)
+    };
+    V8 bf[NMAT][NT];
+    V8 an[IG];
+    read_a(IC<0>{}, an);
+    static_for<0, 2 * NG>([&](auto grp) {
+      constexpr int G2 = decltype(grp)::value, M = G2 / NG, G = G2 % NG;
+      if constexpr (G == 0) {
+        // B operands of the half
 #pragma unroll
-      for (int ig = 0; ig < 8 / IG; ++ig) {
+        for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-        for (int i = IG * ig; i < IG * ig + IG; ++i) {
-          const V8 af = __builtin_bit_cast(V8, src[(16 * i + l16) * 8 + ((2 * q + M) ^ sw)]);
-#pragma unroll
-          for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-            for (int n = 0; n < 2; ++n) acc[mt][n][i] = Op::mfma(af, bf[mt][n], acc[mt][n][i]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
+          for (int n = 0; n < NT; ++n) {
+            bf[mt][n] = w_operand<FMT, BF16, S, M>(wbuf[P % NBUF][mt], mbuf[(P / WS) % NMB][mt], n);
+            // float decodes: one operand's temporaries at a time
+            if constexpr (!(FMT == NX_FMT_Q8_0 && !BF16)) __builtin_amdgcn_sched_barrier(0);
+          }
       }
+      V8 af[IG];
+#pragma unroll
+      for (int k = 0; k < IG; ++k) af[k] = an[k];
+      if constexpr (G2 + 1 < 2 * NG) read_a(IC<G2 + 1>{}, an);
+#pragma unroll
+      for (int k = 0; k < IG; ++k) {
+        const int i = IG * G + k;
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+          for (int n = 0; n < NT; ++n) acc[mt][n][i] = Op::mfma(af[k], bf[mt][n], acc[mt][n][i]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      constexpr int a0 = G * APG < NA ? G * APG : NA;
+      constexpr int a1 = (G + 1) * APG < NA ? (G + 1) * APG : NA;
+      if constexpr (M == 0 && a0 < a1)
+        issue_a_part(IC<(P + RING - 1) % RING>{}, ks0 + P + RING - 1, IC<a0>{}, IC<a1>{});
+      if constexpr (M == 1 && G == 0) issue_late(IC<P>{}, wbase);
+      __builtin_amdgcn_sched_barrier(0);
     });
   };
 
-  issue_a(IC<0>{}, 0);
-  issue_a(IC<1>{}, 1);
-  issue_meta1(IC<0>{}, 0);
-  issue_w(IC<0>{}, 0);
-  issue_a(IC<2>{}, 2);
-  issue_w(IC<1>{}, 0);
-  for (int ks0 = 0, wbase = 0; ks0 < nks; ks0 += NB, wbase += NB / WS)
+  // prologue: the loads of steps -RING+1 .. -1 of the schedule (targets
+  // >= 0), in schedule order
+  static_assert(RING == 4, "prologue written for a 4-stage ring");
+  // (ks_begin is a whole number of bodies: ring stages and code buffers
+  // keep their step-relative indices, wb0 is its window)
+  const int wb0 = ks_begin / WS;
+  if constexpr (PAIR) {
+    issue_a(IC<0>{}, ks_begin);
+    issue_a(IC<1>{}, ks_begin + 1);
+    issue_w(IC<0>{}, wb0);
+    issue_w(IC<1>{}, wb0);
+    issue_a(IC<2>{}, ks_begin + 2);
+    issue_meta1(IC<0>{}, wb0);
+  } else if constexpr (WDIST == 3) {
+    issue_a(IC<0>{}, ks_begin);
+    issue_w(IC<0>{}, wb0);
+    issue_a(IC<1>{}, ks_begin + 1);
+    issue_w(IC<1>{}, wb0);
+    issue_a(IC<2>{}, ks_begin + 2);
+    issue_meta1(IC<0>{}, wb0);
+    issue_w(IC<2>{}, wb0);
+  } else {
+    issue_a(IC<0>{}, ks_begin);
+    issue_a(IC<1>{}, ks_begin + 1);
+    issue_w(IC<0>{}, wb0);
+    issue_a(IC<2>{}, ks_begin + 2);
+    issue_meta1(IC<0>{}, wb0);
+    issue_w(IC<1>{}, wb0);
+  }
+  for (int ks0 = ks_begin, wbase = wb0; ks0 < ks_end; ks0 += NB, wbase += NB / WS)
     static_for<0, NB>([&](auto pos) { step(pos, ks0, wbase); });
   // no direct-to-LDS write may land after the workgroup has ended
   wait_vm<0>();
@@ -635,8 +766,8 @@ __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const G
   // ---- epilogue.  16x16 accumulator layout: lane holds column (lane % 16),
   // register j holds row 4 * (lane / 16) + j.
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
-    const int col = n0 + 32 * wave + 16 * n + l16;
+  for (int n = 0; n < NT; ++n) {
+    const int col = n0 + 16 * NT * wave + 16 * n + l16;
     if (col >= rows) continue;
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -649,7 +780,7 @@ __global__ __launch_bounds__(256, FMT == NX_FMT_F32 ? 1 : 2) void k_gemm(const G
             const float v = silu_mul(acc[0][n][i][j], acc[1][n][i][j]);
             g.act[p * g.act_stride + kslot<FMT>(col)] = Op::bits(v);
           } else {
-            g.y[p * g.y_stride + col] = acc[0][n][i][j];
+            g.y[split * g.y_split + p * g.y_stride + col] = acc[0][n][i][j];
           }
         }
       }
@@ -758,19 +889,22 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
     a.perm_token = nullptr;
     a.y = p.ypair;
     a.y_stride = ex->H;
+    a.y_split = p.pairs_total * (size_t)ex->H;
   }
   const int rows = a.rows > a.srows ? a.rows : a.srows;
+  const int BN = gemm_bn(ex->fmt, gateup);
   a.n_tiles = (rows + BN - 1) / BN;
   a.xcd_split = gateup ? 1 : 0;
   // enough workgroups for either order at the largest M-tile count
-  const long wgs = a.xcd_split ? 8L * ((a.n_tiles + 7) / 8) * p.max_tiles
+  const long per = a.xcd_split ? 8L * ((a.n_tiles + 7) / 8) * p.max_tiles
                                : (long)a.n_tiles * p.max_tiles;
+  a.ksplit = gateup ? 1 : p.ksplit;
+  a.wg_per_split = (int)per;
+  const long wgs = per * a.ksplit;
   if (wgs > 0x7FFFFFFFL) return fail(NX_ERR_UNSUPPORTED, "grouped GEMM grid too large");
   GemmFn fn = pick(ex->fmt, p.bf16, gateup);
   if (!fn) return fail(NX_ERR_UNSUPPORTED, "no grouped-GEMM kernel for this format");
   const char *name = gateup ? "gemm_gateup" : "gemm_down";
-  // (the 64 KB activation ring keeps at most two workgroups per CU, which
-  // also bounds the L2 footprint of the down projection's long K)
   return launch(c, name,
                 [&] { hipLaunchKernelGGL(fn, dim3((unsigned)wgs), dim3(256), 0, c->stream, a); });
 }
@@ -790,6 +924,29 @@ int to_half_fmt(nx_ctx *c, const float *x, int T, int H, int kpad, bool bf16, ui
 }  // namespace
 
 int gemm_tile_m() { return BM; }
+
+// K splits of the down pass: the count (1-4, each split at least four loop
+// bodies) that best fills whole rounds of `slots` concurrent workgroups,
+// with `tiles` M-tiles expected.
+int gemm_down_ksplit(int fmt, int F, int H, int tiles, int slots) {
+  const int steps = kpad_of(fmt, F) / BK;
+  const int body = fmt == NX_FMT_F32 ? 4 : (fmt == NX_FMT_Q8_0 ? 8 : 16);
+  const int nbody = (steps + body - 1) / body;
+  const long wgs = (long)tiles * ((H + 127) / 128);
+  int best = 1;
+  double best_eff = 0;
+  for (int ks = 1; ks <= 4; ++ks) {
+    if (ks > 1 && nbody / ks < 4) break;
+    const long w = wgs * ks;
+    const long rounds = (w + slots - 1) / slots;
+    const double eff = (double)w / (double)(rounds * slots);
+    if (eff > best_eff + 0.02) {
+      best = ks;
+      best_eff = eff;
+    }
+  }
+  return best;
+}
 
 int gemm_kpad(int fmt, int cols) { return kpad_of(fmt, cols); }
 

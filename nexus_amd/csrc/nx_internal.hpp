@@ -162,8 +162,11 @@ int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, 
                          int32_t *d_expert, float *d_weight, int32_t *d_count, int32_t *d_ecount,
                          int32_t *d_offsets, int32_t *d_ptok, int32_t *d_pslot, int32_t *d_inv,
                          int32_t *d_active, int *d_counters, int n_counters);
+// out[t] = sum_r w[t,r] * y[pair(t,r)] (+ y[shared row t]); y is the sum of
+// nsplit partial buffers split_stride floats apart
 int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
-                   const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out);
+                   const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out,
+                   int nsplit = 1, size_t split_stride = 0);
 
 struct GemvPlan {
   const nx_experts *ex;
@@ -200,8 +203,10 @@ struct GemmPlan {
   void *xh;              // [T][x_stride] half precision copy of x, operand order
   int x_stride;
   size_t pairs_total;    // rows of act / ypair
+  int ksplit;            // down pass K splits (ypair holds ksplit partial sums)
 };
 int gemm_tile_m();
+int gemm_down_ksplit(int fmt, int F, int H, int tiles, int slots);
 // width of a row of GEMM operands (operand order pads to whole scale windows)
 int gemm_kpad(int fmt, int cols);
 int launch_to_half(nx_ctx *c, int fmt, const float *x, int T, int H, int kpad, bool bf16, void *out);

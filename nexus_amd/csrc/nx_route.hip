@@ -315,11 +315,23 @@ __global__ __launch_bounds__(256) void k_route_permute(
   }
 }
 
+// y value of row p, column h: the sum of the NS partial buffers (K splits)
+template <int NS>
+__device__ __forceinline__ float y_at(const float *__restrict__ y, size_t stride, int ns, size_t o) {
+  float v = y[o];
+  if constexpr (NS != 1) {
+    for (int s = 1; s < ns; ++s) v += y[s * stride + o];
+  }
+  return v;
+}
+
+template <int NS>
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair,
                                                  const float *__restrict__ rw,
                                                  const int32_t *__restrict__ rcnt,
                                                  const int32_t *__restrict__ inv, int T, int k,
-                                                 int H, int shared, float *__restrict__ out) {
+                                                 int H, int shared, float *__restrict__ out,
+                                                 int ns, size_t stride) {
   const size_t total = (size_t)T * H;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
@@ -328,9 +340,9 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair
     float acc = 0.0f;
     for (int r = 0; r < n; ++r) {
       const int p = inv[(size_t)t * k + r];
-      acc = acc + __fmul_rn(rw[(size_t)t * k + r], ypair[(size_t)p * H + h]);
+      acc = acc + __fmul_rn(rw[(size_t)t * k + r], y_at<NS>(ypair, stride, ns, (size_t)p * H + h));
     }
-    if (shared) acc = acc + ypair[((size_t)T * k + t) * H + h];
+    if (shared) acc = acc + y_at<NS>(ypair, stride, ns, ((size_t)T * k + t) * H + h);
     out[i] = acc;
   }
 }
@@ -397,14 +409,20 @@ int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, 
 }
 
 int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
-                   const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out) {
+                   const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out,
+                   int nsplit, size_t split_stride) {
   const size_t total = (size_t)T * H;
   if (total == 0) return NX_OK;
   size_t g = (total + 255) / 256;
   if (g > 65536) g = 65536;
+  if (nsplit <= 1)
+    return launch(c, "combine", [&] {
+      k_combine<1><<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H,
+                                                       shared ? 1 : 0, d_out, 1, 0);
+    });
   return launch(c, "combine", [&] {
-    k_combine<<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H,
-                                                  shared ? 1 : 0, d_out);
+    k_combine<0><<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H,
+                                                     shared ? 1 : 0, d_out, nsplit, split_stride);
   });
 }
 
