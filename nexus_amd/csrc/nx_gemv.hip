@@ -97,7 +97,39 @@ __device__ __forceinline__ SlotView slot_view(const GemvArgs &a, int slot, int n
     v.rm = a.srow_meta;
     v.routed = false;
   }
+  // every field is wave-uniform (the slot is); say so, or buffer resources
+  // built from them become per-lane values and loads waterfall loops
+  auto ufirst = [](auto x) { return __builtin_amdgcn_readfirstlane(x); };
+  auto uptr = [](const uint8_t *p) {
+    const uint64_t w = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)w);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(w >> 32));
+    return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
+  };
+  v.pair0 = ufirst(v.pair0);
+  v.count = ufirst(v.count);
+  v.rows = ufirst(v.rows);
+  v.cols = ufirst(v.cols);
+  v.nseg = ufirst(v.nseg);
+  v.q0 = uptr(v.q0);
+  v.q1 = uptr(v.q1);
+  v.m0 = uptr(v.m0);
+  v.m1 = uptr(v.m1);
+  v.rq = ufirst(v.rq);
+  v.rm = ufirst(v.rm);
   return v;
+}
+
+// Buffer resource for a wave-uniform base and size: both read back through
+// readfirstlane, so the resource stays in scalar registers even where the
+// compiler lost track of their uniformity (a per-lane resource would turn
+// every load into a waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_u(const void *base, uint32_t bytes) {
+  const uint64_t w = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)w);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(w >> 32));
+  return make_rsrc(reinterpret_cast<const void *>(((uint64_t)hi << 32) | lo),
+                   __builtin_amdgcn_readfirstlane(bytes));
 }
 
 // Register-resident pieces of one row group's work: its segments of a row,
@@ -142,15 +174,19 @@ struct RowGroup {
       moff[m] = S::meta_off(j, jv);
     }
     if constexpr (L >= 64) {
+      // the row is wave-uniform: say so, or the resources below become
+      // per-lane values and every load a waterfall loop
+      const int r0u = __builtin_amdgcn_readfirstlane(r0);
+      const int row_end_u = __builtin_amdgcn_readfirstlane(row_end);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int r = r0 + u;
-        const bool rv = r < row_end;
+        const int r = r0u + u;
+        const bool rv = r < row_end_u;
         const uint32_t nq = rv ? v.rq : 0u, nm = rv ? v.rm : 0u;
-        const __amdgpu_buffer_rsrc_t rq0 = make_rsrc(v.q0 + (size_t)r * v.rq, nq);
-        const __amdgpu_buffer_rsrc_t rq1 = make_rsrc(v.q1 + (size_t)r * v.rq, nq);
-        const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(v.m0 + (size_t)r * v.rm, nm);
-        const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(v.m1 + (size_t)r * v.rm, nm);
+        const __amdgpu_buffer_rsrc_t rq0 = make_rsrc_u(v.q0 + (size_t)r * v.rq, nq);
+        const __amdgpu_buffer_rsrc_t rq1 = make_rsrc_u(v.q1 + (size_t)r * v.rq, nq);
+        const __amdgpu_buffer_rsrc_t rm0 = make_rsrc_u(v.m0 + (size_t)r * v.rm, nm);
+        const __amdgpu_buffer_rsrc_t rm1 = make_rsrc_u(v.m1 + (size_t)r * v.rm, nm);
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt) {
 #pragma unroll
@@ -162,10 +198,10 @@ struct RowGroup {
         }
       }
     } else {
-      const __amdgpu_buffer_rsrc_t rq0 = make_rsrc(v.q0, (uint32_t)v.rows * v.rq);
-      const __amdgpu_buffer_rsrc_t rq1 = make_rsrc(v.q1, (uint32_t)v.rows * v.rq);
-      const __amdgpu_buffer_rsrc_t rm0 = make_rsrc(v.m0, (uint32_t)v.rows * v.rm);
-      const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(v.m1, (uint32_t)v.rows * v.rm);
+      const __amdgpu_buffer_rsrc_t rq0 = make_rsrc_u(v.q0, (uint32_t)v.rows * v.rq);
+      const __amdgpu_buffer_rsrc_t rq1 = make_rsrc_u(v.q1, (uint32_t)v.rows * v.rq);
+      const __amdgpu_buffer_rsrc_t rm0 = make_rsrc_u(v.m0, (uint32_t)v.rows * v.rm);
+      const __amdgpu_buffer_rsrc_t rm1 = make_rsrc_u(v.m1, (uint32_t)v.rows * v.rm);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const bool rv = r0 + u < row_end;
@@ -191,12 +227,14 @@ struct RowGroup {
   template <class RowOf>
   __device__ __forceinline__ void load_x(const float *xbase, int xstride, const SlotView &v, int t0,
                                          RowOf row_of) {
+    // the token group is wave-uniform (see slot_view)
+    const int t0u = __builtin_amdgcn_readfirstlane(t0);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const bool tv = t0 + t < v.count;
+      const bool tv = t0u + t < v.count;
       const float *xrow = xbase;
-      if (tv) xrow = xbase + (size_t)row_of(t0 + t) * xstride;
-      const __amdgpu_buffer_rsrc_t xr = make_rsrc(xrow, tv ? (uint32_t)v.cols * 4u : 0u);
+      if (tv) xrow = xbase + (size_t)__builtin_amdgcn_readfirstlane(row_of(t0u + t)) * xstride;
+      const __amdgpu_buffer_rsrc_t xr = make_rsrc_u(xrow, tv ? (uint32_t)v.cols * 4u : 0u);
 #pragma unroll
       for (int m = 0; m < SPL; ++m) {
         const int j = li + m * L;
@@ -242,7 +280,7 @@ struct RowGroup {
       const bool tv = t0 + t < v.count;
       const float *xrow = xbase;
       if (tv) xrow = xbase + (size_t)row_of(t0 + t) * xstride;
-      const __amdgpu_buffer_rsrc_t xr = make_rsrc(xrow, tv ? (uint32_t)v.cols * 4u : 0u);
+      const __amdgpu_buffer_rsrc_t xr = make_rsrc_u(xrow, tv ? (uint32_t)v.cols * 4u : 0u);
 #pragma unroll
       for (int e = 0; e < XQ; e += 4) {
         const uint4 f = bload16(xr, jv ? (uint32_t)S::xidx(sgm, q * XQ + e) * 4u : OOB);
