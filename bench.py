@@ -9,6 +9,11 @@ W_r ~N(0, 0.02).  Several replicas of the expert set (more than twice the
 ~256 MB Infinity Cache in the bytes a step touches) are rotated step by step
 so the weight bytes come from HBM.
 
+Extras in the same line (skipped with --no-extra): Mixtral decode at 32
+tokens, Mixtral Q8_0 prefill at 2048 tokens (MFMA grouped GEMM), and the
+Qwen3 (E=128, k=8) and DeepSeek (E=256, k=8, sigmoid, shared expert) shapes
+at their decode and batch token counts.
+
 Prints one JSON line (rank 0, N=1).  `value` = tokens/s of the whole layer.
 `roofline` is for the dominant kernel (the gate/up GEMV): algorithmic bytes
 = quantized weight bytes of the experts the step activates, divided by the
@@ -55,15 +60,17 @@ def parse():
     return p.parse_args()
 
 
-def make_expert_sets(nx, ctx, torch, fmt, E, H, F, replicas, seed):
-    """Quantized expert sets generated on the device (N(0, 0.02) -> fmt)."""
+def make_expert_sets(nx, ctx, torch, fmt, E, H, F, replicas, seed, Fs=0):
+    """Quantized expert sets generated on the device (N(0, 0.02) -> fmt); Fs > 0
+    adds a shared expert of width Fs."""
     dev = torch.device("cuda", 0)
     sets = []
     qbuf = None
     for rep in range(replicas):
-        ex = nx.Experts(ctx, fmt, E, H, F)
-        for e in range(E):
-            for role, (r, c) in ((nx.ROLE_GATE, (F, H)), (nx.ROLE_UP, (F, H)), (nx.ROLE_DOWN, (H, F))):
+        ex = nx.Experts(ctx, fmt, E, H, F, shared_ff_dim=Fs)
+        members = [(e, F) for e in range(E)] + ([(nx.EXPERT_SHARED, Fs)] if Fs else [])
+        for e, f in members:
+            for role, (r, c) in ((nx.ROLE_GATE, (f, H)), (nx.ROLE_UP, (f, H)), (nx.ROLE_DOWN, (H, f))):
                 g = torch.Generator(device=dev)
                 g.manual_seed(seed * 1000003 + rep * 10007 + e * 101 + role)
                 w = torch.randn((r, c), generator=g, device=dev, dtype=torch.float32) * 0.02
@@ -140,8 +147,8 @@ def kernel_means(ctx, torch, fn, steps):
     return {name: ms / max(n, 1) for name, (n, ms) in stats.items()}
 
 
-def active_experts(ctx, logits_np, T, E, k):
-    ex_ids, _, cnt, _ = ctx.route_topk(logits_np, T, E, k)
+def active_experts(ctx, logits_np, T, E, k, score=0):
+    ex_ids, _, cnt, _ = ctx.route_topk(logits_np, T, E, k, score_mode=score)
     counts = [0] * E
     for t in range(T):
         for e in ex_ids[t, :cnt[t]]:
@@ -183,6 +190,63 @@ def prefill(nx, ctx, torch, args):
         "gemm_frac_of_fp16_peak": flops / (gemm_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS if gemm_ms else None,
         "kernels_ms": {k_: round(v, 4) for k_, v in kern.items()},
     }
+
+
+MODEL_CONFIGS = [
+    # name, E, H, F, k, shared F, score mode, token counts, replicas rotated
+    ("qwen3_q4k", 128, 2048, 768, 8, 0, 0, (1, 64, 512), 2),
+    ("deepseek_q4k_sigmoid_shared", 256, 7168, 2048, 8, 2048, 1, (1, 4096), 2),
+]
+
+
+def model_config_cases(nx, ctx, torch, args):
+    """The other model shapes of the hot-path survey (Q4_K experts, AUTO path):
+    per token count, ms/step and the fraction of HBM and dense-fp16 MFMA peak
+    on algorithmic bytes / FLOPs (realised routing).  Replicas are rotated so
+    that decode steps read HBM rather than the Infinity Cache."""
+    dev = torch.device("cuda", 0)
+    res = {}
+    for name, E, H, F, k, Fs, score, tokens, reps in MODEL_CONFIGS:
+        print(f"bench: {name}", file=sys.stderr, flush=True)
+        sets = make_expert_sets(nx, ctx, torch, nx.Q4_K, E, H, F, reps, args.seed + 31, Fs)
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed + 41)
+        Tm = max(tokens)
+        x = torch.randn((Tm, H), generator=g, device=dev, dtype=torch.float32)
+        router = torch.randn((E, H), generator=g, device=dev, dtype=torch.float32) * 0.02
+        logits = (x @ router.t()).contiguous()
+        out = torch.empty((Tm, H), device=dev, dtype=torch.float32)
+        cases = {}
+        for T in tokens:
+            counts = active_experts(ctx, logits[:T].cpu().numpy(), T, E, k, score)
+            n_act = sum(1 for c in counts if c) + (1 if Fs else 0)
+            wbytes = (sum(1 for c in counts if c) * 3 * H * F + (3 * H * Fs if Fs else 0)) \
+                * Q4K_BYTES_PER_WEIGHT
+            flops = 2.0 * 3 * H * F * sum(counts) + (2.0 * 3 * H * Fs * T if Fs else 0.0)
+
+            def step(i, T=T):
+                sets[i % len(sets)].forward_dev(x.data_ptr(), logits.data_ptr(), T, k,
+                                                out.data_ptr(), score_mode=score,
+                                                path=nx.PATH_AUTO)
+
+            steps = args.steps if T <= 64 else max(10, args.prefill_steps)
+            ms = time_steps(torch, step, steps, 3)
+            kern = kernel_means(ctx, torch, step, steps)
+            gbps = wbytes / (ms * 1e-3) / 1e9
+            tf = flops / (ms * 1e-3) / 1e12
+            cases[f"T{T}"] = {
+                "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
+                "experts_active": n_act, "weight_bytes": wbytes, "flops": flops,
+                "effective_GBps": gbps, "hbm_frac": gbps / HBM_PEAK_GBPS,
+                "TFLOPs": tf, "mfma_f16_frac": tf / MFMA_F16_PEAK_TFLOPS,
+                "path": "mfma_f16" if any(n.startswith("gemm") for n in kern) else "gemv",
+                "kernels_ms": {k_: round(v, 4) for k_, v in kern.items()}}
+        for s_ in sets:
+            s_.close()
+        res[name] = {"experts": E, "hidden": H, "ffn": F, "top_k": k, "shared_ffn": Fs,
+                     "score": "sigmoid" if score else "softmax", "weights": "Q4_K",
+                     "replicas_rotated": reps, "cases": cases}
+    return res
 
 
 def main():
@@ -260,6 +324,7 @@ def main():
     if not args.no_extra:
         print("bench: prefill", file=sys.stderr, flush=True)
         extra["prefill_2048_tokens"] = prefill(nx, ctx, torch, args)
+        extra["model_configs"] = model_config_cases(nx, ctx, torch, args)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "gemv_gateup_mixtral_q4k_t1_traffic.json")

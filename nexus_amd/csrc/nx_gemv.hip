@@ -328,13 +328,17 @@ struct RowGroup {
   }
 };
 
-template <int FMT, int LPR, int KSPLIT, int SPL, int NT>
+// PLAIN: one matrix (the down projection of one slot per grid.y), no
+// SwiGLU; activations are per pair (row pair0 + t of x) and each row's dot
+// product goes to out[pair][row] for the combine kernel.
+template <int FMT, int LPR, int KSPLIT, int SPL, int NT, bool PLAIN = false>
 __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   constexpr int L = LPR * KSPLIT;
   constexpr int GROUPS = 256 / L;
   constexpr int U = 2;  // rows per pipeline stage
   constexpr int S = 2;  // stages (S - 1 of them in flight while one is decoded)
-  using RG = RowGroup<FMT, L, SPL, NT, U, 2>;
+  constexpr int NMAT = PLAIN ? 1 : 2;
+  using RG = RowGroup<FMT, L, SPL, NT, U, NMAT>;
   const int tid = threadIdx.x, lane = tid & 63;
   // wave index, known to the compiler as wave-uniform
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
   const int slot = blockIdx.y;
   if (slot >= n_slots) return;  // workgroup-uniform
-  __shared__ float red[KSPLIT > 1 ? 4 * U * 2 * NT : 1];
+  __shared__ float red[KSPLIT > 1 ? 4 * U * NMAT * NT : 1];
 
   // one wave per row group: the workgroup shares the activation operands
   constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32;
@@ -355,7 +359,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   const int row_end = min(v.rows, row_begin + a.rows_per_group);
   RG g;
   g.init(KSPLIT == 1 ? (lane % LPR) : tid);
-  auto row_of = [&](int t) { return v.routed ? a.perm_token[v.pair0 + t] : t; };
+  auto row_of = [&](int t) {
+    return PLAIN ? v.pair0 + t : (v.routed ? a.perm_token[v.pair0 + t] : t);
+  };
 
   typename RG::Stage st[S];
   for (int t0 = 0; t0 < v.count; t0 += NT) {
@@ -373,7 +379,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
     }
 
     auto finish = [&](const typename RG::Stage &st, int r0) {
-      float acc[U][2][NT];
+      float acc[U][NMAT][NT];
       g.template compute<LPR>(st, acc);
       bool writer = (g.li % LPR) == LPR - 1;
       if constexpr (KSPLIT > 1) {
@@ -381,9 +387,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+            for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-              for (int t = 0; t < NT; ++t) red[((wave * U + u) * 2 + mt) * NT + t] = acc[u][mt][t];
+              for (int t = 0; t < NT; ++t)
+                red[((wave * U + u) * NMAT + mt) * NT + t] = acc[u][mt][t];
         }
         __syncthreads();
         writer = tid == 255;
@@ -391,12 +398,12 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+            for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
               for (int t = 0; t < NT; ++t) {
                 float s = 0.f;
 #pragma unroll
-                for (int w = 0; w < KSPLIT; ++w) s += red[((w * U + u) * 2 + mt) * NT + t];
+                for (int w = 0; w < KSPLIT; ++w) s += red[((w * U + u) * NMAT + mt) * NT + t];
                 acc[u][mt][t] = s;
               }
         }
@@ -410,8 +417,11 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
             if (t0 + t >= v.count) continue;
-            a.out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
-                silu_mul(acc[u][0][t], acc[u][1][t]);
+            if constexpr (PLAIN)
+              a.out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] = acc[u][0][t];
+            else
+              a.out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
+                  silu_mul(acc[u][0][t], acc[u][NMAT - 1][t]);
           }
         }
       }
@@ -564,16 +574,21 @@ struct Shape {
   int lpr, ksplit, spl;
 };
 
-// kernel instance for (format, tokens per group, shape, role, partials in LDS)
+// kernels: gate/up; down with the workgroup-local combine; down rows per
+// slot (grid.y), combined afterwards by k_combine
+enum GemvKind { KIND_GATEUP, KIND_DOWN_COMBINE, KIND_DOWN_ROWS };
+
+// kernel instance for (format, tokens per group, shape, kind, partials in LDS)
 template <int FMT, int NT, int LPR, int KSPLIT, int SPL>
-KernelFn inst(bool gateup, bool ylds) {
-  if (gateup) return k_gemv_gateup<FMT, LPR, KSPLIT, SPL, NT>;
+KernelFn inst(int kind, bool ylds) {
+  if (kind == KIND_GATEUP) return k_gemv_gateup<FMT, LPR, KSPLIT, SPL, NT>;
+  if (kind == KIND_DOWN_ROWS) return k_gemv_gateup<FMT, LPR, KSPLIT, SPL, NT, true>;
   return ylds ? k_gemv_down<FMT, LPR, KSPLIT, SPL, NT, true>
               : k_gemv_down<FMT, LPR, KSPLIT, SPL, NT, false>;
 }
 
 template <int FMT, int NT>
-KernelFn pick_shape(bool gateup, bool ylds, const Shape &s) {
+KernelFn pick_shape(int gateup, bool ylds, const Shape &s) {
   // two segments per lane exist only where choose_shape allows them
   constexpr bool two = 2 * Seg<FMT>::EPS * NT <= 64;
   if (s.ksplit == 1) {
@@ -591,11 +606,11 @@ KernelFn pick_shape(bool gateup, bool ylds, const Shape &s) {
 }
 
 template <int FMT>
-KernelFn pick_fmt(bool gateup, bool ylds, int nt, const Shape &s) {
+KernelFn pick_fmt(int gateup, bool ylds, int nt, const Shape &s) {
   return nt == 1 ? pick_shape<FMT, 1>(gateup, ylds, s) : pick_shape<FMT, 2>(gateup, ylds, s);
 }
 
-KernelFn pick(int fmt, bool gateup, bool ylds, int nt, const Shape &s) {
+KernelFn pick(int fmt, int gateup, bool ylds, int nt, const Shape &s) {
   switch (fmt) {
   case NX_FMT_Q4_K: return pick_fmt<NX_FMT_Q4_K>(gateup, ylds, nt, s);
   case NX_FMT_Q8_0: return pick_fmt<NX_FMT_Q8_0>(gateup, ylds, nt, s);
@@ -631,6 +646,13 @@ bool choose_shape(int nseg, int eps, int nt, Shape *s) {
 
 // partial sums of the down kernel stay in LDS up to this size per workgroup
 constexpr size_t kDownLdsMax = 64 * 1024;
+
+// slots a launch may see: active experts (at most E, at most T*k) plus the
+// shared expert
+int slots_max_of(const nx_experts *ex, const GemvPlan &p) {
+  const long routed = std::min<long>(ex->E, (long)p.T * p.k);
+  return (int)routed + (ex->Fs > 0 ? 1 : 0);
+}
 
 int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const nx_experts *ex = p.ex;
@@ -689,9 +711,16 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const int groups_per_wg = 256 / L;
   const int slots_max = (ex->E < p.T * p.k ? ex->E : p.T * p.k) + (has_shared ? 1 : 0);
   const int rows = a.rows > a.srows ? a.rows : a.srows;
+  // The down pass combines its rows inside the workgroup when there are at
+  // most two slots (one token's top-2: the halves of the workgroup run them
+  // side by side); beyond that the slots go to grid.y like gate/up, each
+  // writing its rows per pair, and the combine runs as its own kernel.
+  const bool down_rows = !gateup && slots_max_of(ex, p) > DOWN_SG;
+  const int kind = gateup ? KIND_GATEUP : (down_rows ? KIND_DOWN_ROWS : KIND_DOWN_COMBINE);
+  const bool per_slot = gateup || down_rows;
   // residency is register-bound (eight waves per CU by launch bounds)
-  const int threads = gateup ? 256 : 256 * DOWN_SG;
-  KernelFn probe = pick(ex->fmt, gateup, true, nt, sh);
+  const int threads = per_slot ? 256 : 256 * DOWN_SG;
+  KernelFn probe = pick(ex->fmt, kind, true, nt, sh);
   if (!probe) return fail(NX_ERR_UNSUPPORTED, "no GEMV kernel instance for this shape");
   int wg_per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wg_per_cu, reinterpret_cast<const void *>(probe),
@@ -703,7 +732,7 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   // gate/up spreads slots over grid.y; down runs all slots inside each
   // workgroup.  Size the row runs so the launch is one round of resident
   // workgroups with equal work each.
-  const long work_rows = gateup ? (long)rows * slots_max : (long)rows;
+  const long work_rows = per_slot ? (long)rows * slots_max : (long)rows;
   const long groups = (long)c->num_cu * wg_per_cu * groups_per_wg;
   long rpg = (work_rows + groups - 1) / groups;
   if (rpg < 1) rpg = 1;
@@ -716,6 +745,14 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
     return launch(c, "gemv_gateup",
                   [&] { hipLaunchKernelGGL(probe, grid, dim3(256), 0, c->stream, a); });
   }
+  if (down_rows) {
+    a.out = p.ypair;
+    a.out_stride = ex->H;
+    const dim3 grid(gx, (unsigned)slots_max);
+    NX_TRY(launch(c, "gemv_down",
+                  [&] { hipLaunchKernelGGL(probe, grid, dim3(256), 0, c->stream, a); }));
+    return launch_combine(c, p.ypair, p.rw, p.rcnt, p.inv, p.T, p.k, ex->H, has_shared, p.out);
+  }
 
   a.rw = p.rw;
   a.rcnt = p.rcnt;
@@ -724,7 +761,7 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   a.npairs = (int)((long)p.T * p.k + (has_shared ? p.T : 0));
   const size_t part_bytes = (size_t)sh.ksplit * a.npairs * rows_per_wg * sizeof(float);
   const bool ylds = part_bytes <= kDownLdsMax;
-  KernelFn fn = pick(ex->fmt, false, ylds, nt, sh);
+  KernelFn fn = pick(ex->fmt, KIND_DOWN_COMBINE, ylds, nt, sh);
   if (!fn) return fail(NX_ERR_UNSUPPORTED, "no GEMV kernel instance for this shape");
   if (!ylds) {
     void *gp = nullptr;
