@@ -10,9 +10,10 @@ W_r ~N(0, 0.02).  Several replicas of the expert set (more than twice the
 so the weight bytes come from HBM.
 
 Extras in the same line (skipped with --no-extra): Mixtral decode at 32
-tokens, Mixtral Q8_0 prefill at 2048 tokens (MFMA grouped GEMM), and the
-Qwen3 (E=128, k=8) and DeepSeek (E=256, k=8, sigmoid, shared expert) shapes
-at their decode and batch token counts.
+tokens, Mixtral Q8_0 prefill at 2048 tokens (MFMA grouped GEMM), the Qwen3
+(E=128, k=8) and DeepSeek (E=256, k=8, sigmoid, shared expert) shapes at
+their decode and batch token counts, and the router logits (exact and fast
+mode) for the three shapes.
 
 Prints one JSON line (rank 0, N=1).  `value` = tokens/s of the whole layer.
 `roofline` is for the dominant kernel (the gate/up GEMV): algorithmic bytes
@@ -117,7 +118,14 @@ def cpu_baseline(nx, ctx, torch, x, logits, E, H, F, k, seed, ntok):
     for t in range(ntok):
         oracle.dispatch_moe_ffn(xs_h[t], lg_h[t], mats[0], mats[1], mats[2], k, H, F)
     dt = time.perf_counter() - t0
+    # the router matvec (InferenceEngine::matvec on W_r) for the same tokens
+    rw_h = rw.cpu().numpy().ravel()
+    t1 = time.perf_counter()
+    for t in range(ntok):
+        oracle.matvec(rw_h, E, H, xs_h[t])
+    dtr = time.perf_counter() - t1
     return {"value": ntok / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "router_matvec_us_per_token": dtr / ntok * 1e6,
             "sample": f"{ntok} tokens of the same Mixtral Q4_K layer through the oracle's "
                       f"single-threaded dispatch_moe_ffn (f32 weights dequantized from the "
                       f"Q4_K payloads outside the timed region), {dt:.1f} s"}
@@ -197,6 +205,47 @@ MODEL_CONFIGS = [
     ("qwen3_q4k", 128, 2048, 768, 8, 0, 0, (1, 64, 512), 2),
     ("deepseek_q4k_sigmoid_shared", 256, 7168, 2048, 8, 2048, 1, (1, 4096), 2),
 ]
+
+
+ROUTER_SHAPES = [
+    # name, E, H, token counts
+    ("mixtral", 8, 4096, (1, 32, 2048)),
+    ("qwen3", 128, 2048, (1, 512)),
+    ("deepseek", 256, 7168, (1, 4096)),
+]
+
+
+def router_cases(nx, ctx, torch, args):
+    """Router logits on device (logits = x . W_r^T, fp32): kernel mean time of
+    the exact mode (the reference matvec's sequential order, bit-identical)
+    and of the fast mode (parallel order with fma), per model shape and token
+    count."""
+    dev = torch.device("cuda", 0)
+    res = {}
+    for name, E, H, tokens in ROUTER_SHAPES:
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed + 51)
+        Tm = max(tokens)
+        x = torch.randn((Tm, H), generator=g, device=dev, dtype=torch.float32)
+        w = torch.randn((E, H), generator=g, device=dev, dtype=torch.float32) * 0.02
+        out = torch.empty((Tm, E), device=dev, dtype=torch.float32)
+        cases = {}
+        for T in tokens:
+            row = {}
+            for exact in (True, False):
+                def step(i, T=T, exact=exact):
+                    ctx.router_logits_dev(w.data_ptr(), E * H, x.data_ptr(), T * H, T, E, H,
+                                          out.data_ptr(), exact=exact)
+
+                n = 50 if T <= 64 else 10
+                time_steps(torch, step, 3, 2)
+                kern = kernel_means(ctx, torch, step, n)
+                ms = sum(kern.values())
+                row["exact_us" if exact else "fast_us"] = round(ms * 1e3, 2)
+                row["exact_kernel" if exact else "fast_kernel"] = next(iter(kern), None)
+            cases[f"T{T}"] = row
+        res[name] = {"experts": E, "hidden": H, "cases": cases}
+    return res
 
 
 def model_config_cases(nx, ctx, torch, args):
@@ -325,6 +374,8 @@ def main():
         print("bench: prefill", file=sys.stderr, flush=True)
         extra["prefill_2048_tokens"] = prefill(nx, ctx, torch, args)
         extra["model_configs"] = model_config_cases(nx, ctx, torch, args)
+        print("bench: router logits", file=sys.stderr, flush=True)
+        extra["router_logits"] = router_cases(nx, ctx, torch, args)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "gemv_gateup_mixtral_q4k_t1_traffic.json")

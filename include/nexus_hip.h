@@ -14,6 +14,9 @@
  *       InferenceEngine::dispatch_moe_ffn   src/engine/mod.rs:969-1024
  *       (row t of a batch == dispatch_moe_ffn on row t; the expert products
  *        InferenceEngine::matvec src/engine/mod.rs:775-801 run on device)
+ *   nx_router_logits / nx_router_logits_dev
+ *       InferenceEngine::matvec             src/engine/mod.rs:775-801
+ *       applied to the router weight, one call per token
  *   nx_route_topk
  *       InferenceEngine::route_moe_experts  src/engine/mod.rs:918-966
  *   nx_permute
@@ -113,6 +116,22 @@ int nx_quantize_dev(nx_ctx *ctx, int fmt, const float *d_src, size_t n_elems, vo
                     size_t dst_bytes);
 
 /* ---------------------------------------------------------------- routing */
+/* Router logits: logits[t * E + e] = sum_c w_router[e * H + c] * x[t * H + c]
+ * for T = num_tokens, E = num_experts, H = hidden, all fp32.
+ * exact != 0: each (t, e) is summed from 0.0f in column order with every
+ * product and every sum rounded once, the order of InferenceEngine::matvec
+ * (src/engine/mod.rs:775-801) on token row t, so the logits are bit-identical
+ * to the reference's and top-k picks the same experts.  exact == 0: parallel
+ * order with fma; |fast - exact| <= 2 (H+1) 2^-24 sum_c |w x|.
+ * Errors as in matvec (NX_ERR_SHAPE): x_len != T*H gives "Matvec input shape
+ * mismatch: got <x_len>, expected <T*H>"; w_len < E*H gives "Matvec weight
+ * too small: got <w_len>, expected at least <E*H>". */
+int nx_router_logits(nx_ctx *ctx, const float *w_router, size_t w_len, const float *x,
+                     size_t x_len, int num_tokens, int num_experts, int hidden, int exact,
+                     float *logits);
+int nx_router_logits_dev(nx_ctx *ctx, const float *d_w_router, size_t w_len, const float *d_x,
+                         size_t x_len, int num_tokens, int num_experts, int hidden, int exact,
+                         float *d_logits);
 /* Top-k routing of [num_tokens x num_experts] logits.  Outputs are
  * [num_tokens x top_k] (expert -1 / weight 0 padding) and counts[num_tokens].
  * *lists is the number of route lists produced (tokens whose logits lie

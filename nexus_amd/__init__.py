@@ -34,7 +34,8 @@ EXPORTS = [
     "nx_last_error", "nx_version", "nx_device_count", "nx_ctx_create", "nx_ctx_destroy",
     "nx_ctx_set_stream", "nx_ctx_get_stream", "nx_sync", "nx_mem_info", "nx_profile_enable",
     "nx_profile_reset", "nx_profile_count", "nx_profile_get", "nx_quant_bytes", "nx_dequant",
-    "nx_dequant_dev", "nx_quantize", "nx_quantize_dev", "nx_route_topk", "nx_permute",
+    "nx_dequant_dev", "nx_quantize", "nx_quantize_dev", "nx_router_logits",
+    "nx_router_logits_dev", "nx_route_topk", "nx_permute",
     "nx_experts_create", "nx_experts_add_shared", "nx_experts_load", "nx_experts_info",
     "nx_experts_destroy", "nx_moe_forward", "nx_moe_forward_dev",
 ]
@@ -86,6 +87,10 @@ def lib():
         "nx_dequant_dev": ([_vp, C.c_int, _vp, C.c_size_t, C.c_size_t, _vp], C.c_int),
         "nx_quantize": ([_vp, C.c_int, _fp, C.c_size_t, _vp, C.c_size_t], C.c_int),
         "nx_quantize_dev": ([_vp, C.c_int, _vp, C.c_size_t, _vp, C.c_size_t], C.c_int),
+        "nx_router_logits": ([_vp, _fp, C.c_size_t, _fp, C.c_size_t, C.c_int, C.c_int, C.c_int,
+                              C.c_int, _fp], C.c_int),
+        "nx_router_logits_dev": ([_vp, _vp, C.c_size_t, _vp, C.c_size_t, C.c_int, C.c_int,
+                                  C.c_int, C.c_int, _vp], C.c_int),
         "nx_route_topk": ([_vp, _fp, C.c_size_t, C.c_int, C.c_int, C.c_int, C.c_int, _i32p, _fp,
                            _i32p, _ip], C.c_int),
         "nx_permute": ([_vp, _i32p, _i32p, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _i32p, _i32p,
@@ -208,6 +213,36 @@ class Context:
         check(lib().nx_quantize_dev(self.h, fmt, _vp(src_ptr), n, _vp(dst_ptr), dst_bytes))
 
     # ----------------------------------------------------------- routing
+    def router_logits(self, w_router, x, num_experts: int, hidden: int,
+                      exact: bool = True) -> np.ndarray:
+        """logits [T x E] = x [T x H] . w_router[E x H]^T on device.  exact=True
+        reproduces InferenceEngine::matvec (src/engine/mod.rs:775-801) bit for bit."""
+        w = _f32(w_router).ravel()
+        xf = _f32(x).ravel()
+        T = xf.size // hidden if hidden else 0
+        out = np.empty(max(T * num_experts, 1), np.float32)
+        check(lib().nx_router_logits(self.h, _p(w, _fp), w.size, _p(xf, _fp), xf.size, T,
+                                     num_experts, hidden, 1 if exact else 0, _p(out, _fp)))
+        return out[:T * num_experts].reshape(T, num_experts)
+
+    def router_logits_raw(self, w_router, w_len: int, x, x_len: int, num_tokens: int,
+                          num_experts: int, hidden: int, exact: bool = True) -> np.ndarray:
+        """The C call with explicit lengths (for shape-error tests)."""
+        w = _f32(w_router).ravel()
+        xf = _f32(x).ravel()
+        assert w.size >= w_len and xf.size >= x_len
+        out = np.empty(max(num_tokens * num_experts, 1), np.float32)
+        check(lib().nx_router_logits(self.h, _p(w, _fp), w_len, _p(xf, _fp), x_len, num_tokens,
+                                     num_experts, hidden, 1 if exact else 0, _p(out, _fp)))
+        return out[:num_tokens * num_experts].reshape(num_tokens, num_experts)
+
+    def router_logits_dev(self, w_ptr: int, w_len: int, x_ptr: int, x_len: int,
+                          num_tokens: int, num_experts: int, hidden: int, out_ptr: int,
+                          exact: bool = True):
+        check(lib().nx_router_logits_dev(self.h, _vp(w_ptr), w_len, _vp(x_ptr), x_len,
+                                         num_tokens, num_experts, hidden, 1 if exact else 0,
+                                         _vp(out_ptr)))
+
     def route_topk(self, logits, num_tokens: int, num_experts: int, top_k: int,
                    score_mode: int = SCORE_SOFTMAX):
         lg = _f32(logits).ravel()

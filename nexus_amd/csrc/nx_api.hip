@@ -435,6 +435,51 @@ int nx_route_topk(nx_ctx *c, const float *logits, size_t logits_len, int T, int 
   return NX_OK;
 }
 
+// Shape checks of InferenceEngine::matvec (src/engine/mod.rs:776-789), with
+// the input of T tokens taken as one [T x H] array.
+static int check_logits(const float *w, size_t w_len, const float *x, size_t x_len, int T, int E,
+                        int H, const float *out) {
+  if (T < 0 || E < 0 || H < 0) return fail(NX_ERR_INVALID_ARG, "negative size");
+  const size_t need_x = (size_t)T * H, need_w = (size_t)E * H;
+  if (x_len != need_x)
+    return fail(NX_ERR_SHAPE, "Matvec input shape mismatch: got " + std::to_string(x_len) +
+                                  ", expected " + std::to_string(need_x));
+  if (w_len < need_w)
+    return fail(NX_ERR_SHAPE, "Matvec weight too small: got " + std::to_string(w_len) +
+                                  ", expected at least " + std::to_string(need_w));
+  // device offsets are 32-bit
+  if (need_w * 4 > 0x7FFFFF00u || need_x * 4 > 0x7FFFFF00u || (size_t)T * E > 0x7FFFFFFFu)
+    return fail(NX_ERR_UNSUPPORTED, "router weight, input or logits over 2 GiB");
+  if (T > 0 && E > 0 && (!out || (H > 0 && (!w || !x))))
+    return fail(NX_ERR_INVALID_ARG, "null buffer");
+  return NX_OK;
+}
+
+int nx_router_logits_dev(nx_ctx *c, const float *w, size_t w_len, const float *x, size_t x_len,
+                         int T, int E, int H, int exact, float *logits) {
+  NX_TRY(check_ctx(c));
+  NX_TRY(check_logits(w, w_len, x, x_len, T, E, H, logits));
+  return launch_router_logits(c, w, x, T, E, H, exact != 0, logits);
+}
+
+int nx_router_logits(nx_ctx *c, const float *w, size_t w_len, const float *x, size_t x_len,
+                     int T, int E, int H, int exact, float *logits) {
+  NX_TRY(check_ctx(c));
+  NX_TRY(check_logits(w, w_len, x, x_len, T, E, H, logits));
+  if (T == 0 || E == 0) return NX_OK;
+  const size_t nw = (size_t)E * H, nx_ = (size_t)T * H, no = (size_t)T * E;
+  float *d_w, *d_x, *d_o;
+  NX_TRY(ws(c, WS_ROUTER_W, std::max<size_t>(nw, 1), &d_w));
+  NX_TRY(ws(c, WS_XIN, std::max<size_t>(nx_, 1), &d_x));
+  NX_TRY(ws(c, WS_LOGITS, no, &d_o));
+  if (nw) NX_HIP(hipMemcpyAsync(d_w, w, nw * 4, hipMemcpyHostToDevice, c->stream));
+  if (nx_) NX_HIP(hipMemcpyAsync(d_x, x, nx_ * 4, hipMemcpyHostToDevice, c->stream));
+  NX_TRY(launch_router_logits(c, d_w, d_x, T, E, H, exact != 0, d_o));
+  NX_HIP(hipMemcpyAsync(logits, d_o, no * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}
+
 int nx_permute(nx_ctx *c, const int32_t *experts, const int32_t *counts, int T, int k, int E,
                int32_t *ecount, int32_t *offsets, int32_t *ptok, int32_t *pslot, int32_t *inv) {
   NX_TRY(check_ctx(c));

@@ -123,6 +123,7 @@ enum WsSlot {
   WS_OUT,
   WS_TILES,    // grouped-GEMM tile list
   WS_XH,       // half-precision copy of activations for the MFMA path
+  WS_ROUTER_W, // device copy of the router weight for blocking calls
 };
 
 int ws_get(nx_ctx *c, int slot, size_t bytes, void **out);
@@ -162,6 +163,10 @@ int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, 
                          int32_t *d_expert, float *d_weight, int32_t *d_count, int32_t *d_ecount,
                          int32_t *d_offsets, int32_t *d_ptok, int32_t *d_pslot, int32_t *d_inv,
                          int32_t *d_active, int *d_counters, int n_counters);
+// logits[t][e] = sum_c w[e][c] x[t][c]; exact: the reference's sequential
+// order with separately rounded products and sums
+int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, int E, int H,
+                         bool exact, float *d_out);
 // out[t] = sum_r w[t,r] * y[pair(t,r)] (+ y[shared row t]); y is the sum of
 // nsplit partial buffers split_stride floats apart
 int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,

@@ -1,0 +1,442 @@
+// nx_logits.hip — router logits on gfx950: logits[t][e] = sum_c W[e][c] * x[t][c].
+//
+// The reference computes router logits with its host matvec
+// (InferenceEngine::matvec, src/engine/mod.rs:775-801): per output, sum starts
+// at 0.0f and for col in 0..cols adds weight * input, the product rounded to
+// f32 and then the sum rounded to f32 (Rust never fuses a*b+c into an fma).
+// Top-k routing compares those logits exactly, ties going to the lower
+// expert, so a device router that must pick the same experts as the reference
+// has to reproduce that order to the last bit.
+//
+// Exact mode does: every (token, expert) pair is one sequential chain over
+// the columns, with separately rounded products and sums (contraction is off
+// in every kernel here; fast mode asks for fma explicitly).  A sum that
+// starts at +0.0 is never -0.0, so adding +0.0 products for columns past the
+// row end (loads out of range return zeros) leaves it unchanged.
+//
+// Fast mode sums in a parallel order with fma: the result differs from the
+// exact one by at most 2 (H+1) 2^-24 sum_c |W[e][c] x[t][c]| (both lie within
+// (H+1) 2^-24 sum |w x| of the real dot product).
+//
+// Kernels:
+//   k_logits_chain8  exact, few chains (decode).  Eight chains per wavefront,
+//                    eight lanes per chain: in each group of 32 columns lane
+//                    8c+j loads columns 4j..4j+3 of chain c's weight and input
+//                    rows (each chain reads one 128-byte line of each, by DMA
+//                    into an LDS ring) and forms the four products; the
+//                    chain's 32 products go through LDS and are added in
+//                    column order.  Products cost
+//                    4 instructions per 32 columns instead of 32, so a chain
+//                    advances one dependent add per instruction slot (about
+//                    4.4 clocks: a chain's latency is ~H * 1.9 ns).
+//   k_logits_lane    exact or fast, many chains (prefill).  One lane per
+//                    expert and BT tokens; with 64 experts per wave the token
+//                    rows are wave-uniform and read through the scalar cache.
+//   k_logits_dot     fast, few tokens.  A workgroup per (expert, block of
+//                    tokens) strides over the row in 16-byte loads and reduces
+//                    with DPP and LDS.
+#include "nx_device.hpp"
+#include "nx_internal.hpp"
+
+namespace nx {
+
+namespace {
+
+struct F4 {
+  float v[4];
+};
+
+__device__ __forceinline__ F4 load_f4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto q = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  F4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o.v[i] = __uint_as_float(q[i]);
+  return o;
+}
+
+// four columns c..c+3 of a row starting at byte `row`; columns at or past H
+// (and every column of an invalid row) read as zero
+template <bool VEC>
+__device__ __forceinline__ F4 load_cols(__amdgpu_buffer_rsrc_t r, uint32_t row, int c, int H,
+                                        bool valid) {
+  if constexpr (VEC) {  // H % 4 == 0: the four columns are all in or all out
+    return load_f4(r, valid && c < H ? row + 4u * (uint32_t)c : OOB);
+  } else {
+    F4 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o.v[i] = __uint_as_float(bload4(r, valid && c + i < H ? row + 4u * (uint32_t)(c + i) : OOB));
+    return o;
+  }
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt vmcnt(n) with the other counters unconstrained
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+template <int V>
+using IC = std::integral_constant<int, V>;
+
+// Workgroup barrier for LDS hand-offs between waves: waits for this wave's
+// LDS operations only (DMA loads in flight stay in flight).  The wavefront
+// fences keep the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+
+constexpr int C8_G = 4;     // 32-column groups per ring stage
+constexpr int C8_NS = 4;    // ring stages (loads run C8_NS - 1 stages ahead)
+constexpr int C8_ROW = 36;  // floats per chain in the LDS product tile (32 + 4 pad)
+
+// Operands go global -> LDS by DMA (buffer_load ... lds) into a ring of
+// stages, with explicit vmcnt waits, so nothing is carried in registers from
+// one loop trip to the next.  A stage holds, per group, the 64 lanes' four
+// weight and four input columns (lane l's 16 bytes at 16 l with 16-byte
+// loads; with 4-byte loads column i of lane l at 256 i + 4 l).
+template <bool VEC>
+__global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__ W,
+                                                      const float *__restrict__ X, int T, int E,
+                                                      int H, float *__restrict__ out) {
+#pragma clang fp contract(off)
+  // one array per ring stage and operand (eight, as many DMA targets as the
+  // compiler tracks): it then knows which DMA a read depends on and waits for
+  // that one only
+  __shared__ __attribute__((aligned(16))) float ringw0[C8_G][256], ringx0[C8_G][256];
+  __shared__ __attribute__((aligned(16))) float ringw1[C8_G][256], ringx1[C8_G][256];
+  __shared__ __attribute__((aligned(16))) float ringw2[C8_G][256], ringx2[C8_G][256];
+  __shared__ __attribute__((aligned(16))) float ringw3[C8_G][256], ringx3[C8_G][256];
+  __shared__ __attribute__((aligned(16))) float prod0[C8_G][8 * C8_ROW];
+  __shared__ __attribute__((aligned(16))) float prod1[C8_G][8 * C8_ROW];
+  static_assert(C8_NS == 4, "four ring arrays");
+  const bool producer = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == 0;
+  const int lane = threadIdx.x & 63;
+  const int j = lane & 7;
+  const int cw = lane >> 3;  // chain within the wave
+  const int chain = blockIdx.x * 8 + cw;
+  const bool valid = chain < T * E;
+  const int t = valid ? chain / E : 0;
+  const int e = valid ? chain - t * E : 0;
+  const auto rw = make_rsrc(W, (uint32_t)((size_t)E * H * 4));
+  const auto rx = make_rsrc(X, (uint32_t)((size_t)T * H * 4));
+  // lane's first column of every group (invalid chains read past the buffers)
+  const uint32_t wbase = valid ? (uint32_t)e * (uint32_t)H * 4u + 16u * j : OOB;
+  const uint32_t xbase = valid ? (uint32_t)t * (uint32_t)H * 4u + 16u * j : OOB;
+  const int nk = (H + 32 * C8_G - 1) / (32 * C8_G);  // stages
+  // ring slot S: weight (P = 0) or input (P = 1) columns
+  auto slot_of = [&](auto st, auto pt) -> float(*)[256] {
+    constexpr int S = decltype(st)::value, P = decltype(pt)::value;
+    if constexpr (S == 0) return P ? ringx0 : ringw0;
+    else if constexpr (S == 1) return P ? ringx1 : ringw1;
+    else if constexpr (S == 2) return P ? ringx2 : ringw2;
+    else return P ? ringx3 : ringw3;
+  };
+  auto prod_of = [&](auto pb) -> float(*)[8 * C8_ROW] {
+    if constexpr (decltype(pb)::value == 0) return prod0;
+    else return prod1;
+  };
+
+  // DMA of stage k into ring slot S = k % C8_NS.  Columns at or past H read
+  // as zero: whole groups past the end through a uniform offset past the
+  // buffers, the lanes of a group that straddles H through a per-lane test.
+  auto issue = [&](auto st, int k) {
+    float(*sw)[256] = slot_of(st, IC<0>{});
+    float(*sx)[256] = slot_of(st, IC<1>{});
+#pragma unroll
+    for (int g = 0; g < C8_G; ++g) {
+      const int g0 = (k * C8_G + g) * 32;  // first column of the group (uniform)
+      if constexpr (VEC) {
+        const uint32_t uo = g0 < H ? 4u * (uint32_t)g0 : OOB;
+        uint32_t ow = wbase + uo, ox = xbase + uo;
+        if (g0 + 32 > H && g0 < H) {  // the group straddles the row end
+          const bool in = 4 * j < H - g0;
+          ow = in ? ow : OOB;
+          ox = in ? ox : OOB;
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void *)sw[g], 16, ow, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)sx[g], 16, ox, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool in = g0 + 4 * j + i < H;
+          const uint32_t o = 4u * (uint32_t)(g0 + i);
+          const uint32_t ow = in ? wbase + o : OOB;
+          const uint32_t ox = in ? xbase + o : OOB;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void *)(sw[g] + 64 * i), 4, ow, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void *)(sx[g] + 64 * i), 4, ox, 0, 0, 0);
+        }
+      }
+    }
+  };
+  constexpr int LOADS = VEC ? 2 * C8_G : 8 * C8_G;  // loads per stage
+  // stages issued ahead of the one whose products are formed (vmcnt < 64)
+  constexpr int AHEAD = VEC ? C8_NS - 2 : 1;
+
+  // lane (cw, j): the four products of its columns of stage slot S into
+  // product buffer PB
+  auto products = [&](auto st, auto pb) {
+    float(*sw)[256] = slot_of(st, IC<0>{});
+    float(*sx)[256] = slot_of(st, IC<1>{});
+    float(*prod)[8 * C8_ROW] = prod_of(pb);
+#pragma unroll
+    for (int g = 0; g < C8_G; ++g) {
+      float w4[4], x4[4];
+      if constexpr (VEC) {
+        const float4 a = *reinterpret_cast<const float4 *>(&sw[g][4 * lane]);
+        const float4 b = *reinterpret_cast<const float4 *>(&sx[g][4 * lane]);
+        w4[0] = a.x, w4[1] = a.y, w4[2] = a.z, w4[3] = a.w;
+        x4[0] = b.x, x4[1] = b.y, x4[2] = b.z, x4[3] = b.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w4[i] = sw[g][64 * i + lane], x4[i] = sx[g][64 * i + lane];
+      }
+      float4 p;
+      p.x = w4[0] * x4[0];
+      p.y = w4[1] * x4[1];
+      p.z = w4[2] * x4[2];
+      p.w = w4[3] * x4[3];
+      *reinterpret_cast<float4 *>(&prod[g][cw * C8_ROW + 4 * j]) = p;
+    }
+  };
+  float s = 0.f;
+  // every lane of chain cw adds the chain's products of buffer PB in column
+  // order (broadcast reads, one group ahead of the adds)
+  auto adds = [&](auto pb) {
+    float(*prod)[8 * C8_ROW] = prod_of(pb);
+    float4 q[2][8];
+    auto read = [&](int g) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        q[g & 1][m] = *reinterpret_cast<const float4 *>(&prod[g][cw * C8_ROW + 4 * m]);
+    };
+    read(0);
+#pragma unroll
+    for (int g = 0; g < C8_G; ++g) {
+      if (g + 1 < C8_G) read(g + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        s = s + q[g & 1][m].x;
+        s = s + q[g & 1][m].y;
+        s = s + q[g & 1][m].z;
+        s = s + q[g & 1][m].w;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Two waves.  Wave 0 produces: at step k it issues the DMA of stage
+  // k+1+AHEAD and forms the products of stage k+1.  Wave 1 consumes: at step k
+  // it adds the products of stage k, so its instruction stream is the chain's
+  // adds and the LDS reads that feed them.  A workgroup barrier ends each
+  // step: the products of stage k+1 are then complete, and the consumer's
+  // reads of the other buffer are done before the producer rewrites it.
+  if (producer) {
+    issue(IC<0>{}, 0);
+    if constexpr (AHEAD >= 1) issue(IC<1>{}, 1);
+    if constexpr (AHEAD >= 2) issue(IC<2>{}, 2);
+    wait_vm<LOADS * AHEAD>();  // stage 0 has landed
+    __builtin_amdgcn_sched_barrier(0);
+    products(IC<0>{}, IC<0>{});
+  }
+  lds_barrier();
+  auto step = [&](auto st, int k) {
+    constexpr int S = decltype(st)::value;
+    if (producer) {
+      issue(IC<(S + 1 + AHEAD) % C8_NS>{}, k + 1 + AHEAD);  // past the row end: zeros
+      wait_vm<LOADS * AHEAD>();                               // stage k+1 has landed
+      __builtin_amdgcn_sched_barrier(0);
+      products(IC<(S + 1) % C8_NS>{}, IC<(S + 1) % 2>{});
+    } else {
+      adds(IC<S % 2>{});
+    }
+    lds_barrier();
+  };
+  for (int k = 0; k < nk; k += C8_NS) {
+    step(IC<0>{}, k);
+    if (k + 1 >= nk) break;
+    step(IC<1>{}, k + 1);
+    if (k + 2 >= nk) break;
+    step(IC<2>{}, k + 2);
+    if (k + 3 >= nk) break;
+    step(IC<3>{}, k + 3);
+  }
+  wait_vm<0>();  // the DMA of stages past the end has drained
+  if (!producer && valid && j == 0) out[(size_t)t * E + e] = s;
+}
+
+// Workgroup = 4 waves; lane l of wave w holds expert e0 + l % EW and tokens
+// t0 + (w * (64 / EW) + l / EW) * BT + b, b < BT.  Columns advance four at a
+// time with 16-byte loads (H % 4 == 0 and 16-byte aligned rows required).
+template <int EW, int BT, bool EXACT>
+__global__ __launch_bounds__(256) void k_logits_lane(const float *__restrict__ W,
+                                                     const float *__restrict__ X, int T, int E,
+                                                     int H, float *__restrict__ out) {
+#pragma clang fp contract(off)
+  constexpr int TG = 64 / EW;          // token groups per wave
+  constexpr int TPW = TG * BT;         // tokens per wave
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int e = blockIdx.x * EW + lane % EW;
+  const bool e_ok = e < E;
+  const int tw = blockIdx.y * (4 * TPW) + wave * TPW;  // wave's first token (uniform)
+  const int tl = tw + (lane / EW) * BT;                 // lane's first token
+  const auto rw = make_rsrc(W, (uint32_t)((size_t)E * H * 4));
+  const uint32_t wrow = (uint32_t)(e_ok ? e : 0) * (uint32_t)H * 4u;
+  float s[BT];
+#pragma unroll
+  for (int b = 0; b < BT; ++b) s[b] = 0.f;
+  // per-token row pointers; rows past T are clamped (their sums are dropped)
+  const float *xr[BT];
+#pragma unroll
+  for (int b = 0; b < BT; ++b) {
+    const int tb = (EW == 64 ? tw : tl) + b;
+    xr[b] = X + (size_t)(tb < T ? tb : T - 1) * H;
+  }
+  constexpr int U = 8;  // 4-column steps per loop trip
+  F4 wb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) wb[u] = load_f4(rw, e_ok && 4 * u < H ? wrow + 16u * u : OOB);
+  for (int c0 = 0; c0 < H; c0 += 4 * U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 4 * u;
+      const F4 w = wb[u];
+      const int cn = c + 4 * U;
+      wb[u] = load_f4(rw, e_ok && cn < H ? wrow + 4u * (uint32_t)cn : OOB);
+      if (c < H) {
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+          const float4 x = *reinterpret_cast<const float4 *>(xr[b] + c);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float xi = i == 0 ? x.x : i == 1 ? x.y : i == 2 ? x.z : x.w;
+            if constexpr (EXACT)
+              s[b] = s[b] + w.v[i] * xi;
+            else
+              s[b] = __builtin_fmaf(w.v[i], xi, s[b]);
+          }
+        }
+      }
+    }
+  }
+  if (e_ok) {
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+      const int tb = tl + b;
+      if (tb < T) out[(size_t)tb * E + e] = s[b];
+    }
+  }
+}
+
+// fast mode, few tokens: workgroup (expert, token block of BT)
+template <int BT, bool VEC>
+__global__ __launch_bounds__(256) void k_logits_dot(const float *__restrict__ W,
+                                                    const float *__restrict__ X, int T, int E,
+                                                    int H, float *__restrict__ out) {
+  __shared__ float part[4][BT];
+  const int e = blockIdx.x;
+  const int t0 = blockIdx.y * BT;
+  const auto rw = make_rsrc(W, (uint32_t)((size_t)E * H * 4));
+  const auto rx = make_rsrc(X, (uint32_t)((size_t)T * H * 4));
+  const uint32_t wrow = (uint32_t)e * (uint32_t)H * 4u;
+  float s[BT];
+#pragma unroll
+  for (int b = 0; b < BT; ++b) s[b] = 0.f;
+  for (int c = 4 * threadIdx.x; c < H; c += 4 * 256) {
+    const F4 w = load_cols<VEC>(rw, wrow, c, H, true);
+#pragma unroll
+    for (int b = 0; b < BT; ++b) {
+      const bool ok = t0 + b < T;
+      const F4 x = load_cols<VEC>(rx, (uint32_t)(ok ? t0 + b : 0) * (uint32_t)H * 4u, c, H, ok);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[b] = __builtin_fmaf(w.v[i], x.v[i], s[b]);
+    }
+  }
+  group_sum_n<64, BT>(s);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 63) {
+#pragma unroll
+    for (int b = 0; b < BT; ++b) part[wave][b] = s[b];
+  }
+  __syncthreads();
+  if (threadIdx.x < BT && t0 + (int)threadIdx.x < T) {
+    const int b = threadIdx.x;
+    out[(size_t)(t0 + b) * E + e] = (part[0][b] + part[1][b]) + (part[2][b] + part[3][b]);
+  }
+}
+
+template <int EW, bool EXACT>
+void launch_lane(nx_ctx *c, int bt, const float *W, const float *X, int T, int E, int H,
+                 float *out) {
+  const int tpw = (64 / EW) * bt;
+  const dim3 grid((E + EW - 1) / EW, (T + 4 * tpw - 1) / (4 * tpw));
+  switch (bt) {
+    case 8: k_logits_lane<EW, 8, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out); break;
+    case 4: k_logits_lane<EW, 4, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out); break;
+    case 2: k_logits_lane<EW, 2, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out); break;
+    default: k_logits_lane<EW, 1, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out); break;
+  }
+}
+
+template <bool EXACT>
+void launch_lane_ew(nx_ctx *c, int bt, const float *W, const float *X, int T, int E, int H,
+                    float *out) {
+  if (E >= 64) launch_lane<64, EXACT>(c, bt, W, X, T, E, H, out);
+  else if (E > 16) launch_lane<32, EXACT>(c, bt, W, X, T, E, H, out);
+  else if (E > 8) launch_lane<16, EXACT>(c, bt, W, X, T, E, H, out);
+  else launch_lane<8, EXACT>(c, bt, W, X, T, E, H, out);
+}
+
+}  // namespace
+
+// chains (token, expert pairs) up to which the exact path uses k_logits_chain8
+constexpr long LOGITS_CHAIN8_MAX = 16384;
+// fast path: tokens up to which k_logits_dot is used
+constexpr int LOGITS_DOT_MAX_T = 8;
+
+int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, int E, int H,
+                         bool exact, float *d_out) {
+  if (T <= 0 || E <= 0) return NX_OK;
+  const bool vec = H % 4 == 0 && ((uintptr_t)d_w & 15) == 0 && ((uintptr_t)d_x & 15) == 0;
+  const long chains = (long)T * E;
+  // the exact order is also a valid fast order: the chain kernel serves both
+  // modes up to LOGITS_CHAIN8_MAX chains, except fast mode's few-token case
+  const bool dot = !exact && vec && T <= LOGITS_DOT_MAX_T;
+  const bool chain8 = !vec || (!dot && chains <= LOGITS_CHAIN8_MAX);
+  if (chain8) {
+    const unsigned grid = (unsigned)((chains + 7) / 8);
+    return launch(c, "router_logits_chain8", [&] {
+      if (vec)
+        k_logits_chain8<true><<<grid, 128, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
+      else
+        k_logits_chain8<false><<<grid, 128, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
+    });
+  }
+  if (dot) {
+    const int bt = T == 1 ? 1 : (T <= 4 ? 4 : 8);
+    const dim3 grid(E, (T + bt - 1) / bt);
+    return launch(c, "router_logits_dot", [&] {
+      if (bt == 1) k_logits_dot<1, true><<<grid, 256, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
+      else if (bt == 4) k_logits_dot<4, true><<<grid, 256, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
+      else k_logits_dot<8, true><<<grid, 256, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
+    });
+  }
+  // tokens per lane: as many as keep at least 2048 waves in the grid
+  int bt = 8;
+  while (bt > 1 && chains / (64L * bt) < 2048) bt >>= 1;
+  return launch(c, exact ? "router_logits_lane" : "router_logits_lane_fma", [&] {
+    if (exact)
+      launch_lane_ew<true>(c, bt, d_w, d_x, T, E, H, d_out);
+    else
+      launch_lane_ew<false>(c, bt, d_w, d_x, T, E, H, d_out);
+  });
+}
+
+}  // namespace nx

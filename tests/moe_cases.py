@@ -95,3 +95,50 @@ def assert_same_bits(got, ref):
     bad = np.nonzero(got[~gn].view(np.uint32) != ref[~rn].view(np.uint32))[0]
     assert bad.size == 0, (f"{bad.size} values differ; first at {bad[:4]}: "
                            f"{got[~gn][bad[:4]]} vs {ref[~rn][bad[:4]]}")
+
+
+class DeviceArray:
+    """float32 device buffer allocated through the same HIP runtime that
+    libnexus_hip.so links (/opt/rocm's libamdhip64), for tests of the *_dev
+    entry points.  (torch bundles its own HIP runtime, which cannot start once
+    another runtime in the process holds the GPU.)"""
+
+    _hip = None
+
+    @classmethod
+    def hip(cls):
+        if cls._hip is None:
+            import ctypes as C
+            h = C.CDLL("libamdhip64.so.7")
+            h.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+            h.hipFree.argtypes = [C.c_void_p]
+            h.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+            h.hipDeviceSynchronize.argtypes = []
+            cls._hip = h
+        return cls._hip
+
+    def __init__(self, n: int, fill=None):
+        import ctypes as C
+        self.n = n
+        p = C.c_void_p()
+        assert self.hip().hipMalloc(C.byref(p), max(n, 1) * 4) == 0
+        self.ptr = p.value
+        if fill is not None:
+            self.upload(np.full(n, fill, np.float32))
+
+    def upload(self, a, offset: int = 0):
+        a = np.ascontiguousarray(a, np.float32).ravel()
+        assert offset + a.size <= self.n
+        assert self.hip().hipMemcpy(self.ptr + 4 * offset, a.ctypes.data, a.nbytes, 1) == 0
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.n, np.float32)
+        assert self.hip().hipDeviceSynchronize() == 0
+        assert self.hip().hipMemcpy(out.ctypes.data, self.ptr, out.nbytes, 2) == 0
+        return out
+
+    def __del__(self):
+        try:
+            self.hip().hipFree(self.ptr)
+        except Exception:
+            pass
