@@ -29,9 +29,9 @@
 //                    4 instructions per 32 columns instead of 32, so a chain
 //                    advances one dependent add per instruction slot (about
 //                    4.4 clocks: a chain's latency is ~H * 1.9 ns).
-//   k_logits_lane    exact or fast, many chains (prefill).  One lane per
-//                    expert and BT tokens; with 64 experts per wave the token
-//                    rows are wave-uniform and read through the scalar cache.
+//   k_logits_tile    exact or fast, many chains (prefill).  A workgroup owns a
+//                    tile of tokens x experts, each lane a register block of
+//                    chains, with both operands staged through an LDS ring.
 //   k_logits_dot     fast, few tokens.  A workgroup per (expert, block of
 //                    tokens) strides over the row in 16-byte loads and reduces
 //                    with DPP and LDS.
@@ -271,66 +271,140 @@ __global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__
   if (!producer && valid && j == 0) out[(size_t)t * E + e] = s;
 }
 
-// Workgroup = 4 waves; lane l of wave w holds expert e0 + l % EW and tokens
-// t0 + (w * (64 / EW) + l / EW) * BT + b, b < BT.  Columns advance four at a
-// time with 16-byte loads (H % 4 == 0 and 16-byte aligned rows required).
-template <int EW, int BT, bool EXACT>
-__global__ __launch_bounds__(256) void k_logits_lane(const float *__restrict__ W,
+constexpr int TL_NS = 3;  // ring stages of the tiled kernel
+
+// Tile of (16 RB tokens) x (16 RB experts) per 256-thread workgroup: lane l
+// holds the RB x RB chains of tokens t0 + RB (l / 16) + i and experts
+// e0 + RB (l % 16) + j.  Columns are staged KC = 128 / RB at a time (512
+// 16-byte units per operand and stage) in an LDS ring filled by DMA; unit u
+// of row r sits at r * (KC / 4) + (u ^ (r & 7)), so the rows a wave reads at
+// one column spread over the banks.  Each chain is summed in column order,
+// exact mode with separately rounded products and sums, fast mode with fma.
+// Requires H % 4 == 0 and 16-byte aligned rows.
+template <int RB, bool EXACT>
+__global__ __launch_bounds__(256) void k_logits_tile(const float *__restrict__ W,
                                                      const float *__restrict__ X, int T, int E,
                                                      int H, float *__restrict__ out) {
 #pragma clang fp contract(off)
-  constexpr int TG = 64 / EW;          // token groups per wave
-  constexpr int TPW = TG * BT;         // tokens per wave
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int e = blockIdx.x * EW + lane % EW;
-  const bool e_ok = e < E;
-  const int tw = blockIdx.y * (4 * TPW) + wave * TPW;  // wave's first token (uniform)
-  const int tl = tw + (lane / EW) * BT;                 // lane's first token
+  constexpr int ROWS = 16 * RB;   // rows per operand tile
+  constexpr int KC = 128 / RB;    // columns per stage
+  constexpr int U = KC / 4;       // 16-byte units per row
+  constexpr int UNITS = ROWS * U; // = 512
+  // 1 KB DMAs per operand and stage: UNITS / 64 = 8, two per wave
+  constexpr int PW = UNITS / 64 / 4;
+  static_assert(UNITS == 512 && PW == 2, "tile shape");
+  __shared__ __attribute__((aligned(16))) float w0[UNITS * 4], x0[UNITS * 4];
+  __shared__ __attribute__((aligned(16))) float w1[UNITS * 4], x1[UNITS * 4];
+  __shared__ __attribute__((aligned(16))) float w2[UNITS * 4], x2[UNITS * 4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int e0 = blockIdx.x * ROWS, t0 = blockIdx.y * ROWS;
   const auto rw = make_rsrc(W, (uint32_t)((size_t)E * H * 4));
-  const uint32_t wrow = (uint32_t)(e_ok ? e : 0) * (uint32_t)H * 4u;
-  float s[BT];
+  const auto rx = make_rsrc(X, (uint32_t)((size_t)T * H * 4));
+
+  // DMA d of a wave (d < 2 PW: weight units for d < PW, input units after)
+  // writes LDS units b*64 .. b*64+63 of its operand, b = wave * PW + d % PW
+  // < UNITS / 64; lane L fetches the 16 bytes that belong at unit b*64 + L
+  uint32_t doff[2 * PW];
+  int dcol[2 * PW];
 #pragma unroll
-  for (int b = 0; b < BT; ++b) s[b] = 0.f;
-  // per-token row pointers; rows past T are clamped (their sums are dropped)
-  const float *xr[BT];
-#pragma unroll
-  for (int b = 0; b < BT; ++b) {
-    const int tb = (EW == 64 ? tw : tl) + b;
-    xr[b] = X + (size_t)(tb < T ? tb : T - 1) * H;
+  for (int d = 0; d < 2 * PW; ++d) {
+    const int p = (wave * PW + d % PW) * 64 + lane;
+    const int r = p / U, u = (p % U) ^ (r & 7);
+    const int row = (d < PW ? e0 : t0) + r;
+    const bool ok = row < (d < PW ? E : T);
+    doff[d] = ok ? (uint32_t)row * (uint32_t)H * 4u + 16u * (uint32_t)u : OOB;
+    dcol[d] = 4 * u;
   }
-  constexpr int U = 8;  // 4-column steps per loop trip
-  F4 wb[U];
+  auto wbuf = [&](auto st) -> float * {
+    constexpr int S = decltype(st)::value;
+    if constexpr (S == 0) return w0;
+    else if constexpr (S == 1) return w1;
+    else return w2;
+  };
+  auto xbuf = [&](auto st) -> float * {
+    constexpr int S = decltype(st)::value;
+    if constexpr (S == 0) return x0;
+    else if constexpr (S == 1) return x1;
+    else return x2;
+  };
+  auto issue = [&](auto st, int c) {
+    const int k0 = c * KC;
+    float *wb = wbuf(st), *xb = xbuf(st);
 #pragma unroll
-  for (int u = 0; u < U; ++u) wb[u] = load_f4(rw, e_ok && 4 * u < H ? wrow + 16u * u : OOB);
-  for (int c0 = 0; c0 < H; c0 += 4 * U) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + 4 * u;
-      const F4 w = wb[u];
-      const int cn = c + 4 * U;
-      wb[u] = load_f4(rw, e_ok && cn < H ? wrow + 4u * (uint32_t)cn : OOB);
-      if (c < H) {
-#pragma unroll
-        for (int b = 0; b < BT; ++b) {
-          const float4 x = *reinterpret_cast<const float4 *>(xr[b] + c);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float xi = i == 0 ? x.x : i == 1 ? x.y : i == 2 ? x.z : x.w;
-            if constexpr (EXACT)
-              s[b] = s[b] + w.v[i] * xi;
-            else
-              s[b] = __builtin_fmaf(w.v[i], xi, s[b]);
-          }
-        }
-      }
+    for (int d = 0; d < 2 * PW; ++d) {
+      const uint32_t off = k0 + dcol[d] < H ? doff[d] + 4u * (uint32_t)k0 : OOB;
+      float *dst = (d < PW ? wb : xb) + (wave * PW + d % PW) * 256;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(d < PW ? rw : rx, (lds_void *)dst, 16, off, 0, 0,
+                                               0);
     }
-  }
-  if (e_ok) {
+  };
+
+  const int tg = tid >> 4, eg = tid & 15;
+  float s[RB][RB];
 #pragma unroll
-    for (int b = 0; b < BT; ++b) {
-      const int tb = tl + b;
-      if (tb < T) out[(size_t)tb * E + e] = s[b];
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int j = 0; j < RB; ++j) s[i][j] = 0.f;
+  auto compute = [&](auto st) {
+    const float *wb = wbuf(st), *xb = xbuf(st);
+#pragma unroll
+    for (int k4 = 0; k4 < U; ++k4) {
+      float4 xv[RB], wv[RB];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int r = RB * tg + i;
+        xv[i] = *reinterpret_cast<const float4 *>(xb + 4 * (r * U + (k4 ^ (r & 7))));
+      }
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        const int r = RB * eg + j;
+        wv[j] = *reinterpret_cast<const float4 *>(wb + 4 * (r * U + (k4 ^ (r & 7))));
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int j = 0; j < RB; ++j) {
+            const float xk = kk == 0 ? xv[i].x : kk == 1 ? xv[i].y : kk == 2 ? xv[i].z : xv[i].w;
+            const float wk = kk == 0 ? wv[j].x : kk == 1 ? wv[j].y : kk == 2 ? wv[j].z : wv[j].w;
+            if constexpr (EXACT)
+              s[i][j] = s[i][j] + wk * xk;
+            else
+              s[i][j] = __builtin_fmaf(wk, xk, s[i][j]);
+          }
+    }
+  };
+  // stage c: wait for its DMA (stage c+1 may stay in flight), barrier (all
+  // waves' DMA of stage c landed; all reads of stage c-1's slot done), DMA of
+  // stage c+2 into that slot, then the chains advance KC columns
+  auto step = [&](auto st, int c) {
+    constexpr int S = decltype(st)::value;
+    wait_vm<2 * PW>();
+    lds_barrier();
+    issue(IC<(S + 2) % TL_NS>{}, c + 2);
+    compute(st);
+  };
+  const int nst = (H + KC - 1) / KC;
+  issue(IC<0>{}, 0);
+  issue(IC<1>{}, 1);
+  for (int c = 0; c < nst; c += TL_NS) {
+    step(IC<0>{}, c);
+    if (c + 1 >= nst) break;
+    step(IC<1>{}, c + 1);
+    if (c + 2 >= nst) break;
+    step(IC<2>{}, c + 2);
+  }
+  wait_vm<0>();  // the DMA of stages past the end has drained
+#pragma unroll
+  for (int i = 0; i < RB; ++i) {
+    const int t = t0 + RB * tg + i;
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      const int e = e0 + RB * eg + j;
+      if (t < T && e < E) out[(size_t)t * E + e] = s[i][j];
     }
   }
 }
@@ -372,26 +446,14 @@ __global__ __launch_bounds__(256) void k_logits_dot(const float *__restrict__ W,
   }
 }
 
-template <int EW, bool EXACT>
-void launch_lane(nx_ctx *c, int bt, const float *W, const float *X, int T, int E, int H,
-                 float *out) {
-  const int tpw = (64 / EW) * bt;
-  const dim3 grid((E + EW - 1) / EW, (T + 4 * tpw - 1) / (4 * tpw));
-  switch (bt) {
-    case 8: k_logits_lane<EW, 8, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out); break;
-    case 4: k_logits_lane<EW, 4, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out); break;
-    case 2: k_logits_lane<EW, 2, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out); break;
-    default: k_logits_lane<EW, 1, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out); break;
-  }
-}
-
 template <bool EXACT>
-void launch_lane_ew(nx_ctx *c, int bt, const float *W, const float *X, int T, int E, int H,
-                    float *out) {
-  if (E >= 64) launch_lane<64, EXACT>(c, bt, W, X, T, E, H, out);
-  else if (E > 16) launch_lane<32, EXACT>(c, bt, W, X, T, E, H, out);
-  else if (E > 8) launch_lane<16, EXACT>(c, bt, W, X, T, E, H, out);
-  else launch_lane<8, EXACT>(c, bt, W, X, T, E, H, out);
+void launch_tile(nx_ctx *c, int rb, const float *W, const float *X, int T, int E, int H,
+                 float *out) {
+  const int rows = 16 * rb;
+  const dim3 grid((E + rows - 1) / rows, (T + rows - 1) / rows);
+  if (rb == 4) k_logits_tile<4, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out);
+  else if (rb == 2) k_logits_tile<2, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out);
+  else k_logits_tile<1, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out);
 }
 
 }  // namespace
@@ -428,14 +490,13 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
       else k_logits_dot<8, true><<<grid, 256, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
     });
   }
-  // tokens per lane: as many as keep at least 2048 waves in the grid
-  int bt = 8;
-  while (bt > 1 && chains / (64L * bt) < 2048) bt >>= 1;
-  return launch(c, exact ? "router_logits_lane" : "router_logits_lane_fma", [&] {
+  // chains per lane: as many as keep at least 1024 waves in the grid
+  const int rb = chains >= 1024L * 64 * 16 ? 4 : (chains >= 1024L * 64 * 4 ? 2 : 1);
+  return launch(c, exact ? "router_logits_tile" : "router_logits_tile_fma", [&] {
     if (exact)
-      launch_lane_ew<true>(c, bt, d_w, d_x, T, E, H, d_out);
+      launch_tile<true>(c, rb, d_w, d_x, T, E, H, d_out);
     else
-      launch_lane_ew<false>(c, bt, d_w, d_x, T, E, H, d_out);
+      launch_tile<false>(c, rb, d_w, d_x, T, E, H, d_out);
   });
 }
 

@@ -6,9 +6,9 @@ for every token row (NaN positions identical, payloads not compared); fast
 mode within 2 (H+1) 2^-24 sum_c |w x| of the exact logits, the bound that holds
 for any two summation orders of the same rounded-or-fused products.  The
 shapes cover every kernel the dispatcher picks: eight-lane chains (few
-chains, rows not a multiple of 4 floats, unaligned device pointers), one lane
-per chain with 8/16/32/64 experts per wave and 1/2/4/8 tokens per lane, and
-the fast workgroup dot product.
+chains, rows not a multiple of 4 floats, unaligned device pointers), LDS tiles
+with 1x1, 2x2 and 4x4 chains per lane (partial tiles in tokens, experts and
+columns), and the fast workgroup dot product.
 """
 import numpy as np
 import pytest
@@ -54,8 +54,9 @@ def fast_bound(w, x):
     return 2.0 * (H + 1) * U / (1 - (H + 1) * U) * absdot + 1e-38
 
 
-# (T, E, H): chain8 decode shapes, rows not a multiple of 4 floats or 32
-# columns, then one-lane-per-chain grids with each expert width and tokens per lane
+# (T, E, H): chain-kernel decode shapes, rows not a multiple of 4 floats or 32
+# columns, then tiled grids with each register block (1x1: up to 256K chains,
+# 2x2: up to 1M, 4x4 beyond) and partial tiles
 EXACT_SHAPES = [
     (1, 8, 4096), (1, 128, 2048), (1, 256, 7168), (4, 8, 4096), (3, 60, 2880),
     (2, 7, 1001), (5, 3, 100), (1, 1, 1), (64, 256, 512),
