@@ -30,6 +30,14 @@
  *   nx_experts_*
  *       the load-time expert tensors of ModelWeights (src/engine/mod.rs:642),
  *       kept quantized and resident in HBM instead of dequantized to f32
+ *   nx_gguf_*
+ *       GgufReader::parse_file / parse_from_bytes, ModelMetadata::{get_tensor,
+ *       get_usize, get_f32, get_str, absolute_tensor_offset}
+ *                                            src/gguf/mod.rs:485-596, 869-900,
+ *                                            1091-1310
+ *   nx_experts_load_gguf
+ *       the tensor loop of InferenceEngine::new (src/engine/mod.rs:600-650)
+ *       for a block's expert tensors, without the f32 step or the 10M cap
  *   nx_device_count / nx_ctx_* / nx_sync / nx_mem_info
  *       Backend::{is_available, memory_info, synchronize}
  *                                            src/backend/mod.rs:74-96
@@ -55,6 +63,8 @@ extern "C" {
 #define NX_ERR_OOM 5         /* device allocation failed */
 #define NX_ERR_TRUNCATED 6   /* quantized payload shorter than its element count */
 #define NX_ERR_NO_ROUTES 7   /* router produced no route lists (k == 0, E == 0, ...) */
+#define NX_ERR_NOT_FOUND 8   /* named tensor or metadata key absent */
+#define NX_ERR_IO 9          /* file could not be opened or mapped */
 
 /* weight formats: GGUF tensor type ids (src/gguf/mod.rs:106-118) */
 #define NX_FMT_F32 0
@@ -162,6 +172,48 @@ int nx_experts_load(nx_ctx *ctx, nx_experts *ex, int expert, int role, const voi
 int nx_experts_info(const nx_experts *ex, int *fmt, int *num_experts, int *hidden, int *ff_dim,
                     int *shared_ff_dim, size_t *device_bytes);
 int nx_experts_destroy(nx_experts *ex);
+
+/* ---------------------------------------------------------------- GGUF */
+typedef struct nx_gguf nx_gguf;
+/* Q4_K code order of a file's payloads */
+#define NX_Q4K_REFERENCE 0 /* the reference's (element i<128: low nibble of byte i, else high
+                              nibble of byte i-128; src/quant/mod.rs:833-841) */
+#define NX_Q4K_GGML 1      /* upstream ggml's (per 64 elements: low nibbles, then high) */
+
+/* Memory-maps and parses a GGUF v2/v3 file as GgufReader::parse_file does
+ * (src/gguf/mod.rs:869-876, 1091-1310), with its error messages ("Invalid
+ * GGUF magic", "Unsupported GGUF version: 1", "Unexpected EOF reading ...",
+ * "Unknown value type: N", "Unknown data type: N", ...).  No GPU needed. */
+int nx_gguf_open(const char *path, nx_gguf **out);
+int nx_gguf_close(nx_gguf *g);
+/* data_offset: start of the tensor data (table end rounded up to alignment). */
+int nx_gguf_info(const nx_gguf *g, uint32_t *version, size_t *tensor_count, size_t *kv_count,
+                 size_t *alignment, uint64_t *data_offset);
+/* Tensor `index`: name, GGUF type id, dims (innermost first, up to dims_cap),
+ * absolute file offset and payload bytes (TensorInfo::data_size). */
+int nx_gguf_tensor(const nx_gguf *g, size_t index, char *name, size_t name_cap, uint32_t *type,
+                   uint32_t *n_dims, uint64_t *dims, size_t dims_cap, uint64_t *offset,
+                   uint64_t *bytes);
+/* NX_ERR_NOT_FOUND "Missing tensor: <name>" if absent. */
+int nx_gguf_find_tensor(const nx_gguf *g, const char *name, size_t *index);
+/* Pointer into the mapping; NX_ERR_TRUNCATED if the payload passes the file end. */
+int nx_gguf_tensor_data(const nx_gguf *g, size_t index, const void **data, uint64_t *bytes);
+/* ModelMetadata::get_usize (U64, U32, non-negative I64/I32), get_f32, get_str. */
+int nx_gguf_meta_usize(const nx_gguf *g, const char *key, uint64_t *value);
+int nx_gguf_meta_f32(const nx_gguf *g, const char *key, float *value);
+int nx_gguf_meta_str(const nx_gguf *g, const char *key, char *buf, size_t cap, size_t *len);
+/* The MoE expert tensors of block `layer`: merged blk.L.ffn_{gate,up,down}_exps
+ * ([H,F,E] / [F,H,E], innermost first) or one tensor per expert
+ * (blk.L.ffn_gate.e.weight, Mixtral-HF ...experts.e.w1/w3/w2, ...mlp.experts.e.
+ * {gate,up,down}_proj), plus a shared expert (blk.L.ffn_gate_shexp.weight, ...). */
+int nx_gguf_moe_info(const nx_gguf *g, int layer, int *fmt, int *num_experts, int *hidden,
+                     int *ff_dim, int *shared_ff_dim);
+/* Loads block `layer`'s experts into a new resident set, payloads kept
+ * quantized (no f32 copy); q4k_order says how the file orders Q4_K codes. */
+int nx_experts_load_gguf(nx_ctx *ctx, const nx_gguf *g, int layer, int q4k_order,
+                         nx_experts **out);
+/* Q4_K blocks from upstream ggml's code order to the reference's (host). */
+int nx_q4k_from_ggml(const void *src, void *dst, size_t blocks);
 
 /* ---------------------------------------------------------------- forward */
 /* The MoE layer for a batch: out[t] = sum_r w[t,r] * FFN_{e[t,r]}(x[t])

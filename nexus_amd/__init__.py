@@ -20,7 +20,8 @@ ROOT = os.path.dirname(_HERE)
 # status codes / enums (include/nexus_hip.h)
 NX_OK = 0
 NX_ERR_INVALID_ARG, NX_ERR_SHAPE, NX_ERR_UNSUPPORTED, NX_ERR_DEVICE = 1, 2, 3, 4
-NX_ERR_OOM, NX_ERR_TRUNCATED, NX_ERR_NO_ROUTES = 5, 6, 7
+NX_ERR_OOM, NX_ERR_TRUNCATED, NX_ERR_NO_ROUTES, NX_ERR_NOT_FOUND, NX_ERR_IO = 5, 6, 7, 8, 9
+Q4K_REFERENCE, Q4K_GGML = 0, 1
 F32, Q4_0, Q8_0, Q4_K = 0, 2, 8, 12
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 PATH_AUTO, PATH_GEMV, PATH_MFMA_F16, PATH_MFMA_BF16 = 0, 1, 2, 3
@@ -37,7 +38,10 @@ EXPORTS = [
     "nx_dequant_dev", "nx_quantize", "nx_quantize_dev", "nx_router_logits",
     "nx_router_logits_dev", "nx_route_topk", "nx_permute",
     "nx_experts_create", "nx_experts_add_shared", "nx_experts_load", "nx_experts_info",
-    "nx_experts_destroy", "nx_moe_forward", "nx_moe_forward_dev",
+    "nx_experts_destroy", "nx_moe_forward", "nx_moe_forward_dev", "nx_gguf_open",
+    "nx_gguf_close", "nx_gguf_info", "nx_gguf_tensor", "nx_gguf_find_tensor",
+    "nx_gguf_tensor_data", "nx_gguf_meta_usize", "nx_gguf_meta_f32", "nx_gguf_meta_str",
+    "nx_gguf_moe_info", "nx_experts_load_gguf", "nx_q4k_from_ggml",
 ]
 
 _lib = None
@@ -104,6 +108,24 @@ def lib():
         "nx_moe_forward_dev": ([_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp],
                                C.c_int),
     }
+    _u64p = C.POINTER(C.c_uint64)
+    _u32p = C.POINTER(C.c_uint32)
+    _szp = C.POINTER(C.c_size_t)
+    sig.update({
+        "nx_gguf_open": ([C.c_char_p, C.POINTER(_vp)], C.c_int),
+        "nx_gguf_close": ([_vp], C.c_int),
+        "nx_gguf_info": ([_vp, _u32p, _szp, _szp, _szp, _u64p], C.c_int),
+        "nx_gguf_tensor": ([_vp, C.c_size_t, C.c_char_p, C.c_size_t, _u32p, _u32p, _u64p,
+                            C.c_size_t, _u64p, _u64p], C.c_int),
+        "nx_gguf_find_tensor": ([_vp, C.c_char_p, _szp], C.c_int),
+        "nx_gguf_tensor_data": ([_vp, C.c_size_t, C.POINTER(_vp), _u64p], C.c_int),
+        "nx_gguf_meta_usize": ([_vp, C.c_char_p, _u64p], C.c_int),
+        "nx_gguf_meta_f32": ([_vp, C.c_char_p, _fp], C.c_int),
+        "nx_gguf_meta_str": ([_vp, C.c_char_p, C.c_char_p, C.c_size_t, _szp], C.c_int),
+        "nx_gguf_moe_info": ([_vp, C.c_int, _ip, _ip, _ip, _ip, _ip], C.c_int),
+        "nx_experts_load_gguf": ([_vp, _vp, C.c_int, C.c_int, C.POINTER(_vp)], C.c_int),
+        "nx_q4k_from_ggml": ([_vp, _vp, C.c_size_t], C.c_int),
+    })
     for name, (args, res) in sig.items():
         f = getattr(L, name)
         f.argtypes = args
@@ -325,3 +347,104 @@ class Experts:
                     out_ptr: int, score_mode: int = SCORE_SOFTMAX, path: int = PATH_AUTO):
         check(lib().nx_moe_forward_dev(self.ctx.h, self.h, _vp(x_ptr), _vp(logits_ptr),
                                        num_tokens, top_k, score_mode, path, _vp(out_ptr)))
+
+
+class Gguf:
+    """A memory-mapped GGUF file (GgufReader::parse_file).  No GPU needed."""
+
+    def __init__(self, path: str):
+        h = _vp()
+        check(lib().nx_gguf_open(os.fsencode(path), C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().nx_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def info(self) -> dict:
+        v, n, kv, al, off = C.c_uint32(), C.c_size_t(), C.c_size_t(), C.c_size_t(), C.c_uint64()
+        check(lib().nx_gguf_info(self.h, C.byref(v), C.byref(n), C.byref(kv), C.byref(al),
+                                 C.byref(off)))
+        return {"version": v.value, "tensor_count": n.value, "kv_count": kv.value,
+                "alignment": al.value, "data_offset": off.value}
+
+    def tensor(self, index: int) -> dict:
+        name = C.create_string_buffer(512)
+        t, nd, off, nb = C.c_uint32(), C.c_uint32(), C.c_uint64(), C.c_uint64()
+        dims = (C.c_uint64 * 8)()
+        check(lib().nx_gguf_tensor(self.h, index, name, 512, C.byref(t), C.byref(nd), dims, 8,
+                                   C.byref(off), C.byref(nb)))
+        return {"name": name.value.decode(), "type": t.value,
+                "dims": [dims[i] for i in range(min(nd.value, 8))], "offset": off.value,
+                "bytes": nb.value}
+
+    def tensors(self) -> list:
+        return [self.tensor(i) for i in range(self.info()["tensor_count"])]
+
+    def find(self, name: str) -> int:
+        i = C.c_size_t()
+        check(lib().nx_gguf_find_tensor(self.h, name.encode(), C.byref(i)))
+        return i.value
+
+    def data(self, index: int) -> np.ndarray:
+        """A copy of tensor `index`'s payload bytes."""
+        p, nb = _vp(), C.c_uint64()
+        check(lib().nx_gguf_tensor_data(self.h, index, C.byref(p), C.byref(nb)))
+        return np.frombuffer(C.string_at(p.value, nb.value), dtype=np.uint8).copy()
+
+    def meta_usize(self, key: str) -> int:
+        v = C.c_uint64()
+        check(lib().nx_gguf_meta_usize(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_f32(self, key: str) -> float:
+        v = C.c_float()
+        check(lib().nx_gguf_meta_f32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def meta_str(self, key: str) -> str:
+        n = C.c_size_t()
+        check(lib().nx_gguf_meta_str(self.h, key.encode(), None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value + 1)
+        check(lib().nx_gguf_meta_str(self.h, key.encode(), buf, n.value + 1, None))
+        return buf.raw[:n.value].decode()
+
+    def moe_info(self, layer: int) -> dict:
+        f, e, h, ff, fs = C.c_int(), C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        check(lib().nx_gguf_moe_info(self.h, layer, C.byref(f), C.byref(e), C.byref(h),
+                                     C.byref(ff), C.byref(fs)))
+        return {"fmt": f.value, "experts": e.value, "hidden": h.value, "ffn": ff.value,
+                "shared_ffn": fs.value}
+
+
+def q4k_from_ggml(blocks) -> np.ndarray:
+    """Q4_K blocks from upstream ggml's code order to the reference's."""
+    src = np.ascontiguousarray(blocks, dtype=np.uint8).ravel()
+    dst = np.empty_like(src)
+    check(lib().nx_q4k_from_ggml(_vp(src.ctypes.data), _vp(dst.ctypes.data), src.size // 144))
+    return dst
+
+
+def experts_from_gguf(ctx: Context, g: Gguf, layer: int, q4k_order: int = Q4K_REFERENCE):
+    """Block `layer`'s experts loaded quantized-resident from a GGUF file."""
+    h = _vp()
+    check(lib().nx_experts_load_gguf(ctx.h, g.h, layer, q4k_order, C.byref(h)))
+    info = g.moe_info(layer)
+    ex = Experts.__new__(Experts)
+    ex.h, ex.ctx = h, ctx
+    ex.fmt, ex.E, ex.H, ex.F = info["fmt"], info["experts"], info["hidden"], info["ffn"]
+    ex.Fs = info["shared_ffn"]
+    return ex
