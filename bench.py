@@ -12,8 +12,9 @@ so the weight bytes come from HBM.
 Extras in the same line (skipped with --no-extra): Mixtral decode at 32
 tokens, Mixtral Q8_0 prefill at 2048 tokens (MFMA grouped GEMM), the Qwen3
 (E=128, k=8) and DeepSeek (E=256, k=8, sigmoid, shared expert) shapes at
-their decode and batch token counts, and the router logits (exact and fast
-mode) for the three shapes.
+their decode and batch token counts, the router logits (exact and fast
+mode) for the three shapes, and the whole MoE block of a Mixtral decode step
+(RMSNorm, router logits, layer, residual add).
 
 Prints one JSON line (rank 0, N=1).  `value` = tokens/s of the whole layer.
 `roofline` is for the dominant kernel (the gate/up GEMV): algorithmic bytes
@@ -207,6 +208,30 @@ MODEL_CONFIGS = [
 ]
 
 
+def block_case(nx, ctx, torch, sets, x, E, H, k, args):
+    """The whole MoE block of a decode step (RMSNorm -> router logits -> MoE
+    layer -> residual add) on the Mixtral Q4_K sets, exact and fast mode."""
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed + 61)
+    norm_w = 1.0 + 0.1 * torch.randn(H, generator=g, device=dev, dtype=torch.float32)
+    router = torch.randn((E, H), generator=g, device=dev, dtype=torch.float32) * 0.02
+    hidden = x[:1].clone()
+    res = {}
+    for exact in (True, False):
+        def step(i, exact=exact):
+            sets[i % len(sets)].block_dev(hidden.data_ptr(), norm_w.data_ptr(), H, 1e-5,
+                                          router.data_ptr(), E * H, 1, k, path=nx.PATH_GEMV,
+                                          exact=exact)
+
+        ms = time_steps(torch, step, args.steps, args.warmup)
+        kern = kernel_means(ctx, torch, step, args.steps)
+        res["exact" if exact else "fast"] = {
+            "ms_per_step": ms, "tokens_per_s": 1 / (ms * 1e-3),
+            "kernels_ms": {k_: round(v, 4) for k_, v in kern.items()}}
+    return res
+
+
 ROUTER_SHAPES = [
     # name, E, H, token counts
     ("mixtral", 8, 4096, (1, 32, 2048)),
@@ -368,6 +393,9 @@ def main():
             "ms_per_step": ms32, "tokens_per_s": 32 / (ms32 * 1e-3),
             "effective_GBps": (gu32 + dn32) / (ms32 * 1e-3) / 1e9, "path": "auto",
             "kernels_ms": {k_: round(v, 4) for k_, v in kern32.items()}}
+    if not args.no_extra:
+        print("bench: MoE block, 1 token", file=sys.stderr, flush=True)
+        extra["moe_block_1_token"] = block_case(nx, ctx, torch, sets, x, E, H, k, args)
     for s_ in sets:
         s_.close()
     if not args.no_extra:

@@ -17,6 +17,12 @@
  *   nx_router_logits / nx_router_logits_dev
  *       InferenceEngine::matvec             src/engine/mod.rs:775-801
  *       applied to the router weight, one call per token
+ *   nx_rms_norm / nx_rms_norm_dev
+ *       kernel::rms_norm                    src/kernel/mod.rs:199-209
+ *   nx_moe_block / nx_moe_block_dev
+ *       the FFN half of a decode_with_cache layer (rms_norm, the FFN, the
+ *       residual add_inplace)               src/engine/mod.rs:1129-1142, 803-807
+ *       with the MoE layer (router matvec + dispatch_moe_ffn) as the FFN
  *   nx_route_topk
  *       InferenceEngine::route_moe_experts  src/engine/mod.rs:918-966
  *   nx_permute
@@ -142,6 +148,16 @@ int nx_router_logits(nx_ctx *ctx, const float *w_router, size_t w_len, const flo
 int nx_router_logits_dev(nx_ctx *ctx, const float *d_w_router, size_t w_len, const float *d_x,
                          size_t x_len, int num_tokens, int num_experts, int hidden, int exact,
                          float *d_logits);
+/* RMSNorm of T = num_tokens rows of H = hidden floats: out[t] = x[t] * rstd_t *
+ * w with rstd_t = 1 / sqrt(sum_i x[t][i]^2 / H + eps) (kernel::rms_norm,
+ * src/kernel/mod.rs:199-209).  exact != 0: the sum in the reference's order,
+ * output bit-identical; exact == 0: parallel sum.  NX_ERR_SHAPE "RMSNorm input
+ * shape mismatch: got <x_len>, expected <T*H>" or "RMSNorm weight too small:
+ * got <w_len>, expected at least <H>" (the reference panics on the latter). */
+int nx_rms_norm(nx_ctx *ctx, const float *x, size_t x_len, const float *weight, size_t w_len,
+                float eps, int num_tokens, int hidden, int exact, float *out);
+int nx_rms_norm_dev(nx_ctx *ctx, const float *d_x, size_t x_len, const float *d_weight,
+                    size_t w_len, float eps, int num_tokens, int hidden, int exact, float *d_out);
 /* Top-k routing of [num_tokens x num_experts] logits.  Outputs are
  * [num_tokens x top_k] (expert -1 / weight 0 padding) and counts[num_tokens].
  * *lists is the number of route lists produced (tokens whose logits lie
@@ -224,6 +240,19 @@ int nx_moe_forward(nx_ctx *ctx, const nx_experts *ex, const float *x, const floa
 int nx_moe_forward_dev(nx_ctx *ctx, const nx_experts *ex, const float *d_x,
                        const float *d_logits, int num_tokens, int top_k, int score_mode,
                        int path, float *d_out);
+
+/* One MoE block of a decoder layer, in place on hidden [T x H]:
+ *   normed = rms_norm(hidden, norm_w, eps); logits = W_r . normed;
+ *   hidden += MoE(normed, logits).
+ * exact != 0: rms_norm and the logits are bit-identical to the reference's,
+ * so routing is the reference's.  Errors as nx_rms_norm and nx_router_logits
+ * (router_len < E*H: "Matvec weight too small"), then nx_moe_forward. */
+int nx_moe_block(nx_ctx *ctx, const nx_experts *ex, float *hidden, const float *norm_w,
+                 size_t norm_len, float eps, const float *router_w, size_t router_len,
+                 int num_tokens, int top_k, int score_mode, int path, int exact);
+int nx_moe_block_dev(nx_ctx *ctx, const nx_experts *ex, float *d_hidden, const float *d_norm_w,
+                     size_t norm_len, float eps, const float *d_router_w, size_t router_len,
+                     int num_tokens, int top_k, int score_mode, int path, int exact);
 
 #ifdef __cplusplus
 }

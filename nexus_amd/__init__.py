@@ -41,7 +41,8 @@ EXPORTS = [
     "nx_experts_destroy", "nx_moe_forward", "nx_moe_forward_dev", "nx_gguf_open",
     "nx_gguf_close", "nx_gguf_info", "nx_gguf_tensor", "nx_gguf_find_tensor",
     "nx_gguf_tensor_data", "nx_gguf_meta_usize", "nx_gguf_meta_f32", "nx_gguf_meta_str",
-    "nx_gguf_moe_info", "nx_experts_load_gguf", "nx_q4k_from_ggml",
+    "nx_gguf_moe_info", "nx_experts_load_gguf", "nx_q4k_from_ggml", "nx_rms_norm",
+    "nx_rms_norm_dev", "nx_moe_block", "nx_moe_block_dev",
 ]
 
 _lib = None
@@ -125,6 +126,14 @@ def lib():
         "nx_gguf_moe_info": ([_vp, C.c_int, _ip, _ip, _ip, _ip, _ip], C.c_int),
         "nx_experts_load_gguf": ([_vp, _vp, C.c_int, C.c_int, C.POINTER(_vp)], C.c_int),
         "nx_q4k_from_ggml": ([_vp, _vp, C.c_size_t], C.c_int),
+        "nx_rms_norm": ([_vp, _fp, C.c_size_t, _fp, C.c_size_t, C.c_float, C.c_int, C.c_int,
+                         C.c_int, _fp], C.c_int),
+        "nx_rms_norm_dev": ([_vp, _vp, C.c_size_t, _vp, C.c_size_t, C.c_float, C.c_int, C.c_int,
+                             C.c_int, _vp], C.c_int),
+        "nx_moe_block": ([_vp, _vp, _fp, _fp, C.c_size_t, C.c_float, _fp, C.c_size_t, C.c_int,
+                          C.c_int, C.c_int, C.c_int, C.c_int], C.c_int),
+        "nx_moe_block_dev": ([_vp, _vp, _vp, _vp, C.c_size_t, C.c_float, _vp, C.c_size_t,
+                              C.c_int, C.c_int, C.c_int, C.c_int, C.c_int], C.c_int),
     })
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -265,6 +274,17 @@ class Context:
                                          num_tokens, num_experts, hidden, 1 if exact else 0,
                                          _vp(out_ptr)))
 
+    def rms_norm(self, x, weight, eps: float, exact: bool = True) -> np.ndarray:
+        """kernel::rms_norm (src/kernel/mod.rs:199-209) of each row of x [T x H]."""
+        x2 = _f32(x)
+        x2 = x2.reshape(-1, x2.shape[-1])
+        w = _f32(weight).ravel()
+        T, H = x2.shape
+        out = np.empty((max(T, 1), max(H, 1)), np.float32)
+        check(lib().nx_rms_norm(self.h, _p(x2, _fp), x2.size, _p(w, _fp), w.size, eps, T, H,
+                                1 if exact else 0, _p(out, _fp)))
+        return out[:T, :H]
+
     def route_topk(self, logits, num_tokens: int, num_experts: int, top_k: int,
                    score_mode: int = SCORE_SOFTMAX):
         lg = _f32(logits).ravel()
@@ -342,6 +362,26 @@ class Experts:
         check(lib().nx_moe_forward(self.ctx.h, self.h, _p(x, _fp), _p(lg, _fp), T, top_k,
                                    score_mode, path, _p(out, _fp)))
         return out[:T]
+
+    def block(self, hidden, norm_w, eps: float, router_w, top_k: int,
+              score_mode: int = SCORE_SOFTMAX, path: int = PATH_AUTO,
+              exact: bool = True) -> np.ndarray:
+        """One MoE block: hidden + MoE(rms_norm(hidden)) with on-device router logits."""
+        h = _f32(hidden).copy()
+        T = h.shape[0]
+        nw = _f32(norm_w).ravel()
+        rw = _f32(router_w).ravel()
+        check(lib().nx_moe_block(self.ctx.h, self.h, _p(h, _fp), _p(nw, _fp), nw.size, eps,
+                                 _p(rw, _fp), rw.size, T, top_k, score_mode, path,
+                                 1 if exact else 0))
+        return h
+
+    def block_dev(self, hidden_ptr: int, norm_ptr: int, norm_len: int, eps: float,
+                  router_ptr: int, router_len: int, num_tokens: int, top_k: int,
+                  score_mode: int = SCORE_SOFTMAX, path: int = PATH_AUTO, exact: bool = True):
+        check(lib().nx_moe_block_dev(self.ctx.h, self.h, _vp(hidden_ptr), _vp(norm_ptr),
+                                     norm_len, eps, _vp(router_ptr), router_len, num_tokens,
+                                     top_k, score_mode, path, 1 if exact else 0))
 
     def forward_dev(self, x_ptr: int, logits_ptr: int, num_tokens: int, top_k: int,
                     out_ptr: int, score_mode: int = SCORE_SOFTMAX, path: int = PATH_AUTO):

@@ -480,6 +480,52 @@ int nx_router_logits(nx_ctx *c, const float *w, size_t w_len, const float *x, si
   return NX_OK;
 }
 
+// kernel::rms_norm takes weight[i] for i < dim (a shorter weight panics there)
+static int check_norm(const float *x, size_t x_len, const float *w, size_t w_len, int T, int H,
+                      const float *out) {
+  if (T < 0 || H < 0) return fail(NX_ERR_INVALID_ARG, "negative size");
+  const size_t need_x = (size_t)T * H;
+  if (x_len != need_x)
+    return fail(NX_ERR_SHAPE, "RMSNorm input shape mismatch: got " + std::to_string(x_len) +
+                                  ", expected " + std::to_string(need_x));
+  if (w_len < (size_t)H)
+    return fail(NX_ERR_SHAPE, "RMSNorm weight too small: got " + std::to_string(w_len) +
+                                  ", expected at least " + std::to_string(H));
+  if (need_x * 4 > 0x7FFFFF00u) return fail(NX_ERR_UNSUPPORTED, "RMSNorm input over 2 GiB");
+  if (need_x > 0 && (!x || !w || !out)) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  return NX_OK;
+}
+
+int nx_rms_norm_dev(nx_ctx *c, const float *x, size_t x_len, const float *w, size_t w_len,
+                    float eps, int T, int H, int exact, float *out) {
+  NX_TRY(check_ctx(c));
+  NX_TRY(check_norm(x, x_len, w, w_len, T, H, out));
+  if (T == 0 || H == 0) return NX_OK;
+  if (!exact) return launch_rms_fast(c, x, w, eps, T, H, out);
+  float *d_s;
+  NX_TRY(ws(c, WS_SUMSQ, (size_t)T, &d_s));
+  NX_TRY(launch_sumsq_exact(c, x, T, H, d_s));
+  return launch_rms_apply(c, x, d_s, w, eps, T, H, out);
+}
+
+int nx_rms_norm(nx_ctx *c, const float *x, size_t x_len, const float *w, size_t w_len, float eps,
+                int T, int H, int exact, float *out) {
+  NX_TRY(check_ctx(c));
+  NX_TRY(check_norm(x, x_len, w, w_len, T, H, out));
+  if (T == 0 || H == 0) return NX_OK;
+  const size_t n = (size_t)T * H;
+  float *d_x, *d_w, *d_o;
+  NX_TRY(ws(c, WS_XIN, n, &d_x));
+  NX_TRY(ws(c, WS_NORM_W, (size_t)H, &d_w));
+  NX_TRY(ws(c, WS_OUT, n, &d_o));
+  NX_HIP(hipMemcpyAsync(d_x, x, n * 4, hipMemcpyHostToDevice, c->stream));
+  NX_HIP(hipMemcpyAsync(d_w, w, (size_t)H * 4, hipMemcpyHostToDevice, c->stream));
+  NX_TRY(nx_rms_norm_dev(c, d_x, n, d_w, (size_t)H, eps, T, H, exact, d_o));
+  NX_HIP(hipMemcpyAsync(out, d_o, n * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}
+
 int nx_permute(nx_ctx *c, const int32_t *experts, const int32_t *counts, int T, int k, int E,
                int32_t *ecount, int32_t *offsets, int32_t *ptok, int32_t *pslot, int32_t *inv) {
   NX_TRY(check_ctx(c));
@@ -641,6 +687,14 @@ int nx_experts_destroy(nx_experts *ex) {
 // ------------------------------------------------------------------- forward
 int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const float *d_logits,
                        int T, int k, int score_mode, int path, float *d_out) {
+  return moe_forward(c, ex, d_x, d_logits, T, k, score_mode, path, d_out, nullptr);
+}
+
+}  // extern "C"
+
+int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const float *d_logits,
+                    int T, int k, int score_mode, int path, float *d_out,
+                    const float *d_residual) {
   NX_TRY(check_ctx(c));
   if (!ex) return fail(NX_ERR_INVALID_ARG, "null expert set");
   if (ex->ctx != c) return fail(NX_ERR_INVALID_ARG, "expert set belongs to another context");
@@ -693,7 +747,7 @@ int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const 
     float *d_actv;
     NX_TRY(ws(c, WS_ACT, pairs_total * act_stride, &d_actv));
     GemvPlan gp{ex, T, k, d_x, d_pt, d_off, d_act, d_actv, act_stride, d_ypair,
-                d_w, d_cnt, d_inv, d_out};
+                d_w, d_cnt, d_inv, d_out, d_residual};
     NX_TRY(launch_gemv_gateup(c, gp));
     NX_TRY(launch_gemv_down(c, gp));
     return NX_OK;
@@ -728,9 +782,11 @@ int nx_moe_forward_dev(nx_ctx *c, const nx_experts *ex, const float *d_x, const 
   NX_TRY(launch_gemm_gateup(c, mp));
   NX_TRY(launch_gemm_down(c, mp));
   NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out, ksplit,
-                        pairs_total * (size_t)H));
+                        pairs_total * (size_t)H, d_residual));
   return NX_OK;
 }
+
+extern "C" {
 
 int nx_moe_forward(nx_ctx *c, const nx_experts *ex, const float *x, const float *logits, int T,
                    int k, int score_mode, int path, float *out) {
@@ -754,3 +810,52 @@ int nx_moe_forward(nx_ctx *c, const nx_experts *ex, const float *x, const float 
 }
 
 }  // extern "C"
+
+// One MoE block: normed = rms_norm(hidden), logits = W_r . normed,
+// hidden += MoE(normed, logits).  The FFN half of decode_with_cache
+// (src/engine/mod.rs:1129-1142) with the MoE layer in place of the dense FFN.
+int nx_moe_block_dev(nx_ctx *c, const nx_experts *ex, float *d_hidden, const float *d_norm_w,
+                     size_t norm_len, float eps, const float *d_router_w, size_t router_len,
+                     int T, int k, int score_mode, int path, int exact) {
+  NX_TRY(check_ctx(c));
+  if (!ex) return fail(NX_ERR_INVALID_ARG, "null expert set");
+  if (T < 0) return fail(NX_ERR_INVALID_ARG, "negative token count");
+  const int E = ex->E, H = ex->H;
+  const size_t n = (size_t)T * H;
+  NX_TRY(check_norm(d_hidden, n, d_norm_w, norm_len, T, H, d_hidden));
+  NX_TRY(check_logits(d_router_w, router_len, d_hidden, n, T, E, H, d_hidden));
+  if (T == 0) return NX_OK;
+  float *d_n, *d_l;
+  NX_TRY(ws(c, WS_NORMED, n, &d_n));
+  NX_TRY(ws(c, WS_BLK_LOGITS, (size_t)T * E, &d_l));
+  NX_TRY(nx_rms_norm_dev(c, d_hidden, n, d_norm_w, norm_len, eps, T, H, exact, d_n));
+  NX_TRY(launch_router_logits(c, d_router_w, d_n, T, E, H, exact != 0, d_l));
+  // the residual add (hidden + layer output, one rounding) happens in the
+  // combine's final write
+  return moe_forward(c, ex, d_n, d_l, T, k, score_mode, path, d_hidden, d_hidden);
+}
+
+int nx_moe_block(nx_ctx *c, const nx_experts *ex, float *hidden, const float *norm_w,
+                 size_t norm_len, float eps, const float *router_w, size_t router_len, int T,
+                 int k, int score_mode, int path, int exact) {
+  NX_TRY(check_ctx(c));
+  if (!ex) return fail(NX_ERR_INVALID_ARG, "null expert set");
+  if (T < 0) return fail(NX_ERR_INVALID_ARG, "negative token count");
+  const int E = ex->E, H = ex->H;
+  const size_t n = (size_t)T * H;
+  NX_TRY(check_norm(hidden, n, norm_w, norm_len, T, H, hidden));
+  NX_TRY(check_logits(router_w, router_len, hidden, n, T, E, H, hidden));
+  if (T == 0) return NX_OK;
+  float *d_h, *d_nw, *d_rw;
+  NX_TRY(ws(c, WS_BLK_HIDDEN, n, &d_h));
+  NX_TRY(ws(c, WS_NORM_W, (size_t)H, &d_nw));
+  NX_TRY(ws(c, WS_ROUTER_W, (size_t)E * H, &d_rw));
+  NX_HIP(hipMemcpyAsync(d_h, hidden, n * 4, hipMemcpyHostToDevice, c->stream));
+  NX_HIP(hipMemcpyAsync(d_nw, norm_w, (size_t)H * 4, hipMemcpyHostToDevice, c->stream));
+  NX_HIP(hipMemcpyAsync(d_rw, router_w, (size_t)E * H * 4, hipMemcpyHostToDevice, c->stream));
+  NX_TRY(nx_moe_block_dev(c, ex, d_h, d_nw, (size_t)H, eps, d_rw, (size_t)E * H, T, k, score_mode,
+                          path, exact));
+  NX_HIP(hipMemcpyAsync(hidden, d_h, n * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}

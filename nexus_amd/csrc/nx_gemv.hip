@@ -55,6 +55,7 @@ struct GemvArgs {
   const int32_t *rcnt;
   const int32_t *inv;
   float *final_out;
+  const float *residual;  // final_out = residual + combine when set
   int npairs;
   float *gpart;
 };
@@ -564,7 +565,8 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
       acc = acc + __fmul_rn(a.rw[(size_t)t * a.k + r], y(p));
     }
     if (a.has_shared) acc = acc + y(T * a.k + t);
-    a.final_out[(size_t)t * a.rows + rb0 + hl] = acc;
+    const size_t o = (size_t)t * a.rows + rb0 + hl;
+    a.final_out[o] = a.residual ? a.residual[o] + acc : acc;
   }
 }
 
@@ -751,13 +753,15 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
     const dim3 grid(gx, (unsigned)slots_max);
     NX_TRY(launch(c, "gemv_down",
                   [&] { hipLaunchKernelGGL(probe, grid, dim3(256), 0, c->stream, a); }));
-    return launch_combine(c, p.ypair, p.rw, p.rcnt, p.inv, p.T, p.k, ex->H, has_shared, p.out);
+    return launch_combine(c, p.ypair, p.rw, p.rcnt, p.inv, p.T, p.k, ex->H, has_shared, p.out, 1, 0,
+                          p.residual);
   }
 
   a.rw = p.rw;
   a.rcnt = p.rcnt;
   a.inv = p.inv;
   a.final_out = p.out;
+  a.residual = p.residual;
   a.npairs = (int)((long)p.T * p.k + (has_shared ? p.T : 0));
   const size_t part_bytes = (size_t)sh.ksplit * a.npairs * rows_per_wg * sizeof(float);
   const bool ylds = part_bytes <= kDownLdsMax;

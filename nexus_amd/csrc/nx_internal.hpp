@@ -124,6 +124,12 @@ enum WsSlot {
   WS_TILES,    // grouped-GEMM tile list
   WS_XH,       // half-precision copy of activations for the MFMA path
   WS_ROUTER_W, // device copy of the router weight for blocking calls
+  WS_NORMED,   // RMSNorm output of a block
+  WS_BLK_LOGITS,
+  WS_BLK_OUT,
+  WS_SUMSQ,
+  WS_NORM_W,   // device copy of the norm weight for blocking calls
+  WS_BLK_HIDDEN,
 };
 
 int ws_get(nx_ctx *c, int slot, size_t bytes, void **out);
@@ -167,11 +173,18 @@ int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, 
 // order with separately rounded products and sums
 int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, int E, int H,
                          bool exact, float *d_out);
+// per-row sequential sum of squares (rms_norm's variance sum, bit-exact)
+int launch_sumsq_exact(nx_ctx *c, const float *d_x, int T, int H, float *d_out);
+int launch_rms_apply(nx_ctx *c, const float *d_x, const float *d_sumsq, const float *d_w,
+                     float eps, int T, int H, float *d_out);
+int launch_rms_fast(nx_ctx *c, const float *d_x, const float *d_w, float eps, int T, int H,
+                    float *d_out);
 // out[t] = sum_r w[t,r] * y[pair(t,r)] (+ y[shared row t]); y is the sum of
-// nsplit partial buffers split_stride floats apart
+// nsplit partial buffers split_stride floats apart; with a residual,
+// out = residual + that sum (out may be the residual itself)
 int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
                    const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out,
-                   int nsplit = 1, size_t split_stride = 0);
+                   int nsplit = 1, size_t split_stride = 0, const float *d_residual = nullptr);
 
 struct GemvPlan {
   const nx_experts *ex;
@@ -188,6 +201,7 @@ struct GemvPlan {
   const int32_t *rcnt;
   const int32_t *inv;
   float *out;
+  const float *residual = nullptr;  // out = residual + layer output when set
 };
 int launch_gemv_gateup(nx_ctx *c, const GemvPlan &p);
 int launch_gemv_down(nx_ctx *c, const GemvPlan &p);
@@ -210,6 +224,10 @@ struct GemmPlan {
   size_t pairs_total;    // rows of act / ypair
   int ksplit;            // down pass K splits (ypair holds ksplit partial sums)
 };
+// the layer forward behind nx_moe_forward_dev; d_residual (optional) is added
+// to the output in the combine (d_out may equal d_residual)
+int moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const float *d_logits, int T,
+                int k, int score_mode, int path, float *d_out, const float *d_residual);
 int gemm_tile_m();
 int gemm_down_ksplit(int fmt, int F, int H, int tiles, int slots);
 // width of a row of GEMM operands (operand order pads to whole scale windows)

@@ -101,7 +101,9 @@ constexpr int C8_ROW = 36;  // floats per chain in the LDS product tile (32 + 4 
 // one loop trip to the next.  A stage holds, per group, the 64 lanes' four
 // weight and four input columns (lane l's 16 bytes at 16 l with 16-byte
 // loads; with 4-byte loads column i of lane l at 256 i + 4 l).
-template <bool VEC>
+// DIAG: chain t pairs row t of W with row t of X (E = 1), so W = X gives
+// the sequential sum of squares of each row (rms_norm's variance sum).
+template <bool VEC, bool DIAG = false>
 __global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__ W,
                                                       const float *__restrict__ X, int T, int E,
                                                       int H, float *__restrict__ out) {
@@ -124,10 +126,10 @@ __global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__
   const bool valid = chain < T * E;
   const int t = valid ? chain / E : 0;
   const int e = valid ? chain - t * E : 0;
-  const auto rw = make_rsrc(W, (uint32_t)((size_t)E * H * 4));
+  const auto rw = make_rsrc(W, (uint32_t)((size_t)(DIAG ? T : E) * H * 4));
   const auto rx = make_rsrc(X, (uint32_t)((size_t)T * H * 4));
   // lane's first column of every group (invalid chains read past the buffers)
-  const uint32_t wbase = valid ? (uint32_t)e * (uint32_t)H * 4u + 16u * j : OOB;
+  const uint32_t wbase = valid ? (uint32_t)(DIAG ? t : e) * (uint32_t)H * 4u + 16u * j : OOB;
   const uint32_t xbase = valid ? (uint32_t)t * (uint32_t)H * 4u + 16u * j : OOB;
   const int nk = (H + 32 * C8_G - 1) / (32 * C8_G);  // stages
   // ring slot S: weight (P = 0) or input (P = 1) columns
@@ -497,6 +499,18 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
       launch_tile<true>(c, rb, d_w, d_x, T, E, H, d_out);
     else
       launch_tile<false>(c, rb, d_w, d_x, T, E, H, d_out);
+  });
+}
+
+int launch_sumsq_exact(nx_ctx *c, const float *d_x, int T, int H, float *d_out) {
+  if (T <= 0) return NX_OK;
+  const bool vec = H % 4 == 0 && ((uintptr_t)d_x & 15) == 0;
+  const unsigned grid = (unsigned)((T + 7) / 8);
+  return launch(c, "rms_sumsq_chain8", [&] {
+    if (vec)
+      k_logits_chain8<true, true><<<grid, 128, 0, c->stream>>>(d_x, d_x, T, 1, H, d_out);
+    else
+      k_logits_chain8<false, true><<<grid, 128, 0, c->stream>>>(d_x, d_x, T, 1, H, d_out);
   });
 }
 

@@ -330,8 +330,8 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair
                                                  const float *__restrict__ rw,
                                                  const int32_t *__restrict__ rcnt,
                                                  const int32_t *__restrict__ inv, int T, int k,
-                                                 int H, int shared, float *__restrict__ out,
-                                                 int ns, size_t stride) {
+                                                 int H, int shared, float *out,
+                                                 int ns, size_t stride, const float *residual) {
   const size_t total = (size_t)T * H;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair
       acc = acc + __fmul_rn(rw[(size_t)t * k + r], y_at<NS>(ypair, stride, ns, (size_t)p * H + h));
     }
     if (shared) acc = acc + y_at<NS>(ypair, stride, ns, ((size_t)T * k + t) * H + h);
-    out[i] = acc;
+    out[i] = residual ? residual[i] + acc : acc;
   }
 }
 
@@ -410,7 +410,7 @@ int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, 
 
 int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
                    const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out,
-                   int nsplit, size_t split_stride) {
+                   int nsplit, size_t split_stride, const float *d_residual) {
   const size_t total = (size_t)T * H;
   if (total == 0) return NX_OK;
   size_t g = (total + 255) / 256;
@@ -418,11 +418,12 @@ int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const
   if (nsplit <= 1)
     return launch(c, "combine", [&] {
       k_combine<1><<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H,
-                                                       shared ? 1 : 0, d_out, 1, 0);
+                                                       shared ? 1 : 0, d_out, 1, 0, d_residual);
     });
   return launch(c, "combine", [&] {
     k_combine<0><<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H,
-                                                     shared ? 1 : 0, d_out, nsplit, split_stride);
+                                                     shared ? 1 : 0, d_out, nsplit, split_stride,
+                                                     d_residual);
   });
 }
 

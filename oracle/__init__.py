@@ -62,6 +62,7 @@ def lib():
         L.nxo_matvec.argtypes = [_fp, C.c_size_t, C.c_size_t, C.c_size_t, _fp, C.c_size_t, _fp,
                                  C.c_char_p, C.c_size_t]
         L.nxo_matvec.restype = C.c_int
+        L.nxo_rms_norm.argtypes = [_fp, _fp, C.c_size_t, C.c_float, _fp]
         L.nxo_dispatch_moe_ffn.argtypes = [_fp, C.c_size_t, _fp, C.c_size_t,
                                            C.POINTER(_fp), _szp, C.POINTER(_fp), _szp,
                                            C.POINTER(_fp), _szp, C.c_size_t, C.c_size_t,
@@ -176,6 +177,22 @@ def permute(experts, counts, num_experts: int):
 # --------------------------------------------------------------------------- engine
 class OracleError(RuntimeError):
     pass
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    """kernel::rms_norm (src/kernel/mod.rs:199-209) applied to each row of x."""
+    x2 = _f32(x)
+    x2 = x2.reshape(-1, x2.shape[-1]) if x2.ndim > 1 else x2.reshape(1, -1)
+    w = _f32(w).ravel()
+    H = x2.shape[1]
+    assert w.size >= H
+    out = np.empty_like(x2)
+    for t in range(x2.shape[0]):
+        row = np.ascontiguousarray(x2[t])
+        o = np.empty(H, np.float32)
+        lib().nxo_rms_norm(_p(row, _fp), _p(w, _fp), H, eps, _p(o, _fp))
+        out[t] = o
+    return out
 
 
 def matvec(w, rows: int, cols: int, x) -> np.ndarray:

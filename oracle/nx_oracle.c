@@ -481,6 +481,20 @@ size_t nxo_permute(const int32_t *experts, const int32_t *cpt, size_t T, size_t 
 }
 
 /* ------------------------------------------------------------------------ */
+/* rms_norm, src/kernel/mod.rs:199-209                                        */
+/* ------------------------------------------------------------------------ */
+/* variance = (x[0]^2 + x[1]^2 + ...) / dim summed left to right, every
+ * product and sum rounded to f32; rstd = 1 / sqrt(variance + eps) (both
+ * correctly rounded, as sqrtss and divss); out[i] = (x[i] * rstd) * w[i]. */
+void nxo_rms_norm(const float *x, const float *w, size_t dim, float eps, float *out) {
+    float s = 0.0f;
+    for (size_t i = 0; i < dim; ++i) s = s + x[i] * x[i];
+    const float variance = s / (float)dim;
+    const float rstd = 1.0f / sqrtf(variance + eps);
+    for (size_t i = 0; i < dim; ++i) out[i] = x[i] * rstd * w[i];
+}
+
+/* ------------------------------------------------------------------------ */
 /* matvec / dispatch, src/engine/mod.rs:775-801, 969-1024                    */
 /* ------------------------------------------------------------------------ */
 enum { NXO_OK = 0, NXO_E_ALIGN = 1, NXO_E_HIDDEN = 2, NXO_E_NOROUTE = 3, NXO_E_MV_IN = 4,

@@ -61,6 +61,9 @@ size_t nxo_permute(const int32_t *experts, const int32_t *counts_per_token, size
                    size_t top_k, size_t num_experts, int32_t *expert_counts, int32_t *offsets,
                    int32_t *perm_token, int32_t *perm_slot, int32_t *inv_pos);
 
+/* kernel::rms_norm (src/kernel/mod.rs:199-209) of one row of dim values. */
+void nxo_rms_norm(const float *x, const float *w, size_t dim, float eps, float *out);
+
 /* InferenceEngine::matvec (src/engine/mod.rs:775-801).  0 = ok, else an
  * error code whose message is written to err. */
 int nxo_matvec(const float *w, size_t w_len, size_t rows, size_t cols, const float *x,

@@ -285,3 +285,38 @@ def test_swiglu_with_swapped_operands_equals_dispatch(oracle):
 def test_cpu_matmul_known_answer(oracle):
     """src/backend/cpu.rs:234-241."""
     assert oracle.cpu_matmul([1, 2, 3, 4], [5, 6, 7, 8], 2, 2, 2).tolist() == [19, 22, 43, 50]
+
+
+# ----------------------------------------------------------------------------- rms_norm
+def test_rms_norm_reference_case(oracle):
+    # src/kernel/mod.rs:289-301
+    out = oracle.rms_norm([1.0, 2.0, 3.0, 4.0], [1.0, 1.0, 1.0, 1.0], 1e-5)[0]
+    scale = np.float32(1.0) / np.sqrt(np.float32(30.0) / np.float32(4.0))
+    assert out.shape == (4,)
+    assert np.all(np.abs(out - np.array([1, 2, 3, 4], np.float32) * scale) < 1e-5)
+
+
+def test_rms_norm_closed_form(oracle):
+    # x = 2: every square, partial sum and the mean are exact, rstd = 1/2
+    H = 1000
+    w = (np.arange(H, dtype=np.float32) - 300) / np.float32(7)
+    out = oracle.rms_norm(np.full(H, 2.0, np.float32), w, 0.0)[0]
+    np.testing.assert_array_equal(out, w)
+
+
+def test_rms_norm_sequential_order(oracle):
+    rng = np.random.default_rng(21)
+    H = 4096
+    x = (rng.standard_normal(H) * np.exp(rng.uniform(-6, 6, H))).astype(np.float32)
+    w = rng.standard_normal(H).astype(np.float32)
+    eps = np.float32(1e-5)
+    out = oracle.rms_norm(x, w, float(eps))[0]
+    s = np.float32(0.0)
+    for v in x:
+        s = np.float32(s + np.float32(v * v))
+    rstd = np.float32(1.0) / np.sqrt(np.float32(s / np.float32(H)) + eps)
+    np.testing.assert_array_equal(out, (x * rstd) * w)
+    # a pairwise float32 sum of the same squares rounds differently here
+    assert np.float32((x * x).sum(dtype=np.float32)) != s
+    ref64 = x.astype(np.float64) * w / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-5)
+    assert np.max(np.abs(out - ref64) / (np.abs(ref64) + 1e-30)) < 1e-3
