@@ -125,8 +125,22 @@ def cpu_baseline(nx, ctx, torch, x, logits, E, H, F, k, seed, ntok):
     for t in range(ntok):
         oracle.matvec(rw_h, E, H, xs_h[t])
     dtr = time.perf_counter() - t1
+    # kernel::swiglu_ffn (the reference's CPU kernel path) per routed (token,
+    # expert) on one core, and the whole batch row-parallel on every host core
+    t2 = time.perf_counter()
+    for t in range(ntok):
+        for e in ex_ids[t, :cnt[t]]:
+            e = int(e)
+            oracle.swiglu_ffn(xs_h[t], mats[1][e], mats[0][e], mats[2][e], H, F)
+    dts = time.perf_counter() - t2
+    ncores = oracle.default_threads()  # the box's CPU share for one GPU
+    t3 = time.perf_counter()
+    oracle.moe_layer(xs_h, lg_h, mats[0], mats[1], mats[2], k, nthreads=ncores)
+    dtp = time.perf_counter() - t3
     return {"value": ntok / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
             "router_matvec_us_per_token": dtr / ntok * 1e6,
+            "swiglu_ffn_1core_tokens_per_s": ntok / dts,
+            "row_parallel_tokens_per_s": ntok / dtp, "row_parallel_cores": ncores,
             "sample": f"{ntok} tokens of the same Mixtral Q4_K layer through the oracle's "
                       f"single-threaded dispatch_moe_ffn (f32 weights dequantized from the "
                       f"Q4_K payloads outside the timed region), {dt:.1f} s"}
