@@ -216,9 +216,10 @@ def prefill(nx, ctx, torch, args):
 
 
 MODEL_CONFIGS = [
-    # name, E, H, F, k, shared F, score mode, token counts, replicas rotated
-    ("qwen3_q4k", 128, 2048, 768, 8, 0, 0, (1, 64, 512), 2),
-    ("deepseek_q4k_sigmoid_shared", 256, 7168, 2048, 8, 2048, 1, (1, 4096), 2),
+    # name, weight format, E, H, F, k, shared F, score mode, token counts, replicas rotated
+    ("qwen3_q4k", "Q4_K", 128, 2048, 768, 8, 0, 0, (1, 64, 512), 2),
+    ("deepseek_q4k_sigmoid_shared", "Q4_K", 256, 7168, 2048, 8, 2048, 1, (1, 4096), 2),
+    ("mixtral_q2k", "Q2_K", 8, 4096, 14336, 2, 0, 0, (1,), 4),
 ]
 
 
@@ -294,9 +295,14 @@ def model_config_cases(nx, ctx, torch, args):
     that decode steps read HBM rather than the Infinity Cache."""
     dev = torch.device("cuda", 0)
     res = {}
-    for name, E, H, F, k, Fs, score, tokens, reps in MODEL_CONFIGS:
+    for name, fname, E, H, F, k, Fs, score, tokens, reps in MODEL_CONFIGS:
         print(f"bench: {name}", file=sys.stderr, flush=True)
-        sets = make_expert_sets(nx, ctx, torch, nx.Q4_K, E, H, F, reps, args.seed + 31, Fs)
+        fmt = {"Q4_K": nx.Q4_K, "Q2_K": nx.Q2_K}[fname]
+        # GGUF bytes per weight; Q2_K stays resident with its codes widened
+        # to 4 bits (0.625 B/weight read per step)
+        bpw = {"Q4_K": Q4K_BYTES_PER_WEIGHT, "Q2_K": 84.0 / 256.0}[fname]
+        rbpw = {"Q4_K": Q4K_BYTES_PER_WEIGHT, "Q2_K": 0.625}[fname]
+        sets = make_expert_sets(nx, ctx, torch, fmt, E, H, F, reps, args.seed + 31, Fs)
         g = torch.Generator(device=dev)
         g.manual_seed(args.seed + 41)
         Tm = max(tokens)
@@ -308,8 +314,8 @@ def model_config_cases(nx, ctx, torch, args):
         for T in tokens:
             counts = active_experts(ctx, logits[:T].cpu().numpy(), T, E, k, score)
             n_act = sum(1 for c in counts if c) + (1 if Fs else 0)
-            wbytes = (sum(1 for c in counts if c) * 3 * H * F + (3 * H * Fs if Fs else 0)) \
-                * Q4K_BYTES_PER_WEIGHT
+            welems = sum(1 for c in counts if c) * 3 * H * F + (3 * H * Fs if Fs else 0)
+            wbytes = welems * bpw
             flops = 2.0 * 3 * H * F * sum(counts) + (2.0 * 3 * H * Fs * T if Fs else 0.0)
 
             def step(i, T=T):
@@ -326,13 +332,14 @@ def model_config_cases(nx, ctx, torch, args):
                 "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
                 "experts_active": n_act, "weight_bytes": wbytes, "flops": flops,
                 "effective_GBps": gbps, "hbm_frac": gbps / HBM_PEAK_GBPS,
+                "resident_GBps": welems * rbpw / (ms * 1e-3) / 1e9,
                 "TFLOPs": tf, "mfma_f16_frac": tf / MFMA_F16_PEAK_TFLOPS,
                 "path": "mfma_f16" if any(n.startswith("gemm") for n in kern) else "gemv",
                 "kernels_ms": {k_: round(v, 4) for k_, v in kern.items()}}
         for s_ in sets:
             s_.close()
         res[name] = {"experts": E, "hidden": H, "ffn": F, "top_k": k, "shared_ffn": Fs,
-                     "score": "sigmoid" if score else "softmax", "weights": "Q4_K",
+                     "score": "sigmoid" if score else "softmax", "weights": fname,
                      "replicas_rotated": reps, "cases": cases}
     return res
 

@@ -77,6 +77,7 @@ extern "C" {
 #define NX_FMT_Q4_0 2
 #define NX_FMT_Q8_0 8
 #define NX_FMT_Q4_K 12
+#define NX_FMT_Q2_K 10 /* GEMV path only (decode); dequant/quantize bit-exact */
 
 /* router score modes */
 #define NX_SCORE_SOFTMAX 0 /* reference: softmax over the selected top-k logits */

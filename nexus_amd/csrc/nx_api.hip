@@ -28,6 +28,8 @@ bool format_info(int fmt, FormatInfo *fi) {
   case NX_FMT_Q4_K: *fi = {fmt, 256, 144, 128, 16}; return true;
   case NX_FMT_Q8_0: *fi = {fmt, 32, 34, 32, 2}; return true;
   case NX_FMT_Q4_0: *fi = {fmt, 32, 18, 16, 2}; return true;
+  // resident Q2_K: codes widened to 4 bits, 8 scale-plane bytes per segment
+  case NX_FMT_Q2_K: *fi = {fmt, 256, 84, 128, 32}; return true;
   case NX_FMT_F32: *fi = {fmt, 4, 16, 16, 0}; return true;
   }
   return false;
@@ -38,6 +40,7 @@ static const char *fmt_name(int fmt) {
   case NX_FMT_Q4_K: return "Q4_K";
   case NX_FMT_Q8_0: return "Q8_0";
   case NX_FMT_Q4_0: return "Q4_0";
+  case NX_FMT_Q2_K: return "Q2_K";
   case NX_FMT_F32: return "F32";
   }
   return "?";
@@ -48,6 +51,7 @@ static size_t gguf_bytes(int fmt, size_t n) {
   case NX_FMT_Q4_K: return (n + 255) / 256 * 144;
   case NX_FMT_Q8_0: return (n + 31) / 32 * 34;
   case NX_FMT_Q4_0: return (n + 31) / 32 * 18;
+  case NX_FMT_Q2_K: return (n + 255) / 256 * 84;
   case NX_FMT_F32: return n * 4;
   }
   return 0;
@@ -176,6 +180,10 @@ static int init_plane(nx_experts *ex, RolePlane &pl, int count, int rows, int co
   case NX_FMT_Q4_0:
     pl.nseg = (cols / 32 + 1) / 2;
     pl.row_meta = (uint32_t)(pl.nseg * 4);
+    break;
+  case NX_FMT_Q2_K:
+    pl.nseg = cols / 256 * 4;
+    pl.row_meta = (uint32_t)(pl.nseg * 8);
     break;
   default:  // F32
     pl.nseg = (cols + 7) / 8;
@@ -725,6 +733,11 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   NX_TRY(ws(c, WS_ACTIVE, (size_t)E + 1, &d_act));
 
   int use = path;
+  if (ex->fmt == NX_FMT_Q2_K) {  // no MFMA operand path for Q2_K
+    if (use == NX_PATH_MFMA_F16 || use == NX_PATH_MFMA_BF16)
+      return fail(NX_ERR_UNSUPPORTED, "Q2_K experts run on the GEMV path only");
+    use = NX_PATH_GEMV;
+  }
   if (use == NX_PATH_AUTO) {
     // MFMA once experts see enough tokens on average to amortize the tile
     // dequantization; below that the GEMV streams each weight fewer times

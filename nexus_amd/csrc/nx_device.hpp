@@ -246,6 +246,75 @@ __device__ __forceinline__ void prep4(const float *x, X4 &o) {
   planes4(x + 32, sc, o.p[1]);
 }
 
+// activations of one 64-element Q2_K segment: the digit planes of its two
+// 32-element halves plus the sum of each 16-element sub-block
+struct X2 {
+  uint32_t p[2][6][4];
+  float post;
+  float s[4];
+};
+
+__device__ __forceinline__ void prep2(const float *x, X2 &o) {
+  float a = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float su = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) su += x[16 * u + i];
+    o.s[u] = su;
+    a += su;
+  }
+  const int e = blk_exp(abs_max(x, 64));
+  const float sc = __builtin_amdgcn_ldexpf(1.0f, 22 - e);
+  o.post = fabsf(a) <= 3.4e38f ? __builtin_amdgcn_ldexpf(1.0f, e - 22) : __builtin_nanf("");
+  planes4(x, sc, o.p[0]);
+  planes4(x + 32, sc, o.p[1]);
+}
+
+// quarter q of a Q2_K segment = its sub-block q (dwords 2(q&1), 2(q&1)+1 of
+// half q>>1)
+__device__ __forceinline__ void prep2_quarter(const float *x, int q, X2 *o) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s += x[i];
+  const float sp = quad_pair_sum(s);
+  const float sa = sp + quad_swap_halves(sp);
+  const int e = blk_exp(quad_max(abs_max(x, 16)));
+  const float sc = __builtin_amdgcn_ldexpf(1.0f, 22 - e);
+  const int h = q >> 1, k0 = (q & 1) * 2;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    uint32_t pd[6];
+    plane4_dword(x + 8 * kk, sc, pd);
+#pragma unroll
+    for (int d = 0; d < 6; ++d) o->p[h][d][k0 + kk] = pd[d];
+  }
+  o->s[q] = s;
+  if (q == 0)
+    o->post = fabsf(sa) <= 3.4e38f ? __builtin_amdgcn_ldexpf(1.0f, e - 22) : __builtin_nanf("");
+}
+
+// sum_i c_i X_i over the two 16-element sub-blocks of a 4-bit code half:
+// dwords 0-1 (first) and 2-3 (second)
+__device__ __forceinline__ void sumcx4_split(const uint4 &w, const uint32_t (&p)[6][4], float &f0,
+                                             float &f1) {
+  const int ws[4] = {(int)w.x, (int)w.y, (int)w.z, (int)w.w};
+  int32_t a0 = 0, a1 = 0;
+#pragma unroll
+  for (int d = 5; d >= 0; --d) {
+    if (d < 5) {
+      a0 = (int32_t)((uint32_t)a0 << 4);
+      a1 = (int32_t)((uint32_t)a1 << 4);
+    }
+    a0 = __builtin_amdgcn_sdot8(ws[0], (int)p[d][0], a0, false);
+    a0 = __builtin_amdgcn_sdot8(ws[1], (int)p[d][1], a0, false);
+    a1 = __builtin_amdgcn_sdot8(ws[2], (int)p[d][2], a1, false);
+    a1 = __builtin_amdgcn_sdot8(ws[3], (int)p[d][3], a1, false);
+  }
+  f0 = (float)a0;
+  f1 = (float)a1;
+}
+
 template <int FMT>
 struct Seg;
 
@@ -400,6 +469,56 @@ struct Seg<NX_FMT_Q4_0> {
       const float fa = sumcx4(q0, xv[t].p[0], run[t]);
       const float fb = sumcx4(q1, xv[t].p[1], run[t]);
       acc[t] += fmaf(d0, fa, d1 * fb) * xv[t].post;
+    }
+  }
+};
+
+// Q2_K (src/quant/mod.rs:913-937): resident codes are the 2-bit q of a
+// 64-element segment (block j/4, elements 64(j%4) ..) widened to 4-bit
+// nibbles in the 4-bit dword order (non-negative, so no offset); the scale
+// plane holds per segment {f16 d, f16 dmin, the four scale/min bytes}.
+// w = d*sc*q - dmin*m per 16-element sub-block u:
+//   sum w*x = d*sc_u * sum q x - dmin*m_u * sum x
+template <>
+struct Seg<NX_FMT_Q2_K> {
+  static constexpr int EPS = 64;
+  using Meta = uint2;
+  using X = X2;
+  using Run = Run4;
+  __device__ __forceinline__ static int xidx(int j, int v) {
+    return (j >> 2) * 256 + (j & 3) * 64 + v;
+  }
+  __device__ __forceinline__ static uint32_t meta_off(int j, bool valid) {
+    return valid ? (uint32_t)(j * 8) : OOB;
+  }
+  __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    return make_uint2(v[0], v[1]);
+  }
+  __device__ __forceinline__ static void prep(const float *x, X &o) { prep2(x, o); }
+  __device__ __forceinline__ static void prep_quarter(const float *x, int q, X *o) {
+    prep2_quarter(x, q, o);
+  }
+  template <int NT>
+  __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m, int,
+                                             const X *xv, Run *, float *acc) {
+    const float d = h2f(m.x & 0xFFFFu), dmin = h2f(m.x >> 16);
+    float ds[4], dm[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t b = (m.y >> (8 * u)) & 0xFFu;
+      ds[u] = d * (float)(b & 15u);
+      dm[u] = dmin * (float)(b >> 4);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float f[4];
+      sumcx4_split(q0, xv[t].p[0], f[0], f[1]);
+      sumcx4_split(q1, xv[t].p[1], f[2], f[3]);
+      const float cx = fmaf(ds[0], f[0], fmaf(ds[1], f[1], fmaf(ds[2], f[2], ds[3] * f[3])));
+      const float mx = fmaf(dm[0], xv[t].s[0], fmaf(dm[1], xv[t].s[1],
+                                                     fmaf(dm[2], xv[t].s[2], dm[3] * xv[t].s[3])));
+      acc[t] += cx * xv[t].post - mx;
     }
   }
 };

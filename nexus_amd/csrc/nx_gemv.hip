@@ -617,6 +617,7 @@ KernelFn pick(int fmt, int gateup, bool ylds, int nt, const Shape &s) {
   case NX_FMT_Q4_K: return pick_fmt<NX_FMT_Q4_K>(gateup, ylds, nt, s);
   case NX_FMT_Q8_0: return pick_fmt<NX_FMT_Q8_0>(gateup, ylds, nt, s);
   case NX_FMT_Q4_0: return pick_fmt<NX_FMT_Q4_0>(gateup, ylds, nt, s);
+  case NX_FMT_Q2_K: return pick_fmt<NX_FMT_Q2_K>(gateup, ylds, nt, s);
   case NX_FMT_F32: return pick_fmt<NX_FMT_F32>(gateup, ylds, nt, s);
   }
   return nullptr;
@@ -627,6 +628,7 @@ int elems_per_segment(int fmt) {
   case NX_FMT_Q4_K: return 64;
   case NX_FMT_Q8_0: return 32;
   case NX_FMT_Q4_0: return 64;
+  case NX_FMT_Q2_K: return 64;
   default: return 8;
   }
 }

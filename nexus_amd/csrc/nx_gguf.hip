@@ -507,7 +507,8 @@ const nx_gguf::Tensor *find_any(const nx_gguf *g, const std::vector<std::string>
 }
 
 bool supported_fmt(uint32_t type) {
-  return type == NX_FMT_F32 || type == NX_FMT_Q4_0 || type == NX_FMT_Q8_0 || type == NX_FMT_Q4_K;
+  return type == NX_FMT_F32 || type == NX_FMT_Q4_0 || type == NX_FMT_Q8_0 || type == NX_FMT_Q4_K ||
+         type == NX_FMT_Q2_K;
 }
 
 // expert tensors of block `layer`: merged blk.L.ffn_{gate,up,down}_exps
@@ -555,7 +556,7 @@ int moe_layout(const nx_gguf *g, int layer, RoleTensor role[3], int *E, int *H, 
     return fail(NX_ERR_SHAPE, "expert matrix shapes of block " + L + " are inconsistent");
   if (!supported_fmt(tg.type))
     return fail(NX_ERR_UNSUPPORTED, "expert tensor type " + std::to_string(tg.type) +
-                                        " is not resident-capable (F32, Q4_0, Q8_0, Q4_K)");
+                                        " is not resident-capable (F32, Q4_0, Q8_0, Q4_K, Q2_K)");
   if (e_count <= 0 || h > 0x7FFFFFFF || f > 0x7FFFFFFF)
     return fail(NX_ERR_SHAPE, "no experts in block " + L);
   *E = e_count;

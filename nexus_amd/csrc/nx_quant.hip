@@ -2,11 +2,11 @@
 // a device restatement of the reference quantizer, and the repack of GGUF
 // payloads into the resident split code/scale planes.
 //
-// Dequantization (src/gguf/mod.rs:962-1056 == src/quant/mod.rs:689-849):
+// Dequantization (src/gguf/mod.rs:962-1088 == src/quant/mod.rs:689-937):
 // every decoded value is an exact product (Q8_0 q*d, Q4_0 (q-8)*d) or the
-// single rounding of the difference of two exact products (Q4_K d*sc*q -
-// dmin*m), so the device result is bit-identical to the reference whatever
-// the contraction.  Quantization (src/quant/mod.rs:669-818) uses IEEE
+// single rounding of the difference of two exact products (Q4_K and Q2_K
+// d*sc*q - dmin*m), so the device result is bit-identical to the reference
+// whatever the contraction.  Quantization (src/quant/mod.rs:669-818) uses IEEE
 // division, roundf (half away from zero), minNum/maxNum and hardware RNE f16
 // conversion; contraction is switched off so each expression rounds as the
 // Rust f32 expression does.
@@ -36,6 +36,12 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ src
       const int j = (int)(i % 32);
       const int q = j < 16 ? (b[2 + j] & 15) : (b[2 + j - 16] >> 4);
       v = (float)(q - 8) * ld_f16(b);
+    } else if constexpr (FMT == NX_FMT_Q2_K) {  // src/quant/mod.rs:913-937
+      const uint8_t *b = src + (i / 256) * 84;
+      const int j = (int)(i % 256);
+      const uint32_t q = (b[16 + j / 4] >> (2 * (j % 4))) & 3u;
+      const uint32_t packed = b[j / 16];
+      v = ld_f16(b + 80) * (float)(packed & 15u) * (float)q - ld_f16(b + 82) * (float)(packed >> 4);
     } else {  // Q4_K
       const uint8_t *b = src + (i / 256) * 144;
       const int j = (int)(i % 256);
@@ -210,6 +216,75 @@ __global__ __launch_bounds__(256) void k_quant_q4k(const float *__restrict__ src
   }
 }
 
+__device__ __forceinline__ uint8_t quantize_u4(float value, float scale) {
+  if (scale > 0.0f && value > 0.0f) return sat_u8(clampf(roundf(value / scale), 1.0f, 15.0f));
+  return 0;
+}
+__device__ __forceinline__ uint8_t q2k_value(float value, float d, float dmin, uint32_t sq,
+                                             uint32_t mq) {
+  const float scale = d * (float)sq;
+  const float offset = dmin * (float)mq;
+  if (scale > 0.0f) return sat_u8(clampf(roundf((value + offset) / scale), 0.0f, 3.0f));
+  return 0;
+}
+
+// Q2_K (src/quant/mod.rs:851-911): sixteen lanes per 256-element block; lane
+// u owns sub-block u (16 values): its statistics, its scale/min byte and the
+// four code bytes of its values.
+__global__ __launch_bounds__(256) void k_quant_q2k(const float *__restrict__ src, size_t n,
+                                                   uint8_t *__restrict__ dst) {
+  const size_t nb = (n + 255) / 256;
+  const int u = threadIdx.x & 15;
+  const int lane = threadIdx.x & 63;
+  // each wave owns 4 consecutive blocks per step; the loop bound is uniform
+  // across the wave so the shuffles below always see all sixteen lanes
+  const size_t wave_id = blockIdx.x * (size_t)(blockDim.x / 64) + (threadIdx.x >> 6);
+  const size_t wave_stride = (size_t)gridDim.x * (blockDim.x / 64) * 4;
+  for (size_t wb = wave_id * 4; wb < nb; wb += wave_stride) {
+    const size_t b = wb + (size_t)(lane >> 4);
+    const bool live = b < nb;
+    const size_t base = b * 256;
+    auto val = [&](int i) -> float {
+      const size_t idx = base + (size_t)i;
+      return (live && idx < n) ? src[idx] : 0.0f;
+    };
+    float mn = INFINITY, mx = -INFINITY;
+    for (int i = 0; i < 16; ++i) mn = fminf(mn, val(u * 16 + i));
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, val(u * 16 + i));
+    const float offset = mn < 0.0f ? -mn : 0.0f;
+    const float scale = fmaxf((mx + offset) / 3.0f, 0.0f);
+    // neither value can be NaN, so the fold order of max does not matter
+    float max_scale = scale, max_offset = offset;
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+      max_scale = fmaxf(max_scale, __shfl_xor(max_scale, m, 64));
+      max_offset = fmaxf(max_offset, __shfl_xor(max_offset, m, 64));
+    }
+    max_scale = fmaxf(0.0f, max_scale);
+    max_offset = fmaxf(0.0f, max_offset);
+    const float d = max_scale > 0.0f ? max_scale / 15.0f : 0.0f;
+    const float dmin = max_offset > 0.0f ? max_offset / 15.0f : 0.0f;
+    const uint32_t sq = quantize_u4(scale, d) & 15u;
+    const uint32_t mq = quantize_u4(offset, dmin) & 15u;
+    if (live) {
+      uint8_t *o = dst + b * 84;
+      o[u] = (uint8_t)(sq | (mq << 4));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t byte = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          byte |= (uint32_t)(q2k_value(val(u * 16 + 4 * k + i), d, dmin, sq, mq) & 3u) << (2 * i);
+        o[16 + 4 * u + k] = (uint8_t)byte;
+      }
+      if (u == 0) {
+        st_f16(o + 80, d);
+        st_f16(o + 82, dmin);
+      }
+    }
+  }
+}
+
 #pragma clang fp contract(on)
 
 // ---------------------------------------------------------------- repack
@@ -251,6 +326,15 @@ __global__ __launch_bounds__(256) void k_repack_codes(const uint8_t *__restrict_
         const uint8_t *b = src + ((size_t)r * nb + (j >> 2)) * 144 + 16 + (j & 3) * 32;
 #pragma unroll
         for (int i = 0; i < 32; ++i) q[i] = h ? (b[i] >> 4) : (b[i] & 15);
+      } else if constexpr (FMT == NX_FMT_Q2_K) {
+        // segment j = block j/4, elements 64(j%4) + 32h + i; element e of a
+        // block sits in bits 2(e%4) of qs byte e/4.  Codes stay non-negative
+        // (stored as q, not q ^ 8: the dot needs no offset).
+        const int nb = cols / 256;
+        const uint8_t *b = src + ((size_t)r * nb + (j >> 2)) * 84 + 16;
+        const int e0 = (j & 3) * 64 + 32 * h;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) q[i] = ((b[(e0 + i) / 4] >> (2 * ((e0 + i) % 4))) & 3) ^ 8;
       } else {  // Q4_0: segment j = blocks 2j, 2j+1; byte i: element i (low), 16 + i (high)
         const int nb = cols / 32;
         const int blk = 2 * j + h;
@@ -293,6 +377,25 @@ __global__ __launch_bounds__(256) void k_repack_meta(const uint8_t *__restrict__
   }
 }
 
+// Q2_K scale plane: per segment j (block j/4, sub-blocks 4(j%4) ..) the
+// eight bytes {d, dmin, four scale/min bytes}
+__global__ __launch_bounds__(256) void k_repack_meta_q2k(const uint8_t *__restrict__ src, int rows,
+                                                         int cols, int nseg, uint32_t row_meta,
+                                                         uint8_t *__restrict__ meta) {
+  const int nb = cols / 256;
+  const size_t total = (size_t)rows * nseg;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int r = (int)(i / nseg), j = (int)(i - (size_t)r * nseg);
+    uint8_t *dst = meta + (size_t)r * row_meta + (size_t)j * 8;
+    const uint8_t *b = src + ((size_t)r * nb + (j >> 2)) * 84;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dst[v] = b[80 + v];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) dst[4 + v] = b[(j & 3) * 4 + v];
+  }
+}
+
 unsigned grid_for(size_t items, unsigned per_block) {
   size_t g = (items + per_block - 1) / per_block;
   if (g < 1) g = 1;
@@ -313,6 +416,8 @@ int launch_dequant(nx_ctx *c, int fmt, const void *d_src, size_t n, float *d_dst
     return launch(c, "dequant_q4_0", [&] { k_dequant<NX_FMT_Q4_0><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
   case NX_FMT_Q4_K:
     return launch(c, "dequant_q4_k", [&] { k_dequant<NX_FMT_Q4_K><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
+  case NX_FMT_Q2_K:
+    return launch(c, "dequant_q2_k", [&] { k_dequant<NX_FMT_Q2_K><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
   case NX_FMT_F32:
     NX_HIP(hipMemcpyAsync(d_dst, d_src, n * 4, hipMemcpyDeviceToDevice, c->stream));
     return NX_OK;
@@ -335,6 +440,10 @@ int launch_quantize(nx_ctx *c, int fmt, const float *d_src, size_t n, void *d_ds
   case NX_FMT_Q4_K: {
     const unsigned g = grid_for((n + 255) / 256, 32);
     return launch(c, "quantize_q4_k", [&] { k_quant_q4k<<<g, 256, 0, c->stream>>>(d_src, n, d); });
+  }
+  case NX_FMT_Q2_K: {
+    const unsigned g = grid_for((n + 255) / 256, 16);
+    return launch(c, "quantize_q2_k", [&] { k_quant_q2k<<<g, 256, 0, c->stream>>>(d_src, n, d); });
   }
   case NX_FMT_F32:
     NX_HIP(hipMemcpyAsync(d_dst, d_src, n * 4, hipMemcpyDeviceToDevice, c->stream));
@@ -365,6 +474,16 @@ int launch_repack(nx_ctx *c, int fmt, const void *d_src, const RolePlane &pl, ui
   case NX_FMT_Q8_0: NX_RP(NX_FMT_Q8_0, "repack_q8_0");
   case NX_FMT_Q4_0: NX_RP(NX_FMT_Q4_0, "repack_q4_0");
   case NX_FMT_F32: NX_RP(NX_FMT_F32, "repack_f32");
+  case NX_FMT_Q2_K: {
+    NX_TRY(launch(c, "repack_q2_k", [&] {
+      k_repack_codes<NX_FMT_Q2_K><<<gc, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg,
+                                                            pl.row_qs, qs);
+    }));
+    const unsigned g2 = grid_for((size_t)pl.rows * pl.nseg, 256);
+    return launch(c, "repack_q2_k", [&] {
+      k_repack_meta_q2k<<<g2, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_meta, meta);
+    });
+  }
   }
 #undef NX_RP
   return fail(NX_ERR_INVALID_ARG, "unknown weight format");

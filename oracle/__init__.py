@@ -19,8 +19,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 _lib = None
 
-F32, Q4_0, Q8_0, Q4_K = 0, 2, 8, 12
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144)}
+F32, Q4_0, Q8_0, Q4_K, Q2_K = 0, 2, 8, 12, 10
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q2_K: (256, 84)}
 
 _fp = C.POINTER(C.c_float)
 _u8p = C.POINTER(C.c_uint8)

@@ -33,6 +33,7 @@
 #define GGUF_Q4_0 2
 #define GGUF_Q8_0 8
 #define GGUF_Q4_K 12
+#define GGUF_Q2_K 10
 
 /* ------------------------------------------------------------------------ */
 /* parallel-for helper                                                       */
@@ -179,6 +180,7 @@ size_t nxo_quant_bytes(int t, size_t n) {
     case GGUF_Q4_0: return (n + 31) / 32 * 18; /* src/gguf/mod.rs:262-264 */
     case GGUF_Q8_0: return (n + 31) / 32 * 34; /* src/gguf/mod.rs:268 */
     case GGUF_Q4_K: return (n + 255) / 256 * 144; /* src/gguf/mod.rs:272 */
+    case GGUF_Q2_K: return (n + 255) / 256 * 84;  /* src/gguf/mod.rs:270 */
     default: return 0;
     }
 }
@@ -289,6 +291,56 @@ static void q4_k_block(const float *chunk, size_t len, uint8_t *out) {
     }
 }
 
+/* src/quant/mod.rs:1125-1131 */
+static uint8_t quantize_u4(float value, float scale) {
+    if (scale > 0.0f && value > 0.0f) return sat_u8(clampf(roundf(value / scale), 1.0f, 15.0f));
+    return 0;
+}
+
+/* src/quant/mod.rs:1143-1151 */
+static uint8_t q2k_value(float value, float d, float dmin, uint8_t scale_q, uint8_t min_q) {
+    float scale = d * (float)scale_q;
+    float offset = dmin * (float)min_q;
+    if (scale > 0.0f) return sat_u8(clampf(roundf((value + offset) / scale), 0.0f, 3.0f));
+    return 0;
+}
+
+/* src/quant/mod.rs:851-911: 16 sub-blocks of 16; scales[16] (scale | min << 4),
+ * qs[64] (element i in bits 2(i%4) of byte i/4), then f16 d and dmin */
+static void q2_k_block(const float *chunk, size_t len, uint8_t *out) {
+    float block[256];
+    for (size_t i = 0; i < 256; ++i) block[i] = i < len ? chunk[i] : 0.0f;
+    float sub_scales[16], sub_offsets[16];
+    for (int sub = 0; sub < 16; ++sub) {
+        const float *v = block + sub * 16;
+        float mn = INFINITY, mx = -INFINITY;
+        for (int i = 0; i < 16; ++i) mn = fminf(mn, v[i]);
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, v[i]);
+        float offset = mn < 0.0f ? -mn : 0.0f;
+        float scale = fmaxf((mx + offset) / 3.0f, 0.0f);
+        sub_scales[sub] = scale;
+        sub_offsets[sub] = offset;
+    }
+    float max_scale = 0.0f, max_offset = 0.0f;
+    for (int s = 0; s < 16; ++s) max_scale = fmaxf(max_scale, sub_scales[s]);
+    for (int s = 0; s < 16; ++s) max_offset = fmaxf(max_offset, sub_offsets[s]);
+    float d = max_scale > 0.0f ? max_scale / 15.0f : 0.0f;
+    float dmin = max_offset > 0.0f ? max_offset / 15.0f : 0.0f;
+    for (int s = 0; s < 16; ++s) {
+        uint8_t sq = quantize_u4(sub_scales[s], d), mq = quantize_u4(sub_offsets[s], dmin);
+        out[s] = (uint8_t)((sq & 0x0F) | ((mq & 0x0F) << 4));
+    }
+    uint8_t *qs = out + 16;
+    memset(qs, 0, 64);
+    for (int i = 0; i < 256; ++i) {
+        uint8_t packed = out[i / 16];
+        uint8_t q = q2k_value(block[i], d, dmin, packed & 0x0F, packed >> 4);
+        qs[i / 4] |= (uint8_t)((q & 0x03) << ((i % 4) * 2));
+    }
+    wr_f16(out + 80, d);
+    wr_f16(out + 82, dmin);
+}
+
 typedef struct {
     int t;
     const float *src;
@@ -307,6 +359,7 @@ static void quant_range(void *p, size_t lo, size_t hi) {
         case GGUF_Q8_0: q8_0_block(c->src + start, len, o); break;
         case GGUF_Q4_0: q4_0_block(c->src + start, len, o); break;
         case GGUF_Q4_K: q4_k_block(c->src + start, len, o); break;
+        case GGUF_Q2_K: q2_k_block(c->src + start, len, o); break;
         }
     }
 }
@@ -318,6 +371,7 @@ size_t nxo_quantize(int t, const float *src, size_t n, uint8_t *dst, int nthread
     case GGUF_Q8_0: c.blk = 32; c.bytes = 34; break;
     case GGUF_Q4_0: c.blk = 32; c.bytes = 18; break;
     case GGUF_Q4_K: c.blk = 256; c.bytes = 144; break;
+    case GGUF_Q2_K: c.blk = 256; c.bytes = 84; break;
     default: return 0;
     }
     size_t nblocks = (n + c.blk - 1) / c.blk;
@@ -350,6 +404,14 @@ static void dequant_range(void *p, size_t lo, size_t hi) {
                 int q = i < 16 ? (qs[i] & 0x0F) : (qs[i - 16] >> 4);
                 o[i] = (float)(int8_t)(q - 8) * scale;
             }
+        } else if (c->t == GGUF_Q2_K) { /* src/quant/mod.rs:913-937 */
+            float d = rd_f16(blk + 80), dmin = rd_f16(blk + 82);
+            const uint8_t *qs = blk + 16;
+            for (size_t i = 0; i < lim; ++i) {
+                uint8_t q = (uint8_t)((qs[i / 4] >> ((i % 4) * 2)) & 0x03);
+                uint8_t packed = blk[i / 16];
+                o[i] = d * (float)(packed & 0x0F) * (float)q - dmin * (float)(packed >> 4);
+            }
         } else { /* Q4_K, src/quant/mod.rs:820-849 */
             float d = rd_f16(blk), dmin = rd_f16(blk + 2);
             uint8_t scales[8], mins[8];
@@ -377,6 +439,7 @@ size_t nxo_dequantize(int t, const uint8_t *src, size_t src_bytes, size_t output
     case GGUF_Q8_0: c.blk = 32; c.bytes = 34; break;
     case GGUF_Q4_0: c.blk = 32; c.bytes = 18; break;
     case GGUF_Q4_K: c.blk = 256; c.bytes = 144; break;
+    case GGUF_Q2_K: c.blk = 256; c.bytes = 84; break;
     default: return 0;
     }
     size_t whole = src_bytes / c.bytes; /* chunks_exact drops a ragged tail */

@@ -10,7 +10,7 @@ import numpy as np
 
 import oracle
 
-F32, Q4_0, Q8_0, Q4_K = 0, 2, 8, 12
+F32, Q4_0, Q8_0, Q4_K, Q2_K = 0, 2, 8, 12, 10
 
 
 class Layer:

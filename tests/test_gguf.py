@@ -205,7 +205,8 @@ def moe_file(fmt, E, H, F, layer=0, naming="merged", shared_F=0, seed=0):
     w.add("general.architecture", STRING, "mixtral")
     w.add("mixtral.expert_count", U32, E)
     pays = {}
-    gt = {oracle.Q4_K: GT_Q4_K, oracle.Q8_0: GT_Q8_0, oracle.Q4_0: GT_Q4_0, 0: GT_F32}[fmt]
+    gt = {oracle.Q4_K: GT_Q4_K, oracle.Q8_0: GT_Q8_0, oracle.Q4_0: GT_Q4_0, oracle.Q2_K: 10,
+          0: GT_F32}[fmt]
 
     def mat(rows, cols):
         m = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)

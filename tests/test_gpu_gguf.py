@@ -62,7 +62,7 @@ def oracle_layer(fmt, E, H, F, Fs, pays, x, logits, k):
 
 @pytest.mark.parametrize("fmt,naming,Fs", [
     (oracle.Q4_K, "merged", 0), (oracle.Q8_0, "gguf", 256), (oracle.Q4_0, "hf", 0),
-    (0, "merged", 128)])
+    (0, "merged", 128), (oracle.Q2_K, "merged", 256)])
 def test_gguf_layer_matches_direct_load_and_oracle(ctx, tmp_path, fmt, naming, Fs):
     E, H, F, k, T, layer = 6, 512, 768, 2, 5, 1
     print(f"gguf layer fmt={fmt} naming={naming} Fs={Fs}", flush=True)

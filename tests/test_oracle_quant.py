@@ -9,7 +9,7 @@ independent vectorised numpy statement of the GGUF block layouts
 import numpy as np
 import pytest
 
-Q4_0, Q8_0, Q4_K = 2, 8, 12
+Q4_0, Q8_0, Q4_K, Q2_K = 2, 8, 12, 10
 
 
 # ----------------------------------------------------------------------------- f16
@@ -88,6 +88,15 @@ def np_dequant(fmt, data, n):
         qs = b[:, 2:]
         q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.int16) - 8
         v = q.astype(np.float32) * d[:, None]
+    elif fmt == Q2_K:
+        b = data.reshape(-1, 84)
+        d, dmin = f16(b[:, 80:82]), f16(b[:, 82:84])
+        qs = b[:, 16:80]
+        q = np.stack([(qs >> (2 * j)) & 3 for j in range(4)], axis=2).reshape(-1, 256)  # i = 4B + j
+        sub = np.arange(256) // 16
+        sc = (b[:, 0:16] & 15).astype(np.float32)[:, sub]
+        mn = (b[:, 0:16] >> 4).astype(np.float32)[:, sub]
+        v = (d[:, None] * sc) * q.astype(np.float32) - dmin[:, None] * mn
     else:
         b = data.reshape(-1, 144)
         d, dmin = f16(b[:, 0:2]), f16(b[:, 2:4])
@@ -104,11 +113,19 @@ def np_dequant(fmt, data, n):
 
 def crafted_blocks(fmt, nblocks, seed):
     rng = np.random.default_rng(seed)
-    bs = {Q8_0: 34, Q4_0: 18, Q4_K: 144}[fmt]
+    bs = {Q8_0: 34, Q4_0: 18, Q4_K: 144, Q2_K: 84}[fmt]
     data = rng.integers(0, 256, size=(nblocks, bs), dtype=np.uint8)
     # scales: normal, subnormal, zero, negative zero, largest finite
     special = np.array([0x3C00, 0x0001, 0x03FF, 0x0000, 0x8000, 0x7BFF, 0x2E66, 0x8123],
                        np.uint16)
+    if fmt == Q2_K:  # f16 d, dmin at bytes 80..83; every scale/min nibble pair in byte 0..15
+        for off, shift in ((80, 0), (82, 3)):
+            h = data[:, off:off + 2].copy().view(np.uint16).ravel()
+            h[: nblocks // 2] = special[(np.arange(nblocks // 2) + shift) % special.size]
+            data[:, off:off + 2] = h.view(np.uint8).reshape(-1, 2)
+        for b in range(min(nblocks, 16)):
+            data[b, 0:16] = (np.arange(16, dtype=np.uint8) * 16 + b) & 255
+        return data.ravel()
     hdr = data[:, 0:2].copy().view(np.uint16).ravel()
     hdr[: nblocks // 2] = special[np.arange(nblocks // 2) % special.size]
     data[:, 0:2] = hdr.view(np.uint8).reshape(-1, 2)
@@ -230,3 +247,68 @@ def test_q4_k_hand_block(oracle):
     s, m = oracle.unpack_q4k_scales(q[4:16])
     assert s.tolist() == [63] * 8 and m.tolist() == [0] * 8
     assert np.array_equal(dq, (d16 * np.float32(63.0)) * x)
+
+
+# ----------------------------------------------------------------------------- Q2_K
+def test_q2k_reference_roundtrip(oracle):
+    # src/quant/mod.rs:1327-1338 and src/gguf/mod.rs:1697-1714
+    data = (np.arange(300, dtype=np.float32) / np.float32(31.0) - np.float32(4.0)).astype(np.float32)
+    q = oracle.quantize(Q2_K, data)
+    assert q.size == 2 * 84
+    dq = oracle.dequantize(Q2_K, q, 300)
+    assert dq.size == 300
+    assert np.all(np.abs(dq - data) < 1.6)
+
+
+def test_q2k_dequant_matches_layout_statement(oracle):
+    data = crafted_blocks(Q2_K, 128, seed=10)
+    n = 128 * 256
+    got = oracle.dequantize(Q2_K, data, n)
+    ref = np_dequant(Q2_K, data, n)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    got2 = oracle.dequantize(Q2_K, data[: data.size - 5], n - 9)
+    assert got2.size == 127 * 256
+    assert np.array_equal(got2.view(np.uint32), ref[: got2.size].view(np.uint32))
+
+
+def test_q2k_quantizer_invariants(oracle):
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal(64 * 256) * np.exp(rng.uniform(-4, 2, 64 * 256))).astype(np.float32)
+    x[:256] = 0.0                                   # an all-zero block
+    x[256:512] = np.abs(x[256:512])                 # a block without negatives: mins 0
+    x[512:528] = 7.0                                # a constant sub-block
+    q = oracle.quantize(Q2_K, x).reshape(-1, 84)
+    assert np.all(q[0] == 0)
+    assert np.all((q[1, :16] >> 4) == 0)
+    dq = oracle.dequantize(Q2_K, q.ravel(), x.size).reshape(-1, 256)
+    xb = x.reshape(-1, 256)
+    # each value lies within its sub-block's step of the reconstruction grid:
+    # |x - x'| <= 2 * max over the block of (sub-block range / 3) + rounding
+    sub = xb.reshape(-1, 16, 16)
+    span = (sub.max(axis=2) - np.minimum(sub.min(axis=2), 0)).max(axis=1)
+    err = np.abs(dq - xb).max(axis=1)
+    assert np.all(err <= span * (2.0 / 3.0) + 1e-30 + span * 0.2)
+
+
+def test_q2k_hand_worked_block(oracle):
+    # sub-block s holds 16 values s/4 + (i%4)/4 (max 4.5 at s=15): offset 0,
+    # scale (max)/3; d = max_scale/15; every scale nibble rounds from
+    # scale/d; codes round (v / (d * sc)) into 0..3.  Rust's f32::round
+    # rounds halves away from zero (2.5 -> 3, 12.5 -> 13), unlike np.round.
+    rnd = lambda v: np.sign(v) * np.floor(np.abs(v) + np.float32(0.5))  # noqa: E731
+    x = np.array([s / 4 + (i % 4) / 4 for s in range(16) for i in range(16)], np.float32)
+    q = oracle.quantize(Q2_K, x)
+    sc = np.array([(x[16 * s:16 * s + 16].max()) / np.float32(3.0) for s in range(16)], np.float32)
+    d = np.float32(sc.max() / np.float32(15.0))
+    d16 = np.float16(d).astype(np.float32)
+    assert q[80:82].view(np.float16)[0] == np.float16(d)
+    assert q[82:84].view(np.uint16)[0] == 0               # dmin = 0
+    sq = np.clip(rnd(sc / d), 1, 15).astype(np.uint8)
+    sq[sc == 0] = 0
+    np.testing.assert_array_equal(q[:16] & 15, sq)
+    np.testing.assert_array_equal(q[:16] >> 4, 0)
+    codes = np.stack([(q[16:80] >> (2 * j)) & 3 for j in range(4)], axis=1).ravel()
+    step = (d * sq.astype(np.float32)).astype(np.float32)[np.arange(256) // 16]
+    want = np.where(step > 0, np.clip(rnd(x / np.where(step > 0, step, 1)), 0, 3), 0)
+    np.testing.assert_array_equal(codes, want.astype(np.uint8))
+    assert d16 > 0
