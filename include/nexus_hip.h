@@ -97,6 +97,7 @@ extern "C" {
 
 typedef struct nx_ctx nx_ctx;
 typedef struct nx_experts nx_experts;
+typedef struct nx_matrix nx_matrix;
 
 /* ---------------------------------------------------------------- runtime */
 const char *nx_last_error(void);
@@ -190,6 +191,32 @@ int nx_experts_info(const nx_experts *ex, int *fmt, int *num_experts, int *hidde
                     int *shared_ff_dim, size_t *device_bytes);
 int nx_experts_destroy(nx_experts *ex);
 
+/* ---------------------------------------------------------------- dense matrices */
+/* A device-resident dense weight matrix, rows x cols, row-major (a GGUF 2-D
+ * tensor of dims [cols, rows]), kept in its quantized format: the q/k/v/o
+ * projections and the output head of the decode step
+ * (src/engine/mod.rs:1108-1126, 1032-1043), which the reference dequantizes
+ * to f32 at load.  Quantized formats need cols to be a whole number of
+ * blocks. */
+int nx_matrix_create(nx_ctx *ctx, int fmt, int rows, int cols, nx_matrix **out);
+/* Loads the GGUF payload (host or device memory).  A payload holding fewer
+ * than rows*cols weights gives NX_ERR_SHAPE "Matvec weight too small: got
+ * <weights>, expected at least <rows*cols>" (InferenceEngine::matvec,
+ * src/engine/mod.rs:775-801). */
+int nx_matrix_load(nx_ctx *ctx, nx_matrix *m, const void *src, size_t src_bytes,
+                   int src_on_device);
+int nx_matrix_info(const nx_matrix *m, int *fmt, int *rows, int *cols, size_t *device_bytes);
+int nx_matrix_destroy(nx_matrix *m);
+/* y[t * rows + r] = sum_c W[r][c] x[t * cols + c] for T = num_tokens, fp32
+ * in and out: InferenceEngine::matvec (src/engine/mod.rs:775-801) on each
+ * token row, with the dot product in parallel order (fp32 accumulate) over
+ * weights dequantized in registers.  x_len != T*cols gives NX_ERR_SHAPE
+ * "Matvec input shape mismatch: got <x_len>, expected <T*cols>". */
+int nx_matvec(nx_ctx *ctx, const nx_matrix *m, const float *x, size_t x_len, int num_tokens,
+              float *y);
+int nx_matvec_dev(nx_ctx *ctx, const nx_matrix *m, const float *d_x, size_t x_len,
+                  int num_tokens, float *d_y);
+
 /* ---------------------------------------------------------------- GGUF */
 typedef struct nx_gguf nx_gguf;
 /* Q4_K code order of a file's payloads */
@@ -229,6 +256,11 @@ int nx_gguf_moe_info(const nx_gguf *g, int layer, int *fmt, int *num_experts, in
  * quantized (no f32 copy); q4k_order says how the file orders Q4_K codes. */
 int nx_experts_load_gguf(nx_ctx *ctx, const nx_gguf *g, int layer, int q4k_order,
                          nx_experts **out);
+/* Loads the tensor called `name` into a new dense matrix (rows = product of
+ * dims[1..], cols = dims[0]); NX_ERR_NOT_FOUND "Missing tensor: <name>" if
+ * absent (InferenceEngine::tensor, src/engine/mod.rs:718-725). */
+int nx_matrix_load_gguf(nx_ctx *ctx, const nx_gguf *g, const char *name, int q4k_order,
+                        nx_matrix **out);
 /* Q4_K blocks from upstream ggml's code order to the reference's (host). */
 int nx_q4k_from_ggml(const void *src, void *dst, size_t blocks);
 

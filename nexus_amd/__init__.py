@@ -42,7 +42,9 @@ EXPORTS = [
     "nx_gguf_close", "nx_gguf_info", "nx_gguf_tensor", "nx_gguf_find_tensor",
     "nx_gguf_tensor_data", "nx_gguf_meta_usize", "nx_gguf_meta_f32", "nx_gguf_meta_str",
     "nx_gguf_moe_info", "nx_experts_load_gguf", "nx_q4k_from_ggml", "nx_rms_norm",
-    "nx_rms_norm_dev", "nx_moe_block", "nx_moe_block_dev",
+    "nx_rms_norm_dev", "nx_moe_block", "nx_moe_block_dev", "nx_matrix_create",
+    "nx_matrix_load", "nx_matrix_info", "nx_matrix_destroy", "nx_matvec", "nx_matvec_dev",
+    "nx_matrix_load_gguf",
 ]
 
 _lib = None
@@ -134,6 +136,13 @@ def lib():
                           C.c_int, C.c_int, C.c_int, C.c_int], C.c_int),
         "nx_moe_block_dev": ([_vp, _vp, _vp, _vp, C.c_size_t, C.c_float, _vp, C.c_size_t,
                               C.c_int, C.c_int, C.c_int, C.c_int, C.c_int], C.c_int),
+        "nx_matrix_create": ([_vp, C.c_int, C.c_int, C.c_int, C.POINTER(_vp)], C.c_int),
+        "nx_matrix_load": ([_vp, _vp, _vp, C.c_size_t, C.c_int], C.c_int),
+        "nx_matrix_info": ([_vp, _ip, _ip, _ip, _szp], C.c_int),
+        "nx_matrix_destroy": ([_vp], C.c_int),
+        "nx_matvec": ([_vp, _vp, _fp, C.c_size_t, C.c_int, _fp], C.c_int),
+        "nx_matvec_dev": ([_vp, _vp, _vp, C.c_size_t, C.c_int, _vp], C.c_int),
+        "nx_matrix_load_gguf": ([_vp, _vp, C.c_char_p, C.c_int, C.POINTER(_vp)], C.c_int),
     })
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -389,6 +398,61 @@ class Experts:
                                        num_tokens, top_k, score_mode, path, _vp(out_ptr)))
 
 
+class Matrix:
+    """A device-resident dense weight matrix (rows x cols) kept in its GGUF format."""
+
+    def __init__(self, ctx: Context, fmt: int, rows: int, cols: int):
+        h = _vp()
+        check(lib().nx_matrix_create(ctx.h, fmt, rows, cols, C.byref(h)))
+        self.h, self.ctx = h, ctx
+        self.fmt, self.rows, self.cols = fmt, rows, cols
+
+    @classmethod
+    def _wrap(cls, ctx: Context, h):
+        m = cls.__new__(cls)
+        m.h, m.ctx = h, ctx
+        f, r, c = C.c_int(), C.c_int(), C.c_int()
+        check(lib().nx_matrix_info(h, C.byref(f), C.byref(r), C.byref(c), None))
+        m.fmt, m.rows, m.cols = f.value, r.value, c.value
+        return m
+
+    def load(self, payload) -> None:
+        """Load a GGUF payload (numpy array in host memory)."""
+        data = np.ascontiguousarray(payload).view(np.uint8).ravel()
+        check(lib().nx_matrix_load(self.ctx.h, self.h, _vp(data.ctypes.data), data.size, 0))
+
+    def load_dev(self, ptr: int, nbytes: int) -> None:
+        check(lib().nx_matrix_load(self.ctx.h, self.h, _vp(ptr), nbytes, 1))
+
+    def device_bytes(self) -> int:
+        b = C.c_size_t(0)
+        check(lib().nx_matrix_info(self.h, None, None, None, C.byref(b)))
+        return b.value
+
+    def matvec(self, x, num_tokens: int | None = None) -> np.ndarray:
+        """y[t] = W . x[t] for x of shape [T, cols] (or [cols] for one token)."""
+        x = _f32(x)
+        T = (1 if x.ndim == 1 else x.shape[0]) if num_tokens is None else num_tokens
+        y = np.empty((max(T, 1), self.rows), np.float32)
+        xf = x.ravel()
+        check(lib().nx_matvec(self.ctx.h, self.h, _p(xf, _fp), xf.size, T, _p(y, _fp)))
+        return y[:T] if x.ndim != 1 else y[0]
+
+    def matvec_dev(self, x_ptr: int, x_len: int, num_tokens: int, y_ptr: int) -> None:
+        check(lib().nx_matvec_dev(self.ctx.h, self.h, _vp(x_ptr), x_len, num_tokens, _vp(y_ptr)))
+
+    def close(self):
+        if self.h:
+            lib().nx_matrix_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Gguf:
     """A memory-mapped GGUF file (GgufReader::parse_file).  No GPU needed."""
 
@@ -488,3 +552,10 @@ def experts_from_gguf(ctx: Context, g: Gguf, layer: int, q4k_order: int = Q4K_RE
     ex.fmt, ex.E, ex.H, ex.F = info["fmt"], info["experts"], info["hidden"], info["ffn"]
     ex.Fs = info["shared_ffn"]
     return ex
+
+
+def matrix_from_gguf(ctx: Context, g: Gguf, name: str, q4k_order: int = Q4K_REFERENCE) -> Matrix:
+    """The tensor `name` of a GGUF file as a resident dense matrix."""
+    h = _vp()
+    check(lib().nx_matrix_load_gguf(ctx.h, g.h, name.encode(), q4k_order, C.byref(h)))
+    return Matrix._wrap(ctx, h)

@@ -164,10 +164,11 @@ static int ex_alloc(nx_experts *ex, size_t bytes, uint8_t **out) {
   return NX_OK;
 }
 
-static int init_plane(nx_experts *ex, RolePlane &pl, int count, int rows, int cols) {
+// row layout of a plane of `rows` x `cols` in format fmt (no allocation)
+static void plane_layout(int fmt, RolePlane &pl, int rows, int cols) {
   pl.rows = rows;
   pl.cols = cols;
-  switch (ex->fmt) {
+  switch (fmt) {
   case NX_FMT_Q4_K:
     pl.nseg = cols / 256 * 4;
     pl.row_meta = (uint32_t)(cols / 256 * 16);
@@ -194,6 +195,10 @@ static int init_plane(nx_experts *ex, RolePlane &pl, int count, int rows, int co
   // strides rounded to 256 B so every expert's planes start aligned
   pl.qs_stride = ((size_t)rows * pl.row_qs + 255) / 256 * 256;
   pl.meta_stride = ((size_t)rows * pl.row_meta + 255) / 256 * 256;
+}
+
+static int init_plane(nx_experts *ex, RolePlane &pl, int count, int rows, int cols) {
+  plane_layout(ex->fmt, pl, rows, cols);
   NX_TRY(ex_alloc(ex, pl.qs_stride * count, &pl.qs));
   if (pl.row_meta) NX_TRY(ex_alloc(ex, pl.meta_stride * count, &pl.meta));
   return NX_OK;
@@ -689,6 +694,104 @@ int nx_experts_destroy(nx_experts *ex) {
   }
   for (void *p : ex->allocs) (void)hipFree(p);
   delete ex;
+  return NX_OK;
+}
+
+// ------------------------------------------------------------ dense matrices
+int nx_matrix_create(nx_ctx *c, int fmt, int rows, int cols, nx_matrix **out) {
+  NX_TRY(check_ctx(c));
+  if (!out) return fail(NX_ERR_INVALID_ARG, "null output pointer");
+  *out = nullptr;
+  FormatInfo fi;
+  if (!format_info(fmt, &fi)) return fail(NX_ERR_INVALID_ARG, "unknown weight format " + std::to_string(fmt));
+  if (rows <= 0 || cols <= 0) return fail(NX_ERR_INVALID_ARG, "matrix rows and cols must be positive");
+  if (fmt != NX_FMT_F32 && cols % fi.block)
+    return fail(NX_ERR_UNSUPPORTED, std::string(fmt_name(fmt)) + " matrices need cols to be a multiple of " +
+                                        std::to_string(fi.block));
+  nx_experts *ex = new nx_experts();
+  ex->ctx = c;
+  ex->fmt = fmt;
+  ex->E = 1;
+  ex->H = rows;
+  ex->F = cols;
+  RolePlane &pl = ex->role[NX_ROLE_DOWN];
+  int rc = NX_OK;
+  // narrow rows are addressed through one 32-bit buffer range per plane
+  plane_layout(fmt, pl, rows, cols);
+  if (pl.qs_stride > 0xFFFFFF00ull || pl.meta_stride > 0xFFFFFF00ull)
+    rc = fail(NX_ERR_UNSUPPORTED, "matrix plane over 4 GiB resident");
+  else if (!gemv_row_fits(fmt, pl.nseg))
+    rc = fail(NX_ERR_UNSUPPORTED, std::string(fmt_name(fmt)) + " rows of " + std::to_string(cols) +
+                                      " weights are too long for the register-resident GEMV");
+  if (!rc) rc = init_plane(ex, pl, 1, rows, cols);
+  if (rc) {
+    nx_experts_destroy(ex);
+    return rc;
+  }
+  *out = new nx_matrix{ex, rows, cols};
+  return NX_OK;
+}
+
+int nx_matrix_load(nx_ctx *c, nx_matrix *m, const void *src, size_t src_bytes, int on_device) {
+  NX_TRY(check_ctx(c));
+  if (!m || !src) return fail(NX_ERR_INVALID_ARG, "null argument");
+  // InferenceEngine::matvec's weight check, counted in weight elements
+  FormatInfo fi;
+  format_info(m->ex->fmt, &fi);
+  const size_t have = m->ex->fmt == NX_FMT_F32 ? src_bytes / 4 : src_bytes / fi.block_bytes * fi.block;
+  const size_t need = (size_t)m->rows * m->cols;
+  if (have < need)
+    return fail(NX_ERR_SHAPE, "Matvec weight too small: got " + std::to_string(have) +
+                                  ", expected at least " + std::to_string(need));
+  return nx_experts_load(c, m->ex, 0, NX_ROLE_DOWN, src, src_bytes, on_device);
+}
+
+int nx_matrix_info(const nx_matrix *m, int *fmt, int *rows, int *cols, size_t *device_bytes) {
+  if (!m) return fail(NX_ERR_INVALID_ARG, "null matrix");
+  if (fmt) *fmt = m->ex->fmt;
+  if (rows) *rows = m->rows;
+  if (cols) *cols = m->cols;
+  if (device_bytes) *device_bytes = m->ex->device_bytes;
+  return NX_OK;
+}
+
+int nx_matrix_destroy(nx_matrix *m) {
+  if (!m) return NX_OK;
+  nx_experts_destroy(m->ex);
+  delete m;
+  return NX_OK;
+}
+
+static int check_matvec(const nx_matrix *m, const float *x, size_t x_len, int T, const float *y) {
+  if (!m) return fail(NX_ERR_INVALID_ARG, "null matrix");
+  if (T < 0) return fail(NX_ERR_INVALID_ARG, "negative size");
+  const size_t need_x = (size_t)T * m->cols;
+  if (x_len != need_x)
+    return fail(NX_ERR_SHAPE, "Matvec input shape mismatch: got " + std::to_string(x_len) +
+                                  ", expected " + std::to_string(need_x));
+  if (T > 0 && (!x || !y)) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  return NX_OK;
+}
+
+int nx_matvec_dev(nx_ctx *c, const nx_matrix *m, const float *d_x, size_t x_len, int T, float *d_y) {
+  NX_TRY(check_ctx(c));
+  NX_TRY(check_matvec(m, d_x, x_len, T, d_y));
+  if (T == 0) return NX_OK;
+  return launch_gemv_matrix(c, m->ex->fmt, m->ex->role[NX_ROLE_DOWN], d_x, T, d_y);
+}
+
+int nx_matvec(nx_ctx *c, const nx_matrix *m, const float *x, size_t x_len, int T, float *y) {
+  NX_TRY(check_ctx(c));
+  NX_TRY(check_matvec(m, x, x_len, T, y));
+  if (T == 0) return NX_OK;
+  const size_t ny = (size_t)T * m->rows;
+  float *d_x, *d_y;
+  NX_TRY(ws(c, WS_MAT_X, x_len, &d_x));
+  NX_TRY(ws(c, WS_MAT_Y, ny, &d_y));
+  NX_HIP(hipMemcpyAsync(d_x, x, x_len * 4, hipMemcpyHostToDevice, c->stream));
+  NX_TRY(launch_gemv_matrix(c, m->ex->fmt, m->ex->role[NX_ROLE_DOWN], d_x, T, d_y));
+  NX_HIP(hipMemcpyAsync(y, d_y, ny * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
   return NX_OK;
 }
 

@@ -71,9 +71,15 @@ struct SlotView {
 __device__ __forceinline__ SlotView slot_view(const GemvArgs &a, int slot, int n_active) {
   SlotView v;
   if (slot < n_active) {
-    const int e = a.active[slot];
-    v.pair0 = a.offsets[e];
-    v.count = a.offsets[e + 1] - v.pair0;
+    // a launch with no active list is one dense matrix over all T tokens
+    int e = 0;
+    v.pair0 = 0;
+    v.count = a.T;
+    if (a.active) {
+      e = a.active[slot];
+      v.pair0 = a.offsets[e];
+      v.count = a.offsets[e + 1] - v.pair0;
+    }
     v.rows = a.rows;
     v.cols = a.cols;
     v.nseg = a.nseg;
@@ -345,7 +351,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = KSPLIT > 1 ? 0 : (LPR == 64 ? wave : tid / LPR);
 
-  const int n_active = a.active[a.E];
+  const int n_active = a.active ? a.active[a.E] : 1;
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
   const int slot = blockIdx.y;
   if (slot >= n_slots) return;  // workgroup-uniform
@@ -648,6 +654,17 @@ bool choose_shape(int nseg, int eps, int nt, Shape *s) {
   return true;
 }
 
+// tokens per group (two when there are several, unless a row that long only
+// fits one token's activations in registers) and the shape for it
+bool choose_tokens_shape(int nseg, int eps, int T, int *nt, Shape *s) {
+  if (T > 1 && choose_shape(nseg, eps, 2, s)) {
+    *nt = 2;
+    return true;
+  }
+  *nt = 1;
+  return choose_shape(nseg, eps, 1, s);
+}
+
 // partial sums of the down kernel stay in LDS up to this size per workgroup
 constexpr size_t kDownLdsMax = 64 * 1024;
 
@@ -707,9 +724,9 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   }
 
   const int nseg = a.nseg > a.snseg ? a.nseg : a.snseg;
-  const int nt = p.T > 1 ? 2 : 1;
+  int nt;
   Shape sh;
-  if (!choose_shape(nseg, elems_per_segment(ex->fmt), nt, &sh))
+  if (!choose_tokens_shape(nseg, elems_per_segment(ex->fmt), p.T, &nt, &sh))
     return fail(NX_ERR_UNSUPPORTED, "row length too large for the register-resident GEMV");
   const int L = sh.lpr * sh.ksplit;
   const int groups_per_wg = 256 / L;
@@ -779,8 +796,59 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
                 [&] { hipLaunchKernelGGL(fn, dim3(gx), dim3(threads), lds, c->stream, a); });
 }
 
+// One matrix over T tokens: the per-slot kernel with a single dense slot.
+int run_gemv_matrix(nx_ctx *c, int fmt, const RolePlane &pl, const float *x, int T, float *out) {
+  GemvArgs a{};
+  a.qs0 = a.qs1 = pl.qs;
+  a.meta0 = a.meta1 = pl.meta;
+  a.qs_stride = pl.qs_stride;
+  a.meta_stride = pl.meta_stride;
+  a.row_qs = pl.row_qs;
+  a.row_meta = pl.row_meta;
+  a.rows = pl.rows;
+  a.cols = pl.cols;
+  a.nseg = pl.nseg;
+  a.E = 1;
+  a.T = T;
+  a.k = 1;
+  a.x = x;
+  a.x_stride = pl.cols;
+  a.out = out;
+  a.out_stride = pl.rows;
+  int nt;
+  Shape sh;
+  if (!choose_tokens_shape(pl.nseg, elems_per_segment(fmt), T, &nt, &sh))
+    return fail(NX_ERR_UNSUPPORTED, "row length too large for the register-resident GEMV");
+  KernelFn fn = pick(fmt, KIND_DOWN_ROWS, true, nt, sh);
+  if (!fn) return fail(NX_ERR_UNSUPPORTED, "no GEMV kernel instance for this shape");
+  int wg_per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wg_per_cu, reinterpret_cast<const void *>(fn),
+                                                   256, 0) != hipSuccess ||
+      wg_per_cu < 1) {
+    (void)hipGetLastError();
+    wg_per_cu = 1;
+  }
+  const int groups_per_wg = 256 / (sh.lpr * sh.ksplit);
+  const long groups = (long)c->num_cu * wg_per_cu * groups_per_wg;
+  long rpg = (pl.rows + groups - 1) / groups;
+  if (rpg < 1) rpg = 1;
+  a.rows_per_group = (int)rpg;
+  const long rows_per_wg = rpg * groups_per_wg;
+  const unsigned gx = (unsigned)((pl.rows + rows_per_wg - 1) / rows_per_wg);
+  return launch(c, "gemv_matrix",
+                [&] { hipLaunchKernelGGL(fn, dim3(gx, 1), dim3(256), 0, c->stream, a); });
+}
+
 }  // namespace
 
+int launch_gemv_matrix(nx_ctx *c, int fmt, const RolePlane &pl, const float *x, int T, float *out) {
+  return run_gemv_matrix(c, fmt, pl, x, T, out);
+}
+bool gemv_row_fits(int fmt, int nseg) {
+  int nt;
+  Shape sh;
+  return choose_tokens_shape(nseg, elems_per_segment(fmt), 1, &nt, &sh);
+}
 int launch_gemv_gateup(nx_ctx *c, const GemvPlan &p) { return run_gemv(c, p, true); }
 int launch_gemv_down(nx_ctx *c, const GemvPlan &p) { return run_gemv(c, p, false); }
 

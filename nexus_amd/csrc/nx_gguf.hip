@@ -671,4 +671,42 @@ int nx_experts_load_gguf(nx_ctx *ctx, const nx_gguf *g, int layer, int q4k_order
   return NX_OK;
 }
 
+int nx_matrix_load_gguf(nx_ctx *ctx, const nx_gguf *g, const char *name, int q4k_order,
+                        nx_matrix **out) {
+  if (!ctx || !g || !name || !out) return fail(NX_ERR_INVALID_ARG, "null argument");
+  if (q4k_order != NX_Q4K_REFERENCE && q4k_order != NX_Q4K_GGML)
+    return fail(NX_ERR_INVALID_ARG, "unknown Q4_K code order");
+  *out = nullptr;
+  const nx_gguf::Tensor *t = find(g, name);
+  if (!t) return fail(NX_ERR_NOT_FOUND, std::string("Missing tensor: ") + name);
+  if (!supported_fmt(t->type))
+    return fail(NX_ERR_UNSUPPORTED, "tensor type " + std::to_string(t->type) +
+                                        " is not resident-capable (F32, Q4_0, Q8_0, Q4_K, Q2_K)");
+  // dims innermost first: a row is dims[0] long, the rest count rows
+  if (t->dims.empty()) return fail(NX_ERR_SHAPE, "tensor " + t->name + " has no dimensions");
+  uint64_t rows = 1;
+  for (size_t i = 1; i < t->dims.size(); ++i) rows *= t->dims[i];
+  const uint64_t cols = t->dims[0];
+  if (rows == 0 || cols == 0 || rows > 0x7FFFFFFF || cols > 0x7FFFFFFF)
+    return fail(NX_ERR_SHAPE, "tensor " + t->name + " is not a usable matrix");
+  const uint8_t *p;
+  uint64_t bytes;
+  NX_TRY(tensor_payload(g, *t, &p, &bytes));
+  nx_matrix *m = nullptr;
+  NX_TRY(nx_matrix_create(ctx, (int)t->type, (int)rows, (int)cols, &m));
+  std::vector<uint8_t> conv;
+  if (t->type == NX_FMT_Q4_K && q4k_order == NX_Q4K_GGML) {
+    conv.resize(bytes);
+    q4k_ggml_to_reference(p, conv.data(), bytes / 144);
+    p = conv.data();
+  }
+  const int rc = nx_matrix_load(ctx, m, p, bytes, 0);
+  if (rc) {
+    nx_matrix_destroy(m);
+    return rc;
+  }
+  *out = m;
+  return NX_OK;
+}
+
 }  // extern "C"

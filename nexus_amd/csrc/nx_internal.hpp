@@ -83,7 +83,7 @@ struct nx_ctx {
   int num_cu = 0;
   size_t lds_per_cu = 0;  // bytes of LDS per CU
   // workspace
-  nx::DevBuf ws[24];
+  nx::DevBuf ws[32];
   // host-visible staging for blocking calls
   nx::DevBuf host_stage;
   // profiling
@@ -91,6 +91,13 @@ struct nx_ctx {
   std::vector<nx::KernelStat> stats;
   std::vector<nx::PendingEvent> pending;
   std::vector<hipEvent_t> event_pool;
+};
+
+// one dense weight matrix (rows x cols, row-major as GGUF stores it), held
+// as a one-expert set whose down-role plane is the matrix
+struct nx_matrix {
+  nx_experts *ex = nullptr;
+  int rows = 0, cols = 0;
 };
 
 struct nx_experts {
@@ -130,6 +137,8 @@ enum WsSlot {
   WS_SUMSQ,
   WS_NORM_W,   // device copy of the norm weight for blocking calls
   WS_BLK_HIDDEN,
+  WS_MAT_X,    // device copy of matvec inputs for blocking calls
+  WS_MAT_Y,
 };
 
 int ws_get(nx_ctx *c, int slot, size_t bytes, void **out);
@@ -204,6 +213,11 @@ struct GemvPlan {
   const float *residual = nullptr;  // out = residual + layer output when set
 };
 int launch_gemv_gateup(nx_ctx *c, const GemvPlan &p);
+// out[t][r] = sum_c W[r][c] x[t][c] for one resident matrix (x rows pl.cols
+// floats apart, out rows pl.rows floats apart)
+int launch_gemv_matrix(nx_ctx *c, int fmt, const RolePlane &pl, const float *x, int T, float *out);
+// whether a row of nseg segments fits the register-resident GEMV
+bool gemv_row_fits(int fmt, int nseg);
 int launch_gemv_down(nx_ctx *c, const GemvPlan &p);
 
 struct GemmPlan {
