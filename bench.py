@@ -255,6 +255,56 @@ ROUTER_SHAPES = [
 ]
 
 
+DENSE_SHAPES = [
+    # name, rows, cols: Mixtral 8x7B's decode-step projections and output head
+    ("attn_q", 4096, 4096),
+    ("attn_k", 1024, 4096),
+    ("attn_output", 4096, 4096),
+    ("output", 32000, 4096),
+]
+
+
+def dense_cases(nx, ctx, torch, args):
+    """Dense quantized matvec (one token) per projection shape and format:
+    kernel mean time and GB/s on the GGUF bytes of the matrix.  Replicas are
+    rotated so that every call reads its matrix from HBM rather than from the
+    Infinity Cache."""
+    dev = torch.device("cuda", 0)
+    res = {}
+    for fname, fmt in (("Q4_K", nx.Q4_K), ("Q8_0", nx.Q8_0)):
+        blk, bb = nx.BLOCK[fmt]
+        for name, rows, cols in DENSE_SHAPES:
+            g = torch.Generator(device=dev)
+            g.manual_seed(args.seed + rows)
+            w = torch.randn((rows * cols,), generator=g, device=dev, dtype=torch.float32) * 0.05
+            nbytes = nx.quant_bytes(fmt, rows * cols)
+            q = torch.empty((nbytes,), device=dev, dtype=torch.uint8)
+            ctx.quantize_dev(fmt, w.data_ptr(), rows * cols, q.data_ptr(), nbytes)
+            del w
+            reps = max(2, min(512, (1 << 30) // nbytes))
+            mats = []
+            for _ in range(reps):
+                m = nx.Matrix(ctx, fmt, rows, cols)
+                m.load_dev(q.data_ptr(), nbytes)
+                mats.append(m)
+            del q
+            x = torch.randn((cols,), generator=g, device=dev, dtype=torch.float32)
+            y = torch.empty((rows,), device=dev, dtype=torch.float32)
+
+            def step(i, mats=mats, x=x, y=y, cols=cols):
+                mats[i % len(mats)].matvec_dev(x.data_ptr(), cols, 1, y.data_ptr())
+
+            time_steps(torch, step, reps, 2)
+            kern = kernel_means(ctx, torch, step, 4 * reps)
+            ms = kern.get("gemv_matrix", float("nan"))
+            res[f"{name}_{fname}"] = {"rows": rows, "cols": cols, "us": round(ms * 1e3, 2),
+                                      "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                      "replicas": reps}
+            for m in mats:
+                m.close()
+    return res
+
+
 def router_cases(nx, ctx, torch, args):
     """Router logits on device (logits = x . W_r^T, fp32): kernel mean time of
     the exact mode (the reference matvec's sequential order, bit-identical)
@@ -425,6 +475,8 @@ def main():
         extra["model_configs"] = model_config_cases(nx, ctx, torch, args)
         print("bench: router logits", file=sys.stderr, flush=True)
         extra["router_logits"] = router_cases(nx, ctx, torch, args)
+        print("bench: dense matvec", file=sys.stderr, flush=True)
+        extra["dense_matvec_1_token"] = dense_cases(nx, ctx, torch, args)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "gemv_gateup_mixtral_q4k_t1_traffic.json")
