@@ -850,10 +850,12 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
 
   if (use == NX_PATH_GEMV) {
     NX_TRY(ws(c, WS_YPAIR, pairs_total * H, &d_ypair));
-    if (route_permute_fusable(T, E, k)) {
+    // one token: the gate/up kernel routes it itself (no router launch)
+    const bool route_in_gemv = T == 1 && E <= kFusedRouteMaxE && k <= 64;
+    if (!route_in_gemv && route_permute_fusable(T, E, k)) {
       NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
                                   d_pt, d_ps, d_inv, d_act, nullptr, 0));
-    } else {
+    } else if (!route_in_gemv) {
       NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
       NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act,
                             nullptr, 0));
@@ -864,6 +866,8 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
     NX_TRY(ws(c, WS_ACT, pairs_total * act_stride, &d_actv));
     GemvPlan gp{ex, T, k, d_x, d_pt, d_off, d_act, d_actv, act_stride, d_ypair,
                 d_w, d_cnt, d_inv, d_out, d_residual};
+    if (route_in_gemv)
+      gp.route = {d_logits, score_mode, d_exp, d_cnt, d_ec, d_off, d_pt, d_ps, d_inv, d_act, d_w};
     NX_TRY(launch_gemv_gateup(c, gp));
     NX_TRY(launch_gemv_down(c, gp));
     return NX_OK;

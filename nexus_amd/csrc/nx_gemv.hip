@@ -28,6 +28,7 @@
 // and no communication between workgroups.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
+#include "nx_route_dev.hpp"
 
 namespace nx {
 
@@ -58,7 +59,15 @@ struct GemvArgs {
   const float *residual;  // final_out = residual + combine when set
   int npairs;
   float *gpart;
+  // gate/up of one token with the routing done in the kernel: every
+  // workgroup routes the token from route_logits [E]; workgroup (0, 0) also
+  // writes the route and permutation arrays the down pass reads
+  const float *route_logits;
+  int score_mode;
+  int32_t *r_exp, *r_cnt, *r_ecount, *r_off, *r_ptok, *r_pslot, *r_inv, *r_active;
+  float *r_w;
 };
+
 
 // Workgroup-uniform description of one expert slot.
 struct SlotView {
@@ -68,17 +77,19 @@ struct SlotView {
   bool routed;
 };
 
-__device__ __forceinline__ SlotView slot_view(const GemvArgs &a, int slot, int n_active) {
+// active: the active expert list (global, or the workgroup's own routing in
+// LDS); null for a dense matrix, one slot over all T tokens
+__device__ __forceinline__ SlotView slot_view(const GemvArgs &a, int slot, int n_active,
+                                              const int32_t *active, const int32_t *offsets) {
   SlotView v;
   if (slot < n_active) {
-    // a launch with no active list is one dense matrix over all T tokens
     int e = 0;
     v.pair0 = 0;
     v.count = a.T;
-    if (a.active) {
-      e = a.active[slot];
-      v.pair0 = a.offsets[e];
-      v.count = a.offsets[e + 1] - v.pair0;
+    if (active) {
+      e = active[slot];
+      v.pair0 = offsets[e];
+      v.count = offsets[e + 1] - v.pair0;
     }
     v.rows = a.rows;
     v.cols = a.cols;
@@ -335,6 +346,67 @@ struct RowGroup {
   }
 };
 
+// Wave 0 of a gate/up workgroup routes the launch's one token (route_one:
+// top-k with ties to the lower index) and lays out what the permutation
+// kernel would for it: the routed experts sorted by id are the active list,
+// each owning one pair at its rank.  Workgroup (0, 0) writes those arrays to
+// memory for the down pass, with the values k_route_permute gives one token.
+__device__ __forceinline__ void fused_route(const GemvArgs &a, int lane, int32_t *s_active,
+                                            int32_t *s_off, int32_t *s_ptok, int32_t *s_n) {
+  // only the workgroup that writes the routes needs their weights
+  const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+  int e, n;
+  float w;
+  route_one<4>(a.route_logits, a.E, a.k, a.score_mode, lane, &e, &w, &n, writer);
+  // Over the routed experts (n is wave-uniform, so every lane takes part in
+  // each shuffle): this lane's rank among them, and for the ids
+  // x = lane + 64 j <= E the routed experts below x and at x.
+  constexpr int XJ = kFusedRouteMaxE / 64 + 1;
+  int rank = 0, below[XJ], hit[XJ];
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) below[j] = hit[j] = 0;
+  for (int r = 0; r < n; ++r) {
+    const int er = __shfl(e, r, 64);
+    rank += er < e ? 1 : 0;
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) {
+      below[j] += er < lane + 64 * j ? 1 : 0;
+      hit[j] += er == lane + 64 * j ? 1 : 0;
+    }
+  }
+  if (lane < n) {
+    s_active[rank] = e;
+    s_ptok[rank] = 0;
+    if (writer) {
+      a.r_active[rank] = e;
+      a.r_ptok[rank] = 0;
+      a.r_pslot[rank] = lane;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int x = lane + 64 * j;
+    if (x <= a.E) s_off[x] = below[j];
+    if (writer && x < a.E) {
+      a.r_ecount[x] = hit[j];
+      a.r_off[x] = below[j];
+    }
+  }
+  if (lane == 0) *s_n = n;
+  if (writer) {
+    if (lane < a.k) {
+      a.r_exp[lane] = e;
+      a.r_w[lane] = w;
+      a.r_inv[lane] = lane < n ? rank : -1;
+    }
+    if (lane == 0) {
+      a.r_cnt[0] = n;
+      a.r_off[a.E] = n;
+      a.r_active[a.E] = n;
+    }
+  }
+}
+
 // PLAIN: one matrix (the down projection of one slot per grid.y), no
 // SwiGLU; activations are per pair (row pair0 + t of x) and each row's dot
 // product goes to out[pair][row] for the combine kernel.
@@ -351,30 +423,64 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = KSPLIT > 1 ? 0 : (LPR == 64 ? wave : tid / LPR);
 
-  const int n_active = a.active ? a.active[a.E] : 1;
+  // one wave per row group: the workgroup shares the activation operands
+  constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32;
+  __shared__ uint4 xsh[COOP ? NT * 64 * RG::XW : 1];
+  RG g;
+  g.init(KSPLIT == 1 ? (lane % LPR) : tid);
+  float xq[NT][RG::XQ];  // activation quarters in flight (COOP)
+  bool x_issued = false;
+
+  const int32_t *active = a.active, *offsets = a.offsets, *perm_token = a.perm_token;
+  int n_active;
+  if constexpr (!PLAIN) {
+    // one token routed here: ids of the routed experts in ascending order
+    // (the permutation's active list), each with one pair at its rank
+    __shared__ int32_t s_active[64];
+    __shared__ int32_t s_off[kFusedRouteMaxE + 1];
+    __shared__ int32_t s_ptok[64];
+    __shared__ int32_t s_n;
+    if (a.route_logits) {  // kernel-uniform
+      if constexpr (COOP) {
+        // every slot of the one token reads activation row 0 over rows of
+        // a.cols (gate/up and the shared expert alike): load it while the
+        // token is routed
+        SlotView v0;
+        v0.count = 1;
+        v0.cols = a.cols;
+        v0.nseg = a.nseg;
+        g.coop_issue(xq, a.x, a.x_stride, v0, 0, [](int) { return 0; }, tid);
+        x_issued = true;
+      }
+      if (wave == 0) fused_route(a, lane, s_active, s_off, s_ptok, &s_n);
+      __syncthreads();
+      active = s_active;
+      offsets = s_off;
+      perm_token = s_ptok;
+      n_active = s_n;
+    } else {
+      n_active = a.active[a.E];
+    }
+  } else {
+    n_active = a.active ? a.active[a.E] : 1;
+  }
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
   const int slot = blockIdx.y;
   if (slot >= n_slots) return;  // workgroup-uniform
   __shared__ float red[KSPLIT > 1 ? 4 * U * NMAT * NT : 1];
 
-  // one wave per row group: the workgroup shares the activation operands
-  constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32;
-  __shared__ uint4 xsh[COOP ? NT * 64 * RG::XW : 1];
-
-  const SlotView v = slot_view(a, slot, n_active);
+  const SlotView v = slot_view(a, slot, n_active, active, offsets);
   const int row_begin = (blockIdx.x * GROUPS + grp) * a.rows_per_group;
   const int row_end = min(v.rows, row_begin + a.rows_per_group);
-  RG g;
-  g.init(KSPLIT == 1 ? (lane % LPR) : tid);
   auto row_of = [&](int t) {
-    return PLAIN ? v.pair0 + t : (v.routed ? a.perm_token[v.pair0 + t] : t);
+    return PLAIN ? v.pair0 + t : (v.routed ? perm_token[v.pair0 + t] : t);
   };
 
   typename RG::Stage st[S];
   for (int t0 = 0; t0 < v.count; t0 += NT) {
     if constexpr (COOP) {
-      float xq[NT][RG::XQ];
-      g.coop_issue(xq, a.x, a.x_stride, v, t0, row_of, tid);
+      if (!x_issued) g.coop_issue(xq, a.x, a.x_stride, v, t0, row_of, tid);
+      x_issued = false;
 #pragma unroll
       for (int i = 0; i < S - 1; ++i) g.load(st[i], v, row_begin + i * U, row_end);
       g.coop_finish(xq, xsh, tid);
@@ -498,7 +604,7 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
       if (p.t0 >= v.count) {
         p.t0 = 0;
         p.si += DOWN_SG;
-        if (p.si < n_slots) v = slot_view(a, p.si, n_active);
+        if (p.si < n_slots) v = slot_view(a, p.si, n_active, a.active, a.offsets);
       }
     }
   };
@@ -521,7 +627,7 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
 
   if (row_begin < row_end && half < n_slots) {  // uniform within the row group
     Pos pc{half, 0, row_begin};
-    SlotView vc = slot_view(a, half, n_active);
+    SlotView vc = slot_view(a, half, n_active, a.active, a.offsets);
     Pos pl = pc;
     SlotView vl = vc;
     typename RG::Stage A, B;
@@ -718,6 +824,21 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
     a.x_stride = ex->H;
     a.out = p.act;
     a.out_stride = p.act_stride;
+    if (p.route.logits) {
+      if (p.T != 1 || ex->E > kFusedRouteMaxE || p.k > 64)
+        return fail(NX_ERR_INVALID_ARG, "in-kernel routing takes one token and at most 256 experts");
+      a.route_logits = p.route.logits;
+      a.score_mode = p.route.score_mode;
+      a.r_exp = p.route.exp;
+      a.r_w = p.route.w;
+      a.r_cnt = p.route.cnt;
+      a.r_ecount = p.route.ecount;
+      a.r_off = p.route.off;
+      a.r_ptok = p.route.ptok;
+      a.r_pslot = p.route.pslot;
+      a.r_inv = p.route.inv;
+      a.r_active = p.route.active;
+    }
   } else {
     a.x = p.act;
     a.x_stride = p.act_stride;

@@ -211,7 +211,20 @@ struct GemvPlan {
   const int32_t *inv;
   float *out;
   const float *residual = nullptr;  // out = residual + layer output when set
+  // One token routed inside the gate/up kernel from logits [E] (E at most
+  // kFusedRouteMaxE), which also writes the arrays the router and
+  // permutation kernels would (expert, weight, count, ecount, offsets,
+  // perm_token, perm_slot, inv, active); perm_token, offsets and active
+  // above then point at those same arrays for the down pass.
+  struct FusedRoute {
+    const float *logits = nullptr;
+    int score_mode = 0;
+    int32_t *exp = nullptr, *cnt = nullptr, *ecount = nullptr, *off = nullptr, *ptok = nullptr,
+            *pslot = nullptr, *inv = nullptr, *active = nullptr;
+    float *w = nullptr;
+  } route;
 };
+constexpr int kFusedRouteMaxE = 256;
 int launch_gemv_gateup(nx_ctx *c, const GemvPlan &p);
 // out[t][r] = sum_c W[r][c] x[t][c] for one resident matrix (x rows pl.cols
 // floats apart, out rows pl.rows floats apart)
