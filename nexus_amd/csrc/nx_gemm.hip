@@ -13,7 +13,7 @@
 // waves owns a 128 x 64NT output tile (gate/up: two of them, for the gate
 // and the up rows); wave w owns weight rows 16NT w .. 16NT w + 16NT - 1 of
 // the tile for all 128 pairs, as NT x 8 v_mfma_f32_16x16x32 tiles per
-// matrix (NT = 4 for gate/up, 2 for down; see GemmShape).
+// matrix (NT = 2; see GemmShape).
 //
 // Operand order.  The K loop takes 64 positions per step.  Position
 // j = 64 ks + 16 q + i is value i of the lanes of quarter q (lanes 16q ..
@@ -399,11 +399,8 @@ __device__ __forceinline__ void static_for(F &&f) {
 // Kernel shape per format and pass.  NT = 16-row weight sets per wave
 // (the tile has 64 NT weight rows), PAIR = code loads of steps 2k and 2k+1
 // issued back to back (both halves of the same lines, the second load hits
-// the cache), OCC = workgroups per CU.  Gate/up waves own 64 rows (their 256
-// accumulators fill the AGPRs, one workgroup per CU), so each activation
-// stage meets twice the weights; the down pass keeps 32 rows per wave and
-// two workgroups per CU; F32 codes take 4 loads per row per step and are not
-// paired.
+// the cache), OCC = workgroups per CU.  Both passes keep 32 rows per wave
+// (NT = 2) and two workgroups per CU; F32 takes one workgroup per CU.
 template <int FMT, bool GATEUP>
 struct GemmShape {
   static constexpr int NT = 2;

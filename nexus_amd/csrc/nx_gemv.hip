@@ -242,9 +242,14 @@ struct RowGroup {
   // row_of(t) gives the row of the activation matrix for token t of the slot;
   // one buffer resource per row, sized to the row, so columns past the row
   // (padding, absent segments) and absent tokens read as zero.
+  // Raw activations of this lane's segments for one token group: loaded by
+  // load_x_issue, converted into the operands by load_x_prep.  Between the
+  // two, loads issued later (weights) stay in flight while the conversion
+  // waits only for the activations, which went out first.
+  using XRaw = float[SPL][NT][EPS];
   template <class RowOf>
-  __device__ __forceinline__ void load_x(const float *xbase, int xstride, const SlotView &v, int t0,
-                                         RowOf row_of) {
+  __device__ __forceinline__ void load_x_issue(XRaw &x, const float *xbase, int xstride,
+                                               const SlotView &v, int t0, RowOf row_of) const {
     // the token group is wave-uniform (see slot_view)
     const int t0u = __builtin_amdgcn_readfirstlane(t0);
 #pragma unroll
@@ -257,25 +262,38 @@ struct RowGroup {
       for (int m = 0; m < SPL; ++m) {
         const int j = li + m * L;
         const bool jv = j < v.nseg;
-        float x[EPS];
 #pragma unroll
         for (int e = 0; e < EPS; e += 4) {
           const uint32_t xo = jv ? (uint32_t)S::xidx(j, e) * 4u : OOB;
           if constexpr (FMT == NX_FMT_F32) {
             // rows of odd length: element-wise so that each load is wholly in or out
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[e + i] = __uint_as_float(bload4(xr, xo + 4u * i));
+            for (int i = 0; i < 4; ++i) x[m][t][e + i] = __uint_as_float(bload4(xr, xo + 4u * i));
           } else {
             const uint4 f = bload16(xr, xo);
-            x[e] = __uint_as_float(f.x);
-            x[e + 1] = __uint_as_float(f.y);
-            x[e + 2] = __uint_as_float(f.z);
-            x[e + 3] = __uint_as_float(f.w);
+            x[m][t][e] = __uint_as_float(f.x);
+            x[m][t][e + 1] = __uint_as_float(f.y);
+            x[m][t][e + 2] = __uint_as_float(f.z);
+            x[m][t][e + 3] = __uint_as_float(f.w);
           }
         }
-        S::prep(x, xv[m][t]);
       }
     }
+  }
+  __device__ __forceinline__ void load_x_prep(const XRaw &x) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int m = 0; m < SPL; ++m) S::prep(x[m][t], xv[m][t]);
+  }
+  // one buffer resource per row, sized to the row, so columns past the row
+  // (padding, absent segments) and absent tokens read as zero.
+  template <class RowOf>
+  __device__ __forceinline__ void load_x(const float *xbase, int xstride, const SlotView &v, int t0,
+                                         RowOf row_of) {
+    XRaw x;
+    load_x_issue(x, xbase, xstride, v, t0, row_of);
+    load_x_prep(x);
   }
 
   // Workgroup-cooperative activations, for row groups of one whole wave
@@ -429,11 +447,11 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   RG g;
   g.init(KSPLIT == 1 ? (lane % LPR) : tid);
   float xq[NT][RG::XQ];  // activation quarters in flight (COOP)
-  bool x_issued = false;
+  bool x_issued = false;  // set only by the in-kernel routing (NT == 1)
 
   const int32_t *active = a.active, *offsets = a.offsets, *perm_token = a.perm_token;
   int n_active;
-  if constexpr (!PLAIN) {
+  if constexpr (!PLAIN && NT == 1) {
     // one token routed here: ids of the routed experts in ascending order
     // (the permutation's active list), each with one pair at its rank
     __shared__ int32_t s_active[64];
@@ -462,6 +480,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
       n_active = a.active[a.E];
     }
   } else {
+    // (in-kernel routing takes one token, which runs the NT == 1 instances)
     n_active = a.active ? a.active[a.E] : 1;
   }
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
@@ -566,7 +585,9 @@ template <int FMT, int LPR, int KSPLIT, int SPL, int NT, bool YLDS>
 __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a) {
   constexpr int L = LPR * KSPLIT;
   constexpr int GROUPS = 256 / L;
-  constexpr int U = NT == 1 ? 4 : 2;  // rows per pipeline stage
+  constexpr int U = 2;  // rows per pipeline stage
+  // pipeline stages: three where the registers allow (one segment per lane)
+  constexpr int S = (SPL == 1 && L >= 64) ? 3 : 2;
   using RG = RowGroup<FMT, L, SPL, NT, U, 1>;
   extern __shared__ float ypart_lds[];
   const int tid = threadIdx.x, tl = tid & 255, lane = tl & 63;
@@ -608,7 +629,11 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
       }
     }
   };
-  auto finish = [&](const typename RG::Stage &st, const SlotView &v, const Pos &p) {
+  // what finishing a stage needs of its slot and position
+  struct StageInfo {
+    int si, t0, r, pair0, count, cols, nseg;
+  };
+  auto finish = [&](const typename RG::Stage &st, const StageInfo &p) {
     float acc[U][1][NT];
     g.template compute<LPR>(st, acc);
     if (writer) {
@@ -618,43 +643,63 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
         if (r >= row_end) continue;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          if (p.t0 + t >= v.count) continue;
-          ybuf[((size_t)kpart * npairs + v.pair0 + p.t0 + t) * wg_rows + (r - rb0)] = acc[u][0][t];
+          if (p.t0 + t >= p.count) continue;
+          ybuf[((size_t)kpart * npairs + p.pair0 + p.t0 + t) * wg_rows + (r - rb0)] = acc[u][0][t];
         }
       }
     }
   };
 
   if (row_begin < row_end && half < n_slots) {  // uniform within the row group
-    Pos pc{half, 0, row_begin};
-    SlotView vc = slot_view(a, half, n_active, a.active, a.offsets);
-    Pos pl = pc;
-    SlotView vl = vc;
-    typename RG::Stage A, B;
-    // activations go out before weight loads issued at the same time, so
-    // waiting for them does not wait for those weights
-    g.load_x(a.x, a.x_stride, vc, pc.t0, [&](int t) { return vc.pair0 + t; });
-    g.load(A, vc, pc.r, row_end);
-    bool first = true;
-    while (true) {
-      if (pc.r == row_begin && !first)
-        g.load_x(a.x, a.x_stride, vc, pc.t0, [&](int t) { return vc.pair0 + t; });
-      first = false;
-      advance(pl, vl);
-      if (pl.si < n_slots) g.load(B, vl, pl.r, row_end);
-      finish(A, vc, pc);
-      if (pl.si >= n_slots) break;
-      pc = pl;
-      vc = vl;
-
-      if (pc.r == row_begin)
-        g.load_x(a.x, a.x_stride, vc, pc.t0, [&](int t) { return vc.pair0 + t; });
-      advance(pl, vl);
-      if (pl.si < n_slots) g.load(A, vl, pl.r, row_end);
-      finish(B, vc, pc);
-      if (pl.si >= n_slots) break;
-      pc = pl;
-      vc = vl;
+    // S-stage register pipeline over the sequence of (slot, token group,
+    // rows) positions: stage i is decoded while the next S - 1 are in flight
+    Pos pl{half, 0, row_begin};  // next position to issue
+    SlotView vl = slot_view(a, half, n_active, a.active, a.offsets);
+    typename RG::Stage st[S];
+    StageInfo info[S];
+    bool valid[S];
+    auto issue = [&](int j) {
+      valid[j] = pl.si < n_slots;
+      if (valid[j]) {
+        info[j] = StageInfo{pl.si, pl.t0, pl.r, vl.pair0, vl.count, vl.cols, vl.nseg};
+        g.load(st[j], vl, pl.r, row_end);
+        advance(pl, vl);
+      }
+    };
+    // Loads complete in issue order as far as the wait counts go: the first
+    // group's activations go out first, then the first weight stages, and
+    // only then does the conversion wait (for the activations alone).  Later
+    // groups load theirs before the next stage is issued.
+    {
+      typename RG::XRaw xr;
+      g.load_x_issue(xr, a.x, a.x_stride, vl, 0, [&](int t) { return vl.pair0 + t; });
+#pragma unroll
+      for (int i = 0; i < S - 1; ++i) issue(i);
+      g.load_x_prep(xr);
+    }
+    int xsi = half, xt0 = 0;  // the token group whose activations are prepared
+    bool done = false;
+    while (!done) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        if (!valid[i]) {
+          done = true;
+          break;
+        }
+        const StageInfo &p = info[i];
+        if (p.si != xsi || p.t0 != xt0) {
+          SlotView vx;
+          vx.pair0 = p.pair0;
+          vx.count = p.count;
+          vx.cols = p.cols;
+          vx.nseg = p.nseg;
+          g.load_x(a.x, a.x_stride, vx, p.t0, [&](int t) { return p.pair0 + t; });
+          xsi = p.si;
+          xt0 = p.t0;
+        }
+        issue((i + S - 1) % S);
+        finish(st[i], p);
+      }
     }
   }
 
