@@ -44,8 +44,8 @@ Q4K_BYTES_PER_WEIGHT = 144.0 / 256.0
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200)
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--tokens", type=int, default=1)
     p.add_argument("--replicas", type=int, default=4)
     p.add_argument("--path", default="gemv", choices=["auto", "gemv", "mfma_f16", "mfma_bf16"])
