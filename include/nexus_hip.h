@@ -88,6 +88,9 @@ extern "C" {
 #define NX_PATH_GEMV 1      /* dequant-in-register GEMV, fp32 accumulate */
 #define NX_PATH_MFMA_F16 2  /* LDS-dequant grouped GEMM on fp16 MFMA, fp32 accumulate */
 #define NX_PATH_MFMA_BF16 3 /* same on bf16 MFMA */
+#define NX_PATH_MFMA_SPLIT 4 /* few tokens per expert (decode batches), Q4_K: fp16 MFMA on the raw
+                                codes with activations split into two fp16 halves, sub-block
+                                scales applied to the products; no dequantization */
 
 /* expert matrix roles */
 #define NX_ROLE_GATE 0 /* [ff_dim x hidden] */

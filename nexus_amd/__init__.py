@@ -24,7 +24,7 @@ NX_ERR_OOM, NX_ERR_TRUNCATED, NX_ERR_NO_ROUTES, NX_ERR_NOT_FOUND, NX_ERR_IO = 5,
 Q4K_REFERENCE, Q4K_GGML = 0, 1
 F32, Q4_0, Q8_0, Q4_K, Q2_K = 0, 2, 8, 12, 10
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
-PATH_AUTO, PATH_GEMV, PATH_MFMA_F16, PATH_MFMA_BF16 = 0, 1, 2, 3
+PATH_AUTO, PATH_GEMV, PATH_MFMA_F16, PATH_MFMA_BF16, PATH_MFMA_SPLIT = 0, 1, 2, 3, 4
 ROLE_GATE, ROLE_UP, ROLE_DOWN = 0, 1, 2
 EXPERT_SHARED = -1
 FORMAT_NAMES = {F32: "F32", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q2_K: "Q2_K"}

@@ -812,7 +812,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   if (T < 0) return fail(NX_ERR_INVALID_ARG, "negative token count");
   if (score_mode != NX_SCORE_SOFTMAX && score_mode != NX_SCORE_SIGMOID)
     return fail(NX_ERR_INVALID_ARG, "unknown score mode");
-  if (path < NX_PATH_AUTO || path > NX_PATH_MFMA_BF16) return fail(NX_ERR_INVALID_ARG, "unknown path");
+  if (path < NX_PATH_AUTO || path > NX_PATH_MFMA_SPLIT) return fail(NX_ERR_INVALID_ARG, "unknown path");
   if (k <= 0) return fail(NX_ERR_NO_ROUTES, "MoE router produced no routes");  // src/engine/mod.rs:989-991
   if (T == 0) return NX_OK;
   if (!d_x || !d_logits || !d_out) return fail(NX_ERR_INVALID_ARG, "null buffer");
@@ -837,7 +837,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
 
   int use = path;
   if (ex->fmt == NX_FMT_Q2_K) {  // no MFMA operand path for Q2_K
-    if (use == NX_PATH_MFMA_F16 || use == NX_PATH_MFMA_BF16)
+    if (use == NX_PATH_MFMA_F16 || use == NX_PATH_MFMA_BF16 || use == NX_PATH_MFMA_SPLIT)
       return fail(NX_ERR_UNSUPPORTED, "Q2_K experts run on the GEMV path only");
     use = NX_PATH_GEMV;
   }
@@ -871,6 +871,20 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
     NX_TRY(launch_gemv_gateup(c, gp));
     NX_TRY(launch_gemv_down(c, gp));
     return NX_OK;
+  }
+
+  if (use == NX_PATH_MFMA_SPLIT) {
+    if (ex->fmt != NX_FMT_Q4_K)
+      return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path takes Q4_K experts");
+    if (shared) return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path has no shared expert");
+    const int max_tiles = mfv_max_tiles(T, k, E);
+    int32_t *d_tiles;
+    NX_TRY(ws(c, WS_TILES, 2 + 2 * (size_t)max_tiles, &d_tiles));
+    NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
+    NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, kMfvTileM, d_ec, d_off, d_pt, d_ps, d_inv,
+                          d_act, d_tiles, 0));
+    MfvPlan mp{ex, T, k, d_x, d_pt, d_off, d_tiles, max_tiles, d_w, d_cnt, d_inv, d_out, d_residual};
+    return launch_mfv(c, mp);
   }
 
   // grouped GEMM on MFMA

@@ -139,6 +139,7 @@ enum WsSlot {
   WS_BLK_HIDDEN,
   WS_MAT_X,    // device copy of matvec inputs for blocking calls
   WS_MAT_Y,
+  WS_MFV_PART, // gate/up partial sums of the split-activation MFMA path
 };
 
 int ws_get(nx_ctx *c, int slot, size_t bytes, void **out);
@@ -255,6 +256,26 @@ struct GemmPlan {
 // to the output in the combine (d_out may equal d_residual)
 int moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const float *d_logits, int T,
                 int k, int score_mode, int path, float *d_out, const float *d_residual);
+// few-token grouped matvec on MFMA (Q4_K): gate/up over K slices, SwiGLU of
+// the summed slices, down over K slices, then the combine (summing the down
+// slices in order) into out (+ residual)
+struct MfvPlan {
+  const nx_experts *ex;
+  int T, k;
+  const float *x;             // [T][H], 16-byte aligned
+  const int32_t *perm_token;  // [pairs]
+  const int32_t *offsets;     // [E+1]
+  const int32_t *tiles;       // tile list of the permutation with tile_m = kMfvTileM
+  int max_tiles;              // grid bound for the tile list
+  const float *rw;            // combine inputs
+  const int32_t *rcnt;
+  const int32_t *inv;
+  float *out;
+  const float *residual;
+};
+int launch_mfv(nx_ctx *c, const MfvPlan &p);
+int mfv_max_tiles(int T, int k, int E);
+constexpr int kMfvTileM = 16;
 int gemm_tile_m();
 int gemm_down_ksplit(int fmt, int F, int H, int tiles, int slots);
 // width of a row of GEMM operands (operand order pads to whole scale windows)

@@ -1,0 +1,434 @@
+// nx_mfv.hip — few-token grouped matvec on MFMA for Q4_K experts: decode
+// batches whose experts see a handful of tokens each (2 to ~128 tokens).
+//
+// The decode GEMV's exact integer dot costs about one instruction per
+// weight per token, so its time grows with the tokens an expert sees; the
+// prefill GEMM dequantizes every weight into its operands, which costs the
+// same at 8 tokens as at 128.  Here the weights are never dequantized:
+//
+//   sum_i w_i x_i over a 32-weight sub-block s of a Q4_K block
+//     = (d sc_s) sum_i q_i x_i  -  (dmin m_s) sum_i x_i
+//
+// (src/quant/mod.rs:820-849: w_i = d sc_s q_i - dmin m_s).  The code
+// nibbles q_i become fp16 operands by a byte permute alone: with the bits of
+// q in the low mantissa bits and a zero exponent, the fp16 value is q 2^-24
+// (a subnormal, exact), and 2^24 goes into the row's sub-block scale.  One
+// v_mfma_f32_16x16x32_f16 then forms sum_i q_i x_i for 16 rows x 16 pairs
+// over the sub-block, and the scales are applied to its output.
+//
+// Activations keep close to fp32 precision: per pair and 256-element chunk
+// they are scaled by a power of two so the chunk maximum lies in
+// [2^13, 2^14), split into x' = hi + lo with hi = fp16(x') and lo =
+// fp16(x' - hi), and both halves go through the MFMA (two MFMAs per
+// sub-block, chained).  hi + lo carries 22 bits of x', so the dot products
+// match an fp32 evaluation to a few units of 2^-22 of the chunk maximum.
+//
+// Work: a workgroup of 4 waves owns one tile of up to 16 pairs of one
+// expert (the permutation's tile list with tile_m = 16) and 64 weight rows
+// (of both matrices for gate/up); wave w owns 16 of them (RT row tiles of
+// 16).  The K loop takes one Q4_K block (256 positions) per
+// chunk.  The activation chunk of the 16 pairs is staged through a
+// double-buffered LDS area in MFMA operand layout, together with each
+// pair's sub-block sums and unscale factor; every lane reads its operands
+// for the chunk once and applies them to all of its row tiles.  The codes
+// and scales of the next chunk are in flight while a chunk is computed.
+#include "nx_device.hpp"
+#include "nx_internal.hpp"
+
+namespace nx {
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int MV_M = 16;   // pairs per tile
+constexpr int MV_K = 256;  // K positions per chunk (one Q4_K block)
+
+struct MfvArgs {
+  const uint8_t *qs0, *qs1, *meta0, *meta1;  // role planes (gate, up) or (down, -)
+  size_t qs_stride, meta_stride;             // per expert
+  uint32_t row_qs, row_meta;
+  int rows, nseg, nchunk;                    // nchunk = cols / 256
+  const float *x;
+  int x_stride;
+  const int32_t *perm_token;  // gate/up: pair -> token row of x; down: null (pair row)
+  const int32_t *offsets;     // [E + 1]
+  const int32_t *tiles;       // [0] = tile count, [1] unused, then (expert, first pair within it)
+  float *out;                 // partial sums: [slice][pair][out_stride]
+  int out_stride;             // gate/up: 2 F (gate rows, then up rows); down: H
+  size_t out_split;           // floats between slices
+};
+
+// LDS area of one chunk: the A operands (hi, lo) of 8 sub-blocks in lane
+// order, the sub-block sums X[pair][s] and the per-pair unscale factors
+struct MfvStage {
+  uint4 a[8][2][64];  // [sub-block][hi, lo][lane]
+  float xs[MV_M][8];
+  float sx[MV_M];
+};
+
+// 8 codes of a dword (q ^ 8 nibbles, byte i = element i (low) | element 4+i
+// (high)) as fp16 operands q 2^-24 in nibble order: operand p = nibble p
+__device__ __forceinline__ f16x8 codes_to_f16(uint32_t c) {
+  c ^= 0x88888888u;
+  const uint32_t lo = c & 0x0F0F0F0Fu, hi = (c >> 4) & 0x0F0F0F0Fu;
+  uint32_t d[4];
+  // dword k = (lo byte k) | (hi byte k) << 16; selector 0x0C gives a zero byte
+  d[0] = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u);
+  d[1] = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u);
+  d[2] = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u);
+  d[3] = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u);
+  return __builtin_bit_cast(f16x8, d);
+}
+
+// element of sub-block group g held in operand position p: the nibble order
+// of a code dword (positions 2i, 2i+1 = elements i, 4+i)
+__device__ __forceinline__ constexpr int opos_elem(int p) { return (p & 1) * 4 + (p >> 1); }
+
+// one (row tile, chunk) step of a lane: dword (lane / 16) of each sub-block's
+// code half, and the block's scales (d, dmin, scales12)
+template <int NMAT>
+struct MfvStep {
+  uint32_t q[NMAT][8];
+  uint4 m[NMAT];
+};
+
+// Workgroup = (row block of 256 rows, tile of <= 16 pairs, K slice of
+// MV_KS chunks).  Prologue: the slice's activations of the tile's pairs are
+// staged once into LDS (one barrier).  Then wave w streams rows
+// 64 w .. 64 w + 63 of the block as 4 row tiles x MV_KS chunks = 16 steps,
+// with the codes of the next MV_D steps in flight.  Each workgroup writes
+// its slice's partial sums: gate/up to part[slice][pair][2][F] (gate, then
+// up), down to part[slice][pair][H].
+constexpr int MV_KS = 4;   // chunks per K slice
+constexpr int MV_RTW = 4;  // row tiles per wave
+constexpr int MV_D = 4;    // steps in flight
+constexpr int MV_WG_ROWS = 4 * 16 * MV_RTW;
+
+template <bool GATEUP>
+__global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
+  constexpr int NMAT = GATEUP ? 2 : 1;
+  constexpr int NSTEP = MV_RTW * MV_KS;
+  __shared__ MfvStage stage[MV_KS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = blockIdx.y;
+  if (tile >= a.tiles[0]) return;  // workgroup-uniform
+  // tile t: expert tiles[2 + 2t], first pair tiles[3 + 2t] within the expert
+  const int e = __builtin_amdgcn_readfirstlane(a.tiles[2 + 2 * tile]);
+  const int pair0 = __builtin_amdgcn_readfirstlane(a.offsets[e] + a.tiles[3 + 2 * tile]);
+  const int cnt = __builtin_amdgcn_readfirstlane(min(MV_M, a.offsets[e + 1] - pair0));
+  const int slice = blockIdx.z;
+  const int c0 = slice * MV_KS;  // first chunk of the slice
+  const int row_base = blockIdx.x * MV_WG_ROWS + wave * 16 * MV_RTW;
+
+  // ---- stage the slice: thread t owns positions 16j .. 16j+15 of every
+  // chunk of pair m = t / 16; chunks past the row read as zeros
+  {
+    const int sm = tid >> 4, sj = tid & 15;
+    const float *xrow = nullptr;
+    if (sm < cnt) {
+      const int r = a.perm_token ? a.perm_token[pair0 + sm] : pair0 + sm;
+      xrow = a.x + (size_t)r * a.x_stride;
+    }
+    // every lane loads (absent pairs and chunks from row 0 of x, then
+    // zeroed), so the loads are not branched around
+    const bool pv = xrow != nullptr;
+    if (!pv) xrow = a.x;
+    float xv[MV_KS][16];
+#pragma unroll
+    for (int kc = 0; kc < MV_KS; ++kc) {
+      const bool v = pv && c0 + kc < a.nchunk;
+      const float *src = xrow + (size_t)(v ? c0 + kc : 0) * MV_K + 16 * sj;
+#pragma unroll
+      for (int q = 0; q < 16; q += 4) {
+        const float4 f = *reinterpret_cast<const float4 *>(src + q);
+        xv[kc][q] = v ? f.x : 0.f;
+        xv[kc][q + 1] = v ? f.y : 0.f;
+        xv[kc][q + 2] = v ? f.z : 0.f;
+        xv[kc][q + 3] = v ? f.w : 0.f;
+      }
+    }
+#pragma unroll
+    for (int kc = 0; kc < MV_KS; ++kc) {
+      MfvStage &st = stage[kc];
+      float mx = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, fabsf(xv[kc][v]));
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      // max|x| < 2^E; scale the chunk maximum into [2^13, 2^14)
+      int E = 0;
+      if (mx > 0.f && mx <= 3.4e38f) {
+        (void)frexpf(mx, &E);
+        E = max(E, -100);
+      }
+      const float up = __builtin_amdgcn_ldexpf(1.0f, 14 - E);
+      // x' = x 2^(14-E) = hi + lo; the sub-block sums are of hi + lo, the
+      // values the operands carry
+      _Float16 hv[16], lv[16];
+      float sum = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float sv = xv[kc][v] * up;
+        hv[v] = (_Float16)sv;
+        lv[v] = (_Float16)(sv - (float)hv[v]);
+        sum += (float)hv[v] + (float)lv[v];
+      }
+      // operands: position p of group g holds element 8g + opos_elem(p)
+      const int s = sj >> 1;        // sub-block
+      const int g0 = 2 * (sj & 1);  // first of this thread's two groups
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        _Float16 ho[8], lo[8];
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          ho[p] = hv[8 * gg + opos_elem(p)];
+          lo[p] = lv[8 * gg + opos_elem(p)];
+        }
+        const int L = sm + 16 * (g0 + gg);
+        st.a[s][0][L] = __builtin_bit_cast(uint4, ho);
+        st.a[s][1][L] = __builtin_bit_cast(uint4, lo);
+      }
+      sum += __shfl_xor(sum, 1, 64);  // the other half of the sub-block
+      if ((sj & 1) == 0) st.xs[sm][s] = sum;
+      if (sj == 0) st.sx[sm] = __builtin_amdgcn_ldexpf(1.0f, E - 14);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();
+
+  // ---- weights: lane holds row (lane % 16) of each row tile and K group
+  // (lane / 16) of every sub-block
+  const int l16 = lane & 15, g = lane >> 4;
+  __amdgpu_buffer_rsrc_t rq[NMAT], rm[NMAT];
+  {
+    const uint32_t nq = (uint32_t)a.rows * a.row_qs, nm = (uint32_t)a.rows * a.row_meta;
+    rq[0] = make_rsrc(a.qs0 + (size_t)e * a.qs_stride, nq);
+    rm[0] = make_rsrc(a.meta0 + (size_t)e * a.meta_stride, nm);
+    if constexpr (NMAT == 2) {
+      rq[1] = make_rsrc(a.qs1 + (size_t)e * a.qs_stride, nq);
+      rm[1] = make_rsrc(a.meta1 + (size_t)e * a.meta_stride, nm);
+    }
+  }
+  // step i: row tile i / MV_KS, chunk c0 + i % MV_KS
+  // Rows past the matrix read as zeros through the resources' size (row *
+  // row_qs >= rows * row_qs); a chunk past the row (wave-uniform) reads at
+  // OOB.  Per-lane parts of the offsets stay in one register per step; the
+  // rest goes in the scalar offset.
+  auto issue = [&](MfvStep<NMAT> &w, int i) {
+    const int row = row_base + 16 * (i / MV_KS) + l16;
+    const int c = c0 + i % MV_KS;
+    // the chunk's 4 segments share one group of 64: their halves h sit at
+    // base + 16 (s & 3) + h 16 gsz (all wave-uniform); the lane adds its row
+    // and its dword 4 g
+    const int j0 = 4 * c;
+    const int grp = j0 >> 6;
+    const int gsz = min(64, a.nseg - (grp << 6));
+    const uint32_t base = (uint32_t)(grp * 2048 + (j0 & 63) * 16);
+    const bool cv = c < a.nchunk;  // wave-uniform
+    const uint32_t vq = cv ? (uint32_t)row * a.row_qs + 4u * g : OOB;
+    const uint32_t vm = cv ? (uint32_t)row * a.row_meta + 16u * c : OOB;
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const uint32_t so = base + 16u * (s & 3) + (s >> 2) * 16u * gsz;
+        w.q[mt][s] = __builtin_amdgcn_raw_buffer_load_b32(rq[mt], (int)vq, (int)so, 0);
+      }
+      w.m[mt] = bload16(rm[mt], vm);
+    }
+  };
+
+  // step (row tile rt, chunk kc) into accr, the row tile's accumulators
+  auto compute = [&](const MfvStep<NMAT> &w, const MfvStage &st, f32x4 (&accr)[NMAT]) {
+    float sx[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sx[k] = st.sx[4 * g + k];
+    f32x4 ch[NMAT];
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) ch[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float d[NMAT], dmin[NMAT];
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) {
+      d[mt] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x & 0xFFFF));
+      dmin[mt] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x >> 16));
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const f16x8 ahi = __builtin_bit_cast(f16x8, st.a[s][0][lane]);
+      const f16x8 alo = __builtin_bit_cast(f16x8, st.a[s][1][lane]);
+      float xs[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xs[k] = st.xs[4 * g + k][s];
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt) {
+        // get_scale_min_k4 (src/quant/mod.rs:1163-1170) on scales12
+        const uint32_t p03 = w.m[mt].y, p47 = w.m[mt].z, p8b = w.m[mt].w;
+        int sc, mn;
+        if (s < 4) {
+          sc = (p03 >> (8 * s)) & 63;
+          mn = (p47 >> (8 * s)) & 63;
+        } else {
+          const int j = s - 4;
+          sc = ((p8b >> (8 * j)) & 15) | (((p03 >> (8 * j + 6)) & 3) << 4);
+          mn = ((p8b >> (8 * j + 4)) & 15) | (((p47 >> (8 * j + 6)) & 3) << 4);
+        }
+        const float as = d[mt] * (float)sc * 16777216.0f;  // operands carry 2^-24
+        const float cs = dmin[mt] * (float)mn;
+        const f16x8 b = codes_to_f16(w.q[mt][s]);
+        f32x4 y = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        y = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, y, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ch[mt][k] = fmaf(as, y[k], fmaf(-cs, xs[k], ch[mt][k]));
+      }
+      // finish each sub-block's scale products here: left to itself the
+      // compiler keeps every sub-block's MFMA output to apply the scales at
+      // the end, which needs more registers than there are
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+        asm volatile("" : "+v"(ch[mt][0]), "+v"(ch[mt][1]), "+v"(ch[mt][2]), "+v"(ch[mt][3]));
+    }
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) accr[mt][k] = fmaf(sx[k], ch[mt][k], accr[mt][k]);
+  };
+
+  // steps i = MV_KS rt + kc; ring slot i % MV_D = kc (MV_D == MV_KS)
+  static_assert(MV_D == MV_KS, "ring slots are the chunk index");
+  float *out = a.out + (size_t)slice * a.out_split;
+  MfvStep<NMAT> ring[MV_D];
+#pragma unroll
+  for (int i = 0; i < MV_D - 1; ++i) issue(ring[i], i);
+#pragma unroll 1
+  for (int rt = 0; rt < MV_RTW; ++rt) {
+    f32x4 accr[NMAT];
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) accr[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < MV_KS; ++kc) {
+      const int i = MV_KS * rt + kc;
+      // the staged operands do not change over the row tiles: keep the
+      // compiler from hoisting every step's LDS reads out of the loop (they
+      // would need 256 registers)
+      asm volatile("" ::: "memory");
+      if (i + MV_D - 1 < NSTEP) issue(ring[(kc + MV_D - 1) % MV_D], i + MV_D - 1);
+      compute(ring[kc], stage[kc], accr);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // partial sums of the slice: lane holds row (lane % 16), pairs 4g .. 4g+3
+    const int row = row_base + 16 * rt + l16;
+    if (row < a.rows) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int m = 4 * g + k;
+        if (m >= cnt) continue;
+        const size_t o = (size_t)(pair0 + m) * a.out_stride + row;
+        out[o] = accr[0][k];
+        if constexpr (GATEUP) out[o + a.rows] = accr[1][k];
+      }
+    }
+  }
+}
+
+// act[p][f] = silu(sum_s gate_s[p][f]) * sum_s up_s[p][f] over the K slices
+// of the gate/up pass, summed in slice order
+__global__ __launch_bounds__(256) void k_mfv_swiglu(const float *__restrict__ part, int nslice,
+                                                    size_t slice_stride, int pairs, int F,
+                                                    float *__restrict__ act, int act_stride) {
+  const size_t n = (size_t)pairs * F;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t p = i / F, f = i - p * F;
+    const size_t o = p * 2 * F + f;
+    float gs = part[o], us = part[o + F];
+    for (int s = 1; s < nslice; ++s) {
+      gs += part[s * slice_stride + o];
+      us += part[s * slice_stride + o + F];
+    }
+    act[p * act_stride + f] = silu_mul(gs, us);
+  }
+}
+
+}  // namespace
+
+int mfv_max_tiles(int T, int k, int E) {
+  const long pairs = (long)T * k;
+  return (int)((pairs + MV_M - 1) / MV_M + std::min<long>(E, pairs));
+}
+
+int launch_mfv(nx_ctx *c, const MfvPlan &p) {
+  const nx_experts *ex = p.ex;
+  if (ex->fmt != NX_FMT_Q4_K)
+    return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path takes Q4_K experts");
+  // activation rows are read as float4 runs of whole chunks
+  if (reinterpret_cast<uintptr_t>(p.x) & 15)
+    return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path needs 16-byte aligned inputs");
+  const int H = ex->H, F = ex->F;
+  const size_t pairs = (size_t)p.T * p.k;
+  const int nks_g = (H / MV_K + MV_KS - 1) / MV_KS;
+  const int nks_d = (F / MV_K + MV_KS - 1) / MV_KS;
+  void *vg, *va, *vy;
+  NX_TRY(ws_get(c, WS_MFV_PART, (size_t)nks_g * pairs * 2 * F * sizeof(float), &vg));
+  NX_TRY(ws_get(c, WS_ACT, pairs * F * sizeof(float), &va));
+  NX_TRY(ws_get(c, WS_YPAIR, (size_t)nks_d * pairs * H * sizeof(float), &vy));
+  float *gpart = static_cast<float *>(vg), *act = static_cast<float *>(va),
+        *ypart = static_cast<float *>(vy);
+  for (int pass = 0; pass < 2; ++pass) {
+    const bool gateup = pass == 0;
+    const RolePlane &R0 = ex->role[gateup ? NX_ROLE_GATE : NX_ROLE_DOWN];
+    const RolePlane &R1 = ex->role[gateup ? NX_ROLE_UP : NX_ROLE_DOWN];
+    MfvArgs a{};
+    a.qs0 = R0.qs;
+    a.qs1 = R1.qs;
+    a.meta0 = R0.meta;
+    a.meta1 = R1.meta;
+    a.qs_stride = R0.qs_stride;
+    a.meta_stride = R0.meta_stride;
+    a.row_qs = R0.row_qs;
+    a.row_meta = R0.row_meta;
+    a.rows = R0.rows;
+    a.nseg = R0.nseg;
+    a.nchunk = R0.cols / MV_K;
+    a.offsets = p.offsets;
+    a.tiles = p.tiles;
+    if (gateup) {
+      a.x = p.x;
+      a.x_stride = H;
+      a.perm_token = p.perm_token;
+      a.out = gpart;
+      a.out_stride = 2 * F;
+      a.out_split = pairs * 2 * F;
+    } else {
+      a.x = act;
+      a.x_stride = F;
+      a.perm_token = nullptr;
+      a.out = ypart;
+      a.out_stride = H;
+      a.out_split = pairs * H;
+    }
+    const int nks = gateup ? nks_g : nks_d;
+    const dim3 grid((unsigned)((a.rows + MV_WG_ROWS - 1) / MV_WG_ROWS), (unsigned)p.max_tiles,
+                    (unsigned)nks);
+    if (gateup) {
+      NX_TRY(launch(c, "mfv_gateup",
+                    [&] { hipLaunchKernelGGL(k_mfv<true>, grid, dim3(256), 0, c->stream, a); }));
+      const size_t n = pairs * F;
+      unsigned gs = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
+      NX_TRY(launch(c, "mfv_swiglu", [&] {
+        hipLaunchKernelGGL(k_mfv_swiglu, dim3(gs), dim3(256), 0, c->stream, gpart, nks_g,
+                           pairs * 2 * F, (int)pairs, F, act, F);
+      }));
+    } else {
+      NX_TRY(launch(c, "mfv_down",
+                    [&] { hipLaunchKernelGGL(k_mfv<false>, grid, dim3(256), 0, c->stream, a); }));
+    }
+  }
+  return launch_combine(c, ypart, p.rw, p.rcnt, p.inv, p.T, p.k, H, false, p.out, nks_d,
+                        pairs * (size_t)H, p.residual);
+}
+
+}  // namespace nx

@@ -1,0 +1,82 @@
+"""Few-token MoE layer on MFMA with split-fp16 activations (NX_PATH_MFMA_SPLIT).
+
+The Q4_K codes go into fp16 MFMA operands untouched (no dequantization) and
+each 32-weight sub-block's scale and offset are applied to the products;
+activations are split per pair and 256-element chunk into two fp16 halves
+after a power-of-two scaling.  Bar: the GEMV path's, relative L2 1e-4
+against the oracle's dispatch (src/engine/mod.rs:969-1024) over the same
+payloads: 1 to 64 tokens, experts with more than 16 tokens (several tiles),
+top-8 routing, the sigmoid score mode, token rows of very different
+magnitudes and zero rows, and Mixtral's full shape; other formats and shared
+experts are rejected with NX_ERR_UNSUPPORTED.
+"""
+import numpy as np
+import pytest
+
+import nexus_amd as nx
+from moe_cases import Q4_K, Q8_0, Layer, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = nx.Context(0)
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("E,H,F,k,T,score", [
+    (8, 512, 1024, 2, 1, 0), (8, 512, 1024, 2, 5, 0), (8, 256, 768, 2, 33, 0),
+    (32, 512, 256, 8, 24, 1), (16, 1024, 512, 4, 64, 0), (4, 256, 256, 1, 40, 0)])
+def test_split_parity(ctx, E, H, F, k, T, score):
+    print(f"mfma split E={E} H={H} F={F} k={k} T={T} score={score}", flush=True)
+    L = Layer(Q4_K, E, H, F, k, T, seed=E * 5 + H + F + T, score_mode=score)
+    ex = L.upload(nx, ctx)
+    got = ex.forward(L.x, L.logits, k, score, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    assert rel_l2(got, L.oracle_out()) <= TOL
+
+
+def test_split_magnitudes_and_zero_rows(ctx):
+    L = Layer(Q4_K, 8, 512, 512, 2, 12, seed=41)
+    scale = np.array([1e-30, 1e-6, 1.0, 3e3, 1e6, 0.0, 1.0, 1e-3, 7.0, 0.0, 1e4, 1e-2],
+                     np.float32)[:, None]
+    L.x = (L.x * scale).astype(np.float32)
+    L.x[2, :256] = 0.0  # one zero chunk inside a live row
+    ex = L.upload(nx, ctx)
+    got = ex.forward(L.x, L.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    ref = L.oracle_out()
+    # per row, so that small rows are held to their own scale
+    for t in range(L.T):
+        den = np.linalg.norm(ref[t])
+        if den == 0:
+            assert np.all(got[t] == 0)
+        else:
+            assert rel_l2(got[t], ref[t]) <= TOL, t
+
+
+def test_split_mixtral_shape(ctx):
+    L = Layer(Q4_K, 8, 4096, 14336, 2, 8, seed=9)
+    ex = L.upload(nx, ctx)
+    got = ex.forward(L.x, L.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    assert rel_l2(got, L.oracle_out()) <= TOL
+
+
+def test_split_rejects(ctx):
+    L = Layer(Q8_0, 4, 256, 256, 2, 4, seed=3)
+    ex = L.upload(nx, ctx)
+    with pytest.raises(nx.NexusError) as ei:
+        ex.forward(L.x, L.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+    assert ei.value.code == nx.NX_ERR_UNSUPPORTED
+    ex.close()
+    S = Layer(Q4_K, 4, 256, 256, 2, 4, seed=4, shared_F=256)
+    ex = S.upload(nx, ctx)
+    with pytest.raises(nx.NexusError) as ei:
+        ex.forward(S.x, S.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+    assert ei.value.code == nx.NX_ERR_UNSUPPORTED
+    ex.close()
