@@ -48,7 +48,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=200)
     p.add_argument("--tokens", type=int, default=1)
     p.add_argument("--replicas", type=int, default=4)
-    p.add_argument("--path", default="gemv", choices=["auto", "gemv", "mfma_f16", "mfma_bf16"])
+    p.add_argument("--path", default="gemv",
+                   choices=["auto", "gemv", "mfma_f16", "mfma_bf16", "mfma_split"])
     p.add_argument("--cpu-tokens", type=int, default=16, help="tokens in the CPU-baseline sample")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-extra", action="store_true",
@@ -155,6 +156,15 @@ def time_steps(torch, fn, steps, warmup):
         fn(i)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def path_of(kern):
+    """The expert-product path a step ran, from its kernel names."""
+    if any(n.startswith("mfv") for n in kern):
+        return "mfma_split"
+    if any(n.startswith("gemm") for n in kern):
+        return "mfma_f16"
+    return "gemv"
 
 
 def kernel_means(ctx, torch, fn, steps):
@@ -384,7 +394,7 @@ def model_config_cases(nx, ctx, torch, args):
                 "effective_GBps": gbps, "hbm_frac": gbps / HBM_PEAK_GBPS,
                 "resident_GBps": welems * rbpw / (ms * 1e-3) / 1e9,
                 "TFLOPs": tf, "mfma_f16_frac": tf / MFMA_F16_PEAK_TFLOPS,
-                "path": "mfma_f16" if any(n.startswith("gemm") for n in kern) else "gemv",
+                "path": path_of(kern),
                 "kernels_ms": {k_: round(v, 4) for k_, v in kern.items()}}
         for s_ in sets:
             s_.close()
@@ -405,6 +415,7 @@ def main():
 
     E, H, F, k, T = 8, 4096, 14336, 2, args.tokens
     path = {"auto": nx.PATH_AUTO, "gemv": nx.PATH_GEMV, "mfma_f16": nx.PATH_MFMA_F16,
+            "mfma_split": nx.PATH_MFMA_SPLIT,
             "mfma_bf16": nx.PATH_MFMA_BF16}[args.path]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -462,7 +473,7 @@ def main():
         ms32, kern32, gu32, dn32 = decode_case(32, nx.PATH_AUTO)
         extra["decode_32_tokens"] = {
             "ms_per_step": ms32, "tokens_per_s": 32 / (ms32 * 1e-3),
-            "effective_GBps": (gu32 + dn32) / (ms32 * 1e-3) / 1e9, "path": "auto",
+            "effective_GBps": (gu32 + dn32) / (ms32 * 1e-3) / 1e9, "path": "auto: " + path_of(kern32),
             "kernels_ms": {k_: round(v, 4) for k_, v in kern32.items()}}
     if not args.no_extra:
         print("bench: MoE block, 1 token", file=sys.stderr, flush=True)

@@ -84,7 +84,8 @@ extern "C" {
 #define NX_SCORE_SIGMOID 1 /* extension: sigmoid scores renormalised over the top-k */
 
 /* expert-product paths */
-#define NX_PATH_AUTO 0      /* GEMV for few tokens per expert, MFMA otherwise */
+#define NX_PATH_AUTO 0      /* by tokens per expert: GEMV, then (Q4_K, no shared expert)
+                               the split-activation MFMA path, then the grouped GEMM */
 #define NX_PATH_GEMV 1      /* dequant-in-register GEMV, fp32 accumulate */
 #define NX_PATH_MFMA_F16 2  /* LDS-dequant grouped GEMM on fp16 MFMA, fp32 accumulate */
 #define NX_PATH_MFMA_BF16 3 /* same on bf16 MFMA */

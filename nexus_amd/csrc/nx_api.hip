@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -842,10 +843,28 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
     use = NX_PATH_GEMV;
   }
   if (use == NX_PATH_AUTO) {
-    // MFMA once experts see enough tokens on average to amortize the tile
-    // dequantization; below that the GEMV streams each weight fewer times
     const long active_max = std::min<long>(E, (long)T * k);
-    use = ((long)T * k >= 32 * active_max) ? NX_PATH_MFMA_F16 : NX_PATH_GEMV;
+    if (ex->fmt == NX_FMT_Q4_K && !shared) {
+      // Tokens per active expert, with the active count expected under
+      // uniform routing, E (1 - (1 - k/E)^T).  Measured crossovers (Mixtral
+      // and Qwen3 shapes): the GEMV re-reads an expert's weights per pair of
+      // its tokens and wins below ~2 tokens per expert; the split-activation
+      // MFMA path reads them once per 16 tokens and wins up to ~24; the
+      // grouped GEMM beyond.
+      const double kk = std::min(1.0, (double)k / E);
+      const double act = std::max(1.0, E * (1.0 - std::pow(1.0 - kk, (double)T)));
+      const double tpe = (double)T * k / act;
+      if (tpe >= 24.0)
+        use = NX_PATH_MFMA_F16;
+      else if (tpe >= 3.0 || ((long)T * k >= 64 && tpe >= 1.2))
+        use = NX_PATH_MFMA_SPLIT;
+      else
+        use = NX_PATH_GEMV;
+    } else {
+      // MFMA once experts see enough tokens on average to amortize the tile
+      // dequantization; below that the GEMV streams each weight fewer times
+      use = ((long)T * k >= 32 * active_max) ? NX_PATH_MFMA_F16 : NX_PATH_GEMV;
+    }
   }
 
   if (use == NX_PATH_GEMV) {

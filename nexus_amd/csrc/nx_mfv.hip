@@ -9,12 +9,13 @@
 //   sum_i w_i x_i over a 32-weight sub-block s of a Q4_K block
 //     = (d sc_s) sum_i q_i x_i  -  (dmin m_s) sum_i x_i
 //
-// (src/quant/mod.rs:820-849: w_i = d sc_s q_i - dmin m_s).  The code
-// nibbles q_i become fp16 operands by a byte permute alone: with the bits of
-// q in the low mantissa bits and a zero exponent, the fp16 value is q 2^-24
-// (a subnormal, exact), and 2^24 goes into the row's sub-block scale.  One
-// v_mfma_f32_16x16x32_f16 then forms sum_i q_i x_i for 16 rows x 16 pairs
-// over the sub-block, and the scales are applied to its output.
+// (src/quant/mod.rs:820-849: w_i = d sc_s q_i - dmin m_s).  The operand of
+// weight i is the integer q_i sc_s (at most 15 x 63 = 945) written as the
+// bits of an fp16 subnormal, i.e. the exact value q_i sc_s 2^-24: a byte
+// permute and a packed 16-bit multiply per two weights, no float
+// conversion.  With the 6-bit scale inside the operands, one
+// v_mfma_f32_16x16x32_f16 may span several sub-blocks, so the 8 MFMAs of a
+// block accumulate together; d 2^24 and the dmin term apply once per block.
 //
 // Activations keep close to fp32 precision: per pair and 256-element chunk
 // they are scaled by a power of two so the chunk maximum lies in
@@ -60,27 +61,12 @@ struct MfvArgs {
   size_t out_split;           // floats between slices
 };
 
-// LDS area of one chunk: the A operands (hi, lo) of 8 sub-blocks in lane
-// order, the sub-block sums X[pair][s] and the per-pair unscale factors
+// LDS area of one chunk: the A operands (hi, lo) of the 8 MFMAs in lane
+// order and the per-pair unscale factors
 struct MfvStage {
-  uint4 a[8][2][64];  // [sub-block][hi, lo][lane]
-  float xs[MV_M][8];
+  uint4 a[8][2][64];  // [MFMA][hi, lo][lane]
   float sx[MV_M];
 };
-
-// 8 codes of a dword (q ^ 8 nibbles, byte i = element i (low) | element 4+i
-// (high)) as fp16 operands q 2^-24 in nibble order: operand p = nibble p
-__device__ __forceinline__ f16x8 codes_to_f16(uint32_t c) {
-  c ^= 0x88888888u;
-  const uint32_t lo = c & 0x0F0F0F0Fu, hi = (c >> 4) & 0x0F0F0F0Fu;
-  uint32_t d[4];
-  // dword k = (lo byte k) | (hi byte k) << 16; selector 0x0C gives a zero byte
-  d[0] = __builtin_amdgcn_perm(hi, lo, 0x0C040C00u);
-  d[1] = __builtin_amdgcn_perm(hi, lo, 0x0C050C01u);
-  d[2] = __builtin_amdgcn_perm(hi, lo, 0x0C060C02u);
-  d[3] = __builtin_amdgcn_perm(hi, lo, 0x0C070C03u);
-  return __builtin_bit_cast(f16x8, d);
-}
 
 // element of sub-block group g held in operand position p: the nibble order
 // of a code dword (positions 2i, 2i+1 = elements i, 4+i)
@@ -90,7 +76,7 @@ __device__ __forceinline__ constexpr int opos_elem(int p) { return (p & 1) * 4 +
 // code half, and the block's scales (d, dmin, scales12)
 template <int NMAT>
 struct MfvStep {
-  uint32_t q[NMAT][8];
+  uint4 q[NMAT][2];  // sub-block g's code half, then sub-block g + 4's
   uint4 m[NMAT];
 };
 
@@ -169,31 +155,31 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
       // x' = x 2^(14-E) = hi + lo; the sub-block sums are of hi + lo, the
       // values the operands carry
       _Float16 hv[16], lv[16];
-      float sum = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const float sv = xv[kc][v] * up;
         hv[v] = (_Float16)sv;
         lv[v] = (_Float16)(sv - (float)hv[v]);
-        sum += (float)hv[v] + (float)lv[v];
       }
-      // operands: position p of group g holds element 8g + opos_elem(p)
-      const int s = sj >> 1;        // sub-block
-      const int g0 = 2 * (sj & 1);  // first of this thread's two groups
+      // Operands: MFMA u (0..7), lane group g takes elements
+      // 32 g + 8 u (u < 4) or 128 + 32 g + 8 (u - 4) (u >= 4), position p
+      // holding element + opos_elem(p).  This thread's 16 positions
+      // 16 sj .. 16 sj + 15 are those of group g = (sj % 8) / 2, MFMAs
+      // u0, u0 + 1 with u0 = 4 (sj / 8) + 2 (sj % 2).
+      const int gq = (sj & 7) >> 1;
+      const int u0 = 4 * (sj >> 3) + 2 * (sj & 1);
 #pragma unroll
-      for (int gg = 0; gg < 2; ++gg) {
+      for (int uu = 0; uu < 2; ++uu) {
         _Float16 ho[8], lo[8];
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-          ho[p] = hv[8 * gg + opos_elem(p)];
-          lo[p] = lv[8 * gg + opos_elem(p)];
+          ho[p] = hv[8 * uu + opos_elem(p)];
+          lo[p] = lv[8 * uu + opos_elem(p)];
         }
-        const int L = sm + 16 * (g0 + gg);
-        st.a[s][0][L] = __builtin_bit_cast(uint4, ho);
-        st.a[s][1][L] = __builtin_bit_cast(uint4, lo);
+        const int L = sm + 16 * gq;
+        st.a[u0 + uu][0][L] = __builtin_bit_cast(uint4, ho);
+        st.a[u0 + uu][1][L] = __builtin_bit_cast(uint4, lo);
       }
-      sum += __shfl_xor(sum, 1, 64);  // the other half of the sub-block
-      if ((sj & 1) == 0) st.xs[sm][s] = sum;
       if (sj == 0) st.sx[sm] = __builtin_amdgcn_ldexpf(1.0f, E - 14);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -221,80 +207,110 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
   auto issue = [&](MfvStep<NMAT> &w, int i) {
     const int row = row_base + 16 * (i / MV_KS) + l16;
     const int c = c0 + i % MV_KS;
-    // the chunk's 4 segments share one group of 64: their halves h sit at
-    // base + 16 (s & 3) + h 16 gsz (all wave-uniform); the lane adds its row
-    // and its dword 4 g
+    // the chunk's 4 segments share one group of 64: half h of segment
+    // 4c + g sits at base + h 16 gsz + 16 g; the 4 lanes of a row read 64
+    // contiguous bytes per half
     const int j0 = 4 * c;
     const int grp = j0 >> 6;
     const int gsz = min(64, a.nseg - (grp << 6));
     const uint32_t base = (uint32_t)(grp * 2048 + (j0 & 63) * 16);
     const bool cv = c < a.nchunk;  // wave-uniform
-    const uint32_t vq = cv ? (uint32_t)row * a.row_qs + 4u * g : OOB;
+    const uint32_t vq = cv ? (uint32_t)row * a.row_qs + 16u * g : OOB;
     const uint32_t vm = cv ? (uint32_t)row * a.row_meta + 16u * c : OOB;
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const uint32_t so = base + 16u * (s & 3) + (s >> 2) * 16u * gsz;
-        w.q[mt][s] = __builtin_amdgcn_raw_buffer_load_b32(rq[mt], (int)vq, (int)so, 0);
+      for (int h = 0; h < 2; ++h) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rq[mt], (int)vq,
+                                                             (int)(base + h * 16u * gsz), 0);
+        w.q[mt][h] = make_uint4(v[0], v[1], v[2], v[3]);
       }
       w.m[mt] = bload16(rm[mt], vm);
     }
   };
 
   // step (row tile rt, chunk kc) into accr, the row tile's accumulators
+  // q 2^-24 sc as fp16 bits (q sc <= 945 < 1024: an exact subnormal) for
+  // the 8 codes of a dword, in nibble order
+  auto operand = [](uint32_t cw, uint32_t sc2) {
+    cw ^= 0x88888888u;
+    const uint32_t lo = cw & 0x0F0F0F0Fu, hi = (cw >> 4) & 0x0F0F0F0Fu;
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 sv = __builtin_bit_cast(u16x2, sc2);
+    uint32_t d[4];
+    d[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(hi, lo, 0x0C040C00u)) * sv);
+    d[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(hi, lo, 0x0C050C01u)) * sv);
+    d[2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(hi, lo, 0x0C060C02u)) * sv);
+    d[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, __builtin_amdgcn_perm(hi, lo, 0x0C070C03u)) * sv);
+    return __builtin_bit_cast(f16x8, d);
+  };
+
+  // step (row tile rt, chunk kc) into accr, the row tile's accumulators:
+  //   sum_i w_i x_i = d sum_s sc_s sum_{i in s} q_i x_i - dmin sum_s m_s X_s
+  // with sc_s inside the operands, so the 8 MFMAs of the block accumulate
+  // together and d, dmin apply once per block
   auto compute = [&](const MfvStep<NMAT> &w, const MfvStage &st, f32x4 (&accr)[NMAT]) {
+    // this lane's sub-blocks g and g + 4 (get_scale_min_k4,
+    // src/quant/mod.rs:1163-1170, on scales12): the scales go into the code
+    // operands, the mins into operands of their own (m as fp16, all 8
+    // positions), whose MFMAs form sum_s m_s X_s
+    uint32_t sc2[NMAT][2];
+    f16x8 bm[NMAT][2];
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) {
+      const uint32_t p03 = w.m[mt].y, p47 = w.m[mt].z, p8b = w.m[mt].w;
+      const uint32_t sca = (p03 >> (8 * g)) & 63;
+      const uint32_t scb = ((p8b >> (8 * g)) & 15) | (((p03 >> (8 * g + 6)) & 3) << 4);
+      const uint32_t mna = (p47 >> (8 * g)) & 63;
+      const uint32_t mnb = ((p8b >> (8 * g + 4)) & 15) | (((p47 >> (8 * g + 6)) & 3) << 4);
+      sc2[mt][0] = sca | (sca << 16);
+      sc2[mt][1] = scb | (scb << 16);
+      const uint32_t ha = __builtin_bit_cast(uint16_t, (_Float16)(float)mna);
+      const uint32_t hb = __builtin_bit_cast(uint16_t, (_Float16)(float)mnb);
+      const uint32_t da[4] = {ha * 0x10001u, ha * 0x10001u, ha * 0x10001u, ha * 0x10001u};
+      const uint32_t db[4] = {hb * 0x10001u, hb * 0x10001u, hb * 0x10001u, hb * 0x10001u};
+      bm[mt][0] = __builtin_bit_cast(f16x8, da);
+      bm[mt][1] = __builtin_bit_cast(f16x8, db);
+    }
+    f32x4 y[NMAT], ym[NMAT];
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) {
+      y[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      ym[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const f16x8 ahi = __builtin_bit_cast(f16x8, st.a[u][0][lane]);
+      const f16x8 alo = __builtin_bit_cast(f16x8, st.a[u][1][lane]);
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt) {
+        const uint32_t cw = u < 4 ? (&w.q[mt][0].x)[u] : (&w.q[mt][1].x)[u - 4];
+        const f16x8 b = operand(cw, sc2[mt][u >> 2]);
+        y[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, y[mt], 0, 0, 0);
+        y[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, y[mt], 0, 0, 0);
+        ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bm[mt][u >> 2], ym[mt], 0, 0, 0);
+        ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bm[mt][u >> 2], ym[mt], 0, 0, 0);
+      }
+      // one MFMA step's operands live at a time: make the accumulators
+      // exist here, or the compiler gathers every step's operands first
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt) {
+        asm volatile("" : "+v"(y[mt][0]), "+v"(y[mt][1]), "+v"(y[mt][2]), "+v"(y[mt][3]));
+        asm volatile("" : "+v"(ym[mt][0]), "+v"(ym[mt][1]), "+v"(ym[mt][2]), "+v"(ym[mt][3]));
+      }
+    }
     float sx[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) sx[k] = st.sx[4 * g + k];
-    f32x4 ch[NMAT];
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) ch[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float d[NMAT], dmin[NMAT];
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) {
-      d[mt] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x & 0xFFFF));
-      dmin[mt] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x >> 16));
+      const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x & 0xFFFF));
+      const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x >> 16));
+      const float dd = d * 16777216.0f;  // code operands carry 2^-24
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        accr[mt][k] = fmaf(sx[k], fmaf(dd, y[mt][k], -dmin * ym[mt][k]), accr[mt][k]);
     }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const f16x8 ahi = __builtin_bit_cast(f16x8, st.a[s][0][lane]);
-      const f16x8 alo = __builtin_bit_cast(f16x8, st.a[s][1][lane]);
-      float xs[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) xs[k] = st.xs[4 * g + k][s];
-#pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt) {
-        // get_scale_min_k4 (src/quant/mod.rs:1163-1170) on scales12
-        const uint32_t p03 = w.m[mt].y, p47 = w.m[mt].z, p8b = w.m[mt].w;
-        int sc, mn;
-        if (s < 4) {
-          sc = (p03 >> (8 * s)) & 63;
-          mn = (p47 >> (8 * s)) & 63;
-        } else {
-          const int j = s - 4;
-          sc = ((p8b >> (8 * j)) & 15) | (((p03 >> (8 * j + 6)) & 3) << 4);
-          mn = ((p8b >> (8 * j + 4)) & 15) | (((p47 >> (8 * j + 6)) & 3) << 4);
-        }
-        const float as = d[mt] * (float)sc * 16777216.0f;  // operands carry 2^-24
-        const float cs = dmin[mt] * (float)mn;
-        const f16x8 b = codes_to_f16(w.q[mt][s]);
-        f32x4 y = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        y = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, y, 0, 0, 0);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) ch[mt][k] = fmaf(as, y[k], fmaf(-cs, xs[k], ch[mt][k]));
-      }
-      // finish each sub-block's scale products here: left to itself the
-      // compiler keeps every sub-block's MFMA output to apply the scales at
-      // the end, which needs more registers than there are
-#pragma unroll
-      for (int mt = 0; mt < NMAT; ++mt)
-        asm volatile("" : "+v"(ch[mt][0]), "+v"(ch[mt][1]), "+v"(ch[mt][2]), "+v"(ch[mt][3]));
-    }
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) accr[mt][k] = fmaf(sx[k], ch[mt][k], accr[mt][k]);
   };
 
   // steps i = MV_KS rt + kc; ring slot i % MV_D = kc (MV_D == MV_KS)

@@ -80,3 +80,19 @@ def test_split_rejects(ctx):
         ex.forward(S.x, S.logits, 2, 0, nx.PATH_MFMA_SPLIT)
     assert ei.value.code == nx.NX_ERR_UNSUPPORTED
     ex.close()
+
+
+@pytest.mark.parametrize("E,H,F,k,T,want", [
+    (8, 512, 1024, 2, 1, nx.PATH_GEMV), (8, 512, 1024, 2, 8, nx.PATH_GEMV),
+    (8, 512, 1024, 2, 16, nx.PATH_MFMA_SPLIT), (64, 256, 256, 8, 8, nx.PATH_MFMA_SPLIT),
+    (8, 256, 256, 2, 256, nx.PATH_MFMA_F16)])
+def test_auto_path_choice(ctx, E, H, F, k, T, want):
+    """AUTO gives the bits of the path it chooses for Q4_K: the GEMV up to ~2
+    tokens per expert, the split-activation MFMA path up to ~24, the grouped
+    GEMM beyond."""
+    L = Layer(Q4_K, E, H, F, k, T, seed=E + T)
+    ex = L.upload(nx, ctx)
+    auto = ex.forward(L.x, L.logits, k, 0, nx.PATH_AUTO)
+    chosen = ex.forward(L.x, L.logits, k, 0, want)
+    ex.close()
+    np.testing.assert_array_equal(auto.view(np.uint32), chosen.view(np.uint32))
