@@ -110,6 +110,58 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
   const int c0 = slice * MV_KS;  // first chunk of the slice
   const int row_base = blockIdx.x * MV_WG_ROWS + wave * 16 * MV_RTW;
 
+  // ---- weights: lane holds row (lane % 16) of each row tile and K group
+  // (lane / 16) of every sub-block
+  const int l16 = lane & 15, g = lane >> 4;
+  __amdgpu_buffer_rsrc_t rq[NMAT], rm[NMAT];
+  {
+    const uint32_t nq = (uint32_t)a.rows * a.row_qs, nm = (uint32_t)a.rows * a.row_meta;
+    rq[0] = make_rsrc(a.qs0 + (size_t)e * a.qs_stride, nq);
+    rm[0] = make_rsrc(a.meta0 + (size_t)e * a.meta_stride, nm);
+    if constexpr (NMAT == 2) {
+      rq[1] = make_rsrc(a.qs1 + (size_t)e * a.qs_stride, nq);
+      rm[1] = make_rsrc(a.meta1 + (size_t)e * a.meta_stride, nm);
+    }
+  }
+  // step i: row tile i / MV_KS, chunk c0 + i % MV_KS
+  // Rows past the matrix read as zeros through the resources' size (row *
+  // row_qs >= rows * row_qs); a chunk past the row (wave-uniform) reads at
+  // OOB.  Per-lane parts of the offsets stay in one register per step; the
+  // rest goes in the scalar offset.
+  auto issue = [&](MfvStep<NMAT> &w, int i) {
+    const int row = row_base + 16 * (i / MV_KS) + l16;
+    const int c = c0 + i % MV_KS;
+    // the chunk's 4 segments share one group of 64: half h of segment
+    // 4c + g sits at base + h 16 gsz + 16 g; the 4 lanes of a row read 64
+    // contiguous bytes per half
+    const int j0 = 4 * c;
+    const int grp = j0 >> 6;
+    const int gsz = min(64, a.nseg - (grp << 6));
+    const uint32_t base = (uint32_t)(grp * 2048 + (j0 & 63) * 16);
+    // steps past the last (issued by the pipeline's tail) and chunks past
+    // the row read at OOB (wave-uniform)
+    const bool cv = i < NSTEP && c < a.nchunk;
+    const uint32_t vq = cv ? (uint32_t)row * a.row_qs + 16u * g : OOB;
+    const uint32_t vm = cv ? (uint32_t)row * a.row_meta + 16u * c : OOB;
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rq[mt], (int)vq,
+                                                             (int)(base + h * 16u * gsz), 0);
+        w.q[mt][h] = make_uint4(v[0], v[1], v[2], v[3]);
+      }
+      w.m[mt] = bload16(rm[mt], vm);
+    }
+  };
+
+  // step (row tile rt, chunk kc) into accr, the row tile's accumulators
+  // the first steps' codes go out before the staging: the weights do not
+  // depend on the activations, and their latency overlaps the staging's
+  MfvStep<NMAT> ring[MV_D];
+#pragma unroll
+  for (int i = 0; i < MV_D - 1; ++i) issue(ring[i], i);
+
   // ---- stage the slice: thread t owns positions 16j .. 16j+15 of every
   // chunk of pair m = t / 16; chunks past the row read as zeros
   {
@@ -186,50 +238,6 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
   }
   __syncthreads();
 
-  // ---- weights: lane holds row (lane % 16) of each row tile and K group
-  // (lane / 16) of every sub-block
-  const int l16 = lane & 15, g = lane >> 4;
-  __amdgpu_buffer_rsrc_t rq[NMAT], rm[NMAT];
-  {
-    const uint32_t nq = (uint32_t)a.rows * a.row_qs, nm = (uint32_t)a.rows * a.row_meta;
-    rq[0] = make_rsrc(a.qs0 + (size_t)e * a.qs_stride, nq);
-    rm[0] = make_rsrc(a.meta0 + (size_t)e * a.meta_stride, nm);
-    if constexpr (NMAT == 2) {
-      rq[1] = make_rsrc(a.qs1 + (size_t)e * a.qs_stride, nq);
-      rm[1] = make_rsrc(a.meta1 + (size_t)e * a.meta_stride, nm);
-    }
-  }
-  // step i: row tile i / MV_KS, chunk c0 + i % MV_KS
-  // Rows past the matrix read as zeros through the resources' size (row *
-  // row_qs >= rows * row_qs); a chunk past the row (wave-uniform) reads at
-  // OOB.  Per-lane parts of the offsets stay in one register per step; the
-  // rest goes in the scalar offset.
-  auto issue = [&](MfvStep<NMAT> &w, int i) {
-    const int row = row_base + 16 * (i / MV_KS) + l16;
-    const int c = c0 + i % MV_KS;
-    // the chunk's 4 segments share one group of 64: half h of segment
-    // 4c + g sits at base + h 16 gsz + 16 g; the 4 lanes of a row read 64
-    // contiguous bytes per half
-    const int j0 = 4 * c;
-    const int grp = j0 >> 6;
-    const int gsz = min(64, a.nseg - (grp << 6));
-    const uint32_t base = (uint32_t)(grp * 2048 + (j0 & 63) * 16);
-    const bool cv = c < a.nchunk;  // wave-uniform
-    const uint32_t vq = cv ? (uint32_t)row * a.row_qs + 16u * g : OOB;
-    const uint32_t vm = cv ? (uint32_t)row * a.row_meta + 16u * c : OOB;
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rq[mt], (int)vq,
-                                                             (int)(base + h * 16u * gsz), 0);
-        w.q[mt][h] = make_uint4(v[0], v[1], v[2], v[3]);
-      }
-      w.m[mt] = bload16(rm[mt], vm);
-    }
-  };
-
-  // step (row tile rt, chunk kc) into accr, the row tile's accumulators
   // q 2^-24 sc as fp16 bits (q sc <= 945 < 1024: an exact subnormal) for
   // the 8 codes of a dword, in nibble order
   auto operand = [](uint32_t cw, uint32_t sc2) {
@@ -316,10 +324,9 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
   // steps i = MV_KS rt + kc; ring slot i % MV_D = kc (MV_D == MV_KS)
   static_assert(MV_D == MV_KS, "ring slots are the chunk index");
   float *out = a.out + (size_t)slice * a.out_split;
-  MfvStep<NMAT> ring[MV_D];
+  // fully unrolled: ring registers carried around a loop back edge get
+  // copied there, and copying a register with a load in flight waits for it
 #pragma unroll
-  for (int i = 0; i < MV_D - 1; ++i) issue(ring[i], i);
-#pragma unroll 1
   for (int rt = 0; rt < MV_RTW; ++rt) {
     f32x4 accr[NMAT];
 #pragma unroll
@@ -327,11 +334,10 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
 #pragma unroll
     for (int kc = 0; kc < MV_KS; ++kc) {
       const int i = MV_KS * rt + kc;
-      // the staged operands do not change over the row tiles: keep the
-      // compiler from hoisting every step's LDS reads out of the loop (they
-      // would need 256 registers)
-      asm volatile("" ::: "memory");
-      if (i + MV_D - 1 < NSTEP) issue(ring[(kc + MV_D - 1) % MV_D], i + MV_D - 1);
+      // issued unconditionally: a branch around the loads would leave the
+      // compiler unsure how many are outstanding, and it would then wait
+      // for all of them
+      issue(ring[(kc + MV_D - 1) % MV_D], i + MV_D - 1);
       compute(ring[kc], stage[kc], accr);
       __builtin_amdgcn_sched_barrier(0);
     }
