@@ -78,6 +78,9 @@ extern "C" {
 #define NX_FMT_Q8_0 8
 #define NX_FMT_Q4_K 12
 #define NX_FMT_Q2_K 10 /* GEMV path only (decode); dequant/quantize bit-exact */
+#define NX_FMT_F16 1   /* IEEE half, GEMV path only; dequant exact (src/gguf/mod.rs:921-933) */
+#define NX_FMT_BF16 28 /* bfloat16 (the reference's id, src/gguf/mod.rs:135), GEMV path only;
+                          dequant exact (src/gguf/mod.rs:934-946) */
 
 /* router score modes */
 #define NX_SCORE_SOFTMAX 0 /* reference: softmax over the selected top-k logits */

@@ -22,13 +22,15 @@ NX_OK = 0
 NX_ERR_INVALID_ARG, NX_ERR_SHAPE, NX_ERR_UNSUPPORTED, NX_ERR_DEVICE = 1, 2, 3, 4
 NX_ERR_OOM, NX_ERR_TRUNCATED, NX_ERR_NO_ROUTES, NX_ERR_NOT_FOUND, NX_ERR_IO = 5, 6, 7, 8, 9
 Q4K_REFERENCE, Q4K_GGML = 0, 1
-F32, Q4_0, Q8_0, Q4_K, Q2_K = 0, 2, 8, 12, 10
+F32, Q4_0, Q8_0, Q4_K, Q2_K, F16, BF16 = 0, 2, 8, 12, 10, 1, 28
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 PATH_AUTO, PATH_GEMV, PATH_MFMA_F16, PATH_MFMA_BF16, PATH_MFMA_SPLIT = 0, 1, 2, 3, 4
 ROLE_GATE, ROLE_UP, ROLE_DOWN = 0, 1, 2
 EXPERT_SHARED = -1
-FORMAT_NAMES = {F32: "F32", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q2_K: "Q2_K"}
-BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q2_K: (256, 84), F32: (1, 4)}
+FORMAT_NAMES = {F32: "F32", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q2_K: "Q2_K", F16: "F16",
+                BF16: "BF16"}
+BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q2_K: (256, 84), F32: (1, 4),
+         F16: (1, 2), BF16: (1, 2)}
 
 # every symbol the header declares (checked by the CPU test suite)
 EXPORTS = [

@@ -32,6 +32,9 @@ bool format_info(int fmt, FormatInfo *fi) {
   // resident Q2_K: codes widened to 4 bits, 8 scale-plane bytes per segment
   case NX_FMT_Q2_K: *fi = {fmt, 256, 84, 128, 32}; return true;
   case NX_FMT_F32: *fi = {fmt, 4, 16, 16, 0}; return true;
+  // 16-bit floats: 16 values per 32-byte segment, no scale plane
+  case NX_FMT_F16:
+  case NX_FMT_BF16: *fi = {fmt, 1, 2, 2, 0}; return true;
   }
   return false;
 }
@@ -43,6 +46,8 @@ static const char *fmt_name(int fmt) {
   case NX_FMT_Q4_0: return "Q4_0";
   case NX_FMT_Q2_K: return "Q2_K";
   case NX_FMT_F32: return "F32";
+  case NX_FMT_F16: return "F16";
+  case NX_FMT_BF16: return "BF16";
   }
   return "?";
 }
@@ -54,6 +59,8 @@ static size_t gguf_bytes(int fmt, size_t n) {
   case NX_FMT_Q4_0: return (n + 31) / 32 * 18;
   case NX_FMT_Q2_K: return (n + 255) / 256 * 84;
   case NX_FMT_F32: return n * 4;
+  case NX_FMT_F16:
+  case NX_FMT_BF16: return n * 2;
   }
   return 0;
 }
@@ -186,6 +193,11 @@ static void plane_layout(int fmt, RolePlane &pl, int rows, int cols) {
   case NX_FMT_Q2_K:
     pl.nseg = cols / 256 * 4;
     pl.row_meta = (uint32_t)(pl.nseg * 8);
+    break;
+  case NX_FMT_F16:
+  case NX_FMT_BF16:
+    pl.nseg = (cols + 15) / 16;
+    pl.row_meta = 0;
     break;
   default:  // F32
     pl.nseg = (cols + 7) / 8;
@@ -837,9 +849,10 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   NX_TRY(ws(c, WS_ACTIVE, (size_t)E + 1, &d_act));
 
   int use = path;
-  if (ex->fmt == NX_FMT_Q2_K) {  // no MFMA operand path for Q2_K
+  if (ex->fmt == NX_FMT_Q2_K || ex->fmt == NX_FMT_F16 || ex->fmt == NX_FMT_BF16) {
+    // no MFMA operand path for these formats
     if (use == NX_PATH_MFMA_F16 || use == NX_PATH_MFMA_BF16 || use == NX_PATH_MFMA_SPLIT)
-      return fail(NX_ERR_UNSUPPORTED, "Q2_K experts run on the GEMV path only");
+      return fail(NX_ERR_UNSUPPORTED, std::string(fmt_name(ex->fmt)) + " experts run on the GEMV path only");
     use = NX_PATH_GEMV;
   }
   if (use == NX_PATH_AUTO) {

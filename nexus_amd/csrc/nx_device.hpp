@@ -553,6 +553,53 @@ struct Seg<NX_FMT_F32> {
   }
 };
 
+// 16-bit floats: a 32-byte segment is 16 consecutive values of the row,
+// converted exactly to f32 and fma'd with the activations
+template <int FMT>
+struct Seg16 {
+  static constexpr int EPS = 16;
+  using Meta = uint32_t;
+  struct Run {};
+  struct X {
+    float x[16];
+  };
+  __device__ __forceinline__ static int xidx(int j, int v) { return j * 16 + v; }
+  __device__ __forceinline__ static uint32_t meta_off(int, bool) { return 0; }
+  __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t, uint32_t) { return 0; }
+  __device__ __forceinline__ static void prep(const float *x, X &o) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o.x[i] = x[i];
+  }
+  __device__ __forceinline__ static void prep_quarter(const float *, int, X *) {}
+  __device__ __forceinline__ static float lo(uint32_t w) {
+    if constexpr (FMT == NX_FMT_F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+    return __uint_as_float(w << 16);
+  }
+  __device__ __forceinline__ static float hi(uint32_t w) {
+    if constexpr (FMT == NX_FMT_F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+    return __uint_as_float(w & 0xFFFF0000u);
+  }
+  template <int NT>
+  __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &, int,
+                                             const X *xv, Run *, float *acc) {
+    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        a = fmaf(lo(w[i]), xv[t].x[2 * i], a);
+        a = fmaf(hi(w[i]), xv[t].x[2 * i + 1], a);
+      }
+      acc[t] += a;
+    }
+  }
+};
+template <>
+struct Seg<NX_FMT_F16> : Seg16<NX_FMT_F16> {};
+template <>
+struct Seg<NX_FMT_BF16> : Seg16<NX_FMT_BF16> {};
+
 // ---- DPP reductions.  After group_sum<L>, the last lane of each group of L
 // lanes (L = 16, 32, 64) holds the group's sum.
 template <int CTRL, int ROW_MASK = 0xF>

@@ -265,8 +265,8 @@ struct RowGroup {
 #pragma unroll
         for (int e = 0; e < EPS; e += 4) {
           const uint32_t xo = jv ? (uint32_t)S::xidx(j, e) * 4u : OOB;
-          if constexpr (FMT == NX_FMT_F32) {
-            // rows of odd length: element-wise so that each load is wholly in or out
+          if constexpr (FMT == NX_FMT_F32 || FMT == NX_FMT_F16 || FMT == NX_FMT_BF16) {
+            // rows of any length: element-wise so that each load is wholly in or out
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[m][t][e + i] = __uint_as_float(bload4(xr, xo + 4u * i));
           } else {
@@ -442,7 +442,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   const int grp = KSPLIT > 1 ? 0 : (LPR == 64 ? wave : tid / LPR);
 
   // one wave per row group: the workgroup shares the activation operands
-  constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32;
+  constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32 && FMT != NX_FMT_F16 &&
+                        FMT != NX_FMT_BF16;
   __shared__ uint4 xsh[COOP ? NT * 64 * RG::XW : 1];
   RG g;
   g.init(KSPLIT == 1 ? (lane % LPR) : tid);
@@ -776,6 +777,8 @@ KernelFn pick(int fmt, int gateup, bool ylds, int nt, const Shape &s) {
   case NX_FMT_Q4_0: return pick_fmt<NX_FMT_Q4_0>(gateup, ylds, nt, s);
   case NX_FMT_Q2_K: return pick_fmt<NX_FMT_Q2_K>(gateup, ylds, nt, s);
   case NX_FMT_F32: return pick_fmt<NX_FMT_F32>(gateup, ylds, nt, s);
+  case NX_FMT_F16: return pick_fmt<NX_FMT_F16>(gateup, ylds, nt, s);
+  case NX_FMT_BF16: return pick_fmt<NX_FMT_BF16>(gateup, ylds, nt, s);
   }
   return nullptr;
 }
@@ -786,6 +789,8 @@ int elems_per_segment(int fmt) {
   case NX_FMT_Q8_0: return 32;
   case NX_FMT_Q4_0: return 64;
   case NX_FMT_Q2_K: return 64;
+  case NX_FMT_F16:
+  case NX_FMT_BF16: return 16;
   default: return 8;
   }
 }

@@ -508,7 +508,7 @@ const nx_gguf::Tensor *find_any(const nx_gguf *g, const std::vector<std::string>
 
 bool supported_fmt(uint32_t type) {
   return type == NX_FMT_F32 || type == NX_FMT_Q4_0 || type == NX_FMT_Q8_0 || type == NX_FMT_Q4_K ||
-         type == NX_FMT_Q2_K;
+         type == NX_FMT_Q2_K || type == NX_FMT_F16 || type == NX_FMT_BF16;
 }
 
 // expert tensors of block `layer`: merged blk.L.ffn_{gate,up,down}_exps
@@ -556,7 +556,7 @@ int moe_layout(const nx_gguf *g, int layer, RoleTensor role[3], int *E, int *H, 
     return fail(NX_ERR_SHAPE, "expert matrix shapes of block " + L + " are inconsistent");
   if (!supported_fmt(tg.type))
     return fail(NX_ERR_UNSUPPORTED, "expert tensor type " + std::to_string(tg.type) +
-                                        " is not resident-capable (F32, Q4_0, Q8_0, Q4_K, Q2_K)");
+                                        " is not resident-capable (F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q2_K)");
   if (e_count <= 0 || h > 0x7FFFFFFF || f > 0x7FFFFFFF)
     return fail(NX_ERR_SHAPE, "no experts in block " + L);
   *E = e_count;
@@ -681,7 +681,7 @@ int nx_matrix_load_gguf(nx_ctx *ctx, const nx_gguf *g, const char *name, int q4k
   if (!t) return fail(NX_ERR_NOT_FOUND, std::string("Missing tensor: ") + name);
   if (!supported_fmt(t->type))
     return fail(NX_ERR_UNSUPPORTED, "tensor type " + std::to_string(t->type) +
-                                        " is not resident-capable (F32, Q4_0, Q8_0, Q4_K, Q2_K)");
+                                        " is not resident-capable (F32, F16, BF16, Q4_0, Q8_0, Q4_K, Q2_K)");
   // dims innermost first: a row is dims[0] long, the rest count rows
   if (t->dims.empty()) return fail(NX_ERR_SHAPE, "tensor " + t->name + " has no dimensions");
   uint64_t rows = 1;

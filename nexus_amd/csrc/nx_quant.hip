@@ -28,7 +28,11 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t *__restrict__ src
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
        i += (size_t)gridDim.x * blockDim.x) {
     float v;
-    if constexpr (FMT == NX_FMT_Q8_0) {
+    if constexpr (FMT == NX_FMT_F16) {  // src/gguf/mod.rs:921-933
+      v = ld_f16(src + 2 * i);
+    } else if constexpr (FMT == NX_FMT_BF16) {  // src/gguf/mod.rs:934-946
+      v = __uint_as_float((uint32_t)(src[2 * i] | (src[2 * i + 1] << 8)) << 16);
+    } else if constexpr (FMT == NX_FMT_Q8_0) {
       const uint8_t *b = src + (i / 32) * 34;
       v = (float)(int8_t)b[2 + i % 32] * ld_f16(b);
     } else if constexpr (FMT == NX_FMT_Q4_0) {
@@ -312,6 +316,15 @@ __global__ __launch_bounds__(256) void k_repack_codes(const uint8_t *__restrict_
         const int c = 8 * j + 4 * h + v;
         df[v] = c < cols ? sf[c] : 0.0f;
       }
+    } else if constexpr (FMT == NX_FMT_F16 || FMT == NX_FMT_BF16) {
+      // segment j = values 16 j .. 16 j + 15 of the row, half h the 8 from 16 j + 8 h
+      const uint16_t *sh = reinterpret_cast<const uint16_t *>(src) + (size_t)r * cols;
+      uint16_t *dh = reinterpret_cast<uint16_t *>(dst);
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const int c = 16 * j + 8 * h + v;
+        dh[v] = c < cols ? sh[c] : (uint16_t)0;
+      }
     } else if constexpr (FMT == NX_FMT_Q8_0) {
       const int nb = cols / 32;
       const uint8_t *b = src + ((size_t)r * nb + j) * 34 + 2 + h * 16;
@@ -418,6 +431,10 @@ int launch_dequant(nx_ctx *c, int fmt, const void *d_src, size_t n, float *d_dst
     return launch(c, "dequant_q4_k", [&] { k_dequant<NX_FMT_Q4_K><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
   case NX_FMT_Q2_K:
     return launch(c, "dequant_q2_k", [&] { k_dequant<NX_FMT_Q2_K><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
+  case NX_FMT_F16:
+    return launch(c, "dequant_f16", [&] { k_dequant<NX_FMT_F16><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
+  case NX_FMT_BF16:
+    return launch(c, "dequant_bf16", [&] { k_dequant<NX_FMT_BF16><<<g, 256, 0, c->stream>>>(s, n, d_dst); });
   case NX_FMT_F32:
     NX_HIP(hipMemcpyAsync(d_dst, d_src, n * 4, hipMemcpyDeviceToDevice, c->stream));
     return NX_OK;
@@ -462,7 +479,7 @@ int launch_repack(nx_ctx *c, int fmt, const void *d_src, const RolePlane &pl, ui
     NX_TRY(launch(c, NAME, [&] {                                                                \
       k_repack_codes<F><<<gc, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_qs, qs); \
     }));                                                                                        \
-    if (F != NX_FMT_F32)                                                                        \
+    if (F != NX_FMT_F32 && F != NX_FMT_F16 && F != NX_FMT_BF16)                                \
       NX_TRY(launch(c, NAME, [&] {                                                              \
         k_repack_meta<F><<<gm, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_meta, \
                                                     meta);                                      \
@@ -474,6 +491,8 @@ int launch_repack(nx_ctx *c, int fmt, const void *d_src, const RolePlane &pl, ui
   case NX_FMT_Q8_0: NX_RP(NX_FMT_Q8_0, "repack_q8_0");
   case NX_FMT_Q4_0: NX_RP(NX_FMT_Q4_0, "repack_q4_0");
   case NX_FMT_F32: NX_RP(NX_FMT_F32, "repack_f32");
+  case NX_FMT_F16: NX_RP(NX_FMT_F16, "repack_f16");
+  case NX_FMT_BF16: NX_RP(NX_FMT_BF16, "repack_bf16");
   case NX_FMT_Q2_K: {
     NX_TRY(launch(c, "repack_q2_k", [&] {
       k_repack_codes<NX_FMT_Q2_K><<<gc, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg,

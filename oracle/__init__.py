@@ -19,7 +19,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 _lib = None
 
-F32, Q4_0, Q8_0, Q4_K, Q2_K = 0, 2, 8, 12, 10
+F32, Q4_0, Q8_0, Q4_K, Q2_K, F16, BF16 = 0, 2, 8, 12, 10, 1, 28
 BLOCK = {Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q2_K: (256, 84)}
 
 _fp = C.POINTER(C.c_float)
@@ -118,7 +118,8 @@ def quantize(fmt: int, x, nthreads: int | None = None) -> np.ndarray:
 
 
 def dequantize(fmt: int, data, output_len: int, nthreads: int | None = None) -> np.ndarray:
-    """QuantEngine::dequantize (src/quant/mod.rs:643-667) for one format."""
+    """QuantEngine::dequantize (src/quant/mod.rs:643-667) for one format; F16 and
+    BF16 as GgufReader::tensor_bytes_to_f32 (src/gguf/mod.rs:921-946)."""
     data = np.ascontiguousarray(data, dtype=np.uint8).ravel()
     out = np.empty(max(output_len, 1), dtype=np.float32)
     n = lib().nxo_dequantize(fmt, _p(data, _u8p), data.size, output_len, _p(out, _fp),

@@ -34,6 +34,8 @@
 #define GGUF_Q8_0 8
 #define GGUF_Q4_K 12
 #define GGUF_Q2_K 10
+#define GGUF_F16 1
+#define GGUF_BF16 28 /* the reference's id (src/gguf/mod.rs:135) */
 
 /* ------------------------------------------------------------------------ */
 /* parallel-for helper                                                       */
@@ -181,6 +183,8 @@ size_t nxo_quant_bytes(int t, size_t n) {
     case GGUF_Q8_0: return (n + 31) / 32 * 34; /* src/gguf/mod.rs:268 */
     case GGUF_Q4_K: return (n + 255) / 256 * 144; /* src/gguf/mod.rs:272 */
     case GGUF_Q2_K: return (n + 255) / 256 * 84;  /* src/gguf/mod.rs:270 */
+    case GGUF_F16:
+    case GGUF_BF16: return n * 2; /* src/gguf/mod.rs:249-293 */
     default: return 0;
     }
 }
@@ -434,6 +438,15 @@ size_t nxo_dequantize(int t, const uint8_t *src, size_t src_bytes, size_t output
     case GGUF_F32: {
         size_t n = src_bytes / 4 < output_len ? src_bytes / 4 : output_len;
         memcpy(dst, src, n * 4);
+        return n;
+    }
+    case GGUF_F16: /* src/gguf/mod.rs:921-933: half::f16::to_f32 */
+    case GGUF_BF16: { /* src/gguf/mod.rs:934-946: bits << 16 */
+        size_t n = src_bytes / 2 < output_len ? src_bytes / 2 : output_len;
+        for (size_t i = 0; i < n; ++i) {
+            uint16_t h = (uint16_t)(src[2 * i] | (src[2 * i + 1] << 8));
+            dst[i] = t == GGUF_F16 ? nxo_f16_to_f32(h) : u2f((uint32_t)h << 16);
+        }
         return n;
     }
     case GGUF_Q8_0: c.blk = 32; c.bytes = 34; break;

@@ -10,7 +10,26 @@ import numpy as np
 
 import oracle
 
-F32, Q4_0, Q8_0, Q4_K, Q2_K = 0, 2, 8, 12, 10
+F32, Q4_0, Q8_0, Q4_K, Q2_K, F16, BF16 = 0, 2, 8, 12, 10, 1, 28
+
+
+def half_payload(fmt, w) -> np.ndarray:
+    """F16 (IEEE round to nearest even, numpy) or BF16 (round to nearest even
+    on the f32 bits) payload bytes of w."""
+    w = np.ascontiguousarray(w, np.float32).ravel()
+    if fmt == F16:
+        return w.astype(np.float16).view(np.uint8)
+    b = w.view(np.uint32).astype(np.uint64)
+    h = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    return h.view(np.uint8)
+
+
+def payload_of(fmt, w) -> np.ndarray:
+    if fmt == F32:
+        return np.ascontiguousarray(w, np.float32).ravel().view(np.uint8)
+    if fmt in (F16, BF16):
+        return half_payload(fmt, w)
+    return oracle.quantize(fmt, w)
 
 
 class Layer:
@@ -38,7 +57,7 @@ class Layer:
             for role, shape in ((0, (F, H)), (1, (F, H)), (2, (H, F))):
                 r2 = np.random.default_rng([int(wseed), e, role])
                 w = (r2.standard_normal(shape, dtype=np.float32) * np.float32(0.02))
-                q = oracle.quantize(fmt, w) if fmt != F32 else w.ravel().view(np.uint8)
+                q = payload_of(fmt, w)
                 self.payload[(e, role)] = q
                 if e in need:
                     self.dense[(e, role)] = (oracle.dequantize(fmt, q, w.size) if fmt != F32
@@ -51,7 +70,7 @@ class Layer:
             pays = []
             for shape in ((shared_F, H), (shared_F, H), (H, shared_F)):
                 w = (r2.standard_normal(shape, dtype=np.float32) * np.float32(0.02))
-                q = oracle.quantize(fmt, w) if fmt != F32 else w.ravel().view(np.uint8)
+                q = payload_of(fmt, w)
                 pays.append(q)
                 mats.append(oracle.dequantize(fmt, q, w.size) if fmt != F32 else w.ravel())
             self.shared_payload = pays

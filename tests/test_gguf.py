@@ -258,11 +258,18 @@ def test_moe_info_rejects_inconsistent_layers(tmp_path):
         with pytest.raises(nx.NexusError) as ei:
             g.moe_info(0)
         assert ei.value.code == nx.NX_ERR_SHAPE
+    # F16 experts are resident-capable; Q5_0 (type 6, 22 B per 32) is not
     w2 = GgufWriter()
     for r in ("ffn_gate", "ffn_up"):
         w2.add_tensor(f"blk.0.{r}_exps.weight", [64, 96, 2], GT_F16, np.zeros(2 * 64 * 96, np.float16))
     w2.add_tensor("blk.0.ffn_down_exps.weight", [96, 64, 2], GT_F16, np.zeros(2 * 64 * 96, np.float16))
     with open_bytes(tmp_path, w2.tobytes(), "f16.gguf") as g:
+        assert g.moe_info(0)["fmt"] == GT_F16
+    w3 = GgufWriter()
+    for r in ("ffn_gate", "ffn_up"):
+        w3.add_tensor(f"blk.0.{r}_exps.weight", [64, 96, 2], 6, np.zeros(2 * 64 * 96 // 32 * 22, np.uint8))
+    w3.add_tensor("blk.0.ffn_down_exps.weight", [96, 64, 2], 6, np.zeros(2 * 64 * 96 // 32 * 22, np.uint8))
+    with open_bytes(tmp_path, w3.tobytes(), "q5_0.gguf") as g:
         with pytest.raises(nx.NexusError) as ei:
             g.moe_info(0)
         assert ei.value.code == nx.NX_ERR_UNSUPPORTED

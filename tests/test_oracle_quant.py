@@ -312,3 +312,37 @@ def test_q2k_hand_worked_block(oracle):
     want = np.where(step > 0, np.clip(rnd(x / np.where(step > 0, step, 1)), 0, 3), 0)
     np.testing.assert_array_equal(codes, want.astype(np.uint8))
     assert d16 > 0
+
+
+# ------------------------------------------------------------------ F16 / BF16
+def test_f16_dequant_every_pattern(oracle):
+    """F16 (src/gguf/mod.rs:921-933, half::f16::to_f32) on all 65536 bit
+    patterns equals numpy's independent float16 -> float32 conversion."""
+    bits = np.arange(65536, dtype=np.uint16)
+    got = oracle.dequantize(oracle.F16, bits.view(np.uint8), 65536)
+    want = bits.view(np.float16).astype(np.float32)
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn)
+    np.testing.assert_array_equal(got[~gn].view(np.uint32), want[~wn].view(np.uint32))
+    assert oracle.quant_bytes(oracle.F16, 77) == 154
+
+
+def test_bf16_dequant_known_values_and_round_trip(oracle):
+    """BF16 (src/gguf/mod.rs:934-946): known encodings, and every f32 whose low
+    16 bits are zero comes back exactly from its top half."""
+    cases = {0x3F80: 1.0, 0xC000: -2.0, 0x4049: 3.140625, 0x0000: 0.0, 0x8000: -0.0,
+             0x7F80: np.inf, 0xFF80: -np.inf, 0x0001: 2.0 ** -133, 0x0080: 2.0 ** -126,
+             0x7F7F: 3.3895313892515355e38}
+    bits = np.array(list(cases), np.uint16)
+    got = oracle.dequantize(oracle.BF16, bits.view(np.uint8), bits.size)
+    for b, g in zip(cases, got):
+        assert g == np.float32(cases[b]) and np.signbit(g) == np.signbit(np.float32(cases[b])), hex(b)
+    assert np.isnan(oracle.dequantize(oracle.BF16, np.array([0x7FC0], np.uint16).view(np.uint8), 1)[0])
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(4096) * 10.0 ** rng.uniform(-30, 30, 4096)).astype(np.float32)
+    x = (x.view(np.uint32) & 0xFFFF0000).view(np.float32)
+    top = (x.view(np.uint32) >> 16).astype(np.uint16)
+    back = oracle.dequantize(oracle.BF16, top.view(np.uint8), top.size)
+    np.testing.assert_array_equal(back.view(np.uint32), x.view(np.uint32))
+    # a short payload gives what it holds (chunks_exact drops the ragged byte)
+    assert oracle.dequantize(oracle.BF16, top.view(np.uint8)[:7], 10).size == 3
