@@ -25,14 +25,14 @@
 // match an fp32 evaluation to a few units of 2^-22 of the chunk maximum.
 //
 // Work: a workgroup of 4 waves owns one tile of up to 16 pairs of one
-// expert (the permutation's tile list with tile_m = 16) and 64 weight rows
-// (of both matrices for gate/up); wave w owns 16 of them (RT row tiles of
-// 16).  The K loop takes one Q4_K block (256 positions) per
-// chunk.  The activation chunk of the 16 pairs is staged through a
-// double-buffered LDS area in MFMA operand layout, together with each
-// pair's sub-block sums and unscale factor; every lane reads its operands
-// for the chunk once and applies them to all of its row tiles.  The codes
-// and scales of the next chunk are in flight while a chunk is computed.
+// expert (the permutation's tile list with tile_m = 16), 256 weight rows
+// (of both matrices for gate/up) and one K slice of 4 chunks (a chunk is
+// one Q4_K block, 256 positions); wave w streams 64 of the rows as 4 row
+// tiles of 16.  The slice's activations of the tile's pairs are staged
+// once into LDS in MFMA operand layout, with each pair's unscale factor;
+// the codes and scales of the next 3 (row tile, chunk) steps are in flight
+// while a step is computed.  Slices write partial sums, which the SwiGLU
+// kernel (gate/up) and the weighted combine (down) add in slice order.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 
@@ -155,7 +155,6 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
     }
   };
 
-  // step (row tile rt, chunk kc) into accr, the row tile's accumulators
   // the first steps' codes go out before the staging: the weights do not
   // depend on the activations, and their latency overlaps the staging's
   MfvStep<NMAT> ring[MV_D];
