@@ -243,17 +243,33 @@ __global__ __launch_bounds__(256) void k_route_permute(
   }
 }
 
-// y value of row p, column h: the sum of the NS partial buffers (K splits)
+// y value at offset o: the sum of the ns partial buffers (K splits) in
+// split order.  NS == 1: one buffer.  Otherwise the buffers are read 8 at a
+// time (indices past the last clamped to it), so a run of loads is in flight
+// together instead of one dependent load per buffer.
 template <int NS>
 __device__ __forceinline__ float y_at(const float *__restrict__ y, size_t stride, int ns, size_t o) {
-  float v = y[o];
-  if constexpr (NS != 1) {
-    for (int s = 1; s < ns; ++s) v += y[s * stride + o];
+  if constexpr (NS == 1) {
+    return y[o];
+  } else {
+    float v = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float u[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) u[j] = y[(size_t)min(s0 + j, ns - 1) * stride + o];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < ns) v = s0 + j == 0 ? u[j] : v + u[j];
+    }
+    return v;
   }
-  return v;
 }
 
-template <int NS>
+// out[t] = sum_r w[t,r] * y[pair(t,r)] (+ shared) in route order
+// (src/engine/mod.rs:1017-1021).  The routes' pair indices and weights are
+// read RB at a time (clamped to the last route), then their y values, so
+// the loads of a token's routes overlap.
+template <int NS, int RB>
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair,
                                                  const float *__restrict__ rw,
                                                  const int32_t *__restrict__ rcnt,
@@ -265,12 +281,24 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair
        i += (size_t)gridDim.x * blockDim.x) {
     const int t = (int)(i / H), h = (int)(i - (size_t)t * H);
     const int n = rcnt[t];
+    const float sh = shared ? y_at<NS>(ypair, stride, ns, ((size_t)T * k + t) * H + h) : 0.f;
     float acc = 0.0f;
-    for (int r = 0; r < n; ++r) {
-      const int p = inv[(size_t)t * k + r];
-      acc = acc + __fmul_rn(rw[(size_t)t * k + r], y_at<NS>(ypair, stride, ns, (size_t)p * H + h));
+    for (int r0 = 0; r0 < n; r0 += RB) {
+      int p[RB];
+      float w[RB], yv[RB];
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        const size_t r = (size_t)t * k + min(r0 + j, n - 1);
+        p[j] = inv[r];
+        w[j] = rw[r];
+      }
+#pragma unroll
+      for (int j = 0; j < RB; ++j) yv[j] = y_at<NS>(ypair, stride, ns, (size_t)p[j] * H + h);
+#pragma unroll
+      for (int j = 0; j < RB; ++j)
+        if (r0 + j < n) acc = acc + __fmul_rn(w[j], yv[j]);
     }
-    if (shared) acc = acc + y_at<NS>(ypair, stride, ns, ((size_t)T * k + t) * H + h);
+    if (shared) acc = acc + sh;
     out[i] = residual ? residual[i] + acc : acc;
   }
 }
@@ -343,16 +371,23 @@ int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const
   if (total == 0) return NX_OK;
   size_t g = (total + 255) / 256;
   if (g > 65536) g = 65536;
-  if (nsplit <= 1)
+  const int ns = nsplit > 1 ? nsplit : 1;
+  const int sh = shared ? 1 : 0;
+  auto go = [&](auto kern) {
     return launch(c, "combine", [&] {
-      k_combine<1><<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H,
-                                                       shared ? 1 : 0, d_out, 1, 0, d_residual);
+      kern<<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H, sh,
+                                               d_out, ns, split_stride, d_residual);
     });
-  return launch(c, "combine", [&] {
-    k_combine<0><<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H,
-                                                     shared ? 1 : 0, d_out, nsplit, split_stride,
-                                                     d_residual);
-  });
+  };
+  // routes read together: top-k up to 2, 4, else 8 at a time
+  if (ns == 1) {
+    if (k <= 2) return go(k_combine<1, 2>);
+    if (k <= 4) return go(k_combine<1, 4>);
+    return go(k_combine<1, 8>);
+  }
+  if (k <= 2) return go(k_combine<0, 2>);
+  if (k <= 4) return go(k_combine<0, 4>);
+  return go(k_combine<0, 8>);
 }
 
 }  // namespace nx
