@@ -886,7 +886,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
     const bool route_in_gemv = T == 1 && E <= kFusedRouteMaxE && k <= 64;
     if (!route_in_gemv && route_permute_fusable(T, E, k)) {
       NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
-                                  d_pt, d_ps, d_inv, d_act, nullptr, 0));
+                                  d_pt, d_ps, d_inv, d_act, 0, nullptr, nullptr, 0));
     } else if (!route_in_gemv) {
       NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
       NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, 0, d_ec, d_off, d_pt, d_ps, d_inv, d_act,
@@ -912,9 +912,14 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
     const int max_tiles = mfv_max_tiles(T, k, E);
     int32_t *d_tiles;
     NX_TRY(ws(c, WS_TILES, 2 + 2 * (size_t)max_tiles, &d_tiles));
-    NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
-    NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, kMfvTileM, d_ec, d_off, d_pt, d_ps, d_inv,
-                          d_act, d_tiles, 0));
+    if (route_permute_fusable(T, E, k)) {
+      NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
+                                  d_pt, d_ps, d_inv, d_act, kMfvTileM, d_tiles, nullptr, 0));
+    } else {
+      NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
+      NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, kMfvTileM, d_ec, d_off, d_pt, d_ps, d_inv,
+                            d_act, d_tiles, 0));
+    }
     MfvPlan mp{ex, T, k, d_x, d_pt, d_off, d_tiles, max_tiles, d_w, d_cnt, d_inv, d_out, d_residual};
     return launch_mfv(c, mp);
   }

@@ -173,12 +173,14 @@ int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, i
                    int E, int tile_m, int32_t *d_ecount, int32_t *d_offsets, int32_t *d_ptok,
                    int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles,
                    int shared_T);
-// router + permutation in one workgroup, for small batches
+// router + permutation in one workgroup, for small batches; d_tiles
+// (optional) as for launch_permute, without shared-expert tiles
 bool route_permute_fusable(int T, int E, int k);
 int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
                          int32_t *d_expert, float *d_weight, int32_t *d_count, int32_t *d_ecount,
                          int32_t *d_offsets, int32_t *d_ptok, int32_t *d_pslot, int32_t *d_inv,
-                         int32_t *d_active, int *d_counters, int n_counters);
+                         int32_t *d_active, int tile_m, int32_t *d_tiles, int *d_counters,
+                         int n_counters);
 // logits[t][e] = sum_c w[e][c] x[t][c]; exact: the reference's sequential
 // order with separately rounded products and sums
 int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, int E, int H,

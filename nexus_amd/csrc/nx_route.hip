@@ -179,26 +179,34 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
   }
 }
 
-// Router and permutation in one workgroup of 256 threads for small batches
-// (T*k <= 256, E <= 256): each wave routes tokens wave, wave+4, ...; then
-// thread e counts expert e's pairs, the workgroup scans the counts, and
-// thread e assigns its pairs their positions in (token, slot) order.
+// Router and permutation in one workgroup for small batches (T*k <= 256,
+// E <= 256): each of the 16 waves routes tokens wave, wave + 16, ...; each
+// valid pair (token t, slot r), i = t k + r, sets bit i of its expert's row
+// of a bit matrix; thread e counts expert e's pairs, the workgroup scans the
+// counts, and pair i's position within its expert is the number of bits
+// below bit i in that row — the (token, slot) order of k_permute.
+// tiles (optional): the tile list of k_permute, tile_m pairs per tile.
 constexpr int RP_MAX_PAIRS = 256;
+constexpr int RP_THREADS = 1024;
+constexpr int RP_WORDS = RP_MAX_PAIRS / 32;  // bit-matrix words per expert
 
 template <int EPL>
-__global__ __launch_bounds__(256) void k_route_permute(
+__global__ __launch_bounds__(RP_THREADS) void k_route_permute(
     const float *__restrict__ logits, int T, int E, int k, int score_mode,
     int32_t *__restrict__ rexp, float *__restrict__ rw, int32_t *__restrict__ rcnt,
     int32_t *__restrict__ ecount, int32_t *__restrict__ offsets, int32_t *__restrict__ ptok,
     int32_t *__restrict__ pslot, int32_t *__restrict__ inv, int32_t *__restrict__ active,
-    int *__restrict__ counters, int n_counters) {
+    int tile_m, int32_t *__restrict__ tiles, int *__restrict__ counters, int n_counters) {
   __shared__ int s_exp[RP_MAX_PAIRS];
   __shared__ int s_cnt[RP_MAX_PAIRS];
-  __shared__ int wave_tot[PERM_THREADS / 64];
+  __shared__ int s_base[256];
+  __shared__ uint32_t s_bits[256 * RP_WORDS];
+  __shared__ int wave_tot[RP_THREADS / 64];
   __shared__ int total;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int i = tid; i < n_counters; i += 256) counters[i] = 0;
-  for (int t = wave; t < T; t += 4) {
+  for (int i = tid; i < n_counters; i += RP_THREADS) counters[i] = 0;
+  for (int i = tid; i < E * RP_WORDS; i += RP_THREADS) s_bits[i] = 0;
+  for (int t = wave; t < T; t += RP_THREADS / 64) {
     int e, n;
     float w;
     route_one<EPL>(logits + (size_t)t * E, E, k, score_mode, lane, &e, &w, &n);
@@ -206,7 +214,6 @@ __global__ __launch_bounds__(256) void k_route_permute(
       rexp[(size_t)t * k + lane] = e;
       rw[(size_t)t * k + lane] = w;
       s_exp[t * k + lane] = e;
-      inv[(size_t)t * k + lane] = -1;
     }
     if (lane == 0) {
       rcnt[t] = n;
@@ -214,10 +221,16 @@ __global__ __launch_bounds__(256) void k_route_permute(
     }
   }
   __syncthreads();
+  const int pairs = T * k;
+  const int pt = tid / k, pr = tid - pt * k;  // pair tid = (token, slot)
+  const bool pvalid = tid < pairs && pr < s_cnt[pt];
+  const int pe = pvalid ? s_exp[tid] : 0;
+  if (pvalid) atomicOr(&s_bits[pe * RP_WORDS + (tid >> 5)], 1u << (tid & 31));
+  __syncthreads();
   int c = 0;
   if (tid < E) {
-    for (int t = 0; t < T; ++t)
-      for (int r = 0; r < s_cnt[t]; ++r) c += s_exp[t * k + r] == tid;
+#pragma unroll
+    for (int w = 0; w < RP_WORDS; ++w) c += __popc(s_bits[tid * RP_WORDS + w]);
   }
   const int b = block_exclusive_scan(c, wave_tot, &total);
   const int npairs = total;
@@ -226,20 +239,38 @@ __global__ __launch_bounds__(256) void k_route_permute(
   if (tid < E) {
     ecount[tid] = c;
     offsets[tid] = b;
+    s_base[tid] = b;
     if (c > 0) active[act] = tid;
-    int pos = b;
-    for (int t = 0; t < T && pos < b + c; ++t)
-      for (int r = 0; r < s_cnt[t]; ++r)
-        if (s_exp[t * k + r] == tid) {
-          ptok[pos] = t;
-          pslot[pos] = r;
-          inv[(size_t)t * k + r] = pos;
-          ++pos;
-        }
+  }
+  if (tiles != nullptr) {
+    const int nt = tid < E ? (c + tile_m - 1) / tile_m : 0;
+    const int tb = block_exclusive_scan(nt, wave_tot, &total);
+    for (int j = 0; j < nt; ++j) {
+      tiles[2 + 2 * (tb + j)] = tid;
+      tiles[2 + 2 * (tb + j) + 1] = j * tile_m;
+    }
+    if (tid == 0) {
+      tiles[0] = total;
+      tiles[1] = 0;
+    }
   }
   if (tid == 0) {
     offsets[E] = npairs;
     active[E] = n_active;
+  }
+  __syncthreads();
+  if (tid < pairs) {
+    int pos = -1;
+    if (pvalid) {
+      const uint32_t *row = s_bits + pe * RP_WORDS;
+      const int wi = tid >> 5;
+      int rank = __popc(row[wi] & ((1u << (tid & 31)) - 1u));
+      for (int w = 0; w < wi; ++w) rank += __popc(row[w]);
+      pos = s_base[pe] + rank;
+      ptok[pos] = pt;
+      pslot[pos] = pr;
+    }
+    inv[tid] = pos;
   }
 }
 
@@ -348,15 +379,18 @@ bool route_permute_fusable(int T, int E, int k) {
 int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
                          int32_t *d_expert, float *d_weight, int32_t *d_count, int32_t *d_ecount,
                          int32_t *d_offsets, int32_t *d_ptok, int32_t *d_pslot, int32_t *d_inv,
-                         int32_t *d_active, int *d_counters, int n_counters) {
+                         int32_t *d_active, int tile_m, int32_t *d_tiles, int *d_counters,
+                         int n_counters) {
   if (!route_permute_fusable(T, E, k)) return fail(NX_ERR_UNSUPPORTED, "batch too large for the fused router");
   const int epl = (E + 63) / 64;
   const int nc = d_counters ? n_counters : 0;
+  const int tm = tile_m > 0 ? tile_m : 1;
 #define NX_RP(N)                                                                              \
   return launch(c, "route_permute", [&] {                                                     \
-    k_route_permute<N><<<1, 256, 0, c->stream>>>(d_logits, T, E, k, score_mode, d_expert,     \
-                                                 d_weight, d_count, d_ecount, d_offsets, d_ptok, \
-                                                 d_pslot, d_inv, d_active, d_counters, nc);    \
+    k_route_permute<N><<<1, RP_THREADS, 0, c->stream>>>(d_logits, T, E, k, score_mode, d_expert, \
+                                                        d_weight, d_count, d_ecount, d_offsets,  \
+                                                        d_ptok, d_pslot, d_inv, d_active, tm,    \
+                                                        d_tiles, d_counters, nc);                \
   })
   if (epl <= 1) NX_RP(1);
   if (epl <= 2) NX_RP(2);
