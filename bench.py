@@ -463,9 +463,14 @@ def main():
     step_bytes = gateup_bytes + down_bytes
     print("bench: per-kernel mean ms " + json.dumps({k_: round(v, 5) for k_, v in kern.items()}),
           file=sys.stderr, flush=True)
-    gu_ms = kern.get("gemv_gateup", float("nan"))
-    dn_ms = kern.get("gemv_down_combine", float("nan"))
-    achieved = gateup_bytes / (gu_ms * 1e-3) / 1e9
+    # the dominant kernel (gate/up) and the down kernel of the path that ran
+    ran = path_of(kern)
+    gu_name, dn_name = {"gemv": ("gemv_gateup", "gemv_down_combine"),
+                        "mfma_split": ("mfv_gateup", "mfv_down")}.get(ran, (None, None))
+    if dn_name == "gemv_down_combine" and dn_name not in kern:
+        dn_name = "gemv_down"
+    gu_ms, dn_ms = kern.get(gu_name), kern.get(dn_name)
+    achieved = gateup_bytes / (gu_ms * 1e-3) / 1e9 if gu_ms else None
 
     extra = {}
     if not args.no_extra:
@@ -489,9 +494,10 @@ def main():
         print("bench: dense matvec", file=sys.stderr, flush=True)
         extra["dense_matvec_1_token"] = dense_cases(nx, ctx, torch, args)
 
+    # HBM bytes per launch measured by counters exist for the one-token GEMV
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "gemv_gateup_mixtral_q4k_t1_traffic.json")
-    if os.path.exists(tpath):
+    if ran == "gemv" and T == 1 and os.path.exists(tpath):
         try:
             traffic = json.load(open(tpath)).get("bytes_per_launch")
         except Exception:
@@ -522,10 +528,11 @@ def main():
         "effective_GBps": step_bytes / (ms_per_step * 1e-3) / 1e9,
         "layer_hbm_frac": step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS,
         "kernels_ms": {k_: round(v, 5) for k_, v in kern.items()},
-        "roofline": {"bound": "hbm", "kernel": "gemv_gateup", "achieved": achieved,
-                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
+        "roofline": {"bound": "hbm", "kernel": gu_name, "achieved": achieved,
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS if achieved else None,
                      "traffic": traffic, "algorithmic_bytes": gateup_bytes},
-        "down_gemv_GBps": down_bytes / (dn_ms * 1e-3) / 1e9,
+        "down_GBps": down_bytes / (dn_ms * 1e-3) / 1e9 if dn_ms else None,
         "cpu_baseline": cpu,
     }
     rec.update(extra)
