@@ -179,14 +179,14 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
   }
 }
 
-// Router and permutation in one workgroup for small batches (T*k <= 256,
-// E <= 256): each of the 16 waves routes tokens wave, wave + 16, ...; each
-// valid pair (token t, slot r), i = t k + r, sets bit i of its expert's row
+// Router and permutation in one workgroup for small batches (T <= 32,
+// T*k <= 512, E <= 256): each of the 16 waves routes tokens wave,
+// wave + 16; each valid pair (token t, slot r), i = t k + r, sets bit i of its expert's row
 // of a bit matrix; thread e counts expert e's pairs, the workgroup scans the
 // counts, and pair i's position within its expert is the number of bits
 // below bit i in that row — the (token, slot) order of k_permute.
 // tiles (optional): the tile list of k_permute, tile_m pairs per tile.
-constexpr int RP_MAX_PAIRS = 256;
+constexpr int RP_MAX_PAIRS = 512;
 constexpr int RP_THREADS = 1024;
 constexpr int RP_WORDS = RP_MAX_PAIRS / 32;  // bit-matrix words per expert
 
@@ -373,7 +373,10 @@ int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, i
 }
 
 bool route_permute_fusable(int T, int E, int k) {
-  return T >= 1 && (long)T * k <= RP_MAX_PAIRS && E <= 256 && k <= 64;
+  // each wave routes its tokens one after another: beyond two per wave the
+  // router kernel, spread over the chip, is faster
+  return T >= 1 && T <= 2 * (RP_THREADS / 64) && (long)T * k <= RP_MAX_PAIRS && E <= 256 &&
+         k <= 64;
 }
 
 int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,

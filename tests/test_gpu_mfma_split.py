@@ -40,6 +40,21 @@ def test_split_parity(ctx, E, H, F, k, T, score):
     assert rel_l2(got, L.oracle_out()) <= TOL
 
 
+@pytest.mark.parametrize("T,k", [(31, 8), (32, 8), (33, 8), (32, 16), (64, 8)])
+def test_fused_router_limits(ctx, T, k):
+    """Batches around the one-workgroup router's limits (32 tokens, 512
+    pairs; beyond them the router and permutation kernels run), on the split
+    path and the GEMV."""
+    L = Layer(Q4_K, 64, 256, 512, k, T, seed=T + k)
+    ex = L.upload(nx, ctx)
+    split = ex.forward(L.x, L.logits, k, 0, nx.PATH_MFMA_SPLIT)
+    gemv = ex.forward(L.x, L.logits, k, 0, nx.PATH_GEMV)
+    ex.close()
+    ref = L.oracle_out()
+    assert rel_l2(split, ref) <= TOL
+    assert rel_l2(gemv, ref) <= TOL
+
+
 def test_split_magnitudes_and_zero_rows(ctx):
     L = Layer(Q4_K, 8, 512, 512, 2, 12, seed=41)
     scale = np.array([1e-30, 1e-6, 1.0, 3e3, 1e6, 0.0, 1.0, 1e-3, 7.0, 0.0, 1e4, 1e-2],
