@@ -439,14 +439,16 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   // wave index, known to the compiler as wave-uniform
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = KSPLIT > 1 ? 0 : (LPR == 64 ? wave : tid / LPR);
+  // row group of this thread; with KSPLIT > 1, waves grp KSPLIT ..
+  // grp KSPLIT + KSPLIT - 1 share its rows, each over its own segments
+  const int grp = KSPLIT > 1 ? wave / KSPLIT : (LPR == 64 ? wave : tid / LPR);
 
   // one wave per row group: the workgroup shares the activation operands
   constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32 && FMT != NX_FMT_F16 &&
                         FMT != NX_FMT_BF16;
   __shared__ uint4 xsh[COOP ? NT * 64 * RG::XW : 1];
   RG g;
-  g.init(KSPLIT == 1 ? (lane % LPR) : tid);
+  g.init(KSPLIT == 1 ? (lane % LPR) : tid % L);
   float xq[NT][RG::XQ];  // activation quarters in flight (COOP)
   bool x_issued = false;  // set only by the in-kernel routing (NT == 1)
 
@@ -526,7 +528,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
                 red[((wave * U + u) * NMAT + mt) * NT + t] = acc[u][mt][t];
         }
         __syncthreads();
-        writer = tid == 255;
+        writer = tid == grp * L + L - 1;  // the group's last thread
         if (writer) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
@@ -536,7 +538,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
               for (int t = 0; t < NT; ++t) {
                 float s = 0.f;
 #pragma unroll
-                for (int w = 0; w < KSPLIT; ++w) s += red[((w * U + u) * NMAT + mt) * NT + t];
+                for (int w = 0; w < KSPLIT; ++w)
+                  s += red[(((grp * KSPLIT + w) * U + u) * NMAT + mt) * NT + t];
                 acc[u][mt][t] = s;
               }
         }
@@ -560,13 +563,16 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
       }
     };
 
-    // with KSPLIT > 1 the whole workgroup is one row group, so the trip
-    // count (and every barrier in finish) is workgroup-uniform
-    for (int r = row_begin; r < row_end; r += S * U) {
+    // with KSPLIT > 1 finish has barriers, so the trip count must be
+    // workgroup-uniform: one row group per workgroup runs to row_end; with
+    // several, every group runs rows_per_group rows (rows past row_end load
+    // as zeros and are not written)
+    const int row_lim = (KSPLIT > 1 && GROUPS > 1) ? row_begin + a.rows_per_group : row_end;
+    for (int r = row_begin; r < row_lim; r += S * U) {
 #pragma unroll
       for (int i = 0; i < S; ++i) {
         const int rr = r + i * U;
-        if (rr >= row_end) break;
+        if (rr >= row_lim) break;
         g.load(st[(i + S - 1) % S], v, rr + (S - 1) * U, row_end);
         finish(st[i], rr);
       }
@@ -595,8 +601,8 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
   // half and wave index, known to the compiler as wave-uniform
   const int half = __builtin_amdgcn_readfirstlane(tid >> 8);
   const int wave = __builtin_amdgcn_readfirstlane(tl >> 6);
-  const int grp = KSPLIT > 1 ? 0 : (LPR == 64 ? wave : tl / LPR);
-  const int kpart = KSPLIT == 1 ? 0 : wave;  // which partial this wave leaves
+  const int grp = KSPLIT > 1 ? wave / KSPLIT : (LPR == 64 ? wave : tl / LPR);
+  const int kpart = KSPLIT == 1 ? 0 : wave % KSPLIT;  // which partial this wave leaves
 
   const int n_active = a.active[a.E];
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
@@ -609,7 +615,7 @@ __global__ __launch_bounds__(256 * DOWN_SG, 1) void k_gemv_down(const GemvArgs a
   float *ybuf = YLDS ? ypart_lds : a.gpart + (size_t)blockIdx.x * KSPLIT * npairs * wg_rows;
 
   RG g;
-  g.init(KSPLIT == 1 ? (lane % LPR) : tl);
+  g.init(KSPLIT == 1 ? (lane % LPR) : tl % L);
   const bool writer = (g.li % LPR) == LPR - 1;
 
   // Stage positions: (slot, first token of the group, first row).  The
@@ -757,6 +763,8 @@ KernelFn pick_shape(int gateup, bool ylds, const Shape &s) {
     if (s.lpr == 64 && s.spl == 1) return inst<FMT, NT, 64, 1, 1>(gateup, ylds);
     if constexpr (two)
       if (s.lpr == 64 && s.spl == 2) return inst<FMT, NT, 64, 1, 2>(gateup, ylds);
+  } else if (s.ksplit == 2) {
+    if (s.spl == 1) return inst<FMT, NT, 64, 2, 1>(gateup, ylds);
   } else {
     if (s.spl == 1) return inst<FMT, NT, 64, 4, 1>(gateup, ylds);
     if constexpr (two)
@@ -804,6 +812,7 @@ bool choose_shape(int nseg, int eps, int nt, Shape *s) {
   else if (nseg <= 32) *s = {32, 1, 1};
   else if (nseg <= 64) *s = {64, 1, 1};
   else if (nseg <= 128 && 2 * eps * nt <= budget) *s = {64, 1, 2};
+  else if (nseg <= 128) *s = {64, 2, 1};
   else if (nseg <= 256) *s = {64, 4, 1};
   else if (nseg <= 512 && 2 * eps * nt <= budget) *s = {64, 4, 2};
   else return false;
