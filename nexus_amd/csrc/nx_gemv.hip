@@ -489,7 +489,11 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
   const int slot = blockIdx.y;
   if (slot >= n_slots) return;  // workgroup-uniform
-  __shared__ float red[KSPLIT > 1 ? 4 * U * NMAT * NT : 1];
+  // KSPLIT > 1: per-wave partial sums of up to RED_ROWS rows, summed across
+  // the group's waves once per RED_ROWS rows (two barriers), not per stage
+  constexpr int RED_ROWS = 32;
+  static_assert(RED_ROWS % U == 0, "a stage's rows share one run of partials");
+  __shared__ float red[KSPLIT > 1 ? 4 * RED_ROWS * NMAT * NT : 1];
 
   const SlotView v = slot_view(a, slot, n_active, active, offsets);
   const int row_begin = (blockIdx.x * GROUPS + grp) * a.rows_per_group;
@@ -497,6 +501,12 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   auto row_of = [&](int t) {
     return PLAIN ? v.pair0 + t : (v.routed ? perm_token[v.pair0 + t] : t);
   };
+
+  // with KSPLIT > 1 finish has barriers, so the stage sequence must be
+  // workgroup-uniform: one row group per workgroup runs to row_end; with
+  // several, every group runs rows_per_group rows (rows past row_end load as
+  // zeros and are not written)
+  const int row_lim = (KSPLIT > 1 && GROUPS > 1) ? row_begin + a.rows_per_group : row_end;
 
   typename RG::Stage st[S];
   for (int t0 = 0; t0 < v.count; t0 += NT) {
@@ -516,8 +526,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
     auto finish = [&](const typename RG::Stage &st, int r0) {
       float acc[U][NMAT][NT];
       g.template compute<LPR>(st, acc);
-      bool writer = (g.li % LPR) == LPR - 1;
+      const bool writer = (g.li % LPR) == LPR - 1;
       if constexpr (KSPLIT > 1) {
+        // the wave's partials of rows r0 .. r0 + U - 1 (lane 63 holds them)
+        const int sr = (r0 - row_begin) % RED_ROWS;
         if (lane == 63) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
@@ -525,25 +537,32 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
             for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
               for (int t = 0; t < NT; ++t)
-                red[((wave * U + u) * NMAT + mt) * NT + t] = acc[u][mt][t];
+                red[((wave * RED_ROWS + sr + u) * NMAT + mt) * NT + t] = acc[u][mt][t];
         }
-        __syncthreads();
-        writer = tid == grp * L + L - 1;  // the group's last thread
-        if (writer) {
+        // a full run of partials, or the group's last stage (both
+        // workgroup-uniform: every group runs the same stage sequence)
+        if (sr + U == RED_ROWS || r0 + U >= row_lim) {
+          __syncthreads();
+          const int rb = r0 + U - (sr + U);  // first row of the run
+          for (int i = tid % L; i < (sr + U) * NT; i += L) {
+            const int rl = i / NT, t = i - rl * NT;
+            const int r = rb + rl;
+            if (r >= row_end || t0 + t >= v.count) continue;
+            float sm[NMAT];
 #pragma unroll
-          for (int u = 0; u < U; ++u)
+            for (int mt = 0; mt < NMAT; ++mt) {
+              float s = 0.f;
 #pragma unroll
-            for (int mt = 0; mt < NMAT; ++mt)
-#pragma unroll
-              for (int t = 0; t < NT; ++t) {
-                float s = 0.f;
-#pragma unroll
-                for (int w = 0; w < KSPLIT; ++w)
-                  s += red[(((grp * KSPLIT + w) * U + u) * NMAT + mt) * NT + t];
-                acc[u][mt][t] = s;
-              }
+              for (int w = 0; w < KSPLIT; ++w)
+                s += red[(((grp * KSPLIT + w) * RED_ROWS + rl) * NMAT + mt) * NT + t];
+              sm[mt] = s;
+            }
+            a.out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
+                PLAIN ? sm[0] : silu_mul(sm[0], sm[NMAT - 1]);
+          }
+          __syncthreads();
         }
-        __syncthreads();
+        return;
       }
       if (writer) {
 #pragma unroll
@@ -563,11 +582,6 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
       }
     };
 
-    // with KSPLIT > 1 finish has barriers, so the trip count must be
-    // workgroup-uniform: one row group per workgroup runs to row_end; with
-    // several, every group runs rows_per_group rows (rows past row_end load
-    // as zeros and are not written)
-    const int row_lim = (KSPLIT > 1 && GROUPS > 1) ? row_begin + a.rows_per_group : row_end;
     for (int r = row_begin; r < row_lim; r += S * U) {
 #pragma unroll
       for (int i = 0; i < S; ++i) {
