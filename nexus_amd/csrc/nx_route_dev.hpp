@@ -24,10 +24,33 @@ __device__ __forceinline__ float unsortable(uint32_t s) {
   return __uint_as_float((s & 0x80000000u) ? (s & 0x7FFFFFFFu) : ~s);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  const uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
-  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+// v of another lane of the same 16-lane row, by a DPP lane pattern (every
+// lane reads a lane inside its row, so none reads out of range)
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
   return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// maximum over the wave, in every lane: within each 16-lane row by DPP
+// (swap neighbours, swap pairs, mirror halves of 8, mirror the row), then
+// across the four rows from lanes 0, 16, 32, 48
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = max_u64(v, dpp_u64<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = max_u64(v, dpp_u64<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = max_u64(v, dpp_u64<0x141>(v));  // row_half_mirror
+  v = max_u64(v, dpp_u64<0x140>(v));  // row_mirror
+  return max_u64(max_u64(readlane_u64(v, 0), readlane_u64(v, 16)),
+                 max_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
 }
 
 // Routes one token with one wavefront.  On return lane r < *n holds the r-th
@@ -54,11 +77,7 @@ __device__ __forceinline__ void route_one(const float *__restrict__ row, int E, 
     uint64_t best = 0;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
-#pragma unroll
-    for (int m = 32; m > 0; m >>= 1) {
-      const uint64_t o = shfl_xor_u64(best, m);
-      best = o > best ? o : best;
-    }
+    best = wave_max_u64(best);
     if (best == 0) break;  // no finite logits left (uniform across the wave)
 #pragma unroll
     for (int i = 0; i < EPL; ++i)
