@@ -384,7 +384,7 @@ __device__ __forceinline__ void fused_route(const GemvArgs &a, int lane, int32_t
 #pragma unroll
   for (int j = 0; j < XJ; ++j) below[j] = hit[j] = 0;
   for (int r = 0; r < n; ++r) {
-    const int er = __shfl(e, r, 64);
+    const int er = __builtin_amdgcn_readlane(e, r);
     rank += er < e ? 1 : 0;
 #pragma unroll
     for (int j = 0; j < XJ; ++j) {

@@ -95,7 +95,8 @@ __device__ __forceinline__ void route_one(const float *__restrict__ row, int E, 
   *n_out = n;
   *w_out = 0.f;
   if (!weights) return;
-  const float l0 = __shfl(l, 0, 64);  // largest selected logit
+  // largest selected logit (lane 0's)
+  const float l0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l), 0));
   if (lane < n) {
     if (score_mode == NX_SCORE_SOFTMAX) {
       w = (float)exp((double)(l - l0));
@@ -106,7 +107,7 @@ __device__ __forceinline__ void route_one(const float *__restrict__ row, int E, 
   }
   // sequential f32 sum in route order (Iterator::sum)
   float sum = -0.0f;
-  for (int r = 0; r < n; ++r) sum = sum + __shfl(w, r, 64);
+  for (int r = 0; r < n; ++r) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), r));
   if (sum > 0.0f && lane < n) w = w / sum;
   *w_out = w;
 }
