@@ -281,6 +281,16 @@ int nx_moe_forward_dev(nx_ctx *ctx, const nx_experts *ex, const float *d_x,
                        const float *d_logits, int num_tokens, int top_k, int score_mode,
                        int path, float *d_out);
 
+/* The routes of the last nx_moe_forward[_dev] or nx_moe_block[_dev]
+ * on this context, as route_moe_experts returns them (src/engine/mod.rs:
+ * 918-966): experts / weights [num_tokens x top_k] (-1 / 0 padding) and
+ * counts[num_tokens], copied to host memory.  num_tokens and top_k must be the
+ * last call's; valid until the next call on the context.  For a
+ * single token on the GEMV path these are the routes the gate/up kernel
+ * computed itself. */
+int nx_moe_last_routes(nx_ctx *ctx, int num_tokens, int top_k, int32_t *experts, float *weights,
+                       int32_t *counts);
+
 /* One MoE block of a decoder layer, in place on hidden [T x H]:
  *   normed = rms_norm(hidden, norm_w, eps); logits = W_r . normed;
  *   hidden += MoE(normed, logits).

@@ -46,7 +46,7 @@ EXPORTS = [
     "nx_gguf_moe_info", "nx_experts_load_gguf", "nx_q4k_from_ggml", "nx_rms_norm",
     "nx_rms_norm_dev", "nx_moe_block", "nx_moe_block_dev", "nx_matrix_create",
     "nx_matrix_load", "nx_matrix_info", "nx_matrix_destroy", "nx_matvec", "nx_matvec_dev",
-    "nx_matrix_load_gguf",
+    "nx_matrix_load_gguf", "nx_moe_last_routes",
 ]
 
 _lib = None
@@ -145,6 +145,7 @@ def lib():
         "nx_matvec": ([_vp, _vp, _fp, C.c_size_t, C.c_int, _fp], C.c_int),
         "nx_matvec_dev": ([_vp, _vp, _vp, C.c_size_t, C.c_int, _vp], C.c_int),
         "nx_matrix_load_gguf": ([_vp, _vp, C.c_char_p, C.c_int, C.POINTER(_vp)], C.c_int),
+        "nx_moe_last_routes": ([_vp, C.c_int, C.c_int, _i32p, _fp, _i32p], C.c_int),
     })
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -307,6 +308,15 @@ class Context:
         check(lib().nx_route_topk(self.h, _p(lg, _fp), lg.size, T, num_experts, k, score_mode,
                                   _p(ex, _i32p), _p(w, _fp), _p(cnt, _i32p), C.byref(lists)))
         return ex[:T, :k], w[:T, :k], cnt[:T], lists.value
+
+    def last_routes(self, num_tokens: int, top_k: int):
+        """Routes of the last MoE forward on this context (experts, weights, counts)."""
+        T, k = num_tokens, top_k
+        ex = np.full((max(T, 1), max(k, 1)), -1, np.int32)
+        w = np.zeros((max(T, 1), max(k, 1)), np.float32)
+        cnt = np.zeros(max(T, 1), np.int32)
+        check(lib().nx_moe_last_routes(self.h, T, k, _p(ex, _i32p), _p(w, _fp), _p(cnt, _i32p)))
+        return ex[:T, :k], w[:T, :k], cnt[:T]
 
     def permute(self, experts, counts, num_experts: int):
         ex = np.ascontiguousarray(experts, dtype=np.int32)

@@ -66,8 +66,11 @@ static size_t gguf_bytes(int fmt, size_t n) {
 }
 
 int ws_get(nx_ctx *c, int slot, size_t bytes, void **out) {
-  DevBuf &b = c->ws[slot];
   if (bytes == 0) bytes = 256;
+  // any other use of the route slots ends what nx_moe_last_routes can read
+  if (slot == WS_ROUTE_EXPERT || slot == WS_ROUTE_WEIGHT || slot == WS_ROUTE_COUNT)
+    c->last_exp = nullptr;
+  DevBuf &b = c->ws[slot];
   if (b.cap < bytes) {
     if (b.ptr) {
       NX_HIP(hipStreamSynchronize(c->stream));
@@ -847,6 +850,11 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   NX_TRY(ws(c, WS_PERM_SLOT, tk, &d_ps));
   NX_TRY(ws(c, WS_INV_POS, tk, &d_inv));
   NX_TRY(ws(c, WS_ACTIVE, (size_t)E + 1, &d_act));
+  c->last_exp = d_exp;
+  c->last_w = d_w;
+  c->last_cnt = d_cnt;
+  c->last_T = T;
+  c->last_k = k;
 
   int use = path;
   if (ex->fmt == NX_FMT_Q2_K || ex->fmt == NX_FMT_F16 || ex->fmt == NX_FMT_BF16) {
@@ -958,6 +966,22 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
 }
 
 extern "C" {
+
+int nx_moe_last_routes(nx_ctx *c, int T, int k, int32_t *experts, float *weights,
+                       int32_t *counts) {
+  NX_TRY(check_ctx(c));
+  if (!c->last_exp) return fail(NX_ERR_INVALID_ARG, "no forward has run on this context");
+  if (T != c->last_T || k != c->last_k)
+    return fail(NX_ERR_SHAPE, "the last forward routed " + std::to_string(c->last_T) +
+                                  " tokens with top_k " + std::to_string(c->last_k));
+  if (!experts || !weights || !counts) return fail(NX_ERR_INVALID_ARG, "null buffer");
+  const size_t tk = (size_t)T * k;
+  NX_HIP(hipMemcpyAsync(experts, c->last_exp, tk * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipMemcpyAsync(weights, c->last_w, tk * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipMemcpyAsync(counts, c->last_cnt, (size_t)T * 4, hipMemcpyDeviceToHost, c->stream));
+  NX_HIP(hipStreamSynchronize(c->stream));
+  return NX_OK;
+}
 
 int nx_moe_forward(nx_ctx *c, const nx_experts *ex, const float *x, const float *logits, int T,
                    int k, int score_mode, int path, float *out) {

@@ -539,9 +539,13 @@ int moe_layout(const nx_gguf *g, int layer, RoleTensor role[3], int *E, int *H, 
            find_any(g, expert_names(layer, 2, n_sep)))
       ++n_sep;
   }
-  // shapes: gate/up [H cols, F rows], down [F cols, H rows]
+  // shapes: gate/up [H cols, F rows], down [F cols, H rows]; a file may
+  // declare any number of dims, so check before reading them
+  for (int r = 0; r < 3; ++r)
+    if (role[r].t->dims.size() < 2)
+      return fail(NX_ERR_SHAPE, "expert tensor " + role[r].t->name + " has fewer than 2 dims");
   const auto &tg = *role[0].t, &tu = *role[1].t, &td = *role[2].t;
-  const uint64_t h = tg.dims[0], f = tg.dims.size() > 1 ? tg.dims[1] : 1;
+  const uint64_t h = tg.dims[0], f = tg.dims[1];
   for (int r = 0; r < 3; ++r) {
     const auto &t = *role[r].t;
     if (t.type != tg.type)

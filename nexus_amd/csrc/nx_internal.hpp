@@ -84,6 +84,11 @@ struct nx_ctx {
   size_t lds_per_cu = 0;  // bytes of LDS per CU
   // workspace
   nx::DevBuf ws[32];
+  // route arrays of the last forward (for nx_moe_last_routes)
+  const int32_t *last_exp = nullptr;
+  const float *last_w = nullptr;
+  const int32_t *last_cnt = nullptr;
+  int last_T = 0, last_k = 0;
   // host-visible staging for blocking calls
   nx::DevBuf host_stage;
   // profiling

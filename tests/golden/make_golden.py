@@ -1,6 +1,6 @@
 """Writes the golden fixtures under tests/golden/ from the oracle.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [crafted|tiny|configs|fullshape ...]
 
 Fixtures (inputs and expected outputs only):
   crafted_blocks.npz  64 crafted GGUF blocks per format (special f16 scales,
@@ -12,6 +12,14 @@ Fixtures (inputs and expected outputs only):
                       matrices (and the shared expert's), SHA-256 of the
                       routes of the seeded tokens, and sampled output rows at
                       one token.
+  fullshape.npz       the parity workloads at full size (Mixtral Q4_K 32
+                      tokens, Qwen3 Q4_K 64 and 512 tokens, Mixtral Q8_0 2048
+                      tokens with the Zipf(1.2) router, DeepSeek Q4_K 4096
+                      tokens with sigmoid scores and the shared expert): the
+                      SHA-256 of the exact router logits and of every token's
+                      routed experts, the per-expert pair counts, and the
+                      oracle's output rows for a set of tokens that together
+                      route to every expert the workload routes to.
 
 Weights and activations come from numpy's PCG64 generator with seeds derived
 from (configuration id, expert, role); regenerating them is part of each test.
@@ -134,7 +142,123 @@ def configs():
         json.dump(res, f, indent=1)
 
 
+# Full-size parity workloads: name, seed id, tokens, fmt, E, H, F, k, shared F,
+# score mode, zipf.  Shapes, formats, routing and activations are the model
+# configurations'; the expert weights are drawn uniform on +-0.02*sqrt(3) (the
+# configurations' standard deviation 0.02), which numpy draws 13x faster than
+# normal values: DeepSeek's 771 full-size matrices take seconds.
+FULLSHAPE = [
+    ("mixtral_q4k_t32", 101, 32, Q4_K, 8, 4096, 14336, 2, 0, 0, None),
+    ("qwen3_q4k_t64", 102, 64, Q4_K, 128, 2048, 768, 8, 0, 0, None),
+    ("qwen3_q4k_t512", 102, 512, Q4_K, 128, 2048, 768, 8, 0, 0, None),
+    ("mixtral_q8_0_prefill_t2048", 103, 2048, Q8_0, 8, 4096, 14336, 2, 0, 0, 1.2),
+    ("deepseek_q4k_sigmoid_shared_t4096", 104, 4096, Q4_K, 256, 7168, 2048, 8, 2048, 1, None),
+]
+UNIFORM_HALF_WIDTH = np.float32(0.02 * np.sqrt(3.0))
+
+
+def uniform_weight(seed_id, expert, role, rows, cols):
+    """[rows x cols] f32, uniform on [-a, a) with a = 0.02 sqrt(3)."""
+    rng = np.random.default_rng([seed_id, expert, role])
+    u = rng.random((rows, cols), dtype=np.float32)
+    return (u * np.float32(2.0) - np.float32(1.0)) * UNIFORM_HALF_WIDTH
+
+
+def workload_inputs(seed_id, T, H, E):
+    """Activations ~N(0,1) [T x H] and router weight ~N(0,0.02) [E x H], from
+    separate streams, so the first tokens do not depend on T."""
+    x = np.random.default_rng([seed_id, 7]).standard_normal((T, H), dtype=np.float32)
+    router = (np.random.default_rng([seed_id, 8]).standard_normal((E, H), dtype=np.float32)
+              * np.float32(0.02))
+    return x, router
+
+
+def zipf_bias(logits, E, zipf):
+    """logit_e += ln p_e with p_e proportional to (e+1)^-zipf, in f32."""
+    if zipf is None:
+        return logits
+    p = 1.0 / np.arange(1, E + 1) ** zipf
+    return (logits + np.log(p / p.sum()).astype(np.float32)[None, :]).astype(np.float32)
+
+
+def covering_tokens(ex, cnt, E, minimum=8):
+    """Tokens that together route to every routed expert: greedy set cover
+    (most uncovered experts first, lower token first), then evenly spaced
+    tokens up to `minimum`, always including the first and last token."""
+    T = ex.shape[0]
+    routed = [set(int(e) for e in ex[t, :cnt[t]]) for t in range(T)]
+    todo = set().union(*routed)
+    chosen = []
+    while todo:
+        best = max(range(T), key=lambda t: (len(routed[t] & todo), -t))
+        chosen.append(best)
+        todo -= routed[best]
+    for t in np.linspace(0, T - 1, minimum).astype(int):
+        if len(chosen) >= minimum and t not in (0, T - 1):
+            continue
+        if int(t) not in chosen:
+            chosen.append(int(t))
+    return np.array(sorted(chosen), np.int32)
+
+
+def fullshape(only=None):
+    from concurrent.futures import ThreadPoolExecutor
+    path = os.path.join(HERE, "fullshape.npz")
+    out = dict(np.load(path, allow_pickle=False)) if os.path.exists(path) else {}
+    pool = ThreadPoolExecutor(8)
+    for name, sid, T, fmt, E, H, F, k, Fs, score, zipf in FULLSHAPE:
+        if only and name not in only:
+            continue
+        print("fullshape", name, flush=True)
+        x, router = workload_inputs(sid, T, H, E)
+        logits = np.stack(list(pool.map(lambda t: oracle.matvec(router, E, H, x[t]), range(T))))
+        logits = zipf_bias(logits, E, zipf)
+        ex, w, cnt, _ = oracle.route(logits, T, E, k, score)
+        sel = covering_tokens(ex, cnt, E)
+        need = sorted({int(e) for t in sel for e in ex[t, :cnt[t]]})
+        print(f"  {len(sel)} tokens, {len(need)} experts", flush=True)
+
+        def quant(job):
+            e, r, rows, cols = job
+            return (e, r), oracle.quantize(fmt, uniform_weight(sid, e, r, rows, cols), nthreads=1)
+
+        jobs = [(e, r, *shp) for e in need for r, shp in enumerate(shapes(H, F))]
+        if Fs:
+            jobs += [(SHARED, r, *shp) for r, shp in enumerate(shapes(H, Fs))]
+        payload = dict(pool.map(quant, jobs))
+        shared = None
+        if Fs:
+            shared = [oracle.dequantize(fmt, payload[(SHARED, r)], int(np.prod(shp)))
+                      for r, shp in enumerate(shapes(H, Fs))]
+
+        def row(t):
+            mats = [[None] * E for _ in range(3)]
+            for e in ex[t, :cnt[t]]:
+                for r, shp in enumerate(shapes(H, F)):
+                    mats[r][int(e)] = oracle.dequantize(fmt, payload[(int(e), r)],
+                                                        int(np.prod(shp)), nthreads=1)
+            return oracle.moe_layer(x[t:t + 1], logits[t:t + 1], mats[0], mats[1], mats[2], k,
+                                    score, shared=shared, nthreads=1)[0]
+
+        rows = np.stack(list(ThreadPoolExecutor(4).map(row, sel)))
+        out[f"{name}/logits_sha256"] = np.array(sha(logits))
+        out[f"{name}/routes_sha256"] = np.array(sha(ex, cnt))
+        out[f"{name}/expert_counts"] = np.bincount(ex[ex >= 0], minlength=E).astype(np.int32)
+        out[f"{name}/tokens"] = sel
+        out[f"{name}/route_weights"] = w[sel]
+        out[f"{name}/rows"] = rows.astype(np.float32)
+        del payload
+    np.savez(path, **out)
+
+
 if __name__ == "__main__":
-    crafted()
-    tiny()
-    configs()
+    what = sys.argv[1:] or ["crafted", "tiny", "configs", "fullshape"]
+    if "crafted" in what:
+        crafted()
+    if "tiny" in what:
+        tiny()
+    if "configs" in what:
+        configs()
+    if "fullshape" in what:
+        names = [a for a in what if a not in ("crafted", "tiny", "configs", "fullshape")]
+        fullshape(names or None)

@@ -275,6 +275,19 @@ def test_moe_info_rejects_inconsistent_layers(tmp_path):
         assert ei.value.code == nx.NX_ERR_UNSUPPORTED
 
 
+@pytest.mark.parametrize("gate_dims", [[], [64]])
+def test_moe_info_rejects_per_expert_tensors_without_two_dims(tmp_path, gate_dims):
+    """An untrusted file may give a per-expert tensor fewer dims than a
+    matrix has: an error, never a read past the dims it declared."""
+    w, _, _ = moe_file(oracle.Q8_0, 2, 64, 96, naming="gguf")
+    w.tensors = [(n, gate_dims if n == "blk.0.ffn_gate.0.weight" else d, t, p)
+                 for n, d, t, p in w.tensors]
+    with open_bytes(tmp_path, w.tobytes()) as g:
+        with pytest.raises(nx.NexusError, match="fewer than 2 dims") as ei:
+            g.moe_info(0)
+        assert ei.value.code == nx.NX_ERR_SHAPE
+
+
 def ggml_q4k_dequant(blocks: np.ndarray) -> np.ndarray:
     """Upstream ggml's Q4_K block dequantization (per 64 elements j: the 32
     code bytes at 32j hold elements 64j..64j+31 in their low nibbles and

@@ -249,6 +249,95 @@ def test_q4_k_hand_block(oracle):
     assert np.array_equal(dq, (d16 * np.float32(63.0)) * x)
 
 
+def _rust_round(v):
+    """f32::round: halves away from zero."""
+    v = np.float32(v)
+    return np.float32(np.sign(v) * np.floor(np.abs(v) + np.float32(0.5)))
+
+
+# Blocks on which the code of one element depends on whether the quantizer
+# divides by the f32 d / dmin it computed or by their stored f16 roundings.
+# The reference computes codes with the f32 values (src/quant/mod.rs:780-812,
+# quantize_q4_k_value :1133-1141; quantize_q2_k :875-902, quantize_q2_k_value
+# :1143) and only stores f16(d), f16(dmin) (:798-799, :906-907).  d is chosen as 1 + 0.75 * 2^-10,
+# which f16 rounds up to 1 + 2^-10 (relative +2.4e-4), and one element sits
+# just past a rounding boundary of its code by less than that.
+def test_q4k_codes_use_unrounded_d(oracle):
+    f = np.float32
+    d_target = f(1.0 + 0.75 * 2 ** -10)
+    big = f(f(d_target * f(63)) * f(15))          # sub-block 0 max: scale0 = big/15
+    scale0 = f(big / f(15))
+    d = f(scale0 / f(63))                          # max_scale / 63
+    assert d == d_target and f(np.float16(d)) == f(1.0 + 2 ** -10)
+    step = f(d * f(63))                            # scales[0] = round(scale0/d) = 63
+    x1 = f(f(14.502) * step)                       # 14.502 steps above the offset 0
+    x = np.zeros(256, np.float32)
+    x[0], x[1] = big, x1
+    q = oracle.quantize(Q4_K, x)
+    sc, mn = oracle.unpack_q4k_scales(q[4:16])
+    assert sc.tolist() == [63] + [0] * 7 and mn.tolist() == [0] * 8
+    assert q[0:2].view(np.float16)[0] == np.float16(d)
+    with_d = int(_rust_round(f(x1 / step)))                      # 15
+    with_f16 = int(_rust_round(f(x1 / f(f(np.float16(d)) * f(63)))))  # 14
+    assert (with_d, with_f16) == (15, 14)
+    assert q[16] & 15 == 15 and q[17] & 15 == with_d
+
+
+def test_q4k_codes_use_unrounded_dmin(oracle):
+    f = np.float32
+    m = f(f(1.0 + 0.75 * 2 ** -10) * f(63))      # sub-block 0 min is -m: offset0 = m
+    top = f(900.0)
+    scale0 = f(f(top + m) / f(15))
+    d = f(scale0 / f(63))
+    dmin = f(m / f(63))
+    assert f(np.float16(dmin)) > dmin
+    step = f(d * f(63))
+    off = f(dmin * f(63))                          # mins[0] = 63
+    y = f(f(f(7.5 - 0.0001) * step) - off)         # (y + offset)/scale = 7.4999
+    x = np.zeros(256, np.float32)
+    x[0], x[1], x[2] = -m, y, top
+    q = oracle.quantize(Q4_K, x)
+    sc, mn = oracle.unpack_q4k_scales(q[4:16])
+    assert sc[0] == 63 and mn[0] == 63
+    with_dmin = int(_rust_round(f(f(y + off) / step)))
+    with_f16 = int(_rust_round(f(f(y + f(f(np.float16(dmin)) * f(63))) / step)))
+    assert (with_dmin, with_f16) == (7, 8)
+    assert [q[16] & 15, q[17] & 15, q[18] & 15] == [0, with_dmin, 15]
+
+
+def test_q2k_codes_use_unrounded_d_and_dmin(oracle):
+    f = np.float32
+    # d: sub-block 0 = {big, x1, 0 ...}; scale0 = big/3, d = scale0/15
+    big = f(f(f(1.0 + 0.75 * 2 ** -10) * f(15)) * f(3))
+    d = f(f(big / f(3)) / f(15))
+    step = f(d * f(15))
+    x1 = f(f(1.5001) * step)
+    x = np.zeros(256, np.float32)
+    x[0], x[1] = big, x1
+    q = oracle.quantize(Q2_K, x)
+    assert q[0] & 15 == 15 and q[80:82].view(np.float16)[0] == np.float16(d)
+    with_d = int(_rust_round(f(x1 / step)))
+    with_f16 = int(_rust_round(f(x1 / f(f(np.float16(d)) * f(15)))))
+    assert (with_d, with_f16) == (2, 1)
+    assert [q[16] & 3, (q[16] >> 2) & 3] == [3, with_d]
+    # dmin: sub-block 0 = {-m, y, top}
+    m = f(f(1.0 + 0.75 * 2 ** -10) * f(15))
+    top = f(40.0)
+    d = f(f(f(top + m) / f(3)) / f(15))
+    dmin = f(m / f(15))
+    step = f(d * f(15))
+    off = f(dmin * f(15))
+    y = f(f(f(1.5 - 0.0001) * step) - off)
+    x = np.zeros(256, np.float32)
+    x[0], x[1], x[2] = -m, y, top
+    q = oracle.quantize(Q2_K, x)
+    assert q[0] & 15 == 15 and q[0] >> 4 == 15
+    with_dmin = int(_rust_round(f(f(y + off) / step)))
+    with_f16 = int(_rust_round(f(f(y + f(f(np.float16(dmin)) * f(15))) / step)))
+    assert (with_dmin, with_f16) == (1, 2)
+    assert [q[16] & 3, (q[16] >> 2) & 3, (q[16] >> 4) & 3] == [0, with_dmin, 3]
+
+
 # ----------------------------------------------------------------------------- Q2_K
 def test_q2k_reference_roundtrip(oracle):
     # src/quant/mod.rs:1327-1338 and src/gguf/mod.rs:1697-1714
