@@ -281,15 +281,32 @@ int nx_moe_forward_dev(nx_ctx *ctx, const nx_experts *ex, const float *d_x,
                        const float *d_logits, int num_tokens, int top_k, int score_mode,
                        int path, float *d_out);
 
-/* The routes of the last nx_moe_forward[_dev] or nx_moe_block[_dev]
+/* The routes of the last nx_moe_forward[_dev|_noalloc] or nx_moe_block[_dev]
  * on this context, as route_moe_experts returns them (src/engine/mod.rs:
  * 918-966): experts / weights [num_tokens x top_k] (-1 / 0 padding) and
  * counts[num_tokens], copied to host memory.  num_tokens and top_k must be the
- * last call's; valid until the next call on the context.  For a
+ * last call's; valid until the next call on the context (or, after the
+ * no-allocation entry point, the next such call on the device).  For a
  * single token on the GEMV path these are the routes the gate/up kernel
  * computed itself. */
 int nx_moe_last_routes(nx_ctx *ctx, int num_tokens, int top_k, int32_t *experts, float *weights,
                        int32_t *counts);
+
+/* No counterpart in the reference.  nx_moe_forward_dev for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): same arguments, semantics and
+ * kernels, but every intermediate buffer (routes, permutation, SwiGLU
+ * activations, per-pair outputs, tile lists) is carved from one static
+ * 64 MiB device array that each GPU holds until the process ends, and the
+ * call makes no hipMalloc, hipFree, hipMemset or event call.  A call whose
+ * intermediates do not fit returns NX_ERR_UNSUPPORTED before any kernel of the
+ * layer writes d_out (the Mixtral shape fits up to 32 tokens on the decode
+ * paths; prefill batches use nx_moe_forward_dev).  Profiling must
+ * be off.  Every call on one GPU shares that GPU's array, whatever the
+ * context or stream: calls that overlap in time on one GPU race. */
+int nx_moe_forward_noalloc(nx_ctx *ctx, const nx_experts *ex, const float *d_x,
+                           const float *d_logits, int num_tokens, int top_k, int score_mode,
+                           int path, float *d_out);
 
 /* One MoE block of a decoder layer, in place on hidden [T x H]:
  *   normed = rms_norm(hidden, norm_w, eps); logits = W_r . normed;

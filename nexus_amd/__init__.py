@@ -46,7 +46,7 @@ EXPORTS = [
     "nx_gguf_moe_info", "nx_experts_load_gguf", "nx_q4k_from_ggml", "nx_rms_norm",
     "nx_rms_norm_dev", "nx_moe_block", "nx_moe_block_dev", "nx_matrix_create",
     "nx_matrix_load", "nx_matrix_info", "nx_matrix_destroy", "nx_matvec", "nx_matvec_dev",
-    "nx_matrix_load_gguf", "nx_moe_last_routes",
+    "nx_matrix_load_gguf", "nx_moe_last_routes", "nx_moe_forward_noalloc",
 ]
 
 _lib = None
@@ -146,6 +146,8 @@ def lib():
         "nx_matvec_dev": ([_vp, _vp, _vp, C.c_size_t, C.c_int, _vp], C.c_int),
         "nx_matrix_load_gguf": ([_vp, _vp, C.c_char_p, C.c_int, C.POINTER(_vp)], C.c_int),
         "nx_moe_last_routes": ([_vp, C.c_int, C.c_int, _i32p, _fp, _i32p], C.c_int),
+        "nx_moe_forward_noalloc": ([_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int,
+                                    _vp], C.c_int),
     })
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -408,6 +410,12 @@ class Experts:
                     out_ptr: int, score_mode: int = SCORE_SOFTMAX, path: int = PATH_AUTO):
         check(lib().nx_moe_forward_dev(self.ctx.h, self.h, _vp(x_ptr), _vp(logits_ptr),
                                        num_tokens, top_k, score_mode, path, _vp(out_ptr)))
+
+    def forward_noalloc(self, x_ptr: int, logits_ptr: int, num_tokens: int, top_k: int,
+                        out_ptr: int, score_mode: int = SCORE_SOFTMAX, path: int = PATH_AUTO):
+        """forward_dev with every intermediate in the library's static scratch array."""
+        check(lib().nx_moe_forward_noalloc(self.ctx.h, self.h, _vp(x_ptr), _vp(logits_ptr),
+                                           num_tokens, top_k, score_mode, path, _vp(out_ptr)))
 
 
 class Matrix:

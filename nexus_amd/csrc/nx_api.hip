@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -65,11 +66,57 @@ static size_t gguf_bytes(int fmt, size_t n) {
   return 0;
 }
 
+// Scratch of nx_moe_forward_noalloc: one static array per device, resident
+// until the process ends.  Host code never passes `scratch` itself to a
+// kernel (in host code the name is a host-side stand-in, not a device
+// address); it uses the address hipGetSymbolAddress returns for the device.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+static std::mutex g_scratch_mu;
+static std::vector<uint8_t *> g_scratch_ptr;  // per device; null until looked up
+
+// The scratch array's address on `device` (which must be current), looked up
+// once per device.
+static int scratch_address(int device, uint8_t **out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= device) g_scratch_ptr.resize(device + 1, nullptr);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return fail(NX_ERR_DEVICE, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    }
+    g_scratch_ptr[device] = static_cast<uint8_t *>(p);
+  }
+  *out = g_scratch_ptr[device];
+  return NX_OK;
+}
+
 int ws_get(nx_ctx *c, int slot, size_t bytes, void **out) {
   if (bytes == 0) bytes = 256;
   // any other use of the route slots ends what nx_moe_last_routes can read
   if (slot == WS_ROUTE_EXPERT || slot == WS_ROUTE_WEIGHT || slot == WS_ROUTE_COUNT)
     c->last_exp = nullptr;
+  if (c->scratch_mode) {
+    DevBuf &s = c->scratch_slot[slot];
+    if (s.ptr && s.cap >= bytes) {
+      *out = s.ptr;
+      return NX_OK;
+    }
+    const size_t cap = (bytes + 255) / 256 * 256;
+    if (cap > kScratchBytes - c->scratch_used)
+      return fail(NX_ERR_UNSUPPORTED,
+                  "nx_moe_forward_noalloc: this call needs more than the " +
+                      std::to_string(kScratchBytes) + "-byte scratch array (" +
+                      std::to_string(c->scratch_used + cap) + " bytes so far)");
+    s.ptr = c->scratch + c->scratch_used;
+    s.cap = cap;
+    c->scratch_used += cap;
+    *out = s.ptr;
+    return NX_OK;
+  }
   DevBuf &b = c->ws[slot];
   if (b.cap < bytes) {
     if (b.ptr) {
@@ -276,6 +323,12 @@ int nx_ctx_create(int device, nx_ctx **out) {
     return fail(NX_ERR_DEVICE, "hipStreamCreateWithFlags failed");
   }
   c->stream = c->own_stream;
+  // the no-allocation entry point's scratch array on this device
+  if (int rc = scratch_address(device, &c->scratch)) {
+    (void)hipStreamDestroy(c->own_stream);
+    delete c;
+    return rc;
+  }
   *out = c;
   return NX_OK;
 }
@@ -966,6 +1019,22 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
 }
 
 extern "C" {
+
+int nx_moe_forward_noalloc(nx_ctx *c, const nx_experts *ex, const float *d_x,
+                           const float *d_logits, int T, int k, int score_mode, int path,
+                           float *d_out) {
+  NX_TRY(check_ctx(c));
+  if (!c->scratch) return fail(NX_ERR_DEVICE, "no scratch array on this context's device");
+  // profiling creates HIP events: this entry point takes no resources at all
+  if (c->profile)
+    return fail(NX_ERR_INVALID_ARG, "nx_moe_forward_noalloc does not run with profiling enabled");
+  c->scratch_mode = true;
+  c->scratch_used = 0;
+  for (auto &s : c->scratch_slot) s = DevBuf{};
+  const int rc = moe_forward(c, ex, d_x, d_logits, T, k, score_mode, path, d_out, nullptr);
+  c->scratch_mode = false;
+  return rc;
+}
 
 int nx_moe_last_routes(nx_ctx *c, int T, int k, int32_t *experts, float *weights,
                        int32_t *counts) {

@@ -84,6 +84,14 @@ struct nx_ctx {
   size_t lds_per_cu = 0;  // bytes of LDS per CU
   // workspace
   nx::DevBuf ws[32];
+  // The library's static device scratch array on this context's device
+  // (hipGetSymbolAddress at context creation), used instead of ws by
+  // nx_moe_forward_noalloc: while scratch_mode is set, ws_get carves each
+  // slot from it (256-byte aligned, bump order) and never allocates.
+  uint8_t *scratch = nullptr;
+  bool scratch_mode = false;
+  size_t scratch_used = 0;
+  nx::DevBuf scratch_slot[32];
   // route arrays of the last forward (for nx_moe_last_routes)
   const int32_t *last_exp = nullptr;
   const float *last_w = nullptr;

@@ -1,0 +1,101 @@
+"""nx_moe_forward_noalloc (the entry point that allocates nothing) against
+nx_moe_forward_dev, through the C ABI.
+
+Both run the same kernels; the no-allocation call takes every intermediate
+from the library's static scratch array instead of context workspace.  The
+outputs must be bit-identical on two calls in a row, the second with fewer
+tokens (so stale scratch contents from the first call are present), on every
+path the dispatcher has: the one-token GEMV with the router inside the gate/up
+kernel, the decode-batch GEMV, the split-activation MFMA path and the grouped
+GEMM, with and without a shared expert.  Calls whose intermediates do not fit
+the array fail with NX_ERR_UNSUPPORTED and leave the output untouched.
+"""
+import numpy as np
+import pytest
+
+import nexus_amd as nx
+from moe_cases import Q4_K, Q8_0, DeviceArray, Layer, assert_same_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = nx.Context(0)
+    yield c
+    c.close()
+
+
+def run_pair(ex, layer, T, path, score, fn):
+    x = DeviceArray(T * layer.H)
+    x.upload(layer.x[:T])
+    lg = DeviceArray(T * layer.E)
+    lg.upload(layer.logits[:T])
+    out = DeviceArray(T * layer.H, fill=np.nan)
+    fn(x.ptr, lg.ptr, T, layer.k, out.ptr, score_mode=score, path=path)
+    return out.download().reshape(T, layer.H)
+
+
+CASES = [
+    # fmt, E, H, F, k, shared F, score, path, (T first, T second)
+    (Q4_K, 8, 1024, 2048, 2, 0, 0, nx.PATH_GEMV, (1, 1)),
+    (Q4_K, 8, 1024, 2048, 2, 0, 0, nx.PATH_GEMV, (6, 2)),
+    (Q4_K, 8, 1024, 2048, 2, 0, 0, nx.PATH_MFMA_SPLIT, (24, 5)),
+    (Q8_0, 8, 512, 1024, 2, 0, 0, nx.PATH_MFMA_F16, (300, 77)),
+    (Q4_K, 16, 512, 512, 4, 512, 1, nx.PATH_MFMA_BF16, (200, 33)),
+    (Q4_K, 16, 512, 512, 4, 512, 1, nx.PATH_GEMV, (1, 1)),
+    (Q8_0, 8, 512, 1024, 2, 0, 0, nx.PATH_AUTO, (40, 1)),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"{c[0]}-{c[7]}-T{c[8]}" for c in CASES])
+def test_noalloc_matches_forward_dev(ctx, case):
+    fmt, E, H, F, k, Fs, score, path, (T1, T2) = case
+    say(f"noalloc fmt={fmt} E={E} H={H} F={F} k={k} shared={Fs} path={path} T={T1},{T2}")
+    layer = Layer(fmt, E, H, F, k, max(T1, T2), seed=E * 7 + H + T1, shared_F=Fs,
+                  score_mode=score, experts_needed=[])
+    ex = layer.upload(nx, ctx)
+    for T in (T1, T2):
+        got = run_pair(ex, layer, T, path, score, ex.forward_noalloc)
+        routes_na = ctx.last_routes(T, k)
+        ref = run_pair(ex, layer, T, path, score, ex.forward_dev)
+        routes_dev = ctx.last_routes(T, k)
+        assert np.isfinite(got).all()
+        assert_same_bits(got, ref)
+        for a, b in zip(routes_na, routes_dev):
+            np.testing.assert_array_equal(a, b)
+    ex.close()
+
+
+def test_noalloc_rejects_calls_beyond_the_scratch(ctx):
+    E, H, F, k, T = 8, 256, 512, 2, 40000
+    say(f"noalloc oversize T={T}")
+    layer = Layer(Q8_0, E, H, F, k, 4, seed=5, experts_needed=[])
+    ex = layer.upload(nx, ctx)
+    rng = np.random.default_rng(3)
+    x = DeviceArray(T * H)
+    x.upload(rng.standard_normal(T * H).astype(np.float32))
+    lg = DeviceArray(T * E)
+    lg.upload(rng.standard_normal(T * E).astype(np.float32))
+    out = DeviceArray(T * H, fill=7.0)
+    with pytest.raises(nx.NexusError, match="scratch array") as e:
+        ex.forward_noalloc(x.ptr, lg.ptr, T, k, out.ptr, path=nx.PATH_MFMA_F16)
+    assert e.value.code == nx.NX_ERR_UNSUPPORTED
+    assert (out.download() == 7.0).all()
+    # profiling creates events, which this entry point does not
+    ctx.profile(True)
+    try:
+        with pytest.raises(nx.NexusError, match="profiling") as e:
+            ex.forward_noalloc(x.ptr, lg.ptr, 1, k, out.ptr)
+        assert e.value.code == nx.NX_ERR_INVALID_ARG
+    finally:
+        ctx.profile(False)
+    # a call that fits still works after the rejected one
+    small = run_pair(ex, layer, 4, nx.PATH_GEMV, 0, ex.forward_noalloc)
+    ref = run_pair(ex, layer, 4, nx.PATH_GEMV, 0, ex.forward_dev)
+    assert_same_bits(small, ref)
+    ex.close()
