@@ -15,6 +15,11 @@
 
 #include "nx_internal.hpp"
 
+// one token on the GEMV path: the gate/up kernel routes it itself
+#ifndef NX_ROUTE_IN_GEMV
+#define NX_ROUTE_IN_GEMV 1
+#endif
+
 namespace nx {
 
 static thread_local std::string g_err;
@@ -944,7 +949,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   if (use == NX_PATH_GEMV) {
     NX_TRY(ws(c, WS_YPAIR, pairs_total * H, &d_ypair));
     // one token: the gate/up kernel routes it itself (no router launch)
-    const bool route_in_gemv = T == 1 && E <= kFusedRouteMaxE && k <= 64;
+    const bool route_in_gemv = NX_ROUTE_IN_GEMV && T == 1 && E <= kFusedRouteMaxE && k <= 64;
     if (!route_in_gemv && route_permute_fusable(T, E, k)) {
       NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
                                   d_pt, d_ps, d_inv, d_act, 0, nullptr, nullptr, 0));

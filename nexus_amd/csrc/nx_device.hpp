@@ -51,6 +51,17 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
 __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
+// cache policy of the GEMV's scale-plane loads (2: non-temporal)
+#ifndef NX_GEMV_META_CPOL
+#define NX_GEMV_META_CPOL 0
+#endif
+__device__ __forceinline__ uint4 bload16m(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, NX_GEMV_META_CPOL);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t bload4m(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, NX_GEMV_META_CPOL);
+}
 // offset that lies past any matrix (loads there return zeros)
 constexpr uint32_t OOB = 0x7FFFFFF0u;
 
@@ -333,7 +344,7 @@ struct Seg<NX_FMT_Q4_K> {
     return valid ? (uint32_t)((j >> 2) * 16) : OOB;
   }
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return bload16(r, off);
+    return bload16m(r, off);
   }
   __device__ __forceinline__ static void prep(const float *x, X &o) { prep4(x, o); }
   __device__ __forceinline__ static void prep_quarter(const float *x, int q, X *o) {
@@ -379,7 +390,7 @@ struct Seg<NX_FMT_Q8_0> {
   }
   // the f16 scale may sit in either half of an aligned dword
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const uint32_t w = bload4(r, off & ~3u);
+    const uint32_t w = bload4m(r, off & ~3u);
     return (off & 2u) ? (w >> 16) : (w & 0xFFFFu);
   }
   __device__ __forceinline__ static void prep(const float *x, X &o) {
@@ -453,7 +464,7 @@ struct Seg<NX_FMT_Q4_0> {
     return valid ? (uint32_t)(j * 4) : OOB;
   }
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return bload4(r, off);
+    return bload4m(r, off);
   }
   __device__ __forceinline__ static void prep(const float *x, X &o) { prep4(x, o); }
   __device__ __forceinline__ static void prep_quarter(const float *x, int q, X *o) {
@@ -492,7 +503,7 @@ struct Seg<NX_FMT_Q2_K> {
     return valid ? (uint32_t)(j * 8) : OOB;
   }
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, NX_GEMV_META_CPOL);
     return make_uint2(v[0], v[1]);
   }
   __device__ __forceinline__ static void prep(const float *x, X &o) { prep2(x, o); }

@@ -30,6 +30,36 @@
 #include "nx_internal.hpp"
 #include "nx_route_dev.hpp"
 
+// Pipeline depths (stages; S - 1 in flight while one is decoded) of the
+// per-slot kernel: two-matrix gate/up rows and one-matrix (down) rows.
+#ifndef NX_GEMV_GATEUP_STAGES
+#define NX_GEMV_GATEUP_STAGES 2
+#endif
+#ifndef NX_GEMV_PLAIN_STAGES
+#define NX_GEMV_PLAIN_STAGES 2
+#endif
+#ifndef NX_GEMV_FUSE_COMBINE
+#define NX_GEMV_FUSE_COMBINE 0
+#endif
+// Rows of the per-slot kernel interleaved across the row groups of a slot
+// (row = group + i * groups) rather than one contiguous run per group
+#ifndef NX_GEMV_INTERLEAVE
+#define NX_GEMV_INTERLEAVE 0
+#endif
+// down rows longer than 64 segments split into K slices (per-slot kernel)
+#ifndef NX_GEMV_DOWN_SPLIT
+#define NX_GEMV_DOWN_SPLIT 1
+#endif
+// rows per pipeline stage of the one-matrix (down) per-slot kernel
+#ifndef NX_GEMV_PLAIN_ROWS
+#define NX_GEMV_PLAIN_ROWS 2
+#endif
+// cache policy of the weight-code loads (2: non-temporal, streamed past the
+// caches so the small activation and route arrays stay resident)
+#ifndef NX_GEMV_WEIGHT_CPOL
+#define NX_GEMV_WEIGHT_CPOL 2
+#endif
+
 namespace nx {
 
 namespace {
@@ -51,6 +81,9 @@ struct GemvArgs {
   float *out;
   int out_stride;
   int rows_per_group;
+  // per-slot kernel: rows interleaved across the slot's row groups
+  int row_interleave;
+  int groups_per_wg;
   // down projection: combine inputs, pair count, global partial-sum area
   const float *rw;
   const int32_t *rcnt;
@@ -59,6 +92,20 @@ struct GemvArgs {
   const float *residual;  // final_out = residual + combine when set
   int npairs;
   float *gpart;
+  // down rows in K slices (PLAIN, one wave per row): grid.y = slot * kslices
+  // + slice; slice s covers segments 64 s .. 64 s + 63 and writes its partial
+  // sums kslice_stride floats after slice s - 1's
+  int kslices;
+  size_t kslice_stride;
+  // Combine fused into the per-slot down pass (PLAIN, combine_cnt set): the
+  // last workgroup of each row block (grid.x) to finish its rows forms
+  // final_out[t][r] for the block's rows from every slot's and slice's
+  // partial sums; combine_cnt[blockIdx.x] counts the arrivals.  The gate/up
+  // pass that precedes it clears zero_cnt[0 .. n_zero).
+  int *combine_cnt;
+  int combine_rows_per_block;
+  int *zero_cnt;
+  int n_zero;
   // gate/up of one token with the routing done in the kernel: every
   // workgroup routes the token from route_logits [E]; workgroup (0, 0) also
   // writes the route and permutation arrays the down pass reads
@@ -68,6 +115,19 @@ struct GemvArgs {
   float *r_w;
 };
 
+
+__device__ __forceinline__ uint4 bload16w(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, NX_GEMV_WEIGHT_CPOL);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Logical row q of a row group -> matrix row base + q * step, present while
+// below end.
+struct RowMap {
+  int base, step, end;
+  __device__ __forceinline__ int row(int q) const { return base + q * step; }
+  __device__ __forceinline__ bool valid(int q) const { return base + q * step < end; }
+};
 
 // Workgroup-uniform description of one expert slot.
 struct SlotView {
@@ -166,26 +226,32 @@ struct RowGroup {
   };
 
   int li;      // lane index within the row group
+  int seg0;    // first segment of the row group's K slice (0: whole rows)
   XS xv[SPL][NT];  // activations of this lane's segments, per token
   typename S::Run run[NT];  // running integer dot sums, per token
 
-  __device__ __forceinline__ void init(int lane_index) {
+  __device__ __forceinline__ void init(int lane_index, int first_segment = 0) {
     li = lane_index;
+    seg0 = first_segment;
 #pragma unroll
     for (int t = 0; t < NT; ++t) run_init(run[t]);
   }
 
-  // Issue the loads of rows r0 .. r0+U-1 of view v; rows at or past row_end
-  // (and absent segments) read as zero.  When a row group spans whole waves
-  // (L >= 64) the rows are wave-uniform: each row gets its own buffer
-  // resource (size 0 past row_end), built on the scalar unit, and the lane
-  // offsets stay constant.  Otherwise rows differ within a wave and the row
-  // offset is added per lane.
+  // Issue the loads of logical rows q0 .. q0+U-1 (matrix rows rm.row(q)) of
+  // view v; rows at or past rm.end (and absent segments) read as zero.  When
+  // a row group spans whole waves (L >= 64) the rows are wave-uniform: each
+  // row gets its own buffer resource (size 0 past the end), built on the
+  // scalar unit, and the lane offsets stay constant.  Otherwise rows differ
+  // within a wave and the row offset is added per lane.
   __device__ __forceinline__ void load(Stage &st, const SlotView &v, int r0, int row_end) const {
+    load(st, v, RowMap{0, 1, row_end}, r0);
+  }
+  __device__ __forceinline__ void load(Stage &st, const SlotView &v, const RowMap &rm,
+                                       int q0) const {
     uint32_t off0[SPL], off1[SPL], moff[SPL];
 #pragma unroll
     for (int m = 0; m < SPL; ++m) {
-      const int j = li + m * L;
+      const int j = seg0 + li + m * L;
       const bool jv = j < v.nseg;
       off0[m] = jv ? seg_off(j, 0, v.nseg) : OOB;
       off1[m] = jv ? seg_off(j, 1, v.nseg) : OOB;
@@ -194,12 +260,13 @@ struct RowGroup {
     if constexpr (L >= 64) {
       // the row is wave-uniform: say so, or the resources below become
       // per-lane values and every load a waterfall loop
-      const int r0u = __builtin_amdgcn_readfirstlane(r0);
-      const int row_end_u = __builtin_amdgcn_readfirstlane(row_end);
+      const RowMap m{__builtin_amdgcn_readfirstlane(rm.base), __builtin_amdgcn_readfirstlane(rm.step),
+                     __builtin_amdgcn_readfirstlane(rm.end)};
+      const int q0u = __builtin_amdgcn_readfirstlane(q0);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int r = r0u + u;
-        const bool rv = r < row_end_u;
+        const int r = m.row(q0u + u);
+        const bool rv = r < m.end;
         const uint32_t nq = rv ? v.rq : 0u, nm = rv ? v.rm : 0u;
         const __amdgpu_buffer_rsrc_t rq0 = make_rsrc_u(v.q0 + (size_t)r * v.rq, nq);
         const __amdgpu_buffer_rsrc_t rq1 = make_rsrc_u(v.q1 + (size_t)r * v.rq, nq);
@@ -209,8 +276,8 @@ struct RowGroup {
         for (int mt = 0; mt < NMAT; ++mt) {
 #pragma unroll
           for (int m = 0; m < SPL; ++m) {
-            st.q[u][mt][m][0] = bload16(mt == 0 ? rq0 : rq1, off0[m]);
-            st.q[u][mt][m][1] = bload16(mt == 0 ? rq0 : rq1, off1[m]);
+            st.q[u][mt][m][0] = bload16w(mt == 0 ? rq0 : rq1, off0[m]);
+            st.q[u][mt][m][1] = bload16w(mt == 0 ? rq0 : rq1, off1[m]);
             st.m[u][mt][m] = S::load_meta(mt == 0 ? rm0 : rm1, moff[m]);
           }
         }
@@ -222,15 +289,16 @@ struct RowGroup {
       const __amdgpu_buffer_rsrc_t rm1 = make_rsrc_u(v.m1, (uint32_t)v.rows * v.rm);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const bool rv = r0 + u < row_end;
-        const uint32_t rqo = rv ? (uint32_t)(r0 + u) * v.rq : OOB;
-        const uint32_t rmo = rv ? (uint32_t)(r0 + u) * v.rm : OOB;
+        const int r = rm.row(q0 + u);
+        const bool rv = r < rm.end;
+        const uint32_t rqo = rv ? (uint32_t)r * v.rq : OOB;
+        const uint32_t rmo = rv ? (uint32_t)r * v.rm : OOB;
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt) {
 #pragma unroll
           for (int m = 0; m < SPL; ++m) {
-            st.q[u][mt][m][0] = bload16(mt == 0 ? rq0 : rq1, rqo + off0[m]);
-            st.q[u][mt][m][1] = bload16(mt == 0 ? rq0 : rq1, rqo + off1[m]);
+            st.q[u][mt][m][0] = bload16w(mt == 0 ? rq0 : rq1, rqo + off0[m]);
+            st.q[u][mt][m][1] = bload16w(mt == 0 ? rq0 : rq1, rqo + off1[m]);
             st.m[u][mt][m] = S::load_meta(mt == 0 ? rm0 : rm1, rmo + moff[m]);
           }
         }
@@ -260,7 +328,7 @@ struct RowGroup {
       const __amdgpu_buffer_rsrc_t xr = make_rsrc_u(xrow, tv ? (uint32_t)v.cols * 4u : 0u);
 #pragma unroll
       for (int m = 0; m < SPL; ++m) {
-        const int j = li + m * L;
+        const int j = seg0 + li + m * L;
         const bool jv = j < v.nseg;
 #pragma unroll
         for (int e = 0; e < EPS; e += 4) {
@@ -309,7 +377,7 @@ struct RowGroup {
   __device__ __forceinline__ void coop_issue(float (&xq)[NT][XQ], const float *xbase, int xstride,
                                              const SlotView &v, int t0, RowOf row_of,
                                              int tid) const {
-    const int sgm = tid >> 2, q = tid & 3;
+    const int sgm = seg0 + (tid >> 2), q = tid & 3;
     const bool jv = sgm < v.nseg;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -354,8 +422,8 @@ struct RowGroup {
       for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
         for (int m = 0; m < SPL; ++m) {
-          S::template dot<NT>(st.q[u][mt][m][0], st.q[u][mt][m][1], st.m[u][mt][m], li + m * L,
-                              xv[m], run, acc[u][mt]);
+          S::template dot<NT>(st.q[u][mt][m][0], st.q[u][mt][m][1], st.m[u][mt][m],
+                              seg0 + li + m * L, xv[m], run, acc[u][mt]);
           // keep each segment's decode local: without this the scheduler
           // hoists the work of the whole stage and runs out of registers
           __builtin_amdgcn_sched_barrier(0);
@@ -425,6 +493,52 @@ __device__ __forceinline__ void fused_route(const GemvArgs &a, int lane, int32_t
   }
 }
 
+// Partial sums the fused combine exchanges between workgroups go past the
+// per-XCD L2 caches: system-scope relaxed stores and loads are written
+// through to memory and read from it, so the arrival counter needs no cache
+// write-back or invalidate (an agent-scope fence writes back the whole L2).
+__device__ __forceinline__ void store_through(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ float load_through(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// The combine of one row block of the per-slot down pass: final_out[t][r] =
+// (residual +) sum over t's routes, in route order, of w * y[pair][r] (+ the
+// shared expert's y), y being the sum of the pair's nks K-slice partials in
+// slice order -- the arithmetic of k_combine.  nks = 0: no partials (no
+// routes, no shared expert).
+__device__ __forceinline__ void combine_rows(const GemvArgs &a, int nks, int tid) {
+  const int H = a.out_stride;
+  // the row block's rows: those of its row groups, interleaved or contiguous
+  const int nr = a.combine_rows_per_block;
+  const int gw = a.groups_per_wg;
+  const int T = a.T, k = a.k;
+  for (int i = tid; i < nr * T; i += 256) {
+    const int t = i / nr, idx = i - t * nr;
+    const int r = a.row_interleave
+                      ? blockIdx.x * gw + idx % gw + (idx / gw) * (int)gridDim.x * gw
+                      : blockIdx.x * nr + idx;
+    if (r >= H) continue;
+    auto y = [&](int p) {
+      const float *yp = a.out + (size_t)p * H + r;
+      float s = load_through(yp);
+      for (int q = 1; q < nks; ++q) s += load_through(yp + (size_t)q * a.kslice_stride);
+      return s;
+    };
+    const int n = nks ? a.rcnt[t] : 0;
+    float acc = 0.0f;
+    for (int j = 0; j < n; ++j) {
+      const size_t rj = (size_t)t * k + j;
+      acc = acc + __fmul_rn(a.rw[rj], y(a.inv[rj]));
+    }
+    if (nks && a.has_shared) acc = acc + y(T * k + t);
+    const size_t o = (size_t)t * H + r;
+    a.final_out[o] = a.residual ? a.residual[o] + acc : acc;
+  }
+}
+
 // PLAIN: one matrix (the down projection of one slot per grid.y), no
 // SwiGLU; activations are per pair (row pair0 + t of x) and each row's dot
 // product goes to out[pair][row] for the combine kernel.
@@ -432,11 +546,16 @@ template <int FMT, int LPR, int KSPLIT, int SPL, int NT, bool PLAIN = false>
 __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   constexpr int L = LPR * KSPLIT;
   constexpr int GROUPS = 256 / L;
-  constexpr int U = 2;  // rows per pipeline stage
-  constexpr int S = 2;  // stages (S - 1 of them in flight while one is decoded)
   constexpr int NMAT = PLAIN ? 1 : 2;
+  // rows per pipeline stage: one matrix leaves the registers for twice the rows
+  constexpr int U = PLAIN && SPL == 1 && L == 64 ? NX_GEMV_PLAIN_ROWS : 2;
+  // stages (S - 1 of them in flight while one is decoded)
+  constexpr int S = PLAIN ? NX_GEMV_PLAIN_STAGES : (NT == 1 && SPL == 1 ? NX_GEMV_GATEUP_STAGES : 2);
   using RG = RowGroup<FMT, L, SPL, NT, U, NMAT>;
   const int tid = threadIdx.x, lane = tid & 63;
+  if (!PLAIN && a.zero_cnt && blockIdx.x == 0 && blockIdx.y == 0)
+    for (int i = tid; i < a.n_zero; i += 256)
+      __hip_atomic_store(a.zero_cnt + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   // wave index, known to the compiler as wave-uniform
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // row group of this thread; with KSPLIT > 1, waves grp KSPLIT ..
@@ -447,8 +566,12 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32 && FMT != NX_FMT_F16 &&
                         FMT != NX_FMT_BF16;
   __shared__ uint4 xsh[COOP ? NT * 64 * RG::XW : 1];
+  // K slice of this workgroup (PLAIN with kslices > 1; else whole rows)
+  const int kslices = PLAIN ? a.kslices : 1;
+  const int slot = PLAIN ? (int)blockIdx.y / kslices : (int)blockIdx.y;
+  const int kslice = PLAIN ? (int)blockIdx.y - slot * kslices : 0;
   RG g;
-  g.init(KSPLIT == 1 ? (lane % LPR) : tid % L);
+  g.init(KSPLIT == 1 ? (lane % LPR) : tid % L, kslice * L * SPL);
   float xq[NT][RG::XQ];  // activation quarters in flight (COOP)
   bool x_issued = false;  // set only by the in-kernel routing (NT == 1)
 
@@ -487,8 +610,15 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
     n_active = a.active ? a.active[a.E] : 1;
   }
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
-  const int slot = blockIdx.y;
+  const bool fused = PLAIN && a.combine_cnt != nullptr;
+  if (fused && n_slots == 0) {
+    // no token has a route or a shared expert: the output is the residual
+    // (or zero); the first workgroup of each row block writes it
+    if (blockIdx.y == 0) combine_rows(a, 0, tid);
+    return;
+  }
   if (slot >= n_slots) return;  // workgroup-uniform
+  float *const out = a.out + (size_t)kslice * a.kslice_stride;
   // KSPLIT > 1: per-wave partial sums of up to RED_ROWS rows, summed across
   // the group's waves once per RED_ROWS rows (two barriers), not per stage
   constexpr int RED_ROWS = 32;
@@ -496,17 +626,25 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   __shared__ float red[KSPLIT > 1 ? 4 * RED_ROWS * NMAT * NT : 1];
 
   const SlotView v = slot_view(a, slot, n_active, active, offsets);
-  const int row_begin = (blockIdx.x * GROUPS + grp) * a.rows_per_group;
-  const int row_end = min(v.rows, row_begin + a.rows_per_group);
+  // this group's logical rows 0 .. nq-1: interleaved over the slot's row
+  // groups (row = group + q * groups) or one contiguous run
+  const int gidx = blockIdx.x * GROUPS + grp;
+  const int ngroups = gridDim.x * GROUPS;
+  const RowMap rm = a.row_interleave
+                        ? RowMap{gidx, ngroups, v.rows}
+                        : RowMap{gidx * a.rows_per_group, 1,
+                                 min(v.rows, gidx * a.rows_per_group + a.rows_per_group)};
+  const int nq = a.row_interleave ? (v.rows > gidx ? (v.rows - gidx + ngroups - 1) / ngroups : 0)
+                                  : max(0, rm.end - rm.base);
   auto row_of = [&](int t) {
     return PLAIN ? v.pair0 + t : (v.routed ? perm_token[v.pair0 + t] : t);
   };
 
   // with KSPLIT > 1 finish has barriers, so the stage sequence must be
-  // workgroup-uniform: one row group per workgroup runs to row_end; with
-  // several, every group runs rows_per_group rows (rows past row_end load as
+  // workgroup-uniform: one row group per workgroup runs its nq rows; with
+  // several, every group runs rows_per_group rows (rows past the end load as
   // zeros and are not written)
-  const int row_lim = (KSPLIT > 1 && GROUPS > 1) ? row_begin + a.rows_per_group : row_end;
+  const int qlim = (KSPLIT > 1 && GROUPS > 1) ? a.rows_per_group : nq;
 
   typename RG::Stage st[S];
   for (int t0 = 0; t0 < v.count; t0 += NT) {
@@ -514,22 +652,22 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
       if (!x_issued) g.coop_issue(xq, a.x, a.x_stride, v, t0, row_of, tid);
       x_issued = false;
 #pragma unroll
-      for (int i = 0; i < S - 1; ++i) g.load(st[i], v, row_begin + i * U, row_end);
+      for (int i = 0; i < S - 1; ++i) g.load(st[i], v, rm, i * U);
       g.coop_finish(xq, xsh, tid);
     } else {
       // the weight stages do not depend on the activations: issue them first
 #pragma unroll
-      for (int i = 0; i < S - 1; ++i) g.load(st[i], v, row_begin + i * U, row_end);
+      for (int i = 0; i < S - 1; ++i) g.load(st[i], v, rm, i * U);
       g.load_x(a.x, a.x_stride, v, t0, row_of);
     }
 
-    auto finish = [&](const typename RG::Stage &st, int r0) {
+    auto finish = [&](const typename RG::Stage &st, int q0) {
       float acc[U][NMAT][NT];
       g.template compute<LPR>(st, acc);
       const bool writer = (g.li % LPR) == LPR - 1;
       if constexpr (KSPLIT > 1) {
-        // the wave's partials of rows r0 .. r0 + U - 1 (lane 63 holds them)
-        const int sr = (r0 - row_begin) % RED_ROWS;
+        // the wave's partials of rows q0 .. q0 + U - 1 (lane 63 holds them)
+        const int sr = q0 % RED_ROWS;
         if (lane == 63) {
 #pragma unroll
           for (int u = 0; u < U; ++u)
@@ -541,13 +679,13 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
         }
         // a full run of partials, or the group's last stage (both
         // workgroup-uniform: every group runs the same stage sequence)
-        if (sr + U == RED_ROWS || r0 + U >= row_lim) {
+        if (sr + U == RED_ROWS || q0 + U >= qlim) {
           __syncthreads();
-          const int rb = r0 + U - (sr + U);  // first row of the run
+          const int qb = q0 + U - (sr + U);  // first row of the run
           for (int i = tid % L; i < (sr + U) * NT; i += L) {
             const int rl = i / NT, t = i - rl * NT;
-            const int r = rb + rl;
-            if (r >= row_end || t0 + t >= v.count) continue;
+            if (!rm.valid(qb + rl) || t0 + t >= v.count) continue;
+            const int r = rm.row(qb + rl);
             float sm[NMAT];
 #pragma unroll
             for (int mt = 0; mt < NMAT; ++mt) {
@@ -557,7 +695,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
                 s += red[(((grp * KSPLIT + w) * RED_ROWS + rl) * NMAT + mt) * NT + t];
               sm[mt] = s;
             }
-            a.out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
+            out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
                 PLAIN ? sm[0] : silu_mul(sm[0], sm[NMAT - 1]);
           }
           __syncthreads();
@@ -567,30 +705,48 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
       if (writer) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int r = r0 + u;
-          if (r >= row_end) continue;
+          if (!rm.valid(q0 + u)) continue;
+          const int r = rm.row(q0 + u);
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
             if (t0 + t >= v.count) continue;
-            if constexpr (PLAIN)
-              a.out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] = acc[u][0][t];
+            if constexpr (PLAIN) {
+              float *o = &out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r];
+              if (fused)
+                store_through(o, acc[u][0][t]);
+              else
+                *o = acc[u][0][t];
+            }
             else
-              a.out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
+              out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
                   silu_mul(acc[u][0][t], acc[u][NMAT - 1][t]);
           }
         }
       }
     };
 
-    for (int r = row_begin; r < row_lim; r += S * U) {
+    for (int q = 0; q < qlim; q += S * U) {
 #pragma unroll
       for (int i = 0; i < S; ++i) {
-        const int rr = r + i * U;
-        if (rr >= row_lim) break;
-        g.load(st[(i + S - 1) % S], v, rr + (S - 1) * U, row_end);
-        finish(st[i], rr);
+        const int qq = q + i * U;
+        if (qq >= qlim) break;
+        g.load(st[(i + S - 1) % S], v, rm, qq + (S - 1) * U);
+        finish(st[i], qq);
       }
     }
+  }
+  if (fused) {
+    // every wave's written-through partial sums have reached memory (the
+    // wait covers stores on gfx9) before the workgroup counts in; the last
+    // of the n_slots * kslices arrivals reads them all back from memory
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int s_last;
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(&a.combine_cnt[blockIdx.x], 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_SYSTEM) == n_slots * kslices - 1;
+    __syncthreads();
+    if (s_last) combine_rows(a, kslices, tid);
   }
 }
 
@@ -918,9 +1074,17 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   }
 
   const int nseg = a.nseg > a.snseg ? a.nseg : a.snseg;
+  // Down rows longer than one wave's 64 segments (Mixtral's 14336 columns:
+  // 224 segments) are cut into K slices of 64 segments, the code plane's
+  // layout groups: one wave per (row, slice), each workgroup on one (slot,
+  // slice) so it prepares only that slice's activations, and the combine
+  // adds the slices' partial sums in slice order.
+  const bool down_split = NX_GEMV_DOWN_SPLIT && !gateup && nseg > 64;
+  const int kslices = down_split ? (nseg + 63) / 64 : 1;
+  a.kslices = kslices;
   int nt;
   Shape sh;
-  if (!choose_tokens_shape(nseg, elems_per_segment(ex->fmt), p.T, &nt, &sh))
+  if (!choose_tokens_shape(down_split ? 64 : nseg, elems_per_segment(ex->fmt), p.T, &nt, &sh))
     return fail(NX_ERR_UNSUPPORTED, "row length too large for the register-resident GEMV");
   const int L = sh.lpr * sh.ksplit;
   const int groups_per_wg = 256 / L;
@@ -928,9 +1092,10 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const int rows = a.rows > a.srows ? a.rows : a.srows;
   // The down pass combines its rows inside the workgroup when there are at
   // most two slots (one token's top-2: the halves of the workgroup run them
-  // side by side); beyond that the slots go to grid.y like gate/up, each
-  // writing its rows per pair, and the combine runs as its own kernel.
-  const bool down_rows = !gateup && slots_max_of(ex, p) > DOWN_SG;
+  // side by side); beyond that, and for K slices, the slots go to grid.y like
+  // gate/up, each writing its rows per pair, and the combine runs as its own
+  // kernel.
+  const bool down_rows = !gateup && (down_split || slots_max_of(ex, p) > DOWN_SG);
   const int kind = gateup ? KIND_GATEUP : (down_rows ? KIND_DOWN_ROWS : KIND_DOWN_COMBINE);
   const bool per_slot = gateup || down_rows;
   // residency is register-bound (eight waves per CU by launch bounds)
@@ -947,27 +1112,58 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   // gate/up spreads slots over grid.y; down runs all slots inside each
   // workgroup.  Size the row runs so the launch is one round of resident
   // workgroups with equal work each.
-  const long work_rows = per_slot ? (long)rows * slots_max : (long)rows;
+  const long work_rows = per_slot ? (long)rows * slots_max * kslices : (long)rows;
   const long groups = (long)c->num_cu * wg_per_cu * groups_per_wg;
   long rpg = (work_rows + groups - 1) / groups;
   if (rpg < 1) rpg = 1;
   a.rows_per_group = (int)rpg;
+  a.row_interleave = NX_GEMV_INTERLEAVE;
+  a.groups_per_wg = groups_per_wg;
   const long rows_per_wg = rpg * groups_per_wg;
   const unsigned gx = (unsigned)((rows + rows_per_wg - 1) / rows_per_wg);
 
   if (gateup) {
+    // the counters of the down pass's fused combine start at zero
+    void *cnt = nullptr;
+    NX_TRY(ws_get(c, WS_DOWN_CNT, (size_t)ex->H * sizeof(int), &cnt));
+    a.zero_cnt = static_cast<int *>(cnt);
+    a.n_zero = ex->H;
     const dim3 grid(gx, (unsigned)slots_max);
     return launch(c, "gemv_gateup",
                   [&] { hipLaunchKernelGGL(probe, grid, dim3(256), 0, c->stream, a); });
   }
   if (down_rows) {
-    a.out = p.ypair;
+    const size_t pairs_total = (size_t)p.T * p.k + (has_shared ? (size_t)p.T : 0);
+    float *ypair = p.ypair;
+    if (kslices > 1) {
+      void *yp = nullptr;
+      NX_TRY(ws_get(c, WS_YPAIR, (size_t)kslices * pairs_total * ex->H * sizeof(float), &yp));
+      ypair = static_cast<float *>(yp);
+    }
+    a.out = ypair;
     a.out_stride = ex->H;
-    const dim3 grid(gx, (unsigned)slots_max);
-    NX_TRY(launch(c, "gemv_down",
+    a.kslice_stride = pairs_total * ex->H;
+    const dim3 grid(gx, (unsigned)(slots_max * kslices));
+    // Few outputs per row block (decode): the block's last workgroup
+    // combines them, with no combine launch.  Otherwise the combine kernel
+    // spreads them over the GPU.
+    const bool fuse = NX_GEMV_FUSE_COMBINE && (long)p.T * rows_per_wg <= 2048;
+    if (fuse) {
+      void *cnt = nullptr;
+      NX_TRY(ws_get(c, WS_DOWN_CNT, (size_t)ex->H * sizeof(int), &cnt));
+      a.combine_cnt = static_cast<int *>(cnt);
+      a.combine_rows_per_block = (int)rows_per_wg;
+      a.rw = p.rw;
+      a.rcnt = p.rcnt;
+      a.inv = p.inv;
+      a.final_out = p.out;
+      a.residual = p.residual;
+    }
+    NX_TRY(launch(c, fuse ? "gemv_down_combine" : "gemv_down",
                   [&] { hipLaunchKernelGGL(probe, grid, dim3(256), 0, c->stream, a); }));
-    return launch_combine(c, p.ypair, p.rw, p.rcnt, p.inv, p.T, p.k, ex->H, has_shared, p.out, 1, 0,
-                          p.residual);
+    if (fuse) return NX_OK;
+    return launch_combine(c, ypair, p.rw, p.rcnt, p.inv, p.T, p.k, ex->H, has_shared, p.out,
+                          kslices, a.kslice_stride, p.residual);
   }
 
   a.rw = p.rw;
@@ -993,6 +1189,7 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
 // One matrix over T tokens: the per-slot kernel with a single dense slot.
 int run_gemv_matrix(nx_ctx *c, int fmt, const RolePlane &pl, const float *x, int T, float *out) {
   GemvArgs a{};
+  a.kslices = 1;
   a.qs0 = a.qs1 = pl.qs;
   a.meta0 = a.meta1 = pl.meta;
   a.qs_stride = pl.qs_stride;
@@ -1027,6 +1224,8 @@ int run_gemv_matrix(nx_ctx *c, int fmt, const RolePlane &pl, const float *x, int
   long rpg = (pl.rows + groups - 1) / groups;
   if (rpg < 1) rpg = 1;
   a.rows_per_group = (int)rpg;
+  a.row_interleave = NX_GEMV_INTERLEAVE;
+  a.groups_per_wg = groups_per_wg;
   const long rows_per_wg = rpg * groups_per_wg;
   const unsigned gx = (unsigned)((pl.rows + rows_per_wg - 1) / rows_per_wg);
   return launch(c, "gemv_matrix",

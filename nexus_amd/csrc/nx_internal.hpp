@@ -153,6 +153,7 @@ enum WsSlot {
   WS_MAT_X,    // device copy of matvec inputs for blocking calls
   WS_MAT_Y,
   WS_MFV_PART, // gate/up partial sums of the split-activation MFMA path
+  WS_DOWN_CNT, // arrival counters of the decode down pass's fused combine
 };
 
 int ws_get(nx_ctx *c, int slot, size_t bytes, void **out);
