@@ -135,16 +135,64 @@ def cpu_baseline(nx, ctx, torch, x, logits, E, H, F, k, seed, ntok):
             oracle.swiglu_ffn(xs_h[t], mats[1][e], mats[0][e], mats[2][e], H, F)
     dts = time.perf_counter() - t2
     ncores = oracle.default_threads()  # the box's CPU share for one GPU
+    # one-token decode in CpuBackend::matmul's pattern (src/backend/cpu.rs:23-38):
+    # each product of each routed expert as C[rows x 1] = W[rows x cols] . x,
+    # its rows split over every core, token by token
+    ex_w = oracle.route(lg_h, ntok, E, k)[1]
+    t4 = time.perf_counter()
+    for t in range(ntok):
+        out = np.zeros(H, np.float32)
+        for r in range(int(cnt[t])):
+            e = int(ex_ids[t, r])
+            gv = oracle.cpu_matmul(mats[0][e], xs_h[t], F, 1, H, nthreads=ncores)
+            uv = oracle.cpu_matmul(mats[1][e], xs_h[t], F, 1, H, nthreads=ncores)
+            act = (gv / (np.float32(1.0) + np.exp(-gv))) * uv
+            yv = oracle.cpu_matmul(mats[2][e], act, H, 1, F, nthreads=ncores)
+            out += np.float32(ex_w[t, r]) * yv
+    dtd = time.perf_counter() - t4
+    # the whole sample at once, its tokens spread over every core
     t3 = time.perf_counter()
     oracle.moe_layer(xs_h, lg_h, mats[0], mats[1], mats[2], k, nthreads=ncores)
     dtp = time.perf_counter() - t3
     return {"value": ntok / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
             "router_matvec_us_per_token": dtr / ntok * 1e6,
             "swiglu_ffn_1core_tokens_per_s": ntok / dts,
-            "row_parallel_tokens_per_s": ntok / dtp, "row_parallel_cores": ncores,
+            "row_parallel_decode_tokens_per_s": ntok / dtd, "row_parallel_cores": ncores,
+            "token_parallel_tokens_per_s": ntok / dtp, "token_parallel_cores": ncores,
+            "host": host_info(),
             "sample": f"{ntok} tokens of the same Mixtral Q4_K layer through the oracle's "
                       f"single-threaded dispatch_moe_ffn (f32 weights dequantized from the "
-                      f"Q4_K payloads outside the timed region), {dt:.1f} s"}
+                      f"Q4_K payloads outside the timed region), {dt:.1f} s; the row-parallel "
+                      f"decode runs the same tokens one by one, {dtd:.2f} s"}
+
+
+def host_info():
+    """CPU model, logical CPUs and the oracle's compiler and flags."""
+    import platform
+    import subprocess
+
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cflags = ""
+    try:
+        with open(os.path.join(ROOT, "oracle", "Makefile")) as f:
+            for line in f:
+                if line.startswith("CFLAGS"):
+                    cflags = line.split("=", 1)[1].strip()
+    except OSError:
+        pass
+    try:
+        cc = subprocess.run(["gcc", "--version"], capture_output=True, text=True).stdout.split("\n")[0]
+    except OSError:
+        cc = "gcc"
+    return {"cpu_model": model, "nproc": os.cpu_count(), "compiler": cc, "cflags": cflags}
 
 
 def time_steps(torch, fn, steps, warmup):
@@ -156,6 +204,24 @@ def time_steps(torch, fn, steps, warmup):
         fn(i)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def step_distribution(torch, fn, n=200):
+    """Per-step device time over n steps (a HIP event pair around each, on
+    the stream the steps run on): median, 10th and 90th percentile, in ms."""
+    import numpy as np
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n)]
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(ev):
+        a.record()
+        fn(i)
+        b.record()
+    torch.cuda.synchronize()
+    ms = np.array([a.elapsed_time(b) for a, b in ev])
+    return {"iterations": n, "median_ms": float(np.median(ms)), "p10_ms": float(np.percentile(ms, 10)),
+            "p90_ms": float(np.percentile(ms, 90)), "mean_ms": float(ms.mean())}
 
 
 def path_of(kern):
@@ -456,10 +522,12 @@ def main():
 
         ms = time_steps(torch, step, args.steps, args.warmup)
         kern = kernel_means(ctx, torch, step, args.steps)
-        return ms, kern, gu_bytes, dn_bytes
+        return ms, kern, gu_bytes, dn_bytes, step
 
     print("bench: decode", file=sys.stderr, flush=True)
-    ms_per_step, kern, gateup_bytes, down_bytes = decode_case(T, path)
+    ms_per_step, kern, gateup_bytes, down_bytes, decode_step = decode_case(T, path)
+    # after the timed region: the per-step distribution over >= 100 steps
+    dist = step_distribution(torch, decode_step, max(200, args.steps))
     step_bytes = gateup_bytes + down_bytes
     print("bench: per-kernel mean ms " + json.dumps({k_: round(v, 5) for k_, v in kern.items()}),
           file=sys.stderr, flush=True)
@@ -475,7 +543,7 @@ def main():
     extra = {}
     if not args.no_extra:
         print("bench: decode, 32 tokens", file=sys.stderr, flush=True)
-        ms32, kern32, gu32, dn32 = decode_case(32, nx.PATH_AUTO)
+        ms32, kern32, gu32, dn32, _ = decode_case(32, nx.PATH_AUTO)
         extra["decode_32_tokens"] = {
             "ms_per_step": ms32, "tokens_per_s": 32 / (ms32 * 1e-3),
             "effective_GBps": (gu32 + dn32) / (ms32 * 1e-3) / 1e9, "path": "auto: " + path_of(kern32),
@@ -528,6 +596,7 @@ def main():
         "effective_GBps": step_bytes / (ms_per_step * 1e-3) / 1e9,
         "layer_hbm_frac": step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS,
         "kernels_ms": {k_: round(v, 5) for k_, v in kern.items()},
+        "step_time_stats": dist,
         "roofline": {"bound": "hbm", "kernel": gu_name, "achieved": achieved,
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS if achieved else None,

@@ -14,7 +14,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libnexus_hip.so")
+# NEXUS_AMD_LIB points at another build of the same library (for example the
+# host-sanitizer build, nexus_amd/csrc: make san)
+LIB_PATH = os.environ.get("NEXUS_AMD_LIB") or os.path.join(_HERE, "libnexus_hip.so")
 ROOT = os.path.dirname(_HERE)
 
 # status codes / enums (include/nexus_hip.h)

@@ -921,6 +921,9 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
       return fail(NX_ERR_UNSUPPORTED, std::string(fmt_name(ex->fmt)) + " experts run on the GEMV path only");
     use = NX_PATH_GEMV;
   }
+  // AUTO takes bf16 operands on the grouped GEMM: fp16's range ends at
+  // 65504, which SwiGLU activations of real models can pass; bf16 keeps
+  // float32's range, runs as fast here, and stays within the MFMA bar.
   if (use == NX_PATH_AUTO) {
     const long active_max = std::min<long>(E, (long)T * k);
     if (ex->fmt == NX_FMT_Q4_K && !shared) {
@@ -934,7 +937,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
       const double act = std::max(1.0, E * (1.0 - std::pow(1.0 - kk, (double)T)));
       const double tpe = (double)T * k / act;
       if (tpe >= 24.0)
-        use = NX_PATH_MFMA_F16;
+        use = NX_PATH_MFMA_BF16;
       else if (tpe >= 3.0 || ((long)T * k >= 64 && tpe >= 1.2))
         use = NX_PATH_MFMA_SPLIT;
       else
@@ -942,7 +945,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
     } else {
       // MFMA once experts see enough tokens on average to amortize the tile
       // dequantization; below that the GEMV streams each weight fewer times
-      use = ((long)T * k >= 32 * active_max) ? NX_PATH_MFMA_F16 : NX_PATH_GEMV;
+      use = ((long)T * k >= 32 * active_max) ? NX_PATH_MFMA_BF16 : NX_PATH_GEMV;
     }
   }
 

@@ -298,8 +298,9 @@ __device__ __forceinline__ float y_at(const float *__restrict__ y, size_t stride
 
 // out[t] = sum_r w[t,r] * y[pair(t,r)] (+ shared) in route order
 // (src/engine/mod.rs:1017-1021).  The routes' pair indices and weights are
-// read RB at a time (clamped to the last route), then their y values, so
-// the loads of a token's routes overlap.
+// read RB at a time (clamped to the last slot, k - 1) together with the
+// route count, then their y values, so a token's loads take two dependent
+// rounds and the routes' loads overlap.
 template <int NS, int RB>
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair,
                                                  const float *__restrict__ rw,
@@ -311,20 +312,22 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
     const int t = (int)(i / H), h = (int)(i - (size_t)t * H);
-    const int n = rcnt[t];
     const float sh = shared ? y_at<NS>(ypair, stride, ns, ((size_t)T * k + t) * H + h) : 0.f;
     float acc = 0.0f;
+    int n = k;  // the route count arrives with the first batch of routes
     for (int r0 = 0; r0 < n; r0 += RB) {
       int p[RB];
       float w[RB], yv[RB];
+      if (r0 == 0) n = rcnt[t];
 #pragma unroll
       for (int j = 0; j < RB; ++j) {
-        const size_t r = (size_t)t * k + min(r0 + j, n - 1);
+        const size_t r = (size_t)t * k + min(r0 + j, k - 1);
         p[j] = inv[r];
         w[j] = rw[r];
       }
 #pragma unroll
-      for (int j = 0; j < RB; ++j) yv[j] = y_at<NS>(ypair, stride, ns, (size_t)p[j] * H + h);
+      for (int j = 0; j < RB; ++j)
+        yv[j] = r0 + j < n ? y_at<NS>(ypair, stride, ns, (size_t)p[j] * H + h) : 0.f;
 #pragma unroll
       for (int j = 0; j < RB; ++j)
         if (r0 + j < n) acc = acc + __fmul_rn(w[j], yv[j]);

@@ -16,7 +16,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# NEXUS_ORACLE_LIB points at another build (the sanitizer build,
+# oracle/Makefile: liboracle_san.so)
+_LIB_PATH = os.environ.get("NEXUS_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 F32, Q4_0, Q8_0, Q4_K, Q2_K, F16, BF16 = 0, 2, 8, 12, 10, 1, 28

@@ -319,3 +319,42 @@ def test_q4k_ggml_order_conversion():
     got = oracle.dequantize(oracle.Q4_K, conv, 4 * 256)
     want = ggml_q4k_dequant(src)
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_corrupt_files_error_or_parse(tmp_path, seed):
+    """A valid MoE file, truncated at random lengths or with random bytes
+    changed in its header, metadata and tensor table: every open, lookup and
+    payload access either works or raises NexusError -- never reads outside
+    the mapping (the CPU suite also runs under the host-sanitizer build)."""
+    rng = np.random.default_rng(seed)
+    w, _, _ = moe_file(oracle.Q8_0, 2, 64, 96, naming="gguf", shared_F=32)
+    good = w.tobytes()
+    head = len(good) - sum(len(t[3]) for t in w.tensors)  # header, metadata, tensor table
+    for case in range(60):
+        data = bytearray(good)
+        if case % 3 == 0:
+            data = data[: int(rng.integers(0, len(good)))]
+        else:
+            for _ in range(int(rng.integers(1, 6))):
+                i = int(rng.integers(0, head))
+                data[i] = int(rng.integers(0, 256))
+        p = tmp_path / f"c{case}.gguf"
+        p.write_bytes(bytes(data))
+        try:
+            g = nx.Gguf(str(p))
+        except nx.NexusError:
+            continue
+        try:
+            for t in g.tensors():
+                try:
+                    g.data(g.find(t["name"]))
+                except nx.NexusError:
+                    pass
+            for layer in (0, 1):
+                try:
+                    g.moe_info(layer)
+                except nx.NexusError:
+                    pass
+        finally:
+            g.close()

@@ -241,6 +241,34 @@ def test_layer_mfma_shared_expert_sigmoid(ctx):
     assert rel_l2(run_layer(ctx, L, nx.PATH_MFMA_F16), L.oracle_out()) <= MFMA_TOL
 
 
+@pytest.mark.parametrize("fmt", [Q8_0, Q4_K])
+def test_auto_mfma_keeps_float_range(ctx, fmt):
+    """Activations near 1e3 give SwiGLU outputs near 1e5, past fp16's 65504:
+    the grouped GEMM that AUTO picks (bf16 operands) stays within the MFMA
+    bar of the oracle."""
+    L = Layer(fmt, 8, 512, 512, 2, 256, seed=31)
+    L.x = (L.x * np.float32(1000.0)).astype(np.float32)
+    ref = L.oracle_out()
+    act_max = 0.0
+    for e in L.routed[:2]:
+        g = L.dense[(e, 0)].reshape(512, 512) @ L.x[0].astype(np.float64)
+        u = L.dense[(e, 1)].reshape(512, 512) @ L.x[0].astype(np.float64)
+        with np.errstate(over="ignore"):  # exp(-g) for g << 0: silu -> -0
+            act_max = max(act_max, float(np.max(np.abs(g / (1 + np.exp(-g)) * u))))
+    say(f"auto mfma range fmt={fmt}: max |act| of token 0 = {act_max:.3g}")
+    assert act_max > 65504.0  # the inputs do leave fp16's range
+    ex = L.upload(nx, ctx)
+    ctx.profile(True)
+    ctx.profile_reset()
+    out = ex.forward(L.x, L.logits, L.k, path=nx.PATH_AUTO)
+    stats = ctx.profile_stats()
+    ctx.profile(False)
+    ex.close()
+    assert "gemm_gateup" in stats
+    assert np.isfinite(out).all()
+    assert rel_l2(out, ref) <= MFMA_TOL
+
+
 def test_auto_path_picks_mfma_for_prefill(ctx):
     L = Layer(Q8_0, 8, 512, 512, 2, 256, seed=8)
     ex = L.upload(nx, ctx)
