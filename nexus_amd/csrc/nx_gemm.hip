@@ -280,6 +280,28 @@ __device__ __forceinline__ void fetch_meta(WMeta<FMT, NT> &m, __amdgpu_buffer_rs
   }
 }
 
+// byte N of x as a float (v_cvt_f32_ubyteN).  The compiler forms only
+// ubyte0 from a shift and mask; the others are written out, so that one
+// masked word feeds four conversions without a shift each.
+template <int N>
+__device__ __forceinline__ float ubyte_f32(uint32_t x) {
+  float r;
+  if constexpr (N == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (N == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x));
+  else if constexpr (N == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
+// bf16(a) in the low half, bf16(b) in the high half, each rounded to
+// nearest even (v_cvt_pk_bf16_f32, the conversion the compiler emits for a
+// float -> __bf16 cast)
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // values 8M .. 8M+7 of the 16 of row n at step S of the window, as a B operand
 template <int FMT, bool BF16, int S, int M, typename WC, typename WM>
 __device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WC &w, const WM &mt, int n) {
@@ -312,35 +334,43 @@ __device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WC &w, const W
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           v[4 * k + i] = (float)(int32_t)(int8_t)((ws[k] >> (8 * i)) & 0xFFu) * d;
-    } else if constexpr (FMT == NX_FMT_Q4_K) {
-      // sub-block t + 4p of the block; src/quant/mod.rs:841: d * sc * q - dmin * m
+    } else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) {
+      // value = A q + B for the nibble q = 0..15 of the sub-block:
+      // Q4_K (src/quant/mod.rs:841) d * sc * q - dmin * m, A = d sc and
+      // B = -dmin m; Q4_0 (q - 8) d, A = d and B = -8 d (exact, so the fma
+      // rounds (q - 8) d once)
       constexpr int t = S & 3, p = S >> 2;
-      const uint4 Q = mt.m[n];
-      const float d = h2f(Q.x & 0xFFFFu), dmin = h2f(Q.x >> 16);
-      const uint32_t b0 = (Q.y >> (8 * t)) & 0xFFu;
-      const uint32_t b4 = (Q.z >> (8 * t)) & 0xFFu;
-      const uint32_t b8 = (Q.w >> (8 * t)) & 0xFFu;
-      const float sc = p ? (float)((b8 & 15u) | ((b0 >> 6) << 4)) : (float)(b0 & 63u);
-      const float mn = p ? (float)((b8 >> 4) | ((b4 >> 6) << 4)) : (float)(b4 & 63u);
-      const uint32_t ws = M ? w.c[n].y : w.c[n].x;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t byte = ((ws >> (8 * i)) & 0xFFu) ^ 0x88u;  // stored nibbles are q ^ 8
-        v[i] = d * sc * (float)(byte & 15u) - dmin * mn;
-        v[4 + i] = d * sc * (float)(byte >> 4) - dmin * mn;
+      float A, B;
+      if constexpr (FMT == NX_FMT_Q4_K) {
+        // sub-block t + 4p of the block
+        const uint4 Q = mt.m[n];
+        const float d = h2f(Q.x & 0xFFFFu), dmin = h2f(Q.x >> 16);
+        const uint32_t b0 = (Q.y >> (8 * t)) & 0xFFu;
+        const uint32_t b4 = (Q.z >> (8 * t)) & 0xFFu;
+        const uint32_t b8 = (Q.w >> (8 * t)) & 0xFFu;
+        const float sc = p ? (float)((b8 & 15u) | ((b0 >> 6) << 4)) : (float)(b0 & 63u);
+        const float mn = p ? (float)((b8 >> 4) | ((b4 >> 6) << 4)) : (float)(b4 & 63u);
+        A = d * sc;
+        B = -(dmin * mn);
+      } else {
+        // segment 8u + 4(q/2) + t: dword t of the scales, block half p
+        const uint32_t mw = t == 0 ? mt.m[n].x : (t == 1 ? mt.m[n].y : (t == 2 ? mt.m[n].z : mt.m[n].w));
+        A = h2f((mw >> (16 * p)) & 0xFFFFu);
+        B = -8.0f * A;
       }
-    } else if constexpr (FMT == NX_FMT_Q4_0) {
-      // segment 8u + 4(q/2) + t: dword t of the scales, block half p
-      constexpr int t = S & 3, p = S >> 2;
-      const uint32_t mw = t == 0 ? mt.m[n].x : (t == 1 ? mt.m[n].y : (t == 2 ? mt.m[n].z : mt.m[n].w));
-      const float d = h2f((mw >> (16 * p)) & 0xFFFFu);
-      const uint32_t ws = M ? w.c[n].y : w.c[n].x;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t byte = ((ws >> (8 * i)) & 0xFFu) ^ 0x88u;
-        v[i] = (float)((int)(byte & 15u) - 8) * d;
-        v[4 + i] = (float)((int)(byte >> 4) - 8) * d;
-      }
+      // the eight nibbles at once: stored nibbles are q ^ 8; value i is the
+      // low nibble of byte i, value 4 + i its high nibble (each conversion
+      // reads one byte of a masked word)
+      const uint32_t u = (M ? w.c[n].y : w.c[n].x) ^ 0x88888888u;
+      const uint32_t lo = u & 0x0F0F0F0Fu, hi = (u >> 4) & 0x0F0F0F0Fu;
+      v[0] = __builtin_fmaf(ubyte_f32<0>(lo), A, B);
+      v[1] = __builtin_fmaf(ubyte_f32<1>(lo), A, B);
+      v[2] = __builtin_fmaf(ubyte_f32<2>(lo), A, B);
+      v[3] = __builtin_fmaf(ubyte_f32<3>(lo), A, B);
+      v[4] = __builtin_fmaf(ubyte_f32<0>(hi), A, B);
+      v[5] = __builtin_fmaf(ubyte_f32<1>(hi), A, B);
+      v[6] = __builtin_fmaf(ubyte_f32<2>(hi), A, B);
+      v[7] = __builtin_fmaf(ubyte_f32<3>(hi), A, B);
     } else {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
@@ -351,10 +381,18 @@ __device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WC &w, const W
         v[4 * k + 3] = __uint_as_float(c.w);
       }
     }
-    typename Op::V8 b;
+    if constexpr (BF16) {
+      // pairs packed in operand order (the compiler otherwise pairs
+      // neighbours across the pairs and realigns them)
+      const uint4 u = {pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
+                       pack_bf16(v[6], v[7])};
+      return __builtin_bit_cast(typename Op::V8, u);
+    } else {
+      typename Op::V8 b;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) b[i] = (typename Op::T)v[i];
-    return b;
+      for (int i = 0; i < 8; ++i) b[i] = (typename Op::T)v[i];
+      return b;
+    }
   }
 }
 
@@ -401,18 +439,43 @@ __device__ __forceinline__ void static_for(F &&f) {
 // issued back to back (both halves of the same lines, the second load hits
 // the cache), OCC = workgroups per CU.  Both passes keep 32 rows per wave
 // (NT = 2) and two workgroups per CU; F32 takes one workgroup per CU.
+// Measured on the Qwen3 (E = 128, T = 512) and DeepSeek (E = 256,
+// T = 4096) Q4_K layers and the Mixtral Q8_0 prefill: NT = 1 and NT = 4
+// are slower in both passes, and fetching the codes 3 to 8 steps ahead
+// instead of 2 gains nothing.
+// weight rows per wave (16 NT) per format family and pass
+#ifndef NX_GEMM_NT_Q4
+#define NX_GEMM_NT_Q4 2
+#endif
+#ifndef NX_GEMM_NT_Q4_DOWN
+#define NX_GEMM_NT_Q4_DOWN 2
+#endif
+#ifndef NX_GEMM_NT_Q8
+#define NX_GEMM_NT_Q8 2
+#endif
+__host__ __device__ constexpr int gemm_nt(int fmt, bool gateup) {
+  return (fmt == NX_FMT_Q4_K || fmt == NX_FMT_Q4_0) ? (gateup ? NX_GEMM_NT_Q4 : NX_GEMM_NT_Q4_DOWN)
+                                                     : (fmt == NX_FMT_Q8_0 ? NX_GEMM_NT_Q8 : 2);
+}
+// steps the codes are fetched ahead, and whether the scales of the 4-bit
+// formats are double-buffered (fetched with the codes of a window's first
+// step) rather than reloaded after a window's last decode
+#ifndef NX_GEMM_WDIST_Q4
+#define NX_GEMM_WDIST_Q4 WDIST_CFG
+#endif
+#ifndef NX_GEMM_META2_Q4
+#define NX_GEMM_META2_Q4 0
+#endif
 template <int FMT, bool GATEUP>
 struct GemmShape {
-  static constexpr int NT = 2;
+  static constexpr int NT = gemm_nt(FMT, GATEUP);
+  static constexpr bool Q4 = FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0;
   static constexpr bool PAIR = false;
-  static constexpr int WDIST = WDIST_CFG;  // steps the codes are fetched ahead
+  static constexpr int WDIST = Q4 ? NX_GEMM_WDIST_Q4 : WDIST_CFG;
+  static constexpr bool META2 = FMT == NX_FMT_Q8_0 || (Q4 && NX_GEMM_META2_Q4);
   static constexpr int OCC = (NT == 4 || FMT == NX_FMT_F32) ? 1 : 2;
 };
-int gemm_bn(int fmt, bool gateup) {
-  (void)fmt;
-  (void)gateup;
-  return 128;
-}
+int gemm_bn(int fmt, bool gateup) { return 64 * gemm_nt(fmt, gateup); }
 
 // Load schedule of the K loop (body positions; it repeats every body).
 // Step t issues, in this order: at its start the activation stage
@@ -429,16 +492,18 @@ struct LoadSchedule {
   constexpr int outstanding(int P) const {
     const int wstart = P - mod(P, ws);
     int after = 0;
-    for (int t = P - 32; t < P; ++t) {
-      after += na;
+    // loads whose target step or window lies before step 0 are never issued
+    for (int t = P - 40; t < P; ++t) {
+      if (t + ring - 1 >= 0) after += na;
       if (t + ring - 1 == P) after = 0;
-      if (!meta2 && nmw > 0 && mod(t + 1, ws) == 0) {
+      if (!meta2 && nmw > 0 && mod(t + 1, ws) == 0 && t + 1 >= 0) {
         after += nmw;
         if (t + 1 == wstart) after = 0;
       }
       const int nj = pair ? (mod(t, 2) == 0 ? 2 : 0) : 1;
       for (int k = 0; k < nj; ++k) {
         const int j = t + (pair ? 2 : wdist) + k;
+        if (j < 0) continue;
         if (meta2 && nmw > 0 && mod(j, ws) == 0) {
           after += nmw;
           if (j == wstart) after = 0;
@@ -465,11 +530,15 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   // the codes of a window's first step; the 16-byte scales of the 4-bit
   // formats have one buffer, reloaded right after the last decode of a
   // window.
-  constexpr bool META2 = FMT == NX_FMT_Q8_0;
+  constexpr bool META2 = Shape::META2;
   constexpr int NMB = META2 ? 2 : 1;
   constexpr int WDIST = Shape::WDIST;
-  constexpr int NBUF = (PAIR || WDIST > 2) ? 4 : 2;  // code buffers (steps mod NBUF)
+  // code buffers (steps mod NBUF)
+  constexpr int NBUF = PAIR ? 4 : (WDIST <= 2 ? 2 : (WDIST <= 4 ? 4 : 8));
   static_assert(PAIR || WDIST <= NBUF, "code buffers");  // issued after the decode
+  // a window's double-buffered scales are fetched after the last decode of
+  // the window two back
+  static_assert(!META2 || PAIR || WDIST <= win_steps<FMT>() + 1, "scale buffers");
   // steps per loop body: whole rounds of the ring, of the code buffers and
   // of the scale buffers
   constexpr int NB0 = RING > NBUF ? RING : NBUF, NB1 = META2 ? 2 * WS : WS;
@@ -662,6 +731,8 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   // conditional load would make the compiler copy its registers, waiting for
   // all loads in flight).
   const int sw = (l16 >> 1) & 7;
+  // 16-row sets of the tile holding pairs (workgroup-uniform)
+  const int msub = __builtin_amdgcn_readfirstlane((mrows + 15) >> 4);
   auto step = [&](auto pos, int ks0, int wbase) {
     constexpr int P = decltype(pos)::value;
     constexpr int S = P % WS;
@@ -708,13 +779,15 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
 #pragma unroll
       for (int k = 0; k < IG; ++k) af[k] = an[k];
       if constexpr (G2 + 1 < 2 * NG) read_a(IC<G2 + 1>{}, an);
+      if (IG * G < msub) {  // groups of 16-row sets past the tile's last pair are skipped
 #pragma unroll
-      for (int k = 0; k < IG; ++k) {
-        const int i = IG * G + k;
+        for (int k = 0; k < IG; ++k) {
+          const int i = IG * G + k;
 #pragma unroll
-        for (int mt = 0; mt < NMAT; ++mt)
+          for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-          for (int n = 0; n < NT; ++n) acc[mt][n][i] = Op::mfma(af[k], bf[mt][n], acc[mt][n][i]);
+            for (int n = 0; n < NT; ++n) acc[mt][n][i] = Op::mfma(af[k], bf[mt][n], acc[mt][n][i]);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
       constexpr int a0 = G * APG < NA ? G * APG : NA;
@@ -726,35 +799,26 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
     });
   };
 
-  // prologue: the loads of steps -RING+1 .. -1 of the schedule (targets
-  // >= 0), in schedule order
-  static_assert(RING == 4, "prologue written for a 4-stage ring");
+  // prologue: the loads the schedule issues at steps -PRO .. -1 (those
+  // whose target step or window is >= 0), in schedule order: at step t the
+  // activation stage t + RING - 1, then the late loads
   // (ks_begin is a whole number of bodies: ring stages and code buffers
   // keep their step-relative indices, wb0 is its window)
   const int wb0 = ks_begin / WS;
-  if constexpr (PAIR) {
-    issue_a(IC<0>{}, ks_begin);
-    issue_a(IC<1>{}, ks_begin + 1);
-    issue_w(IC<0>{}, wb0);
-    issue_w(IC<1>{}, wb0);
-    issue_a(IC<2>{}, ks_begin + 2);
-    issue_meta1(IC<0>{}, wb0);
-  } else if constexpr (WDIST == 3) {
-    issue_a(IC<0>{}, ks_begin);
-    issue_w(IC<0>{}, wb0);
-    issue_a(IC<1>{}, ks_begin + 1);
-    issue_w(IC<1>{}, wb0);
-    issue_a(IC<2>{}, ks_begin + 2);
-    issue_meta1(IC<0>{}, wb0);
-    issue_w(IC<2>{}, wb0);
-  } else {
-    issue_a(IC<0>{}, ks_begin);
-    issue_a(IC<1>{}, ks_begin + 1);
-    issue_w(IC<0>{}, wb0);
-    issue_a(IC<2>{}, ks_begin + 2);
-    issue_meta1(IC<0>{}, wb0);
-    issue_w(IC<1>{}, wb0);
-  }
+  constexpr int PRO = (PAIR ? 3 : WDIST) > RING - 1 ? (PAIR ? 3 : WDIST) : RING - 1;
+  static_for<0, PRO>([&](auto i) {
+    constexpr int t = (int)decltype(i)::value - PRO;
+    if constexpr (t + RING - 1 >= 0) issue_a(IC<t + RING - 1>{}, ks_begin + t + RING - 1);
+    if constexpr (t == -1) issue_meta1(IC<0>{}, wb0);
+    if constexpr (PAIR) {
+      if constexpr ((t & 1) == 0) {
+        if constexpr (t + 2 >= 0) issue_w(IC<t + 2>{}, wb0);
+        if constexpr (t + 3 >= 0) issue_w(IC<t + 3>{}, wb0);
+      }
+    } else if constexpr (t + WDIST >= 0) {
+      issue_w(IC<t + WDIST>{}, wb0);
+    }
+  });
   for (int ks0 = ks_begin, wbase = wb0; ks0 < ks_end; ks0 += NB, wbase += NB / WS)
     static_for<0, NB>([&](auto pos) { step(pos, ks0, wbase); });
   // no direct-to-LDS write may land after the workgroup has ended

@@ -337,6 +337,99 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair
   }
 }
 
+// float4 form of y_at: four consecutive columns, the same sums
+template <int NS>
+__device__ __forceinline__ float4 y4_at(const float *__restrict__ y, size_t stride, int ns,
+                                        size_t o) {
+  if constexpr (NS == 1) {
+    return *reinterpret_cast<const float4 *>(y + o);
+  } else {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+      float4 u[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        u[j] = *reinterpret_cast<const float4 *>(y + (size_t)min(s0 + j, ns - 1) * stride + o);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < ns) {
+          if (s0 + j == 0) {
+            v = u[j];
+          } else {
+            v.x = v.x + u[j].x;
+            v.y = v.y + u[j].y;
+            v.z = v.z + u[j].z;
+            v.w = v.w + u[j].w;
+          }
+        }
+    }
+    return v;
+  }
+}
+
+// k_combine with the token's routes read once per workgroup: workgroup
+// blockIdx.x covers 1024 columns (four per thread, float4 loads and stores)
+// of token blockIdx.x / nchunk, so the token's count, pair indices and
+// weights are workgroup-uniform loads and no thread divides its index by H.
+// Per element the same operations in the same order as k_combine.
+// Requires H % 4 == 0 and 16-byte aligned ypair, out and residual.
+template <int NS, int RB>
+__global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ ypair,
+                                                  const float *__restrict__ rw,
+                                                  const int32_t *__restrict__ rcnt,
+                                                  const int32_t *__restrict__ inv, int T, int k,
+                                                  int H, int shared, float *out, int ns,
+                                                  size_t stride, const float *residual,
+                                                  int nchunk) {
+  const int t = (int)(blockIdx.x / (unsigned)nchunk);
+  const int c4 = (int)(blockIdx.x - (unsigned)t * (unsigned)nchunk) * 256 + (int)threadIdx.x;
+  if (4 * c4 >= H) return;
+  const size_t col = 4 * (size_t)c4;
+  const float4 sh = shared ? y4_at<NS>(ypair, stride, ns, ((size_t)T * k + t) * H + col)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  int n = k;  // the route count arrives with the first batch of routes
+  for (int r0 = 0; r0 < n; r0 += RB) {
+    int p[RB];
+    float w[RB];
+    float4 yv[RB];
+    if (r0 == 0) n = rcnt[t];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      const size_t r = (size_t)t * k + min(r0 + j, k - 1);
+      p[j] = inv[r];
+      w[j] = rw[r];
+    }
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+      yv[j] = r0 + j < n ? y4_at<NS>(ypair, stride, ns, (size_t)p[j] * H + col)
+                         : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+      if (r0 + j < n) {
+        acc.x = acc.x + __fmul_rn(w[j], yv[j].x);
+        acc.y = acc.y + __fmul_rn(w[j], yv[j].y);
+        acc.z = acc.z + __fmul_rn(w[j], yv[j].z);
+        acc.w = acc.w + __fmul_rn(w[j], yv[j].w);
+      }
+  }
+  if (shared) {
+    acc.x = acc.x + sh.x;
+    acc.y = acc.y + sh.y;
+    acc.z = acc.z + sh.z;
+    acc.w = acc.w + sh.w;
+  }
+  const size_t i = (size_t)t * H + col;
+  if (residual) {
+    const float4 rv = *reinterpret_cast<const float4 *>(residual + i);
+    acc.x = rv.x + acc.x;
+    acc.y = rv.y + acc.y;
+    acc.z = rv.z + acc.z;
+    acc.w = rv.w + acc.w;
+  }
+  *reinterpret_cast<float4 *>(out + i) = acc;
+}
+
 }  // namespace
 
 int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
@@ -409,10 +502,30 @@ int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const
                    int nsplit, size_t split_stride, const float *d_residual) {
   const size_t total = (size_t)T * H;
   if (total == 0) return NX_OK;
-  size_t g = (total + 255) / 256;
-  if (g > 65536) g = 65536;
   const int ns = nsplit > 1 ? nsplit : 1;
   const int sh = shared ? 1 : 0;
+  auto al16 = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
+  const int nchunk = (H / 4 + 255) / 256;
+  if (H % 4 == 0 && al16(d_ypair) && al16(d_out) && al16(d_residual) &&
+      (size_t)T * nchunk < (1u << 31)) {
+    auto go4 = [&](auto kern) {
+      return launch(c, "combine", [&] {
+        kern<<<(unsigned)(T * nchunk), 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T,
+                                                            k, H, sh, d_out, ns, split_stride,
+                                                            d_residual, nchunk);
+      });
+    };
+    if (ns == 1) {
+      if (k <= 2) return go4(k_combine4<1, 2>);
+      if (k <= 4) return go4(k_combine4<1, 4>);
+      return go4(k_combine4<1, 8>);
+    }
+    if (k <= 2) return go4(k_combine4<0, 2>);
+    if (k <= 4) return go4(k_combine4<0, 4>);
+    return go4(k_combine4<0, 8>);
+  }
+  size_t g = (total + 255) / 256;
+  if (g > 65536) g = 65536;
   auto go = [&](auto kern) {
     return launch(c, "combine", [&] {
       kern<<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H, sh,
