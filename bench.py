@@ -55,7 +55,11 @@ def parse():
     p.add_argument("--no-extra", action="store_true",
                    help="skip the 32-token decode and 2048-token prefill measurements")
     p.add_argument("--prefill-steps", type=int, default=20)
-    p.add_argument("--prefill-path", default="mfma_f16", choices=["mfma_f16", "mfma_bf16"])
+    p.add_argument("--prefill-path", default="auto", choices=["auto", "mfma_f16", "mfma_bf16"])
+    p.add_argument("--only", default=None,
+                   help="run one workload alone and print its record (for profilers): "
+                        "decode, prefill, block, router, dense, or a model shape "
+                        "NAME[:T<tokens>] (qwen3_q4k, deepseek_q4k_sigmoid_shared, mixtral_q2k)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="run one device-to-device copy of this size first (calibrates HBM "
                         "byte counters under rocprofv3 --pmc)")
@@ -229,7 +233,7 @@ def path_of(kern):
     if any(n.startswith("mfv") for n in kern):
         return "mfma_split"
     if any(n.startswith("gemm") for n in kern):
-        return "mfma_f16"
+        return "mfma_bf16" if "to_bf16" in kern else "mfma_f16"
     return "gemv"
 
 
@@ -271,7 +275,8 @@ def prefill(nx, ctx, torch, args):
     out = torch.empty((T, H), device=dev, dtype=torch.float32)
     counts = active_experts(ctx, logits.cpu().numpy(), T, E, k)
     flops = 2.0 * 3 * H * F * sum(counts)
-    path = nx.PATH_MFMA_F16 if args.prefill_path == "mfma_f16" else nx.PATH_MFMA_BF16
+    path = {"auto": nx.PATH_AUTO, "mfma_f16": nx.PATH_MFMA_F16,
+            "mfma_bf16": nx.PATH_MFMA_BF16}[args.prefill_path]
 
     def step(i):
         ex.forward_dev(x.data_ptr(), logits.data_ptr(), T, k, out.data_ptr(), path=path)
@@ -282,7 +287,7 @@ def prefill(nx, ctx, torch, args):
     ex.close()
     return {
         "workload": "Mixtral-8x7B MoE layer, prefill, Q8_0, Zipf(1.2) router",
-        "tokens": T, "path": args.prefill_path, "expert_tokens": counts,
+        "tokens": T, "path": f"{args.prefill_path}: {path_of(kern)}", "expert_tokens": counts,
         "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3),
         "layer_TFLOPs": flops / (ms * 1e-3) / 1e12,
         "gemm_TFLOPs": flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None,
@@ -414,7 +419,7 @@ def router_cases(nx, ctx, torch, args):
     return res
 
 
-def model_config_cases(nx, ctx, torch, args):
+def model_config_cases(nx, ctx, torch, args, only=None):
     """The other model shapes of the hot-path survey (Q4_K experts, AUTO path):
     per token count, ms/step and the fraction of HBM and dense-fp16 MFMA peak
     on algorithmic bytes / FLOPs (realised routing).  Replicas are rotated so
@@ -422,6 +427,11 @@ def model_config_cases(nx, ctx, torch, args):
     dev = torch.device("cuda", 0)
     res = {}
     for name, fname, E, H, F, k, Fs, score, tokens, reps in MODEL_CONFIGS:
+        if only is not None:  # (name, token count or None)
+            if name != only[0]:
+                continue
+            if only[1] is not None:
+                tokens = (only[1],)
         print(f"bench: {name}", file=sys.stderr, flush=True)
         fmt = {"Q4_K": nx.Q4_K, "Q2_K": nx.Q2_K}[fname]
         # GGUF bytes per weight; Q2_K stays resident with its codes widened
@@ -470,6 +480,31 @@ def model_config_cases(nx, ctx, torch, args):
     return res
 
 
+def only_case(nx, ctx, torch, args):
+    """One extra workload by itself (--only)."""
+    if args.only == "prefill":
+        return {"prefill_2048_tokens": prefill(nx, ctx, torch, args)}
+    if args.only == "router":
+        return {"router_logits": router_cases(nx, ctx, torch, args)}
+    if args.only == "dense":
+        return {"dense_matvec_1_token": dense_cases(nx, ctx, torch, args)}
+    if args.only == "block":
+        E, H, k = 8, 4096, 2
+        sets = make_expert_sets(nx, ctx, torch, nx.Q4_K, E, H, 14336, args.replicas, args.seed)
+        g = torch.Generator(device=torch.device("cuda", 0))
+        g.manual_seed(args.seed + 1)
+        x = torch.randn((32, H), generator=g, device=torch.device("cuda", 0), dtype=torch.float32)
+        rec = {"moe_block_1_token": block_case(nx, ctx, torch, sets, x, E, H, k, args)}
+        for s_ in sets:
+            s_.close()
+        return rec
+    name, _, tok = args.only.partition(":")
+    if name not in [m[0] for m in MODEL_CONFIGS]:
+        raise SystemExit(f"--only: unknown workload {args.only!r}")
+    T = int(tok.lstrip("T")) if tok else None
+    return {"model_configs": model_config_cases(nx, ctx, torch, args, only=(name, T))}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -500,6 +535,10 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.only and args.only != "decode":
+        print(json.dumps(only_case(nx, ctx, torch, args)), flush=True)
+        ctx.close()
+        return
     print(f"bench: building {args.replicas} Q4_K expert replicas (E={E} H={H} F={F})",
           file=sys.stderr, flush=True)
     sets = make_expert_sets(nx, ctx, torch, nx.Q4_K, E, H, F, args.replicas, args.seed)
@@ -541,19 +580,19 @@ def main():
     achieved = gateup_bytes / (gu_ms * 1e-3) / 1e9 if gu_ms else None
 
     extra = {}
-    if not args.no_extra:
+    if not args.no_extra and not args.only:
         print("bench: decode, 32 tokens", file=sys.stderr, flush=True)
         ms32, kern32, gu32, dn32, _ = decode_case(32, nx.PATH_AUTO)
         extra["decode_32_tokens"] = {
             "ms_per_step": ms32, "tokens_per_s": 32 / (ms32 * 1e-3),
             "effective_GBps": (gu32 + dn32) / (ms32 * 1e-3) / 1e9, "path": "auto: " + path_of(kern32),
             "kernels_ms": {k_: round(v, 4) for k_, v in kern32.items()}}
-    if not args.no_extra:
+    if not args.no_extra and not args.only:
         print("bench: MoE block, 1 token", file=sys.stderr, flush=True)
         extra["moe_block_1_token"] = block_case(nx, ctx, torch, sets, x, E, H, k, args)
     for s_ in sets:
         s_.close()
-    if not args.no_extra:
+    if not args.no_extra and not args.only:
         print("bench: prefill", file=sys.stderr, flush=True)
         extra["prefill_2048_tokens"] = prefill(nx, ctx, torch, args)
         extra["model_configs"] = model_config_cases(nx, ctx, torch, args)
@@ -572,7 +611,7 @@ def main():
             traffic = None
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.only:
         print(f"bench: cpu baseline on {args.cpu_tokens} tokens", file=sys.stderr, flush=True)
         cpu = cpu_baseline(nx, ctx, torch, x, {"router": router}, E, H, F, k, args.seed,
                            args.cpu_tokens)

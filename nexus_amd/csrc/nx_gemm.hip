@@ -398,14 +398,20 @@ __device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WC &w, const W
 
 // LDS ring of activation stages: stage = the 128 x 64 activation tile of one
 // K step as 128 rows of eight 16-byte chunks (chunk c = operand positions
-// 8c .. 8c+7 of the step); chunk c of row r is stored at slot
-// c ^ ((r / 2) % 8).  A 16-lane group of an MFMA operand read takes one chunk
-// of 16 consecutive rows: rows 2k and 2k+1 fall in the two halves of the
-// 64 banks, and the swizzle spreads the eight row pairs over eight slots, so
-// the read is free of bank conflicts.  Distinct arrays per stage let the
+// 8c .. 8c+7 of the step); chunk c of row r is stored at slot c ^ swz(r),
+// swz(r) = (r ^ (r / 8 % 2)) % 8.  ds_read_b128 serves eight lanes per
+// cycle from 32 four-byte banks (128 bytes); an MFMA operand read takes one
+// chunk of 16 consecutive rows, lanes 8j .. 8j+7 rows 8j .. 8j+7, and swz
+// sends those eight rows to eight different 16-byte slots, so the read is
+// free of bank conflicts (SQ_LDS_BANK_CONFLICT reads 0; (r / 2) % 8, which
+// pairs rows 2k and 2k+1 on one slot, read 4 conflict cycles per
+// ds_read_b128).  Distinct arrays per stage let the
 // compiler track each stage's direct-to-LDS loads separately.
 constexpr int RING = 4;
 typedef __attribute__((address_space(3))) void lds_void;
+
+// the slot permutation of row r: chunk c is stored at slot c ^ swz(r)
+__device__ __forceinline__ int swz(int r) { return (r ^ ((r >> 3) & 1)) & 7; }
 
 template <int S>
 __device__ __forceinline__ uint4 *ring_stage(uint4 *r0, uint4 *r1, uint4 *r2, uint4 *r3) {
@@ -435,9 +441,10 @@ __device__ __forceinline__ void static_for(F &&f) {
 }
 
 // Kernel shape per format and pass.  NT = 16-row weight sets per wave
-// (the tile has 64 NT weight rows), PAIR = code loads of steps 2k and 2k+1
-// issued back to back (both halves of the same lines, the second load hits
-// the cache), OCC = workgroups per CU.  Both passes keep 32 rows per wave
+// (the tile has 64 NT weight rows), GRP > 1: the code loads of steps
+// GRP k .. GRP k + GRP - 1 issued back to back (they read parts of the same
+// lines, so a line is fetched once while all of them are in flight), OCC =
+// workgroups per CU.  Both passes keep 32 rows per wave
 // (NT = 2) and two workgroups per CU; F32 takes one workgroup per CU.
 // Measured on the Qwen3 (E = 128, T = 512) and DeepSeek (E = 256,
 // T = 4096) Q4_K layers and the Mixtral Q8_0 prefill: NT = 1 and NT = 4
@@ -466,11 +473,14 @@ __host__ __device__ constexpr int gemm_nt(int fmt, bool gateup) {
 #ifndef NX_GEMM_META2_Q4
 #define NX_GEMM_META2_Q4 0
 #endif
+#ifndef NX_GEMM_GRP_Q4
+#define NX_GEMM_GRP_Q4 1
+#endif
 template <int FMT, bool GATEUP>
 struct GemmShape {
   static constexpr int NT = gemm_nt(FMT, GATEUP);
   static constexpr bool Q4 = FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0;
-  static constexpr bool PAIR = false;
+  static constexpr int GRP = Q4 ? NX_GEMM_GRP_Q4 : 1;
   static constexpr int WDIST = Q4 ? NX_GEMM_WDIST_Q4 : WDIST_CFG;
   static constexpr bool META2 = FMT == NX_FMT_Q8_0 || (Q4 && NX_GEMM_META2_Q4);
   static constexpr int OCC = (NT == 4 || FMT == NX_FMT_F32) ? 1 : 2;
@@ -486,8 +496,8 @@ int gemm_bn(int fmt, bool gateup) { return 64 * gemm_nt(fmt, gateup); }
 // step P lets through the loads issued after the last one P needs (its
 // activation stage, its codes, its window's scales).
 struct LoadSchedule {
-  int ring, ws, na, ncw, nmw, wdist;
-  bool pair, meta2;
+  int ring, ws, na, ncw, nmw, wdist, grp;
+  bool meta2;
   static constexpr int mod(int x, int m) { return ((x % m) + m) % m; }
   constexpr int outstanding(int P) const {
     const int wstart = P - mod(P, ws);
@@ -500,9 +510,9 @@ struct LoadSchedule {
         after += nmw;
         if (t + 1 == wstart) after = 0;
       }
-      const int nj = pair ? (mod(t, 2) == 0 ? 2 : 0) : 1;
+      const int nj = grp > 1 ? (mod(t, grp) == 0 ? grp : 0) : 1;
       for (int k = 0; k < nj; ++k) {
-        const int j = t + (pair ? 2 : wdist) + k;
+        const int j = t + (grp > 1 ? grp : wdist) + k;
         if (j < 0) continue;
         if (meta2 && nmw > 0 && mod(j, ws) == 0) {
           after += nmw;
@@ -522,7 +532,8 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   using V8 = typename Op::V8;
   using Shape = GemmShape<FMT, GATEUP>;
   constexpr int NT = Shape::NT;
-  constexpr bool PAIR = Shape::PAIR;
+  constexpr int GRP = Shape::GRP;
+  static_assert(GRP == 1 || GRP == 2 || GRP == 4, "code load groups");
   constexpr int BN = 64 * NT;
   constexpr int NMAT = GATEUP ? 2 : 1;
   constexpr int WS = win_steps<FMT>();
@@ -534,11 +545,12 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   constexpr int NMB = META2 ? 2 : 1;
   constexpr int WDIST = Shape::WDIST;
   // code buffers (steps mod NBUF)
-  constexpr int NBUF = PAIR ? 4 : (WDIST <= 2 ? 2 : (WDIST <= 4 ? 4 : 8));
-  static_assert(PAIR || WDIST <= NBUF, "code buffers");  // issued after the decode
+  constexpr int NBUF = GRP > 1 ? 2 * GRP : (WDIST <= 2 ? 2 : (WDIST <= 4 ? 4 : 8));
+  static_assert(GRP > 1 || WDIST <= NBUF, "code buffers");  // issued after the decode
   // a window's double-buffered scales are fetched after the last decode of
   // the window two back
-  static_assert(!META2 || PAIR || WDIST <= win_steps<FMT>() + 1, "scale buffers");
+  static_assert(!META2 || (GRP > 1 ? 2 * GRP <= win_steps<FMT>() + 2
+                                     : WDIST <= win_steps<FMT>() + 1), "scale buffers");
   // steps per loop body: whole rounds of the ring, of the code buffers and
   // of the scale buffers
   constexpr int NB0 = RING > NBUF ? RING : NBUF, NB1 = META2 ? 2 * WS : WS;
@@ -547,7 +559,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   constexpr int NA = 4;
   constexpr int IG = GATEUP ? 2 : 4;  // M-tiles per scheduling group
   constexpr LoadSchedule sched{RING, WS, NA, NMAT * NT * n_code_loads<FMT>(),
-                               NMAT * NT * n_meta_loads<FMT>(), WDIST, PAIR, META2};
+                               NMAT * NT * n_meta_loads<FMT>(), WDIST, GRP, META2};
   __shared__ __attribute__((aligned(16))) uint4 ring0[BM * 8];
   __shared__ __attribute__((aligned(16))) uint4 ring1[BM * 8];
   __shared__ __attribute__((aligned(16))) uint4 ring2[BM * 8];
@@ -555,13 +567,15 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // Tile order.  xcd_split (gate/up): workgroup L runs on XCD L % 8; XCD x
+  // Tile order.  xcd_split 1 (gate/up): workgroup L runs on XCD L % 8; XCD x
   // owns N-tiles [x * npx, (x+1) * npx) and takes the experts in tile-list
   // order, each as a block of (its m_e M-tiles) x (the XCD's N-tiles), in
   // groups of g_e = XCD_WGS / m_e N-tiles with the M-tiles fastest: about
   // XCD_WGS workgroups, as many as an XCD runs at once, share g_e weight
-  // tiles and m_e activation tiles through the XCD's L2.  Otherwise (down,
-  // whose activation tiles span K = the expert width and are the larger
+  // tiles and m_e activation tiles through the XCD's L2.  xcd_split 2
+  // (gate/up, few pairs per expert): XCD x runs one contiguous chunk of the
+  // M-tile-major list (N-tiles fastest).  xcd_split 0 (down, whose
+  // activation tiles span K = the expert width and are the larger
   // operand): N-tiles fastest, so the N-tiles of one activation tile run
   // together.
   constexpr int XCD_WGS = 32 * Shape::OCC;  // 32 CUs x OCC workgroups
@@ -572,7 +586,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   const int mcount = g.tiles[0];
   if (mcount <= 0) return;
   int tile, ntile;
-  if (g.xcd_split) {
+  if (g.xcd_split == 1) {
     const int xcd = L & 7, j = L >> 3, npx = (g.n_tiles + 7) >> 3;
     // the expert's block: tiles of one expert are consecutive, first rows
     // 0, BM, 2 BM, ...
@@ -588,6 +602,17 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
     tile = te + r2 % me;
     ntile = xcd * npx + grp * ge + r2 / me;
     if (ntile >= g.n_tiles) return;  // workgroup-uniform
+  } else if (g.xcd_split == 2) {
+    // XCD x runs items [x per, (x+1) per) of the list: the N-tiles of an
+    // M-tile, and the M-tiles of an expert, run together on one XCD
+    const int xcd = L & 7, j = L >> 3;
+    const long items = (long)mcount * g.n_tiles;
+    const long per = (items + 7) >> 3;
+    if (j >= per) return;  // workgroup-uniform
+    const long it = xcd * per + j;
+    if (it >= items) return;
+    tile = (int)(it / g.n_tiles);
+    ntile = (int)(it - (long)tile * g.n_tiles);
   } else {
     tile = L / g.n_tiles;
     ntile = L - tile * g.n_tiles;
@@ -617,7 +642,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
 
   // ---- activation chunks: instruction i of this wave fills stage chunks
   // (4 * wave + i) * 64 + lane, i.e. row r_i = (4 * wave + i) * 8 + lane / 8,
-  // slot lane % 8, which holds chunk (lane % 8) ^ ((r_i / 2) % 8) of that row
+  // slot lane % 8, which holds chunk (lane % 8) ^ swz(r_i) of that row
   // (gathered through the permutation for gate/up).  One wave-uniform
   // resource spans the activation buffer; absent rows, and every step past
   // the padded width, read zero (rows are zero between the width and the
@@ -636,7 +661,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
     const int r = (4 * wave + i) * 8 + (lane >> 3);
-    const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+    const int chunk = (lane & 7) ^ swz(r);
     abase[i] = r < mrows ? (uint32_t)arow[i] * (uint32_t)g.a_stride * 2u + 16u * chunk : OOB;
   }
   // steps holding data (the padded width), and this workgroup's steps:
@@ -702,11 +727,9 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   auto issue_late = [&](auto pos, int wbase) {
     constexpr int T = decltype(pos)::value;
     if constexpr ((T + 1) % WS == 0) issue_meta1(IC<T + 1>{}, wbase);
-    if constexpr (PAIR) {
-      if constexpr (T % 2 == 0) {
-        issue_w(IC<T + 2>{}, wbase);
-        issue_w(IC<T + 3>{}, wbase);
-      }
+    if constexpr (GRP > 1) {
+      if constexpr (T % GRP == 0)
+        static_for<0, GRP>([&](auto k) { issue_w(IC<T + GRP + decltype(k)::value>{}, wbase); });
     } else {
       issue_w(IC<T + WDIST>{}, wbase);
     }
@@ -730,7 +753,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   // after the last decode.  Every step issues its loads unconditionally (a
   // conditional load would make the compiler copy its registers, waiting for
   // all loads in flight).
-  const int sw = (l16 >> 1) & 7;
+  const int sw = swz(l16);
   // 16-row sets of the tile holding pairs (workgroup-uniform)
   const int msub = __builtin_amdgcn_readfirstlane((mrows + 15) >> 4);
   auto step = [&](auto pos, int ks0, int wbase) {
@@ -805,16 +828,15 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   // (ks_begin is a whole number of bodies: ring stages and code buffers
   // keep their step-relative indices, wb0 is its window)
   const int wb0 = ks_begin / WS;
-  constexpr int PRO = (PAIR ? 3 : WDIST) > RING - 1 ? (PAIR ? 3 : WDIST) : RING - 1;
+  constexpr int WD = GRP > 1 ? GRP : WDIST;  // first code step issued at step -WD
+  constexpr int PRO = WD > RING - 1 ? WD : RING - 1;
   static_for<0, PRO>([&](auto i) {
     constexpr int t = (int)decltype(i)::value - PRO;
     if constexpr (t + RING - 1 >= 0) issue_a(IC<t + RING - 1>{}, ks_begin + t + RING - 1);
     if constexpr (t == -1) issue_meta1(IC<0>{}, wb0);
-    if constexpr (PAIR) {
-      if constexpr ((t & 1) == 0) {
-        if constexpr (t + 2 >= 0) issue_w(IC<t + 2>{}, wb0);
-        if constexpr (t + 3 >= 0) issue_w(IC<t + 3>{}, wb0);
-      }
+    if constexpr (GRP > 1) {
+      if constexpr (((t % GRP) + GRP) % GRP == 0 && t + GRP >= 0)
+        static_for<0, GRP>([&](auto k) { issue_w(IC<t + GRP + decltype(k)::value>{}, wb0); });
     } else if constexpr (t + WDIST >= 0) {
       issue_w(IC<t + WDIST>{}, wb0);
     }
@@ -955,10 +977,21 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   const int rows = a.rows > a.srows ? a.rows : a.srows;
   const int BN = gemm_bn(ex->fmt, gateup);
   a.n_tiles = (rows + BN - 1) / BN;
-  a.xcd_split = gateup ? 1 : 0;
-  // enough workgroups for either order at the largest M-tile count
-  const long per = a.xcd_split ? 8L * ((a.n_tiles + 7) / 8) * p.max_tiles
-                               : (long)a.n_tiles * p.max_tiles;
+  // tile order (see k_gemm): gate/up with at most two M-tiles per active
+  // expert on average takes the XCD-chunked M-tile-major order (an M-tile's
+  // N-tiles share its activation tile in one L2), with more the XCD split
+  // by N-tiles (an N-tile group's weights serve all of the expert's
+  // M-tiles); down N-tiles fastest.  Measured: Qwen3 T = 512 gate/up
+  // 120 -> 101 us and DeepSeek T = 4096 2.93 -> 2.82 ms (HBM reads 14.7 ->
+  // 9.9 GB) with the chunked order; Mixtral Q8_0 prefill (four M-tiles per
+  // expert) 0.98 -> 1.17 ms with it, so it keeps the split.
+  const long pairs = (long)p.T * p.k;
+  const long active = std::max<long>(1, std::min<long>(ex->E, pairs));
+  a.xcd_split = gateup ? (pairs <= 2L * BM * active ? 2 : 1) : 0;
+  // enough workgroups for the order at the largest M-tile count
+  const long per = a.xcd_split == 1 ? 8L * ((a.n_tiles + 7) / 8) * p.max_tiles
+                   : a.xcd_split == 2 ? 8L * (((long)a.n_tiles * p.max_tiles + 7) / 8)
+                                      : (long)a.n_tiles * p.max_tiles;
   a.ksplit = gateup ? 1 : p.ksplit;
   a.wg_per_split = (int)per;
   const long wgs = per * a.ksplit;
