@@ -198,6 +198,8 @@ int nx_experts_load(nx_ctx *ctx, nx_experts *ex, int expert, int role, const voi
                     size_t src_bytes, int src_on_device);
 int nx_experts_info(const nx_experts *ex, int *fmt, int *num_experts, int *hidden, int *ff_dim,
                     int *shared_ff_dim, size_t *device_bytes);
+// Frees the set's device planes (after the device's work in flight); the
+// set may be destroyed before or after its context.
 int nx_experts_destroy(nx_experts *ex);
 
 /* ---------------------------------------------------------------- dense matrices */

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import sys
 import subprocess
 
 import numpy as np
@@ -204,6 +205,8 @@ class Context:
         self.close()
 
     def __del__(self):
+        if sys.is_finalizing():  # the process is ending: leave it to the OS
+            return
         try:
             self.close()
         except Exception:
@@ -373,6 +376,8 @@ class Experts:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():  # the process is ending: leave it to the OS
+            return
         try:
             self.close()
         except Exception:
@@ -469,6 +474,8 @@ class Matrix:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():  # the process is ending: leave it to the OS
+            return
         try:
             self.close()
         except Exception:
@@ -495,6 +502,8 @@ class Gguf:
         self.close()
 
     def __del__(self):
+        if sys.is_finalizing():  # the process is ending: leave it to the OS
+            return
         try:
             self.close()
         except Exception:

@@ -676,6 +676,7 @@ int nx_experts_create(nx_ctx *c, int fmt, int E, int H, int F, nx_experts **out)
                                         std::to_string(fi.block));
   nx_experts *ex = new nx_experts();
   ex->ctx = c;
+  ex->device = c->device;
   ex->fmt = fmt;
   ex->E = E;
   ex->H = H;
@@ -760,12 +761,11 @@ int nx_experts_info(const nx_experts *ex, int *fmt, int *E, int *H, int *F, int 
   return NX_OK;
 }
 
+// The set may outlive its context (its context pointer is not followed
+// here): hipFree waits for the device's work in flight before it frees.
 int nx_experts_destroy(nx_experts *ex) {
   if (!ex) return NX_OK;
-  if (ex->ctx) {
-    (void)hipSetDevice(ex->ctx->device);
-    (void)hipStreamSynchronize(ex->ctx->stream);
-  }
+  (void)hipSetDevice(ex->device);
   for (void *p : ex->allocs) (void)hipFree(p);
   delete ex;
   return NX_OK;
@@ -784,6 +784,7 @@ int nx_matrix_create(nx_ctx *c, int fmt, int rows, int cols, nx_matrix **out) {
                                         std::to_string(fi.block));
   nx_experts *ex = new nx_experts();
   ex->ctx = c;
+  ex->device = c->device;
   ex->fmt = fmt;
   ex->E = 1;
   ex->H = rows;
@@ -925,27 +926,35 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   // 65504, which SwiGLU activations of real models can pass; bf16 keeps
   // float32's range, runs as fast here, and stays within the MFMA bar.
   if (use == NX_PATH_AUTO) {
-    const long active_max = std::min<long>(E, (long)T * k);
+    // Tokens per active expert, with the active count expected under
+    // uniform routing, E (1 - (1 - k/E)^T).
+    const double kk = std::min(1.0, (double)k / E);
+    const double act = std::max(1.0, E * (1.0 - std::pow(1.0 - kk, (double)T)));
+    const double tpe = (double)T * k / act;
     if (ex->fmt == NX_FMT_Q4_K && !shared) {
-      // Tokens per active expert, with the active count expected under
-      // uniform routing, E (1 - (1 - k/E)^T).  Measured crossovers (Mixtral
-      // and Qwen3 shapes): the GEMV re-reads an expert's weights per pair of
-      // its tokens and wins below ~2 tokens per expert; the split-activation
-      // MFMA path reads them once per 16 tokens and wins up to ~24; the
-      // grouped GEMM beyond.
-      const double kk = std::min(1.0, (double)k / E);
-      const double act = std::max(1.0, E * (1.0 - std::pow(1.0 - kk, (double)T)));
-      const double tpe = (double)T * k / act;
+      // Measured crossovers (Mixtral and Qwen3 shapes): the GEMV re-reads an
+      // expert's weights per pair of its tokens and wins below ~2 tokens per
+      // expert; the split-activation MFMA path reads them once per 16 tokens
+      // and wins up to ~24; the grouped GEMM beyond.
       if (tpe >= 24.0)
         use = NX_PATH_MFMA_BF16;
       else if (tpe >= 3.0 || ((long)T * k >= 64 && tpe >= 1.2))
         use = NX_PATH_MFMA_SPLIT;
       else
         use = NX_PATH_GEMV;
-    } else {
-      // MFMA once experts see enough tokens on average to amortize the tile
-      // dequantization; below that the GEMV streams each weight fewer times
+    } else if (ex->fmt == NX_FMT_F32) {
+      // f32 weights keep their precision on the GEMV; the bf16 grouped GEMM
+      // only once experts see 32 tokens on average
+      const long active_max = std::min<long>(E, (long)T * k);
       use = ((long)T * k >= 32 * active_max) ? NX_PATH_MFMA_BF16 : NX_PATH_GEMV;
+    } else {
+      // The grouped GEMM from ~3 tokens per routed expert (Mixtral Q8_0 and
+      // Q4_0 at 8 and 16 tokens, Qwen3 Q8_0 at 32), or from 6 tokens when a
+      // shared expert sees them all: the GEMV passes over the shared expert
+      // per pair of tokens and over the routed experts per token group
+      // (DeepSeek Q4_K with its shared expert: GEMV 0.29 / 0.81 / 10.5 ms
+      // at 4 / 8 / 32 tokens, grouped GEMM 0.36 / 0.61 / 1.44 ms).
+      use = (tpe >= 3.0 || (shared && T >= 6)) ? NX_PATH_MFMA_BF16 : NX_PATH_GEMV;
     }
   }
 
@@ -1083,6 +1092,12 @@ int nx_moe_forward(nx_ctx *c, const nx_experts *ex, const float *x, const float 
 
 }  // extern "C"
 
+// tokens up to which the exact block runs its prologue as one launch
+#ifndef NX_BLOCK_PROLOGUE_MAX_T
+#define NX_BLOCK_PROLOGUE_MAX_T 64
+#endif
+constexpr int BLOCK_PROLOGUE_MAX_T = NX_BLOCK_PROLOGUE_MAX_T;
+
 // One MoE block: normed = rms_norm(hidden), logits = W_r . normed,
 // hidden += MoE(normed, logits).  The FFN half of decode_with_cache
 // (src/engine/mod.rs:1129-1142) with the MoE layer in place of the dense FFN.
@@ -1100,8 +1115,15 @@ int nx_moe_block_dev(nx_ctx *c, const nx_experts *ex, float *d_hidden, const flo
   float *d_n, *d_l;
   NX_TRY(ws(c, WS_NORMED, n, &d_n));
   NX_TRY(ws(c, WS_BLK_LOGITS, (size_t)T * E, &d_l));
-  NX_TRY(nx_rms_norm_dev(c, d_hidden, n, d_norm_w, norm_len, eps, T, H, exact, d_n));
-  NX_TRY(launch_router_logits(c, d_router_w, d_n, T, E, H, exact != 0, d_l));
+  if (exact && T <= BLOCK_PROLOGUE_MAX_T &&
+      block_prologue_fits(H, d_hidden, d_norm_w, d_router_w, d_n)) {
+    // one launch: each workgroup repeats its token's (parallel, latency-bound)
+    // sum-of-squares chain instead of waiting on a separate kernel
+    NX_TRY(launch_block_prologue(c, d_hidden, d_norm_w, eps, d_router_w, T, E, H, d_n, d_l));
+  } else {
+    NX_TRY(nx_rms_norm_dev(c, d_hidden, n, d_norm_w, norm_len, eps, T, H, exact, d_n));
+    NX_TRY(launch_router_logits(c, d_router_w, d_n, T, E, H, exact != 0, d_l));
+  }
   // the residual add (hidden + layer output, one rounding) happens in the
   // combine's final write
   return moe_forward(c, ex, d_n, d_l, T, k, score_mode, path, d_hidden, d_hidden);

@@ -114,7 +114,8 @@ struct nx_matrix {
 };
 
 struct nx_experts {
-  nx_ctx *ctx = nullptr;
+  nx_ctx *ctx = nullptr;  // compared, never followed, once the set exists
+  int device = 0;         // the device its planes live on
   int fmt = 0;
   int E = 0, H = 0, F = 0, Fs = 0;
   nx::RolePlane role[3];
@@ -201,6 +202,11 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
                          bool exact, float *d_out);
 // per-row sequential sum of squares (rms_norm's variance sum, bit-exact)
 int launch_sumsq_exact(nx_ctx *c, const float *d_x, int T, int H, float *d_out);
+// exact RMSNorm + router logits of T tokens in one launch (block prologue);
+// block_prologue_fits: the row shape and alignment it takes
+int launch_block_prologue(nx_ctx *c, const float *d_x, const float *d_nw, float eps,
+                          const float *d_w, int T, int E, int H, float *d_xn, float *d_logits);
+bool block_prologue_fits(int H, const void *x, const void *nw, const void *w, const void *xn);
 int launch_rms_apply(nx_ctx *c, const float *d_x, const float *d_sumsq, const float *d_w,
                      float eps, int T, int H, float *d_out);
 int launch_rms_fast(nx_ctx *c, const float *d_x, const float *d_w, float eps, int T, int H,

@@ -103,10 +103,14 @@ constexpr int C8_ROW = 36;  // floats per chain in the LDS product tile (32 + 4 
 // loads; with 4-byte loads column i of lane l at 256 i + 4 l).
 // DIAG: chain t pairs row t of W with row t of X (E = 1), so W = X gives
 // the sequential sum of squares of each row (rms_norm's variance sum).
-template <bool VEC, bool DIAG = false>
-__global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__ W,
-                                                      const float *__restrict__ X, int T, int E,
-                                                      int H, float *__restrict__ out) {
+// chain8_run: the engine, for a 128-thread workgroup, chains chain0 ..
+// chain0 + 7 (chain = t E + e); returns chain chain0 + lane / 8 % 8's sum in
+// the lanes of the second wave (the first wave's return value is
+// meaningless).  Every wave's DMA has drained when it returns.
+template <bool VEC>
+__device__ __forceinline__ float chain8_run(const float *__restrict__ W,
+                                            const float *__restrict__ X, int T, int E, int H,
+                                            int chain0, bool DIAG) {
 #pragma clang fp contract(off)
   // one array per ring stage and operand (eight, as many DMA targets as the
   // compiler tracks): it then knows which DMA a read depends on and waits for
@@ -122,7 +126,7 @@ __global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__
   const int lane = threadIdx.x & 63;
   const int j = lane & 7;
   const int cw = lane >> 3;  // chain within the wave
-  const int chain = blockIdx.x * 8 + cw;
+  const int chain = chain0 + cw;
   const bool valid = chain < T * E;
   const int t = valid ? chain / E : 0;
   const int e = valid ? chain - t * E : 0;
@@ -270,7 +274,159 @@ __global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__
     step(IC<3>{}, k + 3);
   }
   wait_vm<0>();  // the DMA of stages past the end has drained
-  if (!producer && valid && j == 0) out[(size_t)t * E + e] = s;
+  return s;
+}
+
+template <bool VEC, bool DIAG = false>
+__global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__ W,
+                                                      const float *__restrict__ X, int T, int E,
+                                                      int H, float *__restrict__ out) {
+  const int chain = blockIdx.x * 8 + ((threadIdx.x >> 3) & 7);
+  const float s = chain8_run<VEC>(W, X, T, E, H, blockIdx.x * 8, DIAG);
+  if ((threadIdx.x >> 6) == 1 && chain < T * E && (threadIdx.x & 7) == 0) out[chain] = s;
+}
+
+// The exact prologue of one MoE block (RMSNorm, then the router logits of
+// the normalised row) in one launch: workgroup (g, t) takes token t and
+// experts 8g .. 8g+7, 256 threads.  Requires H % 4 == 0, H <= BP_MAXH and
+// 16-byte aligned rows.
+//  1. Row t goes to LDS, and its squares (separately rounded) with it.
+//  2. Wave 0 adds the squares in column order, reading them from LDS
+//     (every lane the same chain; four columns per 16-byte read, the reads
+//     of the next 32 columns in flight during the adds), while waves 1-3 pull
+//     the group's router rows into the cache.  rstd = 1 / sqrt(sum / H + eps).
+//     A chain's adds are dependent: about 8 clocks each, the same with only
+//     one quarter of the wave's lanes active, so the two chains (4096
+//     columns each at H = 4096) are the kernel's floor.
+//  3. Every thread forms its columns of the normalised row, (x_i rstd) w_i,
+//     into LDS and to xn (each workgroup of a token writes the same values).
+//  4. The group's chains: waves 1-3 form the products W[e][c] * xn[c] of
+//     512 columns at a time into one of two LDS buffers while wave 0 adds the
+//     previous 512 in column order (lane 8 m + j: chain m); one barrier per
+//     512 columns.
+// The arithmetic is that of the RMSNorm kernel and the chain kernel, so the
+// row and the logits are bit-identical to theirs.
+constexpr int BP_MAXH = 8192;
+constexpr int BP_CH = 512;  // columns per product buffer
+
+// s += v[0] + ... + v[7] (32 columns), in order
+__device__ __forceinline__ void add32(float &s, const float4 (&v)[8]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    s = s + v[m].x;
+    s = s + v[m].y;
+    s = s + v[m].z;
+    s = s + v[m].w;
+  }
+}
+
+// the column-order sum of n4 float4 (n4 % 8 == 0) at src, this lane's
+// 32-column reads one group ahead of its adds
+__device__ __forceinline__ float sum_ordered(const float4 *src, int n4, float s) {
+  float4 a[8], b[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) a[m] = src[m];
+  for (int g = 0; g < n4; g += 16) {
+    if (g + 8 < n4) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) b[m] = src[g + 8 + m];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    add32(s, a);
+    __builtin_amdgcn_sched_barrier(0);
+    if (g + 8 >= n4) break;
+    if (g + 16 < n4) {
+#pragma unroll
+      for (int m = 0; m < 8; ++m) a[m] = src[g + 16 + m];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    add32(s, b);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return s;
+}
+
+__global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict__ x,
+                                                        const float *__restrict__ nw, float eps,
+                                                        const float *__restrict__ W, int E, int H,
+                                                        float *__restrict__ xn,
+                                                        float *__restrict__ logits) {
+#pragma clang fp contract(off)
+  __shared__ float4 row4[BP_MAXH / 4];            // x, then the normalised row
+  __shared__ float4 prod4[2][8][BP_CH / 4];       // squares (flat), rstd, then products
+  float4 *sq4 = &prod4[0][0][0];                  // BP_MAXH / 4 float4
+  const int t = blockIdx.y, e0 = blockIdx.x * 8, tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int ne = min(8, E - e0);
+  const int H4 = H >> 2;
+  const int H4p = (H4 + 7) & ~7;                  // whole 32-column groups (zero padded)
+  const float4 *xr4 = reinterpret_cast<const float4 *>(x + (size_t)t * H);
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  // 1. the row and its squares
+  for (int i = tid; i < H4p; i += 256) {
+    const float4 v = i < H4 ? xr4[i] : z4;
+    row4[i] = v;
+    sq4[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+  }
+  __syncthreads();
+  // 2. the sum of squares; the other waves touch the group's router rows
+  if (wave == 0) {
+    const float ss = sum_ordered(sq4, H4p, 0.f);
+    // (every lane of the wave has read its last squares)
+    if (lane == 0) sq4[0].x = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
+  } else if (wave > 0) {  // (index i = tid - 64 >= 0)
+    const float4 *w4 = reinterpret_cast<const float4 *>(W + (size_t)e0 * H);
+    uint32_t acc = 0;
+    for (int i = tid - 64; i < ne * H4; i += 192) {
+      const float4 v = w4[i];
+      acc ^= __float_as_uint(v.x) ^ __float_as_uint(v.w);
+    }
+    asm volatile("" ::"v"(acc));  // the loads are kept for their cache fills
+  }
+  __syncthreads();
+  const float r = sq4[0].x;
+  // 3. the normalised row
+  const float4 *nw4 = reinterpret_cast<const float4 *>(nw);
+  float4 *xo4 = reinterpret_cast<float4 *>(xn + (size_t)t * H);
+  for (int i = tid; i < H4; i += 256) {
+    const float4 v = row4[i], w = nw4[i];
+    const float4 o = make_float4((v.x * r) * w.x, (v.y * r) * w.y, (v.z * r) * w.z, (v.w * r) * w.w);
+    row4[i] = o;
+    if (blockIdx.x == 0) xo4[i] = o;
+  }
+  __syncthreads();
+  // 4. the router chains, 512 columns per step
+  const int nch = (H4 + BP_CH / 4 - 1) / (BP_CH / 4);
+  auto produce = [&](int k, int buf) {  // waves 1-3
+    for (int i = tid - 64; i < 8 * (BP_CH / 4); i += 192) {
+      const int m = i / (BP_CH / 4), c4 = i - m * (BP_CH / 4);
+      const int col4 = k * (BP_CH / 4) + c4;
+      float4 p = z4;
+      if (m < ne && col4 < H4) {
+        const float4 w = reinterpret_cast<const float4 *>(W + (size_t)(e0 + m) * H)[col4];
+        const float4 v = row4[col4];
+        p = make_float4(w.x * v.x, w.y * v.y, w.z * v.z, w.w * v.w);
+      }
+      prod4[buf][m][c4] = p;
+    }
+  };
+  if (wave > 0) produce(0, 0);
+  __syncthreads();
+  float s = 0.f;
+  for (int k = 0; k < nch; ++k) {
+    if (wave == 0) {
+      // the last buffer's columns past the row end are zero products; the
+      // chain adds them after its last column: s + 0 = s (s is never -0:
+      // it starts at +0)
+      s = sum_ordered(&prod4[k & 1][lane >> 3][0], BP_CH / 4, s);
+    } else if (wave > 0 && k + 1 < nch) {  // (index i = tid - 64 >= 0)
+      produce(k + 1, (k + 1) & 1);
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && (lane & 7) == 0 && (lane >> 3) < ne)
+    logits[(size_t)t * E + e0 + (lane >> 3)] = s;
 }
 
 constexpr int TL_NS = 3;  // ring stages of the tiled kernel
@@ -500,6 +656,22 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
     else
       launch_tile<false>(c, rb, d_w, d_x, T, E, H, d_out);
   });
+}
+
+int launch_block_prologue(nx_ctx *c, const float *d_x, const float *d_nw, float eps,
+                          const float *d_w, int T, int E, int H, float *d_xn, float *d_logits) {
+  if (T <= 0 || E <= 0) return NX_OK;
+  if (!block_prologue_fits(H, d_x, d_nw, d_w, d_xn))
+    return fail(NX_ERR_UNSUPPORTED, "block prologue: row shape or alignment not supported");
+  const dim3 grid((unsigned)((E + 7) / 8), (unsigned)T);
+  return launch(c, "block_prologue", [&] {
+    k_block_prologue<<<grid, 256, 0, c->stream>>>(d_x, d_nw, eps, d_w, E, H, d_xn, d_logits);
+  });
+}
+
+bool block_prologue_fits(int H, const void *x, const void *nw, const void *w, const void *xn) {
+  auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+  return H > 0 && H % 4 == 0 && H <= BP_MAXH && al(x) && al(nw) && al(w) && al(xn);
 }
 
 int launch_sumsq_exact(nx_ctx *c, const float *d_x, int T, int H, float *d_out) {

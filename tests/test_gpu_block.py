@@ -112,6 +112,35 @@ def test_moe_block_exact(ctx, fmt, E, H, F, k, T, shared):
     ex.close()
 
 
+@pytest.mark.parametrize("fmt,E,H,F,k,T", [
+    (Q4_K, 8, 4096, 256, 2, 1),    # Mixtral's width, one expert group
+    (Q8_0, 20, 2048, 128, 4, 5),   # three expert groups, the last partial
+    (Q8_0, 128, 1024, 64, 8, 2),   # sixteen groups per token
+    (Q8_0, 8, 10240, 64, 2, 2),    # a row wider than the one launch holds: three launches
+    (Q8_0, 8, 512, 64, 2, 64)])    # the most tokens the single launch takes
+def test_moe_block_exact_prologue(ctx, fmt, E, H, F, k, T):
+    """The exact block's prologue (one launch: the sum-of-squares chain, the
+    normalised row, the router chains) gives the oracle's normalised rows and
+    logits: the block output equals hidden + the layer on them, bit for bit."""
+    print(f"block prologue fmt={fmt} E={E} H={H} F={F} k={k} T={T}", flush=True)
+    L, hidden, norm_w, router = block_case(fmt, E, H, F, k, T, seed=3 * E + H + T)
+    eps = 1e-6
+    normed, logits, ffn = oracle_block(L, hidden, norm_w, eps, router)
+    ex = L.upload(nx, ctx)
+    ctx.profile(True)
+    ctx.profile_reset()
+    got = ex.block(hidden, norm_w, eps, router, k, path=nx.PATH_GEMV, exact=True)
+    ran = set(ctx.profile_stats())
+    ctx.profile(False)
+    fused = H % 4 == 0 and H <= 8192
+    assert ("block_prologue" in ran) == fused, ran
+    assert ("rms_sumsq_chain8" in ran) == (not fused), ran
+    want = (hidden + ex.forward(normed, logits, k, path=nx.PATH_GEMV)).astype(np.float32)
+    assert_same_bits(got, want)
+    assert rel_l2(got.astype(np.float64) - hidden, ffn) <= 1e-4
+    ex.close()
+
+
 def test_moe_block_mfma_residual(ctx):
     E, H, F, k, T = 8, 512, 512, 2, 192
     L, hidden, norm_w, router = block_case(Q8_0, E, H, F, k, T, seed=31, shared_F=512)
@@ -158,4 +187,13 @@ def test_moe_block_errors(ctx):
         ex.block(hidden, norm_w[:100], 1e-5, router, k)
     with pytest.raises(nx.NexusError, match=r"^MoE router produced no routes$"):
         ex.block(hidden, norm_w, 1e-5, router, 0)
+    ex.close()
+
+
+def test_experts_outlive_context():
+    """An expert set destroyed after its context (a set kept alive past the
+    context's close, e.g. by a failing test's traceback) frees cleanly."""
+    c2 = nx.Context(0)
+    ex = nx.Experts(c2, Q8_0, 4, 256, 256)
+    c2.close()
     ex.close()

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import nexus_amd as nx
-from moe_cases import Q4_K, Q8_0, Layer, rel_l2
+from moe_cases import Q4_0, Q4_K, Q8_0, Layer, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -106,6 +106,24 @@ def test_auto_path_choice(ctx, E, H, F, k, T, want):
     tokens per expert, the split-activation MFMA path up to ~24, the grouped
     GEMM beyond."""
     L = Layer(Q4_K, E, H, F, k, T, seed=E + T)
+    ex = L.upload(nx, ctx)
+    auto = ex.forward(L.x, L.logits, k, 0, nx.PATH_AUTO)
+    chosen = ex.forward(L.x, L.logits, k, 0, want)
+    ex.close()
+    np.testing.assert_array_equal(auto.view(np.uint32), chosen.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt,E,H,F,k,T,shared,want", [
+    (Q8_0, 8, 512, 1024, 2, 8, 0, nx.PATH_GEMV),        # 2 tokens per expert
+    (Q8_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_BF16),  # 4
+    (Q4_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_BF16),
+    (Q4_K, 16, 512, 512, 4, 4, 512, nx.PATH_GEMV),      # a shared expert, 4 tokens
+    (Q4_K, 16, 512, 512, 4, 8, 512, nx.PATH_MFMA_BF16)])  # a shared expert, 8 tokens
+def test_auto_path_choice_other(ctx, fmt, E, H, F, k, T, shared, want):
+    """AUTO for formats other than Q4_K and for layers with a shared expert:
+    the grouped GEMM from ~3 tokens per routed expert, or from 6 tokens with
+    a shared expert; the GEMV below (the bits of the chosen path)."""
+    L = Layer(fmt, E, H, F, k, T, seed=E + T + fmt, shared_F=shared)
     ex = L.upload(nx, ctx)
     auto = ex.forward(L.x, L.logits, k, 0, nx.PATH_AUTO)
     chosen = ex.forward(L.x, L.logits, k, 0, want)
