@@ -26,6 +26,14 @@
 // workgroup forms out[t] = sum_r w[t,r] * y[pair(t,r)] (+ shared) for its
 // rows in route order — the reference's accumulation order, with no atomics
 // and no communication between workgroups.
+//
+// Down rows longer than 64 segments (Mixtral's F = 14336: 224) take the
+// per-slot kernel in K slices instead: one wave per (row, slice of 64
+// segments), grid y = slot x slice, the slot's activations prepared once per
+// workgroup into LDS; the slices' partial sums go to the route-order combine
+// kernel, which adds them in slice order.  Weight codes are loaded with the
+// non-temporal policy: they are read once, and the activation, scale and
+// route arrays that every workgroup rereads stay in the caches.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 #include "nx_route_dev.hpp"
