@@ -16,6 +16,9 @@
 #include "nx_internal.hpp"
 
 // one token on the GEMV path: the gate/up kernel routes it itself
+#ifndef NX_ROUTE_IN_GEMV_MAX_E
+#define NX_ROUTE_IN_GEMV_MAX_E kFusedRouteMaxE
+#endif
 #ifndef NX_ROUTE_IN_GEMV
 #define NX_ROUTE_IN_GEMV 1
 #endif
@@ -935,8 +938,10 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
       // Measured crossovers (Mixtral and Qwen3 shapes): the GEMV re-reads an
       // expert's weights per pair of its tokens and wins below ~2 tokens per
       // expert; the split-activation MFMA path reads them once per 16 tokens
-      // and wins up to ~24; the grouped GEMM beyond.
-      if (tpe >= 24.0)
+      // and wins up to ~12 (Mixtral: 0.31 against 0.36 ms at 8 tokens per
+      // expert, 0.45 against 0.36 at 16; Qwen3: 0.17 / 0.20 at 8, 0.24 /
+      // 0.21 at 16); the grouped GEMM beyond.
+      if (tpe >= 12.0)
         use = NX_PATH_MFMA_BF16;
       else if (tpe >= 3.0 || ((long)T * k >= 64 && tpe >= 1.2))
         use = NX_PATH_MFMA_SPLIT;
@@ -961,7 +966,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   if (use == NX_PATH_GEMV) {
     NX_TRY(ws(c, WS_YPAIR, pairs_total * H, &d_ypair));
     // one token: the gate/up kernel routes it itself (no router launch)
-    const bool route_in_gemv = NX_ROUTE_IN_GEMV && T == 1 && E <= kFusedRouteMaxE && k <= 64;
+    const bool route_in_gemv = NX_ROUTE_IN_GEMV && T == 1 && E <= NX_ROUTE_IN_GEMV_MAX_E && k <= 64;
     if (!route_in_gemv && route_permute_fusable(T, E, k)) {
       NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
                                   d_pt, d_ps, d_inv, d_act, 0, nullptr, nullptr, 0));

@@ -100,10 +100,10 @@ def test_split_rejects(ctx):
 @pytest.mark.parametrize("E,H,F,k,T,want", [
     (8, 512, 1024, 2, 1, nx.PATH_GEMV), (8, 512, 1024, 2, 8, nx.PATH_GEMV),
     (8, 512, 1024, 2, 16, nx.PATH_MFMA_SPLIT), (64, 256, 256, 8, 8, nx.PATH_MFMA_SPLIT),
-    (8, 256, 256, 2, 256, nx.PATH_MFMA_BF16)])
+    (8, 256, 256, 2, 64, nx.PATH_MFMA_BF16), (8, 256, 256, 2, 256, nx.PATH_MFMA_BF16)])
 def test_auto_path_choice(ctx, E, H, F, k, T, want):
     """AUTO gives the bits of the path it chooses for Q4_K: the GEMV up to ~2
-    tokens per expert, the split-activation MFMA path up to ~24, the grouped
+    tokens per expert, the split-activation MFMA path up to ~12, the grouped
     GEMM beyond."""
     L = Layer(Q4_K, E, H, F, k, T, seed=E + T)
     ex = L.upload(nx, ctx)
