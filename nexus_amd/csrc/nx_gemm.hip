@@ -868,6 +868,19 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
         }
       }
   }
+  // gate/up: the workgroup holding the matrix's last rows also writes the
+  // zeros between the expert's width and act's padded width for its pairs
+  // (the down pass reads whole windows; kslot permutes within a window, so
+  // these slots are not any column's)
+  if constexpr (GATEUP) {
+    const int span = g.act_stride - rows;
+    if (span > 0 && n0 + BN >= rows) {
+      for (int i = tid; i < mrows * span; i += 256) {
+        const int r = i / span, e = rows + (i - r * span);
+        g.act[(size_t)(pair0 + m0 + r) * g.act_stride + kslot<FMT>(e)] = 0;
+      }
+    }
+  }
 }
 
 // f32 activations [T][H] -> operand type in operand order [T][kpad]
@@ -881,23 +894,6 @@ __global__ __launch_bounds__(256) void k_to_half(const float *__restrict__ x, in
     const size_t t = i / (size_t)kpad;
     const int e = kpos<FMT>((int)(i - t * kpad));
     out[i] = e < H ? OpT<BF16>::bits(x[t * H + e]) : (uint16_t)0;
-  }
-}
-
-// zero act's operand positions of elements width(p) .. kpad-1 (width F for
-// routed pairs, Fs for the shared expert's pairs p >= routed)
-template <int FMT>
-__global__ __launch_bounds__(256) void k_zero_pad(uint16_t *__restrict__ act, int stride,
-                                                  size_t routed, size_t pairs, int F, int Fs,
-                                                  int kpad) {
-  const int wmin = min(F, Fs > 0 ? Fs : F);
-  const int span = kpad - wmin;
-  const size_t n = pairs * (size_t)span;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
-       i += (size_t)gridDim.x * blockDim.x) {
-    const size_t p = i / (size_t)span;
-    const int e = wmin + (int)(i - p * span);
-    if (e >= (p < routed ? F : Fs)) act[p * stride + kslot<FMT>(e)] = 0;
   }
 }
 
@@ -1058,31 +1054,7 @@ int launch_to_half(nx_ctx *c, int fmt, const float *x, int T, int H, int kpad, b
 }
 
 int launch_gemm_gateup(nx_ctx *c, const GemmPlan &p) {
-  // act rows hold zeros between each expert's width and the padded width
-  const nx_experts *ex = p.ex;
-  const int wmin = ex->Fs > 0 ? std::min(ex->F, ex->Fs) : ex->F;
-  if (p.act_stride > wmin) {
-    const size_t routed = (size_t)p.T * p.k;
-    const size_t n = p.pairs_total * (size_t)(p.act_stride - wmin);
-    const unsigned gb = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
-    uint16_t *act = static_cast<uint16_t *>(p.act);
-    const int F = ex->F, Fs = ex->Fs, st = p.act_stride;
-    int rc = NX_OK;
-    switch (ex->fmt) {
-#define NX_ZP(F_)                                                                            \
-  case F_:                                                                                   \
-    rc = launch(c, "zero_pad", [&] {                                                         \
-      k_zero_pad<F_><<<gb, 256, 0, c->stream>>>(act, st, routed, p.pairs_total, F, Fs, st); \
-    });                                                                                      \
-    break;
-      NX_ZP(NX_FMT_Q4_K)
-      NX_ZP(NX_FMT_Q8_0)
-      NX_ZP(NX_FMT_Q4_0)
-      NX_ZP(NX_FMT_F32)
-#undef NX_ZP
-    }
-    NX_TRY(rc);
-  }
+  // (act's pad columns are zeroed by the gate/up kernel's epilogue)
   return run(c, p, true);
 }
 int launch_gemm_down(nx_ctx *c, const GemmPlan &p) { return run(c, p, false); }

@@ -76,6 +76,7 @@ __device__ int block_exclusive_scan(int v, int *wave_tot, int *total) {
 
 constexpr int PERM_THREADS = 1024;
 constexpr int PERM_WORDS = 4096;  // LDS words per bit matrix
+constexpr int PERM_KREG = 8;      // routes per token the permutation keeps in registers
 
 __global__ __launch_bounds__(PERM_THREADS) void k_permute(
     const int32_t *__restrict__ rexp, const int32_t *__restrict__ rcnt, int T, int k, int E,
@@ -142,19 +143,37 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
     const int t = t0 + tl;
     const bool mine = tl < CT && t < T;
     int nr = 0;
+    // up to PERM_KREG routes per token are read once, all in flight together,
+    // and kept for the rank pass
+    int er[PERM_KREG];
+    const bool kreg = k <= PERM_KREG;
     if (mine) {
       nr = rcnt[t];
-      for (int r = 0; r < nr; ++r) {
-        const int e = rexp[(size_t)t * k + r];
-        atomicOr(&bits[e * W + (tl >> 5)], 1u << (tl & 31));
+      if (kreg) {
+#pragma unroll
+        for (int r = 0; r < PERM_KREG; ++r) er[r] = r < k ? rexp[(size_t)t * k + r] : 0;
+#pragma unroll
+        for (int r = 0; r < PERM_KREG; ++r)
+          if (r < nr) atomicOr(&bits[er[r] * W + (tl >> 5)], 1u << (tl & 31));
+      } else {
+        for (int r = 0; r < nr; ++r) {
+          const int e = rexp[(size_t)t * k + r];
+          atomicOr(&bits[e * W + (tl >> 5)], 1u << (tl & 31));
+        }
       }
     }
     __syncthreads();
-    for (int i = tid; i < E * W; i += PERM_THREADS) {
-      const int e = i / W, w = i - e * W;
-      uint32_t s = 0;
-      for (int j = 0; j < w; ++j) s += __popc(bits[e * W + j]);
-      pref[i] = s;
+    // pref[e W + w] = set bits of row e's words 0 .. w-1: W (a power of two
+    // dividing 64) consecutive lanes hold one row, scanned with shuffles
+    for (int i0 = 0; i0 < E * W; i0 += PERM_THREADS) {
+      const int i = i0 + tid;  // every lane of a wave takes part in the shuffles
+      const int v = i < E * W ? __popc(bits[i]) : 0;
+      int x = v;
+      for (int d = 1; d < W; d <<= 1) {
+        const int y = __shfl_up(x, d, W);
+        if ((tid & (W - 1)) >= d) x += y;
+      }
+      if (i < E * W) pref[i] = (uint32_t)(x - v);
     }
     __syncthreads();
     if (mine) {
@@ -163,7 +182,14 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
           inv[(size_t)t * k + r] = -1;
           continue;
         }
-        const int e = rexp[(size_t)t * k + r];
+        int e;
+        if (kreg) {
+          e = 0;
+#pragma unroll
+          for (int j = 0; j < PERM_KREG; ++j) e = j == r ? er[j] : e;  // stays in registers
+        } else {
+          e = rexp[(size_t)t * k + r];
+        }
         const int wi = e * W + (tl >> 5);
         const int rank = (int)pref[wi] + __popc(bits[wi] & ((1u << (tl & 31)) - 1u));
         const int pos = base[e] + run[e] + rank;
@@ -460,6 +486,7 @@ int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, i
   int W = PERM_WORDS / (E > 0 ? E : 1);
   if (W > PERM_THREADS / 32) W = PERM_THREADS / 32;
   if (W < 1) W = 1;
+  while (W & (W - 1)) W &= W - 1;  // a power of two: rows are scanned within a wave
   return launch(c, "permute", [&] {
     k_permute<<<1, PERM_THREADS, 0, c->stream>>>(d_expert, d_count, T, k, E, W,
                                                  tile_m > 0 ? tile_m : 1, d_ecount, d_offsets,
