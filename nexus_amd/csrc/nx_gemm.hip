@@ -884,7 +884,42 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
 }
 
 // f32 activations [T][H] -> operand type in operand order [T][kpad]
-// (positions past H are zero)
+// (positions past H are zero).  kslot keeps runs of 16 consecutive elements
+// together, so slots 16g .. 16g+15 of a row are elements kpos(16g) .. +15:
+// a thread converts one such run of token blockIdx.y (four 16-byte loads
+// when the row allows them, two 16-byte stores).
+template <int FMT, bool BF16>
+__global__ __launch_bounds__(256) void k_to_half16(const float *__restrict__ x, int H, int kpad,
+                                                   bool vec, uint16_t *__restrict__ out) {
+  const int t = blockIdx.y;
+  const int ng = kpad >> 4;
+  const float *xr = x + (size_t)t * H;
+  uint4 *orow = reinterpret_cast<uint4 *>(out + (size_t)t * kpad);
+  for (int g = blockIdx.x * 256 + threadIdx.x; g < ng; g += gridDim.x * 256) {
+    const int e0 = kpos<FMT>(g << 4);
+    float v[16];
+    if (vec && e0 + 16 <= H) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 f = *reinterpret_cast<const float4 *>(xr + e0 + 4 * q);
+        v[4 * q] = f.x;
+        v[4 * q + 1] = f.y;
+        v[4 * q + 2] = f.z;
+        v[4 * q + 3] = f.w;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] = e0 + q < H ? xr[e0 + q] : 0.f;
+    }
+    uint32_t w[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      w[q] = (uint32_t)OpT<BF16>::bits(v[2 * q]) | ((uint32_t)OpT<BF16>::bits(v[2 * q + 1]) << 16);
+    orow[2 * g] = make_uint4(w[0], w[1], w[2], w[3]);
+    orow[2 * g + 1] = make_uint4(w[4], w[5], w[6], w[7]);
+  }
+}
+
 template <int FMT, bool BF16>
 __global__ __launch_bounds__(256) void k_to_half(const float *__restrict__ x, int T, int H, int kpad,
                                                  uint16_t *__restrict__ out) {
@@ -1001,6 +1036,18 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
 
 template <int FMT>
 int to_half_fmt(nx_ctx *c, const float *x, int T, int H, int kpad, bool bf16, uint16_t *o) {
+  if (kpad % 16 == 0 && T <= 65535 && ((uintptr_t)o & 15) == 0) {
+    const bool vec = H % 4 == 0 && ((uintptr_t)x & 15) == 0;
+    const int ng = kpad / 16;
+    const dim3 grid((unsigned)std::max(1, std::min((ng + 255) / 256, 64)), (unsigned)T);
+    if (bf16)
+      return launch(c, "to_bf16", [&] {
+        k_to_half16<FMT, true><<<grid, 256, 0, c->stream>>>(x, H, kpad, vec, o);
+      });
+    return launch(c, "to_f16", [&] {
+      k_to_half16<FMT, false><<<grid, 256, 0, c->stream>>>(x, H, kpad, vec, o);
+    });
+  }
   size_t gblocks = ((size_t)T * kpad + 255) / 256;
   if (gblocks > 65536) gblocks = 65536;
   const unsigned gb = (unsigned)gblocks;
