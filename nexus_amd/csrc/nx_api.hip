@@ -180,12 +180,19 @@ int begin_launch(nx_ctx *c, const char *name, int *stat_index) {
   NX_HIP(hipEventRecord(pe.start, c->stream));
   c->pending.push_back(pe);
   *stat_index = (int)c->pending.size() - 1;
+  // a kernel started with go() binds both events to its own dispatch (the
+  // start recorded here is then superseded); other work is bracketed by
+  // the records on the stream
+  c->launch_start = pe.start;
+  c->launch_stop = pe.stop;
+  c->launch_timed = false;
   return NX_OK;
 }
 
 int end_launch(nx_ctx *c, int pending_index) {
   if (pending_index < 0) return NX_OK;
-  NX_HIP(hipEventRecord(c->pending[pending_index].stop, c->stream));
+  c->launch_start = c->launch_stop = nullptr;
+  if (!c->launch_timed) NX_HIP(hipEventRecord(c->pending[pending_index].stop, c->stream));
   return NX_OK;
 }
 

@@ -1031,7 +1031,7 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   if (!fn) return fail(NX_ERR_UNSUPPORTED, "no grouped-GEMM kernel for this format");
   const char *name = gateup ? "gemm_gateup" : "gemm_down";
   return launch(c, name,
-                [&] { hipLaunchKernelGGL(fn, dim3((unsigned)wgs), dim3(256), 0, c->stream, a); });
+                [&] { go(c, fn, dim3((unsigned)wgs), dim3(256), 0, a); });
 }
 
 template <int FMT>
@@ -1042,10 +1042,10 @@ int to_half_fmt(nx_ctx *c, const float *x, int T, int H, int kpad, bool bf16, ui
     const dim3 grid((unsigned)std::max(1, std::min((ng + 255) / 256, 64)), (unsigned)T);
     if (bf16)
       return launch(c, "to_bf16", [&] {
-        k_to_half16<FMT, true><<<grid, 256, 0, c->stream>>>(x, H, kpad, vec, o);
+        go(c, k_to_half16<FMT, true>, dim3(grid), dim3(256), 0, x, H, kpad, vec, o);
       });
     return launch(c, "to_f16", [&] {
-      k_to_half16<FMT, false><<<grid, 256, 0, c->stream>>>(x, H, kpad, vec, o);
+      go(c, k_to_half16<FMT, false>, dim3(grid), dim3(256), 0, x, H, kpad, vec, o);
     });
   }
   size_t gblocks = ((size_t)T * kpad + 255) / 256;
@@ -1053,9 +1053,9 @@ int to_half_fmt(nx_ctx *c, const float *x, int T, int H, int kpad, bool bf16, ui
   const unsigned gb = (unsigned)gblocks;
   if (bf16)
     return launch(c, "to_bf16",
-                  [&] { k_to_half<FMT, true><<<gb, 256, 0, c->stream>>>(x, T, H, kpad, o); });
+                  [&] { go(c, k_to_half<FMT, true>, dim3(gb), dim3(256), 0, x, T, H, kpad, o); });
   return launch(c, "to_f16",
-                [&] { k_to_half<FMT, false><<<gb, 256, 0, c->stream>>>(x, T, H, kpad, o); });
+                [&] { go(c, k_to_half<FMT, false>, dim3(gb), dim3(256), 0, x, T, H, kpad, o); });
 }
 
 }  // namespace

@@ -1131,14 +1131,16 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const unsigned gx = (unsigned)((rows + rows_per_wg - 1) / rows_per_wg);
 
   if (gateup) {
-    // the counters of the down pass's fused combine start at zero
-    void *cnt = nullptr;
-    NX_TRY(ws_get(c, WS_DOWN_CNT, (size_t)ex->H * sizeof(int), &cnt));
-    a.zero_cnt = static_cast<int *>(cnt);
-    a.n_zero = ex->H;
+    if (NX_GEMV_FUSE_COMBINE) {
+      // the counters of the down pass's fused combine start at zero
+      void *cnt = nullptr;
+      NX_TRY(ws_get(c, WS_DOWN_CNT, (size_t)ex->H * sizeof(int), &cnt));
+      a.zero_cnt = static_cast<int *>(cnt);
+      a.n_zero = ex->H;
+    }
     const dim3 grid(gx, (unsigned)slots_max);
     return launch(c, "gemv_gateup",
-                  [&] { hipLaunchKernelGGL(probe, grid, dim3(256), 0, c->stream, a); });
+                  [&] { go(c, probe, grid, dim3(256), 0, a); });
   }
   if (down_rows) {
     const size_t pairs_total = (size_t)p.T * p.k + (has_shared ? (size_t)p.T : 0);
@@ -1168,7 +1170,7 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
       a.residual = p.residual;
     }
     NX_TRY(launch(c, fuse ? "gemv_down_combine" : "gemv_down",
-                  [&] { hipLaunchKernelGGL(probe, grid, dim3(256), 0, c->stream, a); }));
+                  [&] { go(c, probe, grid, dim3(256), 0, a); }));
     if (fuse) return NX_OK;
     return launch_combine(c, ypair, p.rw, p.rcnt, p.inv, p.T, p.k, ex->H, has_shared, p.out,
                           kslices, a.kslice_stride, p.residual);
@@ -1191,7 +1193,7 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   }
   const unsigned lds = ylds ? (unsigned)part_bytes : 0u;
   return launch(c, "gemv_down_combine",
-                [&] { hipLaunchKernelGGL(fn, dim3(gx), dim3(threads), lds, c->stream, a); });
+                [&] { go(c, fn, dim3(gx), dim3(threads), lds, a); });
 }
 
 // One matrix over T tokens: the per-slot kernel with a single dense slot.
@@ -1237,7 +1239,7 @@ int run_gemv_matrix(nx_ctx *c, int fmt, const RolePlane &pl, const float *x, int
   const long rows_per_wg = rpg * groups_per_wg;
   const unsigned gx = (unsigned)((pl.rows + rows_per_wg - 1) / rows_per_wg);
   return launch(c, "gemv_matrix",
-                [&] { hipLaunchKernelGGL(fn, dim3(gx, 1), dim3(256), 0, c->stream, a); });
+                [&] { go(c, fn, dim3(gx, 1), dim3(256), 0, a); });
 }
 
 }  // namespace

@@ -2,6 +2,7 @@
 // expert layout, workspace, launch helpers).  Not part of the C ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -104,6 +105,11 @@ struct nx_ctx {
   std::vector<nx::KernelStat> stats;
   std::vector<nx::PendingEvent> pending;
   std::vector<hipEvent_t> event_pool;
+  // events of the launch in progress (profiling): a kernel started with
+  // nx::go takes them into its dispatch, which records them at the kernel's
+  // own start and end
+  hipEvent_t launch_start = nullptr, launch_stop = nullptr;
+  bool launch_timed = false;
 };
 
 // one dense weight matrix (rows x cols, row-major as GGUF stores it), held
@@ -163,13 +169,31 @@ int ws_get(nx_ctx *c, int slot, size_t bytes, void **out);
 int begin_launch(nx_ctx *c, const char *name, int *stat_index);
 int end_launch(nx_ctx *c, int stat_index);
 
+// Starts kernel `k` on the context's stream.  While profiling, the dispatch
+// records the launch's events (hipExtLaunchKernelGGL), so the measured time
+// is the kernel's execution alone: an event pair recorded around the launch
+// would add the records' own latency to it.
+template <typename K, typename... Args>
+void go(nx_ctx *c, K k, dim3 grid, dim3 block, uint32_t lds, Args... args) {
+  if (c->launch_start) {
+    hipExtLaunchKernelGGL(k, grid, block, lds, c->stream, c->launch_start, c->launch_stop, 0,
+                          args...);
+    c->launch_timed = true;
+  } else {
+    hipLaunchKernelGGL(k, grid, block, lds, c->stream, args...);
+  }
+}
+
 template <typename F>
 int launch(nx_ctx *c, const char *name, F &&fn) {
   int si = -1;
   NX_TRY(begin_launch(c, name, &si));
   fn();
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(NX_ERR_DEVICE, std::string("launch ") + name + ": " + hipGetErrorString(e));
+  if (e != hipSuccess) {
+    c->launch_start = c->launch_stop = nullptr;
+    return fail(NX_ERR_DEVICE, std::string("launch ") + name + ": " + hipGetErrorString(e));
+  }
   return end_launch(c, si);
 }
 

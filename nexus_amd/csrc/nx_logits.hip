@@ -609,9 +609,9 @@ void launch_tile(nx_ctx *c, int rb, const float *W, const float *X, int T, int E
                  float *out) {
   const int rows = 16 * rb;
   const dim3 grid((E + rows - 1) / rows, (T + rows - 1) / rows);
-  if (rb == 4) k_logits_tile<4, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out);
-  else if (rb == 2) k_logits_tile<2, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out);
-  else k_logits_tile<1, EXACT><<<grid, 256, 0, c->stream>>>(W, X, T, E, H, out);
+  if (rb == 4) go(c, k_logits_tile<4, EXACT>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
+  else if (rb == 2) go(c, k_logits_tile<2, EXACT>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
+  else go(c, k_logits_tile<1, EXACT>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
 }
 
 }  // namespace
@@ -634,18 +634,18 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
     const unsigned grid = (unsigned)((chains + 7) / 8);
     return launch(c, "router_logits_chain8", [&] {
       if (vec)
-        k_logits_chain8<true><<<grid, 128, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
+        go(c, k_logits_chain8<true>, dim3(grid), dim3(128), 0, d_w, d_x, T, E, H, d_out);
       else
-        k_logits_chain8<false><<<grid, 128, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
+        go(c, k_logits_chain8<false>, dim3(grid), dim3(128), 0, d_w, d_x, T, E, H, d_out);
     });
   }
   if (dot) {
     const int bt = T == 1 ? 1 : (T <= 4 ? 4 : 8);
     const dim3 grid(E, (T + bt - 1) / bt);
     return launch(c, "router_logits_dot", [&] {
-      if (bt == 1) k_logits_dot<1, true><<<grid, 256, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
-      else if (bt == 4) k_logits_dot<4, true><<<grid, 256, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
-      else k_logits_dot<8, true><<<grid, 256, 0, c->stream>>>(d_w, d_x, T, E, H, d_out);
+      if (bt == 1) go(c, k_logits_dot<1, true>, dim3(grid), dim3(256), 0, d_w, d_x, T, E, H, d_out);
+      else if (bt == 4) go(c, k_logits_dot<4, true>, dim3(grid), dim3(256), 0, d_w, d_x, T, E, H, d_out);
+      else go(c, k_logits_dot<8, true>, dim3(grid), dim3(256), 0, d_w, d_x, T, E, H, d_out);
     });
   }
   // chains per lane: as many as keep at least 1024 waves in the grid
@@ -665,7 +665,7 @@ int launch_block_prologue(nx_ctx *c, const float *d_x, const float *d_nw, float 
     return fail(NX_ERR_UNSUPPORTED, "block prologue: row shape or alignment not supported");
   const dim3 grid((unsigned)((E + 7) / 8), (unsigned)T);
   return launch(c, "block_prologue", [&] {
-    k_block_prologue<<<grid, 256, 0, c->stream>>>(d_x, d_nw, eps, d_w, E, H, d_xn, d_logits);
+    go(c, k_block_prologue, dim3(grid), dim3(256), 0, d_x, d_nw, eps, d_w, E, H, d_xn, d_logits);
   });
 }
 
@@ -680,9 +680,9 @@ int launch_sumsq_exact(nx_ctx *c, const float *d_x, int T, int H, float *d_out) 
   const unsigned grid = (unsigned)((T + 7) / 8);
   return launch(c, "rms_sumsq_chain8", [&] {
     if (vec)
-      k_logits_chain8<true, true><<<grid, 128, 0, c->stream>>>(d_x, d_x, T, 1, H, d_out);
+      go(c, k_logits_chain8<true, true>, dim3(grid), dim3(128), 0, d_x, d_x, T, 1, H, d_out);
     else
-      k_logits_chain8<false, true><<<grid, 128, 0, c->stream>>>(d_x, d_x, T, 1, H, d_out);
+      go(c, k_logits_chain8<false, true>, dim3(grid), dim3(128), 0, d_x, d_x, T, 1, H, d_out);
   });
 }
 

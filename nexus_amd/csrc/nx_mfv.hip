@@ -436,16 +436,16 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
                     (unsigned)nks);
     if (gateup) {
       NX_TRY(launch(c, "mfv_gateup",
-                    [&] { hipLaunchKernelGGL(k_mfv<true>, grid, dim3(256), 0, c->stream, a); }));
+                    [&] { go(c, k_mfv<true>, grid, dim3(256), 0, a); }));
       const size_t n = pairs * F;
       unsigned gs = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
       NX_TRY(launch(c, "mfv_swiglu", [&] {
-        hipLaunchKernelGGL(k_mfv_swiglu, dim3(gs), dim3(256), 0, c->stream, gpart, nks_g,
+        go(c, k_mfv_swiglu, dim3(gs), dim3(256), 0, gpart, nks_g,
                            pairs * 2 * F, (int)pairs, F, act, F);
       }));
     } else {
       NX_TRY(launch(c, "mfv_down",
-                    [&] { hipLaunchKernelGGL(k_mfv<false>, grid, dim3(256), 0, c->stream, a); }));
+                    [&] { go(c, k_mfv<false>, grid, dim3(256), 0, a); }));
     }
   }
   return launch_combine(c, ypart, p.rw, p.rcnt, p.inv, p.T, p.k, H, false, p.out, nks_d,

@@ -95,7 +95,7 @@ int launch_rms_apply(nx_ctx *c, const float *d_x, const float *d_sumsq, const fl
   if (T <= 0 || H <= 0) return NX_OK;
   const dim3 grid((H + 1023) / 1024, T);
   return launch(c, "rms_apply", [&] {
-    k_rms_apply<<<grid, 256, 0, c->stream>>>(d_x, d_sumsq, d_w, eps, H, d_out);
+    go(c, k_rms_apply, dim3(grid), dim3(256), 0, d_x, d_sumsq, d_w, eps, H, d_out);
   });
 }
 
@@ -103,7 +103,7 @@ int launch_rms_fast(nx_ctx *c, const float *d_x, const float *d_w, float eps, in
                     float *d_out) {
   if (T <= 0 || H <= 0) return NX_OK;
   return launch(c, "rms_fast", [&] {
-    k_rms_fast<<<T, 1024, 0, c->stream>>>(d_x, d_w, eps, H, d_out);
+    go(c, k_rms_fast, dim3(T), dim3(1024), 0, d_x, d_w, eps, H, d_out);
   });
 }
 

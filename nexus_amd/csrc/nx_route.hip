@@ -467,7 +467,7 @@ int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int scor
   const int epl = (E + 63) / 64;
 #define NX_ROUTE(N)                                                                        \
   return launch(c, "route_topk", [&] {                                                     \
-    k_route<N><<<g, 256, 0, c->stream>>>(d_logits, T, E, k, score_mode, d_expert, d_weight, \
+    go(c, k_route<N>, dim3(g), dim3(256), 0, d_logits, T, E, k, score_mode, d_expert, d_weight, \
                                          d_count);                                          \
   })
   if (epl <= 1) NX_ROUTE(1);
@@ -488,7 +488,7 @@ int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, i
   if (W < 1) W = 1;
   while (W & (W - 1)) W &= W - 1;  // a power of two: rows are scanned within a wave
   return launch(c, "permute", [&] {
-    k_permute<<<1, PERM_THREADS, 0, c->stream>>>(d_expert, d_count, T, k, E, W,
+    go(c, k_permute, dim3(1), dim3(PERM_THREADS), 0, d_expert, d_count, T, k, E, W,
                                                  tile_m > 0 ? tile_m : 1, d_ecount, d_offsets,
                                                  d_ptok, d_pslot, d_inv, d_active, d_tiles,
                                                  shared_T);
@@ -513,7 +513,7 @@ int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, 
   const int tm = tile_m > 0 ? tile_m : 1;
 #define NX_RP(N)                                                                              \
   return launch(c, "route_permute", [&] {                                                     \
-    k_route_permute<N><<<1, RP_THREADS, 0, c->stream>>>(d_logits, T, E, k, score_mode, d_expert, \
+    go(c, k_route_permute<N>, dim3(1), dim3(RP_THREADS), 0, d_logits, T, E, k, score_mode, d_expert, \
                                                         d_weight, d_count, d_ecount, d_offsets,  \
                                                         d_ptok, d_pslot, d_inv, d_active, tm,    \
                                                         d_tiles, d_counters, nc);                \
@@ -535,39 +535,39 @@ int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const
   const int nchunk = (H / 4 + 255) / 256;
   if (H % 4 == 0 && al16(d_ypair) && al16(d_out) && al16(d_residual) &&
       (size_t)T * nchunk < (1u << 31)) {
-    auto go4 = [&](auto kern) {
+    auto run4 = [&](auto kern) {
       return launch(c, "combine", [&] {
-        kern<<<(unsigned)(T * nchunk), 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T,
+        go(c, kern, dim3((unsigned)(T * nchunk)), dim3(256), 0, d_ypair, d_weight, d_count, d_inv, T,
                                                             k, H, sh, d_out, ns, split_stride,
                                                             d_residual, nchunk);
       });
     };
     if (ns == 1) {
-      if (k <= 2) return go4(k_combine4<1, 2>);
-      if (k <= 4) return go4(k_combine4<1, 4>);
-      return go4(k_combine4<1, 8>);
+      if (k <= 2) return run4(k_combine4<1, 2>);
+      if (k <= 4) return run4(k_combine4<1, 4>);
+      return run4(k_combine4<1, 8>);
     }
-    if (k <= 2) return go4(k_combine4<0, 2>);
-    if (k <= 4) return go4(k_combine4<0, 4>);
-    return go4(k_combine4<0, 8>);
+    if (k <= 2) return run4(k_combine4<0, 2>);
+    if (k <= 4) return run4(k_combine4<0, 4>);
+    return run4(k_combine4<0, 8>);
   }
   size_t g = (total + 255) / 256;
   if (g > 65536) g = 65536;
-  auto go = [&](auto kern) {
+  auto run1 = [&](auto kern) {
     return launch(c, "combine", [&] {
-      kern<<<(unsigned)g, 256, 0, c->stream>>>(d_ypair, d_weight, d_count, d_inv, T, k, H, sh,
+      go(c, kern, dim3((unsigned)g), dim3(256), 0, d_ypair, d_weight, d_count, d_inv, T, k, H, sh,
                                                d_out, ns, split_stride, d_residual);
     });
   };
   // routes read together: top-k up to 2, 4, else 8 at a time
   if (ns == 1) {
-    if (k <= 2) return go(k_combine<1, 2>);
-    if (k <= 4) return go(k_combine<1, 4>);
-    return go(k_combine<1, 8>);
+    if (k <= 2) return run1(k_combine<1, 2>);
+    if (k <= 4) return run1(k_combine<1, 4>);
+    return run1(k_combine<1, 8>);
   }
-  if (k <= 2) return go(k_combine<0, 2>);
-  if (k <= 4) return go(k_combine<0, 4>);
-  return go(k_combine<0, 8>);
+  if (k <= 2) return run1(k_combine<0, 2>);
+  if (k <= 4) return run1(k_combine<0, 4>);
+  return run1(k_combine<0, 8>);
 }
 
 }  // namespace nx
