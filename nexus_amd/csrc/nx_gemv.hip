@@ -1008,6 +1008,17 @@ bool choose_tokens_shape(int nseg, int eps, int T, int *nt, Shape *s) {
   return choose_shape(nseg, eps, 1, s);
 }
 
+// Rows per row group, from rpg up, for which the grid of ceil(rows / (rpg *
+// gpw)) x grid_y workgroups fits `cap` resident workgroups (or rpg itself
+// when no length does).
+long fit_one_round(long rows, long rpg, int gpw, long grid_y, long cap) {
+  for (long r = rpg; r <= rows; ++r) {
+    if ((rows + r * gpw - 1) / (r * gpw) * grid_y <= cap) return r;
+    if ((rows + r * gpw - 1) / (r * gpw) == 1) break;
+  }
+  return rpg;
+}
+
 // partial sums of the down kernel stay in LDS up to this size per workgroup
 constexpr size_t kDownLdsMax = 64 * 1024;
 
@@ -1124,6 +1135,11 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const long groups = (long)c->num_cu * wg_per_cu * groups_per_wg;
   long rpg = (work_rows + groups - 1) / groups;
   if (rpg < 1) rpg = 1;
+  // whole row blocks per slot round the grid up: lengthen the runs until
+  // it fits one round (a workgroup left over for a second round runs alone
+  // and nearly doubles the launch)
+  const long grid_y = per_slot ? (long)slots_max * kslices : 1;
+  rpg = fit_one_round(rows, rpg, groups_per_wg, grid_y, (long)c->num_cu * wg_per_cu);
   a.rows_per_group = (int)rpg;
   a.row_interleave = NX_GEMV_INTERLEAVE;
   a.groups_per_wg = groups_per_wg;
@@ -1233,6 +1249,7 @@ int run_gemv_matrix(nx_ctx *c, int fmt, const RolePlane &pl, const float *x, int
   const long groups = (long)c->num_cu * wg_per_cu * groups_per_wg;
   long rpg = (pl.rows + groups - 1) / groups;
   if (rpg < 1) rpg = 1;
+  rpg = fit_one_round(pl.rows, rpg, groups_per_wg, 1, (long)c->num_cu * wg_per_cu);
   a.rows_per_group = (int)rpg;
   a.row_interleave = NX_GEMV_INTERLEAVE;
   a.groups_per_wg = groups_per_wg;
