@@ -3,9 +3,9 @@
 // itself instead of waiting on a router launch).
 //
 // InferenceEngine::route_moe_experts (src/engine/mod.rs:918-966): each finite
-// logit becomes a 64-bit key (total-order-sortable f32 bits << 32 | ~expert),
-// so a wave-wide max picks the largest logit and, among identical bit
-// patterns, the lowest expert index; non-finite logits are never selected.
+// logit becomes a 32-bit total-order-sortable key, a wave-wide max picks the
+// largest logit and a ballot of its holders the lowest expert index among
+// identical bit patterns; non-finite logits are never selected.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -27,69 +27,78 @@ __device__ __forceinline__ float unsortable(uint32_t s) {
 // v of another lane of the same 16-lane row, by a DPP lane pattern (every
 // lane reads a lane inside its row, so none reads out of range)
 template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
-  return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
 }
-
-__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
-  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
-  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
-  return ((uint64_t)hi << 32) | lo;
-}
-
-__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 // maximum over the wave, in every lane: within each 16-lane row by DPP
 // (swap neighbours, swap pairs, mirror halves of 8, mirror the row), then
 // across the four rows from lanes 0, 16, 32, 48
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  v = max_u64(v, dpp_u64<0xB1>(v));   // quad_perm [1, 0, 3, 2]
-  v = max_u64(v, dpp_u64<0x4E>(v));   // quad_perm [2, 3, 0, 1]
-  v = max_u64(v, dpp_u64<0x141>(v));  // row_half_mirror
-  v = max_u64(v, dpp_u64<0x140>(v));  // row_mirror
-  return max_u64(max_u64(readlane_u64(v, 0), readlane_u64(v, 16)),
-                 max_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = max(v, dpp_u32<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = max(v, dpp_u32<0x141>(v));  // row_half_mirror
+  v = max(v, dpp_u32<0x140>(v));  // row_mirror
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
 }
 
 // Routes one token with one wavefront.  On return lane r < *n holds the r-th
 // route (expert *e, weight *w); lanes >= *n hold e = -1, w = 0.  With
 // weights false (wave-uniform) only the selection is made and *w is 0.
+//
+// Expert lane + 64 i keeps key[i] = the total-order-sortable bits of its
+// logit (0 for a non-finite logit, a value no finite logit maps to).  Each
+// selection takes the wave's largest key, then, among the experts holding
+// exactly that key, the lowest index (the first set bit of the lowest
+// non-empty ballot): the stable descending sort of the reference.
 template <int EPL>
 __device__ __forceinline__ void route_one(const float *__restrict__ row, int E, int k,
                                           int score_mode, int lane, int *e_out, float *w_out,
                                           int *n_out, bool weights = true) {
-  uint64_t key[EPL];
+  uint32_t key[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int e = lane + 64 * i;
     key[i] = 0;
     if (e < E) {
       const float l = row[e];
-      if (isfinite(l)) key[i] = ((uint64_t)sortable(l) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)e);
+      if (isfinite(l)) key[i] = sortable(l);
     }
   }
   const int kk = k < E ? k : E;
-  uint64_t mine = 0;  // lane r keeps the r-th selection
+  uint32_t mine = 0;  // lane r keeps the r-th selection: its key and expert
+  int mine_e = -1;
   int n = 0;
   for (int r = 0; r < kk; ++r) {
-    uint64_t best = 0;
+    uint32_t best = key[0];
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) best = key[i] > best ? key[i] : best;
-    best = wave_max_u64(best);
+    for (int i = 1; i < EPL; ++i) best = max(best, key[i]);
+    best = wave_max_u32(best);
     if (best == 0) break;  // no finite logits left (uniform across the wave)
+    int win = -1;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const unsigned long long m = __ballot(key[i] == best);
+      if (win < 0 && m != 0ull) win = 64 * i + (int)__builtin_ctzll(m);
+    }
 #pragma unroll
     for (int i = 0; i < EPL; ++i)
-      if (key[i] == best) key[i] = 0;
-    if (lane == r) mine = best;
+      if (win == lane + 64 * i) key[i] = 0;
+    if (lane == r) {
+      mine = best;
+      mine_e = win;
+    }
     ++n;
   }
   float l = 0.f, w = 0.f;
   int e = -1;
   if (lane < n) {
-    l = unsortable((uint32_t)(mine >> 32));
-    e = (int)(0xFFFFFFFFu - (uint32_t)mine);
+    l = unsortable(mine);
+    e = mine_e;
   }
   *e_out = e;
   *n_out = n;
