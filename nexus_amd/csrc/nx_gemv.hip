@@ -62,6 +62,11 @@
 #ifndef NX_GEMV_PLAIN_ROWS
 #define NX_GEMV_PLAIN_ROWS 2
 #endif
+// most slots (active experts + shared) the down pass combines inside its
+// workgroups; more go through the per-slot kernel and the combine kernel
+#ifndef NX_GEMV_COMBINE_SLOTS
+#define NX_GEMV_COMBINE_SLOTS 2
+#endif
 // cache policy of the weight-code loads (2: non-temporal, streamed past the
 // caches so the small activation and route arrays stay resident)
 #ifndef NX_GEMV_WEIGHT_CPOL
@@ -1114,7 +1119,7 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   // side by side); beyond that, and for K slices, the slots go to grid.y like
   // gate/up, each writing its rows per pair, and the combine runs as its own
   // kernel.
-  const bool down_rows = !gateup && (down_split || slots_max_of(ex, p) > DOWN_SG);
+  const bool down_rows = !gateup && (down_split || slots_max_of(ex, p) > NX_GEMV_COMBINE_SLOTS);
   const int kind = gateup ? KIND_GATEUP : (down_rows ? KIND_DOWN_ROWS : KIND_DOWN_COMBINE);
   const bool per_slot = gateup || down_rows;
   // residency is register-bound (eight waves per CU by launch bounds)
