@@ -94,9 +94,23 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
   for (int e = tid; e < E; e += PERM_THREADS) cnt[e] = 0;
   __syncthreads();
   const int pairs = T * k;
-  for (int i = tid; i < pairs; i += PERM_THREADS) {
-    const int t = i / k, r = i - t * k;
-    if (r < rcnt[t]) atomicAdd(&cnt[rexp[i]], 1);
+  // PERM_HB pairs per thread at a time: their route and count loads all go
+  // out before the first is used (no dependent round trip per pair)
+  constexpr int PERM_HB = 8;
+  for (int i0 = tid; i0 < pairs; i0 += PERM_HB * PERM_THREADS) {
+    int ev[PERM_HB], nv[PERM_HB], rv[PERM_HB];
+#pragma unroll
+    for (int j = 0; j < PERM_HB; ++j) {
+      const int i = i0 + j * PERM_THREADS;
+      const int ic = i < pairs ? i : 0;
+      const int t = ic / k;
+      rv[j] = i < pairs ? ic - t * k : k;  // slot (k: no pair)
+      ev[j] = rexp[ic];
+      nv[j] = rcnt[t];
+    }
+#pragma unroll
+    for (int j = 0; j < PERM_HB; ++j)
+      if (rv[j] < nv[j]) atomicAdd(&cnt[ev[j]], 1);
   }
   __syncthreads();
   // E <= PERM_THREADS: one expert per thread
@@ -495,11 +509,14 @@ int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, i
   });
 }
 
+#ifndef NX_RP_TOKENS_PER_WAVE
+#define NX_RP_TOKENS_PER_WAVE 2
+#endif
 bool route_permute_fusable(int T, int E, int k) {
-  // each wave routes its tokens one after another: beyond two per wave the
+  // each wave routes its tokens one after another: beyond a few per wave the
   // router kernel, spread over the chip, is faster
-  return T >= 1 && T <= 2 * (RP_THREADS / 64) && (long)T * k <= RP_MAX_PAIRS && E <= 256 &&
-         k <= 64;
+  return T >= 1 && T <= NX_RP_TOKENS_PER_WAVE * (RP_THREADS / 64) &&
+         (long)T * k <= RP_MAX_PAIRS && E <= 256 && k <= 64;
 }
 
 int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
