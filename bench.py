@@ -285,6 +285,11 @@ def prefill(nx, ctx, torch, args):
     kern = kernel_means(ctx, torch, step, args.prefill_steps)
     gemm_ms = kern.get("gemm_gateup", 0.0) + kern.get("gemm_down", 0.0)
     ex.close()
+    # the vendor library's dense bf16 GEMM on the same products, for scale:
+    # the most loaded expert's gate+up and down, and all tokens as one dense
+    # expert
+    lib = library_gemm_reference(torch, [(counts[0], 2 * F, H), (counts[0], H, F),
+                                         (T, 2 * F, H), (T, H, F)])
     return {
         "workload": "Mixtral-8x7B MoE layer, prefill, Q8_0, Zipf(1.2) router",
         "tokens": T, "path": f"{args.prefill_path}: {path_of(kern)}", "expert_tokens": counts,
@@ -293,7 +298,30 @@ def prefill(nx, ctx, torch, args):
         "gemm_TFLOPs": flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms else None,
         "gemm_frac_of_fp16_peak": flops / (gemm_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS if gemm_ms else None,
         "kernels_ms": {k_: round(v, 4) for k_, v in kern.items()},
+        "torch_bf16_matmul_TFLOPs": lib,
     }
+
+
+def library_gemm_reference(torch, shapes, iters=20):
+    """TFLOP/s of torch.matmul (hipBLASLt) on dense bf16 operands of shape
+    [M x K] . [K x N] for each (M, N, K): what the vendor library sustains on
+    the plain product, with no dequantization and no grouping."""
+    dev = torch.device("cuda", 0)
+    res = {}
+    for M, N, K in shapes:
+        a = torch.randn((M, K), device=dev, dtype=torch.bfloat16)
+        b = torch.randn((K, N), device=dev, dtype=torch.bfloat16)
+        for _ in range(3):
+            c = a @ b
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            c = a @ b
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / iters
+        res[f"{M}x{N}x{K}"] = round(2.0 * M * N * K / dt / 1e12, 1)
+        del a, b, c
+    return res
 
 
 MODEL_CONFIGS = [
