@@ -560,8 +560,13 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   constexpr int L = LPR * KSPLIT;
   constexpr int GROUPS = 256 / L;
   constexpr int NMAT = PLAIN ? 1 : 2;
-  // rows per pipeline stage: one matrix leaves the registers for twice the rows
-  constexpr int U = PLAIN && SPL == 1 && L == 64 ? NX_GEMV_PLAIN_ROWS : 2;
+  // rows per pipeline stage: one matrix leaves the registers for twice the
+  // rows; two tokens' activations in registers (no shared LDS operands, or
+  // two segments per lane) leave room for one row per stage (two rows
+  // spilled, and one is faster: Qwen3 gate/up at 2 tokens 20.5 -> 16.4 us)
+  constexpr int U = PLAIN && SPL == 1 && L == 64 ? NX_GEMV_PLAIN_ROWS
+                    : (!PLAIN && NT == 2 && (L < 64 || SPL == 2)) ? 1
+                                                                  : 2;
   // stages (S - 1 of them in flight while one is decoded)
   constexpr int S = PLAIN ? NX_GEMV_PLAIN_STAGES : (NT == 1 && SPL == 1 ? NX_GEMV_GATEUP_STAGES : 2);
   using RG = RowGroup<FMT, L, SPL, NT, U, NMAT>;
