@@ -141,6 +141,34 @@ def test_moe_block_exact_prologue(ctx, fmt, E, H, F, k, T):
     ex.close()
 
 
+def test_moe_block_exact_prologue_special_rows(ctx):
+    """Rows that stress the prologue's sum of squares: dyadic values (squares
+    that land exactly halfway between representable sums), magnitudes across
+    the exponent range (the running sum changes binade many times), tiny
+    values (subnormal squares), zeros, and a square near the top of the
+    float range (the sum overflows to inf, rstd becomes 0).  Normalised rows
+    and logits must stay the oracle's, so the block output is bit-identical
+    to hidden + the layer on the oracle's normalised rows."""
+    E, H, F, k = 8, 1536, 128, 2
+    T = 6
+    L, hidden, norm_w, router = block_case(Q8_0, E, H, F, k, T, seed=97)
+    rng = np.random.default_rng(98)
+    hidden[1] = rng.integers(-12, 13, H).astype(np.float32) / 8
+    hidden[2] = (rng.standard_normal(H) * 10.0 ** rng.integers(-12, 12, H)).astype(np.float32)
+    hidden[3] = (rng.standard_normal(H) * 1e-23).astype(np.float32)
+    hidden[4] = 0.0
+    hidden[5, :] = rng.standard_normal(H).astype(np.float32)
+    hidden[5, 100] = np.float32(3e19)
+    eps = 1e-6
+    normed, logits, _ = oracle_block(L, hidden, norm_w, eps, router)
+    assert np.all(np.isfinite(normed)) and np.all(np.isfinite(logits))
+    ex = L.upload(nx, ctx)
+    got = ex.block(hidden, norm_w, eps, router, k, path=nx.PATH_GEMV, exact=True)
+    want = (hidden + ex.forward(normed, logits, k, path=nx.PATH_GEMV)).astype(np.float32)
+    assert_same_bits(got, want)
+    ex.close()
+
+
 def test_moe_block_mfma_residual(ctx):
     E, H, F, k, T = 8, 512, 512, 2, 192
     L, hidden, norm_w, router = block_case(Q8_0, E, H, F, k, T, seed=31, shared_F=512)
