@@ -226,6 +226,11 @@ MFMA_TOL = 1e-2
     (F32, 8, 512, 1024, 2, 64, None),
     (Q4_K, 32, 256, 512, 4, 77, None),
     (Q8_0, 4, 256, 320, 1, 129, None),   # F not a multiple of the 128-row tile
+    # a hundred or more pairs per expert: several M-tiles per expert, full
+    # and partial, with Zipf-skewed counts and rows not a multiple of 128
+    (Q8_0, 4, 512, 640, 2, 700, 1.2),
+    (Q4_K, 4, 512, 768, 2, 600, None),
+    (Q4_0, 2, 256, 320, 1, 400, None),
 ])
 def test_layer_mfma_parity(ctx, path, fmt, E, H, F, k, T, zipf):
     L = Layer(fmt, E, H, F, k, T, seed=3 * E + H + F + T, zipf=zipf)
@@ -239,6 +244,10 @@ def test_layer_mfma_shared_expert_sigmoid(ctx):
     L = Layer(Q4_K, 16, 512, 512, 4, 96, seed=5, shared_F=512, score_mode=1)
     say("layer mfma shared + sigmoid")
     assert rel_l2(run_layer(ctx, L, nx.PATH_MFMA_F16), L.oracle_out()) <= MFMA_TOL
+    # the shared expert's 300 tokens over three M-tiles, the last partial
+    L = Layer(Q4_K, 4, 512, 512, 2, 300, seed=6, shared_F=512, score_mode=1)
+    say("layer mfma shared + sigmoid, many pairs per expert")
+    assert rel_l2(run_layer(ctx, L, nx.PATH_MFMA_BF16), L.oracle_out()) <= MFMA_TOL
 
 
 @pytest.mark.parametrize("fmt", [Q8_0, Q4_K])
