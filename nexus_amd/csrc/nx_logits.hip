@@ -29,12 +29,16 @@
 //                    4 instructions per 32 columns instead of 32, so a chain
 //                    advances one dependent add per instruction slot (about
 //                    4.4 clocks: a chain's latency is ~H * 1.9 ns).
-//   k_logits_tile    exact or fast, many chains (prefill).  A workgroup owns a
-//                    tile of tokens x experts, each lane a register block of
+//   k_logits_tile    exact, many chains (prefill).  A workgroup owns a tile
+//                    of tokens x experts, each lane a register block of
 //                    chains, with both operands staged through an LDS ring.
 //   k_logits_dot     fast, few tokens.  A workgroup per (expert, block of
 //                    tokens) strides over the row in 16-byte loads and reduces
 //                    with DPP and LDS.
+//   Fast mode with more tokens is a plain f32 GEMM (rocBLAS sgemm on the
+//   matrix cores).
+#include <rocblas/rocblas.h>
+
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 
@@ -436,10 +440,10 @@ constexpr int TL_NS = 3;  // ring stages of the tiled kernel
 // e0 + RB (l % 16) + j.  Columns are staged KC = 128 / RB at a time (512
 // 16-byte units per operand and stage) in an LDS ring filled by DMA; unit u
 // of row r sits at r * (KC / 4) + (u ^ (r & 7)), so the rows a wave reads at
-// one column spread over the banks.  Each chain is summed in column order,
-// exact mode with separately rounded products and sums, fast mode with fma.
+// one column spread over the banks.  Each chain is summed in column order
+// with separately rounded products and sums (exact mode).
 // Requires H % 4 == 0 and 16-byte aligned rows.
-template <int RB, bool EXACT>
+template <int RB>
 __global__ __launch_bounds__(256) void k_logits_tile(const float *__restrict__ W,
                                                      const float *__restrict__ X, int T, int E,
                                                      int H, float *__restrict__ out) {
@@ -528,10 +532,7 @@ __global__ __launch_bounds__(256) void k_logits_tile(const float *__restrict__ W
           for (int j = 0; j < RB; ++j) {
             const float xk = kk == 0 ? xv[i].x : kk == 1 ? xv[i].y : kk == 2 ? xv[i].z : xv[i].w;
             const float wk = kk == 0 ? wv[j].x : kk == 1 ? wv[j].y : kk == 2 ? wv[j].z : wv[j].w;
-            if constexpr (EXACT)
-              s[i][j] = s[i][j] + wk * xk;
-            else
-              s[i][j] = __builtin_fmaf(wk, xk, s[i][j]);
+            s[i][j] = s[i][j] + wk * xk;
           }
     }
   };
@@ -604,17 +605,36 @@ __global__ __launch_bounds__(256) void k_logits_dot(const float *__restrict__ W,
   }
 }
 
-template <bool EXACT>
 void launch_tile(nx_ctx *c, int rb, const float *W, const float *X, int T, int E, int H,
                  float *out) {
   const int rows = 16 * rb;
   const dim3 grid((E + rows - 1) / rows, (T + rows - 1) / rows);
-  if (rb == 4) go(c, k_logits_tile<4, EXACT>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
-  else if (rb == 2) go(c, k_logits_tile<2, EXACT>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
-  else go(c, k_logits_tile<1, EXACT>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
+  if (rb == 4) go(c, k_logits_tile<4>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
+  else if (rb == 2) go(c, k_logits_tile<2>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
+  else go(c, k_logits_tile<1>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
+}
+
+// the context's rocBLAS handle, created on first use on the context's device
+int blas_handle(nx_ctx *c) {
+  if (c->blas) return NX_OK;
+  NX_HIP(hipSetDevice(c->device));
+  rocblas_handle h = nullptr;
+  if (rocblas_create_handle(&h) != rocblas_status_success)
+    return fail(NX_ERR_DEVICE, "rocblas_create_handle failed");
+  if (rocblas_set_stream(h, c->stream) != rocblas_status_success) {
+    (void)rocblas_destroy_handle(h);
+    return fail(NX_ERR_DEVICE, "rocblas_set_stream failed");
+  }
+  c->blas = h;
+  return NX_OK;
 }
 
 }  // namespace
+
+void release_blas(nx_ctx *c) {
+  if (c->blas) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(c->blas));
+  c->blas = nullptr;
+}
 
 // chains (token, expert pairs) up to which the exact path uses k_logits_chain8
 constexpr long LOGITS_CHAIN8_MAX = 16384;
@@ -626,10 +646,11 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
   if (T <= 0 || E <= 0) return NX_OK;
   const bool vec = H % 4 == 0 && ((uintptr_t)d_w & 15) == 0 && ((uintptr_t)d_x & 15) == 0;
   const long chains = (long)T * E;
-  // the exact order is also a valid fast order: the chain kernel serves both
-  // modes up to LOGITS_CHAIN8_MAX chains, except fast mode's few-token case
+  // fast mode: few tokens on k_logits_dot, more on the GEMM below; the exact
+  // order is also a valid fast order, so the chain kernel serves rows it
+  // cannot load whole (unaligned, H % 4 != 0) in both modes
   const bool dot = !exact && vec && T <= LOGITS_DOT_MAX_T;
-  const bool chain8 = !vec || (!dot && chains <= LOGITS_CHAIN8_MAX);
+  const bool chain8 = !vec || (exact && chains <= LOGITS_CHAIN8_MAX);
   if (chain8) {
     const unsigned grid = (unsigned)((chains + 7) / 8);
     return launch(c, "router_logits_chain8", [&] {
@@ -648,14 +669,28 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
       else go(c, k_logits_dot<8, true>, dim3(grid), dim3(256), 0, d_w, d_x, T, E, H, d_out);
     });
   }
+  if (!exact) {
+    // Fast mode, more than a few tokens: logits = X . W^T is a plain f32
+    // GEMM, which rocBLAS runs on the matrix cores; any summation order is
+    // within fast mode's bound.  Column-major view: out^T (E x T, ld E) =
+    // W' (H x E, ld H) transposed times X' (H x T, ld H).
+    NX_TRY(blas_handle(c));
+    if (rocblas_set_stream(static_cast<rocblas_handle>(c->blas), c->stream) != rocblas_status_success)
+      return fail(NX_ERR_DEVICE, "rocblas_set_stream failed");
+    const float one = 1.0f, zero = 0.0f;
+    rocblas_status st = rocblas_status_success;
+    NX_TRY(launch(c, "router_logits_gemm", [&] {
+      st = rocblas_sgemm(static_cast<rocblas_handle>(c->blas), rocblas_operation_transpose,
+                         rocblas_operation_none, E, T, H, &one, d_w, H, d_x, H, &zero, d_out, E);
+    }));
+    if (st != rocblas_status_success)
+      return fail(NX_ERR_DEVICE, std::string("router logits GEMM: ") + rocblas_status_to_string(st));
+    return NX_OK;
+  }
   // chains per lane: as many as keep at least 1024 waves in the grid
   const int rb = chains >= 1024L * 64 * 16 ? 4 : (chains >= 1024L * 64 * 4 ? 2 : 1);
-  return launch(c, exact ? "router_logits_tile" : "router_logits_tile_fma", [&] {
-    if (exact)
-      launch_tile<true>(c, rb, d_w, d_x, T, E, H, d_out);
-    else
-      launch_tile<false>(c, rb, d_w, d_x, T, E, H, d_out);
-  });
+  return launch(c, "router_logits_tile",
+                [&] { launch_tile(c, rb, d_w, d_x, T, E, H, d_out); });
 }
 
 int launch_block_prologue(nx_ctx *c, const float *d_x, const float *d_nw, float eps,
