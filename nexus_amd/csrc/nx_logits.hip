@@ -292,64 +292,41 @@ __global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__
 
 // The exact prologue of one MoE block (RMSNorm, then the router logits of
 // the normalised row) in one launch: workgroup (g, t) takes token t and
-// experts 8g .. 8g+7, 256 threads.  Requires H % 4 == 0, H <= BP_MAXH and
-// 16-byte aligned rows.
-//  1. Row t goes to LDS, and its squares (separately rounded) with it.
-//  2. Wave 0 adds the squares in column order, reading them from LDS
-//     (every lane the same chain; four columns per 16-byte read, the reads
-//     of the next 32 columns in flight during the adds), while waves 1-3 pull
-//     the group's router rows into the cache.  rstd = 1 / sqrt(sum / H + eps).
-//     A chain's adds are dependent: about 8 clocks each, the same with only
-//     one quarter of the wave's lanes active, so the two chains (4096
-//     columns each at H = 4096) are the kernel's floor.
-//  3. Every thread forms its columns of the normalised row, (x_i rstd) w_i,
-//     into LDS and to xn (each workgroup of a token writes the same values).
-//  4. The group's chains: waves 1-3 form the products W[e][c] * xn[c] of
-//     512 columns at a time into one of two LDS buffers while wave 0 adds the
-//     previous 512 in column order (lane 8 m + j: chain m); one barrier per
-//     512 columns.
+// experts 8g .. 8g+7, four waves, two router chains per wave (one per 32-lane
+// half); every wave also runs the sum of squares itself.  Requires
+// H % 4 == 0, H <= BP_MAXH and 16-byte aligned rows.
+//
+// A sequential f32 sum is bound by its dependent adds, and it reaches that
+// bound only when every operand is already in a register: reading operands
+// from LDS or memory while the chain runs roughly doubles its time.  So each
+// chain is cut into runs of BP_RUN consecutive columns, run r held in the
+// registers of lane r of the chain's 32 lanes, loaded and formed before the
+// chain starts.  Every lane adds its run to the chain's value on entry (one
+// instruction advances all lanes); the value lane r ends with is the chain's
+// value after run r, read out with readlane and handed to run r + 1.  The
+// adds are those of a left-to-right sum, so the result is bit-identical to
+// the column-order chain.
+//
+// Rows reach the runs through LDS: coalesced 16-byte loads, stored run by
+// run with one float4 of padding per run (BP_RUN4 + 1 float4 apart), so the
+// lanes reading their runs' k-th float4 hit different banks.
+//  1. Each wave stages its two router rows in its own LDS buffers; the row
+//     (x) goes to a shared buffer, zero-padded to 32 runs, and each thread
+//     keeps its share of the row and of the norm weight in registers.
+//  2. The sum of squares: 64 runs of BP_RUN / 2 columns, run r in lane r
+//     (runs past the row end are skipped; a partial last run adds +0 to a
+//     sum that started at +0, which leaves it unchanged).
+//     rstd = 1 / sqrt(sum / H + eps).
+//  3. Each thread forms its share of the normalised row, (x_i rstd) w_i,
+//     into the shared buffer (workgroup 0 also writes it to xn); each lane
+//     then forms the products W[e][i] xn_i of its run.
+//  4. The router chains, run r of half h in lane 32 h + r.
 // The arithmetic is that of the RMSNorm kernel and the chain kernel, so the
 // row and the logits are bit-identical to theirs.
-constexpr int BP_MAXH = 8192;
-constexpr int BP_CH = 512;  // columns per product buffer
-
-// s += v[0] + ... + v[7] (32 columns), in order
-__device__ __forceinline__ void add32(float &s, const float4 (&v)[8]) {
-#pragma clang fp contract(off)
-#pragma unroll
-  for (int m = 0; m < 8; ++m) {
-    s = s + v[m].x;
-    s = s + v[m].y;
-    s = s + v[m].z;
-    s = s + v[m].w;
-  }
-}
-
-// the column-order sum of n4 float4 (n4 % 8 == 0) at src, this lane's
-// 32-column reads one group ahead of its adds
-__device__ __forceinline__ float sum_ordered(const float4 *src, int n4, float s) {
-  float4 a[8], b[8];
-#pragma unroll
-  for (int m = 0; m < 8; ++m) a[m] = src[m];
-  for (int g = 0; g < n4; g += 16) {
-    if (g + 8 < n4) {
-#pragma unroll
-      for (int m = 0; m < 8; ++m) b[m] = src[g + 8 + m];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    add32(s, a);
-    __builtin_amdgcn_sched_barrier(0);
-    if (g + 8 >= n4) break;
-    if (g + 16 < n4) {
-#pragma unroll
-      for (int m = 0; m < 8; ++m) a[m] = src[g + 16 + m];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    add32(s, b);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  return s;
-}
+constexpr int BP_RUN = 128;              // columns per run of a router chain
+constexpr int BP_RUN4 = BP_RUN / 4;      // float4 per run
+constexpr int BP_MAXH = 32 * BP_RUN;     // 4096
+constexpr int BP_PAD4 = 32 * (BP_RUN4 + 1);  // padded row, in float4
 
 __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict__ x,
                                                         const float *__restrict__ nw, float eps,
@@ -357,80 +334,116 @@ __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict_
                                                         float *__restrict__ xn,
                                                         float *__restrict__ logits) {
 #pragma clang fp contract(off)
-  __shared__ float4 row4[BP_MAXH / 4];            // x, then the normalised row
-  __shared__ float4 prod4[2][8][BP_CH / 4];       // squares (flat), rstd, then products
-  float4 *sq4 = &prod4[0][0][0];                  // BP_MAXH / 4 float4
-  const int t = blockIdx.y, e0 = blockIdx.x * 8, tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int ne = min(8, E - e0);
+  constexpr int S4 = BP_RUN4 / 2;          // float4 per lane, sum of squares
+  constexpr int RJ = 32 * BP_RUN4 / 64;    // float4 per lane of a staged router row
+  constexpr int XJ = 32 * BP_RUN4 / 256;   // float4 per thread of the row
+  __shared__ float4 xs[BP_PAD4], ws[4][2][BP_PAD4];  // 152 KB
+  const int t = blockIdx.y, tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, half = lane >> 5, hl = lane & 31;
+  const int e0 = blockIdx.x * 8 + wave * 2;  // the wave's experts: e0 (half 0), e0 + 1
   const int H4 = H >> 2;
-  const int H4p = (H4 + 7) & ~7;                  // whole 32-column groups (zero padded)
-  const float4 *xr4 = reinterpret_cast<const float4 *>(x + (size_t)t * H);
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  // 1. the row and its squares
-  for (int i = tid; i < H4p; i += 256) {
-    const float4 v = i < H4 ? xr4[i] : z4;
-    row4[i] = v;
-    sq4[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
-  }
-  __syncthreads();
-  // 2. the sum of squares; the other waves touch the group's router rows
-  if (wave == 0) {
-    const float ss = sum_ordered(sq4, H4p, 0.f);
-    // (every lane of the wave has read its last squares)
-    if (lane == 0) sq4[0].x = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
-  } else if (wave > 0) {  // (index i = tid - 64 >= 0)
-    const float4 *w4 = reinterpret_cast<const float4 *>(W + (size_t)e0 * H);
-    uint32_t acc = 0;
-    for (int i = tid - 64; i < ne * H4; i += 192) {
-      const float4 v = w4[i];
-      acc ^= __float_as_uint(v.x) ^ __float_as_uint(v.w);
+  auto pad = [](int i) { return i + i / BP_RUN4; };  // float4 i of the row -> LDS slot
+  // 1. loads with indices clamped into the rows and values selected
+  // afterwards: no branches, so every load is issued before the first wait
+  float4 xv[XJ], nv[XJ];
+  {
+    const float4 *xr4 = reinterpret_cast<const float4 *>(x + (size_t)t * H);
+    const float4 *nw4 = reinterpret_cast<const float4 *>(nw);
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) {
+      const int i = min(j * 256 + tid, H4 - 1);
+      xv[j] = xr4[i];
+      nv[j] = nw4[i];
     }
-    asm volatile("" ::"v"(acc));  // the loads are kept for their cache fills
   }
-  __syncthreads();
-  const float r = sq4[0].x;
-  // 3. the normalised row
-  const float4 *nw4 = reinterpret_cast<const float4 *>(nw);
-  float4 *xo4 = reinterpret_cast<float4 *>(xn + (size_t)t * H);
-  for (int i = tid; i < H4; i += 256) {
-    const float4 v = row4[i], w = nw4[i];
-    const float4 o = make_float4((v.x * r) * w.x, (v.y * r) * w.y, (v.z * r) * w.z, (v.w * r) * w.w);
-    row4[i] = o;
-    if (blockIdx.x == 0) xo4[i] = o;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int e = e0 + h;
+    const float4 *r4 = reinterpret_cast<const float4 *>(W + (size_t)(e < E ? e : 0) * H);
+    float4 wr[RJ];
+#pragma unroll
+    for (int j = 0; j < RJ; ++j) wr[j] = r4[min(j * 64 + lane, H4 - 1)];
+#pragma unroll
+    for (int j = 0; j < RJ; ++j) {
+      const int i = j * 64 + lane;
+      float4 v = wr[j];
+      if (e >= E || i >= H4) v = z4;
+      ws[wave][h][pad(i)] = v;
+    }
   }
-  __syncthreads();
-  // 4. the router chains, 512 columns per step
-  const int nch = (H4 + BP_CH / 4 - 1) / (BP_CH / 4);
-  auto produce = [&](int k, int buf) {  // waves 1-3
-    for (int i = tid - 64; i < 8 * (BP_CH / 4); i += 192) {
-      const int m = i / (BP_CH / 4), c4 = i - m * (BP_CH / 4);
-      const int col4 = k * (BP_CH / 4) + c4;
-      float4 p = z4;
-      if (m < ne && col4 < H4) {
-        const float4 w = reinterpret_cast<const float4 *>(W + (size_t)(e0 + m) * H)[col4];
-        const float4 v = row4[col4];
-        p = make_float4(w.x * v.x, w.y * v.y, w.z * v.z, w.w * v.w);
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int i = j * 256 + tid;
+    if (i >= H4) xv[j] = z4;  // (the padding: zero squares and products)
+    xs[pad(i)] = xv[j];
+  }
+  __syncthreads();  // the row is in LDS
+  // 2. the sum of squares, run r (float4 S4 r .. of the row) in lane r
+  float ss = 0.f;
+  {
+    float4 q[S4];
+#pragma unroll
+    for (int k = 0; k < S4; ++k) {
+      const float4 v = xs[pad(lane * S4 + k)];
+      q[k] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+    }
+    const int nsq = (H4 + S4 - 1) / S4;
+    for (int r = 0; r < nsq; ++r) {
+      float a = ss;
+#pragma unroll
+      for (int k = 0; k < S4; ++k) {
+        a = a + q[k].x;
+        a = a + q[k].y;
+        a = a + q[k].z;
+        a = a + q[k].w;
       }
-      prod4[buf][m][c4] = p;
+      ss = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), r));
     }
-  };
-  if (wave > 0) produce(0, 0);
-  __syncthreads();
-  float s = 0.f;
-  for (int k = 0; k < nch; ++k) {
-    if (wave == 0) {
-      // the last buffer's columns past the row end are zero products; the
-      // chain adds them after its last column: s + 0 = s (s is never -0:
-      // it starts at +0)
-      s = sum_ordered(&prod4[k & 1][lane >> 3][0], BP_CH / 4, s);
-    } else if (wave > 0 && k + 1 < nch) {  // (index i = tid - 64 >= 0)
-      produce(k + 1, (k + 1) & 1);
-    }
-    __syncthreads();
   }
-  if (wave == 0 && (lane & 7) == 0 && (lane >> 3) < ne)
-    logits[(size_t)t * E + e0 + (lane >> 3)] = s;
+  const float rs = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
+  // 3. the normalised row (into the shared buffer once every wave has read
+  // its squares), then the products of each lane's run
+  __syncthreads();
+  {
+    float4 *xo4 = reinterpret_cast<float4 *>(xn + (size_t)t * H);
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) {
+      const int i = j * 256 + tid;
+      const float4 v = xv[j], w = nv[j];
+      const float4 o = make_float4((v.x * rs) * w.x, (v.y * rs) * w.y, (v.z * rs) * w.z,
+                                   (v.w * rs) * w.w);
+      xs[pad(i)] = o;
+      if (blockIdx.x == 0 && i < H4) xo4[i] = o;
+    }
+  }
+  __syncthreads();
+  float4 p[BP_RUN4];
+  {
+    const float4 *my = ws[wave][half];
+#pragma unroll
+    for (int k = 0; k < BP_RUN4; ++k) {
+      const int c = hl * (BP_RUN4 + 1) + k;
+      const float4 w = my[c], o = xs[c];
+      p[k] = make_float4(w.x * o.x, w.y * o.y, w.z * o.z, w.w * o.w);
+    }
+  }
+  // 4. the two router chains, run r of half h in lane 32 h + r
+  const int nrt = (H4 + BP_RUN4 - 1) / BP_RUN4;
+  float s0 = 0.f, s1 = 0.f;
+  for (int r = 0; r < nrt; ++r) {
+    float a = half ? s1 : s0;
+#pragma unroll
+    for (int k = 0; k < BP_RUN4; ++k) {
+      a = a + p[k].x;
+      a = a + p[k].y;
+      a = a + p[k].z;
+      a = a + p[k].w;
+    }
+    s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), r));
+    s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32 + r));
+  }
+  if (hl == 0 && e0 + half < E) logits[(size_t)t * E + e0 + half] = half ? s1 : s0;
 }
 
 constexpr int TL_NS = 3;  // ring stages of the tiled kernel
@@ -700,7 +713,7 @@ int launch_block_prologue(nx_ctx *c, const float *d_x, const float *d_nw, float 
     return fail(NX_ERR_UNSUPPORTED, "block prologue: row shape or alignment not supported");
   const dim3 grid((unsigned)((E + 7) / 8), (unsigned)T);
   return launch(c, "block_prologue", [&] {
-    go(c, k_block_prologue, dim3(grid), dim3(256), 0, d_x, d_nw, eps, d_w, E, H, d_xn, d_logits);
+    go(c, k_block_prologue, grid, dim3(256), 0, d_x, d_nw, eps, d_w, E, H, d_xn, d_logits);
   });
 }
 

@@ -113,10 +113,13 @@ def test_moe_block_exact(ctx, fmt, E, H, F, k, T, shared):
 
 
 @pytest.mark.parametrize("fmt,E,H,F,k,T", [
-    (Q4_K, 8, 4096, 256, 2, 1),    # Mixtral's width, one expert group
+    (Q4_K, 8, 4096, 256, 2, 1),    # Mixtral's width, one expert group: 32 runs of 128 columns
     (Q8_0, 20, 2048, 128, 4, 5),   # three expert groups, the last partial
     (Q8_0, 128, 1024, 64, 8, 2),   # sixteen groups per token
-    (Q8_0, 8, 10240, 64, 2, 2),    # a row wider than the one launch holds: three launches
+    (Q8_0, 12, 1056, 64, 2, 3),    # a partial last run
+    (Q8_0, 8, 4128, 64, 2, 3),     # just past the one launch's 4096 columns: three launches
+    (Q4_K, 12, 7168, 256, 2, 2),   # DeepSeek's width
+    (Q8_0, 8, 10240, 64, 2, 2),
     (Q8_0, 8, 512, 64, 2, 64)])    # the most tokens the single launch takes
 def test_moe_block_exact_prologue(ctx, fmt, E, H, F, k, T):
     """The exact block's prologue (one launch: the sum-of-squares chain, the
@@ -132,7 +135,7 @@ def test_moe_block_exact_prologue(ctx, fmt, E, H, F, k, T):
     got = ex.block(hidden, norm_w, eps, router, k, path=nx.PATH_GEMV, exact=True)
     ran = set(ctx.profile_stats())
     ctx.profile(False)
-    fused = H % 4 == 0 and H <= 8192
+    fused = H % 4 == 0 and H <= 4096
     assert ("block_prologue" in ran) == fused, ran
     assert ("rms_sumsq_chain8" in ran) == (not fused), ran
     want = (hidden + ex.forward(normed, logits, k, path=nx.PATH_GEMV)).astype(np.float32)
@@ -141,7 +144,8 @@ def test_moe_block_exact_prologue(ctx, fmt, E, H, F, k, T):
     ex.close()
 
 
-def test_moe_block_exact_prologue_special_rows(ctx):
+@pytest.mark.parametrize("H", [1536, 4096])
+def test_moe_block_exact_prologue_special_rows(ctx, H):
     """Rows that stress the prologue's sum of squares: dyadic values (squares
     that land exactly halfway between representable sums), magnitudes across
     the exponent range (the running sum changes binade many times), tiny
@@ -149,8 +153,9 @@ def test_moe_block_exact_prologue_special_rows(ctx):
     float range (the sum overflows to inf, rstd becomes 0).  Normalised rows
     and logits must stay the oracle's, so the block output is bit-identical
     to hidden + the layer on the oracle's normalised rows."""
-    E, H, F, k = 8, 1536, 128, 2
+    E, F, k = 8, 128, 2
     T = 6
+    print(f"block prologue special rows H={H}", flush=True)
     L, hidden, norm_w, router = block_case(Q8_0, E, H, F, k, T, seed=97)
     rng = np.random.default_rng(98)
     hidden[1] = rng.integers(-12, 13, H).astype(np.float32) / 8
