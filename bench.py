@@ -462,10 +462,11 @@ def model_config_cases(nx, ctx, torch, args, only=None):
                 tokens = (only[1],)
         print(f"bench: {name}", file=sys.stderr, flush=True)
         fmt = {"Q4_K": nx.Q4_K, "Q2_K": nx.Q2_K}[fname]
-        # GGUF bytes per weight; Q2_K stays resident with its codes widened
-        # to 4 bits (0.625 B/weight read per step)
+        # GGUF bytes per weight; Q2_K stays resident as 16 bytes of 2-bit
+        # codes and 8 scale-plane bytes per 64 weights (0.375 B/weight read
+        # per step)
         bpw = {"Q4_K": Q4K_BYTES_PER_WEIGHT, "Q2_K": 84.0 / 256.0}[fname]
-        rbpw = {"Q4_K": Q4K_BYTES_PER_WEIGHT, "Q2_K": 0.625}[fname]
+        rbpw = {"Q4_K": Q4K_BYTES_PER_WEIGHT, "Q2_K": 0.375}[fname]
         sets = make_expert_sets(nx, ctx, torch, fmt, E, H, F, reps, args.seed + 31, Fs)
         g = torch.Generator(device=dev)
         g.manual_seed(args.seed + 41)

@@ -38,8 +38,9 @@ bool format_info(int fmt, FormatInfo *fi) {
   case NX_FMT_Q4_K: *fi = {fmt, 256, 144, 128, 16}; return true;
   case NX_FMT_Q8_0: *fi = {fmt, 32, 34, 32, 2}; return true;
   case NX_FMT_Q4_0: *fi = {fmt, 32, 18, 16, 2}; return true;
-  // resident Q2_K: codes widened to 4 bits, 8 scale-plane bytes per segment
-  case NX_FMT_Q2_K: *fi = {fmt, 256, 84, 128, 32}; return true;
+  // resident Q2_K: 2-bit codes (16 bytes per 64-element segment), 8
+  // scale-plane bytes per segment
+  case NX_FMT_Q2_K: *fi = {fmt, 256, 84, 64, 32}; return true;
   case NX_FMT_F32: *fi = {fmt, 4, 16, 16, 0}; return true;
   // 16-bit floats: 16 values per 32-byte segment, no scale plane
   case NX_FMT_F16:
@@ -269,7 +270,8 @@ static void plane_layout(int fmt, RolePlane &pl, int rows, int cols) {
     pl.row_meta = 0;
     break;
   }
-  pl.row_qs = (uint32_t)pl.nseg * 32;
+  // two 16-byte code chunks per segment, one for Q2_K's 2-bit codes
+  pl.row_qs = (uint32_t)pl.nseg * (fmt == NX_FMT_Q2_K ? 16 : 32);
   // strides rounded to 256 B so every expert's planes start aligned
   pl.qs_stride = ((size_t)rows * pl.row_qs + 255) / 256 * 256;
   pl.meta_stride = ((size_t)rows * pl.row_meta + 255) / 256 * 256;

@@ -78,6 +78,13 @@ __device__ __forceinline__ uint32_t seg_off(int j, int h, int nseg) {
   return (uint32_t)(g * 2048 + h * gsz * 16 + (j & 63) * 16);
 }
 
+// 16-byte code chunks per segment: two (the halves above) for every format
+// but Q2_K, whose 2-bit codes fill one chunk per segment, stored at 16 j
+template <int FMT>
+constexpr int code_chunks() {
+  return FMT == NX_FMT_Q2_K ? 1 : 2;
+}
+
 // ---- Integer-dot GEMV operands.
 //
 // The decode GEMV computes sum_i q_i x_i with exact integer dot products.  A
@@ -484,10 +491,14 @@ struct Seg<NX_FMT_Q4_0> {
   }
 };
 
-// Q2_K (src/quant/mod.rs:913-937): resident codes are the 2-bit q of a
-// 64-element segment (block j/4, elements 64(j%4) ..) widened to 4-bit
-// nibbles in the 4-bit dword order (non-negative, so no offset); the scale
-// plane holds per segment {f16 d, f16 dmin, the four scale/min bytes}.
+// Q2_K (src/quant/mod.rs:913-937): the resident codes of a 64-element
+// segment (block j/4, elements 64(j%4) ..) are its 2-bit q in one 16-byte
+// chunk.  Dword k packs nibble dword k of both 32-element halves in the 4-bit
+// dword order (byte 4k+i: elements 8k+i, 8k+4+i of the half): half 0's codes
+// in bits 0-1 of each nibble, half 1's in bits 2-3, so
+//   half 0 = c & 0x33333333,  half 1 = (c >> 2) & 0x33333333
+// are the widened non-negative 4-bit codes (no offset).  The scale plane
+// holds per segment {f16 d, f16 dmin, the four scale/min bytes}.
 // w = d*sc*q - dmin*m per 16-element sub-block u:
 //   sum w*x = d*sc_u * sum q x - dmin*m_u * sum x
 template <>
@@ -510,9 +521,13 @@ struct Seg<NX_FMT_Q2_K> {
   __device__ __forceinline__ static void prep_quarter(const float *x, int q, X *o) {
     prep2_quarter(x, q, o);
   }
+  // (q1, the second chunk of the other formats, is not loaded)
   template <int NT>
-  __device__ __forceinline__ static void dot(const uint4 &q0, const uint4 &q1, const Meta &m, int,
+  __device__ __forceinline__ static void dot(const uint4 &q, const uint4 &, const Meta &m, int,
                                              const X *xv, Run *, float *acc) {
+    constexpr uint32_t M2 = 0x33333333u;
+    const uint4 q0 = make_uint4(q.x & M2, q.y & M2, q.z & M2, q.w & M2);
+    const uint4 q1 = make_uint4((q.x >> 2) & M2, (q.y >> 2) & M2, (q.z >> 2) & M2, (q.w >> 2) & M2);
     const float d = h2f(m.x & 0xFFFFu), dmin = h2f(m.x >> 16);
     float ds[4], dm[4];
 #pragma unroll

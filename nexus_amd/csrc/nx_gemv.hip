@@ -261,12 +261,13 @@ struct RowGroup {
   }
   __device__ __forceinline__ void load(Stage &st, const SlotView &v, const RowMap &rm,
                                        int q0) const {
+    constexpr int CH = code_chunks<FMT>();
     uint32_t off0[SPL], off1[SPL], moff[SPL];
 #pragma unroll
     for (int m = 0; m < SPL; ++m) {
       const int j = seg0 + li + m * L;
       const bool jv = j < v.nseg;
-      off0[m] = jv ? seg_off(j, 0, v.nseg) : OOB;
+      off0[m] = jv ? (CH == 1 ? (uint32_t)j * 16u : seg_off(j, 0, v.nseg)) : OOB;
       off1[m] = jv ? seg_off(j, 1, v.nseg) : OOB;
       moff[m] = S::meta_off(j, jv);
     }
@@ -290,7 +291,7 @@ struct RowGroup {
 #pragma unroll
           for (int m = 0; m < SPL; ++m) {
             st.q[u][mt][m][0] = bload16w(mt == 0 ? rq0 : rq1, off0[m]);
-            st.q[u][mt][m][1] = bload16w(mt == 0 ? rq0 : rq1, off1[m]);
+            st.q[u][mt][m][1] = CH == 2 ? bload16w(mt == 0 ? rq0 : rq1, off1[m]) : make_uint4(0, 0, 0, 0);
             st.m[u][mt][m] = S::load_meta(mt == 0 ? rm0 : rm1, moff[m]);
           }
         }
@@ -311,7 +312,8 @@ struct RowGroup {
 #pragma unroll
           for (int m = 0; m < SPL; ++m) {
             st.q[u][mt][m][0] = bload16w(mt == 0 ? rq0 : rq1, rqo + off0[m]);
-            st.q[u][mt][m][1] = bload16w(mt == 0 ? rq0 : rq1, rqo + off1[m]);
+            st.q[u][mt][m][1] =
+                CH == 2 ? bload16w(mt == 0 ? rq0 : rq1, rqo + off1[m]) : make_uint4(0, 0, 0, 0);
             st.m[u][mt][m] = S::load_meta(mt == 0 ? rm0 : rm1, rmo + moff[m]);
           }
         }

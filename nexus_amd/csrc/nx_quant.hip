@@ -339,15 +339,6 @@ __global__ __launch_bounds__(256) void k_repack_codes(const uint8_t *__restrict_
         const uint8_t *b = src + ((size_t)r * nb + (j >> 2)) * 144 + 16 + (j & 3) * 32;
 #pragma unroll
         for (int i = 0; i < 32; ++i) q[i] = h ? (b[i] >> 4) : (b[i] & 15);
-      } else if constexpr (FMT == NX_FMT_Q2_K) {
-        // segment j = block j/4, elements 64(j%4) + 32h + i; element e of a
-        // block sits in bits 2(e%4) of qs byte e/4.  Codes stay non-negative
-        // (stored as q, not q ^ 8: the dot needs no offset).
-        const int nb = cols / 256;
-        const uint8_t *b = src + ((size_t)r * nb + (j >> 2)) * 84 + 16;
-        const int e0 = (j & 3) * 64 + 32 * h;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) q[i] = ((b[(e0 + i) / 4] >> (2 * ((e0 + i) % 4))) & 3) ^ 8;
       } else {  // Q4_0: segment j = blocks 2j, 2j+1; byte i: element i (low), 16 + i (high)
         const int nb = cols / 32;
         const int blk = 2 * j + h;
@@ -387,6 +378,32 @@ __global__ __launch_bounds__(256) void k_repack_meta(const uint8_t *__restrict__
     const uint8_t *s = b < nb ? src + ((size_t)r * nb + b) * BB : nullptr;
 #pragma unroll
     for (int v = 0; v < MB; ++v) dst[v] = s ? s[v] : (uint8_t)0;
+  }
+}
+
+// Q2_K code plane: one thread per 64-element segment j (block j/4, elements
+// 64(j%4) ..), its 16 bytes at 16 j.  Element e of a block sits in bits
+// 2(e%4) of qs byte e/4; resident byte 4k+i holds, from bit 0, the codes of
+// elements 8k+i and 32+8k+i, then 8k+4+i and 32+8k+4+i of the segment (the
+// 4-bit dword order of each half, the halves two bits apart).
+__global__ __launch_bounds__(256) void k_repack_codes_q2k(const uint8_t *__restrict__ src, int rows,
+                                                          int cols, int nseg, uint32_t row_qs,
+                                                          uint8_t *__restrict__ qs) {
+  const int nb = cols / 256;
+  const size_t total = (size_t)rows * nseg;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const int r = (int)(i / nseg), j = (int)(i - (size_t)r * nseg);
+    const uint8_t *b = src + ((size_t)r * nb + (j >> 2)) * 84 + 16;
+    const int e0 = (j & 3) * 64;
+    auto code = [&](int e) { return (uint32_t)(b[(e0 + e) >> 2] >> (2 * ((e0 + e) & 3))) & 3u; };
+    uint8_t *dst = qs + (size_t)r * row_qs + (size_t)j * 16;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        dst[4 * k + c] = (uint8_t)(code(8 * k + c) | (code(32 + 8 * k + c) << 2) |
+                                   (code(8 * k + 4 + c) << 4) | (code(32 + 8 * k + 4 + c) << 6));
   }
 }
 
@@ -494,11 +511,10 @@ int launch_repack(nx_ctx *c, int fmt, const void *d_src, const RolePlane &pl, ui
   case NX_FMT_F16: NX_RP(NX_FMT_F16, "repack_f16");
   case NX_FMT_BF16: NX_RP(NX_FMT_BF16, "repack_bf16");
   case NX_FMT_Q2_K: {
-    NX_TRY(launch(c, "repack_q2_k", [&] {
-      k_repack_codes<NX_FMT_Q2_K><<<gc, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg,
-                                                            pl.row_qs, qs);
-    }));
     const unsigned g2 = grid_for((size_t)pl.rows * pl.nseg, 256);
+    NX_TRY(launch(c, "repack_q2_k", [&] {
+      k_repack_codes_q2k<<<g2, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_qs, qs);
+    }));
     return launch(c, "repack_q2_k", [&] {
       k_repack_meta_q2k<<<g2, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_meta, meta);
     });

@@ -56,7 +56,11 @@ def test_q2k_quantize_bit_exact(ctx, scale):
 
 @pytest.mark.parametrize("E,H,F,k,T,shared,score", [
     (8, 512, 1024, 2, 1, 0, 0), (8, 1024, 512, 2, 5, 0, 0), (16, 256, 768, 4, 16, 256, 1),
-    (32, 512, 256, 8, 64, 0, 0)])
+    (32, 512, 256, 8, 64, 0, 0),
+    (4, 4096, 512, 2, 1, 0, 0),     # gate/up rows of 64 segments: one wave per row, shared operands
+    (4, 4096, 512, 2, 2, 0, 0),     # the same, two tokens per group
+    (4, 512, 14336, 2, 1, 0, 0),    # down rows of 224 segments: K slices
+    (8, 7168, 256, 4, 1, 256, 1)])  # gate/up rows of 112 segments: two-wave row groups
 def test_q2k_layer_gemv_parity(ctx, E, H, F, k, T, shared, score):
     print(f"q2k layer E={E} H={H} F={F} k={k} T={T} shared={shared}", flush=True)
     L = Layer(Q2_K, E, H, F, k, T, seed=E + H + F + T, shared_F=shared, score_mode=score)
