@@ -944,7 +944,18 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
     const double kk = std::min(1.0, (double)k / E);
     const double act = std::max(1.0, E * (1.0 - std::pow(1.0 - kk, (double)T)));
     const double tpe = (double)T * k / act;
-    if (ex->fmt == NX_FMT_Q4_K && !shared) {
+    if (ex->fmt == NX_FMT_Q4_K && shared && ex->Fs == ex->F) {
+      // A shared expert sees every token: the GEMV walks it a token pair at
+      // a time, the split-activation path 16 tokens at a time.  Measured
+      // (DeepSeek shapes, ms, GEMV / split / grouped GEMM): 2 tokens 0.115 /
+      // 0.173 / 0.268, 4: 0.270 / 0.264 / 0.321, 8: 0.887 / 0.508 / 0.588,
+      // 16: 3.69 / 0.904 / 0.996, 32: - / 1.31 / 1.52, 64: - / 1.76 / 2.04;
+      // the grouped GEMM from the routed experts' 12 tokens each, as below.
+      if (tpe >= 12.0)
+        use = NX_PATH_MFMA_BF16;
+      else
+        use = T >= 4 ? NX_PATH_MFMA_SPLIT : NX_PATH_GEMV;
+    } else if (ex->fmt == NX_FMT_Q4_K && !shared) {
       // Measured crossovers (Mixtral and Qwen3 shapes): the GEMV re-reads an
       // expert's weights per pair of its tokens and wins below ~2 tokens per
       // expert; the split-activation MFMA path reads them once per 16 tokens
@@ -967,7 +978,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
       // Q4_0 at 8 and 16 tokens, Qwen3 Q8_0 at 32), or from 6 tokens when a
       // shared expert sees them all: the GEMV passes over the shared expert
       // per pair of tokens and over the routed experts per token group
-      // (DeepSeek Q4_K with its shared expert: GEMV 0.29 / 0.81 / 10.5 ms
+      // (DeepSeek shapes with a shared expert: GEMV 0.29 / 0.81 / 10.5 ms
       // at 4 / 8 / 32 tokens, grouped GEMM 0.36 / 0.61 / 1.44 ms).
       use = (tpe >= 3.0 || (shared && T >= 6)) ? NX_PATH_MFMA_BF16 : NX_PATH_GEMV;
     }
@@ -1001,17 +1012,20 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   if (use == NX_PATH_MFMA_SPLIT) {
     if (ex->fmt != NX_FMT_Q4_K)
       return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path takes Q4_K experts");
-    if (shared) return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path has no shared expert");
-    const int max_tiles = mfv_max_tiles(T, k, E);
+    if (shared && ex->Fs != ex->F)
+      return fail(NX_ERR_UNSUPPORTED,
+                  "the split-activation MFMA path takes a shared expert as wide as the routed ones");
+    const int max_tiles = mfv_max_tiles(T, k, E, shared);
     int32_t *d_tiles;
     NX_TRY(ws(c, WS_TILES, 2 + 2 * (size_t)max_tiles, &d_tiles));
-    if (route_permute_fusable(T, E, k)) {
+    // (the fused router lists no shared-expert tiles)
+    if (!shared && route_permute_fusable(T, E, k)) {
       NX_TRY(launch_route_permute(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt, d_ec, d_off,
                                   d_pt, d_ps, d_inv, d_act, kMfvTileM, d_tiles, nullptr, 0));
     } else {
       NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
       NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, kMfvTileM, d_ec, d_off, d_pt, d_ps, d_inv,
-                            d_act, d_tiles, 0));
+                            d_act, d_tiles, shared ? T : 0));
     }
     MfvPlan mp{ex, T, k, d_x, d_pt, d_off, d_tiles, max_tiles, d_w, d_cnt, d_inv, d_out, d_residual};
     return launch_mfv(c, mp);

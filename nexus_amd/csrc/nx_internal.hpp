@@ -325,7 +325,7 @@ struct MfvPlan {
   const float *residual;
 };
 int launch_mfv(nx_ctx *c, const MfvPlan &p);
-int mfv_max_tiles(int T, int k, int E);
+int mfv_max_tiles(int T, int k, int E, bool shared);
 constexpr int kMfvTileM = 16;
 int gemm_tile_m();
 int gemm_down_ksplit(int fmt, int F, int H, int tiles, int slots);

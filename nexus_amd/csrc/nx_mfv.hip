@@ -1,5 +1,7 @@
 // nx_mfv.hip — few-token grouped matvec on MFMA for Q4_K experts: decode
-// batches whose experts see a handful of tokens each (2 to ~128 tokens).
+// batches whose experts see a handful of tokens each (2 to ~128 tokens),
+// with or without a shared expert (as wide as the routed ones) that sees
+// every token.
 //
 // The decode GEMV's exact integer dot costs about one instruction per
 // weight per token, so its time grows with the tokens an expert sees; the
@@ -56,6 +58,10 @@ struct MfvArgs {
   const int32_t *perm_token;  // gate/up: pair -> token row of x; down: null (pair row)
   const int32_t *offsets;     // [E + 1]
   const int32_t *tiles;       // [0] = tile count, [1] unused, then (expert, first pair within it)
+  // the shared expert (tiles of expert E; pairs T k + t, t the token), with
+  // the routed experts' row layout
+  const uint8_t *sqs0, *sqs1, *smeta0, *smeta1;
+  int E, T, k;
   float *out;                 // partial sums: [slice][pair][out_stride]
   int out_stride;             // gate/up: 2 F (gate rows, then up rows); down: H
   size_t out_split;           // floats between slices
@@ -102,10 +108,14 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tile = blockIdx.y;
   if (tile >= a.tiles[0]) return;  // workgroup-uniform
-  // tile t: expert tiles[2 + 2t], first pair tiles[3 + 2t] within the expert
+  // tile t: expert tiles[2 + 2t] (E: the shared expert), first pair
+  // tiles[3 + 2t] within the expert
   const int e = __builtin_amdgcn_readfirstlane(a.tiles[2 + 2 * tile]);
-  const int pair0 = __builtin_amdgcn_readfirstlane(a.offsets[e] + a.tiles[3 + 2 * tile]);
-  const int cnt = __builtin_amdgcn_readfirstlane(min(MV_M, a.offsets[e + 1] - pair0));
+  const int m0 = __builtin_amdgcn_readfirstlane(a.tiles[3 + 2 * tile]);
+  const bool routed = e < a.E;
+  const int pair0 = __builtin_amdgcn_readfirstlane(routed ? a.offsets[e] + m0 : a.T * a.k + m0);
+  const int cnt = __builtin_amdgcn_readfirstlane(
+      min(MV_M, routed ? a.offsets[e + 1] - pair0 : a.T - m0));
   const int slice = blockIdx.z;
   const int c0 = slice * MV_KS;  // first chunk of the slice
   const int row_base = blockIdx.x * MV_WG_ROWS + wave * 16 * MV_RTW;
@@ -116,11 +126,11 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
   __amdgpu_buffer_rsrc_t rq[NMAT], rm[NMAT];
   {
     const uint32_t nq = (uint32_t)a.rows * a.row_qs, nm = (uint32_t)a.rows * a.row_meta;
-    rq[0] = make_rsrc(a.qs0 + (size_t)e * a.qs_stride, nq);
-    rm[0] = make_rsrc(a.meta0 + (size_t)e * a.meta_stride, nm);
+    rq[0] = make_rsrc(routed ? a.qs0 + (size_t)e * a.qs_stride : a.sqs0, nq);
+    rm[0] = make_rsrc(routed ? a.meta0 + (size_t)e * a.meta_stride : a.smeta0, nm);
     if constexpr (NMAT == 2) {
-      rq[1] = make_rsrc(a.qs1 + (size_t)e * a.qs_stride, nq);
-      rm[1] = make_rsrc(a.meta1 + (size_t)e * a.meta_stride, nm);
+      rq[1] = make_rsrc(routed ? a.qs1 + (size_t)e * a.qs_stride : a.sqs1, nq);
+      rm[1] = make_rsrc(routed ? a.meta1 + (size_t)e * a.meta_stride : a.smeta1, nm);
     }
   }
   // step i: row tile i / MV_KS, chunk c0 + i % MV_KS
@@ -167,7 +177,9 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
     const int sm = tid >> 4, sj = tid & 15;
     const float *xrow = nullptr;
     if (sm < cnt) {
-      const int r = a.perm_token ? a.perm_token[pair0 + sm] : pair0 + sm;
+      // gate/up: the pair's token (a shared pair's is its index in the
+      // tile's run); down: the pair's row of act
+      const int r = a.perm_token ? (routed ? a.perm_token[pair0 + sm] : m0 + sm) : pair0 + sm;
       xrow = a.x + (size_t)r * a.x_stride;
     }
     // every lane loads (absent pairs and chunks from row 0 of x, then
@@ -376,9 +388,10 @@ __global__ __launch_bounds__(256) void k_mfv_swiglu(const float *__restrict__ pa
 
 }  // namespace
 
-int mfv_max_tiles(int T, int k, int E) {
+int mfv_max_tiles(int T, int k, int E, bool shared) {
   const long pairs = (long)T * k;
-  return (int)((pairs + MV_M - 1) / MV_M + std::min<long>(E, pairs));
+  return (int)((pairs + MV_M - 1) / MV_M + std::min<long>(E, pairs) +
+               (shared ? (T + MV_M - 1) / MV_M : 0));
 }
 
 int launch_mfv(nx_ctx *c, const MfvPlan &p) {
@@ -388,8 +401,13 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
   // activation rows are read as float4 runs of whole chunks
   if (reinterpret_cast<uintptr_t>(p.x) & 15)
     return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path needs 16-byte aligned inputs");
+  const bool shared = ex->Fs > 0;
+  if (shared && ex->Fs != ex->F)
+    return fail(NX_ERR_UNSUPPORTED,
+                "the split-activation MFMA path takes a shared expert as wide as the routed ones");
   const int H = ex->H, F = ex->F;
-  const size_t pairs = (size_t)p.T * p.k;
+  // routed pairs, then one pair per token for the shared expert
+  const size_t pairs = (size_t)p.T * p.k + (shared ? (size_t)p.T : 0);
   const int nks_g = (H / MV_K + MV_KS - 1) / MV_KS;
   const int nks_d = (F / MV_K + MV_KS - 1) / MV_KS;
   void *vg, *va, *vy;
@@ -416,6 +434,17 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
     a.nchunk = R0.cols / MV_K;
     a.offsets = p.offsets;
     a.tiles = p.tiles;
+    a.E = ex->E;
+    a.T = p.T;
+    a.k = p.k;
+    if (shared) {
+      const RolePlane &S0 = ex->shared[gateup ? NX_ROLE_GATE : NX_ROLE_DOWN];
+      const RolePlane &S1 = ex->shared[gateup ? NX_ROLE_UP : NX_ROLE_DOWN];
+      a.sqs0 = S0.qs;
+      a.sqs1 = S1.qs;
+      a.smeta0 = S0.meta;
+      a.smeta1 = S1.meta;
+    }
     if (gateup) {
       a.x = p.x;
       a.x_stride = H;
@@ -448,7 +477,7 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
                     [&] { go(c, k_mfv<false>, grid, dim3(256), 0, a); }));
     }
   }
-  return launch_combine(c, ypart, p.rw, p.rcnt, p.inv, p.T, p.k, H, false, p.out, nks_d,
+  return launch_combine(c, ypart, p.rw, p.rcnt, p.inv, p.T, p.k, H, shared, p.out, nks_d,
                         pairs * (size_t)H, p.residual);
 }
 

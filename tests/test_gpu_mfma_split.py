@@ -7,8 +7,9 @@ after a power-of-two scaling.  Bar: the GEMV path's, relative L2 1e-4
 against the oracle's dispatch (src/engine/mod.rs:969-1024) over the same
 payloads: 1 to 64 tokens, experts with more than 16 tokens (several tiles),
 top-8 routing, the sigmoid score mode, token rows of very different
-magnitudes and zero rows, and Mixtral's full shape; other formats and shared
-experts are rejected with NX_ERR_UNSUPPORTED.
+magnitudes and zero rows, Mixtral's full shape, and a shared expert as wide
+as the routed ones (one pair per token, several tiles of 16); other formats
+and shared experts of another width are rejected with NX_ERR_UNSUPPORTED.
 """
 import numpy as np
 import pytest
@@ -34,6 +35,20 @@ def ctx():
 def test_split_parity(ctx, E, H, F, k, T, score):
     print(f"mfma split E={E} H={H} F={F} k={k} T={T} score={score}", flush=True)
     L = Layer(Q4_K, E, H, F, k, T, seed=E * 5 + H + F + T, score_mode=score)
+    ex = L.upload(nx, ctx)
+    got = ex.forward(L.x, L.logits, k, score, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    assert rel_l2(got, L.oracle_out()) <= TOL
+
+
+@pytest.mark.parametrize("E,H,F,k,T,score", [
+    (16, 512, 512, 4, 1, 1), (16, 512, 512, 4, 8, 1), (8, 256, 768, 2, 40, 0),
+    (64, 1024, 256, 8, 17, 1)])
+def test_split_parity_shared_expert(ctx, E, H, F, k, T, score):
+    """A shared expert (every token, after the routed experts) on the split
+    path: its tiles come after the routed ones in the permutation's list."""
+    print(f"mfma split shared E={E} H={H} F={F} k={k} T={T} score={score}", flush=True)
+    L = Layer(Q4_K, E, H, F, k, T, seed=E * 7 + H + F + T, shared_F=F, score_mode=score)
     ex = L.upload(nx, ctx)
     got = ex.forward(L.x, L.logits, k, score, nx.PATH_MFMA_SPLIT)
     ex.close()
@@ -89,7 +104,7 @@ def test_split_rejects(ctx):
         ex.forward(L.x, L.logits, 2, 0, nx.PATH_MFMA_SPLIT)
     assert ei.value.code == nx.NX_ERR_UNSUPPORTED
     ex.close()
-    S = Layer(Q4_K, 4, 256, 256, 2, 4, seed=4, shared_F=256)
+    S = Layer(Q4_K, 4, 256, 256, 2, 4, seed=4, shared_F=512)  # a wider shared expert
     ex = S.upload(nx, ctx)
     with pytest.raises(nx.NexusError) as ei:
         ex.forward(S.x, S.logits, 2, 0, nx.PATH_MFMA_SPLIT)
@@ -117,12 +132,17 @@ def test_auto_path_choice(ctx, E, H, F, k, T, want):
     (Q8_0, 8, 512, 1024, 2, 8, 0, nx.PATH_GEMV),        # 2 tokens per expert
     (Q8_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_BF16),  # 4
     (Q4_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_BF16),
-    (Q4_K, 16, 512, 512, 4, 4, 512, nx.PATH_GEMV),      # a shared expert, 4 tokens
-    (Q4_K, 16, 512, 512, 4, 8, 512, nx.PATH_MFMA_BF16)])  # a shared expert, 8 tokens
+    (Q4_K, 16, 512, 512, 4, 2, 512, nx.PATH_GEMV),        # a shared expert, 2 tokens
+    (Q4_K, 16, 512, 512, 4, 4, 512, nx.PATH_MFMA_SPLIT),  # ... 4 tokens
+    (Q4_K, 16, 512, 512, 4, 8, 512, nx.PATH_MFMA_SPLIT),  # ... 8 tokens
+    (Q4_K, 4, 256, 256, 2, 48, 256, nx.PATH_MFMA_BF16),   # ... 24 tokens per routed expert
+    (Q4_K, 16, 512, 512, 4, 8, 1024, nx.PATH_MFMA_BF16)])  # a wider shared expert, 8 tokens
 def test_auto_path_choice_other(ctx, fmt, E, H, F, k, T, shared, want):
     """AUTO for formats other than Q4_K and for layers with a shared expert:
     the grouped GEMM from ~3 tokens per routed expert, or from 6 tokens with
-    a shared expert; the GEMV below (the bits of the chosen path)."""
+    a shared expert, the GEMV below; Q4_K with a shared expert as wide as the
+    routed ones takes the split-activation path from 4 tokens up to 12
+    tokens per routed expert (the bits of the chosen path)."""
     L = Layer(fmt, E, H, F, k, T, seed=E + T + fmt, shared_F=shared)
     ex = L.upload(nx, ctx)
     auto = ex.forward(L.x, L.logits, k, 0, nx.PATH_AUTO)
