@@ -1033,15 +1033,19 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
 
   // grouped GEMM on MFMA
   const bool bf16 = use == NX_PATH_MFMA_BF16;
-  const int tm = gemm_tile_m();
+  // gate/up and down take M-tiles of their own heights: one tile list each
   const long active_max = std::min<long>(E, (long)T * k);
-  const int max_tiles = (int)(((long)T * k + tm - 1) / tm + active_max +
-                              (shared ? ((long)T + tm - 1) / tm : 0));
-  int32_t *d_tiles;
+  auto tiles_bound = [&](int tm) {
+    return (int)(((long)T * k + tm - 1) / tm + active_max + (shared ? ((long)T + tm - 1) / tm : 0));
+  };
+  const int tm = gemm_tile_m(), tm_down = gemm_tile_m_down(T, k, E);
+  const int max_tiles = tiles_bound(tm), max_tiles_down = tiles_bound(tm_down);
+  int32_t *d_tiles, *d_tiles_down;
   NX_TRY(ws(c, WS_TILES, 2 + 2 * (size_t)max_tiles, &d_tiles));
+  NX_TRY(ws(c, WS_TILES_DOWN, 2 + 2 * (size_t)max_tiles_down, &d_tiles_down));
   NX_TRY(launch_route(c, d_logits, T, E, k, score_mode, d_exp, d_w, d_cnt));
   NX_TRY(launch_permute(c, d_exp, d_cnt, T, k, E, tm, d_ec, d_off, d_pt, d_ps, d_inv, d_act,
-                        d_tiles, shared ? T : 0));
+                        d_tiles, shared ? T : 0, tm_down, d_tiles_down));
   void *d_xh, *d_acth;
   // operands in the kernels' K order, rows padded to whole scale windows
   const int x_stride = gemm_kpad(ex->fmt, H);
@@ -1053,10 +1057,12 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   NX_TRY(ws_get(c, WS_ACT, pairs_total * act_stride * 2, &d_acth));
   // the down pass splits K when that fills the CUs' rounds better; each
   // split writes its own partial sums, added by the combine
-  const int ksplit = gemm_down_ksplit(ex->fmt, std::max(ex->F, ex->Fs), H, max_tiles, 2 * c->num_cu);
+  const int ksplit =
+      gemm_down_ksplit(ex->fmt, std::max(ex->F, ex->Fs), H, max_tiles_down, 2 * c->num_cu);
   NX_TRY(ws(c, WS_YPAIR, (size_t)ksplit * pairs_total * H, &d_ypair));
-  GemmPlan mp{ex, T, k, bf16, d_x, d_pt, d_off, d_act, d_tiles, max_tiles, d_acth, act_stride,
-              d_ypair, d_xh, x_stride, pairs_total, ksplit};
+  GemmPlan mp{ex,       T,      k,          bf16,          d_x,  d_pt,     d_off,
+              d_act,    d_tiles, max_tiles, d_tiles_down, max_tiles_down, tm_down, d_acth,
+              act_stride, d_ypair, d_xh,    x_stride,     pairs_total, ksplit};
   NX_TRY(launch_gemm_gateup(c, mp));
   NX_TRY(launch_gemm_down(c, mp));
   NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out, ksplit,

@@ -8,12 +8,13 @@
 //   down:    y[p] = W_down . act[p]  (fp32), then the route-weighted combine.
 //
 // Work decomposition.  The permutation kernel lists M-tiles (expert, first
-// pair) of 128 pairs; the 1-D grid covers (M-tile, 128-row N-tile) pairs in
-// an XCD-aware order (see k_gemm; extra workgroups exit).  A workgroup of 4
-// waves owns a 128 x 64NT output tile (gate/up: two of them, for the gate
-// and the up rows); wave w owns weight rows 16NT w .. 16NT w + 16NT - 1 of
-// the tile for all 128 pairs, as NT x 8 v_mfma_f32_16x16x32 tiles per
-// matrix (NT = 2; see GemmShape).
+// pair) of BM pairs (128 for gate/up; 128 or 160 for down: one list each); the 1-D
+// grid covers (M-tile, 128-row N-tile) pairs in an XCD-aware order (see
+// k_gemm; extra workgroups exit).  A workgroup of 4 waves owns a BM x 64NT
+// output tile (gate/up: two of them, for the gate and the up rows); wave w
+// owns weight rows 16NT w .. 16NT w + 16NT - 1 of the tile for all BM pairs,
+// as NT x BM/16 v_mfma_f32_16x16x32 tiles per matrix (NT = 2; see
+// GemmShape).
 //
 // Operand order.  The K loop takes 64 positions per step.  Position
 // j = 64 ks + 16 q + i is value i of the lanes of quarter q (lanes 16q ..
@@ -32,6 +33,8 @@
 // (bit-exact f32, rounded once to the operand type) straight into its MFMA B
 // operands.  Codes are fetched two steps ahead, scales once per window of
 // steps, activations three steps ahead.
+#include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "nx_device.hpp"
@@ -49,7 +52,16 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 128;   // pairs per tile
+// Pairs per M-tile.  Gate/up's two matrices' accumulators leave room for
+// 128 (160 spilled: Qwen3 T = 512 gate/up 101 -> 156 us).  The down pass
+// takes 160 when experts hold about 100-160 pairs each, so that most of them
+// stream and decode their weights once instead of twice (DeepSeek T = 4096,
+// ~128 pairs per expert: down 1.76 -> 1.45 ms), and 128 otherwise (Qwen3
+// T = 512, 32 per expert: 80 -> 85 us with 160; the Mixtral prefill, ~500
+// per expert, gains 13 us in the down pass and loses 20 us to a second K
+// split).  With 160 the down pass's LDS ring is 80 KB: two workgroups fill
+// a CU.
+constexpr int BM_GATEUP = 128, BM_DOWN_WIDE = 160;
 constexpr int BK = 64;    // K positions per step
 
 template <bool BF16>
@@ -396,8 +408,8 @@ __device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WC &w, const W
   }
 }
 
-// LDS ring of activation stages: stage = the 128 x 64 activation tile of one
-// K step as 128 rows of eight 16-byte chunks (chunk c = operand positions
+// LDS ring of activation stages: stage = the BM x 64 activation tile of one
+// K step as BM rows of eight 16-byte chunks (chunk c = operand positions
 // 8c .. 8c+7 of the step); chunk c of row r is stored at slot c ^ swz(r),
 // swz(r) = (r ^ (r / 8 % 2)) % 8.  ds_read_b128 serves eight lanes per
 // cycle from 32 four-byte banks (128 bytes); an MFMA operand read takes one
@@ -526,7 +538,7 @@ struct LoadSchedule {
   }
 };
 
-template <int FMT, bool BF16, bool GATEUP>
+template <int FMT, bool BF16, bool GATEUP, int BMT>
 __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(const GemmArgs g) {
   using Op = OpT<BF16>;
   using V8 = typename Op::V8;
@@ -556,8 +568,12 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   constexpr int NB0 = RING > NBUF ? RING : NBUF, NB1 = META2 ? 2 * WS : WS;
   constexpr int NB = NB0 > NB1 ? NB0 : NB1;
   static_assert(NB % RING == 0 && NB % NBUF == 0 && NB % (NMB * WS) == 0, "loop body");
-  constexpr int NA = 4;
-  constexpr int IG = GATEUP ? 2 : 4;  // M-tiles per scheduling group
+  constexpr int BM = BMT;  // pairs per tile
+  static_assert(BM % 32 == 0, "whole activation loads per wave");
+  constexpr int MB = BM / 16;  // 16-pair MFMA row sets per tile
+  constexpr int NA = BM / 32;  // activation loads per wave and step (8 rows each)
+  constexpr int IG = GATEUP || MB % 4 ? 2 : 4;  // M-tiles per scheduling group
+  static_assert(MB % IG == 0, "whole scheduling groups");
   constexpr LoadSchedule sched{RING, WS, NA, NMAT * NT * n_code_loads<FMT>(),
                                NMAT * NT * n_meta_loads<FMT>(), WDIST, GRP, META2};
   __shared__ __attribute__((aligned(16))) uint4 ring0[BM * 8];
@@ -641,7 +657,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   const __amdgpu_buffer_rsrc_t rm1 = make_rsrc(m1p, (uint32_t)rows * rm);
 
   // ---- activation chunks: instruction i of this wave fills stage chunks
-  // (4 * wave + i) * 64 + lane, i.e. row r_i = (4 * wave + i) * 8 + lane / 8,
+  // (NA * wave + i) * 64 + lane, i.e. row r_i = (NA * wave + i) * 8 + lane / 8,
   // slot lane % 8, which holds chunk (lane % 8) ^ swz(r_i) of that row
   // (gathered through the permutation for gate/up).  One wave-uniform
   // resource spans the activation buffer; absent rows, and every step past
@@ -652,7 +668,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   int arow[NA];
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const int r = (4 * wave + i) * 8 + (lane >> 3);
+    const int r = (NA * wave + i) * 8 + (lane >> 3);
     // absent rows look up the tile's first pair (always present) and are
     // masked below, so the four lookups go out together
     const int p = pair0 + m0 + (r < mrows ? r : 0);
@@ -660,7 +676,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   }
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const int r = (4 * wave + i) * 8 + (lane >> 3);
+    const int r = (NA * wave + i) * 8 + (lane >> 3);
     const int chunk = (lane & 7) ^ swz(r);
     abase[i] = r < mrows ? (uint32_t)arow[i] * (uint32_t)g.a_stride * 2u + 16u * chunk : OOB;
   }
@@ -692,7 +708,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
 #pragma unroll
     for (int i = decltype(i0)::value; i < decltype(i1)::value; ++i) {
       const uint32_t off = abase[i] + koff;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(dst + (4 * wave + i) * 64), 16, off,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(dst + (NA * wave + i) * 64), 16, off,
                                                0, 0, 0);
     }
   };
@@ -736,13 +752,13 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   };
 
   // ---- accumulators: acc[mt][n][i] = pairs 16i .. 16i+15 x rows 16n .. of this wave
-  f32x4 acc[NMAT][NT][8];
+  f32x4 acc[NMAT][NT][MB];
 #pragma unroll
   for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[mt][n][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < MB; ++i) acc[mt][n][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Software pipeline.  Step ks: wait until this wave's loads of activation
   // stage ks, codes ks and its window's scales have landed (the loads issued
@@ -770,7 +786,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
     // a wave held up issuing a load (memory pipeline full) still has MFMAs
     // queued: the activation loads after the first-half groups, the late
     // loads after the first second-half group.
-    constexpr int NG = 8 / IG;          // groups per half
+    constexpr int NG = MB / IG;         // groups per half
     constexpr int APG = (NA + NG - 1) / NG;  // activation loads per group
     // A operands are read one group ahead (across the halves too), so each
     // group's MFMAs cover the LDS latency of the next group's reads
@@ -853,7 +869,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
     const int col = n0 + 16 * NT * wave + 16 * n + l16;
     if (col >= rows) continue;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int row = 16 * i + 4 * q + j;
@@ -934,20 +950,22 @@ __global__ __launch_bounds__(256) void k_to_half(const float *__restrict__ x, in
 
 using GemmFn = void (*)(GemmArgs);
 
-template <bool BF16, bool GATEUP>
+template <bool BF16, bool GATEUP, int BMT>
 GemmFn pick_fmt(int fmt) {
   switch (fmt) {
-  case NX_FMT_Q4_K: return k_gemm<NX_FMT_Q4_K, BF16, GATEUP>;
-  case NX_FMT_Q8_0: return k_gemm<NX_FMT_Q8_0, BF16, GATEUP>;
-  case NX_FMT_Q4_0: return k_gemm<NX_FMT_Q4_0, BF16, GATEUP>;
-  case NX_FMT_F32: return k_gemm<NX_FMT_F32, BF16, GATEUP>;
+  case NX_FMT_Q4_K: return k_gemm<NX_FMT_Q4_K, BF16, GATEUP, BMT>;
+  case NX_FMT_Q8_0: return k_gemm<NX_FMT_Q8_0, BF16, GATEUP, BMT>;
+  case NX_FMT_Q4_0: return k_gemm<NX_FMT_Q4_0, BF16, GATEUP, BMT>;
+  case NX_FMT_F32: return k_gemm<NX_FMT_F32, BF16, GATEUP, BMT>;
   }
   return nullptr;
 }
 
-GemmFn pick(int fmt, bool bf16, bool gateup) {
-  if (bf16) return gateup ? pick_fmt<true, true>(fmt) : pick_fmt<true, false>(fmt);
-  return gateup ? pick_fmt<false, true>(fmt) : pick_fmt<false, false>(fmt);
+GemmFn pick(int fmt, bool bf16, bool gateup, int bm) {
+  if (gateup) return bf16 ? pick_fmt<true, true, BM_GATEUP>(fmt) : pick_fmt<false, true, BM_GATEUP>(fmt);
+  if (bm == BM_DOWN_WIDE)
+    return bf16 ? pick_fmt<true, false, BM_DOWN_WIDE>(fmt) : pick_fmt<false, false, BM_DOWN_WIDE>(fmt);
+  return bf16 ? pick_fmt<true, false, BM_GATEUP>(fmt) : pick_fmt<false, false, BM_GATEUP>(fmt);
 }
 
 void fill_weights(GemmArgs &a, const nx_experts *ex, bool gateup) {
@@ -984,7 +1002,8 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   GemmArgs a{};
   fill_weights(a, ex, gateup);
   a.offsets = p.offsets;
-  a.tiles = p.tiles;
+  a.tiles = gateup ? p.tiles : p.tiles_down;
+  const int max_tiles = gateup ? p.max_tiles : p.max_tiles_down;
   a.E = ex->E;
   a.T = p.T;
   a.k = p.k;
@@ -1018,16 +1037,16 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   // expert) 0.98 -> 1.17 ms with it, so it keeps the split.
   const long pairs = (long)p.T * p.k;
   const long active = std::max<long>(1, std::min<long>(ex->E, pairs));
-  a.xcd_split = gateup ? (pairs <= 2L * BM * active ? 2 : 1) : 0;
+  a.xcd_split = gateup ? (pairs <= 2L * BM_GATEUP * active ? 2 : 1) : 0;
   // enough workgroups for the order at the largest M-tile count
-  const long per = a.xcd_split == 1 ? 8L * ((a.n_tiles + 7) / 8) * p.max_tiles
-                   : a.xcd_split == 2 ? 8L * (((long)a.n_tiles * p.max_tiles + 7) / 8)
-                                      : (long)a.n_tiles * p.max_tiles;
+  const long per = a.xcd_split == 1 ? 8L * ((a.n_tiles + 7) / 8) * max_tiles
+                   : a.xcd_split == 2 ? 8L * (((long)a.n_tiles * max_tiles + 7) / 8)
+                                      : (long)a.n_tiles * max_tiles;
   a.ksplit = gateup ? 1 : p.ksplit;
   a.wg_per_split = (int)per;
   const long wgs = per * a.ksplit;
   if (wgs > 0x7FFFFFFFL) return fail(NX_ERR_UNSUPPORTED, "grouped GEMM grid too large");
-  GemmFn fn = pick(ex->fmt, p.bf16, gateup);
+  GemmFn fn = pick(ex->fmt, p.bf16, gateup, gateup ? BM_GATEUP : p.tile_m_down);
   if (!fn) return fail(NX_ERR_UNSUPPORTED, "no grouped-GEMM kernel for this format");
   const char *name = gateup ? "gemm_gateup" : "gemm_down";
   return launch(c, name,
@@ -1060,7 +1079,16 @@ int to_half_fmt(nx_ctx *c, const float *x, int T, int H, int kpad, bool bf16, ui
 
 }  // namespace
 
-int gemm_tile_m() { return BM; }
+int gemm_tile_m() { return BM_GATEUP; }
+
+int gemm_tile_m_down(int T, int k, int E) {
+  // pairs per active expert, with the active count expected under uniform
+  // routing, E (1 - (1 - k/E)^T)
+  const double kk = std::min(1.0, (double)k / E);
+  const double act = std::max(1.0, E * (1.0 - std::pow(1.0 - kk, (double)T)));
+  const double per = (double)T * k / act;
+  return per > 96.0 && per <= BM_DOWN_WIDE ? BM_DOWN_WIDE : BM_GATEUP;
+}
 
 // K splits of the down pass: the count (1-4, each split at least four loop
 // bodies) that best fills whole rounds of `slots` concurrent workgroups,

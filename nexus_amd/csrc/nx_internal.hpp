@@ -164,7 +164,10 @@ enum WsSlot {
   WS_MAT_Y,
   WS_MFV_PART, // gate/up partial sums of the split-activation MFMA path
   WS_DOWN_CNT, // arrival counters of the decode down pass's fused combine
+  WS_TILES_DOWN, // grouped-GEMM tile list of the down pass
+  WS_COUNT
 };
+static_assert(WS_COUNT <= 32, "workspace slots of a context");
 
 int ws_get(nx_ctx *c, int slot, size_t bytes, void **out);
 
@@ -214,7 +217,7 @@ int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int scor
 int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, int T, int k,
                    int E, int tile_m, int32_t *d_ecount, int32_t *d_offsets, int32_t *d_ptok,
                    int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles,
-                   int shared_T);
+                   int shared_T, int tile_m2 = 0, int32_t *d_tiles2 = nullptr);
 // router + permutation in one workgroup, for small batches; d_tiles
 // (optional) as for launch_permute, without shared-expert tiles
 bool route_permute_fusable(int T, int E, int k);
@@ -293,8 +296,11 @@ struct GemmPlan {
   const int32_t *perm_token;
   const int32_t *offsets;
   const int32_t *active;
-  const int32_t *tiles;  // tile list from the permutation kernel
+  const int32_t *tiles;  // tile list from the permutation kernel (gate/up M-tiles)
   int max_tiles;         // grid bound for the tile list
+  const int32_t *tiles_down;  // the down pass's tile list (its own M-tile height)
+  int max_tiles_down;
+  int tile_m_down;
   void *act;             // [pairs_total][act_stride] half precision
   int act_stride;
   float *ypair;
@@ -327,7 +333,8 @@ struct MfvPlan {
 int launch_mfv(nx_ctx *c, const MfvPlan &p);
 int mfv_max_tiles(int T, int k, int E, bool shared);
 constexpr int kMfvTileM = 16;
-int gemm_tile_m();
+int gemm_tile_m();                         // gate/up M-tile height
+int gemm_tile_m_down(int T, int k, int E);  // down M-tile height for a batch
 int gemm_down_ksplit(int fmt, int F, int H, int tiles, int slots);
 // width of a row of GEMM operands (operand order pads to whole scale windows)
 int gemm_kpad(int fmt, int cols);

@@ -82,7 +82,8 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
     const int32_t *__restrict__ rexp, const int32_t *__restrict__ rcnt, int T, int k, int E,
     int W, int tile_m, int32_t *__restrict__ ecount, int32_t *__restrict__ offsets,
     int32_t *__restrict__ ptok, int32_t *__restrict__ pslot, int32_t *__restrict__ inv,
-    int32_t *__restrict__ active, int32_t *__restrict__ tiles, int shared_T) {
+    int32_t *__restrict__ active, int32_t *__restrict__ tiles, int shared_T, int tile_m2,
+    int32_t *__restrict__ tiles2) {
   __shared__ int cnt[PERM_THREADS];
   __shared__ int base[PERM_THREADS];
   __shared__ int run[PERM_THREADS];
@@ -128,25 +129,28 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
   const int n_active = total;
   if (tid < E && c > 0) active[act] = tid;
   if (tid == 0) active[E] = n_active;
-  // tile list for the grouped GEMM: (expert, first row) per tile_m rows
-  if (tiles != nullptr) {
-    const int nt = tid < E ? (c + tile_m - 1) / tile_m : 0;
+  // tile lists for the grouped GEMM: (expert, first row) per tm rows, the
+  // shared expert's tiles last; a second list for a second tile height
+  auto tile_list = [&](int tm, int32_t *out) {
+    const int nt = tid < E ? (c + tm - 1) / tm : 0;
     const int tb = block_exclusive_scan(nt, wave_tot, &total);
     const int ntiles = total;
     for (int j = 0; j < nt; ++j) {
-      tiles[2 + 2 * (tb + j)] = tid;
-      tiles[2 + 2 * (tb + j) + 1] = j * tile_m;
+      out[2 + 2 * (tb + j)] = tid;
+      out[2 + 2 * (tb + j) + 1] = j * tm;
     }
-    const int nshared = (shared_T + tile_m - 1) / tile_m;
+    const int nshared = (shared_T + tm - 1) / tm;
     for (int j = tid; j < nshared; j += PERM_THREADS) {
-      tiles[2 + 2 * (ntiles + j)] = E;
-      tiles[2 + 2 * (ntiles + j) + 1] = j * tile_m;
+      out[2 + 2 * (ntiles + j)] = E;
+      out[2 + 2 * (ntiles + j) + 1] = j * tm;
     }
     if (tid == 0) {
-      tiles[0] = ntiles + nshared;
-      tiles[1] = 0;
+      out[0] = ntiles + nshared;
+      out[1] = 0;
     }
-  }
+  };
+  if (tiles != nullptr) tile_list(tile_m, tiles);
+  if (tiles2 != nullptr) tile_list(tile_m2, tiles2);
   __syncthreads();
   // ranks: chunks of CT = 32*W tokens, one token per thread
   const int CT = 32 * W;
@@ -495,7 +499,7 @@ int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int scor
 int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, int T, int k,
                    int E, int tile_m, int32_t *d_ecount, int32_t *d_offsets, int32_t *d_ptok,
                    int32_t *d_pslot, int32_t *d_inv, int32_t *d_active, int32_t *d_tiles,
-                   int shared_T) {
+                   int shared_T, int tile_m2, int32_t *d_tiles2) {
   if (E > PERM_THREADS) return fail(NX_ERR_UNSUPPORTED, "permutation supports at most 1024 experts");
   int W = PERM_WORDS / (E > 0 ? E : 1);
   if (W > PERM_THREADS / 32) W = PERM_THREADS / 32;
@@ -505,7 +509,7 @@ int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, i
     go(c, k_permute, dim3(1), dim3(PERM_THREADS), 0, d_expert, d_count, T, k, E, W,
                                                  tile_m > 0 ? tile_m : 1, d_ecount, d_offsets,
                                                  d_ptok, d_pslot, d_inv, d_active, d_tiles,
-                                                 shared_T);
+                                                 shared_T, tile_m2 > 0 ? tile_m2 : 1, d_tiles2);
   });
 }
 
