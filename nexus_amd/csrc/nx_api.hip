@@ -1038,7 +1038,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   auto tiles_bound = [&](int tm) {
     return (int)(((long)T * k + tm - 1) / tm + active_max + (shared ? ((long)T + tm - 1) / tm : 0));
   };
-  const int tm = gemm_tile_m(), tm_down = gemm_tile_m_down(T, k, E);
+  const int tm = gemm_tile_m(ex->fmt, true, T, k, E), tm_down = gemm_tile_m(ex->fmt, false, T, k, E);
   const int max_tiles = tiles_bound(tm), max_tiles_down = tiles_bound(tm_down);
   int32_t *d_tiles, *d_tiles_down;
   NX_TRY(ws(c, WS_TILES, 2 + 2 * (size_t)max_tiles, &d_tiles));
@@ -1060,9 +1060,9 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   const int ksplit =
       gemm_down_ksplit(ex->fmt, std::max(ex->F, ex->Fs), H, max_tiles_down, 2 * c->num_cu);
   NX_TRY(ws(c, WS_YPAIR, (size_t)ksplit * pairs_total * H, &d_ypair));
-  GemmPlan mp{ex,       T,      k,          bf16,          d_x,  d_pt,     d_off,
-              d_act,    d_tiles, max_tiles, d_tiles_down, max_tiles_down, tm_down, d_acth,
-              act_stride, d_ypair, d_xh,    x_stride,     pairs_total, ksplit};
+  GemmPlan mp{ex,        T,       k,         bf16, d_x,          d_pt,           d_off,
+              d_act,     d_tiles, max_tiles, tm,   d_tiles_down, max_tiles_down, tm_down,
+              d_acth,    act_stride, d_ypair, d_xh, x_stride,    pairs_total,    ksplit};
   NX_TRY(launch_gemm_gateup(c, mp));
   NX_TRY(launch_gemm_down(c, mp));
   NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out, ksplit,

@@ -8,7 +8,7 @@
 //   down:    y[p] = W_down . act[p]  (fp32), then the route-weighted combine.
 //
 // Work decomposition.  The permutation kernel lists M-tiles (expert, first
-// pair) of BM pairs (128 for gate/up; 128 or 160 for down: one list each); the 1-D
+// pair) of BM pairs (128 or 160, for gate/up and for down: one list each); the 1-D
 // grid covers (M-tile, 128-row N-tile) pairs in an XCD-aware order (see
 // k_gemm; extra workgroups exit).  A workgroup of 4 waves owns a BM x 64NT
 // output tile (gate/up: two of them, for the gate and the up rows); wave w
@@ -52,16 +52,17 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-// Pairs per M-tile.  Gate/up's two matrices' accumulators leave room for
-// 128 (160 spilled: Qwen3 T = 512 gate/up 101 -> 156 us).  The down pass
-// takes 160 when experts hold about 100-160 pairs each, so that most of them
-// stream and decode their weights once instead of twice (DeepSeek T = 4096,
-// ~128 pairs per expert: down 1.76 -> 1.45 ms), and 128 otherwise (Qwen3
-// T = 512, 32 per expert: 80 -> 85 us with 160; the Mixtral prefill, ~500
-// per expert, gains 13 us in the down pass and loses 20 us to a second K
-// split).  With 160 the down pass's LDS ring is 80 KB: two workgroups fill
-// a CU.
-constexpr int BM_GATEUP = 128, BM_DOWN_WIDE = 160;
+// Pairs per M-tile: 128, or 160 when experts hold about 100-160 pairs each,
+// so that most of them stream and decode their weights once instead of
+// twice (DeepSeek T = 4096, ~128 pairs per expert: gate/up 2.82 -> 2.44 ms,
+// down 1.76 -> 1.45 ms).  Elsewhere 128 is as fast or faster (Qwen3 T = 512,
+// 32 per expert: down 80 -> 85 us with 160; the Mixtral prefill, ~500 per
+// expert, gains 13 us in the down pass and loses 20 us to a second K
+// split).  Gate/up on 160-pair tiles holds its two matrices' accumulators
+// with one code buffer (codes one step ahead) and one M-tile per scheduling
+// group; Q8_0's operands do not fit beside them, so Q8_0 gate/up stays at
+// 128.  With 160 the LDS ring is 80 KB: two workgroups fill a CU.
+constexpr int BM_GATEUP = 128, BM_WIDE = 160;
 constexpr int BK = 64;    // K positions per step
 
 template <bool BF16>
@@ -488,12 +489,14 @@ __host__ __device__ constexpr int gemm_nt(int fmt, bool gateup) {
 #ifndef NX_GEMM_GRP_Q4
 #define NX_GEMM_GRP_Q4 1
 #endif
-template <int FMT, bool GATEUP>
+template <int FMT, bool GATEUP, int BM>
 struct GemmShape {
   static constexpr int NT = gemm_nt(FMT, GATEUP);
   static constexpr bool Q4 = FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0;
   static constexpr int GRP = Q4 ? NX_GEMM_GRP_Q4 : 1;
-  static constexpr int WDIST = Q4 ? NX_GEMM_WDIST_Q4 : WDIST_CFG;
+  // gate/up on 160-pair tiles fetches codes one step ahead: one code buffer,
+  // so that its 160 accumulators fit beside the operands without spilling
+  static constexpr int WDIST = Q4 ? (GATEUP && BM > BM_GATEUP ? 1 : NX_GEMM_WDIST_Q4) : WDIST_CFG;
   static constexpr bool META2 = FMT == NX_FMT_Q8_0 || (Q4 && NX_GEMM_META2_Q4);
   static constexpr int OCC = (NT == 4 || FMT == NX_FMT_F32) ? 1 : 2;
 };
@@ -539,10 +542,10 @@ struct LoadSchedule {
 };
 
 template <int FMT, bool BF16, bool GATEUP, int BMT>
-__global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(const GemmArgs g) {
+__global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gemm(const GemmArgs g) {
   using Op = OpT<BF16>;
   using V8 = typename Op::V8;
-  using Shape = GemmShape<FMT, GATEUP>;
+  using Shape = GemmShape<FMT, GATEUP, BMT>;
   constexpr int NT = Shape::NT;
   constexpr int GRP = Shape::GRP;
   static_assert(GRP == 1 || GRP == 2 || GRP == 4, "code load groups");
@@ -557,7 +560,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   constexpr int NMB = META2 ? 2 : 1;
   constexpr int WDIST = Shape::WDIST;
   // code buffers (steps mod NBUF)
-  constexpr int NBUF = GRP > 1 ? 2 * GRP : (WDIST <= 2 ? 2 : (WDIST <= 4 ? 4 : 8));
+  constexpr int NBUF = GRP > 1 ? 2 * GRP : (WDIST <= 1 ? 1 : (WDIST <= 2 ? 2 : (WDIST <= 4 ? 4 : 8)));
   static_assert(GRP > 1 || WDIST <= NBUF, "code buffers");  // issued after the decode
   // a window's double-buffered scales are fetched after the last decode of
   // the window two back
@@ -572,7 +575,9 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP>::OCC)) void k_gemm(con
   static_assert(BM % 32 == 0, "whole activation loads per wave");
   constexpr int MB = BM / 16;  // 16-pair MFMA row sets per tile
   constexpr int NA = BM / 32;  // activation loads per wave and step (8 rows each)
-  constexpr int IG = GATEUP || MB % 4 ? 2 : 4;  // M-tiles per scheduling group
+  // M-tiles per scheduling group (gate/up on 160-pair tiles: one, for the
+  // registers)
+  constexpr int IG = GATEUP ? (BM > BM_GATEUP ? 1 : 2) : (MB % 4 ? 2 : 4);
   static_assert(MB % IG == 0, "whole scheduling groups");
   constexpr LoadSchedule sched{RING, WS, NA, NMAT * NT * n_code_loads<FMT>(),
                                NMAT * NT * n_meta_loads<FMT>(), WDIST, GRP, META2};
@@ -954,17 +959,23 @@ template <bool BF16, bool GATEUP, int BMT>
 GemmFn pick_fmt(int fmt) {
   switch (fmt) {
   case NX_FMT_Q4_K: return k_gemm<NX_FMT_Q4_K, BF16, GATEUP, BMT>;
-  case NX_FMT_Q8_0: return k_gemm<NX_FMT_Q8_0, BF16, GATEUP, BMT>;
   case NX_FMT_Q4_0: return k_gemm<NX_FMT_Q4_0, BF16, GATEUP, BMT>;
-  case NX_FMT_F32: return k_gemm<NX_FMT_F32, BF16, GATEUP, BMT>;
+  }
+  if constexpr (!GATEUP || BMT == BM_GATEUP) {
+    switch (fmt) {
+    case NX_FMT_Q8_0: return k_gemm<NX_FMT_Q8_0, BF16, GATEUP, BMT>;
+    case NX_FMT_F32: return k_gemm<NX_FMT_F32, BF16, GATEUP, BMT>;
+    }
   }
   return nullptr;
 }
 
 GemmFn pick(int fmt, bool bf16, bool gateup, int bm) {
+  if (bm == BM_WIDE) {
+    if (gateup) return bf16 ? pick_fmt<true, true, BM_WIDE>(fmt) : pick_fmt<false, true, BM_WIDE>(fmt);
+    return bf16 ? pick_fmt<true, false, BM_WIDE>(fmt) : pick_fmt<false, false, BM_WIDE>(fmt);
+  }
   if (gateup) return bf16 ? pick_fmt<true, true, BM_GATEUP>(fmt) : pick_fmt<false, true, BM_GATEUP>(fmt);
-  if (bm == BM_DOWN_WIDE)
-    return bf16 ? pick_fmt<true, false, BM_DOWN_WIDE>(fmt) : pick_fmt<false, false, BM_DOWN_WIDE>(fmt);
   return bf16 ? pick_fmt<true, false, BM_GATEUP>(fmt) : pick_fmt<false, false, BM_GATEUP>(fmt);
 }
 
@@ -1037,7 +1048,7 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   // expert) 0.98 -> 1.17 ms with it, so it keeps the split.
   const long pairs = (long)p.T * p.k;
   const long active = std::max<long>(1, std::min<long>(ex->E, pairs));
-  a.xcd_split = gateup ? (pairs <= 2L * BM_GATEUP * active ? 2 : 1) : 0;
+  a.xcd_split = gateup ? (pairs <= 2L * p.tile_m * active ? 2 : 1) : 0;
   // enough workgroups for the order at the largest M-tile count
   const long per = a.xcd_split == 1 ? 8L * ((a.n_tiles + 7) / 8) * max_tiles
                    : a.xcd_split == 2 ? 8L * (((long)a.n_tiles * max_tiles + 7) / 8)
@@ -1046,7 +1057,7 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   a.wg_per_split = (int)per;
   const long wgs = per * a.ksplit;
   if (wgs > 0x7FFFFFFFL) return fail(NX_ERR_UNSUPPORTED, "grouped GEMM grid too large");
-  GemmFn fn = pick(ex->fmt, p.bf16, gateup, gateup ? BM_GATEUP : p.tile_m_down);
+  GemmFn fn = pick(ex->fmt, p.bf16, gateup, gateup ? p.tile_m : p.tile_m_down);
   if (!fn) return fail(NX_ERR_UNSUPPORTED, "no grouped-GEMM kernel for this format");
   const char *name = gateup ? "gemm_gateup" : "gemm_down";
   return launch(c, name,
@@ -1079,15 +1090,14 @@ int to_half_fmt(nx_ctx *c, const float *x, int T, int H, int kpad, bool bf16, ui
 
 }  // namespace
 
-int gemm_tile_m() { return BM_GATEUP; }
-
-int gemm_tile_m_down(int T, int k, int E) {
+int gemm_tile_m(int fmt, bool gateup, int T, int k, int E) {
   // pairs per active expert, with the active count expected under uniform
   // routing, E (1 - (1 - k/E)^T)
   const double kk = std::min(1.0, (double)k / E);
   const double act = std::max(1.0, E * (1.0 - std::pow(1.0 - kk, (double)T)));
   const double per = (double)T * k / act;
-  return per > 96.0 && per <= BM_DOWN_WIDE ? BM_DOWN_WIDE : BM_GATEUP;
+  const bool wide_ok = !gateup || fmt == NX_FMT_Q4_K || fmt == NX_FMT_Q4_0;
+  return wide_ok && per > 96.0 && per <= BM_WIDE ? BM_WIDE : BM_GATEUP;
 }
 
 // K splits of the down pass: the count (1-4, each split at least four loop

@@ -298,6 +298,7 @@ struct GemmPlan {
   const int32_t *active;
   const int32_t *tiles;  // tile list from the permutation kernel (gate/up M-tiles)
   int max_tiles;         // grid bound for the tile list
+  int tile_m;            // gate/up M-tile height
   const int32_t *tiles_down;  // the down pass's tile list (its own M-tile height)
   int max_tiles_down;
   int tile_m_down;
@@ -333,8 +334,8 @@ struct MfvPlan {
 int launch_mfv(nx_ctx *c, const MfvPlan &p);
 int mfv_max_tiles(int T, int k, int E, bool shared);
 constexpr int kMfvTileM = 16;
-int gemm_tile_m();                         // gate/up M-tile height
-int gemm_tile_m_down(int T, int k, int E);  // down M-tile height for a batch
+// grouped-GEMM M-tile height of a pass for a batch
+int gemm_tile_m(int fmt, bool gateup, int T, int k, int E);
 int gemm_down_ksplit(int fmt, int F, int H, int tiles, int slots);
 // width of a row of GEMM operands (operand order pads to whole scale windows)
 int gemm_kpad(int fmt, int cols);

@@ -231,10 +231,11 @@ MFMA_TOL = 1e-2
     (Q8_0, 4, 512, 640, 2, 700, 1.2),
     (Q4_K, 4, 512, 768, 2, 600, None),
     (Q4_0, 2, 256, 320, 1, 400, None),
-    # about 100-160 pairs per expert: the down pass on 160-pair M-tiles
-    # (gate/up on 128), some experts past 160 with Zipf-skewed counts
+    # about 100-160 pairs per expert: 160-pair M-tiles (Q8_0: down only),
+    # some experts past 160 with Zipf-skewed counts
     (Q8_0, 4, 512, 512, 2, 250, None),
     (Q4_K, 8, 256, 512, 2, 560, 1.1),
+    (Q4_0, 4, 256, 256, 2, 260, None),
 ])
 def test_layer_mfma_parity(ctx, path, fmt, E, H, F, k, T, zipf):
     L = Layer(fmt, E, H, F, k, T, seed=3 * E + H + F + T, zipf=zipf)
@@ -248,9 +249,8 @@ def test_layer_mfma_shared_expert_sigmoid(ctx):
     L = Layer(Q4_K, 16, 512, 512, 4, 96, seed=5, shared_F=512, score_mode=1)
     say("layer mfma shared + sigmoid")
     assert rel_l2(run_layer(ctx, L, nx.PATH_MFMA_F16), L.oracle_out()) <= MFMA_TOL
-    # the shared expert's 300 tokens over three gate/up M-tiles and two of
-    # the down pass (150 pairs per routed expert: 160-pair tiles), the last
-    # partial
+    # the shared expert's 300 tokens over two 160-pair M-tiles (150 pairs
+    # per routed expert), the last partial
     L = Layer(Q4_K, 4, 512, 512, 2, 300, seed=6, shared_F=512, score_mode=1)
     say("layer mfma shared + sigmoid, many pairs per expert")
     assert rel_l2(run_layer(ctx, L, nx.PATH_MFMA_BF16), L.oracle_out()) <= MFMA_TOL
