@@ -291,10 +291,11 @@ __global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__
 }
 
 // The exact prologue of one MoE block (RMSNorm, then the router logits of
-// the normalised row) in one launch: workgroup (g, t) takes token t and
+// the normalised row) in one launch, or (NORM false) exact router logits of
+// few tokens by themselves: workgroup (g, t) takes token t and
 // experts 8g .. 8g+7, four waves, two router chains per wave (one per 32-lane
 // half); every wave also runs the sum of squares itself.  Requires
-// H % 4 == 0, H <= BP_MAXH and 16-byte aligned rows.
+// H % 4 == 0, 0 < H <= BP_MAXH and 16-byte aligned rows.
 //
 // A sequential f32 sum is bound by its dependent adds, and it reaches that
 // bound only when every operand is already in a register: reading operands
@@ -328,6 +329,7 @@ constexpr int BP_RUN4 = BP_RUN / 4;      // float4 per run
 constexpr int BP_MAXH = 32 * BP_RUN;     // 4096
 constexpr int BP_PAD4 = 32 * (BP_RUN4 + 1);  // padded row, in float4
 
+template <bool NORM>
 __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict__ x,
                                                         const float *__restrict__ nw, float eps,
                                                         const float *__restrict__ W, int E, int H,
@@ -354,7 +356,7 @@ __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict_
     for (int j = 0; j < XJ; ++j) {
       const int i = min(j * 256 + tid, H4 - 1);
       xv[j] = xr4[i];
-      nv[j] = nw4[i];
+      if constexpr (NORM) nv[j] = nw4[i];
     }
   }
 #pragma unroll
@@ -379,33 +381,33 @@ __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict_
     xs[pad(i)] = xv[j];
   }
   __syncthreads();  // the row is in LDS
-  // 2. the sum of squares, run r (float4 S4 r .. of the row) in lane r
-  float ss = 0.f;
-  {
-    float4 q[S4];
-#pragma unroll
-    for (int k = 0; k < S4; ++k) {
-      const float4 v = xs[pad(lane * S4 + k)];
-      q[k] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
-    }
-    const int nsq = (H4 + S4 - 1) / S4;
-    for (int r = 0; r < nsq; ++r) {
-      float a = ss;
+  if constexpr (NORM) {
+    // 2. the sum of squares, run r (float4 S4 r .. of the row) in lane r
+    float ss = 0.f;
+    {
+      float4 q[S4];
 #pragma unroll
       for (int k = 0; k < S4; ++k) {
-        a = a + q[k].x;
-        a = a + q[k].y;
-        a = a + q[k].z;
-        a = a + q[k].w;
+        const float4 v = xs[pad(lane * S4 + k)];
+        q[k] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
       }
-      ss = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), r));
+      const int nsq = (H4 + S4 - 1) / S4;
+      for (int r = 0; r < nsq; ++r) {
+        float a = ss;
+#pragma unroll
+        for (int k = 0; k < S4; ++k) {
+          a = a + q[k].x;
+          a = a + q[k].y;
+          a = a + q[k].z;
+          a = a + q[k].w;
+        }
+        ss = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), r));
+      }
     }
-  }
-  const float rs = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
-  // 3. the normalised row (into the shared buffer once every wave has read
-  // its squares), then the products of each lane's run
-  __syncthreads();
-  {
+    const float rs = 1.0f / __builtin_sqrtf(ss / (float)H + eps);
+    // 3. the normalised row, into the shared buffer once every wave has
+    // read its squares
+    __syncthreads();
     float4 *xo4 = reinterpret_cast<float4 *>(xn + (size_t)t * H);
 #pragma unroll
     for (int j = 0; j < XJ; ++j) {
@@ -416,8 +418,9 @@ __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict_
       xs[pad(i)] = o;
       if (blockIdx.x == 0 && i < H4) xo4[i] = o;
     }
+    __syncthreads();
   }
-  __syncthreads();
+  // the products of each lane's run
   float4 p[BP_RUN4];
   {
     const float4 *my = ws[wave][half];
@@ -651,6 +654,7 @@ void release_blas(nx_ctx *c) {
 
 // chains (token, expert pairs) up to which the exact path uses k_logits_chain8
 constexpr long LOGITS_CHAIN8_MAX = 16384;
+constexpr long LOGITS_RUNS_MAX_WG = 256;  // workgroups of the register-run chains
 // fast path: tokens up to which k_logits_dot is used
 constexpr int LOGITS_DOT_MAX_T = 8;
 
@@ -664,6 +668,16 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
   // cannot load whole (unaligned, H % 4 != 0) in both modes
   const bool dot = !exact && vec && T <= LOGITS_DOT_MAX_T;
   const bool chain8 = !vec || (exact && chains <= LOGITS_CHAIN8_MAX);
+  // exact, rows up to 4096, up to one round of workgroups (each holds a CU's
+  // LDS): the register-run chains of the block prologue without its RMSNorm
+  // (H > 0: the kernel clamps its load indices to the row's last float4)
+  if (exact && vec && H > 0 && H <= BP_MAXH && (long)T * ((E + 7) / 8) <= LOGITS_RUNS_MAX_WG) {
+    const dim3 grid((unsigned)((E + 7) / 8), (unsigned)T);
+    return launch(c, "router_logits_runs", [&] {
+      go(c, k_block_prologue<false>, grid, dim3(256), 0, d_x, nullptr, 0.f, d_w, E, H, nullptr,
+         d_out);
+    });
+  }
   if (chain8) {
     const unsigned grid = (unsigned)((chains + 7) / 8);
     return launch(c, "router_logits_chain8", [&] {
@@ -713,7 +727,7 @@ int launch_block_prologue(nx_ctx *c, const float *d_x, const float *d_nw, float 
     return fail(NX_ERR_UNSUPPORTED, "block prologue: row shape or alignment not supported");
   const dim3 grid((unsigned)((E + 7) / 8), (unsigned)T);
   return launch(c, "block_prologue", [&] {
-    go(c, k_block_prologue, grid, dim3(256), 0, d_x, d_nw, eps, d_w, E, H, d_xn, d_logits);
+    go(c, k_block_prologue<true>, grid, dim3(256), 0, d_x, d_nw, eps, d_w, E, H, d_xn, d_logits);
   });
 }
 
