@@ -45,7 +45,8 @@ PATHS = {
     "qwen3_q4k_t64": [nx.PATH_GEMV, nx.PATH_MFMA_SPLIT],
     "qwen3_q4k_t512": [nx.PATH_MFMA_SPLIT, nx.PATH_MFMA_F16, nx.PATH_MFMA_BF16],
     "mixtral_q8_0_prefill_t2048": [nx.PATH_GEMV, nx.PATH_MFMA_F16, nx.PATH_MFMA_BF16],
-    "deepseek_q4k_sigmoid_shared_t4096": [nx.PATH_GEMV, nx.PATH_MFMA_F16, nx.PATH_MFMA_BF16],
+    "deepseek_q4k_sigmoid_shared_t4096": [nx.PATH_GEMV, nx.PATH_MFMA_SPLIT, nx.PATH_MFMA_F16,
+                                          nx.PATH_MFMA_BF16],
 }
 
 
