@@ -292,16 +292,17 @@ __global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__
 
 // The exact prologue of one MoE block (RMSNorm, then the router logits of
 // the normalised row) in one launch, or (NORM false) exact router logits of
-// few tokens by themselves: workgroup (g, t) takes token t and
-// experts 8g .. 8g+7, four waves, two router chains per wave (one per 32-lane
-// half); every wave also runs the sum of squares itself.  Requires
-// H % 4 == 0, 0 < H <= BP_MAXH and 16-byte aligned rows.
+// few tokens by themselves: workgroup (g, t) takes token t and CPG experts,
+// four waves with one router chain per LPC lanes (LPC = 32: two chains per
+// wave, 8 per workgroup, rows up to 4096; LPC = 64: one per wave, 4 per
+// workgroup, rows up to 7168); every wave also runs the sum of squares
+// itself.  Requires H % 4 == 0, 0 < H <= LPC RUN and 16-byte aligned rows.
 //
 // A sequential f32 sum is bound by its dependent adds, and it reaches that
 // bound only when every operand is already in a register: reading operands
 // from LDS or memory while the chain runs roughly doubles its time.  So each
-// chain is cut into runs of BP_RUN consecutive columns, run r held in the
-// registers of lane r of the chain's 32 lanes, loaded and formed before the
+// chain is cut into LPC runs of RUN consecutive columns, run r held in the
+// registers of lane r of the chain's lanes, loaded and formed before the
 // chain starts.  Every lane adds its run to the chain's value on entry (one
 // instruction advances all lanes); the value lane r ends with is the chain's
 // value after run r, read out with readlane and handed to run r + 1.  The
@@ -309,43 +310,54 @@ __global__ __launch_bounds__(128) void k_logits_chain8(const float *__restrict__
 // the column-order chain.
 //
 // Rows reach the runs through LDS: coalesced 16-byte loads, stored run by
-// run with one float4 of padding per run (BP_RUN4 + 1 float4 apart), so the
+// run with one float4 of padding per run (RUN / 4 + 1 float4 apart), so the
 // lanes reading their runs' k-th float4 hit different banks.
-//  1. Each wave stages its two router rows in its own LDS buffers; the row
-//     (x) goes to a shared buffer, zero-padded to 32 runs, and each thread
+//  1. Each wave stages its router rows in its own LDS buffers; the row (x)
+//     goes to a shared buffer, zero-padded to LPC runs, and each thread
 //     keeps its share of the row and of the norm weight in registers.
-//  2. The sum of squares: 64 runs of BP_RUN / 2 columns, run r in lane r
+//  2. The sum of squares: 64 runs of RUN LPC / 64 columns, run r in lane r
 //     (runs past the row end are skipped; a partial last run adds +0 to a
 //     sum that started at +0, which leaves it unchanged).
 //     rstd = 1 / sqrt(sum / H + eps).
 //  3. Each thread forms its share of the normalised row, (x_i rstd) w_i,
 //     into the shared buffer (workgroup 0 also writes it to xn); each lane
 //     then forms the products W[e][i] xn_i of its run.
-//  4. The router chains, run r of half h in lane 32 h + r.
+//  4. The router chains, run r of the chain on lanes LPC h .. in lane
+//     LPC h + r.
 // The arithmetic is that of the RMSNorm kernel and the chain kernel, so the
 // row and the logits are bit-identical to theirs.
-constexpr int BP_RUN = 128;              // columns per run of a router chain
-constexpr int BP_RUN4 = BP_RUN / 4;      // float4 per run
-constexpr int BP_MAXH = 32 * BP_RUN;     // 4096
-constexpr int BP_PAD4 = 32 * (BP_RUN4 + 1);  // padded row, in float4
+template <int LPC>
+struct PrologueShape {
+  static_assert(LPC == 32 || LPC == 64, "lanes per chain");
+  static constexpr int RUN = LPC == 32 ? 128 : 112;   // columns per run
+  static constexpr int RUN4 = RUN / 4;                // float4 per run
+  static constexpr int MAXH = LPC * RUN;              // 4096 / 7168
+  static constexpr int PAD4 = LPC * (RUN4 + 1);       // padded row, in float4
+  static constexpr int CPW = 64 / LPC;                // chains per wave
+  static constexpr int CPG = 4 * CPW;                 // chains (experts) per workgroup
+  static constexpr int S4 = RUN4 * LPC / 64;          // float4 per lane, sum of squares
+  static constexpr int RJ = LPC * RUN4 / 64;          // float4 per lane of a staged router row
+  static constexpr int XJ = LPC * RUN4 / 256;         // float4 per thread of the row
+  static_assert(LPC * RUN4 % 256 == 0, "whole float4 of the row per thread");
+};
+constexpr int BP_MAXH = PrologueShape<64>::MAXH;      // 7168
 
-template <bool NORM>
+template <bool NORM, int LPC>
 __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict__ x,
                                                         const float *__restrict__ nw, float eps,
                                                         const float *__restrict__ W, int E, int H,
                                                         float *__restrict__ xn,
                                                         float *__restrict__ logits) {
 #pragma clang fp contract(off)
-  constexpr int S4 = BP_RUN4 / 2;          // float4 per lane, sum of squares
-  constexpr int RJ = 32 * BP_RUN4 / 64;    // float4 per lane of a staged router row
-  constexpr int XJ = 32 * BP_RUN4 / 256;   // float4 per thread of the row
-  __shared__ float4 xs[BP_PAD4], ws[4][2][BP_PAD4];  // 152 KB
+  using PS = PrologueShape<LPC>;
+  constexpr int RUN4 = PS::RUN4, CPW = PS::CPW, S4 = PS::S4, RJ = PS::RJ, XJ = PS::XJ;
+  __shared__ float4 xs[PS::PAD4], ws[4][CPW][PS::PAD4];  // 152 KB / 148.5 KB
   const int t = blockIdx.y, tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, half = lane >> 5, hl = lane & 31;
-  const int e0 = blockIdx.x * 8 + wave * 2;  // the wave's experts: e0 (half 0), e0 + 1
+  const int wave = tid >> 6, lane = tid & 63, hl = lane % LPC, ch = lane / LPC;
+  const int e0 = blockIdx.x * PS::CPG + wave * CPW;  // the wave's experts: e0 .. e0 + CPW - 1
   const int H4 = H >> 2;
   const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  auto pad = [](int i) { return i + i / BP_RUN4; };  // float4 i of the row -> LDS slot
+  auto pad = [](int i) { return i + i / RUN4; };  // float4 i of the row -> LDS slot
   // 1. loads with indices clamped into the rows and values selected
   // afterwards: no branches, so every load is issued before the first wait
   float4 xv[XJ], nv[XJ];
@@ -360,7 +372,7 @@ __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict_
     }
   }
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < CPW; ++h) {
     const int e = e0 + h;
     const float4 *r4 = reinterpret_cast<const float4 *>(W + (size_t)(e < E ? e : 0) * H);
     float4 wr[RJ];
@@ -421,32 +433,32 @@ __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict_
     __syncthreads();
   }
   // the products of each lane's run
-  float4 p[BP_RUN4];
+  float4 p[RUN4];
   {
-    const float4 *my = ws[wave][half];
+    const float4 *my = ws[wave][ch];
 #pragma unroll
-    for (int k = 0; k < BP_RUN4; ++k) {
-      const int c = hl * (BP_RUN4 + 1) + k;
+    for (int k = 0; k < RUN4; ++k) {
+      const int c = hl * (RUN4 + 1) + k;
       const float4 w = my[c], o = xs[c];
       p[k] = make_float4(w.x * o.x, w.y * o.y, w.z * o.z, w.w * o.w);
     }
   }
-  // 4. the two router chains, run r of half h in lane 32 h + r
-  const int nrt = (H4 + BP_RUN4 - 1) / BP_RUN4;
+  // 4. the router chains, run r of chain h in lane LPC h + r
+  const int nrt = (H4 + RUN4 - 1) / RUN4;
   float s0 = 0.f, s1 = 0.f;
   for (int r = 0; r < nrt; ++r) {
-    float a = half ? s1 : s0;
+    float a = (CPW == 2 && ch) ? s1 : s0;
 #pragma unroll
-    for (int k = 0; k < BP_RUN4; ++k) {
+    for (int k = 0; k < RUN4; ++k) {
       a = a + p[k].x;
       a = a + p[k].y;
       a = a + p[k].z;
       a = a + p[k].w;
     }
     s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), r));
-    s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32 + r));
+    if constexpr (CPW == 2) s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32 + r));
   }
-  if (hl == 0 && e0 + half < E) logits[(size_t)t * E + e0 + half] = half ? s1 : s0;
+  if (hl == 0 && e0 + ch < E) logits[(size_t)t * E + e0 + ch] = (CPW == 2 && ch) ? s1 : s0;
 }
 
 constexpr int TL_NS = 3;  // ring stages of the tiled kernel
@@ -668,14 +680,21 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
   // cannot load whole (unaligned, H % 4 != 0) in both modes
   const bool dot = !exact && vec && T <= LOGITS_DOT_MAX_T;
   const bool chain8 = !vec || (exact && chains <= LOGITS_CHAIN8_MAX);
-  // exact, rows up to 4096, up to one round of workgroups (each holds a CU's
+  // exact, rows up to 7168, up to one round of workgroups (each holds a CU's
   // LDS): the register-run chains of the block prologue without its RMSNorm
   // (H > 0: the kernel clamps its load indices to the row's last float4)
-  if (exact && vec && H > 0 && H <= BP_MAXH && (long)T * ((E + 7) / 8) <= LOGITS_RUNS_MAX_WG) {
-    const dim3 grid((unsigned)((E + 7) / 8), (unsigned)T);
+  const bool narrow = H <= PrologueShape<32>::MAXH;
+  const int cpg = narrow ? PrologueShape<32>::CPG : PrologueShape<64>::CPG;
+  if (exact && vec && H > 0 && H <= BP_MAXH &&
+      (long)T * ((E + cpg - 1) / cpg) <= LOGITS_RUNS_MAX_WG) {
+    const dim3 grid((unsigned)((E + cpg - 1) / cpg), (unsigned)T);
     return launch(c, "router_logits_runs", [&] {
-      go(c, k_block_prologue<false>, grid, dim3(256), 0, d_x, nullptr, 0.f, d_w, E, H, nullptr,
-         d_out);
+      if (narrow)
+        go(c, k_block_prologue<false, 32>, grid, dim3(256), 0, d_x, nullptr, 0.f, d_w, E, H,
+           nullptr, d_out);
+      else
+        go(c, k_block_prologue<false, 64>, grid, dim3(256), 0, d_x, nullptr, 0.f, d_w, E, H,
+           nullptr, d_out);
     });
   }
   if (chain8) {
@@ -725,9 +744,20 @@ int launch_block_prologue(nx_ctx *c, const float *d_x, const float *d_nw, float 
   if (T <= 0 || E <= 0) return NX_OK;
   if (!block_prologue_fits(H, d_x, d_nw, d_w, d_xn))
     return fail(NX_ERR_UNSUPPORTED, "block prologue: row shape or alignment not supported");
-  const dim3 grid((unsigned)((E + 7) / 8), (unsigned)T);
+  // runs of 128 columns on 32 lanes (rows up to 4096), else of 112 on 64
+  if (H <= PrologueShape<32>::MAXH) {
+    const dim3 grid((unsigned)((E + PrologueShape<32>::CPG - 1) / PrologueShape<32>::CPG),
+                    (unsigned)T);
+    return launch(c, "block_prologue", [&] {
+      go(c, k_block_prologue<true, 32>, grid, dim3(256), 0, d_x, d_nw, eps, d_w, E, H, d_xn,
+         d_logits);
+    });
+  }
+  const dim3 grid((unsigned)((E + PrologueShape<64>::CPG - 1) / PrologueShape<64>::CPG),
+                  (unsigned)T);
   return launch(c, "block_prologue", [&] {
-    go(c, k_block_prologue<true>, grid, dim3(256), 0, d_x, d_nw, eps, d_w, E, H, d_xn, d_logits);
+    go(c, k_block_prologue<true, 64>, grid, dim3(256), 0, d_x, d_nw, eps, d_w, E, H, d_xn,
+       d_logits);
   });
 }
 

@@ -117,8 +117,9 @@ def test_moe_block_exact(ctx, fmt, E, H, F, k, T, shared):
     (Q8_0, 20, 2048, 128, 4, 5),   # three expert groups, the last partial
     (Q8_0, 128, 1024, 64, 8, 2),   # sixteen groups per token
     (Q8_0, 12, 1056, 64, 2, 3),    # a partial last run
-    (Q8_0, 8, 4128, 64, 2, 3),     # just past the one launch's 4096 columns: three launches
-    (Q4_K, 12, 7168, 256, 2, 2),   # DeepSeek's width
+    (Q8_0, 8, 4128, 64, 2, 3),     # just past 4096: chains on 64 lanes, runs of 112 columns
+    (Q4_K, 12, 7168, 256, 2, 2),   # DeepSeek's width: 64 full runs, three expert groups
+    (Q8_0, 8, 7200, 64, 2, 2),     # wider than the one launch holds: three launches
     (Q8_0, 8, 10240, 64, 2, 2),
     (Q8_0, 8, 512, 64, 2, 64)])    # the most tokens the single launch takes
 def test_moe_block_exact_prologue(ctx, fmt, E, H, F, k, T):
@@ -135,7 +136,7 @@ def test_moe_block_exact_prologue(ctx, fmt, E, H, F, k, T):
     got = ex.block(hidden, norm_w, eps, router, k, path=nx.PATH_GEMV, exact=True)
     ran = set(ctx.profile_stats())
     ctx.profile(False)
-    fused = H % 4 == 0 and H <= 4096
+    fused = H % 4 == 0 and H <= 7168
     assert ("block_prologue" in ran) == fused, ran
     assert ("rms_sumsq_chain8" in ran) == (not fused), ran
     want = (hidden + ex.forward(normed, logits, k, path=nx.PATH_GEMV)).astype(np.float32)
@@ -144,7 +145,7 @@ def test_moe_block_exact_prologue(ctx, fmt, E, H, F, k, T):
     ex.close()
 
 
-@pytest.mark.parametrize("H", [1536, 4096])
+@pytest.mark.parametrize("H", [1536, 4096, 5120, 7168])  # chains of 32 and 64 lanes
 def test_moe_block_exact_prologue_special_rows(ctx, H):
     """Rows that stress the prologue's sum of squares: dyadic values (squares
     that land exactly halfway between representable sums), magnitudes across

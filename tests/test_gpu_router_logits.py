@@ -54,14 +54,16 @@ def fast_bound(w, x):
     return 2.0 * (H + 1) * U / (1 - (H + 1) * U) * absdot + 1e-38
 
 
-# (T, E, H): register-run chains (rows of whole float4 up to 4096, up to 256
-# groups of 8 experts: partial groups, a partial last run, the limit either
+# (T, E, H): register-run chains (rows of whole float4 up to 4096 on 32-lane
+# chains in groups of 8 experts, up to 7168 on 64-lane chains in groups of 4;
+# at most 256 groups: partial groups, partial last runs, the limit either
 # side), chain-kernel shapes, rows not a multiple of 4 floats or 32 columns,
 # then tiled grids with each register block (1x1: up to 256K chains, 2x2: up
 # to 1M, 4x4 beyond) and partial tiles
 EXACT_SHAPES = [
     (1, 8, 4096), (1, 128, 2048), (1, 256, 7168), (4, 8, 4096), (3, 60, 2880),
     (32, 8, 4096), (1, 20, 1056), (2, 128, 4), (16, 128, 1024), (17, 128, 1024),
+    (2, 10, 4100), (3, 7, 5000), (4, 256, 7168), (5, 256, 7168),
     (2, 7, 1001), (5, 3, 100), (1, 1, 1), (64, 256, 512),
     (300, 64, 512), (2100, 8, 256), (700, 40, 128), (1500, 12, 64),
     (1024, 256, 1024), (4096, 128, 256), (8192, 256, 64),
