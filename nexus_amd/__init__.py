@@ -304,6 +304,12 @@ class Context:
                                 1 if exact else 0, _p(out, _fp)))
         return out[:T, :H]
 
+    def rms_norm_dev(self, x_ptr: int, x_len: int, w_ptr: int, w_len: int, eps: float,
+                     num_tokens: int, hidden: int, out_ptr: int, exact: bool = True):
+        """nx_rms_norm_dev on device pointers (enqueued on the context's stream)."""
+        check(lib().nx_rms_norm_dev(self.h, _vp(x_ptr), x_len, _vp(w_ptr), w_len, eps,
+                                    num_tokens, hidden, 1 if exact else 0, _vp(out_ptr)))
+
     def route_topk(self, logits, num_tokens: int, num_experts: int, top_k: int,
                    score_mode: int = SCORE_SOFTMAX):
         lg = _f32(logits).ravel()

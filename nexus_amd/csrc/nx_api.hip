@@ -602,6 +602,7 @@ int nx_rms_norm_dev(nx_ctx *c, const float *x, size_t x_len, const float *w, siz
   NX_TRY(check_norm(x, x_len, w, w_len, T, H, out));
   if (T == 0 || H == 0) return NX_OK;
   if (!exact) return launch_rms_fast(c, x, w, eps, T, H, out);
+  if (rms_runs_fit(H, x, w, out)) return launch_rms_exact_runs(c, x, w, eps, T, H, out);
   float *d_s;
   NX_TRY(ws(c, WS_SUMSQ, (size_t)T, &d_s));
   NX_TRY(launch_sumsq_exact(c, x, T, H, d_s));

@@ -239,6 +239,10 @@ int launch_sumsq_exact(nx_ctx *c, const float *d_x, int T, int H, float *d_out);
 int launch_block_prologue(nx_ctx *c, const float *d_x, const float *d_nw, float eps,
                           const float *d_w, int T, int E, int H, float *d_xn, float *d_logits);
 bool block_prologue_fits(int H, const void *x, const void *nw, const void *w, const void *xn);
+// exact RMSNorm in one launch for rows of whole float4 up to 7168
+bool rms_runs_fit(int H, const void *x, const void *w, const void *out);
+int launch_rms_exact_runs(nx_ctx *c, const float *d_x, const float *d_w, float eps, int T, int H,
+                          float *d_out);
 int launch_rms_apply(nx_ctx *c, const float *d_x, const float *d_sumsq, const float *d_w,
                      float eps, int T, int H, float *d_out);
 int launch_rms_fast(nx_ctx *c, const float *d_x, const float *d_w, float eps, int T, int H,

@@ -15,7 +15,7 @@ import pytest
 
 import nexus_amd as nx
 import oracle
-from moe_cases import Q4_K, Q8_0, Layer, assert_same_bits, rel_l2
+from moe_cases import Q4_K, Q8_0, DeviceArray, Layer, assert_same_bits, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -29,13 +29,36 @@ def ctx():
     c.close()
 
 
-@pytest.mark.parametrize("T,H", [(1, 4096), (3, 7168), (33, 2048), (2, 1001), (4, 5), (9, 64)])
+# rows of whole float4 up to 4096 and up to 7168 (one wave per token, four
+# tokens per workgroup: partial workgroups, partial last runs), then rows the
+# two-launch chain path takes (not whole float4, or longer than 7168)
+@pytest.mark.parametrize("T,H", [(1, 4096), (3, 7168), (33, 2048), (5, 5120), (2, 4100),
+                                 (6, 4), (1, 1056), (2, 1001), (4, 5), (9, 64), (2, 7200)])
 def test_rms_norm_exact_bit_identical(ctx, T, H):
     rng = np.random.default_rng(T * 1000 + H)
     x = (rng.standard_normal((T, H)) * np.exp(rng.uniform(-3, 3, (T, 1)))).astype(np.float32)
     w = rng.standard_normal(H).astype(np.float32)
     got = ctx.rms_norm(x, w, 1e-5, exact=True)
     assert_same_bits(got, oracle.rms_norm(x, w, 1e-5))
+
+
+def test_rms_norm_dev_unaligned_and_reused(ctx):
+    # rows offset by one float: not 16-byte aligned, so the chain path runs;
+    # then the aligned copies, on the same buffers
+    T, H = 3, 2048
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    w = rng.standard_normal(H).astype(np.float32)
+    ref = oracle.rms_norm(x, w, 1e-5)
+    dx, dw, do = DeviceArray(T * H + 4), DeviceArray(H + 4), DeviceArray(T * H + 4, fill=np.nan)
+    for off in (1, 0, 1):
+        dx.upload(x, off)
+        dw.upload(w, off)
+        ctx.rms_norm_dev(dx.ptr + 4 * off, T * H, dw.ptr + 4 * off, H, 1e-5, T, H,
+                         do.ptr + 4 * off, exact=True)
+        ctx.sync()
+        o = do.download()
+        assert_same_bits(o[off:off + T * H].reshape(T, H), ref)
 
 
 def test_rms_norm_special_rows(ctx):
