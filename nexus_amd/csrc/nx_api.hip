@@ -1059,7 +1059,8 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   // the down pass splits K when that fills the CUs' rounds better; each
   // split writes its own partial sums, added by the combine
   const int ksplit =
-      gemm_down_ksplit(ex->fmt, std::max(ex->F, ex->Fs), H, max_tiles_down, 2 * c->num_cu);
+      gemm_down_ksplit(ex->fmt, std::max(ex->F, ex->Fs), H, max_tiles_down,
+                       gemm_wg_per_cu(ex->fmt, tm_down) * c->num_cu);
   NX_TRY(ws(c, WS_YPAIR, (size_t)ksplit * pairs_total * H, &d_ypair));
   GemmPlan mp{ex,        T,       k,         bf16, d_x,          d_pt,           d_off,
               d_act,     d_tiles, max_tiles, tm,   d_tiles_down, max_tiles_down, tm_down,

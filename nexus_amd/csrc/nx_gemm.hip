@@ -8,7 +8,7 @@
 //   down:    y[p] = W_down . act[p]  (fp32), then the route-weighted combine.
 //
 // Work decomposition.  The permutation kernel lists M-tiles (expert, first
-// pair) of BM pairs (128 or 160, for gate/up and for down: one list each); the 1-D
+// pair) of BM pairs (64, 128 or 160, for gate/up and for down: one list each); the 1-D
 // grid covers (M-tile, 128-row N-tile) pairs in an XCD-aware order (see
 // k_gemm; extra workgroups exit).  A workgroup of 4 waves owns a BM x 64NT
 // output tile (gate/up: two of them, for the gate and the up rows); wave w
@@ -62,7 +62,16 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 // with one code buffer (codes one step ahead) and one M-tile per scheduling
 // group; Q8_0's operands do not fit beside them, so Q8_0 gate/up stays at
 // 128.  With 160 the LDS ring is 80 KB: two workgroups fill a CU.
-constexpr int BM_GATEUP = 128, BM_WIDE = 160;
+// 64-pair tiles when experts hold at most 48 pairs each: a 32 KB ring and
+// a third (gate/up, 158 VGPRs) or fourth (down, 111 VGPRs) workgroup per
+// CU, so more waves hide the weight loads of the short tiles (Qwen3 T = 512:
+// gate/up 101 -> 90 us, down 81 -> 70 us; Mixtral T = 128: down 125 ->
+// 101 us; DeepSeek T = 256: 2.41 -> 2.17 ms).  At 64 pairs per expert
+// (Mixtral T = 256, Qwen3 T = 1024) they are slower (gate/up 226 -> 294,
+// 115 -> 136 us): the experts past 64 pairs stream their weights twice.
+constexpr int BM_GATEUP = 128, BM_WIDE = 160, BM_NARROW = 64;
+constexpr double NARROW_PER_MAX = 48.0;  // expected pairs per active expert
+constexpr int OCC_NARROW = 3;            // workgroups per CU the 64-pair gate/up is built for
 constexpr int BK = 64;    // K positions per step
 
 template <bool BF16>
@@ -498,7 +507,8 @@ struct GemmShape {
   // so that its 160 accumulators fit beside the operands without spilling
   static constexpr int WDIST = Q4 ? (GATEUP && BM > BM_GATEUP ? 1 : NX_GEMM_WDIST_Q4) : WDIST_CFG;
   static constexpr bool META2 = FMT == NX_FMT_Q8_0 || (Q4 && NX_GEMM_META2_Q4);
-  static constexpr int OCC = (NT == 4 || FMT == NX_FMT_F32) ? 1 : 2;
+  static constexpr int OCC =
+      (NT == 4 || FMT == NX_FMT_F32) ? 1 : (BM <= BM_NARROW ? OCC_NARROW : 2);
 };
 int gemm_bn(int fmt, bool gateup) { return 64 * gemm_nt(fmt, gateup); }
 
@@ -961,16 +971,21 @@ GemmFn pick_fmt(int fmt) {
   case NX_FMT_Q4_K: return k_gemm<NX_FMT_Q4_K, BF16, GATEUP, BMT>;
   case NX_FMT_Q4_0: return k_gemm<NX_FMT_Q4_0, BF16, GATEUP, BMT>;
   }
-  if constexpr (!GATEUP || BMT == BM_GATEUP) {
-    switch (fmt) {
-    case NX_FMT_Q8_0: return k_gemm<NX_FMT_Q8_0, BF16, GATEUP, BMT>;
-    case NX_FMT_F32: return k_gemm<NX_FMT_F32, BF16, GATEUP, BMT>;
-    }
+  if constexpr (!GATEUP || BMT <= BM_GATEUP) {
+    if (fmt == NX_FMT_Q8_0) return k_gemm<NX_FMT_Q8_0, BF16, GATEUP, BMT>;
+  }
+  if constexpr (BMT == BM_GATEUP || (!GATEUP && BMT == BM_WIDE)) {
+    if (fmt == NX_FMT_F32) return k_gemm<NX_FMT_F32, BF16, GATEUP, BMT>;
   }
   return nullptr;
 }
 
 GemmFn pick(int fmt, bool bf16, bool gateup, int bm) {
+  if (bm == BM_NARROW) {
+    if (gateup)
+      return bf16 ? pick_fmt<true, true, BM_NARROW>(fmt) : pick_fmt<false, true, BM_NARROW>(fmt);
+    return bf16 ? pick_fmt<true, false, BM_NARROW>(fmt) : pick_fmt<false, false, BM_NARROW>(fmt);
+  }
   if (bm == BM_WIDE) {
     if (gateup) return bf16 ? pick_fmt<true, true, BM_WIDE>(fmt) : pick_fmt<false, true, BM_WIDE>(fmt);
     return bf16 ? pick_fmt<true, false, BM_WIDE>(fmt) : pick_fmt<false, false, BM_WIDE>(fmt);
@@ -1096,8 +1111,15 @@ int gemm_tile_m(int fmt, bool gateup, int T, int k, int E) {
   const double kk = std::min(1.0, (double)k / E);
   const double act = std::max(1.0, E * (1.0 - std::pow(1.0 - kk, (double)T)));
   const double per = (double)T * k / act;
+  if (fmt != NX_FMT_F32 && per <= NARROW_PER_MAX) return BM_NARROW;
   const bool wide_ok = !gateup || fmt == NX_FMT_Q4_K || fmt == NX_FMT_Q4_0;
   return wide_ok && per > 96.0 && per <= BM_WIDE ? BM_WIDE : BM_GATEUP;
+}
+
+// workgroups per CU of the grouped GEMM on M-tiles of tile_m pairs
+int gemm_wg_per_cu(int fmt, int tile_m) {
+  if (fmt == NX_FMT_F32 || gemm_nt(fmt, false) == 4) return 1;
+  return tile_m <= BM_NARROW ? OCC_NARROW : 2;
 }
 
 // K splits of the down pass: the count (1-4, each split at least four loop

@@ -340,6 +340,7 @@ int mfv_max_tiles(int T, int k, int E, bool shared);
 constexpr int kMfvTileM = 16;
 // grouped-GEMM M-tile height of a pass for a batch
 int gemm_tile_m(int fmt, bool gateup, int T, int k, int E);
+int gemm_wg_per_cu(int fmt, int tile_m);
 int gemm_down_ksplit(int fmt, int F, int H, int tiles, int slots);
 // width of a row of GEMM operands (operand order pads to whole scale windows)
 int gemm_kpad(int fmt, int cols);

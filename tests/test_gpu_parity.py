@@ -236,6 +236,11 @@ MFMA_TOL = 1e-2
     (Q8_0, 4, 512, 512, 2, 250, None),
     (Q4_K, 8, 256, 512, 2, 560, 1.1),
     (Q4_0, 4, 256, 256, 2, 260, None),
+    # at most 48 pairs per expert: 64-pair M-tiles, with the Zipf-popular
+    # experts spread over several of them (full and partial)
+    (Q8_0, 16, 512, 640, 2, 300, 1.2),
+    (Q4_0, 16, 256, 320, 2, 200, 1.1),
+    (Q4_K, 16, 512, 768, 4, 150, None),
 ])
 def test_layer_mfma_parity(ctx, path, fmt, E, H, F, k, T, zipf):
     L = Layer(fmt, E, H, F, k, T, seed=3 * E + H + F + T, zipf=zipf)
@@ -246,6 +251,8 @@ def test_layer_mfma_parity(ctx, path, fmt, E, H, F, k, T, zipf):
 
 
 def test_layer_mfma_shared_expert_sigmoid(ctx):
+    # 24 pairs per routed expert: 64-pair M-tiles, the shared expert's 96
+    # tokens over two of them
     L = Layer(Q4_K, 16, 512, 512, 4, 96, seed=5, shared_F=512, score_mode=1)
     say("layer mfma shared + sigmoid")
     assert rel_l2(run_layer(ctx, L, nx.PATH_MFMA_F16), L.oracle_out()) <= MFMA_TOL
