@@ -165,6 +165,7 @@ enum WsSlot {
   WS_MFV_PART, // gate/up partial sums of the split-activation MFMA path
   WS_DOWN_CNT, // arrival counters of the decode down pass's fused combine
   WS_TILES_DOWN, // grouped-GEMM tile list of the down pass
+  WS_PERM_CHUNK, // per-chunk expert counts of the many-workgroup permutation
   WS_COUNT
 };
 static_assert(WS_COUNT <= 32, "workspace slots of a context");

@@ -223,6 +223,217 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute(
   }
 }
 
+// The permutation over many workgroups, for larger batches: chunk c (one
+// workgroup) holds tokens [32 W c, 32 W c + 32 W).  k_perm_count marks the
+// chunk's tokens in one bit row per expert (bit j of row e: token
+// 32 W c + j routes to e) and writes the chunk's count per expert.
+// k_perm_scatter rebuilds the rows, takes for each expert the sum over all
+// chunks (the expert's count) and over the chunks before its own, scans the
+// counts into the experts' bases, and places pair (t, r) of expert e at
+// base(e) + pairs of e in earlier chunks + set bits of e's row below token
+// t: the (token, slot) order of k_permute, so every output is the same.
+// Workgroup 0 also writes the counts, offsets, active list and tile lists.
+constexpr int PCH_THREADS = 256;
+constexpr int PCH_WORDS = 8192;   // LDS words per bit matrix (E W)
+constexpr int PCH_MAX_CHUNKS = 64;
+
+// the chunk's bit rows in `bits` (E W words), zeroed first
+__device__ __forceinline__ void chunk_bits(const int32_t *__restrict__ rexp,
+                                           const int32_t *__restrict__ rcnt, int T, int k, int E,
+                                           int W, int t0, uint32_t *bits) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < E * W; i += PCH_THREADS) bits[i] = 0;
+  __syncthreads();
+  const int np = 32 * W * k;
+  // four pairs per thread at a time, their loads issued together
+  for (int i0 = tid; i0 < np; i0 += 4 * PCH_THREADS) {
+    int ev[4], ok[4], tl[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j * PCH_THREADS;
+      const int l = i / k, r = i - l * k, t = t0 + l;
+      const bool in = i < np && t < T;
+      tl[j] = l;
+      ev[j] = in ? rexp[(size_t)t * k + r] : 0;
+      ok[j] = in ? r < rcnt[t] : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (ok[j]) atomicOr(&bits[ev[j] * W + (tl[j] >> 5)], 1u << (tl[j] & 31));
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(PCH_THREADS) void k_perm_count(const int32_t *__restrict__ rexp,
+                                                            const int32_t *__restrict__ rcnt,
+                                                            int T, int k, int E, int W,
+                                                            int32_t *__restrict__ chunk_cnt) {
+  __shared__ uint32_t bits[PCH_WORDS];
+  chunk_bits(rexp, rcnt, T, k, E, W, blockIdx.x * 32 * W, bits);
+  for (int e = threadIdx.x; e < E; e += PCH_THREADS) {
+    int c = 0;
+    for (int w = 0; w < W; ++w) c += __popc(bits[e * W + w]);
+    chunk_cnt[(size_t)blockIdx.x * E + e] = c;
+  }
+}
+
+__global__ __launch_bounds__(PCH_THREADS) void k_perm_scatter(
+    const int32_t *__restrict__ rexp, const int32_t *__restrict__ rcnt, int T, int k, int E,
+    int W, int nch, const int32_t *__restrict__ chunk_cnt, int tile_m,
+    int32_t *__restrict__ ecount, int32_t *__restrict__ offsets, int32_t *__restrict__ ptok,
+    int32_t *__restrict__ pslot, int32_t *__restrict__ inv, int32_t *__restrict__ active,
+    int32_t *__restrict__ tiles, int shared_T, int tile_m2, int32_t *__restrict__ tiles2) {
+  __shared__ uint32_t bits[PCH_WORDS];
+  __shared__ uint32_t pref[PCH_WORDS];
+  __shared__ int base[PERM_THREADS];  // E <= 1024
+  __shared__ int wave_tot[PCH_THREADS / 64];
+  __shared__ int total;
+  const int tid = threadIdx.x, ch = blockIdx.x, t0 = ch * 32 * W;
+  // the chunk's pairs, four per thread at a time (pair i0 + 256 j): routes
+  // and route counts.  A chunk of at most 1024 pairs is loaded once, before
+  // anything else, and kept in registers for the bit rows and the ranks.
+  const int np = 32 * W * k;
+  const bool onepass = np <= 4 * PCH_THREADS;
+  int ev[4], nr[4];
+  auto load_pairs = [&](int i0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j * PCH_THREADS;
+      const int l = i / k, r = i - l * k, t = t0 + l;
+      const bool in = i < np && t < T;
+      ev[j] = in ? rexp[(size_t)t * k + r] : 0;
+      nr[j] = in ? rcnt[t] : 0;
+    }
+  };
+  if (onepass) load_pairs(tid);
+  // experts 4 tid .. 4 tid + 3: their counts over all chunks and over the
+  // chunks before this one, the loads of 16 chunks issued together (one
+  // memory round trip per 16 chunks, not per chunk)
+  int tot[4] = {0, 0, 0, 0}, bef[4] = {0, 0, 0, 0};
+  constexpr int CB = 16;
+  for (int c0 = 0; c0 < nch; c0 += CB) {
+    int v[CB][4];
+#pragma unroll
+    for (int u = 0; u < CB; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = c0 + u, e = 4 * tid + j;
+        v[u][j] = c < nch && e < E ? chunk_cnt[(size_t)c * E + e] : 0;
+      }
+#pragma unroll
+    for (int u = 0; u < CB; ++u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        tot[j] += v[u][j];
+        bef[j] += c0 + u < ch ? v[u][j] : 0;
+      }
+  }
+  const int sum4 = tot[0] + tot[1] + tot[2] + tot[3];
+  const int b = block_exclusive_scan(sum4, wave_tot, &total);
+  const int npairs = total;
+  {
+    int eb = b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * tid + j;
+      if (e < E) {
+        base[e] = eb + bef[j];
+        if (ch == 0) {
+          ecount[e] = tot[j];
+          offsets[e] = eb;
+        }
+      }
+      eb += tot[j];
+    }
+  }
+  if (ch == 0) {  // workgroup-uniform
+    if (tid == 0) offsets[E] = npairs;
+    int na = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) na += (4 * tid + j < E && tot[j] > 0) ? 1 : 0;
+    int a = block_exclusive_scan(na, wave_tot, &total);
+    const int n_active = total;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * tid + j < E && tot[j] > 0) active[a++] = 4 * tid + j;
+    if (tid == 0) active[E] = n_active;
+    // tile lists: (expert, first row) per tm rows, the shared expert's last
+    auto tile_list = [&](int tm, int32_t *out) {
+      int nt4 = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) nt4 += 4 * tid + j < E ? (tot[j] + tm - 1) / tm : 0;
+      int tb = block_exclusive_scan(nt4, wave_tot, &total);
+      const int ntiles = total;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * tid + j;
+        const int nt = e < E ? (tot[j] + tm - 1) / tm : 0;
+        for (int q = 0; q < nt; ++q, ++tb) {
+          out[2 + 2 * tb] = e;
+          out[2 + 2 * tb + 1] = q * tm;
+        }
+      }
+      const int nshared = (shared_T + tm - 1) / tm;
+      for (int q = tid; q < nshared; q += PCH_THREADS) {
+        out[2 + 2 * (ntiles + q)] = E;
+        out[2 + 2 * (ntiles + q) + 1] = q * tm;
+      }
+      if (tid == 0) {
+        out[0] = ntiles + nshared;
+        out[1] = 0;
+      }
+    };
+    if (tiles != nullptr) tile_list(tile_m, tiles);
+    if (tiles2 != nullptr) tile_list(tile_m2, tiles2);
+  }
+  for (int i = tid; i < E * W; i += PCH_THREADS) bits[i] = 0;
+  __syncthreads();  // (also orders base[] before the ranks)
+  for (int i0 = tid; i0 < np; i0 += 4 * PCH_THREADS) {
+    if (!onepass) load_pairs(i0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j * PCH_THREADS;
+      const int l = i / k, r = i - l * k;
+      if (i < np && t0 + l < T && r < nr[j])
+        atomicOr(&bits[ev[j] * W + (l >> 5)], 1u << (l & 31));
+    }
+  }
+  __syncthreads();
+  // pref[e W + w] = set bits of row e's words 0 .. w-1 (W consecutive lanes
+  // hold a row, scanned with shuffles)
+  for (int i0 = 0; i0 < E * W; i0 += PCH_THREADS) {
+    const int i = i0 + tid;
+    const int v = i < E * W ? __popc(bits[i]) : 0;
+    int x = v;
+    for (int d = 1; d < W; d <<= 1) {
+      const int y = __shfl_up(x, d, W);
+      if ((tid & (W - 1)) >= d) x += y;
+    }
+    if (i < E * W) pref[i] = (uint32_t)(x - v);
+  }
+  __syncthreads();
+  for (int i0 = tid; i0 < np; i0 += 4 * PCH_THREADS) {
+    if (!onepass) load_pairs(i0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + j * PCH_THREADS;
+      const int l = i / k, r = i - l * k, t = t0 + l;
+      if (i >= np || t >= T) continue;
+      const size_t ix = (size_t)t * k + r;
+      if (r >= nr[j]) {
+        inv[ix] = -1;
+        continue;
+      }
+      const int e = ev[j];
+      const int wi = e * W + (l >> 5);
+      const int pos = base[e] + (int)pref[wi] + __popc(bits[wi] & ((1u << (l & 31)) - 1u));
+      inv[ix] = pos;
+      ptok[pos] = t;
+      pslot[pos] = r;
+    }
+  }
+}
+
 // Router and permutation in one workgroup for small batches (T <= 32,
 // T*k <= 512, E <= 256): each of the 16 waves routes tokens wave,
 // wave + 16; each valid pair (token t, slot r), i = t k + r, sets bit i of its expert's row
@@ -505,6 +716,33 @@ int launch_permute(nx_ctx *c, const int32_t *d_expert, const int32_t *d_count, i
   if (W > PERM_THREADS / 32) W = PERM_THREADS / 32;
   if (W < 1) W = 1;
   while (W & (W - 1)) W &= W - 1;  // a power of two: rows are scanned within a wave
+  // Large batches: one workgroup per chunk of 32 Wc tokens (Wc the smallest
+  // power of two from 2 that gives at most 64 chunks), two launches.  Below
+  // 4096 pairs, and with few experts up to two of the single workgroup's
+  // chunks, the one launch is as fast or faster (measured, us: Mixtral
+  // 256 / 2048 tokens 7.6 / 14.3 against 13.0 / 16.6; Qwen3 128 tokens 11.8
+  // against 13.8; Qwen3 512 tokens 16.2 against 13.7; DeepSeek 4096 tokens
+  // 82.8 against 20.0).
+  const int one_wg_chunks = (T + 32 * W - 1) / (32 * W);
+  if ((long)T * k >= 4096 && E > 0 && (E >= 64 || one_wg_chunks >= 3)) {
+    int Wc = 2;
+    while (Wc < 32 && (T + 32 * Wc - 1) / (32 * Wc) > PCH_MAX_CHUNKS && E * 2 * Wc <= PCH_WORDS)
+      Wc *= 2;
+    const int nch = (T + 32 * Wc - 1) / (32 * Wc);
+    if (E * Wc <= PCH_WORDS && nch <= PCH_MAX_CHUNKS) {
+      void *vcc;
+      NX_TRY(ws_get(c, WS_PERM_CHUNK, (size_t)nch * E * sizeof(int32_t), &vcc));
+      int32_t *d_cc = static_cast<int32_t *>(vcc);
+      NX_TRY(launch(c, "permute_count", [&] {
+        go(c, k_perm_count, dim3(nch), dim3(PCH_THREADS), 0, d_expert, d_count, T, k, E, Wc, d_cc);
+      }));
+      return launch(c, "permute", [&] {
+        go(c, k_perm_scatter, dim3(nch), dim3(PCH_THREADS), 0, d_expert, d_count, T, k, E, Wc,
+           nch, (const int32_t *)d_cc, tile_m > 0 ? tile_m : 1, d_ecount, d_offsets, d_ptok,
+           d_pslot, d_inv, d_active, d_tiles, shared_T, tile_m2 > 0 ? tile_m2 : 1, d_tiles2);
+      });
+    }
+  }
   return launch(c, "permute", [&] {
     go(c, k_permute, dim3(1), dim3(PERM_THREADS), 0, d_expert, d_count, T, k, E, W,
                                                  tile_m > 0 ? tile_m : 1, d_ecount, d_offsets,

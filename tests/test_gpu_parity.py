@@ -122,8 +122,13 @@ def test_router_reference_case_and_short_logits(ctx):
     assert ctx.route_topk([1.0, 2.0], 1, 2, 0)[3] == 0
 
 
-@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (32, 8, 2), (2048, 8, 2), (512, 128, 8),
-                                   (4096, 256, 8), (3000, 1000, 5), (100, 3, 3)])
+# one workgroup (up to 4096 pairs; few experts over at most two of its
+# chunks), then one workgroup per chunk of 64 to 1024 tokens (at most 64
+# chunks: partial last chunks, chunks of 64, 128 and 512 tokens, 8 to 1000
+# experts)
+@pytest.mark.parametrize("T,E,k", [(1, 8, 2), (32, 8, 2), (64, 16, 4), (65, 16, 4), (2048, 8, 2),
+                                   (512, 128, 8), (4096, 256, 8), (3000, 1000, 5), (100, 3, 3),
+                                   (4000, 8, 2), (8192, 64, 6), (20000, 128, 8)])
 def test_permutation_bit_exact(ctx, T, E, k):
     rng = np.random.default_rng(T + E)
     lg = router_case(rng, T, E, 0.05)
