@@ -467,7 +467,8 @@ __device__ __forceinline__ void static_for(F &&f) {
 // GRP k .. GRP k + GRP - 1 issued back to back (they read parts of the same
 // lines, so a line is fetched once while all of them are in flight), OCC =
 // workgroups per CU.  Both passes keep 32 rows per wave
-// (NT = 2) and two workgroups per CU; F32 takes one workgroup per CU.
+// (NT = 2) and two workgroups per CU (three on 64-pair tiles); F32 takes one
+// workgroup per CU.
 // Measured on the Qwen3 (E = 128, T = 512) and DeepSeek (E = 256,
 // T = 4096) Q4_K layers and the Mixtral Q8_0 prefill: NT = 1 and NT = 4
 // are slower in both passes, and fetching the codes 3 to 8 steps ahead
