@@ -951,8 +951,10 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
       // (DeepSeek shapes, ms, GEMV / split / grouped GEMM): 2 tokens 0.115 /
       // 0.173 / 0.268, 4: 0.270 / 0.264 / 0.321, 8: 0.887 / 0.508 / 0.588,
       // 16: 3.69 / 0.904 / 0.996, 32: - / 1.31 / 1.52, 64: - / 1.76 / 2.04;
-      // the grouped GEMM from the routed experts' 12 tokens each, as below.
-      if (tpe >= 12.0)
+      // the grouped GEMM (64-pair tiles at these counts) from the routed
+      // experts' 8 tokens each: 192 tokens (6 each) split 2.08-2.18 / GEMM
+      // 2.11, 256 tokens (8 each) 2.19-2.29 / 2.13.
+      if (tpe >= 8.0)
         use = NX_PATH_MFMA_BF16;
       else
         use = T >= 4 ? NX_PATH_MFMA_SPLIT : NX_PATH_GEMV;

@@ -135,13 +135,15 @@ def test_auto_path_choice(ctx, E, H, F, k, T, want):
     (Q4_K, 16, 512, 512, 4, 2, 512, nx.PATH_GEMV),        # a shared expert, 2 tokens
     (Q4_K, 16, 512, 512, 4, 4, 512, nx.PATH_MFMA_SPLIT),  # ... 4 tokens
     (Q4_K, 16, 512, 512, 4, 8, 512, nx.PATH_MFMA_SPLIT),  # ... 8 tokens
+    (Q4_K, 16, 512, 512, 4, 24, 512, nx.PATH_MFMA_SPLIT),  # ... 6 tokens per routed expert
+    (Q4_K, 16, 512, 512, 4, 32, 512, nx.PATH_MFMA_BF16),   # ... 8 tokens per routed expert
     (Q4_K, 4, 256, 256, 2, 48, 256, nx.PATH_MFMA_BF16),   # ... 24 tokens per routed expert
     (Q4_K, 16, 512, 512, 4, 8, 1024, nx.PATH_MFMA_BF16)])  # a wider shared expert, 8 tokens
 def test_auto_path_choice_other(ctx, fmt, E, H, F, k, T, shared, want):
     """AUTO for formats other than Q4_K and for layers with a shared expert:
     the grouped GEMM from ~3 tokens per routed expert, or from 6 tokens with
     a shared expert, the GEMV below; Q4_K with a shared expert as wide as the
-    routed ones takes the split-activation path from 4 tokens up to 12
+    routed ones takes the split-activation path from 4 tokens up to 8
     tokens per routed expert (the bits of the chosen path)."""
     L = Layer(fmt, E, H, F, k, T, seed=E + T + fmt, shared_F=shared)
     ex = L.upload(nx, ctx)
