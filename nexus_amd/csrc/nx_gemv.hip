@@ -13,9 +13,10 @@
 // before the current U rows are decoded and reduced (DPP adds within a
 // wave's row group).
 //
-// Gate/up (k_gemv_gateup): grid x = row blocks, y = expert slot (the i-th
-// active expert from the permutation, then one slot for the shared expert);
-// the epilogue applies SwiGLU and stores the activation row of each pair.
+// Gate/up (k_gemv_gateup): one workgroup per (expert slot, row block) on a
+// one-dimensional grid (slot = the i-th active expert from the permutation,
+// then one slot for the shared expert); the epilogue applies SwiGLU and
+// stores the activation row of each pair.
 //
 // Down + combine (k_gemv_down): grid x = row blocks only.  Each half of a
 // 512-thread workgroup walks every (slot, token group, row stage) of its
@@ -29,8 +30,8 @@
 //
 // Down rows longer than 64 segments (Mixtral's F = 14336: 224) take the
 // per-slot kernel in K slices instead: one wave per (row, slice of 64
-// segments), grid y = slot x slice, the slot's activations prepared once per
-// workgroup into LDS; the slices' partial sums go to the route-order combine
+// segments), one workgroup per (slot, slice, row block), the slot's
+// activations prepared once per workgroup into LDS; the slices' partial sums go to the route-order combine
 // kernel, which adds them in slice order.  Weight codes are loaded with the
 // non-temporal policy: they are read once, and the activation, scale and
 // route arrays that every workgroup rereads stay in the caches.
@@ -45,14 +46,6 @@
 #endif
 #ifndef NX_GEMV_PLAIN_STAGES
 #define NX_GEMV_PLAIN_STAGES 2
-#endif
-#ifndef NX_GEMV_FUSE_COMBINE
-#define NX_GEMV_FUSE_COMBINE 0
-#endif
-// Rows of the per-slot kernel interleaved across the row groups of a slot
-// (row = group + i * groups) rather than one contiguous run per group
-#ifndef NX_GEMV_INTERLEAVE
-#define NX_GEMV_INTERLEAVE 0
 #endif
 // down rows longer than 64 segments split into K slices (per-slot kernel)
 #ifndef NX_GEMV_DOWN_SPLIT
@@ -94,9 +87,6 @@ struct GemvArgs {
   float *out;
   int out_stride;
   int rows_per_group;
-  // per-slot kernel: rows interleaved across the slot's row groups
-  int row_interleave;
-  int groups_per_wg;
   // down projection: combine inputs, pair count, global partial-sum area
   const float *rw;
   const int32_t *rcnt;
@@ -105,20 +95,20 @@ struct GemvArgs {
   const float *residual;  // final_out = residual + combine when set
   int npairs;
   float *gpart;
-  // down rows in K slices (PLAIN, one wave per row): grid.y = slot * kslices
-  // + slice; slice s covers segments 64 s .. 64 s + 63 and writes its partial
-  // sums kslice_stride floats after slice s - 1's
+  // down rows in K slices (PLAIN, one wave per row): slice s covers segments
+  // 64 s .. 64 s + 63 and writes its partial sums kslice_stride floats after
+  // slice s - 1's
   int kslices;
   size_t kslice_stride;
-  // Combine fused into the per-slot down pass (PLAIN, combine_cnt set): the
-  // last workgroup of each row block (grid.x) to finish its rows forms
-  // final_out[t][r] for the block's rows from every slot's and slice's
-  // partial sums; combine_cnt[blockIdx.x] counts the arrivals.  The gate/up
-  // pass that precedes it clears zero_cnt[0 .. n_zero).
-  int *combine_cnt;
-  int combine_rows_per_block;
-  int *zero_cnt;
-  int n_zero;
+  // row blocks per (slot, slice): the per-slot kernel's grid is
+  // one-dimensional, workgroup b = (slot * kslices + slice) * kgx + row block
+  // (a two-dimensional grid of the same workgroups ran the Mixtral down pass
+  // about 1 us slower)
+  int kgx;
+  // one token (T == 1): slot s < n_active is the s-th active expert and owns
+  // pair s, so the expert id and the active count load together and the
+  // activation row needs no lookup
+  int one_token;
   // gate/up of one token with the routing done in the kernel: every
   // workgroup routes the token from route_logits [E]; workgroup (0, 0) also
   // writes the route and permutation arrays the down pass reads
@@ -151,15 +141,21 @@ struct SlotView {
 };
 
 // active: the active expert list (global, or the workgroup's own routing in
-// LDS); null for a dense matrix, one slot over all T tokens
+// LDS); null for a dense matrix, one slot over all T tokens.  e_one >= 0: one
+// token, slot < n_active is expert e_one (loaded by the caller) with pair slot.
 __device__ __forceinline__ SlotView slot_view(const GemvArgs &a, int slot, int n_active,
-                                              const int32_t *active, const int32_t *offsets) {
+                                              const int32_t *active, const int32_t *offsets,
+                                              int e_one = -1) {
   SlotView v;
   if (slot < n_active) {
     int e = 0;
     v.pair0 = 0;
     v.count = a.T;
-    if (active) {
+    if (e_one >= 0) {
+      e = e_one;
+      v.pair0 = slot;
+      v.count = 1;
+    } else if (active) {
       e = active[slot];
       v.pair0 = offsets[e];
       v.count = offsets[e + 1] - v.pair0;
@@ -455,7 +451,7 @@ struct RowGroup {
 __device__ __forceinline__ void fused_route(const GemvArgs &a, int lane, int32_t *s_active,
                                             int32_t *s_off, int32_t *s_ptok, int32_t *s_n) {
   // only the workgroup that writes the routes needs their weights
-  const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+  const bool writer = blockIdx.x == 0;
   int e, n;
   float w;
   route_one<4>(a.route_logits, a.E, a.k, a.score_mode, lane, &e, &w, &n, writer);
@@ -508,52 +504,6 @@ __device__ __forceinline__ void fused_route(const GemvArgs &a, int lane, int32_t
   }
 }
 
-// Partial sums the fused combine exchanges between workgroups go past the
-// per-XCD L2 caches: system-scope relaxed stores and loads are written
-// through to memory and read from it, so the arrival counter needs no cache
-// write-back or invalidate (an agent-scope fence writes back the whole L2).
-__device__ __forceinline__ void store_through(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-__device__ __forceinline__ float load_through(const float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
-// The combine of one row block of the per-slot down pass: final_out[t][r] =
-// (residual +) sum over t's routes, in route order, of w * y[pair][r] (+ the
-// shared expert's y), y being the sum of the pair's nks K-slice partials in
-// slice order -- the arithmetic of k_combine.  nks = 0: no partials (no
-// routes, no shared expert).
-__device__ __forceinline__ void combine_rows(const GemvArgs &a, int nks, int tid) {
-  const int H = a.out_stride;
-  // the row block's rows: those of its row groups, interleaved or contiguous
-  const int nr = a.combine_rows_per_block;
-  const int gw = a.groups_per_wg;
-  const int T = a.T, k = a.k;
-  for (int i = tid; i < nr * T; i += 256) {
-    const int t = i / nr, idx = i - t * nr;
-    const int r = a.row_interleave
-                      ? blockIdx.x * gw + idx % gw + (idx / gw) * (int)gridDim.x * gw
-                      : blockIdx.x * nr + idx;
-    if (r >= H) continue;
-    auto y = [&](int p) {
-      const float *yp = a.out + (size_t)p * H + r;
-      float s = load_through(yp);
-      for (int q = 1; q < nks; ++q) s += load_through(yp + (size_t)q * a.kslice_stride);
-      return s;
-    };
-    const int n = nks ? a.rcnt[t] : 0;
-    float acc = 0.0f;
-    for (int j = 0; j < n; ++j) {
-      const size_t rj = (size_t)t * k + j;
-      acc = acc + __fmul_rn(a.rw[rj], y(a.inv[rj]));
-    }
-    if (nks && a.has_shared) acc = acc + y(T * k + t);
-    const size_t o = (size_t)t * H + r;
-    a.final_out[o] = a.residual ? a.residual[o] + acc : acc;
-  }
-}
-
 // PLAIN: one matrix (the down projection of one slot per grid.y), no
 // SwiGLU; activations are per pair (row pair0 + t of x) and each row's dot
 // product goes to out[pair][row] for the combine kernel.
@@ -573,9 +523,6 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   constexpr int S = PLAIN ? NX_GEMV_PLAIN_STAGES : (NT == 1 && SPL == 1 ? NX_GEMV_GATEUP_STAGES : 2);
   using RG = RowGroup<FMT, L, SPL, NT, U, NMAT>;
   const int tid = threadIdx.x, lane = tid & 63;
-  if (!PLAIN && a.zero_cnt && blockIdx.x == 0 && blockIdx.y == 0)
-    for (int i = tid; i < a.n_zero; i += 256)
-      __hip_atomic_store(a.zero_cnt + i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   // wave index, known to the compiler as wave-uniform
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // row group of this thread; with KSPLIT > 1, waves grp KSPLIT ..
@@ -586,10 +533,13 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32 && FMT != NX_FMT_F16 &&
                         FMT != NX_FMT_BF16;
   __shared__ uint4 xsh[COOP ? NT * 64 * RG::XW : 1];
-  // K slice of this workgroup (PLAIN with kslices > 1; else whole rows)
+  // slot, K slice (PLAIN with kslices > 1; else whole rows) and row block
   const int kslices = PLAIN ? a.kslices : 1;
-  const int slot = PLAIN ? (int)blockIdx.y / kslices : (int)blockIdx.y;
-  const int kslice = PLAIN ? (int)blockIdx.y - slot * kslices : 0;
+  const int sk = (int)blockIdx.x / a.kgx;
+  const int bx = (int)blockIdx.x - sk * a.kgx;
+  const int slot = sk / kslices;
+  const int kslice = sk - slot * kslices;
+  const int rpg = a.rows_per_group;
   RG g;
   g.init(KSPLIT == 1 ? (lane % LPR) : tid % L, kslice * L * SPL);
   float xq[NT][RG::XQ];  // activation quarters in flight (COOP)
@@ -597,6 +547,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
 
   const int32_t *active = a.active, *offsets = a.offsets, *perm_token = a.perm_token;
   int n_active;
+  // one token: this slot's expert, loaded together with the active count
+  // (slot <= E, so the load is in range even for an absent slot)
+  int e_one = -1;
   if constexpr (!PLAIN && NT == 1) {
     // one token routed here: ids of the routed experts in ascending order
     // (the permutation's active list), each with one pair at its rank
@@ -623,20 +576,15 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
       perm_token = s_ptok;
       n_active = s_n;
     } else {
+      if (a.one_token) e_one = a.active[min(slot, a.E)];
       n_active = a.active[a.E];
     }
   } else {
     // (in-kernel routing takes one token, which runs the NT == 1 instances)
+    if (a.one_token) e_one = a.active[min(slot, a.E)];
     n_active = a.active ? a.active[a.E] : 1;
   }
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
-  const bool fused = PLAIN && a.combine_cnt != nullptr;
-  if (fused && n_slots == 0) {
-    // no token has a route or a shared expert: the output is the residual
-    // (or zero); the first workgroup of each row block writes it
-    if (blockIdx.y == 0) combine_rows(a, 0, tid);
-    return;
-  }
   if (slot >= n_slots) return;  // workgroup-uniform
   float *const out = a.out + (size_t)kslice * a.kslice_stride;
   // KSPLIT > 1: per-wave partial sums of up to RED_ROWS rows, summed across
@@ -645,26 +593,22 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   static_assert(RED_ROWS % U == 0, "a stage's rows share one run of partials");
   __shared__ float red[KSPLIT > 1 ? 4 * RED_ROWS * NMAT * NT : 1];
 
-  const SlotView v = slot_view(a, slot, n_active, active, offsets);
-  // this group's logical rows 0 .. nq-1: interleaved over the slot's row
-  // groups (row = group + q * groups) or one contiguous run
-  const int gidx = blockIdx.x * GROUPS + grp;
-  const int ngroups = gridDim.x * GROUPS;
-  const RowMap rm = a.row_interleave
-                        ? RowMap{gidx, ngroups, v.rows}
-                        : RowMap{gidx * a.rows_per_group, 1,
-                                 min(v.rows, gidx * a.rows_per_group + a.rows_per_group)};
-  const int nq = a.row_interleave ? (v.rows > gidx ? (v.rows - gidx + ngroups - 1) / ngroups : 0)
-                                  : max(0, rm.end - rm.base);
+  const SlotView v = slot_view(a, slot, n_active, active, offsets, e_one);
+  // this group's logical rows 0 .. nq-1: one contiguous run of rpg rows
+  const int gidx = bx * GROUPS + grp;
+  const RowMap rm{gidx * rpg, 1, min(v.rows, gidx * rpg + rpg)};
+  const int nq = max(0, rm.end - rm.base);
+  // activation row of token t of the slot (one token: row 0, no lookup)
   auto row_of = [&](int t) {
-    return PLAIN ? v.pair0 + t : (v.routed ? perm_token[v.pair0 + t] : t);
+    return PLAIN ? v.pair0 + t
+                 : (v.routed && e_one < 0 ? perm_token[v.pair0 + t] : (e_one >= 0 ? 0 : t));
   };
 
   // with KSPLIT > 1 finish has barriers, so the stage sequence must be
   // workgroup-uniform: one row group per workgroup runs its nq rows; with
   // several, every group runs rows_per_group rows (rows past the end load as
   // zeros and are not written)
-  const int qlim = (KSPLIT > 1 && GROUPS > 1) ? a.rows_per_group : nq;
+  const int qlim = (KSPLIT > 1 && GROUPS > 1) ? rpg : nq;
 
   typename RG::Stage st[S];
   for (int t0 = 0; t0 < v.count; t0 += NT) {
@@ -730,13 +674,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
             if (t0 + t >= v.count) continue;
-            if constexpr (PLAIN) {
-              float *o = &out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r];
-              if (fused)
-                store_through(o, acc[u][0][t]);
-              else
-                *o = acc[u][0][t];
-            }
+            if constexpr (PLAIN)
+              out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] = acc[u][0][t];
             else
               out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
                   silu_mul(acc[u][0][t], acc[u][NMAT - 1][t]);
@@ -754,19 +693,6 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
         finish(st[i], qq);
       }
     }
-  }
-  if (fused) {
-    // every wave's written-through partial sums have reached memory (the
-    // wait covers stores on gfx9) before the workgroup counts in; the last
-    // of the n_slots * kslices arrivals reads them all back from memory
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    __shared__ int s_last;
-    if (tid == 0)
-      s_last = __hip_atomic_fetch_add(&a.combine_cnt[blockIdx.x], 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_SYSTEM) == n_slots * kslices - 1;
-    __syncthreads();
-    if (s_last) combine_rows(a, kslices, tid);
   }
 }
 
@@ -1153,20 +1079,13 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const long grid_y = per_slot ? (long)slots_max * kslices : 1;
   rpg = fit_one_round(rows, rpg, groups_per_wg, grid_y, (long)c->num_cu * wg_per_cu);
   a.rows_per_group = (int)rpg;
-  a.row_interleave = NX_GEMV_INTERLEAVE;
-  a.groups_per_wg = groups_per_wg;
+  a.one_token = p.T == 1 ? 1 : 0;
   const long rows_per_wg = rpg * groups_per_wg;
   const unsigned gx = (unsigned)((rows + rows_per_wg - 1) / rows_per_wg);
+  a.kgx = (int)gx;
 
   if (gateup) {
-    if (NX_GEMV_FUSE_COMBINE) {
-      // the counters of the down pass's fused combine start at zero
-      void *cnt = nullptr;
-      NX_TRY(ws_get(c, WS_DOWN_CNT, (size_t)ex->H * sizeof(int), &cnt));
-      a.zero_cnt = static_cast<int *>(cnt);
-      a.n_zero = ex->H;
-    }
-    const dim3 grid(gx, (unsigned)slots_max);
+    const dim3 grid(gx * (unsigned)slots_max);
     return launch(c, "gemv_gateup",
                   [&] { go(c, probe, grid, dim3(256), 0, a); });
   }
@@ -1181,25 +1100,8 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
     a.out = ypair;
     a.out_stride = ex->H;
     a.kslice_stride = pairs_total * ex->H;
-    const dim3 grid(gx, (unsigned)(slots_max * kslices));
-    // Few outputs per row block (decode): the block's last workgroup
-    // combines them, with no combine launch.  Otherwise the combine kernel
-    // spreads them over the GPU.
-    const bool fuse = NX_GEMV_FUSE_COMBINE && (long)p.T * rows_per_wg <= 2048;
-    if (fuse) {
-      void *cnt = nullptr;
-      NX_TRY(ws_get(c, WS_DOWN_CNT, (size_t)ex->H * sizeof(int), &cnt));
-      a.combine_cnt = static_cast<int *>(cnt);
-      a.combine_rows_per_block = (int)rows_per_wg;
-      a.rw = p.rw;
-      a.rcnt = p.rcnt;
-      a.inv = p.inv;
-      a.final_out = p.out;
-      a.residual = p.residual;
-    }
-    NX_TRY(launch(c, fuse ? "gemv_down_combine" : "gemv_down",
-                  [&] { go(c, probe, grid, dim3(256), 0, a); }));
-    if (fuse) return NX_OK;
+    const dim3 grid(gx * (unsigned)(slots_max * kslices));
+    NX_TRY(launch(c, "gemv_down", [&] { go(c, probe, grid, dim3(256), 0, a); }));
     return launch_combine(c, ypair, p.rw, p.rcnt, p.inv, p.T, p.k, ex->H, has_shared, p.out,
                           kslices, a.kslice_stride, p.residual);
   }
@@ -1263,12 +1165,11 @@ int run_gemv_matrix(nx_ctx *c, int fmt, const RolePlane &pl, const float *x, int
   if (rpg < 1) rpg = 1;
   rpg = fit_one_round(pl.rows, rpg, groups_per_wg, 1, (long)c->num_cu * wg_per_cu);
   a.rows_per_group = (int)rpg;
-  a.row_interleave = NX_GEMV_INTERLEAVE;
-  a.groups_per_wg = groups_per_wg;
   const long rows_per_wg = rpg * groups_per_wg;
   const unsigned gx = (unsigned)((pl.rows + rows_per_wg - 1) / rows_per_wg);
+  a.kgx = (int)gx;
   return launch(c, "gemv_matrix",
-                [&] { go(c, fn, dim3(gx, 1), dim3(256), 0, a); });
+                [&] { go(c, fn, dim3(gx), dim3(256), 0, a); });
 }
 
 }  // namespace
