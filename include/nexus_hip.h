@@ -293,7 +293,8 @@ int nx_moe_forward_dev(nx_ctx *ctx, const nx_experts *ex, const float *d_x,
  * last call's; valid until the next call on the context (or, after the
  * no-allocation entry point, the next such call on the device).  For a
  * single token on the GEMV path these are the routes the gate/up kernel
- * computed itself. */
+ * computed itself.  A forward that failed records no routes: this call then
+ * returns NX_ERR_INVALID_ARG until a forward completes. */
 int nx_moe_last_routes(nx_ctx *ctx, int num_tokens, int top_k, int32_t *experts, float *weights,
                        int32_t *counts);
 

@@ -923,11 +923,18 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   NX_TRY(ws(c, WS_PERM_SLOT, tk, &d_ps));
   NX_TRY(ws(c, WS_INV_POS, tk, &d_inv));
   NX_TRY(ws(c, WS_ACTIVE, (size_t)E + 1, &d_act));
-  c->last_exp = d_exp;
-  c->last_w = d_w;
-  c->last_cnt = d_cnt;
-  c->last_T = T;
-  c->last_k = k;
+  // the routes this call writes become the context's last routes only once
+  // every launch of the call is enqueued: a later workspace failure can move
+  // the slots carved above, and a failed call leaves no routes to read back
+  c->last_exp = nullptr;
+  auto remember_routes = [&] {
+    c->last_exp = d_exp;
+    c->last_w = d_w;
+    c->last_cnt = d_cnt;
+    c->last_T = T;
+    c->last_k = k;
+    return NX_OK;
+  };
 
   int use = path;
   if (ex->fmt == NX_FMT_Q2_K || ex->fmt == NX_FMT_F16 || ex->fmt == NX_FMT_BF16) {
@@ -1005,11 +1012,12 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
     NX_TRY(ws(c, WS_ACT, pairs_total * act_stride, &d_actv));
     GemvPlan gp{ex, T, k, d_x, d_pt, d_off, d_act, d_actv, act_stride, d_ypair,
                 d_w, d_cnt, d_inv, d_out, d_residual};
+    gp.pslot = d_ps;
     if (route_in_gemv)
       gp.route = {d_logits, score_mode, d_exp, d_cnt, d_ec, d_off, d_pt, d_ps, d_inv, d_act, d_w};
     NX_TRY(launch_gemv_gateup(c, gp));
     NX_TRY(launch_gemv_down(c, gp));
-    return NX_OK;
+    return remember_routes();
   }
 
   if (use == NX_PATH_MFMA_SPLIT) {
@@ -1031,7 +1039,8 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
                             d_act, d_tiles, shared ? T : 0));
     }
     MfvPlan mp{ex, T, k, d_x, d_pt, d_off, d_tiles, max_tiles, d_w, d_cnt, d_inv, d_out, d_residual};
-    return launch_mfv(c, mp);
+    NX_TRY(launch_mfv(c, mp));
+    return remember_routes();
   }
 
   // grouped GEMM on MFMA
@@ -1071,7 +1080,7 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   NX_TRY(launch_gemm_down(c, mp));
   NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out, ksplit,
                         pairs_total * (size_t)H, d_residual));
-  return NX_OK;
+  return remember_routes();
 }
 
 extern "C" {
@@ -1095,7 +1104,8 @@ int nx_moe_forward_noalloc(nx_ctx *c, const nx_experts *ex, const float *d_x,
 int nx_moe_last_routes(nx_ctx *c, int T, int k, int32_t *experts, float *weights,
                        int32_t *counts) {
   NX_TRY(check_ctx(c));
-  if (!c->last_exp) return fail(NX_ERR_INVALID_ARG, "no forward has run on this context");
+  if (!c->last_exp)
+    return fail(NX_ERR_INVALID_ARG, "no routes recorded: no forward has completed on this context");
   if (T != c->last_T || k != c->last_k)
     return fail(NX_ERR_SHAPE, "the last forward routed " + std::to_string(c->last_T) +
                                   " tokens with top_k " + std::to_string(c->last_k));

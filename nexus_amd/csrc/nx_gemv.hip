@@ -81,6 +81,7 @@ struct GemvArgs {
   const float *x;
   int x_stride;
   const int32_t *perm_token;  // gate/up: pair -> token
+  const int32_t *pslot;       // pair -> route slot (one-token down pass)
   const int32_t *offsets;
   const int32_t *active;
   int E, T, k, has_shared;
@@ -504,7 +505,7 @@ __device__ __forceinline__ void fused_route(const GemvArgs &a, int lane, int32_t
   }
 }
 
-// PLAIN: one matrix (the down projection of one slot per grid.y), no
+// PLAIN: one matrix (the down projection of one slot per workgroup), no
 // SwiGLU; activations are per pair (row pair0 + t of x) and each row's dot
 // product goes to out[pair][row] for the combine kernel.
 template <int FMT, int LPR, int KSPLIT, int SPL, int NT, bool PLAIN = false>
@@ -533,7 +534,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   constexpr bool COOP = L == 64 && SPL == 1 && FMT != NX_FMT_F32 && FMT != NX_FMT_F16 &&
                         FMT != NX_FMT_BF16;
   __shared__ uint4 xsh[COOP ? NT * 64 * RG::XW : 1];
-  // slot, K slice (PLAIN with kslices > 1; else whole rows) and row block
+  // slot, K slice (PLAIN with kslices > 1; else whole rows) and row block:
+  // workgroup = (slot, slice, row block)
   const int kslices = PLAIN ? a.kslices : 1;
   const int sk = (int)blockIdx.x / a.kgx;
   const int bx = (int)blockIdx.x - sk * a.kgx;
@@ -548,8 +550,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   const int32_t *active = a.active, *offsets = a.offsets, *perm_token = a.perm_token;
   int n_active;
   // one token: this slot's expert, loaded together with the active count
-  // (slot <= E, so the load is in range even for an absent slot)
-  int e_one = -1;
+  // (slot <= E, so the load is in range even for an absent slot), and for
+  // the down pass the route slot its rows are written at (clamped to the
+  // T * k = k route slots; only a routed slot uses it)
+  int e_one = -1, ps_one = 0;
   if constexpr (!PLAIN && NT == 1) {
     // one token routed here: ids of the routed experts in ascending order
     // (the permutation's active list), each with one pair at its rank
@@ -581,12 +585,18 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
     }
   } else {
     // (in-kernel routing takes one token, which runs the NT == 1 instances)
-    if (a.one_token) e_one = a.active[min(slot, a.E)];
+    if (a.one_token) {
+      e_one = a.active[min(slot, a.E)];
+      if (PLAIN && a.pslot) ps_one = a.pslot[min(slot, a.k - 1)];
+    }
     n_active = a.active ? a.active[a.E] : 1;
   }
   const int n_slots = n_active + (a.has_shared ? 1 : 0);
   if (slot >= n_slots) return;  // workgroup-uniform
   float *const out = a.out + (size_t)kslice * a.kslice_stride;
+  // first output row of the slot: its pair, or (one-token down pass) the
+  // routed pair's route slot
+  const int orow0 = (PLAIN && e_one >= 0 && a.pslot && slot < n_active) ? ps_one : -1;
   // KSPLIT > 1: per-wave partial sums of up to RED_ROWS rows, summed across
   // the group's waves once per RED_ROWS rows (two barriers), not per stage
   constexpr int RED_ROWS = 32;
@@ -659,7 +669,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
                 s += red[(((grp * KSPLIT + w) * RED_ROWS + rl) * NMAT + mt) * NT + t];
               sm[mt] = s;
             }
-            out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
+            out[(size_t)((orow0 >= 0 ? orow0 : v.pair0) + t0 + t) * a.out_stride + r] =
                 PLAIN ? sm[0] : silu_mul(sm[0], sm[NMAT - 1]);
           }
           __syncthreads();
@@ -675,9 +685,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
           for (int t = 0; t < NT; ++t) {
             if (t0 + t >= v.count) continue;
             if constexpr (PLAIN)
-              out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] = acc[u][0][t];
+              out[(size_t)((orow0 >= 0 ? orow0 : v.pair0) + t0 + t) * a.out_stride + r] = acc[u][0][t];
             else
-              out[(size_t)(v.pair0 + t0 + t) * a.out_stride + r] =
+              out[(size_t)((orow0 >= 0 ? orow0 : v.pair0) + t0 + t) * a.out_stride + r] =
                   silu_mul(acc[u][0][t], acc[u][NMAT - 1][t]);
           }
         }
@@ -999,6 +1009,7 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
     a.snseg = S0.nseg;
   }
   a.perm_token = p.perm_token;
+  a.pslot = p.T == 1 ? p.pslot : nullptr;
   a.offsets = p.offsets;
   a.active = p.active;
   a.E = ex->E;
@@ -1102,7 +1113,9 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
     a.kslice_stride = pairs_total * ex->H;
     const dim3 grid(gx * (unsigned)(slots_max * kslices));
     NX_TRY(launch(c, "gemv_down", [&] { go(c, probe, grid, dim3(256), 0, a); }));
-    return launch_combine(c, ypair, p.rw, p.rcnt, p.inv, p.T, p.k, ex->H, has_shared, p.out,
+    // one token: the rows are in route order (see a.pslot), no pair lookup
+    return launch_combine(c, ypair, p.rw, p.rcnt, a.pslot ? nullptr : p.inv, p.T, p.k, ex->H,
+                          has_shared, p.out,
                           kslices, a.kslice_stride, p.residual);
   }
 

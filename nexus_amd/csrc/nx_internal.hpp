@@ -163,7 +163,6 @@ enum WsSlot {
   WS_MAT_X,    // device copy of matvec inputs for blocking calls
   WS_MAT_Y,
   WS_MFV_PART, // gate/up partial sums of the split-activation MFMA path
-  WS_DOWN_CNT, // arrival counters of the decode down pass's fused combine
   WS_TILES_DOWN, // grouped-GEMM tile list of the down pass
   WS_PERM_CHUNK, // per-chunk expert counts of the many-workgroup permutation
   WS_COUNT
@@ -250,7 +249,8 @@ int launch_rms_fast(nx_ctx *c, const float *d_x, const float *d_w, float eps, in
                     float *d_out);
 // out[t] = sum_r w[t,r] * y[pair(t,r)] (+ y[shared row t]); y is the sum of
 // nsplit partial buffers split_stride floats apart; with a residual,
-// out = residual + that sum (out may be the residual itself)
+// out = residual + that sum (out may be the residual itself).  d_inv null:
+// the routed rows are stored in route order (pair(t,r) = t * k + r)
 int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
                    const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out,
                    int nsplit = 1, size_t split_stride = 0, const float *d_residual = nullptr);
@@ -271,6 +271,10 @@ struct GemvPlan {
   const int32_t *inv;
   float *out;
   const float *residual = nullptr;  // out = residual + layer output when set
+  // pair -> route slot t * k + r ([T * k]); with one token the down pass
+  // writes each routed pair's rows at its route slot, so the combine looks
+  // up no pair indices
+  const int32_t *pslot = nullptr;
   // One token routed inside the gate/up kernel from logits [E] (E at most
   // kFusedRouteMaxE), which also writes the arrays the router and
   // permutation kernels would (expert, weight, count, ecount, offsets,

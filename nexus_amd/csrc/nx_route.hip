@@ -555,7 +555,10 @@ __device__ __forceinline__ float y_at(const float *__restrict__ y, size_t stride
 // (src/engine/mod.rs:1017-1021).  The routes' pair indices and weights are
 // read RB at a time (clamped to the last slot, k - 1) together with the
 // route count, then their y values, so a token's loads take two dependent
-// rounds and the routes' loads overlap.
+// rounds and the routes' loads overlap.  inv == nullptr: the y rows are
+// stored in route order (route r of token t at row t * k + r, as the
+// one-token decode GEMV writes them), so every load of the token is issued
+// at once and the rows of absent routes are read but not used.
 template <int NS, int RB>
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair,
                                                  const float *__restrict__ rw,
@@ -577,12 +580,12 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair
 #pragma unroll
       for (int j = 0; j < RB; ++j) {
         const size_t r = (size_t)t * k + min(r0 + j, k - 1);
-        p[j] = inv[r];
+        p[j] = inv ? inv[r] : (int)r;
         w[j] = rw[r];
       }
 #pragma unroll
       for (int j = 0; j < RB; ++j)
-        yv[j] = r0 + j < n ? y_at<NS>(ypair, stride, ns, (size_t)p[j] * H + h) : 0.f;
+        yv[j] = (!inv || r0 + j < n) ? y_at<NS>(ypair, stride, ns, (size_t)p[j] * H + h) : 0.f;
 #pragma unroll
       for (int j = 0; j < RB; ++j)
         if (r0 + j < n) acc = acc + __fmul_rn(w[j], yv[j]);
@@ -652,13 +655,13 @@ __global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ ypai
 #pragma unroll
     for (int j = 0; j < RB; ++j) {
       const size_t r = (size_t)t * k + min(r0 + j, k - 1);
-      p[j] = inv[r];
+      p[j] = inv ? inv[r] : (int)r;
       w[j] = rw[r];
     }
 #pragma unroll
     for (int j = 0; j < RB; ++j)
-      yv[j] = r0 + j < n ? y4_at<NS>(ypair, stride, ns, (size_t)p[j] * H + col)
-                         : make_float4(0.f, 0.f, 0.f, 0.f);
+      yv[j] = (!inv || r0 + j < n) ? y4_at<NS>(ypair, stride, ns, (size_t)p[j] * H + col)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int j = 0; j < RB; ++j)
       if (r0 + j < n) {
