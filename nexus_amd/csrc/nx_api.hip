@@ -13,6 +13,7 @@
 #include <string>
 #include <vector>
 
+#include "nx_device.hpp"
 #include "nx_internal.hpp"
 
 // one token on the GEMV path: the gate/up kernel routes it itself
@@ -270,8 +271,16 @@ static void plane_layout(int fmt, RolePlane &pl, int rows, int cols) {
     pl.row_meta = 0;
     break;
   }
-  // two 16-byte code chunks per segment, one for Q2_K's 2-bit codes
-  pl.row_qs = (uint32_t)pl.nseg * (fmt == NX_FMT_Q2_K ? 16 : 32);
+  // two 16-byte code chunks per segment, one for Q2_K's 2-bit codes; rows of
+  // more than 64 segments are stored in panels of 64 (nx_device.hpp), the
+  // last one zero-padded, so their bytes per row count whole panels
+  const int np = panel_count(pl.nseg);
+  pl.row_qs = (uint32_t)np * panel_row_bytes(pl.nseg, fmt == NX_FMT_Q2_K ? 16 : 32);
+  if (pl.row_meta) {
+    // scale bytes per segment: Q4_K 16 per block of 4, Q8_0 2, Q4_0 4, Q2_K 8
+    const int mu = fmt == NX_FMT_Q8_0 ? 2 : (fmt == NX_FMT_Q2_K ? 8 : 4);
+    pl.row_meta = (uint32_t)np * panel_row_bytes(pl.nseg, mu);
+  }
   // strides rounded to 256 B so every expert's planes start aligned
   pl.qs_stride = ((size_t)rows * pl.row_qs + 255) / 256 * 256;
   pl.meta_stride = ((size_t)rows * pl.row_meta + 255) / 256 * 256;

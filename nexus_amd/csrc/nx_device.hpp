@@ -16,11 +16,12 @@
 //   Q8_0 (src/quant/mod.rs:689-703): segment j = block j in element order,
 //        y = (int8)q * d.
 //   F32: segment j = floats 8j .. 8j+7.
-// Segments are stored half-interleaved per group of 64: half h (16 B) of
-// segment j lives at (j/64)*2048 + h*G*16 + (j%64)*16 with G the group's
-// size, so the 64 lanes of a wave that own 64 consecutive segments read two
-// fully contiguous 1 KB runs.  Each segment's values are ordered so that its
-// x operand is one or two contiguous runs of the activation row.
+// Segments are stored half-interleaved per group of 64: within a group of G
+// segments, half h (16 B) of segment j lives at h*G*16 + (j%64)*16, so the
+// 64 lanes of a wave that own 64 consecutive segments read two fully
+// contiguous 1 KB runs.  Rows longer than one group are stored in panels, one
+// per group (see panel_row_off below).  Each segment's values are ordered so
+// that its x operand is one or two contiguous runs of the activation row.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -71,11 +72,40 @@ __device__ __forceinline__ uint4 ld_stream16(const uint8_t *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// half-interleaved offset of half h of segment j in a row of nseg segments
-__device__ __forceinline__ uint32_t seg_off(int j, int h, int nseg) {
-  const int g = j >> 6;
-  const int gsz = min(64, nseg - (g << 6));
-  return (uint32_t)(g * 2048 + h * gsz * 16 + (j & 63) * 16);
+// ---- Panels.  A matrix whose rows hold more than 64 segments is stored one
+// panel per group of 64 segments: group g of every row (gsz = min(64, nseg -
+// 64 g) segments) forms the panel [rows x 64 segments] at g * rows * 64 *
+// unit bytes (unit = a segment's bytes in the plane), its row parts one after
+// another; inside a panel row the group keeps the layout above, and the last
+// group, when shorter, is followed by zeros up to the panel row's end.  A
+// kernel that streams one group of many rows (the K-sliced decode down pass)
+// then reads one contiguous run: 2 KB pieces of rows 7 KB apart (the
+// row-major form of Mixtral's down rows) read at 3.6 TB/s on the box, the
+// same bytes in panels at 5.3 TB/s.  Rows of at most 64 segments are one
+// panel without padding: the plain row-major layout.
+__host__ __device__ __forceinline__ int panel_gsz(int g, int nseg) {
+  const int s = nseg - 64 * g;
+  return s < 0 ? 0 : (s > 64 ? 64 : s);
+}
+// panels of a row of nseg segments
+__host__ __device__ __forceinline__ int panel_count(int nseg) { return nseg > 64 ? (nseg + 63) / 64 : 1; }
+// bytes of one row's part of a panel: 64 segments' when the row spans several
+// panels, else the row's own (in whole dwords: Q8_0's 2-byte scales)
+__host__ __device__ __forceinline__ uint32_t panel_row_bytes(int nseg, int unit) {
+  return nseg > 64 ? 64u * (uint32_t)unit : ((uint32_t)(nseg * unit) + 3u) & ~3u;
+}
+// offset of row r's part of panel g in a plane of `rows` rows
+__host__ __device__ __forceinline__ uint32_t panel_row_off(int r, int g, int rows, int nseg,
+                                                           int unit) {
+  return ((uint32_t)g * (uint32_t)rows + (uint32_t)r) * panel_row_bytes(nseg, unit);
+}
+// offset of half h of segment j within its panel row (32-byte segments)
+__host__ __device__ __forceinline__ uint32_t seg_off(int j, int h, int nseg) {
+  return (uint32_t)(h * panel_gsz(j >> 6, nseg) * 16 + (j & 63) * 16);
+}
+// offset of half h of segment j of row r in a code plane of 32-byte segments
+__host__ __device__ __forceinline__ uint32_t code_off(int r, int j, int h, int rows, int nseg) {
+  return panel_row_off(r, j >> 6, rows, nseg, 32) + seg_off(j, h, nseg);
 }
 
 // 16-byte code chunks per segment: two (the halves above) for every format
@@ -346,9 +376,11 @@ struct Seg<NX_FMT_Q4_K> {
   __device__ __forceinline__ static int xidx(int j, int v) {
     return (j >> 2) * 256 + (j & 3) * 32 + (v & 31) + ((v >> 5) << 7);
   }
-  // scale-plane byte offset of segment j within its row (OOB when invalid)
+  static constexpr int MU = 4;  // scale-plane bytes per segment (16 per block)
+  // scale-plane byte offset of segment j within its panel row (OOB when
+  // invalid)
   __device__ __forceinline__ static uint32_t meta_off(int j, bool valid) {
-    return valid ? (uint32_t)((j >> 2) * 16) : OOB;
+    return valid ? (uint32_t)(((j & 63) >> 2) * 16) : OOB;
   }
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return bload16m(r, off);
@@ -392,8 +424,9 @@ struct Seg<NX_FMT_Q8_0> {
     float post;
   };
   __device__ __forceinline__ static int xidx(int j, int v) { return j * 32 + v; }
+  static constexpr int MU = 2;  // scale-plane bytes per segment
   __device__ __forceinline__ static uint32_t meta_off(int j, bool valid) {
-    return valid ? (uint32_t)(j * 2) : OOB;
+    return valid ? (uint32_t)((j & 63) * 2) : OOB;
   }
   // the f16 scale may sit in either half of an aligned dword
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -467,8 +500,9 @@ struct Seg<NX_FMT_Q4_0> {
   using X = X4;
   using Run = Run4;
   __device__ __forceinline__ static int xidx(int j, int v) { return j * 64 + v; }
+  static constexpr int MU = 4;  // scale-plane bytes per segment
   __device__ __forceinline__ static uint32_t meta_off(int j, bool valid) {
-    return valid ? (uint32_t)(j * 4) : OOB;
+    return valid ? (uint32_t)((j & 63) * 4) : OOB;
   }
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return bload4m(r, off);
@@ -510,8 +544,9 @@ struct Seg<NX_FMT_Q2_K> {
   __device__ __forceinline__ static int xidx(int j, int v) {
     return (j >> 2) * 256 + (j & 3) * 64 + v;
   }
+  static constexpr int MU = 8;  // scale-plane bytes per segment
   __device__ __forceinline__ static uint32_t meta_off(int j, bool valid) {
-    return valid ? (uint32_t)(j * 8) : OOB;
+    return valid ? (uint32_t)((j & 63) * 8) : OOB;
   }
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, NX_GEMV_META_CPOL);
@@ -558,6 +593,7 @@ struct Seg<NX_FMT_F32> {
     float x[8];
   };
   __device__ __forceinline__ static int xidx(int j, int v) { return j * 8 + v; }
+  static constexpr int MU = 0;  // no scale plane
   __device__ __forceinline__ static uint32_t meta_off(int, bool) { return 0; }
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t, uint32_t) { return 0; }
   __device__ __forceinline__ static void prep(const float *x, X &o) {
@@ -590,6 +626,7 @@ struct Seg16 {
     float x[16];
   };
   __device__ __forceinline__ static int xidx(int j, int v) { return j * 16 + v; }
+  static constexpr int MU = 0;  // no scale plane
   __device__ __forceinline__ static uint32_t meta_off(int, bool) { return 0; }
   __device__ __forceinline__ static Meta load_meta(__amdgpu_buffer_rsrc_t, uint32_t) { return 0; }
   __device__ __forceinline__ static void prep(const float *x, X &o) {

@@ -244,11 +244,16 @@ __device__ __forceinline__ int kpad_steps(int cols) {
   return (cols + kwin<FMT>() - 1) / kwin<FMT>() * win_steps<FMT>();
 }
 
-// Weight addressing.  A lane's loads of row n are at lane base lq[n] (row
-// offset plus the lane quarter's place in the line) + a wave-uniform part
-// (group, plane half and line of the step's window) + a constant.  Every
-// part goes into the range-checked offset, so rows past the matrix read zero;
-// blocks past a row's end (last partial window only) read finite neighbours,
+// Weight addressing.  The planes are in panels of 64 segments (nx_device.hpp):
+// window win lies in panel g = win / 8, and every row has prq code bytes and
+// prm scale bytes in each panel.  A lane's loads of row n are at lane base
+// lq[n] (the row times prq plus the lane quarter's place in the line) + a
+// wave-uniform part (panel base, plane half and line of the step's window) +
+// a constant.  Every part goes into the range-checked offset: the plane ends
+// at the last panel, where rows past the matrix read zero (rows past the
+// matrix in an earlier panel read the next panel's finite weights; their
+// outputs are never written); blocks past a row's end (last partial window
+// only) read finite neighbours or the zero padding of a short last panel,
 // which meet zero activations.
 template <int FMT>
 __device__ __forceinline__ uint32_t code_lane_off(uint32_t row_off, int q) {
@@ -261,28 +266,28 @@ __device__ __forceinline__ uint32_t meta_lane_off(uint32_t row_off, int q) {
   if constexpr (FMT == NX_FMT_Q8_0) return row_off + 4u * q;
   return row_off + 16u * (q >> 1);
 }
-// uniform part of window win, code-plane half p: group (64 segments), half,
+// uniform part of window win, code-plane half p: panel (64 segments), half,
 // 8-segment line
-__device__ __forceinline__ uint32_t code_win_off(int win, int p, int nseg) {
+__device__ __forceinline__ uint32_t code_win_off(int win, int p, int rows, int nseg) {
   const int g = win >> 3;
-  const int gsz = min(64, nseg - 64 * g);
-  return (uint32_t)(g * 2048 + p * gsz * 16 + (win & 7) * 128);
+  return (uint32_t)g * (uint32_t)rows * panel_row_bytes(nseg, 32) +
+         (uint32_t)(p * panel_gsz(g, nseg) * 16 + (win & 7) * 128);
 }
 
 // codes of step S of window win
 template <int FMT, int S, int NT>
 __device__ __forceinline__ void fetch_codes(WCodes<FMT, NT> &w, __amdgpu_buffer_rsrc_t rq,
-                                            const uint32_t (&lq)[NT], int win, int nseg) {
+                                            const uint32_t (&lq)[NT], int win, int rows, int nseg) {
   if constexpr (FMT == NX_FMT_Q8_0) {
-    const uint32_t u = code_win_off(win, S >> 1, nseg);
+    const uint32_t u = code_win_off(win, S >> 1, rows, nseg);
 #pragma unroll
     for (int n = 0; n < NT; ++n) w.c[n] = bload16(rq, lq[n] + u + 16u * (S & 1));
   } else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) {
-    const uint32_t u = code_win_off(win, S >> 2, nseg);
+    const uint32_t u = code_win_off(win, S >> 2, rows, nseg);
 #pragma unroll
     for (int n = 0; n < NT; ++n) w.c[n] = bload8(rq, lq[n] + u + 16u * (S & 3));
   } else {  // F32: segments 8 win + 2q (+1), both halves: floats 64 win + 16q ..
-    const uint32_t u0 = code_win_off(win, 0, nseg), u1 = code_win_off(win, 1, nseg);
+    const uint32_t u0 = code_win_off(win, 0, rows, nseg), u1 = code_win_off(win, 1, rows, nseg);
 #pragma unroll
     for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -290,15 +295,23 @@ __device__ __forceinline__ void fetch_codes(WCodes<FMT, NT> &w, __amdgpu_buffer_
   }
 }
 
-// scales of window win: Q8_0 blocks 8 win + 2q, +1 (one dword, rows padded
-// to whole dwords); Q4_K block 2 win + q/2; Q4_0 segments 8 win + 4(q/2) .. +3
+// scales of window win: Q8_0 blocks 8 win + 2q, +1 (one dword, panel rows
+// padded to whole dwords); Q4_K block 2 win + q/2; Q4_0 segments 8 win +
+// 4(q/2) .. +3.  A window's scales are 8 MU bytes of its panel row (MU scale
+// bytes per segment), full panel rows 64 MU.
 template <int FMT, int NT>
 __device__ __forceinline__ void fetch_meta(WMeta<FMT, NT> &m, __amdgpu_buffer_rsrc_t rm,
-                                           const uint32_t (&lm)[NT], int win) {
+                                           const uint32_t (&lm)[NT], int win, int rows, int nseg) {
+  constexpr int MU = Seg<FMT>::MU;
+  if constexpr (MU > 0) {
+    const int g = win >> 3;
+    const uint32_t u = (uint32_t)g * (uint32_t)rows * panel_row_bytes(nseg, MU) +
+                       (uint32_t)(win & 7) * (8u * MU);
 #pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    if constexpr (FMT == NX_FMT_Q8_0) m.m[n] = bload4(rm, lm[n] + 16u * win);
-    else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) m.m[n] = bload16(rm, lm[n] + 32u * win);
+    for (int n = 0; n < NT; ++n) {
+      if constexpr (FMT == NX_FMT_Q8_0) m.m[n] = bload4(rm, lm[n] + u);
+      else m.m[n] = bload16(rm, lm[n] + u);
+    }
   }
 }
 
@@ -705,13 +718,15 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
   const int ks_end = (split + 1) * nbody / g.ksplit * NB;
 
   // ---- weights: rows n0 + 16 NT wave + 16 n + lane % 16, quarter lane / 16
+  // (lane bases at the rows' offsets in a panel)
   const int l16 = lane & 15, q = lane >> 4;
+  const uint32_t rbq = panel_row_bytes(nseg, 32), rbm = panel_row_bytes(nseg, Seg<FMT>::MU);
   uint32_t lq[NT], lm[NT];
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const uint32_t wrow = (uint32_t)(n0 + 16 * NT * wave + 16 * n + l16);
-    lq[n] = code_lane_off<FMT>(wrow * rq, q);
-    lm[n] = meta_lane_off<FMT>(wrow * rm, q);
+    lq[n] = code_lane_off<FMT>(wrow * rbq, q);
+    lm[n] = meta_lane_off<FMT>(wrow * rbm, q);
   }
 
   // activation loads I0 .. I1-1 of stage ks
@@ -740,11 +755,11 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
     if constexpr (META2 && S == 0) {
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
-        fetch_meta<FMT, NT>(mbuf[(J / WS) % NMB][mt], mt == 0 ? rm0 : rm1, lm, win);
+        fetch_meta<FMT, NT>(mbuf[(J / WS) % NMB][mt], mt == 0 ? rm0 : rm1, lm, win, rows, nseg);
     }
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
-      fetch_codes<FMT, S, NT>(wbuf[J % NBUF][mt], mt == 0 ? rq0 : rq1, lq, win, nseg);
+      fetch_codes<FMT, S, NT>(wbuf[J % NBUF][mt], mt == 0 ? rq0 : rq1, lq, win, rows, nseg);
   };
   // single-buffered scales of the window that starts at step J
   auto issue_meta1 = [&](auto pos, int wbase) {
@@ -752,7 +767,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
     if constexpr (!META2 && n_meta_loads<FMT>() > 0) {
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
-        fetch_meta<FMT, NT>(mbuf[0][mt], mt == 0 ? rm0 : rm1, lm, wbase + J / WS);
+        fetch_meta<FMT, NT>(mbuf[0][mt], mt == 0 ? rm0 : rm1, lm, wbase + J / WS, rows, nseg);
     }
   };
   // the late issues of step T (see LoadSchedule)

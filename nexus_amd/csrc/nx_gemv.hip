@@ -60,6 +60,10 @@
 #ifndef NX_GEMV_COMBINE_SLOTS
 #define NX_GEMV_COMBINE_SLOTS 2
 #endif
+// rows of a workgroup's run interleaved over its row groups (see k_gemv_gateup)
+#ifndef NX_GEMV_WG_INTERLEAVE
+#define NX_GEMV_WG_INTERLEAVE 1
+#endif
 // cache policy of the weight-code loads (2: non-temporal, streamed past the
 // caches so the small activation and route arrays stay resident)
 #ifndef NX_GEMV_WEIGHT_CPOL
@@ -248,49 +252,56 @@ struct RowGroup {
   }
 
   // Issue the loads of logical rows q0 .. q0+U-1 (matrix rows rm.row(q)) of
-  // view v; rows at or past rm.end (and absent segments) read as zero.  When
-  // a row group spans whole waves (L >= 64) the rows are wave-uniform: each
-  // row gets its own buffer resource (size 0 past the end), built on the
-  // scalar unit, and the lane offsets stay constant.  Otherwise rows differ
-  // within a wave and the row offset is added per lane.
+  // view v; rows at or past rm.end (and absent segments) read as zero.  The
+  // planes are in panels of 64 segments (nx_device.hpp).  When a row group
+  // spans whole waves (L >= 64) with one segment per lane, a wave's segments
+  // are one panel and the rows are wave-uniform: each row gets its own buffer
+  // resource at its part of that panel (size 0 past the end), built on the
+  // scalar unit, and the lane offsets stay constant.  Otherwise the lanes
+  // add their rows' panel offsets to plane-wide resources.
   __device__ __forceinline__ void load(Stage &st, const SlotView &v, int r0, int row_end) const {
     load(st, v, RowMap{0, 1, row_end}, r0);
   }
   __device__ __forceinline__ void load(Stage &st, const SlotView &v, const RowMap &rm,
                                        int q0) const {
     constexpr int CH = code_chunks<FMT>();
+    constexpr int CU = 16 * CH;  // code bytes per segment
     uint32_t off0[SPL], off1[SPL], moff[SPL];
 #pragma unroll
     for (int m = 0; m < SPL; ++m) {
       const int j = seg0 + li + m * L;
       const bool jv = j < v.nseg;
-      off0[m] = jv ? (CH == 1 ? (uint32_t)j * 16u : seg_off(j, 0, v.nseg)) : OOB;
+      off0[m] = jv ? (CH == 1 ? (uint32_t)(j & 63) * 16u : seg_off(j, 0, v.nseg)) : OOB;
       off1[m] = jv ? seg_off(j, 1, v.nseg) : OOB;
       moff[m] = S::meta_off(j, jv);
     }
-    if constexpr (L >= 64) {
+    if constexpr (L >= 64 && SPL == 1) {
       // the row is wave-uniform: say so, or the resources below become
       // per-lane values and every load a waterfall loop
       const RowMap m{__builtin_amdgcn_readfirstlane(rm.base), __builtin_amdgcn_readfirstlane(rm.step),
                      __builtin_amdgcn_readfirstlane(rm.end)};
       const int q0u = __builtin_amdgcn_readfirstlane(q0);
+      // the wave's panel (seg0 and L are whole groups of 64)
+      const int g = __builtin_amdgcn_readfirstlane((seg0 + li) >> 6);
+      const uint32_t pq = panel_row_bytes(v.nseg, CU), pm = panel_row_bytes(v.nseg, S::MU);
+      const uint8_t *bq0 = v.q0 + (size_t)g * v.rows * pq;
+      const uint8_t *bq1 = v.q1 + (size_t)g * v.rows * pq;
+      const uint8_t *bm0 = v.m0 + (size_t)g * v.rows * pm;
+      const uint8_t *bm1 = v.m1 + (size_t)g * v.rows * pm;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int r = m.row(q0u + u);
         const bool rv = r < m.end;
-        const uint32_t nq = rv ? v.rq : 0u, nm = rv ? v.rm : 0u;
-        const __amdgpu_buffer_rsrc_t rq0 = make_rsrc_u(v.q0 + (size_t)r * v.rq, nq);
-        const __amdgpu_buffer_rsrc_t rq1 = make_rsrc_u(v.q1 + (size_t)r * v.rq, nq);
-        const __amdgpu_buffer_rsrc_t rm0 = make_rsrc_u(v.m0 + (size_t)r * v.rm, nm);
-        const __amdgpu_buffer_rsrc_t rm1 = make_rsrc_u(v.m1 + (size_t)r * v.rm, nm);
+        const uint32_t nq = rv ? pq : 0u, nm = rv ? pm : 0u;
+        const __amdgpu_buffer_rsrc_t rq0 = make_rsrc_u(bq0 + (size_t)r * pq, nq);
+        const __amdgpu_buffer_rsrc_t rq1 = make_rsrc_u(bq1 + (size_t)r * pq, nq);
+        const __amdgpu_buffer_rsrc_t rm0 = make_rsrc_u(bm0 + (size_t)r * pm, nm);
+        const __amdgpu_buffer_rsrc_t rm1 = make_rsrc_u(bm1 + (size_t)r * pm, nm);
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt) {
-#pragma unroll
-          for (int m = 0; m < SPL; ++m) {
-            st.q[u][mt][m][0] = bload16w(mt == 0 ? rq0 : rq1, off0[m]);
-            st.q[u][mt][m][1] = CH == 2 ? bload16w(mt == 0 ? rq0 : rq1, off1[m]) : make_uint4(0, 0, 0, 0);
-            st.m[u][mt][m] = S::load_meta(mt == 0 ? rm0 : rm1, moff[m]);
-          }
+          st.q[u][mt][0][0] = bload16w(mt == 0 ? rq0 : rq1, off0[0]);
+          st.q[u][mt][0][1] = CH == 2 ? bload16w(mt == 0 ? rq0 : rq1, off1[0]) : make_uint4(0, 0, 0, 0);
+          st.m[u][mt][0] = S::load_meta(mt == 0 ? rm0 : rm1, moff[0]);
         }
       }
     } else {
@@ -298,16 +309,26 @@ struct RowGroup {
       const __amdgpu_buffer_rsrc_t rq1 = make_rsrc_u(v.q1, (uint32_t)v.rows * v.rq);
       const __amdgpu_buffer_rsrc_t rm0 = make_rsrc_u(v.m0, (uint32_t)v.rows * v.rm);
       const __amdgpu_buffer_rsrc_t rm1 = make_rsrc_u(v.m1, (uint32_t)v.rows * v.rm);
+      // each segment index m's panel, wave-uniform (rows of one panel below
+      // 64 lanes; one panel per m from 64), and the panel row bytes
+      const uint32_t prq = panel_row_bytes(v.nseg, CU), prm = panel_row_bytes(v.nseg, S::MU);
+      uint32_t pbq[SPL], pbm[SPL];
+#pragma unroll
+      for (int m = 0; m < SPL; ++m) {
+        const int g = __builtin_amdgcn_readfirstlane((seg0 + li + m * L) >> 6);
+        pbq[m] = panel_row_off(0, g, v.rows, v.nseg, CU);
+        pbm[m] = panel_row_off(0, g, v.rows, v.nseg, S::MU);
+      }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int r = rm.row(q0 + u);
         const bool rv = r < rm.end;
-        const uint32_t rqo = rv ? (uint32_t)r * v.rq : OOB;
-        const uint32_t rmo = rv ? (uint32_t)r * v.rm : OOB;
 #pragma unroll
-        for (int mt = 0; mt < NMAT; ++mt) {
+        for (int m = 0; m < SPL; ++m) {
+          const uint32_t rqo = rv ? pbq[m] + (uint32_t)r * prq : OOB;
+          const uint32_t rmo = rv ? pbm[m] + (uint32_t)r * prm : OOB;
 #pragma unroll
-          for (int m = 0; m < SPL; ++m) {
+          for (int mt = 0; mt < NMAT; ++mt) {
             st.q[u][mt][m][0] = bload16w(mt == 0 ? rq0 : rq1, rqo + off0[m]);
             st.q[u][mt][m][1] =
                 CH == 2 ? bload16w(mt == 0 ? rq0 : rq1, rqo + off1[m]) : make_uint4(0, 0, 0, 0);
@@ -604,10 +625,19 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
   __shared__ float red[KSPLIT > 1 ? 4 * RED_ROWS * NMAT * NT : 1];
 
   const SlotView v = slot_view(a, slot, n_active, active, offsets, e_one);
-  // this group's logical rows 0 .. nq-1: one contiguous run of rpg rows
+  // this group's logical rows 0 .. nq-1: the workgroup owns one contiguous
+  // run of GROUPS * rpg rows; interleaved, its row groups take every
+  // GROUPS-th row of it (row = run start + q * GROUPS + group), so that at
+  // each stage the waves read neighbouring rows, else one run of rpg rows each
+#if NX_GEMV_WG_INTERLEAVE
+  const int wg0 = bx * GROUPS * rpg;
+  const RowMap rm{wg0 + grp, GROUPS, min(v.rows, wg0 + GROUPS * rpg)};
+  const int nq = rm.end > rm.base ? (rm.end - rm.base + GROUPS - 1) / GROUPS : 0;
+#else
   const int gidx = bx * GROUPS + grp;
   const RowMap rm{gidx * rpg, 1, min(v.rows, gidx * rpg + rpg)};
   const int nq = max(0, rm.end - rm.base);
+#endif
   // activation row of token t of the slot (one token: row 0, no lookup)
   auto row_of = [&](int t) {
     return PLAIN ? v.pair0 + t

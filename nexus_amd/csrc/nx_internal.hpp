@@ -32,7 +32,8 @@ void clear_error();
 // Resident per-format layout.  A GGUF block of `block` elements and
 // `block_bytes` bytes is split into a code plane (qs_bytes per block) and a
 // scale plane (meta_bytes per block); the code plane of each row is cut into
-// 32-byte segments stored half-interleaved (nx_device.hpp).  Q4_K: 144 B =
+// 32-byte segments stored half-interleaved, rows of more than 64 segments in
+// panels of 64 segments (nx_device.hpp).  Q4_K: 144 B =
 // 128 B codes + 16 B {d, dmin, scales12}; Q8_0: 34 B = 32 B codes + 2 B d;
 // Q4_0: 18 B = 16 B codes + 2 B d; F32: rows padded to 8 floats, no scales.
 struct FormatInfo {
@@ -54,7 +55,9 @@ struct RolePlane {
   int rows = 0;
   int cols = 0;        // logical columns
   int nseg = 0;        // 32-byte code segments per row
-  uint32_t row_qs = 0;    // code-plane bytes per row (nseg * 32)
+  // bytes per row: nseg * 32 (codes) when a row is one panel, else whole
+  // zero-padded panels of 64 segments (plane bytes = rows * row_qs)
+  uint32_t row_qs = 0;    // code-plane bytes per row
   uint32_t row_meta = 0;  // scale-plane bytes per row
 };
 

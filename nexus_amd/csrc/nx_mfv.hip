@@ -134,10 +134,13 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
     }
   }
   // step i: row tile i / MV_KS, chunk c0 + i % MV_KS
-  // Rows past the matrix read as zeros through the resources' size (row *
-  // row_qs >= rows * row_qs); a chunk past the row (wave-uniform) reads at
-  // OOB.  Per-lane parts of the offsets stay in one register per step; the
-  // rest goes in the scalar offset.
+  // The planes are in panels of 64 segments (nx_device.hpp): the chunk's
+  // panel grp starts at grp * rows * prq (codes) and grp * rows * prm
+  // (scales), prq and prm a row's bytes in a panel, and holds gsz segments
+  // of each row.  Rows past the matrix and chunks past the row (wave-uniform)
+  // read at OOB.  Per-lane parts
+  // of the offsets stay in one register per step; the rest goes in the scalar
+  // offset.
   auto issue = [&](MfvStep<NMAT> &w, int i) {
     const int row = row_base + 16 * (i / MV_KS) + l16;
     const int c = c0 + i % MV_KS;
@@ -147,12 +150,14 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
     const int j0 = 4 * c;
     const int grp = j0 >> 6;
     const int gsz = min(64, a.nseg - (grp << 6));
-    const uint32_t base = (uint32_t)(grp * 2048 + (j0 & 63) * 16);
-    // steps past the last (issued by the pipeline's tail) and chunks past
-    // the row read at OOB (wave-uniform)
-    const bool cv = i < NSTEP && c < a.nchunk;
-    const uint32_t vq = cv ? (uint32_t)row * a.row_qs + 16u * g : OOB;
-    const uint32_t vm = cv ? (uint32_t)row * a.row_meta + 16u * c : OOB;
+    const uint32_t prq = panel_row_bytes(a.nseg, 32), prm = panel_row_bytes(a.nseg, 4);
+    const uint32_t base = (uint32_t)grp * (uint32_t)a.rows * prq + (uint32_t)((j0 & 63) * 16);
+    // steps past the last (issued by the pipeline's tail), chunks past the
+    // row (wave-uniform) and rows past the matrix read at OOB
+    const bool cv = i < NSTEP && c < a.nchunk && row < a.rows;
+    const uint32_t vq = cv ? (uint32_t)row * prq + 16u * g : OOB;
+    const uint32_t vm = cv ? ((uint32_t)grp * (uint32_t)a.rows + (uint32_t)row) * prm + 16u * (uint32_t)(c - 16 * grp)
+                           : OOB;
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) {
 #pragma unroll

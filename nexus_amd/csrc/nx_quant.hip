@@ -294,12 +294,12 @@ __global__ __launch_bounds__(256) void k_quant_q2k(const float *__restrict__ src
 // ---------------------------------------------------------------- repack
 // GGUF row-major blocks -> resident planes (nx_device.hpp): the code plane is
 // written as 16-byte halves of 32-byte segments at their half-interleaved
-// offsets, the scale plane as {d, dmin, scales12} (Q4_K) or d (Q8_0, Q4_0).
-// One thread per 16-byte code half; byte copies because GGUF blocks are not
-// 4-byte aligned.
+// offsets within the panels of 64 segments, the scale plane as {d, dmin,
+// scales12} (Q4_K) or d (Q8_0, Q4_0) in the same panels.  One thread per
+// 16-byte code half; byte copies because GGUF blocks are not 4-byte aligned.
 template <int FMT>
 __global__ __launch_bounds__(256) void k_repack_codes(const uint8_t *__restrict__ src, int rows,
-                                                      int cols, int nseg, uint32_t row_qs,
+                                                      int cols, int nseg,
                                                       uint8_t *__restrict__ qs) {
   const size_t total = (size_t)rows * nseg * 2;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(256) void k_repack_codes(const uint8_t *__restrict_
     const int h = (int)(i & 1);
     const size_t rj = i >> 1;
     const int r = (int)(rj / nseg), j = (int)(rj - (size_t)r * nseg);
-    uint8_t *dst = qs + (size_t)r * row_qs + seg_off(j, h, nseg);
+    uint8_t *dst = qs + code_off(r, j, h, rows, nseg);
     if constexpr (FMT == NX_FMT_F32) {
       const float *sf = reinterpret_cast<const float *>(src) + (size_t)r * cols;
       float *df = reinterpret_cast<float *>(dst);
@@ -362,11 +362,13 @@ __global__ __launch_bounds__(256) void k_repack_codes(const uint8_t *__restrict_
 
 template <int FMT>
 __global__ __launch_bounds__(256) void k_repack_meta(const uint8_t *__restrict__ src, int rows,
-                                                     int cols, int nseg, uint32_t row_meta,
+                                                     int cols, int nseg,
                                                      uint8_t *__restrict__ meta) {
   constexpr int BLK = FMT == NX_FMT_Q4_K ? 256 : 32;
   constexpr int BB = FMT == NX_FMT_Q4_K ? 144 : (FMT == NX_FMT_Q8_0 ? 34 : 18);
   constexpr int MB = FMT == NX_FMT_Q4_K ? 16 : 2;
+  // scale bytes per segment, and blocks per panel of 64 segments
+  constexpr int MU = Seg<FMT>::MU, BPP = MU > 0 ? 64 * MU / MB : 1;
   const int nb = cols / BLK;
   // Q4_0 rows are padded to an even block count (two blocks per segment)
   const int slots = FMT == NX_FMT_Q4_0 ? 2 * nseg : nb;
@@ -374,7 +376,7 @@ __global__ __launch_bounds__(256) void k_repack_meta(const uint8_t *__restrict__
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
     const int r = (int)(i / slots), b = (int)(i - (size_t)r * slots);
-    uint8_t *dst = meta + (size_t)r * row_meta + (size_t)b * MB;
+    uint8_t *dst = meta + panel_row_off(r, b / BPP, rows, nseg, MU) + (uint32_t)(b % BPP) * MB;
     const uint8_t *s = b < nb ? src + ((size_t)r * nb + b) * BB : nullptr;
 #pragma unroll
     for (int v = 0; v < MB; ++v) dst[v] = s ? s[v] : (uint8_t)0;
@@ -382,12 +384,13 @@ __global__ __launch_bounds__(256) void k_repack_meta(const uint8_t *__restrict__
 }
 
 // Q2_K code plane: one thread per 64-element segment j (block j/4, elements
-// 64(j%4) ..), its 16 bytes at 16 j.  Element e of a block sits in bits
+// 64(j%4) ..), its 16 bytes at 16 (j % 64) in its panel row (16 bytes per
+// segment).  Element e of a block sits in bits
 // 2(e%4) of qs byte e/4; resident byte 4k+i holds, from bit 0, the codes of
 // elements 8k+i and 32+8k+i, then 8k+4+i and 32+8k+4+i of the segment (the
 // 4-bit dword order of each half, the halves two bits apart).
 __global__ __launch_bounds__(256) void k_repack_codes_q2k(const uint8_t *__restrict__ src, int rows,
-                                                          int cols, int nseg, uint32_t row_qs,
+                                                          int cols, int nseg,
                                                           uint8_t *__restrict__ qs) {
   const int nb = cols / 256;
   const size_t total = (size_t)rows * nseg;
@@ -397,7 +400,7 @@ __global__ __launch_bounds__(256) void k_repack_codes_q2k(const uint8_t *__restr
     const uint8_t *b = src + ((size_t)r * nb + (j >> 2)) * 84 + 16;
     const int e0 = (j & 3) * 64;
     auto code = [&](int e) { return (uint32_t)(b[(e0 + e) >> 2] >> (2 * ((e0 + e) & 3))) & 3u; };
-    uint8_t *dst = qs + (size_t)r * row_qs + (size_t)j * 16;
+    uint8_t *dst = qs + panel_row_off(r, j >> 6, rows, nseg, 16) + (uint32_t)(j & 63) * 16;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
@@ -410,14 +413,14 @@ __global__ __launch_bounds__(256) void k_repack_codes_q2k(const uint8_t *__restr
 // Q2_K scale plane: per segment j (block j/4, sub-blocks 4(j%4) ..) the
 // eight bytes {d, dmin, four scale/min bytes}
 __global__ __launch_bounds__(256) void k_repack_meta_q2k(const uint8_t *__restrict__ src, int rows,
-                                                         int cols, int nseg, uint32_t row_meta,
+                                                         int cols, int nseg,
                                                          uint8_t *__restrict__ meta) {
   const int nb = cols / 256;
   const size_t total = (size_t)rows * nseg;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
        i += (size_t)gridDim.x * blockDim.x) {
     const int r = (int)(i / nseg), j = (int)(i - (size_t)r * nseg);
-    uint8_t *dst = meta + (size_t)r * row_meta + (size_t)j * 8;
+    uint8_t *dst = meta + panel_row_off(r, j >> 6, rows, nseg, 8) + (uint32_t)(j & 63) * 8;
     const uint8_t *b = src + ((size_t)r * nb + (j >> 2)) * 84;
 #pragma unroll
     for (int v = 0; v < 4; ++v) dst[v] = b[80 + v];
@@ -494,11 +497,11 @@ int launch_repack(nx_ctx *c, int fmt, const void *d_src, const RolePlane &pl, ui
 #define NX_RP(F, NAME)                                                                          \
   do {                                                                                          \
     NX_TRY(launch(c, NAME, [&] {                                                                \
-      k_repack_codes<F><<<gc, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_qs, qs); \
+      k_repack_codes<F><<<gc, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, qs); \
     }));                                                                                        \
     if (F != NX_FMT_F32 && F != NX_FMT_F16 && F != NX_FMT_BF16)                                \
       NX_TRY(launch(c, NAME, [&] {                                                              \
-        k_repack_meta<F><<<gm, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_meta, \
+        k_repack_meta<F><<<gm, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, \
                                                     meta);                                      \
       }));                                                                                      \
     return NX_OK;                                                                               \
@@ -513,10 +516,10 @@ int launch_repack(nx_ctx *c, int fmt, const void *d_src, const RolePlane &pl, ui
   case NX_FMT_Q2_K: {
     const unsigned g2 = grid_for((size_t)pl.rows * pl.nseg, 256);
     NX_TRY(launch(c, "repack_q2_k", [&] {
-      k_repack_codes_q2k<<<g2, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_qs, qs);
+      k_repack_codes_q2k<<<g2, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, qs);
     }));
     return launch(c, "repack_q2_k", [&] {
-      k_repack_meta_q2k<<<g2, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, pl.row_meta, meta);
+      k_repack_meta_q2k<<<g2, 256, 0, c->stream>>>(s, pl.rows, pl.cols, pl.nseg, meta);
     });
   }
   }
