@@ -371,7 +371,6 @@ int nx_ctx_destroy(nx_ctx *c) {
     (void)hipEventDestroy(pe.stop);
   }
   for (auto e : c->event_pool) (void)hipEventDestroy(e);
-  release_blas(c);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
   return NX_OK;

@@ -113,9 +113,6 @@ struct nx_ctx {
   // own start and end
   hipEvent_t launch_start = nullptr, launch_stop = nullptr;
   bool launch_timed = false;
-  // rocBLAS handle on this context's device (fast-mode router logits of
-  // token batches, a plain f32 GEMM), created on first use
-  void *blas = nullptr;
 };
 
 // one dense weight matrix (rows x cols, row-major as GGUF stores it), held
@@ -233,8 +230,6 @@ int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, 
 // order with separately rounded products and sums
 int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, int E, int H,
                          bool exact, float *d_out);
-// destroys the context's rocBLAS handle, if one was created
-void release_blas(nx_ctx *c);
 // per-row sequential sum of squares (rms_norm's variance sum, bit-exact)
 int launch_sumsq_exact(nx_ctx *c, const float *d_x, int T, int H, float *d_out);
 // exact RMSNorm + router logits of T tokens in one launch (block prologue);

@@ -35,10 +35,7 @@
 //   k_logits_dot     fast, few tokens.  A workgroup per (expert, block of
 //                    tokens) strides over the row in 16-byte loads and reduces
 //                    with DPP and LDS.
-//   Fast mode with more tokens is a plain f32 GEMM (rocBLAS sgemm on the
-//   matrix cores).
-#include <rocblas/rocblas.h>
-
+//   k_logits_mfma    fast, more tokens: f32 MFMA tiles of tokens x experts.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 
@@ -633,6 +630,109 @@ __global__ __launch_bounds__(256) void k_logits_dot(const float *__restrict__ W,
   }
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Fast mode, many tokens, on the matrix cores (v_mfma_f32_16x16x4_f32, f32
+// operands and sums): logits = X . W^T.  A wave owns MT x NT tiles of 16
+// tokens x 16 experts over a range of 16-column steps.  Lane l feeds row
+// l % 16 of each operand tile (token t0 + 16 m + l % 16 of X, expert e0 + 16
+// n + l % 16 of W) with one 16-byte load per step, columns k + 4 (l / 16) ..
+// + 3, one per MFMA: the four MFMAs of a step cover the step's 16 columns in
+// a permuted order, the same for both operands, which fast mode allows.
+// KS waves of a workgroup split the steps and add their tiles through LDS in
+// wave order; with KS = 1 the four waves own four neighbouring token tiles.
+// Lane l holds output rows 4 (l / 16) .. + 3 of column l % 16 of a tile.
+// Rows of X and W past the matrices, and columns past the row (whole float4s:
+// H % 4 == 0), read as zeros.  D steps are in flight while one is multiplied.
+template <int MT, int NT, int KS>
+__global__ __launch_bounds__(256) void k_logits_mfma(const float *__restrict__ W,
+                                                     const float *__restrict__ X, int T, int E,
+                                                     int H, float *__restrict__ out) {
+  constexpr int WT = 4 / KS;  // a workgroup's output tiles, along the tokens
+  constexpr int D = 3;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int kpart = wave % KS, tw = wave / KS;
+  const int t0 = ((int)blockIdx.x * WT + tw) * 16 * MT, e0 = (int)blockIdx.y * 16 * NT;
+  const int r = lane & 15, g = lane >> 4;
+  const auto rx = make_rsrc(X, (uint32_t)((size_t)T * H * 4));
+  const auto rw = make_rsrc(W, (uint32_t)((size_t)E * H * 4));
+  uint32_t xo[MT], wo[NT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const int t = t0 + 16 * m + r;
+    xo[m] = t < T ? (uint32_t)t * (uint32_t)H * 4u : OOB;
+  }
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int e = e0 + 16 * n + r;
+    wo[n] = e < E ? (uint32_t)e * (uint32_t)H * 4u : OOB;
+  }
+  const int nsteps = (H + 15) / 16;
+  const int sb = kpart * nsteps / KS, se = (kpart + 1) * nsteps / KS;
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[m][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  uint4 a[D][MT], b[D][NT];
+  // loads of step s into ring slot j (steps past the range read zeros)
+  auto issue = [&](int j, int s) {
+    const int k = 16 * s + 4 * g;
+    const uint32_t ko = s < se && k < H ? 4u * (uint32_t)k : OOB;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) a[j][m] = bload16(rx, xo[m] + ko);
+#pragma unroll
+    for (int n = 0; n < NT; ++n) b[j][n] = bload16(rw, wo[n] + ko);
+  };
+  auto lane_f = [](const uint4 &v, int i) {
+    return __uint_as_float(i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w);
+  };
+#pragma unroll
+  for (int j = 0; j < D - 1; ++j) issue(j, sb + j);
+  for (int s = sb; s < se; s += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      if (s + j >= se) break;  // wave-uniform
+      issue((j + D - 1) % D, s + j + D - 1);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int n = 0; n < NT; ++n)
+            acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(lane_f(a[j][m], i), lane_f(b[j][n], i),
+                                                             acc[m][n], 0, 0, 0);
+    }
+  }
+  if constexpr (KS > 1) {
+    __shared__ f32x4_t red[4 * MT * NT * 64];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) red[((wave * MT + m) * NT + n) * 64 + lane] = acc[m][n];
+    __syncthreads();
+    if (kpart != 0) return;  // wave-uniform
+#pragma unroll
+    for (int q = 1; q < KS; ++q)
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int n = 0; n < NT; ++n) acc[m][n] += red[(((tw * KS + q) * MT + m) * NT + n) * 64 + lane];
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int e = e0 + 16 * n + r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 16 * m + 4 * g + i;
+        if (t < T && e < E) out[(size_t)t * E + e] = acc[m][n][i];
+      }
+    }
+}
+
 void launch_tile(nx_ctx *c, int rb, const float *W, const float *X, int T, int E, int H,
                  float *out) {
   const int rows = 16 * rb;
@@ -642,33 +742,15 @@ void launch_tile(nx_ctx *c, int rb, const float *W, const float *X, int T, int E
   else go(c, k_logits_tile<1>, dim3(grid), dim3(256), 0, W, X, T, E, H, out);
 }
 
-// the context's rocBLAS handle, created on first use on the context's device
-int blas_handle(nx_ctx *c) {
-  if (c->blas) return NX_OK;
-  NX_HIP(hipSetDevice(c->device));
-  rocblas_handle h = nullptr;
-  if (rocblas_create_handle(&h) != rocblas_status_success)
-    return fail(NX_ERR_DEVICE, "rocblas_create_handle failed");
-  if (rocblas_set_stream(h, c->stream) != rocblas_status_success) {
-    (void)rocblas_destroy_handle(h);
-    return fail(NX_ERR_DEVICE, "rocblas_set_stream failed");
-  }
-  c->blas = h;
-  return NX_OK;
-}
-
 }  // namespace
-
-void release_blas(nx_ctx *c) {
-  if (c->blas) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(c->blas));
-  c->blas = nullptr;
-}
 
 // chains (token, expert pairs) up to which the exact path uses k_logits_chain8
 constexpr long LOGITS_CHAIN8_MAX = 16384;
 constexpr long LOGITS_RUNS_MAX_WG = 256;  // workgroups of the register-run chains
-// fast path: tokens up to which k_logits_dot is used
-constexpr int LOGITS_DOT_MAX_T = 8;
+// fast path: tokens up to which k_logits_dot is used (eight tokens per
+// workgroup beyond 4; the MFMA tiles have too few workgroups below ~32 tokens:
+// Mixtral at 32 tokens 12.5 us on two of them)
+constexpr int LOGITS_DOT_MAX_T = 32;
 
 int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, int E, int H,
                          bool exact, float *d_out) {
@@ -715,23 +797,24 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
       else go(c, k_logits_dot<8, true>, dim3(grid), dim3(256), 0, d_w, d_x, T, E, H, d_out);
     });
   }
-  if (!exact) {
-    // Fast mode, more than a few tokens: logits = X . W^T is a plain f32
-    // GEMM, which rocBLAS runs on the matrix cores; any summation order is
-    // within fast mode's bound.  Column-major view: out^T (E x T, ld E) =
-    // W' (H x E, ld H) transposed times X' (H x T, ld H).
-    NX_TRY(blas_handle(c));
-    if (rocblas_set_stream(static_cast<rocblas_handle>(c->blas), c->stream) != rocblas_status_success)
-      return fail(NX_ERR_DEVICE, "rocblas_set_stream failed");
-    const float one = 1.0f, zero = 0.0f;
-    rocblas_status st = rocblas_status_success;
-    NX_TRY(launch(c, "router_logits_gemm", [&] {
-      st = rocblas_sgemm(static_cast<rocblas_handle>(c->blas), rocblas_operation_transpose,
-                         rocblas_operation_none, E, T, H, &one, d_w, H, d_x, H, &zero, d_out, E);
-    }));
-    if (st != rocblas_status_success)
-      return fail(NX_ERR_DEVICE, std::string("router logits GEMM: ") + rocblas_status_to_string(st));
-    return NX_OK;
+  if (!exact && (size_t)T * H * 4 < (1u << 31) && (size_t)E * H * 4 < (1u << 31)) {
+    // Fast mode, more than a few tokens: logits = X . W^T on the matrix
+    // cores in f32 (any summation order is within fast mode's bound).  Tiles
+    // of 16 x 16 for up to 16 experts, else of 32 x 32 per wave; the four
+    // waves of a workgroup split K unless the output tiles alone fill two
+    // workgroups per CU.
+    const int nt = E <= 16 ? 1 : 2;
+    const long tiles_n = (E + 16 * nt - 1) / (16 * nt);
+    // tokens per workgroup: 16 (16 x 16 tiles, K split), 128 (four 32 x 32
+    // tiles) or 32 (one 32 x 32 tile, K split)
+    const bool ks1 = nt == 2 && (long)((T + 127) / 128) * tiles_n >= 2L * c->num_cu;
+    const int tm = nt == 1 ? 16 : (ks1 ? 128 : 32);
+    const dim3 grid((unsigned)((T + tm - 1) / tm), (unsigned)tiles_n);
+    return launch(c, "router_logits_mfma", [&] {
+      if (nt == 1) go(c, k_logits_mfma<1, 1, 4>, grid, dim3(256), 0, d_w, d_x, T, E, H, d_out);
+      else if (ks1) go(c, k_logits_mfma<2, 2, 1>, grid, dim3(256), 0, d_w, d_x, T, E, H, d_out);
+      else go(c, k_logits_mfma<2, 2, 4>, grid, dim3(256), 0, d_w, d_x, T, E, H, d_out);
+    });
   }
   // chains per lane: as many as keep at least 1024 waves in the grid
   const int rb = chains >= 1024L * 64 * 16 ? 4 : (chains >= 1024L * 64 * 4 ? 2 : 1);

@@ -111,8 +111,17 @@ def test_exact_special_values(ctx):
     assert got[0, 0] != 0.0 and abs(got[0, 0]) < 1.2e-38  # subnormal kept, not flushed
 
 
+# (T, E, H): the workgroup dot product (up to 32 tokens, partial token blocks;
+# rows not a multiple of 4 floats on the chain kernel), then the f32 MFMA
+# tiles (more tokens): 16 x 16 with K
+# split four ways (up to 16 experts), one 32 x 32 tile per workgroup with K
+# split (fewer than two workgroups per CU of output tiles), four 32 x 32
+# tiles per workgroup; partial token and expert tiles and a partial last
+# 16-column step (H % 16 != 0) on each
 FAST_SHAPES = [(1, 8, 4096), (1, 256, 7168), (3, 128, 2048), (8, 60, 2880), (2, 7, 1001),
-               (64, 256, 512), (2100, 8, 256), (4096, 128, 256)]
+               (64, 256, 512), (2100, 8, 256), (4096, 128, 256), (9, 8, 4096), (50, 5, 100),
+               (1000, 40, 1000), (8200, 250, 72), (1030, 256, 7168), (32, 8, 4096),
+               (27, 128, 2048), (33, 9, 4096)]
 
 
 @pytest.mark.parametrize("T,E,H", FAST_SHAPES)
