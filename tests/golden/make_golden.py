@@ -15,7 +15,8 @@ Fixtures (inputs and expected outputs only):
   fullshape.npz       the parity workloads at full size (Mixtral Q4_K 32
                       tokens, Qwen3 Q4_K 64 and 512 tokens, Mixtral Q8_0 2048
                       tokens with the Zipf(1.2) router, DeepSeek Q4_K 4096
-                      tokens with sigmoid scores and the shared expert): the
+                      tokens with sigmoid scores and the shared expert,
+                      Mixtral-shaped Q4_0 at 1 and 256 tokens): the
                       SHA-256 of the exact router logits and of every token's
                       routed experts, the per-expert pair counts, and the
                       oracle's output rows for a set of tokens that together
@@ -143,25 +144,19 @@ def configs():
 
 
 # Full-size parity workloads: name, seed id, tokens, fmt, E, H, F, k, shared F,
-# score mode, zipf.  Shapes, formats, routing and activations are the model
-# configurations'; the expert weights are drawn uniform on +-0.02*sqrt(3) (the
-# configurations' standard deviation 0.02), which numpy draws 13x faster than
-# normal values: DeepSeek's 771 full-size matrices take seconds.
+# score mode, zipf.  Shapes, formats, routing, activations and the expert
+# weights' distribution (N(0, 0.02), drawn by weight() above, then quantized)
+# are the model configurations'.  The Q4_0 workloads (a format no
+# configuration names) take the Mixtral shape.
 FULLSHAPE = [
     ("mixtral_q4k_t32", 101, 32, Q4_K, 8, 4096, 14336, 2, 0, 0, None),
     ("qwen3_q4k_t64", 102, 64, Q4_K, 128, 2048, 768, 8, 0, 0, None),
     ("qwen3_q4k_t512", 102, 512, Q4_K, 128, 2048, 768, 8, 0, 0, None),
     ("mixtral_q8_0_prefill_t2048", 103, 2048, Q8_0, 8, 4096, 14336, 2, 0, 0, 1.2),
     ("deepseek_q4k_sigmoid_shared_t4096", 104, 4096, Q4_K, 256, 7168, 2048, 8, 2048, 1, None),
+    ("mixtral_q4_0_t1", 105, 1, Q4_0, 8, 4096, 14336, 2, 0, 0, None),
+    ("mixtral_q4_0_t256", 105, 256, Q4_0, 8, 4096, 14336, 2, 0, 0, None),
 ]
-UNIFORM_HALF_WIDTH = np.float32(0.02 * np.sqrt(3.0))
-
-
-def uniform_weight(seed_id, expert, role, rows, cols):
-    """[rows x cols] f32, uniform on [-a, a) with a = 0.02 sqrt(3)."""
-    rng = np.random.default_rng([seed_id, expert, role])
-    u = rng.random((rows, cols), dtype=np.float32)
-    return (u * np.float32(2.0) - np.float32(1.0)) * UNIFORM_HALF_WIDTH
 
 
 def workload_inputs(seed_id, T, H, E):
@@ -220,7 +215,7 @@ def fullshape(only=None):
 
         def quant(job):
             e, r, rows, cols = job
-            return (e, r), oracle.quantize(fmt, uniform_weight(sid, e, r, rows, cols), nthreads=1)
+            return (e, r), oracle.quantize(fmt, weight(sid, e, r, rows, cols), nthreads=1)
 
         jobs = [(e, r, *shp) for e in need for r, shp in enumerate(shapes(H, F))]
         if Fs:

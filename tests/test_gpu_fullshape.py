@@ -3,7 +3,9 @@
 Each workload of tests/golden/make_golden.py's FULLSHAPE list (Mixtral Q4_K at
 32 tokens, Qwen3 Q4_K at 64 and 512 tokens, Mixtral Q8_0 at 2048 tokens with
 the Zipf(1.2) router, DeepSeek Q4_K at 4096 tokens with sigmoid scores and the
-shared expert) is built on the device at its real shape, with every expert of
+shared expert, Q4_0 at the Mixtral shape at 1 and 256 tokens), its expert
+weights drawn from N(0, 0.02) as the configurations name them, is built on
+the device at its real shape, with every expert of
 the configuration resident, and run at its full token count on the path the
 dispatcher picks (NX_PATH_AUTO) and on each explicit path.  Against the
 oracle's fixtures (tests/golden/fullshape.npz):
@@ -29,8 +31,7 @@ import numpy as np
 import pytest
 
 import nexus_amd as nx
-from golden.make_golden import (FULLSHAPE, SHARED, sha, shapes, uniform_weight, workload_inputs,
-                                zipf_bias)
+from golden.make_golden import FULLSHAPE, SHARED, sha, shapes, weight, workload_inputs, zipf_bias
 from moe_cases import DeviceArray, rel_l2
 
 pytestmark = [pytest.mark.gpu, pytest.mark.slow]
@@ -47,6 +48,8 @@ PATHS = {
     "mixtral_q8_0_prefill_t2048": [nx.PATH_GEMV, nx.PATH_MFMA_F16, nx.PATH_MFMA_BF16],
     "deepseek_q4k_sigmoid_shared_t4096": [nx.PATH_GEMV, nx.PATH_MFMA_SPLIT, nx.PATH_MFMA_F16,
                                           nx.PATH_MFMA_BF16],
+    "mixtral_q4_0_t1": [nx.PATH_GEMV],
+    "mixtral_q4_0_t256": [nx.PATH_MFMA_BF16],
 }
 
 
@@ -85,7 +88,7 @@ def build_experts(ctx, sid, fmt, E, H, F, Fs):
                 j = next(it, None)
                 if j is None:
                     return
-                window.append((j, pool.submit(uniform_weight, sid, j[1], j[2], *j[3])))
+                window.append((j, pool.submit(weight, sid, j[1], j[2], *j[3])))
 
         refill()
         while window:
