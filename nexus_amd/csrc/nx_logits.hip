@@ -38,6 +38,7 @@
 //   k_logits_mfma    fast, more tokens: f32 MFMA tiles of tokens x experts.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
+#include "nx_rows.hpp"
 
 namespace nx {
 
@@ -338,6 +339,7 @@ struct PrologueShape {
   static_assert(LPC * RUN4 % 256 == 0, "whole float4 of the row per thread");
 };
 constexpr int BP_MAXH = PrologueShape<64>::MAXH;      // 7168
+static_assert(BP_MAXH == kPrologueMaxH, "the register-run chains' widest row");
 
 template <bool NORM, int LPC>
 __global__ __launch_bounds__(256) void k_block_prologue(const float *__restrict__ x,
@@ -764,10 +766,10 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
   const bool chain8 = !vec || (exact && chains <= LOGITS_CHAIN8_MAX);
   // exact, rows up to 7168, up to one round of workgroups (each holds a CU's
   // LDS): the register-run chains of the block prologue without its RMSNorm
-  // (H > 0: the kernel clamps its load indices to the row's last float4)
+  // (its loads clamp their indices into the row: register_row_fits)
   const bool narrow = H <= PrologueShape<32>::MAXH;
   const int cpg = narrow ? PrologueShape<32>::CPG : PrologueShape<64>::CPG;
-  if (exact && vec && H > 0 && H <= BP_MAXH &&
+  if (exact && vec && register_row_fits(H, kPrologueMaxH) &&
       (long)T * ((E + cpg - 1) / cpg) <= LOGITS_RUNS_MAX_WG) {
     const dim3 grid((unsigned)((E + cpg - 1) / cpg), (unsigned)T);
     return launch(c, "router_logits_runs", [&] {
@@ -846,7 +848,7 @@ int launch_block_prologue(nx_ctx *c, const float *d_x, const float *d_nw, float 
 
 bool block_prologue_fits(int H, const void *x, const void *nw, const void *w, const void *xn) {
   auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
-  return H > 0 && H % 4 == 0 && H <= BP_MAXH && al(x) && al(nw) && al(w) && al(xn);
+  return register_row_fits(H, kPrologueMaxH) && al(x) && al(nw) && al(w) && al(xn);
 }
 
 int launch_sumsq_exact(nx_ctx *c, const float *d_x, int T, int H, float *d_out) {

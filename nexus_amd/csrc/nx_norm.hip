@@ -14,6 +14,7 @@
 // write of the layer's combine.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
+#include "nx_rows.hpp"
 
 namespace nx {
 
@@ -129,6 +130,9 @@ __global__ __launch_bounds__(256) void k_rms_runs(const float *__restrict__ x,
       my[pad(i)] = v[j];
     }
   }
+  // the runs below read other lanes' staged float4s: keep every staging
+  // store of the wave ahead of them (a wave's LDS accesses complete in order)
+  __builtin_amdgcn_wave_barrier();
   float ss = 0.f;
   {
     float4 q[S4];
@@ -166,8 +170,9 @@ __global__ __launch_bounds__(256) void k_rms_runs(const float *__restrict__ x,
 }  // namespace
 
 bool rms_runs_fit(int H, const void *x, const void *w, const void *out) {
+  static_assert(kRmsRunsMaxH == 256 * 28, "k_rms_runs<28>: 64 runs of 28 float4s");
   auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
-  return H > 0 && H % 4 == 0 && H <= 256 * 28 && al(x) && al(w) && al(out);
+  return register_row_fits(H, kRmsRunsMaxH) && al(x) && al(w) && al(out);
 }
 
 int launch_rms_exact_runs(nx_ctx *c, const float *d_x, const float *d_w, float eps, int T, int H,

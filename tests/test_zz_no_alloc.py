@@ -71,6 +71,68 @@ def test_noalloc_matches_forward_dev(ctx, case):
     ex.close()
 
 
+def device_experts(ctx, fmt, E, H, F, seed):
+    """Experts of the given shape built on the device: uniform weights (the
+    distribution does not matter here), quantized by the library."""
+    ex = nx.Experts(ctx, fmt, E, H, F)
+    src = DeviceArray(H * F)
+    q = DeviceArray(nx.quant_bytes(fmt, H * F) // 4 + 1)
+    rng = np.random.default_rng(seed)
+    for e in range(E):
+        for role, (r, c) in ((nx.ROLE_GATE, (F, H)), (nx.ROLE_UP, (F, H)), (nx.ROLE_DOWN, (H, F))):
+            src.upload((rng.random(r * c, dtype=np.float32) - np.float32(0.5)) * np.float32(0.07))
+            nb = nx.quant_bytes(fmt, r * c)
+            ctx.quantize_dev(fmt, src.ptr, r * c, q.ptr, nb)
+            ex.load_dev(e, role, q.ptr, nb)
+            ctx.sync()  # src and q are reused
+    return ex
+
+
+def test_noalloc_allocates_nothing_at_the_mixtral_shape(ctx):
+    """On a fresh context (empty workspace), Mixtral-shaped Q4_K layers at 32
+    and then 8 tokens on the GEMV and the split-activation path (about 48 MB of
+    the 64 MiB array at 32 tokens): free device memory is the same before and
+    after the calls, and the outputs equal nx_moe_forward_dev's, which runs
+    afterwards."""
+    E, H, F, k = 8, 4096, 14336, 2
+    say(f"noalloc Mixtral shape E={E} H={H} F={F} k={k}, free memory")
+    # load the library's kernels on the device first (a process's first
+    # launch loads the code object), on another context
+    warm = Layer(Q4_K, 8, 256, 512, 2, 2, seed=11, experts_needed=[])
+    wex = warm.upload(nx, ctx)
+    run_pair(wex, warm, 2, nx.PATH_GEMV, 0, wex.forward_noalloc)
+    wex.close()
+    fresh = nx.Context(0)
+    try:
+        ex = device_experts(fresh, Q4_K, E, H, F, seed=21)
+        rng = np.random.default_rng(22)
+        T = 32
+        x = DeviceArray(T * H)
+        x.upload(rng.standard_normal((T, H), dtype=np.float32))
+        rw = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+        lg = DeviceArray(T * E)
+        xs = x.download().reshape(T, H)
+        lg.upload((xs.astype(np.float64) @ rw.T.astype(np.float64)).astype(np.float32))
+        cases = [(p, t) for p in (nx.PATH_GEMV, nx.PATH_MFMA_SPLIT) for t in (32, 8)]
+        outs = {c: DeviceArray(T * H, fill=np.nan) for c in cases}
+        fresh.sync()
+        free0 = fresh.mem_info()[0]
+        for (path, t), out in outs.items():
+            ex.forward_noalloc(x.ptr, lg.ptr, t, k, out.ptr, path=path)
+        fresh.sync()
+        free1 = fresh.mem_info()[0]
+        assert free1 == free0, f"free device memory changed by {free0 - free1} bytes"
+        for (path, t), out in outs.items():
+            ref = DeviceArray(T * H, fill=np.nan)
+            ex.forward_dev(x.ptr, lg.ptr, t, k, ref.ptr, path=path)
+            got = out.download().reshape(T, H)[:t]
+            assert np.isfinite(got).all()
+            assert_same_bits(got, ref.download().reshape(T, H)[:t])
+        ex.close()
+    finally:
+        fresh.close()
+
+
 def test_noalloc_rejects_calls_beyond_the_scratch(ctx):
     E, H, F, k, T = 8, 256, 512, 2, 40000
     say(f"noalloc oversize T={T}")
