@@ -579,17 +579,18 @@ def main():
     out = torch.empty((max(T, 32), H), device=dev, dtype=torch.float32)
 
     def decode_case(ntok, pth):
-        counts = active_experts(ctx, logits[:ntok].cpu().numpy(), ntok, E, k)
-        n_act = sum(1 for c in counts if c)
-        gu_bytes = n_act * 2 * F * H * Q4K_BYTES_PER_WEIGHT
-        dn_bytes = n_act * H * F * Q4K_BYTES_PER_WEIGHT
-
         def step(i):
             sets[i % len(sets)].forward_dev(x.data_ptr(), logits.data_ptr(), ntok, k,
                                             out.data_ptr(), path=pth)
 
         ms = time_steps(torch, step, args.steps, args.warmup)
         kern = kernel_means(ctx, torch, step, args.steps)
+        # the bytes of the experts the steps activate (the routes are read back
+        # to the host after the timed steps, so no host round trip precedes them)
+        counts = active_experts(ctx, logits[:ntok].cpu().numpy(), ntok, E, k)
+        n_act = sum(1 for c in counts if c)
+        gu_bytes = n_act * 2 * F * H * Q4K_BYTES_PER_WEIGHT
+        dn_bytes = n_act * H * F * Q4K_BYTES_PER_WEIGHT
         return ms, kern, gu_bytes, dn_bytes, step
 
     print("bench: decode", file=sys.stderr, flush=True)

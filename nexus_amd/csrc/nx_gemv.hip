@@ -35,6 +35,10 @@
 // kernel, which adds them in slice order.  Weight codes are loaded with the
 // non-temporal policy: they are read once, and the activation, scale and
 // route arrays that every workgroup rereads stay in the caches.
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 #include "nx_route_dev.hpp"
@@ -997,6 +1001,29 @@ long fit_one_round(long rows, long rpg, int gpw, long grid_y, long cap) {
   return rpg;
 }
 
+// Resident workgroups per CU of a kernel at a block size.  The occupancy
+// query costs microseconds of host time per call and its answer is fixed per
+// kernel, so it is asked once.
+int wg_per_cu_of(KernelFn fn, int threads) {
+  static std::mutex mu;
+  static std::map<std::pair<const void *, int>, int> cache;
+  const auto key = std::make_pair(reinterpret_cast<const void *>(fn), threads);
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, key.first, threads, 0) != hipSuccess ||
+      n < 1) {
+    (void)hipGetLastError();
+    n = 1;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  cache[key] = n;
+  return n;
+}
+
 // partial sums of the down kernel stay in LDS up to this size per workgroup
 constexpr size_t kDownLdsMax = 64 * 1024;
 
@@ -1100,13 +1127,7 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const int threads = per_slot ? 256 : 256 * DOWN_SG;
   KernelFn probe = pick(ex->fmt, kind, true, nt, sh);
   if (!probe) return fail(NX_ERR_UNSUPPORTED, "no GEMV kernel instance for this shape");
-  int wg_per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wg_per_cu, reinterpret_cast<const void *>(probe),
-                                                   threads, 0) != hipSuccess ||
-      wg_per_cu < 1) {
-    (void)hipGetLastError();
-    wg_per_cu = 1;
-  }
+  const int wg_per_cu = wg_per_cu_of(probe, threads);
   // gate/up spreads slots over grid.y; down runs all slots inside each
   // workgroup.  Size the row runs so the launch is one round of resident
   // workgroups with equal work each.
@@ -1195,13 +1216,7 @@ int run_gemv_matrix(nx_ctx *c, int fmt, const RolePlane &pl, const float *x, int
     return fail(NX_ERR_UNSUPPORTED, "row length too large for the register-resident GEMV");
   KernelFn fn = pick(fmt, KIND_DOWN_ROWS, true, nt, sh);
   if (!fn) return fail(NX_ERR_UNSUPPORTED, "no GEMV kernel instance for this shape");
-  int wg_per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wg_per_cu, reinterpret_cast<const void *>(fn),
-                                                   256, 0) != hipSuccess ||
-      wg_per_cu < 1) {
-    (void)hipGetLastError();
-    wg_per_cu = 1;
-  }
+  const int wg_per_cu = wg_per_cu_of(fn, 256);
   const int groups_per_wg = 256 / (sh.lpr * sh.ksplit);
   const long groups = (long)c->num_cu * wg_per_cu * groups_per_wg;
   long rpg = (pl.rows + groups - 1) / groups;
