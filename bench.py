@@ -199,10 +199,27 @@ def host_info():
     return {"cpu_model": model, "nproc": os.cpu_count(), "compiler": cc, "cflags": cflags}
 
 
-def time_steps(torch, fn, steps, warmup):
+# Secondary cases warm up for at least this long before their timed steps.
+# Right after the host-side set-up between cases the GPU clock is still low,
+# and MFMA/VALU-heavy steps (the split-activation path at 32 tokens) then run
+# ~15% slower for the first few ms; back-to-back windows settle.
+SETTLE_MS = 30.0
+
+
+def time_steps(torch, fn, steps, warmup, settle_ms=0.0):
+    """Mean wall ms per step over `steps` timed steps, after `warmup` untimed
+    steps and, with settle_ms, further untimed steps until that much time has
+    passed since the warm-up began."""
+    t_w = time.perf_counter()
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    i = warmup
+    while (time.perf_counter() - t_w) * 1e3 < settle_ms:
+        for _ in range(4):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         fn(i)
@@ -281,7 +298,7 @@ def prefill(nx, ctx, torch, args):
     def step(i):
         ex.forward_dev(x.data_ptr(), logits.data_ptr(), T, k, out.data_ptr(), path=path)
 
-    ms = time_steps(torch, step, args.prefill_steps, 3)
+    ms = time_steps(torch, step, args.prefill_steps, 3, SETTLE_MS)
     kern = kernel_means(ctx, torch, step, args.prefill_steps)
     gemm_ms = kern.get("gemm_gateup", 0.0) + kern.get("gemm_down", 0.0)
     ex.close()
@@ -348,7 +365,7 @@ def block_case(nx, ctx, torch, sets, x, E, H, k, args):
                                           router.data_ptr(), E * H, 1, k, path=nx.PATH_GEMV,
                                           exact=exact)
 
-        ms = time_steps(torch, step, args.steps, args.warmup)
+        ms = time_steps(torch, step, args.steps, args.warmup, SETTLE_MS)
         kern = kernel_means(ctx, torch, step, args.steps)
         res["exact" if exact else "fast"] = {
             "ms_per_step": ms, "tokens_per_s": 1 / (ms * 1e-3),
@@ -489,7 +506,7 @@ def model_config_cases(nx, ctx, torch, args, only=None):
                                                 path=nx.PATH_AUTO)
 
             steps = args.steps if T <= 64 else max(10, args.prefill_steps)
-            ms = time_steps(torch, step, steps, 3)
+            ms = time_steps(torch, step, steps, 3, SETTLE_MS)
             kern = kernel_means(ctx, torch, step, steps)
             gbps = wbytes / (ms * 1e-3) / 1e9
             tf = flops / (ms * 1e-3) / 1e12
@@ -578,12 +595,12 @@ def main():
     logits = (x @ router.t()).contiguous()
     out = torch.empty((max(T, 32), H), device=dev, dtype=torch.float32)
 
-    def decode_case(ntok, pth):
+    def decode_case(ntok, pth, settle_ms=0.0):
         def step(i):
             sets[i % len(sets)].forward_dev(x.data_ptr(), logits.data_ptr(), ntok, k,
                                             out.data_ptr(), path=pth)
 
-        ms = time_steps(torch, step, args.steps, args.warmup)
+        ms = time_steps(torch, step, args.steps, args.warmup, settle_ms)
         kern = kernel_means(ctx, torch, step, args.steps)
         # the bytes of the experts the steps activate (the routes are read back
         # to the host after the timed steps, so no host round trip precedes them)
@@ -612,9 +629,9 @@ def main():
     extra = {}
     if not args.no_extra and not args.only:
         print("bench: decode, 32 tokens", file=sys.stderr, flush=True)
-        ms32, kern32, gu32, dn32, _ = decode_case(32, nx.PATH_AUTO)
+        ms32, kern32, gu32, dn32, _ = decode_case(32, nx.PATH_AUTO, SETTLE_MS)
         extra["decode_32_tokens"] = {
-            "ms_per_step": ms32, "tokens_per_s": 32 / (ms32 * 1e-3),
+            "ms_per_step": ms32, "settle_ms": SETTLE_MS, "tokens_per_s": 32 / (ms32 * 1e-3),
             "effective_GBps": (gu32 + dn32) / (ms32 * 1e-3) / 1e9, "path": "auto: " + path_of(kern32),
             "kernels_ms": {k_: round(v, 4) for k_, v in kern32.items()}}
     if not args.no_extra and not args.only:
@@ -653,6 +670,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        # the secondary cases also run untimed steps for this long first
+        "secondary_settle_ms": SETTLE_MS,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",

@@ -204,8 +204,9 @@ class Context:
     def __exit__(self, *a):
         self.close()
 
-    def __del__(self):
-        if sys.is_finalizing():  # the process is ending: leave it to the OS
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # bound at definition: module globals may already be None at exit
+        if _finalizing():  # the process is ending: leave it to the OS
             return
         try:
             self.close()
@@ -381,8 +382,9 @@ class Experts:
             lib().nx_experts_destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        if sys.is_finalizing():  # the process is ending: leave it to the OS
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # bound at definition: module globals may already be None at exit
+        if _finalizing():  # the process is ending: leave it to the OS
             return
         try:
             self.close()
@@ -479,8 +481,9 @@ class Matrix:
             lib().nx_matrix_destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        if sys.is_finalizing():  # the process is ending: leave it to the OS
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # bound at definition: module globals may already be None at exit
+        if _finalizing():  # the process is ending: leave it to the OS
             return
         try:
             self.close()
@@ -507,8 +510,9 @@ class Gguf:
     def __exit__(self, *a):
         self.close()
 
-    def __del__(self):
-        if sys.is_finalizing():  # the process is ending: leave it to the OS
+    def __del__(self, _finalizing=sys.is_finalizing):
+        # bound at definition: module globals may already be None at exit
+        if _finalizing():  # the process is ending: leave it to the OS
             return
         try:
             self.close()

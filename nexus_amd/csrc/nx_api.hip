@@ -1080,14 +1080,25 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   const int ksplit =
       gemm_down_ksplit(ex->fmt, std::max(ex->F, ex->Fs), H, max_tiles_down,
                        gemm_wg_per_cu(ex->fmt, tm_down) * c->num_cu);
-  NX_TRY(ws(c, WS_YPAIR, (size_t)ksplit * pairs_total * H, &d_ypair));
+  // the bf16 path keeps its per-pair partial sums in bf16 too (half the
+  // bytes the down pass writes and the combine reads; two columns per store,
+  // so rows of even length)
+  const bool ybf = bf16 && H % 2 == 0;
+  const size_t y_elems = (size_t)ksplit * pairs_total * H;
+  NX_TRY(ws(c, WS_YPAIR, ybf ? (y_elems + 1) / 2 : y_elems, &d_ypair));
   GemmPlan mp{ex,        T,       k,         bf16, d_x,          d_pt,           d_off,
               d_act,     d_tiles, max_tiles, tm,   d_tiles_down, max_tiles_down, tm_down,
-              d_acth,    act_stride, d_ypair, d_xh, x_stride,    pairs_total,    ksplit};
+              d_acth,    act_stride, d_ypair, ybf, d_xh,         x_stride,       pairs_total,
+              ksplit};
   NX_TRY(launch_gemm_gateup(c, mp));
   NX_TRY(launch_gemm_down(c, mp));
-  NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out, ksplit,
-                        pairs_total * (size_t)H, d_residual));
+  if (ybf)
+    NX_TRY(launch_combine_bf16(c, reinterpret_cast<const uint16_t *>(d_ypair), d_w, d_cnt, d_inv,
+                               T, k, H, shared, d_out, ksplit, pairs_total * (size_t)H,
+                               d_residual));
+  else
+    NX_TRY(launch_combine(c, d_ypair, d_w, d_cnt, d_inv, T, k, H, shared, d_out, ksplit,
+                          pairs_total * (size_t)H, d_residual));
   return remember_routes();
 }
 

@@ -182,8 +182,9 @@ struct GemmArgs {
   uint16_t *act;  // gate/up: [pairs][act_stride] operand type, operand order
   int act_stride;
   float *y;       // down: [ksplit][pairs][H], one partial sum per K split
+  uint16_t *yb;   // down, bf16 kernels, when set instead of y: the partial sums as bf16
   int y_stride;
-  size_t y_split;  // floats between the K splits' partial sums
+  size_t y_split;  // elements between the K splits' partial sums
   // grid decomposition (see k_gemm): N-tiles, the tile order, and (down)
   // the K splits, each over wg_per_split workgroups
   int n_tiles, xcd_split, ksplit, wg_per_split;
@@ -895,6 +896,36 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
 
   // ---- epilogue.  16x16 accumulator layout: lane holds column (lane % 16),
   // register j holds row 4 * (lane / 16) + j.
+  if constexpr (!GATEUP && BF16) {
+    if (g.yb) {
+      // bf16 partial sums, two columns per 32-bit store: lanes 2c and 2c+1
+      // swap one value of each register pair (j, j+1), so the even lane
+      // holds columns (2c, 2c+1) of row j and the odd lane those of row j+1.
+      // Rows are even (H % 2 == 0, checked by the host), so a lane pair is
+      // in or out of range together.
+      const bool odd = l16 & 1;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const int col = n0 + 16 * NT * wave + 16 * n + (l16 & ~1);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; j += 2) {
+            const float a0 = acc[0][n][i][j], a1 = acc[0][n][i][j + 1];
+            const float other = __int_as_float(
+                __builtin_amdgcn_mov_dpp(__float_as_int(odd ? a0 : a1), 0xB1, 0xF, 0xF, false));
+            const float lo = odd ? other : a0, hi = odd ? a1 : other;
+            const int row = 16 * i + 4 * q + j + (odd ? 1 : 0);
+            if (col < rows && row < mrows) {
+              const size_t p = (size_t)(pair0 + m0 + row);
+              *reinterpret_cast<uint32_t *>(g.yb + split * g.y_split + p * g.y_stride + col) =
+                  (uint32_t)OpT<true>::bits(lo) | ((uint32_t)OpT<true>::bits(hi) << 16);
+            }
+          }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int col = n0 + 16 * NT * wave + 16 * n + l16;
@@ -1062,7 +1093,10 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
     a.a_stride = p.act_stride;
     a.a_bytes = (uint32_t)(p.pairs_total * p.act_stride * 2);
     a.perm_token = nullptr;
-    a.y = p.ypair;
+    if (p.ypair_bf16 && p.bf16)
+      a.yb = reinterpret_cast<uint16_t *>(p.ypair);
+    else
+      a.y = p.ypair;
     a.y_stride = ex->H;
     a.y_split = p.pairs_total * (size_t)ex->H;
   }

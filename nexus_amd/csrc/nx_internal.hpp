@@ -252,6 +252,11 @@ int launch_rms_fast(nx_ctx *c, const float *d_x, const float *d_w, float eps, in
 int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
                    const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out,
                    int nsplit = 1, size_t split_stride = 0, const float *d_residual = nullptr);
+// the same, over bf16 per-pair rows (the bf16 grouped GEMM's down pass)
+int launch_combine_bf16(nx_ctx *c, const uint16_t *d_ypair, const float *d_weight,
+                        const int32_t *d_count, const int32_t *d_inv, int T, int k, int H,
+                        bool shared, float *d_out, int nsplit, size_t split_stride,
+                        const float *d_residual);
 
 struct GemvPlan {
   const nx_experts *ex;
@@ -312,6 +317,7 @@ struct GemmPlan {
   void *act;             // [pairs_total][act_stride] half precision
   int act_stride;
   float *ypair;
+  bool ypair_bf16;       // ypair holds bf16 partial sums (uint16_t elements)
   void *xh;              // [T][x_stride] half precision copy of x, operand order
   int x_stride;
   size_t pairs_total;    // rows of act / ypair

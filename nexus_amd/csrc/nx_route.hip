@@ -529,20 +529,34 @@ __global__ __launch_bounds__(RP_THREADS) void k_route_permute(
   }
 }
 
+// per-pair row elements: f32, or bf16 (the upper half of an f32, exact)
+__device__ __forceinline__ float yval(const float *__restrict__ y, size_t o) { return y[o]; }
+__device__ __forceinline__ float yval(const uint16_t *__restrict__ y, size_t o) {
+  return __uint_as_float((uint32_t)y[o] << 16);
+}
+__device__ __forceinline__ float4 yval4(const float *__restrict__ y, size_t o) {
+  return *reinterpret_cast<const float4 *>(y + o);
+}
+__device__ __forceinline__ float4 yval4(const uint16_t *__restrict__ y, size_t o) {
+  const uint2 u = *reinterpret_cast<const uint2 *>(y + o);
+  return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                     __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+}
+
 // y value at offset o: the sum of the ns partial buffers (K splits) in
 // split order.  NS == 1: one buffer.  Otherwise the buffers are read 8 at a
 // time (indices past the last clamped to it), so a run of loads is in flight
 // together instead of one dependent load per buffer.
-template <int NS>
-__device__ __forceinline__ float y_at(const float *__restrict__ y, size_t stride, int ns, size_t o) {
+template <int NS, typename YT>
+__device__ __forceinline__ float y_at(const YT *__restrict__ y, size_t stride, int ns, size_t o) {
   if constexpr (NS == 1) {
-    return y[o];
+    return yval(y, o);
   } else {
     float v = 0.f;
     for (int s0 = 0; s0 < ns; s0 += 8) {
       float u[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) u[j] = y[(size_t)min(s0 + j, ns - 1) * stride + o];
+      for (int j = 0; j < 8; ++j) u[j] = yval(y, (size_t)min(s0 + j, ns - 1) * stride + o);
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (s0 + j < ns) v = s0 + j == 0 ? u[j] : v + u[j];
@@ -559,8 +573,8 @@ __device__ __forceinline__ float y_at(const float *__restrict__ y, size_t stride
 // stored in route order (route r of token t at row t * k + r, as the
 // one-token decode GEMV writes them), so every load of the token is issued
 // at once and the rows of absent routes are read but not used.
-template <int NS, int RB>
-__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair,
+template <int NS, int RB, typename YT>
+__global__ __launch_bounds__(256) void k_combine(const YT *__restrict__ ypair,
                                                  const float *__restrict__ rw,
                                                  const int32_t *__restrict__ rcnt,
                                                  const int32_t *__restrict__ inv, int T, int k,
@@ -596,18 +610,18 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ ypair
 }
 
 // float4 form of y_at: four consecutive columns, the same sums
-template <int NS>
-__device__ __forceinline__ float4 y4_at(const float *__restrict__ y, size_t stride, int ns,
+template <int NS, typename YT>
+__device__ __forceinline__ float4 y4_at(const YT *__restrict__ y, size_t stride, int ns,
                                         size_t o) {
   if constexpr (NS == 1) {
-    return *reinterpret_cast<const float4 *>(y + o);
+    return yval4(y, o);
   } else {
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s0 = 0; s0 < ns; s0 += 8) {
       float4 u[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        u[j] = *reinterpret_cast<const float4 *>(y + (size_t)min(s0 + j, ns - 1) * stride + o);
+        u[j] = yval4(y, (size_t)min(s0 + j, ns - 1) * stride + o);
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (s0 + j < ns) {
@@ -626,13 +640,16 @@ __device__ __forceinline__ float4 y4_at(const float *__restrict__ y, size_t stri
 }
 
 // k_combine with the token's routes read once per workgroup: workgroup
-// blockIdx.x covers 1024 columns (four per thread, float4 loads and stores)
-// of token blockIdx.x / nchunk, so the token's count, pair indices and
-// weights are workgroup-uniform loads and no thread divides its index by H.
-// Per element the same operations in the same order as k_combine.
-// Requires H % 4 == 0 and 16-byte aligned ypair, out and residual.
-template <int NS, int RB>
-__global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ ypair,
+// blockIdx.x covers 1024 columns (four per thread, float4 stores) of token
+// blockIdx.x / nchunk, so the token's count, pair indices and weights are
+// workgroup-uniform loads and no thread divides its index by H.  (Whole rows
+// per workgroup, with the route loads paid once per token, measured slower
+// at 2048-4096 tokens: the chunks' parallelism matters more.)  Per element
+// the same operations in the same order as k_combine.  Requires H % 4 == 0,
+// 16-byte aligned out and residual, and ypair aligned to four of its
+// elements.
+template <int NS, int RB, typename YT>
+__global__ __launch_bounds__(256) void k_combine4(const YT *__restrict__ ypair,
                                                   const float *__restrict__ rw,
                                                   const int32_t *__restrict__ rcnt,
                                                   const int32_t *__restrict__ inv, int T, int k,
@@ -786,16 +803,19 @@ int launch_route_permute(nx_ctx *c, const float *d_logits, int T, int E, int k, 
 #undef NX_RP
 }
 
-int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
-                   const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out,
-                   int nsplit, size_t split_stride, const float *d_residual) {
+namespace {
+template <typename YT>
+int combine_rows(nx_ctx *c, const YT *d_ypair, const float *d_weight, const int32_t *d_count,
+                 const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out, int nsplit,
+                 size_t split_stride, const float *d_residual) {
   const size_t total = (size_t)T * H;
   if (total == 0) return NX_OK;
   const int ns = nsplit > 1 ? nsplit : 1;
   const int sh = shared ? 1 : 0;
   auto al16 = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
+  const bool y_al = ((uintptr_t)d_ypair & (4 * sizeof(YT) - 1)) == 0;
   const int nchunk = (H / 4 + 255) / 256;
-  if (H % 4 == 0 && al16(d_ypair) && al16(d_out) && al16(d_residual) &&
+  if (H % 4 == 0 && y_al && al16(d_out) && al16(d_residual) &&
       (size_t)T * nchunk < (1u << 31)) {
     auto run4 = [&](auto kern) {
       return launch(c, "combine", [&] {
@@ -805,13 +825,13 @@ int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const
       });
     };
     if (ns == 1) {
-      if (k <= 2) return run4(k_combine4<1, 2>);
-      if (k <= 4) return run4(k_combine4<1, 4>);
-      return run4(k_combine4<1, 8>);
+      if (k <= 2) return run4(k_combine4<1, 2, YT>);
+      if (k <= 4) return run4(k_combine4<1, 4, YT>);
+      return run4(k_combine4<1, 8, YT>);
     }
-    if (k <= 2) return run4(k_combine4<0, 2>);
-    if (k <= 4) return run4(k_combine4<0, 4>);
-    return run4(k_combine4<0, 8>);
+    if (k <= 2) return run4(k_combine4<0, 2, YT>);
+    if (k <= 4) return run4(k_combine4<0, 4, YT>);
+    return run4(k_combine4<0, 8, YT>);
   }
   size_t g = (total + 255) / 256;
   if (g > 65536) g = 65536;
@@ -823,13 +843,30 @@ int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const
   };
   // routes read together: top-k up to 2, 4, else 8 at a time
   if (ns == 1) {
-    if (k <= 2) return run1(k_combine<1, 2>);
-    if (k <= 4) return run1(k_combine<1, 4>);
-    return run1(k_combine<1, 8>);
+    if (k <= 2) return run1(k_combine<1, 2, YT>);
+    if (k <= 4) return run1(k_combine<1, 4, YT>);
+    return run1(k_combine<1, 8, YT>);
   }
-  if (k <= 2) return run1(k_combine<0, 2>);
-  if (k <= 4) return run1(k_combine<0, 4>);
-  return run1(k_combine<0, 8>);
+  if (k <= 2) return run1(k_combine<0, 2, YT>);
+  if (k <= 4) return run1(k_combine<0, 4, YT>);
+  return run1(k_combine<0, 8, YT>);
+}
+
+}  // namespace
+
+int launch_combine(nx_ctx *c, const float *d_ypair, const float *d_weight, const int32_t *d_count,
+                   const int32_t *d_inv, int T, int k, int H, bool shared, float *d_out,
+                   int nsplit, size_t split_stride, const float *d_residual) {
+  return combine_rows(c, d_ypair, d_weight, d_count, d_inv, T, k, H, shared, d_out, nsplit,
+                      split_stride, d_residual);
+}
+
+int launch_combine_bf16(nx_ctx *c, const uint16_t *d_ypair, const float *d_weight,
+                        const int32_t *d_count, const int32_t *d_inv, int T, int k, int H,
+                        bool shared, float *d_out, int nsplit, size_t split_stride,
+                        const float *d_residual) {
+  return combine_rows(c, d_ypair, d_weight, d_count, d_inv, T, k, H, shared, d_out, nsplit,
+                      split_stride, d_residual);
 }
 
 }  // namespace nx
