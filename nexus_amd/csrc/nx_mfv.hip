@@ -316,11 +316,14 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
         ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bm[mt][u >> 2], ym[mt], 0, 0, 0);
       }
       // one MFMA step's operands live at a time: make the accumulators
-      // exist here, or the compiler gathers every step's operands first
+      // exist here, or the compiler gathers every step's operands first.
+      // Each is pinned as one register tuple (pinning its four elements
+      // separately made the compiler move them between registers: ~64
+      // extra moves per step)
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt) {
-        asm volatile("" : "+v"(y[mt][0]), "+v"(y[mt][1]), "+v"(y[mt][2]), "+v"(y[mt][3]));
-        asm volatile("" : "+v"(ym[mt][0]), "+v"(ym[mt][1]), "+v"(ym[mt][2]), "+v"(ym[mt][3]));
+        asm volatile("" : "+v"(y[mt]));
+        asm volatile("" : "+v"(ym[mt]));
       }
     }
     float sx[4];
