@@ -246,6 +246,10 @@ MFMA_TOL = 1e-2
     (Q8_0, 16, 512, 640, 2, 300, 1.2),
     (Q4_0, 16, 256, 320, 2, 200, 1.1),
     (Q4_K, 16, 512, 768, 4, 150, None),
+    # output rows the bf16 per-pair rows cannot take in pairs (odd H: f32
+    # rows) or in fours (H % 4 == 2: bf16 rows through the scalar combine)
+    (F32, 4, 37, 24, 2, 70, None),
+    (F32, 4, 38, 24, 2, 70, None),
 ])
 def test_layer_mfma_parity(ctx, path, fmt, E, H, F, k, T, zipf):
     L = Layer(fmt, E, H, F, k, T, seed=3 * E + H + F + T, zipf=zipf)
