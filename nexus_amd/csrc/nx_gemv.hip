@@ -469,64 +469,53 @@ struct RowGroup {
   }
 };
 
-// Wave 0 of a gate/up workgroup routes the launch's one token (route_one:
-// top-k with ties to the lower index) and lays out what the permutation
-// kernel would for it: the routed experts sorted by id are the active list,
-// each owning one pair at its rank.  Workgroup (0, 0) writes those arrays to
-// memory for the down pass, with the values k_route_permute gives one token.
-__device__ __forceinline__ void fused_route(const GemvArgs &a, int lane, int32_t *s_active,
-                                            int32_t *s_off, int32_t *s_ptok, int32_t *s_n) {
+// Wave 0 of a gate/up workgroup routes the launch's one token (route_select:
+// top-k with ties to the lower index) from the logits route_load gave, and
+// finds what the permutation kernel would give it: the routed experts sorted
+// by id are the active list, each owning one pair at its rank.  Every
+// workgroup needs only the active list (s_active, s_n in LDS).  Workgroup 0
+// also writes the arrays the later kernels and the route query read, with
+// the values k_route_permute gives one token.
+template <int EPL>
+__device__ __forceinline__ void fused_route(const GemvArgs &a, int lane,
+                                            const float (&lv)[kFusedRouteMaxE / 64],
+                                            int32_t *s_active, int32_t *s_n) {
   // only the workgroup that writes the routes needs their weights
   const bool writer = blockIdx.x == 0;
   int e, n;
   float w;
-  route_one<4>(a.route_logits, a.E, a.k, a.score_mode, lane, &e, &w, &n, writer);
-  // Over the routed experts (n is wave-uniform, so every lane takes part in
-  // each shuffle): this lane's rank among them, and for the ids
-  // x = lane + 64 j <= E the routed experts below x and at x.
-  constexpr int XJ = kFusedRouteMaxE / 64 + 1;
-  int rank = 0, below[XJ], hit[XJ];
-#pragma unroll
-  for (int j = 0; j < XJ; ++j) below[j] = hit[j] = 0;
-  for (int r = 0; r < n; ++r) {
-    const int er = __builtin_amdgcn_readlane(e, r);
-    rank += er < e ? 1 : 0;
-#pragma unroll
-    for (int j = 0; j < XJ; ++j) {
-      below[j] += er < lane + 64 * j ? 1 : 0;
-      hit[j] += er == lane + 64 * j ? 1 : 0;
-    }
-  }
-  if (lane < n) {
-    s_active[rank] = e;
-    s_ptok[rank] = 0;
-    if (writer) {
-      a.r_active[rank] = e;
-      a.r_ptok[rank] = 0;
-      a.r_pslot[rank] = lane;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < XJ; ++j) {
-    const int x = lane + 64 * j;
-    if (x <= a.E) s_off[x] = below[j];
-    if (writer && x < a.E) {
-      a.r_ecount[x] = hit[j];
-      a.r_off[x] = below[j];
-    }
-  }
+  route_select<EPL>(lv, a.E, a.k, a.score_mode, lane, &e, &w, &n, writer);
+  // this route's rank among the routed experts in ascending id order (n is
+  // wave-uniform, so every lane takes part in each read)
+  int rank = 0;
+  for (int r = 0; r < n; ++r) rank += __builtin_amdgcn_readlane(e, r) < e ? 1 : 0;
+  if (lane < n) s_active[rank] = e;
   if (lane == 0) *s_n = n;
-  if (writer) {
-    if (lane < a.k) {
-      a.r_exp[lane] = e;
-      a.r_w[lane] = w;
-      a.r_inv[lane] = lane < n ? rank : -1;
+  if (!writer) return;
+  if (lane < n) {
+    a.r_active[rank] = e;
+    a.r_ptok[rank] = 0;
+    a.r_pslot[rank] = lane;
+  }
+  if (lane < a.k) {
+    a.r_exp[lane] = e;
+    a.r_w[lane] = w;
+    a.r_inv[lane] = lane < n ? rank : -1;
+  }
+  if (lane == 0) {
+    a.r_cnt[0] = n;
+    a.r_active[a.E] = n;
+  }
+  // per expert x <= E: the routed experts below x (its offset) and at x
+  for (int x = lane; x <= a.E; x += 64) {
+    int below = 0, hit = 0;
+    for (int r = 0; r < n; ++r) {
+      const int er = __builtin_amdgcn_readlane(e, r);
+      below += er < x ? 1 : 0;
+      hit += er == x ? 1 : 0;
     }
-    if (lane == 0) {
-      a.r_cnt[0] = n;
-      a.r_off[a.E] = n;
-      a.r_active[a.E] = n;
-    }
+    a.r_off[x] = below;
+    if (x < a.E) a.r_ecount[x] = hit;
   }
 }
 
@@ -583,10 +572,12 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
     // one token routed here: ids of the routed experts in ascending order
     // (the permutation's active list), each with one pair at its rank
     __shared__ int32_t s_active[64];
-    __shared__ int32_t s_off[kFusedRouteMaxE + 1];
-    __shared__ int32_t s_ptok[64];
     __shared__ int32_t s_n;
     if (a.route_logits) {  // kernel-uniform
+      // the logits go out first: loads complete in issue order, so the
+      // routing then waits for them alone, not for the activations too
+      float lv[kFusedRouteMaxE / 64];
+      if (wave == 0) route_load(a.route_logits, a.E, lane, lv);
       if constexpr (COOP) {
         // every slot of the one token reads activation row 0 over rows of
         // a.cols (gate/up and the shared expert alike): load it while the
@@ -598,12 +589,18 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
         g.coop_issue(xq, a.x, a.x_stride, v0, 0, [](int) { return 0; }, tid);
         x_issued = true;
       }
-      if (wave == 0) fused_route(a, lane, s_active, s_off, s_ptok, &s_n);
+      if (wave == 0) {  // as few keys per lane as the experts need
+        if (a.E <= 64)
+          fused_route<1>(a, lane, lv, s_active, &s_n);
+        else if (a.E <= 128)
+          fused_route<2>(a, lane, lv, s_active, &s_n);
+        else
+          fused_route<4>(a, lane, lv, s_active, &s_n);
+      }
       __syncthreads();
-      active = s_active;
-      offsets = s_off;
-      perm_token = s_ptok;
       n_active = s_n;
+      // this slot's expert (one pair, at the slot's rank)
+      if (slot < n_active) e_one = s_active[slot];
     } else {
       if (a.one_token) e_one = a.active[min(slot, a.E)];
       n_active = a.active[a.E];

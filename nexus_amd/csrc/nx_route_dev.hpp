@@ -46,7 +46,19 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return max(max(a, b), max(c, d));
 }
 
-// Routes one token with one wavefront.  On return lane r < *n holds the r-th
+// The logits of one token as held by the router: lane holds expert
+// lane + 64 i in l[i].  The loads are unconditional (indices clamped to the
+// last expert, E >= 1), so they are in flight together and a caller can
+// issue them before other loads it does not want the routing to wait for.
+template <int EPL>
+__device__ __forceinline__ void route_load(const float *__restrict__ row, int E, int lane,
+                                           float (&l)[EPL]) {
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) l[i] = row[min(lane + 64 * i, E - 1)];
+}
+
+// Routes one token with one wavefront from the logits route_load gave (the
+// first EPL of them; 64 EPL >= E).  On return lane r < *n holds the r-th
 // route (expert *e, weight *w); lanes >= *n hold e = -1, w = 0.  With
 // weights false (wave-uniform) only the selection is made and *w is 0.
 //
@@ -55,20 +67,15 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 // selection takes the wave's largest key, then, among the experts holding
 // exactly that key, the lowest index (the first set bit of the lowest
 // non-empty ballot): the stable descending sort of the reference.
-template <int EPL>
-__device__ __forceinline__ void route_one(const float *__restrict__ row, int E, int k,
-                                          int score_mode, int lane, int *e_out, float *w_out,
-                                          int *n_out, bool weights = true) {
+template <int EPL, int LN>
+__device__ __forceinline__ void route_select(const float (&lv)[LN], int E, int k, int score_mode,
+                                             int lane, int *e_out, float *w_out, int *n_out,
+                                             bool weights = true) {
+  static_assert(EPL <= LN, "the logits of every expert are loaded");
   uint32_t key[EPL];
 #pragma unroll
-  for (int i = 0; i < EPL; ++i) {
-    const int e = lane + 64 * i;
-    key[i] = 0;
-    if (e < E) {
-      const float l = row[e];
-      if (isfinite(l)) key[i] = sortable(l);
-    }
-  }
+  for (int i = 0; i < EPL; ++i)
+    key[i] = lane + 64 * i < E && isfinite(lv[i]) ? sortable(lv[i]) : 0u;
   const int kk = k < E ? k : E;
   uint32_t mine = 0;  // lane r keeps the r-th selection: its key and expert
   int mine_e = -1;
@@ -119,6 +126,16 @@ __device__ __forceinline__ void route_one(const float *__restrict__ row, int E, 
   for (int r = 0; r < n; ++r) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), r));
   if (sum > 0.0f && lane < n) w = w / sum;
   *w_out = w;
+}
+
+// route_load + route_select: routes the token whose logits are row[0 .. E)
+template <int EPL>
+__device__ __forceinline__ void route_one(const float *__restrict__ row, int E, int k,
+                                          int score_mode, int lane, int *e_out, float *w_out,
+                                          int *n_out, bool weights = true) {
+  float l[EPL];
+  route_load<EPL>(row, E, lane, l);
+  route_select<EPL>(l, E, k, score_mode, lane, e_out, w_out, n_out, weights);
 }
 
 }  // namespace nx
