@@ -109,7 +109,10 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
   const int tile = blockIdx.y;
   if (tile >= a.tiles[0]) return;  // workgroup-uniform
   // tile t: expert tiles[2 + 2t] (E: the shared expert), first pair
-  // tiles[3 + 2t] within the expert
+  // tiles[3 + 2t] within the expert.  These and the expert's offsets are
+  // scalar loads, which do not queue behind the weight stream's vector loads
+  // (loading every expert's offset with vector loads ahead of the expert id
+  // was slower: Mixtral 32 tokens 266 -> 274 us)
   const int e = __builtin_amdgcn_readfirstlane(a.tiles[2 + 2 * tile]);
   const int m0 = __builtin_amdgcn_readfirstlane(a.tiles[3 + 2 * tile]);
   const bool routed = e < a.E;
@@ -170,39 +173,52 @@ __global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
     }
   };
 
-  // the first steps' codes go out before the staging: the weights do not
-  // depend on the activations, and their latency overlaps the staging's
+  // ---- stage the slice: thread t owns positions 16j .. 16j+15 of every
+  // chunk of pair m = t / 16; chunks past the row read as zeros.  The token
+  // lookup and the activation loads go out before the first weight steps:
+  // vector loads complete in issue order, so activation loads issued after
+  // the weights would wait for them (at 32 tokens the staging then took
+  // ~12 of a ~38 us workgroup), while the weights are needed only after the
+  // staging's barrier anyway.
+  const int sm = tid >> 4, sj = tid & 15;
+  const float *xrow = nullptr;
+  if (sm < cnt) {
+    // gate/up: the pair's token (a shared pair's is its index in the
+    // tile's run); down: the pair's row of act
+    const int r = a.perm_token ? (routed ? a.perm_token[pair0 + sm] : m0 + sm) : pair0 + sm;
+    xrow = a.x + (size_t)r * a.x_stride;
+  }
+  // every lane loads (absent pairs and chunks from row 0 of x, zeroed when
+  // converted), so the loads are not branched around
+  const bool pv = xrow != nullptr;
+  if (!pv) xrow = a.x;
+  float4 xr[MV_KS][4];
+#pragma unroll
+  for (int kc = 0; kc < MV_KS; ++kc) {
+    const bool v = pv && c0 + kc < a.nchunk;
+    const float *src = xrow + (size_t)(v ? c0 + kc : 0) * MV_K + 16 * sj;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xr[kc][q] = *reinterpret_cast<const float4 *>(src + 4 * q);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // the first weight steps, in flight during the staging
   MfvStep<NMAT> ring[MV_D];
 #pragma unroll
   for (int i = 0; i < MV_D - 1; ++i) issue(ring[i], i);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- stage the slice: thread t owns positions 16j .. 16j+15 of every
-  // chunk of pair m = t / 16; chunks past the row read as zeros
   {
-    const int sm = tid >> 4, sj = tid & 15;
-    const float *xrow = nullptr;
-    if (sm < cnt) {
-      // gate/up: the pair's token (a shared pair's is its index in the
-      // tile's run); down: the pair's row of act
-      const int r = a.perm_token ? (routed ? a.perm_token[pair0 + sm] : m0 + sm) : pair0 + sm;
-      xrow = a.x + (size_t)r * a.x_stride;
-    }
-    // every lane loads (absent pairs and chunks from row 0 of x, then
-    // zeroed), so the loads are not branched around
-    const bool pv = xrow != nullptr;
-    if (!pv) xrow = a.x;
     float xv[MV_KS][16];
 #pragma unroll
     for (int kc = 0; kc < MV_KS; ++kc) {
       const bool v = pv && c0 + kc < a.nchunk;
-      const float *src = xrow + (size_t)(v ? c0 + kc : 0) * MV_K + 16 * sj;
 #pragma unroll
-      for (int q = 0; q < 16; q += 4) {
-        const float4 f = *reinterpret_cast<const float4 *>(src + q);
-        xv[kc][q] = v ? f.x : 0.f;
-        xv[kc][q + 1] = v ? f.y : 0.f;
-        xv[kc][q + 2] = v ? f.z : 0.f;
-        xv[kc][q + 3] = v ? f.w : 0.f;
+      for (int q = 0; q < 4; ++q) {
+        xv[kc][4 * q] = v ? xr[kc][q].x : 0.f;
+        xv[kc][4 * q + 1] = v ? xr[kc][q].y : 0.f;
+        xv[kc][4 * q + 2] = v ? xr[kc][q].z : 0.f;
+        xv[kc][4 * q + 3] = v ? xr[kc][q].w : 0.f;
       }
     }
 #pragma unroll
