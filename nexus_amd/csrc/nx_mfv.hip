@@ -28,12 +28,12 @@
 //
 // Work: a workgroup of 4 waves owns one tile of up to 16 pairs of one
 // expert (the permutation's tile list with tile_m = 16), 256 weight rows
-// (of both matrices for gate/up) and one K slice of 4 chunks (a chunk is
-// one Q4_K block, 256 positions); wave w streams 64 of the rows as 4 row
-// tiles of 16.  The slice's activations of the tile's pairs are staged
-// once into LDS in MFMA operand layout, with each pair's unscale factor;
-// the codes and scales of the next 3 (row tile, chunk) steps are in flight
-// while a step is computed.  Slices write partial sums, which the SwiGLU
+// (of both matrices for gate/up) and one K slice of 4 (gate/up) or 3 (down)
+// chunks (a chunk is one Q4_K block, 256 positions); wave w streams 64 of
+// the rows as 4 row tiles of 16.  The slice's activations of the tile's
+// pairs are staged once into LDS in MFMA operand layout, with each pair's
+// unscale factor; the codes and scales of the next 3 (gate/up) or 2 (down)
+// (row tile, chunk) steps are in flight while a step is computed.  Slices write partial sums, which the SwiGLU
 // kernel (gate/up) and the weighted combine (down) add in slice order.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
@@ -89,17 +89,21 @@ struct MfvStep {
 // Workgroup = (row block of 256 rows, tile of <= 16 pairs, K slice of
 // MV_KS chunks).  Prologue: the slice's activations of the tile's pairs are
 // staged once into LDS (one barrier).  Then wave w streams rows
-// 64 w .. 64 w + 63 of the block as 4 row tiles x MV_KS chunks = 16 steps,
+// 64 w .. 64 w + 63 of the block as 4 row tiles x MV_KS chunks (16 or 12 steps),
 // with the codes of the next MV_D steps in flight.  Each workgroup writes
 // its slice's partial sums: gate/up to part[slice][pair][2][F] (gate, then
 // up), down to part[slice][pair][H].
-constexpr int MV_KS = 4;   // chunks per K slice
+// chunks per K slice: four for gate/up; three for down, whose 48 KB stage
+// and 112 VGPRs then fit three workgroups on a CU (Mixtral 32 tokens: down
+// 83 -> 80 us; 64 tokens 116 -> 109 us; two chunks, four workgroups per
+// CU, gained no more and added combine work)
+constexpr int MV_KS_GATEUP = 4, MV_KS_DOWN = 3;
 constexpr int MV_RTW = 4;  // row tiles per wave
-constexpr int MV_D = 4;    // steps in flight
 constexpr int MV_WG_ROWS = 4 * 16 * MV_RTW;
 
-template <bool GATEUP>
-__global__ __launch_bounds__(256, 2) void k_mfv(const MfvArgs a) {
+template <bool GATEUP, int MV_KS>
+__global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a) {
+  constexpr int MV_D = MV_KS;  // steps in flight
   constexpr int NMAT = GATEUP ? 2 : 1;
   constexpr int NSTEP = MV_RTW * MV_KS;
   __shared__ MfvStage stage[MV_KS];
@@ -432,8 +436,8 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
   const int H = ex->H, F = ex->F;
   // routed pairs, then one pair per token for the shared expert
   const size_t pairs = (size_t)p.T * p.k + (shared ? (size_t)p.T : 0);
-  const int nks_g = (H / MV_K + MV_KS - 1) / MV_KS;
-  const int nks_d = (F / MV_K + MV_KS - 1) / MV_KS;
+  const int nks_g = (H / MV_K + MV_KS_GATEUP - 1) / MV_KS_GATEUP;
+  const int nks_d = (F / MV_K + MV_KS_DOWN - 1) / MV_KS_DOWN;
   void *vg, *va, *vy;
   NX_TRY(ws_get(c, WS_MFV_PART, (size_t)nks_g * pairs * 2 * F * sizeof(float), &vg));
   NX_TRY(ws_get(c, WS_ACT, pairs * F * sizeof(float), &va));
@@ -489,7 +493,7 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
                     (unsigned)nks);
     if (gateup) {
       NX_TRY(launch(c, "mfv_gateup",
-                    [&] { go(c, k_mfv<true>, grid, dim3(256), 0, a); }));
+                    [&] { go(c, k_mfv<true, MV_KS_GATEUP>, grid, dim3(256), 0, a); }));
       const size_t n = pairs * F;
       unsigned gs = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
       NX_TRY(launch(c, "mfv_swiglu", [&] {
@@ -498,7 +502,7 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
       }));
     } else {
       NX_TRY(launch(c, "mfv_down",
-                    [&] { go(c, k_mfv<false>, grid, dim3(256), 0, a); }));
+                    [&] { go(c, k_mfv<false, MV_KS_DOWN>, grid, dim3(256), 0, a); }));
     }
   }
   return launch_combine(c, ypart, p.rw, p.rcnt, p.inv, p.T, p.k, H, shared, p.out, nks_d,
