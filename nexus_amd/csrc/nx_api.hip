@@ -973,13 +973,20 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
         use = NX_PATH_MFMA_BF16;
       else
         use = T >= 4 ? NX_PATH_MFMA_SPLIT : NX_PATH_GEMV;
-    } else if (ex->fmt == NX_FMT_Q4_K && !shared) {
+    } else if ((ex->fmt == NX_FMT_Q4_K || (ex->fmt == NX_FMT_Q4_0 && mfv_supports(ex))) &&
+               !shared) {
       // Measured crossovers (Mixtral and Qwen3 shapes): the GEMV re-reads an
       // expert's weights per pair of its tokens and wins below ~2 tokens per
       // expert; the split-activation MFMA path reads them once per 16 tokens
       // and wins up to ~12 (Mixtral: 0.31 against 0.36 ms at 8 tokens per
       // expert, 0.45 against 0.36 at 16; Qwen3: 0.17 / 0.20 at 8, 0.24 /
-      // 0.21 at 16); the grouped GEMM beyond.
+      // 0.21 at 16); the grouped GEMM beyond.  Q4_0 (ms, GEMV / split /
+      // grouped GEMM): Mixtral 2 tokens per expert 0.183 / 0.233 / 0.290,
+      // 4: 0.368 / 0.253 / 0.295, 8: - / 0.272 / 0.297, 16: - / 0.343 /
+      // 0.299; Qwen3 1.2: 0.079 / 0.069 / 0.095, 4: 0.285 / 0.135 / 0.160.
+      // (With a shared expert Q4_0 keeps the rule below: at DeepSeek's
+      // shape the split path and the grouped GEMM are within 4% from 16
+      // tokens.)
       if (tpe >= 12.0)
         use = NX_PATH_MFMA_BF16;
       else if (tpe >= 3.0 || ((long)T * k >= 64 && tpe >= 1.2))
@@ -1029,8 +1036,10 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   }
 
   if (use == NX_PATH_MFMA_SPLIT) {
-    if (ex->fmt != NX_FMT_Q4_K)
-      return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path takes Q4_K experts");
+    if (!mfv_supports(ex))
+      return fail(NX_ERR_UNSUPPORTED,
+                  "the split-activation MFMA path takes Q4_K experts, or Q4_0 experts whose "
+                  "hidden and FFN widths are multiples of 256");
     if (shared && ex->Fs != ex->F)
       return fail(NX_ERR_UNSUPPORTED,
                   "the split-activation MFMA path takes a shared expert as wide as the routed ones");

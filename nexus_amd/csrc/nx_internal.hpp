@@ -345,6 +345,9 @@ struct MfvPlan {
   const float *residual;
 };
 int launch_mfv(nx_ctx *c, const MfvPlan &p);
+// whether the split-activation path takes these experts: Q4_K, or Q4_0
+// with hidden and FFN widths that are multiples of 256
+bool mfv_supports(const nx_experts *ex);
 int mfv_max_tiles(int T, int k, int E, bool shared);
 constexpr int kMfvTileM = 16;
 // grouped-GEMM M-tile height of a pass for a batch

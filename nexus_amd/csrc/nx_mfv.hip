@@ -1,4 +1,4 @@
-// nx_mfv.hip — few-token grouped matvec on MFMA for Q4_K experts: decode
+// nx_mfv.hip — few-token grouped matvec on MFMA for Q4_K and Q4_0 experts: decode
 // batches whose experts see a handful of tokens each (2 to ~128 tokens),
 // with or without a shared expert (as wide as the routed ones) that sees
 // every token.
@@ -35,6 +35,14 @@
 // unscale factor; the codes and scales of the next 3 (gate/up) or 2 (down)
 // (row tile, chunk) steps are in flight while a step is computed.  Slices write partial sums, which the SwiGLU
 // kernel (gate/up) and the weighted combine (down) add in slice order.
+//
+// Q4_0 (w_i = d (q_i - 8) per 32-weight block, src/quant/mod.rs:723-745)
+// runs the same kernel on chunks of 8 blocks: one MFMA pair per block, the
+// codes unsigned (q_i 2^-24) and the 8 taken off through each block's
+// staged activation sum, the f16 block scale d applied to that MFMA's
+// result.  The loads give a lane group two whole blocks; a 4 x 4 dword
+// transpose across the lane groups hands every lane group its 8 weights of
+// each block.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 
@@ -68,11 +76,36 @@ struct MfvArgs {
 };
 
 // LDS area of one chunk: the A operands (hi, lo) of the 8 MFMAs in lane
-// order and the per-pair unscale factors
-struct MfvStage {
+// order and the per-pair unscale factors; Q4_0 also keeps each block's
+// activation sum (times 8) per pair
+struct MfvStageBase {
   uint4 a[8][2][64];  // [MFMA][hi, lo][lane]
   float sx[MV_M];
 };
+template <int FMT>
+struct MfvStage : MfvStageBase {};
+template <>
+struct MfvStage<NX_FMT_Q4_0> : MfvStageBase {
+  float xs[8][MV_M];  // [block][pair]: 8 times the block's sum of the operand values
+};
+
+// 4 x 4 transpose of dwords across the four 16-lane groups: on return
+// c[k] of lane group g holds what c[g] of lane group k held (register
+// swaps between lane halves, then between neighbouring lane groups)
+__device__ __forceinline__ void transpose_groups(uint32_t (&c)[4]) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const auto v = __builtin_amdgcn_permlane32_swap(c[k], c[k + 2], false, false);
+    c[k] = v[0];
+    c[k + 2] = v[1];
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k += 2) {
+    const auto v = __builtin_amdgcn_permlane16_swap(c[k], c[k + 1], false, false);
+    c[k] = v[0];
+    c[k + 1] = v[1];
+  }
+}
 
 // element of sub-block group g held in operand position p: the nibble order
 // of a code dword (positions 2i, 2i+1 = elements i, 4+i)
@@ -101,12 +134,14 @@ constexpr int MV_KS_GATEUP = 4, MV_KS_DOWN = 3;
 constexpr int MV_RTW = 4;  // row tiles per wave
 constexpr int MV_WG_ROWS = 4 * 16 * MV_RTW;
 
-template <bool GATEUP, int MV_KS>
+template <bool GATEUP, int MV_KS, int FMT>
 __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a) {
+  static_assert(FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0, "Q4_K and Q4_0 codes");
+  constexpr bool Q40 = FMT == NX_FMT_Q4_0;
   constexpr int MV_D = MV_KS;  // steps in flight
   constexpr int NMAT = GATEUP ? 2 : 1;
   constexpr int NSTEP = MV_RTW * MV_KS;
-  __shared__ MfvStage stage[MV_KS];
+  __shared__ MfvStage<FMT> stage[MV_KS];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -227,7 +262,7 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
     }
 #pragma unroll
     for (int kc = 0; kc < MV_KS; ++kc) {
-      MfvStage &st = stage[kc];
+      MfvStage<FMT> &st = stage[kc];
       float mx = 0.f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) mx = fmaxf(mx, fabsf(xv[kc][v]));
@@ -249,13 +284,14 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
         hv[v] = (_Float16)sv;
         lv[v] = (_Float16)(sv - (float)hv[v]);
       }
-      // Operands: MFMA u (0..7), lane group g takes elements
+      // Operands, Q4_K: MFMA u (0..7), lane group g takes elements
       // 32 g + 8 u (u < 4) or 128 + 32 g + 8 (u - 4) (u >= 4), position p
       // holding element + opos_elem(p).  This thread's 16 positions
       // 16 sj .. 16 sj + 15 are those of group g = (sj % 8) / 2, MFMAs
-      // u0, u0 + 1 with u0 = 4 (sj / 8) + 2 (sj % 2).
-      const int gq = (sj & 7) >> 1;
-      const int u0 = 4 * (sj >> 3) + 2 * (sj & 1);
+      // u0, u0 + 1 with u0 = 4 (sj / 8) + 2 (sj % 2).  Q4_0: MFMA b is
+      // block b (elements 32 b ..), lane group g taking its elements
+      // 32 b + 8 g + opos_elem(p); this thread's positions are block sj / 2,
+      // groups 2 (sj % 2) and 2 (sj % 2) + 1.
 #pragma unroll
       for (int uu = 0; uu < 2; ++uu) {
         _Float16 ho[8], lo[8];
@@ -264,9 +300,20 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
           ho[p] = hv[8 * uu + opos_elem(p)];
           lo[p] = lv[8 * uu + opos_elem(p)];
         }
+        const int gq = Q40 ? 2 * (sj & 1) + uu : (sj & 7) >> 1;
+        const int u = Q40 ? sj >> 1 : 4 * (sj >> 3) + 2 * (sj & 1) + uu;
         const int L = sm + 16 * gq;
-        st.a[u0 + uu][0][L] = __builtin_bit_cast(uint4, ho);
-        st.a[u0 + uu][1][L] = __builtin_bit_cast(uint4, lo);
+        st.a[u][0][L] = __builtin_bit_cast(uint4, ho);
+        st.a[u][1][L] = __builtin_bit_cast(uint4, lo);
+      }
+      if constexpr (Q40) {
+        // the block's sum of the values the operands carry (hi + lo, exact
+        // in f32), over this thread's half and its neighbour's
+        float bs = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) bs += (float)hv[v] + (float)lv[v];
+        bs += __shfl_xor(bs, 1, 64);
+        if ((sj & 1) == 0) st.xs[sj >> 1][sm] = 8.0f * bs;
       }
       if (sj == 0) st.sx[sm] = __builtin_amdgcn_ldexpf(1.0f, E - 14);
       __builtin_amdgcn_sched_barrier(0);
@@ -293,7 +340,58 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
   //   sum_i w_i x_i = d sum_s sc_s sum_{i in s} q_i x_i - dmin sum_s m_s X_s
   // with sc_s inside the operands, so the 8 MFMAs of the block accumulate
   // together and d, dmin apply once per block
-  auto compute = [&](const MfvStep<NMAT> &w, const MfvStage &st, f32x4 (&accr)[NMAT]) {
+  auto compute = [&](const MfvStep<NMAT> &w, const MfvStage<FMT> &st, f32x4 (&accr)[NMAT]) {
+    if constexpr (Q40) {
+      // Q4_0 (src/quant/mod.rs:723-745: w = d (q - 8) per 32-weight block).
+      // One MFMA per block: lane group g holds dword g of the block (its
+      // elements 8 g ..), so the block scale d applies to the MFMA's
+      // result; the codes go in unsigned (q as an fp16 subnormal, q 2^-24)
+      // and the staged block sums X take off the 8:
+      //   sum_i w_i x_i = d (2^24 sum_i (q_i 2^-24) x_i - 8 X).
+      // The loads give lane group g the 16 bytes of blocks 2 g and 2 g + 1
+      // (halves 0 and 1 of segment g); transposed across the lane groups,
+      // dword s of half h is then dword g of block 2 s + h.
+      uint32_t cq[NMAT][2][4];
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          cq[mt][h][0] = w.q[mt][h].x;
+          cq[mt][h][1] = w.q[mt][h].y;
+          cq[mt][h][2] = w.q[mt][h].z;
+          cq[mt][h][3] = w.q[mt][h].w;
+          transpose_groups(cq[mt][h]);
+        }
+      float sx[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sx[k] = st.sx[4 * g + k];
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const f16x8 ahi = __builtin_bit_cast(f16x8, st.a[b][0][lane]);
+        const f16x8 alo = __builtin_bit_cast(f16x8, st.a[b][1][lane]);
+        const float4 xs = *reinterpret_cast<const float4 *>(&st.xs[b][4 * g]);
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt) {
+          const f16x8 bq = operand(cq[mt][b & 1][b >> 1], 0x00010001u);
+          f32x4 y = f32x4{0.f, 0.f, 0.f, 0.f};
+          y = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, y, 0, 0, 0);
+          y = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, y, 0, 0, 0);
+          asm volatile("" : "+v"(y));
+          // block b's scale: the f16 at half (b % 2) of scale dword b / 2
+          const uint32_t dw = (&w.m[mt].x)[b >> 1];
+          const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 1 ? dw >> 16 : dw & 0xFFFFu));
+          accr[mt][0] = fmaf(sx[0] * d, fmaf(16777216.0f, y[0], -xs.x), accr[mt][0]);
+          accr[mt][1] = fmaf(sx[1] * d, fmaf(16777216.0f, y[1], -xs.y), accr[mt][1]);
+          accr[mt][2] = fmaf(sx[2] * d, fmaf(16777216.0f, y[2], -xs.z), accr[mt][2]);
+          accr[mt][3] = fmaf(sx[3] * d, fmaf(16777216.0f, y[3], -xs.w), accr[mt][3]);
+          // the block's scaling happens here: left free, the compiler sinks
+          // every block's scaling to the step's end and holds all 8 blocks'
+          // results meanwhile (1480 bytes of spills per lane)
+          asm volatile("" : "+v"(accr[mt]));
+        }
+      }
+      return;
+    }
     // this lane's sub-blocks g and g + 4 (get_scale_min_k4,
     // src/quant/mod.rs:1163-1170, on scales12): the scales go into the code
     // operands, the mins into operands of their own (m as fp16, all 8
@@ -422,10 +520,19 @@ int mfv_max_tiles(int T, int k, int E, bool shared) {
                (shared ? (T + MV_M - 1) / MV_M : 0));
 }
 
+bool mfv_supports(const nx_experts *ex) {
+  // whole 256-weight chunks in both products: Q4_K always, Q4_0 when H and
+  // F are multiples of 256
+  if (ex->fmt == NX_FMT_Q4_K) return true;
+  return ex->fmt == NX_FMT_Q4_0 && ex->H % MV_K == 0 && ex->F % MV_K == 0;
+}
+
 int launch_mfv(nx_ctx *c, const MfvPlan &p) {
   const nx_experts *ex = p.ex;
-  if (ex->fmt != NX_FMT_Q4_K)
-    return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path takes Q4_K experts");
+  if (!mfv_supports(ex))
+    return fail(NX_ERR_UNSUPPORTED,
+                "the split-activation MFMA path takes Q4_K experts, or Q4_0 experts whose "
+                "hidden and FFN widths are multiples of 256");
   // activation rows are read as float4 runs of whole chunks
   if (reinterpret_cast<uintptr_t>(p.x) & 15)
     return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path needs 16-byte aligned inputs");
@@ -493,7 +600,12 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
                     (unsigned)nks);
     if (gateup) {
       NX_TRY(launch(c, "mfv_gateup",
-                    [&] { go(c, k_mfv<true, MV_KS_GATEUP>, grid, dim3(256), 0, a); }));
+                    [&] {
+                      if (ex->fmt == NX_FMT_Q4_0)
+                        go(c, k_mfv<true, MV_KS_GATEUP, NX_FMT_Q4_0>, grid, dim3(256), 0, a);
+                      else
+                        go(c, k_mfv<true, MV_KS_GATEUP, NX_FMT_Q4_K>, grid, dim3(256), 0, a);
+                    }));
       const size_t n = pairs * F;
       unsigned gs = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
       NX_TRY(launch(c, "mfv_swiglu", [&] {
@@ -502,7 +614,12 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
       }));
     } else {
       NX_TRY(launch(c, "mfv_down",
-                    [&] { go(c, k_mfv<false, MV_KS_DOWN>, grid, dim3(256), 0, a); }));
+                    [&] {
+                      if (ex->fmt == NX_FMT_Q4_0)
+                        go(c, k_mfv<false, MV_KS_DOWN, NX_FMT_Q4_0>, grid, dim3(256), 0, a);
+                      else
+                        go(c, k_mfv<false, MV_KS_DOWN, NX_FMT_Q4_K>, grid, dim3(256), 0, a);
+                    }));
     }
   }
   return launch_combine(c, ypart, p.rw, p.rcnt, p.inv, p.T, p.k, H, shared, p.out, nks_d,

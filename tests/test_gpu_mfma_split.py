@@ -8,8 +8,10 @@ against the oracle's dispatch (src/engine/mod.rs:969-1024) over the same
 payloads: 1 to 64 tokens, experts with more than 16 tokens (several tiles),
 top-8 routing, the sigmoid score mode, token rows of very different
 magnitudes and zero rows, Mixtral's full shape, and a shared expert as wide
-as the routed ones (one pair per token, several tiles of 16); other formats
-and shared experts of another width are rejected with NX_ERR_UNSUPPORTED.
+as the routed ones (one pair per token, several tiles of 16); Q4_0 experts
+whose widths are whole 256-weight chunks on the same kinds of case; other
+formats, other Q4_0 widths and shared experts of another width are rejected
+with NX_ERR_UNSUPPORTED.
 """
 import numpy as np
 import pytest
@@ -97,6 +99,44 @@ def test_split_mixtral_shape(ctx):
     assert rel_l2(got, L.oracle_out()) <= TOL
 
 
+@pytest.mark.parametrize("E,H,F,k,T,Fs,score", [
+    (8, 512, 1024, 2, 1, 0, 0), (8, 256, 768, 2, 33, 0, 0), (32, 512, 256, 8, 24, 0, 1),
+    (16, 1024, 512, 4, 64, 0, 0), (16, 512, 512, 4, 8, 512, 1), (8, 256, 768, 2, 40, 768, 0)])
+def test_split_parity_q4_0(ctx, E, H, F, k, T, Fs, score):
+    """Q4_0 experts (w = d (q - 8) per 32-weight block, src/quant/mod.rs:
+    723-745) on the split path: one MFMA per block with the unsigned codes,
+    the block sums of the staged activations taking off the 8."""
+    print(f"mfma split q4_0 E={E} H={H} F={F} k={k} T={T} Fs={Fs} score={score}", flush=True)
+    L = Layer(Q4_0, E, H, F, k, T, seed=E * 3 + H + F + T, shared_F=Fs, score_mode=score)
+    ex = L.upload(nx, ctx)
+    got = ex.forward(L.x, L.logits, k, score, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    assert rel_l2(got, L.oracle_out()) <= TOL
+
+
+def test_split_q4_0_magnitudes_and_mixtral_shape(ctx):
+    L = Layer(Q4_0, 8, 512, 512, 2, 12, seed=43)
+    scale = np.array([1e-30, 1e-6, 1.0, 3e3, 1e6, 0.0, 1.0, 1e-3, 7.0, 0.0, 1e4, 1e-2],
+                     np.float32)[:, None]
+    L.x = (L.x * scale).astype(np.float32)
+    L.x[2, 256:] = 0.0  # one zero chunk inside a live row
+    ex = L.upload(nx, ctx)
+    got = ex.forward(L.x, L.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    ref = L.oracle_out()
+    for t in range(L.T):
+        den = np.linalg.norm(ref[t])
+        if den == 0:
+            assert np.all(got[t] == 0)
+        else:
+            assert rel_l2(got[t], ref[t]) <= TOL, t
+    M = Layer(Q4_0, 8, 4096, 14336, 2, 8, seed=10)
+    ex = M.upload(nx, ctx)
+    got = ex.forward(M.x, M.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    assert rel_l2(got, M.oracle_out()) <= TOL
+
+
 def test_split_rejects(ctx):
     L = Layer(Q8_0, 4, 256, 256, 2, 4, seed=3)
     ex = L.upload(nx, ctx)
@@ -104,6 +144,13 @@ def test_split_rejects(ctx):
         ex.forward(L.x, L.logits, 2, 0, nx.PATH_MFMA_SPLIT)
     assert ei.value.code == nx.NX_ERR_UNSUPPORTED
     ex.close()
+    for H, F in ((288, 256), (256, 224)):  # Q4_0 widths that are not whole 256-weight chunks
+        Q = Layer(Q4_0, 4, H, F, 2, 4, seed=5)
+        ex = Q.upload(nx, ctx)
+        with pytest.raises(nx.NexusError) as ei:
+            ex.forward(Q.x, Q.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+        assert ei.value.code == nx.NX_ERR_UNSUPPORTED
+        ex.close()
     S = Layer(Q4_K, 4, 256, 256, 2, 4, seed=4, shared_F=512)  # a wider shared expert
     ex = S.upload(nx, ctx)
     with pytest.raises(nx.NexusError) as ei:
@@ -131,7 +178,11 @@ def test_auto_path_choice(ctx, E, H, F, k, T, want):
 @pytest.mark.parametrize("fmt,E,H,F,k,T,shared,want", [
     (Q8_0, 8, 512, 1024, 2, 8, 0, nx.PATH_GEMV),        # 2 tokens per expert
     (Q8_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_BF16),  # 4
-    (Q4_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_BF16),
+    (Q4_0, 8, 512, 1024, 2, 4, 0, nx.PATH_GEMV),         # 1 token per expert
+    (Q4_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_SPLIT),  # 4
+    (Q4_0, 8, 512, 1024, 2, 64, 0, nx.PATH_MFMA_BF16),   # 16
+    (Q4_0, 8, 512, 992, 2, 16, 0, nx.PATH_MFMA_BF16),    # F not whole 256-weight chunks
+    (Q4_0, 16, 512, 512, 4, 8, 512, nx.PATH_MFMA_BF16),  # a shared expert, 8 tokens
     (Q4_K, 16, 512, 512, 4, 2, 512, nx.PATH_GEMV),        # a shared expert, 2 tokens
     (Q4_K, 16, 512, 512, 4, 4, 512, nx.PATH_MFMA_SPLIT),  # ... 4 tokens
     (Q4_K, 16, 512, 512, 4, 8, 512, nx.PATH_MFMA_SPLIT),  # ... 8 tokens
@@ -142,9 +193,11 @@ def test_auto_path_choice(ctx, E, H, F, k, T, want):
 def test_auto_path_choice_other(ctx, fmt, E, H, F, k, T, shared, want):
     """AUTO for formats other than Q4_K and for layers with a shared expert:
     the grouped GEMM from ~3 tokens per routed expert, or from 6 tokens with
-    a shared expert, the GEMV below; Q4_K with a shared expert as wide as the
-    routed ones takes the split-activation path from 4 tokens up to 8
-    tokens per routed expert (the bits of the chosen path)."""
+    a shared expert, the GEMV below; Q4_0 without a shared expert, in whole
+    256-weight chunks, follows Q4_K's rule (split path from ~3 tokens per
+    expert up to 12); Q4_K with a shared expert as wide as the routed ones
+    takes the split-activation path from 4 tokens up to 8 tokens per routed
+    expert (the bits of the chosen path)."""
     L = Layer(fmt, E, H, F, k, T, seed=E + T + fmt, shared_F=shared)
     ex = L.upload(nx, ctx)
     auto = ex.forward(L.x, L.logits, k, 0, nx.PATH_AUTO)
