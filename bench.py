@@ -346,7 +346,7 @@ MODEL_CONFIGS = [
     # name, weight format, E, H, F, k, shared F, score mode, token counts, replicas rotated
     ("qwen3_q4k", "Q4_K", 128, 2048, 768, 8, 0, 0, (1, 64, 512), 2),
     ("deepseek_q4k_sigmoid_shared", "Q4_K", 256, 7168, 2048, 8, 2048, 1, (1, 4096), 2),
-    ("mixtral_q2k", "Q2_K", 8, 4096, 14336, 2, 0, 0, (1,), 4),
+    ("mixtral_q2k", "Q2_K", 8, 4096, 14336, 2, 0, 0, (1, 32), 4),
     ("mixtral_q4_0", "Q4_0", 8, 4096, 14336, 2, 0, 0, (1, 32), 4),
 ]
 

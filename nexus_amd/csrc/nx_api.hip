@@ -945,11 +945,16 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
   };
 
   int use = path;
-  if (ex->fmt == NX_FMT_Q2_K || ex->fmt == NX_FMT_F16 || ex->fmt == NX_FMT_BF16) {
+  if (ex->fmt == NX_FMT_F16 || ex->fmt == NX_FMT_BF16) {
     // no MFMA operand path for these formats
     if (use == NX_PATH_MFMA_F16 || use == NX_PATH_MFMA_BF16 || use == NX_PATH_MFMA_SPLIT)
       return fail(NX_ERR_UNSUPPORTED, std::string(fmt_name(ex->fmt)) + " experts run on the GEMV path only");
     use = NX_PATH_GEMV;
+  }
+  if (ex->fmt == NX_FMT_Q2_K && (use == NX_PATH_MFMA_F16 || use == NX_PATH_MFMA_BF16)) {
+    // Q2_K: the GEMV and the split-activation MFMA path (no grouped GEMM)
+    return fail(NX_ERR_UNSUPPORTED,
+                "Q2_K experts run on the GEMV and the split-activation MFMA path only");
   }
   // AUTO takes bf16 operands on the grouped GEMM: fp16's range ends at
   // 65504, which SwiGLU activations of real models can pass; bf16 keeps
@@ -960,7 +965,19 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
     const double kk = std::min(1.0, (double)k / E);
     const double act = std::max(1.0, E * (1.0 - std::pow(1.0 - kk, (double)T)));
     const double tpe = (double)T * k / act;
-    if (ex->fmt == NX_FMT_Q4_K && shared && ex->Fs == ex->F) {
+    if (ex->fmt == NX_FMT_Q2_K) {
+      // The GEMV or the split-activation path (Q2_K has no grouped GEMM).
+      // Measured (ms, GEMV / split): Mixtral 2 tokens 0.101 / 0.122, 4:
+      // 0.173 / 0.188, 8: 0.243 / 0.193, 32: 0.939 / 0.238, 128: 2.82 /
+      // 0.534; Qwen3 4 tokens 0.048 / 0.048, 8: 0.093 / 0.065, 512: 1.84 /
+      // 0.265; DeepSeek with its shared expert 2 tokens 0.119 / 0.137, 4:
+      // 0.307 / 0.218, 64: 44.1 / 1.52.
+      if (shared)
+        use = (ex->Fs == ex->F && T >= 4) ? NX_PATH_MFMA_SPLIT : NX_PATH_GEMV;
+      else
+        use = (tpe >= 1.8 || ((long)T * k >= 64 && tpe >= 1.2)) ? NX_PATH_MFMA_SPLIT
+                                                                 : NX_PATH_GEMV;
+    } else if (ex->fmt == NX_FMT_Q4_K && shared && ex->Fs == ex->F) {
       // A shared expert sees every token: the GEMV walks it a token pair at
       // a time, the split-activation path 16 tokens at a time.  Measured
       // (DeepSeek shapes, ms, GEMV / split / grouped GEMM): 2 tokens 0.115 /

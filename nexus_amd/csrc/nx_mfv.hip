@@ -1,4 +1,4 @@
-// nx_mfv.hip — few-token grouped matvec on MFMA for Q4_K and Q4_0 experts: decode
+// nx_mfv.hip — few-token grouped matvec on MFMA for Q4_K, Q4_0 and Q2_K experts: decode
 // batches whose experts see a handful of tokens each (2 to ~128 tokens),
 // with or without a shared expert (as wide as the routed ones) that sees
 // every token.
@@ -43,6 +43,12 @@
 // result.  The loads give a lane group two whole blocks; a 4 x 4 dword
 // transpose across the lane groups hands every lane group its 8 weights of
 // each block.
+//
+// Q2_K (w_i = d sc q_i - dmin m per 16-weight sub-block, 4-bit sc and m,
+// src/quant/mod.rs:913-937): a chunk is one block, its 4 resident segments
+// (64 weights in 16 bytes) one per lane group; MFMA u takes dword u % 4 of
+// half u / 4, 8 weights of sub-block 4 g + u / 2, whose scale goes into the
+// operands (q sc <= 45) and whose min into the min operands, as for Q4_K.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 
@@ -111,12 +117,20 @@ __device__ __forceinline__ void transpose_groups(uint32_t (&c)[4]) {
 // of a code dword (positions 2i, 2i+1 = elements i, 4+i)
 __device__ __forceinline__ constexpr int opos_elem(int p) { return (p & 1) * 4 + (p >> 1); }
 
-// one (row tile, chunk) step of a lane: dword (lane / 16) of each sub-block's
-// code half, and the block's scales (d, dmin, scales12)
-template <int NMAT>
+// one (row tile, chunk) step of a lane: Q4_K dword (lane / 16) of each
+// sub-block's code half, and the block's scales (d, dmin, scales12); Q4_0
+// blocks 2 g and 2 g + 1 and the chunk's 8 block scales
+template <int NMAT, int FMT>
 struct MfvStep {
   uint4 q[NMAT][2];  // sub-block g's code half, then sub-block g + 4's
   uint4 m[NMAT];
+};
+// Q2_K: segment g of the chunk (64 weights in 16 bytes) and its scale-plane
+// entry {f16 d, f16 dmin, the segment's four scale/min bytes}
+template <int NMAT>
+struct MfvStep<NMAT, NX_FMT_Q2_K> {
+  uint4 q[NMAT][1];
+  uint2 m[NMAT];
 };
 
 // Workgroup = (row block of 256 rows, tile of <= 16 pairs, K slice of
@@ -136,8 +150,9 @@ constexpr int MV_WG_ROWS = 4 * 16 * MV_RTW;
 
 template <bool GATEUP, int MV_KS, int FMT>
 __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a) {
-  static_assert(FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0, "Q4_K and Q4_0 codes");
-  constexpr bool Q40 = FMT == NX_FMT_Q4_0;
+  static_assert(FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0 || FMT == NX_FMT_Q2_K,
+                "Q4_K, Q4_0 and Q2_K codes");
+  constexpr bool Q40 = FMT == NX_FMT_Q4_0, Q2K = FMT == NX_FMT_Q2_K;
   constexpr int MV_D = MV_KS;  // steps in flight
   constexpr int NMAT = GATEUP ? 2 : 1;
   constexpr int NSTEP = MV_RTW * MV_KS;
@@ -183,32 +198,53 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
   // read at OOB.  Per-lane parts
   // of the offsets stay in one register per step; the rest goes in the scalar
   // offset.
-  auto issue = [&](MfvStep<NMAT> &w, int i) {
+  auto issue = [&](MfvStep<NMAT, FMT> &w, int i) {
     const int row = row_base + 16 * (i / MV_KS) + l16;
     const int c = c0 + i % MV_KS;
-    // the chunk's 4 segments share one group of 64: half h of segment
-    // 4c + g sits at base + h 16 gsz + 16 g; the 4 lanes of a row read 64
-    // contiguous bytes per half
-    const int j0 = 4 * c;
-    const int grp = j0 >> 6;
-    const int gsz = min(64, a.nseg - (grp << 6));
-    const uint32_t prq = panel_row_bytes(a.nseg, 32), prm = panel_row_bytes(a.nseg, 4);
-    const uint32_t base = (uint32_t)grp * (uint32_t)a.rows * prq + (uint32_t)((j0 & 63) * 16);
-    // steps past the last (issued by the pipeline's tail), chunks past the
-    // row (wave-uniform) and rows past the matrix read at OOB
-    const bool cv = i < NSTEP && c < a.nchunk && row < a.rows;
-    const uint32_t vq = cv ? (uint32_t)row * prq + 16u * g : OOB;
-    const uint32_t vm = cv ? ((uint32_t)grp * (uint32_t)a.rows + (uint32_t)row) * prm + 16u * (uint32_t)(c - 16 * grp)
-                           : OOB;
+    if constexpr (Q2K) {
+      // 16 bytes of codes and 8 of scales per segment: segment 4c + g at
+      // 16 (j % 64) and 8 (j % 64) of the row's part of its panel; the 4
+      // lanes of a row read 64 contiguous code bytes
+      const int j0 = 4 * c;
+      const int grp = j0 >> 6;
+      const uint32_t prq = panel_row_bytes(a.nseg, 16), prm = panel_row_bytes(a.nseg, 8);
+      const uint32_t base = (uint32_t)grp * (uint32_t)a.rows * prq + (uint32_t)((j0 & 63) * 16);
+      const uint32_t mbase = (uint32_t)grp * (uint32_t)a.rows * prm + (uint32_t)((j0 & 63) * 8);
+      const bool cv = i < NSTEP && c < a.nchunk && row < a.rows;
+      const uint32_t vq = cv ? (uint32_t)row * prq + 16u * g : OOB;
+      const uint32_t vm = cv ? (uint32_t)row * prm + 8u * g : OOB;
 #pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rq[mt], (int)vq,
-                                                             (int)(base + h * 16u * gsz), 0);
-        w.q[mt][h] = make_uint4(v[0], v[1], v[2], v[3]);
+      for (int mt = 0; mt < NMAT; ++mt) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rq[mt], (int)vq, (int)base, 0);
+        w.q[mt][0] = make_uint4(v[0], v[1], v[2], v[3]);
+        const auto u = __builtin_amdgcn_raw_buffer_load_b64(rm[mt], (int)vm, (int)mbase, 0);
+        w.m[mt] = make_uint2(u[0], u[1]);
       }
-      w.m[mt] = bload16(rm[mt], vm);
+    } else {
+      // the chunk's 4 segments share one group of 64: half h of segment
+      // 4c + g sits at base + h 16 gsz + 16 g; the 4 lanes of a row read 64
+      // contiguous bytes per half
+      const int j0 = 4 * c;
+      const int grp = j0 >> 6;
+      const int gsz = min(64, a.nseg - (grp << 6));
+      const uint32_t prq = panel_row_bytes(a.nseg, 32), prm = panel_row_bytes(a.nseg, 4);
+      const uint32_t base = (uint32_t)grp * (uint32_t)a.rows * prq + (uint32_t)((j0 & 63) * 16);
+      // steps past the last (issued by the pipeline's tail), chunks past the
+      // row (wave-uniform) and rows past the matrix read at OOB
+      const bool cv = i < NSTEP && c < a.nchunk && row < a.rows;
+      const uint32_t vq = cv ? (uint32_t)row * prq + 16u * g : OOB;
+      const uint32_t vm = cv ? ((uint32_t)grp * (uint32_t)a.rows + (uint32_t)row) * prm + 16u * (uint32_t)(c - 16 * grp)
+                             : OOB;
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(rq[mt], (int)vq,
+                                                               (int)(base + h * 16u * gsz), 0);
+          w.q[mt][h] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+        w.m[mt] = bload16(rm[mt], vm);
+      }
     }
   };
 
@@ -242,7 +278,7 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
   __builtin_amdgcn_sched_barrier(0);
 
   // the first weight steps, in flight during the staging
-  MfvStep<NMAT> ring[MV_D];
+  MfvStep<NMAT, FMT> ring[MV_D];
 #pragma unroll
   for (int i = 0; i < MV_D - 1; ++i) issue(ring[i], i);
   __builtin_amdgcn_sched_barrier(0);
@@ -291,7 +327,11 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
       // u0, u0 + 1 with u0 = 4 (sj / 8) + 2 (sj % 2).  Q4_0: MFMA b is
       // block b (elements 32 b ..), lane group g taking its elements
       // 32 b + 8 g + opos_elem(p); this thread's positions are block sj / 2,
-      // groups 2 (sj % 2) and 2 (sj % 2) + 1.
+      // groups 2 (sj % 2) and 2 (sj % 2) + 1.  Q2_K: lane group g takes
+      // segment g (elements 64 g ..), MFMA u its elements 32 (u / 4) +
+      // 8 (u % 4) + opos_elem(p) (dword u % 4 of half u / 4); this thread's
+      // positions are segment sj / 4, half (sj / 2) % 2, dwords 2 (sj % 2)
+      // and 2 (sj % 2) + 1.
 #pragma unroll
       for (int uu = 0; uu < 2; ++uu) {
         _Float16 ho[8], lo[8];
@@ -300,8 +340,10 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
           ho[p] = hv[8 * uu + opos_elem(p)];
           lo[p] = lv[8 * uu + opos_elem(p)];
         }
-        const int gq = Q40 ? 2 * (sj & 1) + uu : (sj & 7) >> 1;
-        const int u = Q40 ? sj >> 1 : 4 * (sj >> 3) + 2 * (sj & 1) + uu;
+        const int gq = Q40 ? 2 * (sj & 1) + uu : Q2K ? sj >> 2 : (sj & 7) >> 1;
+        const int u = Q40   ? sj >> 1
+                      : Q2K ? 4 * ((sj >> 1) & 1) + 2 * (sj & 1) + uu
+                            : 4 * (sj >> 3) + 2 * (sj & 1) + uu;
         const int L = sm + 16 * gq;
         st.a[u][0][L] = __builtin_bit_cast(uint4, ho);
         st.a[u][1][L] = __builtin_bit_cast(uint4, lo);
@@ -322,9 +364,9 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
   __syncthreads();
 
   // q 2^-24 sc as fp16 bits (q sc <= 945 < 1024: an exact subnormal) for
-  // the 8 codes of a dword, in nibble order
+  // the 8 unsigned codes of a dword, in nibble order (the 4-bit planes hold
+  // q ^ 8: their callers flip it back)
   auto operand = [](uint32_t cw, uint32_t sc2) {
-    cw ^= 0x88888888u;
     const uint32_t lo = cw & 0x0F0F0F0Fu, hi = (cw >> 4) & 0x0F0F0F0Fu;
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     const u16x2 sv = __builtin_bit_cast(u16x2, sc2);
@@ -340,7 +382,7 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
   //   sum_i w_i x_i = d sum_s sc_s sum_{i in s} q_i x_i - dmin sum_s m_s X_s
   // with sc_s inside the operands, so the 8 MFMAs of the block accumulate
   // together and d, dmin apply once per block
-  auto compute = [&](const MfvStep<NMAT> &w, const MfvStage<FMT> &st, f32x4 (&accr)[NMAT]) {
+  auto compute = [&](const MfvStep<NMAT, FMT> &w, const MfvStage<FMT> &st, f32x4 (&accr)[NMAT]) {
     if constexpr (Q40) {
       // Q4_0 (src/quant/mod.rs:723-745: w = d (q - 8) per 32-weight block).
       // One MFMA per block: lane group g holds dword g of the block (its
@@ -372,7 +414,7 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
         const float4 xs = *reinterpret_cast<const float4 *>(&st.xs[b][4 * g]);
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt) {
-          const f16x8 bq = operand(cq[mt][b & 1][b >> 1], 0x00010001u);
+          const f16x8 bq = operand(cq[mt][b & 1][b >> 1] ^ 0x88888888u, 0x00010001u);
           f32x4 y = f32x4{0.f, 0.f, 0.f, 0.f};
           y = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, y, 0, 0, 0);
           y = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, y, 0, 0, 0);
@@ -392,27 +434,40 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
       }
       return;
     }
-    // this lane's sub-blocks g and g + 4 (get_scale_min_k4,
-    // src/quant/mod.rs:1163-1170, on scales12): the scales go into the code
-    // operands, the mins into operands of their own (m as fp16, all 8
-    // positions), whose MFMAs form sum_s m_s X_s
-    uint32_t sc2[NMAT][2];
-    f16x8 bm[NMAT][2];
+    // Q4_K: this lane's sub-blocks g and g + 4 (get_scale_min_k4,
+    // src/quant/mod.rs:1163-1170, on scales12), MFMAs u < 4 and u >= 4.
+    // Q2_K (src/quant/mod.rs:913-937: w = d sc q - dmin m per 16-weight
+    // sub-block, sc and m the low and high nibble of its scale byte): this
+    // lane's sub-blocks 4 g + v, v = u / 2, from the segment's four scale
+    // bytes.  The scales go into the code operands, the mins into operands
+    // of their own (m as fp16, all 8 positions), whose MFMAs form
+    // sum_s m_s X_s
+    constexpr int NV = Q2K ? 4 : 2;
+    uint32_t sc2[NMAT][NV];
+    f16x8 bm[NMAT][NV];
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt) {
-      const uint32_t p03 = w.m[mt].y, p47 = w.m[mt].z, p8b = w.m[mt].w;
-      const uint32_t sca = (p03 >> (8 * g)) & 63;
-      const uint32_t scb = ((p8b >> (8 * g)) & 15) | (((p03 >> (8 * g + 6)) & 3) << 4);
-      const uint32_t mna = (p47 >> (8 * g)) & 63;
-      const uint32_t mnb = ((p8b >> (8 * g + 4)) & 15) | (((p47 >> (8 * g + 6)) & 3) << 4);
-      sc2[mt][0] = sca | (sca << 16);
-      sc2[mt][1] = scb | (scb << 16);
-      const uint32_t ha = __builtin_bit_cast(uint16_t, (_Float16)(float)mna);
-      const uint32_t hb = __builtin_bit_cast(uint16_t, (_Float16)(float)mnb);
-      const uint32_t da[4] = {ha * 0x10001u, ha * 0x10001u, ha * 0x10001u, ha * 0x10001u};
-      const uint32_t db[4] = {hb * 0x10001u, hb * 0x10001u, hb * 0x10001u, hb * 0x10001u};
-      bm[mt][0] = __builtin_bit_cast(f16x8, da);
-      bm[mt][1] = __builtin_bit_cast(f16x8, db);
+      uint32_t scv[NV], mnv[NV];
+      if constexpr (Q2K) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+          scv[v] = (w.m[mt].y >> (8 * v)) & 15;
+          mnv[v] = (w.m[mt].y >> (8 * v + 4)) & 15;
+        }
+      } else {
+        const uint32_t p03 = w.m[mt].y, p47 = w.m[mt].z, p8b = w.m[mt].w;
+        scv[0] = (p03 >> (8 * g)) & 63;
+        scv[1] = ((p8b >> (8 * g)) & 15) | (((p03 >> (8 * g + 6)) & 3) << 4);
+        mnv[0] = (p47 >> (8 * g)) & 63;
+        mnv[1] = ((p8b >> (8 * g + 4)) & 15) | (((p47 >> (8 * g + 6)) & 3) << 4);
+      }
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        sc2[mt][v] = scv[v] | (scv[v] << 16);
+        const uint32_t hm = __builtin_bit_cast(uint16_t, (_Float16)(float)mnv[v]);
+        const uint32_t dm[4] = {hm * 0x10001u, hm * 0x10001u, hm * 0x10001u, hm * 0x10001u};
+        bm[mt][v] = __builtin_bit_cast(f16x8, dm);
+      }
     }
     f32x4 y[NMAT], ym[NMAT];
 #pragma unroll
@@ -426,12 +481,17 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
       const f16x8 alo = __builtin_bit_cast(f16x8, st.a[u][1][lane]);
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt) {
-        const uint32_t cw = u < 4 ? (&w.q[mt][0].x)[u] : (&w.q[mt][1].x)[u - 4];
-        const f16x8 b = operand(cw, sc2[mt][u >> 2]);
+        uint32_t cw;
+        if constexpr (Q2K)  // the 2-bit codes of half u / 4 widened to nibbles (no offset)
+          cw = ((&w.q[mt][0].x)[u & 3] >> (2 * (u >> 2))) & 0x33333333u;
+        else
+          cw = (u < 4 ? (&w.q[mt][0].x)[u] : (&w.q[mt][1].x)[u - 4]) ^ 0x88888888u;
+        constexpr int vsh = Q2K ? 1 : 2;
+        const f16x8 b = operand(cw, sc2[mt][u >> vsh]);
         y[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, y[mt], 0, 0, 0);
         y[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, y[mt], 0, 0, 0);
-        ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bm[mt][u >> 2], ym[mt], 0, 0, 0);
-        ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bm[mt][u >> 2], ym[mt], 0, 0, 0);
+        ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bm[mt][u >> vsh], ym[mt], 0, 0, 0);
+        ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bm[mt][u >> vsh], ym[mt], 0, 0, 0);
       }
       // one MFMA step's operands live at a time: make the accumulators
       // exist here, or the compiler gathers every step's operands first.
@@ -521,9 +581,9 @@ int mfv_max_tiles(int T, int k, int E, bool shared) {
 }
 
 bool mfv_supports(const nx_experts *ex) {
-  // whole 256-weight chunks in both products: Q4_K always, Q4_0 when H and
-  // F are multiples of 256
-  if (ex->fmt == NX_FMT_Q4_K) return true;
+  // whole 256-weight chunks in both products: Q4_K and Q2_K always, Q4_0
+  // when H and F are multiples of 256
+  if (ex->fmt == NX_FMT_Q4_K || ex->fmt == NX_FMT_Q2_K) return true;
   return ex->fmt == NX_FMT_Q4_0 && ex->H % MV_K == 0 && ex->F % MV_K == 0;
 }
 
@@ -531,8 +591,8 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
   const nx_experts *ex = p.ex;
   if (!mfv_supports(ex))
     return fail(NX_ERR_UNSUPPORTED,
-                "the split-activation MFMA path takes Q4_K experts, or Q4_0 experts whose "
-                "hidden and FFN widths are multiples of 256");
+                "the split-activation MFMA path takes Q4_K and Q2_K experts, or Q4_0 experts "
+                "whose hidden and FFN widths are multiples of 256");
   // activation rows are read as float4 runs of whole chunks
   if (reinterpret_cast<uintptr_t>(p.x) & 15)
     return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path needs 16-byte aligned inputs");
@@ -603,6 +663,8 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
                     [&] {
                       if (ex->fmt == NX_FMT_Q4_0)
                         go(c, k_mfv<true, MV_KS_GATEUP, NX_FMT_Q4_0>, grid, dim3(256), 0, a);
+                      else if (ex->fmt == NX_FMT_Q2_K)
+                        go(c, k_mfv<true, MV_KS_GATEUP, NX_FMT_Q2_K>, grid, dim3(256), 0, a);
                       else
                         go(c, k_mfv<true, MV_KS_GATEUP, NX_FMT_Q4_K>, grid, dim3(256), 0, a);
                     }));
@@ -617,6 +679,8 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
                     [&] {
                       if (ex->fmt == NX_FMT_Q4_0)
                         go(c, k_mfv<false, MV_KS_DOWN, NX_FMT_Q4_0>, grid, dim3(256), 0, a);
+                      else if (ex->fmt == NX_FMT_Q2_K)
+                        go(c, k_mfv<false, MV_KS_DOWN, NX_FMT_Q2_K>, grid, dim3(256), 0, a);
                       else
                         go(c, k_mfv<false, MV_KS_DOWN, NX_FMT_Q4_K>, grid, dim3(256), 0, a);
                     }));

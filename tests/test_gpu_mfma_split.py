@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 
 import nexus_amd as nx
-from moe_cases import Q4_0, Q4_K, Q8_0, Layer, rel_l2
+from moe_cases import Q2_K, Q4_0, Q4_K, Q8_0, Layer, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -183,6 +183,12 @@ def test_auto_path_choice(ctx, E, H, F, k, T, want):
     (Q4_0, 8, 512, 1024, 2, 64, 0, nx.PATH_MFMA_BF16),   # 16
     (Q4_0, 8, 512, 992, 2, 16, 0, nx.PATH_MFMA_BF16),    # F not whole 256-weight chunks
     (Q4_0, 16, 512, 512, 4, 8, 512, nx.PATH_MFMA_BF16),  # a shared expert, 8 tokens
+    (Q2_K, 8, 512, 1024, 2, 4, 0, nx.PATH_GEMV),         # 1.5 tokens per expert
+    (Q2_K, 8, 512, 1024, 2, 8, 0, nx.PATH_MFMA_SPLIT),   # 2.2
+    (Q2_K, 8, 256, 256, 2, 256, 0, nx.PATH_MFMA_SPLIT),  # 64: no grouped GEMM for Q2_K
+    (Q2_K, 16, 512, 512, 4, 2, 512, nx.PATH_GEMV),         # a shared expert, 2 tokens
+    (Q2_K, 16, 512, 512, 4, 4, 512, nx.PATH_MFMA_SPLIT),   # ... 4 tokens
+    (Q2_K, 16, 256, 768, 4, 16, 256, nx.PATH_GEMV),        # a narrower shared expert
     (Q4_K, 16, 512, 512, 4, 2, 512, nx.PATH_GEMV),        # a shared expert, 2 tokens
     (Q4_K, 16, 512, 512, 4, 4, 512, nx.PATH_MFMA_SPLIT),  # ... 4 tokens
     (Q4_K, 16, 512, 512, 4, 8, 512, nx.PATH_MFMA_SPLIT),  # ... 8 tokens
@@ -195,7 +201,9 @@ def test_auto_path_choice_other(ctx, fmt, E, H, F, k, T, shared, want):
     the grouped GEMM from ~3 tokens per routed expert, or from 6 tokens with
     a shared expert, the GEMV below; Q4_0 without a shared expert, in whole
     256-weight chunks, follows Q4_K's rule (split path from ~3 tokens per
-    expert up to 12); Q4_K with a shared expert as wide as the routed ones
+    expert up to 12); Q2_K takes the split path from ~1.8 tokens per expert
+    (or 4 tokens with a shared expert as wide as the routed ones), the GEMV
+    below; Q4_K with a shared expert as wide as the routed ones
     takes the split-activation path from 4 tokens up to 8 tokens per routed
     expert (the bits of the chosen path)."""
     L = Layer(fmt, E, H, F, k, T, seed=E + T + fmt, shared_F=shared)

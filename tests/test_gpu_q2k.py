@@ -5,8 +5,11 @@ Bars: dequantization and the quantizer bit-exact against the oracle
 data at several magnitudes, zero, positive-only and constant sub-blocks, a
 ragged tail); the MoE layer with Q2_K experts on the GEMV path within
 relative L2 1e-4 of the oracle over the same payloads (1 to 64 tokens, a
-shared expert, the sigmoid score mode); the MFMA paths reject Q2_K with
-NX_ERR_UNSUPPORTED and AUTO runs it on the GEMV path.
+shared expert, the sigmoid score mode); the split-activation MFMA path to the
+same bar (1 to 64 tokens, several tiles per expert, a shared expert as wide as
+the routed ones, rows of very different magnitudes, Mixtral's full shape); the
+grouped GEMM paths reject Q2_K with NX_ERR_UNSUPPORTED; AUTO gives the bits of
+the path it picks.
 """
 import numpy as np
 import pytest
@@ -66,11 +69,49 @@ def test_q2k_layer_gemv_parity(ctx, E, H, F, k, T, shared, score):
     L = Layer(Q2_K, E, H, F, k, T, seed=E + H + F + T, shared_F=shared, score_mode=score)
     ex = L.upload(nx, ctx)
     got = ex.forward(L.x, L.logits, k, score, nx.PATH_GEMV)
-    auto = ex.forward(L.x, L.logits, k, score, nx.PATH_AUTO)
     ex.close()
     ref = L.oracle_out()
     assert rel_l2(got, ref) <= GEMV_TOL
-    assert_same_bits(auto, got)
+
+
+@pytest.mark.parametrize("E,H,F,k,T,shared,score", [
+    (8, 512, 1024, 2, 1, 0, 0), (8, 1024, 512, 2, 5, 0, 0), (8, 256, 768, 2, 33, 0, 0),
+    (32, 512, 256, 8, 24, 0, 1), (16, 1024, 512, 4, 64, 0, 0),
+    (16, 512, 512, 4, 8, 512, 1), (8, 256, 768, 2, 40, 768, 0),
+    (4, 4096, 512, 2, 3, 0, 0), (4, 512, 14336, 2, 6, 0, 0)])
+def test_q2k_layer_split_parity(ctx, E, H, F, k, T, shared, score):
+    """Q2_K on the split-activation MFMA path: segment g of a 256-weight
+    chunk per lane group, each 16-weight sub-block's 4-bit scale inside the
+    code operands and its 4-bit min in operands of its own."""
+    print(f"q2k split E={E} H={H} F={F} k={k} T={T} shared={shared}", flush=True)
+    L = Layer(Q2_K, E, H, F, k, T, seed=E * 3 + H + F + T, shared_F=shared, score_mode=score)
+    ex = L.upload(nx, ctx)
+    got = ex.forward(L.x, L.logits, k, score, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    assert rel_l2(got, L.oracle_out()) <= GEMV_TOL
+
+
+def test_q2k_split_magnitudes_and_mixtral_shape(ctx):
+    L = Layer(Q2_K, 8, 512, 512, 2, 12, seed=45)
+    scale = np.array([1e-30, 1e-6, 1.0, 3e3, 1e6, 0.0, 1.0, 1e-3, 7.0, 0.0, 1e4, 1e-2],
+                     np.float32)[:, None]
+    L.x = (L.x * scale).astype(np.float32)
+    L.x[2, 256:] = 0.0  # one zero chunk inside a live row
+    ex = L.upload(nx, ctx)
+    got = ex.forward(L.x, L.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    ref = L.oracle_out()
+    for t in range(L.T):
+        den = np.linalg.norm(ref[t])
+        if den == 0:
+            assert np.all(got[t] == 0)
+        else:
+            assert rel_l2(got[t], ref[t]) <= GEMV_TOL, t
+    M = Layer(Q2_K, 8, 4096, 14336, 2, 8, seed=11)
+    ex = M.upload(nx, ctx)
+    got = ex.forward(M.x, M.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    assert rel_l2(got, M.oracle_out()) <= GEMV_TOL
 
 
 def test_q2k_rejects_mfma(ctx):
