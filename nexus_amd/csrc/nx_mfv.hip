@@ -57,6 +57,7 @@ namespace nx {
 namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int MV_M = 16;   // pairs per tile
@@ -83,13 +84,24 @@ struct MfvArgs {
 
 // LDS area of one chunk: the A operands (hi, lo) of the 8 MFMAs in lane
 // order and the per-pair unscale factors; Q4_0 also keeps each block's
-// activation sum (times 8) per pair
+// activation sum (times 8) per pair, Q4_K and Q2_K the A operand of the
+// min-term MFMA (each sub-block's activation sum, hi and lo)
 struct MfvStageBase {
   uint4 a[8][2][64];  // [MFMA][hi, lo][lane]
   float sx[MV_M];
 };
 template <int FMT>
-struct MfvStage : MfvStageBase {};
+struct MfvStage : MfvStageBase {
+  // Q4_K: lane L holds pair L % 16's sums of sub-blocks 2 (L / 16) and
+  // 2 (L / 16) + 1, each as (hi, lo) fp16
+  uint2 xm[64];
+};
+template <>
+struct MfvStage<NX_FMT_Q2_K> : MfvStageBase {
+  // Q2_K: lane L holds pair L % 16's sums of sub-blocks 4 (L / 16) ..
+  // 4 (L / 16) + 3, each as (hi, lo) fp16
+  uint4 xm[64];
+};
 template <>
 struct MfvStage<NX_FMT_Q4_0> : MfvStageBase {
   float xs[8][MV_M];  // [block][pair]: 8 times the block's sum of the operand values
@@ -348,14 +360,27 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
         st.a[u][0][L] = __builtin_bit_cast(uint4, ho);
         st.a[u][1][L] = __builtin_bit_cast(uint4, lo);
       }
-      if constexpr (Q40) {
-        // the block's sum of the values the operands carry (hi + lo, exact
-        // in f32), over this thread's half and its neighbour's
-        float bs = 0.f;
+      // the sums of the values the operands carry (hi + lo) over this
+      // thread's 16 positions: Q2_K sub-block sj; with the neighbour's, Q4_0
+      // block sj / 2 and Q4_K sub-block sj / 2
+      float bs = 0.f;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) bs += (float)hv[v] + (float)lv[v];
-        bs += __shfl_xor(bs, 1, 64);
+      for (int v = 0; v < 16; ++v) bs += (float)hv[v] + (float)lv[v];
+      if constexpr (!Q2K) bs += __shfl_xor(bs, 1, 64);
+      if constexpr (Q40) {
         if ((sj & 1) == 0) st.xs[sj >> 1][sm] = 8.0f * bs;
+      } else {
+        // the min-term operand: X 2^-6 (|X| <= 32 x 2^14) as hi + lo fp16
+        const float xq = bs * 0.015625f;
+        const _Float16 xh = (_Float16)xq, xl = (_Float16)(xq - (float)xh);
+        const uint32_t hl = (uint32_t)__builtin_bit_cast(uint16_t, xh) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, xl) << 16);
+        if constexpr (Q2K) {
+          (&st.xm[sm + 16 * (sj >> 2)].x)[sj & 3] = hl;
+        } else {
+          const int sb = sj >> 1;  // sub-block
+          if ((sj & 1) == 0) (&st.xm[sm + 16 * (sb >> 1)].x)[sb & 1] = hl;
+        }
       }
       if (sj == 0) st.sx[sm] = __builtin_amdgcn_ldexpf(1.0f, E - 14);
       __builtin_amdgcn_sched_barrier(0);
@@ -432,89 +457,105 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
           asm volatile("" : "+v"(accr[mt]));
         }
       }
-      return;
-    }
-    // Q4_K: this lane's sub-blocks g and g + 4 (get_scale_min_k4,
-    // src/quant/mod.rs:1163-1170, on scales12), MFMAs u < 4 and u >= 4.
-    // Q2_K (src/quant/mod.rs:913-937: w = d sc q - dmin m per 16-weight
-    // sub-block, sc and m the low and high nibble of its scale byte): this
-    // lane's sub-blocks 4 g + v, v = u / 2, from the segment's four scale
-    // bytes.  The scales go into the code operands, the mins into operands
-    // of their own (m as fp16, all 8 positions), whose MFMAs form
-    // sum_s m_s X_s
-    constexpr int NV = Q2K ? 4 : 2;
-    uint32_t sc2[NMAT][NV];
-    f16x8 bm[NMAT][NV];
+    } else {
+      // Q4_K: this lane's sub-blocks g and g + 4 (get_scale_min_k4,
+      // src/quant/mod.rs:1163-1170, on scales12), MFMAs u < 4 and u >= 4.
+      // Q2_K (src/quant/mod.rs:913-937: w = d sc q - dmin m per 16-weight
+      // sub-block, sc and m the low and high nibble of its scale byte): this
+      // lane's sub-blocks 4 g + v, v = u / 2, from the segment's four scale
+      // bytes.  The scales go into the code operands.  sum_s m_s X_s is one
+      // more MFMA per chunk, on the staged sub-block sums X_s (hi, lo) and
+      // the row's mins (each twice, for hi and lo): Q4_K K = 16 (lane group g
+      // takes sub-blocks 2 g, 2 g + 1), Q2_K K = 32 (sub-blocks 4 g ..
+      // 4 g + 3).  (Mins in operands of their own under every code MFMA
+      // cost 16 MFMAs per chunk instead of one: Mixtral 32 tokens 262 ->
+      // 247 us, Q2_K 64 tokens 285 -> 248 us.)
+      constexpr int NV = Q2K ? 4 : 2;
+      uint32_t sc2[NMAT][NV], bm[NMAT][NV];
 #pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) {
-      uint32_t scv[NV], mnv[NV];
-      if constexpr (Q2K) {
+      for (int mt = 0; mt < NMAT; ++mt) {
+        uint32_t scv[NV], mnv[NV];
+        if constexpr (Q2K) {
+#pragma unroll
+          for (int v = 0; v < NV; ++v) {
+            scv[v] = (w.m[mt].y >> (8 * v)) & 15;
+            mnv[v] = (w.m[mt].y >> (8 * v + 4)) & 15;
+          }
+        } else {
+          const uint32_t p03 = w.m[mt].y, p47 = w.m[mt].z, p8b = w.m[mt].w;
+          scv[0] = (p03 >> (8 * g)) & 63;
+          scv[1] = ((p8b >> (8 * g)) & 15) | (((p03 >> (8 * g + 6)) & 3) << 4);
+          // mins of sub-blocks j = 2 g + v: j < 4 from p47 alone, j >= 4
+          // from p8b's high nibble and p47's top bits
+#pragma unroll
+          for (int v = 0; v < 2; ++v) {
+            const int jb = 8 * ((2 * g + v) & 3);
+            const uint32_t lo6 = (p47 >> jb) & 63;
+            const uint32_t hi6 = ((p8b >> (jb + 4)) & 15) | (((p47 >> (jb + 6)) & 3) << 4);
+            mnv[v] = g < 2 ? lo6 : hi6;
+          }
+        }
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
-          scv[v] = (w.m[mt].y >> (8 * v)) & 15;
-          mnv[v] = (w.m[mt].y >> (8 * v + 4)) & 15;
+          sc2[mt][v] = scv[v] | (scv[v] << 16);
+          bm[mt][v] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)mnv[v]) * 0x10001u;
         }
-      } else {
-        const uint32_t p03 = w.m[mt].y, p47 = w.m[mt].z, p8b = w.m[mt].w;
-        scv[0] = (p03 >> (8 * g)) & 63;
-        scv[1] = ((p8b >> (8 * g)) & 15) | (((p03 >> (8 * g + 6)) & 3) << 4);
-        mnv[0] = (p47 >> (8 * g)) & 63;
-        mnv[1] = ((p8b >> (8 * g + 4)) & 15) | (((p47 >> (8 * g + 6)) & 3) << 4);
       }
-#pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        sc2[mt][v] = scv[v] | (scv[v] << 16);
-        const uint32_t hm = __builtin_bit_cast(uint16_t, (_Float16)(float)mnv[v]);
-        const uint32_t dm[4] = {hm * 0x10001u, hm * 0x10001u, hm * 0x10001u, hm * 0x10001u};
-        bm[mt][v] = __builtin_bit_cast(f16x8, dm);
-      }
-    }
-    f32x4 y[NMAT], ym[NMAT];
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) {
-      y[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      ym[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const f16x8 ahi = __builtin_bit_cast(f16x8, st.a[u][0][lane]);
-      const f16x8 alo = __builtin_bit_cast(f16x8, st.a[u][1][lane]);
+      f32x4 y[NMAT], ym[NMAT];
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt) {
-        uint32_t cw;
-        if constexpr (Q2K)  // the 2-bit codes of half u / 4 widened to nibbles (no offset)
-          cw = ((&w.q[mt][0].x)[u & 3] >> (2 * (u >> 2))) & 0x33333333u;
-        else
-          cw = (u < 4 ? (&w.q[mt][0].x)[u] : (&w.q[mt][1].x)[u - 4]) ^ 0x88888888u;
-        constexpr int vsh = Q2K ? 1 : 2;
-        const f16x8 b = operand(cw, sc2[mt][u >> vsh]);
-        y[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, y[mt], 0, 0, 0);
-        y[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, y[mt], 0, 0, 0);
-        ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bm[mt][u >> vsh], ym[mt], 0, 0, 0);
-        ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bm[mt][u >> vsh], ym[mt], 0, 0, 0);
+        y[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (Q2K) {
+          const uint4 xa = st.xm[lane];
+          const uint32_t av[4] = {xa.x, xa.y, xa.z, xa.w};
+          ym[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av),
+                                                          __builtin_bit_cast(f16x8, bm[mt]),
+                                                          f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        } else {
+          const uint2 xa = st.xm[lane];
+          const uint32_t av[2] = {xa.x, xa.y};
+          ym[mt] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, av),
+                                                         __builtin_bit_cast(f16x4, bm[mt]),
+                                                         f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        }
       }
-      // one MFMA step's operands live at a time: make the accumulators
-      // exist here, or the compiler gathers every step's operands first.
-      // Each is pinned as one register tuple (pinning its four elements
-      // separately made the compiler move them between registers: ~64
-      // extra moves per step)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const f16x8 ahi = __builtin_bit_cast(f16x8, st.a[u][0][lane]);
+        const f16x8 alo = __builtin_bit_cast(f16x8, st.a[u][1][lane]);
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt) {
+          uint32_t cw;
+          if constexpr (Q2K)  // the 2-bit codes of half u / 4 widened to nibbles (no offset)
+            cw = ((&w.q[mt][0].x)[u & 3] >> (2 * (u >> 2))) & 0x33333333u;
+          else
+            cw = (u < 4 ? (&w.q[mt][0].x)[u] : (&w.q[mt][1].x)[u - 4]) ^ 0x88888888u;
+          constexpr int vsh = Q2K ? 1 : 2;
+          const f16x8 b = operand(cw, sc2[mt][u >> vsh]);
+          y[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, b, y[mt], 0, 0, 0);
+          y[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, b, y[mt], 0, 0, 0);
+        }
+        // one MFMA step's operands live at a time: make the accumulators
+        // exist here, or the compiler gathers every step's operands first.
+        // Each is pinned as one register tuple (pinning its four elements
+        // separately made the compiler move them between registers: ~64
+        // extra moves per step)
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt) asm volatile("" : "+v"(y[mt]));
+      }
+      float sx[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sx[k] = st.sx[4 * g + k];
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt) {
-        asm volatile("" : "+v"(y[mt]));
-        asm volatile("" : "+v"(ym[mt]));
+        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x & 0xFFFF));
+        const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x >> 16));
+        const float dd = d * 16777216.0f;  // code operands carry 2^-24
+        const float dm = dmin * 64.0f;     // the min-term operands carry X 2^-6
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          accr[mt][k] = fmaf(sx[k], fmaf(dd, y[mt][k], -dm * ym[mt][k]), accr[mt][k]);
       }
-    }
-    float sx[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) sx[k] = st.sx[4 * g + k];
-#pragma unroll
-    for (int mt = 0; mt < NMAT; ++mt) {
-      const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x & 0xFFFF));
-      const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(w.m[mt].x >> 16));
-      const float dd = d * 16777216.0f;  // code operands carry 2^-24
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        accr[mt][k] = fmaf(sx[k], fmaf(dd, y[mt][k], -dmin * ym[mt][k]), accr[mt][k]);
     }
   };
 

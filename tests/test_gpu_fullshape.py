@@ -49,7 +49,7 @@ PATHS = {
     "deepseek_q4k_sigmoid_shared_t4096": [nx.PATH_GEMV, nx.PATH_MFMA_SPLIT, nx.PATH_MFMA_F16,
                                           nx.PATH_MFMA_BF16],
     "mixtral_q4_0_t1": [nx.PATH_GEMV],
-    "mixtral_q4_0_t256": [nx.PATH_MFMA_BF16],
+    "mixtral_q4_0_t256": [nx.PATH_MFMA_SPLIT, nx.PATH_MFMA_BF16],
 }
 
 
