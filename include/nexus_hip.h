@@ -88,18 +88,20 @@ extern "C" {
 
 /* expert-product paths */
 #define NX_PATH_AUTO 0      /* by tokens per expert: GEMV, then (Q4_K and Q2_K with no shared
-                               expert or one as wide as the routed experts; Q4_0 in whole
-                               256-weight chunks with no shared expert) the split-activation
-                               MFMA path, then (not Q2_K) the grouped GEMM on bf16 operands */
+                               expert or one as wide as the routed experts; Q4_0 and Q8_0 in
+                               whole 256-weight chunks with no shared expert) the
+                               split-activation MFMA path, then (not Q2_K) the grouped GEMM
+                               on bf16 operands */
 #define NX_PATH_GEMV 1      /* dequant-in-register GEMV, fp32 accumulate */
 #define NX_PATH_MFMA_F16 2  /* grouped GEMM on fp16 MFMA, fp32 accumulate; activations and
                                SwiGLU outputs must stay within fp16's range (|v| < 65504) */
 #define NX_PATH_MFMA_BF16 3 /* same on bf16 MFMA */
-#define NX_PATH_MFMA_SPLIT 4 /* few tokens per expert (decode batches), Q4_K, Q2_K, or Q4_0 whose
-                                hidden and ff dims are multiples of 256: fp16 MFMA on the raw
-                                codes with activations split into two fp16 halves, block and
-                                sub-block scales applied to the products; no dequantization.
-                                A shared expert must have the routed experts' ff_dim */
+#define NX_PATH_MFMA_SPLIT 4 /* few tokens per expert (decode batches), Q4_K, Q2_K, or Q4_0 and
+                                Q8_0 whose hidden and ff dims are multiples of 256: fp16 MFMA
+                                on the raw codes with activations split into two fp16 halves,
+                                block and sub-block scales applied to the products; no
+                                dequantization.  A shared expert must have the routed experts'
+                                ff_dim */
 
 /* expert matrix roles */
 #define NX_ROLE_GATE 0 /* [ff_dim x hidden] */

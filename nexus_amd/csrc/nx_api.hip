@@ -990,7 +990,8 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
         use = NX_PATH_MFMA_BF16;
       else
         use = T >= 4 ? NX_PATH_MFMA_SPLIT : NX_PATH_GEMV;
-    } else if ((ex->fmt == NX_FMT_Q4_K || (ex->fmt == NX_FMT_Q4_0 && mfv_supports(ex))) &&
+    } else if ((ex->fmt == NX_FMT_Q4_K ||
+                ((ex->fmt == NX_FMT_Q4_0 || ex->fmt == NX_FMT_Q8_0) && mfv_supports(ex))) &&
                !shared) {
       // Measured crossovers (Mixtral and Qwen3 shapes): the GEMV re-reads an
       // expert's weights per pair of its tokens and wins below ~2 tokens per
@@ -1001,9 +1002,12 @@ int nx::moe_forward(nx_ctx *c, const nx_experts *ex, const float *d_x, const flo
       // grouped GEMM): Mixtral 2 tokens per expert 0.183 / 0.233 / 0.290,
       // 4: 0.368 / 0.253 / 0.295, 8: - / 0.272 / 0.297, 16: - / 0.343 /
       // 0.299; Qwen3 1.2: 0.079 / 0.069 / 0.095, 4: 0.285 / 0.135 / 0.160.
-      // (With a shared expert Q4_0 keeps the rule below: at DeepSeek's
-      // shape the split path and the grouped GEMM are within 4% from 16
-      // tokens.)
+      // Q8_0: Mixtral 2 tokens per expert 0.287 / 0.317 / 0.351, 4: 0.600 /
+      // 0.344 / 0.359, 8: - / 0.366 / 0.379, 16: - / 0.435 / 0.383; Qwen3
+      // 1.2: 0.083 / 0.081 / 0.103, 4: 0.347 / 0.169 / 0.184, 8: - / 0.175 /
+      // 0.188, 16: - / 0.247 / 0.192.  (With a shared expert Q4_0 and Q8_0
+      // keep the rule below: at DeepSeek's shape the split path and the
+      // grouped GEMM are within 4% from 16 tokens.)
       if (tpe >= 12.0)
         use = NX_PATH_MFMA_BF16;
       else if (tpe >= 3.0 || ((long)T * k >= 64 && tpe >= 1.2))

@@ -1,4 +1,4 @@
-// nx_mfv.hip — few-token grouped matvec on MFMA for Q4_K, Q4_0 and Q2_K experts: decode
+// nx_mfv.hip — few-token grouped matvec on MFMA for Q4_K, Q4_0, Q8_0 and Q2_K experts: decode
 // batches whose experts see a handful of tokens each (2 to ~128 tokens),
 // with or without a shared expert (as wide as the routed ones) that sees
 // every token.
@@ -42,7 +42,10 @@
 // staged activation sum, the f16 block scale d applied to that MFMA's
 // result.  The loads give a lane group two whole blocks; a 4 x 4 dword
 // transpose across the lane groups hands every lane group its 8 weights of
-// each block.
+// each block.  Q8_0 (w_i = d q_i, q_i a signed byte, src/quant/mod.rs:
+// 689-703) likewise, with the operand q_i + 128 (one byte permute per two
+// weights), 128 X taken off, and dword pairs transposed (a lane group loads
+// two whole blocks of 32 bytes).
 //
 // Q2_K (w_i = d sc q_i - dmin m per 16-weight sub-block, 4-bit sc and m,
 // src/quant/mod.rs:913-937): a chunk is one block, its 4 resident segments
@@ -106,6 +109,10 @@ template <>
 struct MfvStage<NX_FMT_Q4_0> : MfvStageBase {
   float xs[8][MV_M];  // [block][pair]: 8 times the block's sum of the operand values
 };
+template <>
+struct MfvStage<NX_FMT_Q8_0> : MfvStageBase {
+  float xs[8][MV_M];  // [block][pair]: 128 times the block's sum of the operand values
+};
 
 // 4 x 4 transpose of dwords across the four 16-lane groups: on return
 // c[k] of lane group g holds what c[g] of lane group k held (register
@@ -137,6 +144,13 @@ struct MfvStep {
   uint4 q[NMAT][2];  // sub-block g's code half, then sub-block g + 4's
   uint4 m[NMAT];
 };
+// Q8_0: blocks 2 g and 2 g + 1 of the chunk (halves 0 and 1 each) and the
+// chunk's 8 block scales
+template <int NMAT>
+struct MfvStep<NMAT, NX_FMT_Q8_0> {
+  uint4 q[NMAT][4];  // [2 t + h]: half h of block 2 g + t
+  uint4 m[NMAT];
+};
 // Q2_K: segment g of the chunk (64 weights in 16 bytes) and its scale-plane
 // entry {f16 d, f16 dmin, the segment's four scale/min bytes}
 template <int NMAT>
@@ -157,15 +171,25 @@ struct MfvStep<NMAT, NX_FMT_Q2_K> {
 // 83 -> 80 us; 64 tokens 116 -> 109 us; two chunks, four workgroups per
 // CU, gained no more and added combine work)
 constexpr int MV_KS_GATEUP = 4, MV_KS_DOWN = 3;
+// steps in flight + 1: one per chunk of the slice, but for Q8_0's gate/up
+// pass, whose steps carry twice the code bytes (two steps in flight, for
+// the registers)
+template <bool GATEUP, int FMT>
+constexpr int mv_ring() {
+  return GATEUP ? (FMT == NX_FMT_Q8_0 ? 3 : MV_KS_GATEUP) : MV_KS_DOWN;
+}
 constexpr int MV_RTW = 4;  // row tiles per wave
 constexpr int MV_WG_ROWS = 4 * 16 * MV_RTW;
 
-template <bool GATEUP, int MV_KS, int FMT>
+template <bool GATEUP, int MV_KS, int FMT, int MV_D>
 __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a) {
-  static_assert(FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0 || FMT == NX_FMT_Q2_K,
-                "Q4_K, Q4_0 and Q2_K codes");
-  constexpr bool Q40 = FMT == NX_FMT_Q4_0, Q2K = FMT == NX_FMT_Q2_K;
-  constexpr int MV_D = MV_KS;  // steps in flight
+  static_assert(FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0 || FMT == NX_FMT_Q2_K ||
+                    FMT == NX_FMT_Q8_0,
+                "Q4_K, Q4_0, Q2_K and Q8_0 codes");
+  // Q4_0 and Q8_0: one MFMA per 32-weight block, scaled per block
+  constexpr bool Q40 = FMT == NX_FMT_Q4_0, Q2K = FMT == NX_FMT_Q2_K, Q80 = FMT == NX_FMT_Q8_0;
+  constexpr bool BLK = Q40 || Q80;
+  // MV_D ring slots: MV_D - 1 steps in flight while one is computed
   constexpr int NMAT = GATEUP ? 2 : 1;
   constexpr int NSTEP = MV_RTW * MV_KS;
   __shared__ MfvStage<FMT> stage[MV_KS];
@@ -231,6 +255,30 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
         w.q[mt][0] = make_uint4(v[0], v[1], v[2], v[3]);
         const auto u = __builtin_amdgcn_raw_buffer_load_b64(rm[mt], (int)vm, (int)mbase, 0);
         w.m[mt] = make_uint2(u[0], u[1]);
+      }
+    } else if constexpr (Q80) {
+      // 8 segments (blocks) per chunk, in one group of 64: half h of
+      // segment 8c + 2g + t sits at base + h 16 gsz + 32 g + 16 t; the
+      // chunk's 8 f16 scales are 16 bytes of the scale plane's panel row
+      const int j0 = 8 * c;
+      const int grp = j0 >> 6;
+      const int gsz = min(64, a.nseg - (grp << 6));
+      const uint32_t prq = panel_row_bytes(a.nseg, 32), prm = panel_row_bytes(a.nseg, 2);
+      const uint32_t base = (uint32_t)grp * (uint32_t)a.rows * prq + (uint32_t)((j0 & 63) * 16);
+      const bool cv = i < NSTEP && c < a.nchunk && row < a.rows;
+      const uint32_t vq = cv ? (uint32_t)row * prq + 32u * g : OOB;
+      const uint32_t vm = cv ? ((uint32_t)grp * (uint32_t)a.rows + (uint32_t)row) * prm + 2u * (uint32_t)(j0 & 63)
+                             : OOB;
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt) {
+#pragma unroll
+        for (int th = 0; th < 4; ++th) {
+          const int t = th >> 1, h = th & 1;
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+              rq[mt], (int)vq, (int)(base + h * 16u * gsz + 16u * t), 0);
+          w.q[mt][th] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+        w.m[mt] = bload16(rm[mt], vm);
       }
     } else {
       // the chunk's 4 segments share one group of 64: half h of segment
@@ -349,11 +397,13 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
         _Float16 ho[8], lo[8];
 #pragma unroll
         for (int p = 0; p < 8; ++p) {
-          ho[p] = hv[8 * uu + opos_elem(p)];
-          lo[p] = lv[8 * uu + opos_elem(p)];
+          // Q8_0 operands hold their 8 codes in element order
+          const int e = Q80 ? p : opos_elem(p);
+          ho[p] = hv[8 * uu + e];
+          lo[p] = lv[8 * uu + e];
         }
-        const int gq = Q40 ? 2 * (sj & 1) + uu : Q2K ? sj >> 2 : (sj & 7) >> 1;
-        const int u = Q40   ? sj >> 1
+        const int gq = BLK ? 2 * (sj & 1) + uu : Q2K ? sj >> 2 : (sj & 7) >> 1;
+        const int u = BLK   ? sj >> 1
                       : Q2K ? 4 * ((sj >> 1) & 1) + 2 * (sj & 1) + uu
                             : 4 * (sj >> 3) + 2 * (sj & 1) + uu;
         const int L = sm + 16 * gq;
@@ -367,8 +417,9 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
 #pragma unroll
       for (int v = 0; v < 16; ++v) bs += (float)hv[v] + (float)lv[v];
       if constexpr (!Q2K) bs += __shfl_xor(bs, 1, 64);
-      if constexpr (Q40) {
-        if ((sj & 1) == 0) st.xs[sj >> 1][sm] = 8.0f * bs;
+      if constexpr (BLK) {
+        // the codes' offset times the block sum: Q4_0 8, Q8_0 128
+        if ((sj & 1) == 0) st.xs[sj >> 1][sm] = (Q80 ? 128.0f : 8.0f) * bs;
       } else {
         // the min-term operand: X 2^-6 (|X| <= 32 x 2^14) as hi + lo fp16
         const float xq = bs * 0.015625f;
@@ -408,27 +459,56 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
   // with sc_s inside the operands, so the 8 MFMAs of the block accumulate
   // together and d, dmin apply once per block
   auto compute = [&](const MfvStep<NMAT, FMT> &w, const MfvStage<FMT> &st, f32x4 (&accr)[NMAT]) {
-    if constexpr (Q40) {
-      // Q4_0 (src/quant/mod.rs:723-745: w = d (q - 8) per 32-weight block).
-      // One MFMA per block: lane group g holds dword g of the block (its
-      // elements 8 g ..), so the block scale d applies to the MFMA's
-      // result; the codes go in unsigned (q as an fp16 subnormal, q 2^-24)
-      // and the staged block sums X take off the 8:
-      //   sum_i w_i x_i = d (2^24 sum_i (q_i 2^-24) x_i - 8 X).
-      // The loads give lane group g the 16 bytes of blocks 2 g and 2 g + 1
-      // (halves 0 and 1 of segment g); transposed across the lane groups,
-      // dword s of half h is then dword g of block 2 s + h.
-      uint32_t cq[NMAT][2][4];
+    if constexpr (BLK) {
+      // Q4_0 (src/quant/mod.rs:723-745: w = d (q - 8) per 32-weight block)
+      // and Q8_0 (src/quant/mod.rs:689-703: w = d q, q a signed byte).  One
+      // MFMA per block: lane group g holds the block's elements 8 g ..
+      // 8 g + 7, so the block scale d applies to the MFMA's result; the
+      // codes go in unsigned, q + o as an fp16 subnormal ((q + o) 2^-24,
+      // Q4_0 o = -8 + 8 from the stored q ^ 8, Q8_0 o = 128), and the staged
+      // block sums X take off the offset:
+      //   sum_i w_i x_i = d (2^24 sum_i ((q_i + o) 2^-24) x_i - o X).
+      // Q4_0: the loads give lane group g the 16 bytes of blocks 2 g and
+      // 2 g + 1 (halves 0 and 1 of segment g); transposed across the lane
+      // groups, dword s of half h is then dword g of block 2 s + h.  Q8_0:
+      // lane group g loads blocks 2 g + t (t = 0, 1) whole; the dword pairs
+      // (2 k, 2 k + 1) transposed across the lane groups, pair s of parity t
+      // is then dwords 2 g, 2 g + 1 of block 2 s + t.
+      constexpr int NW = Q80 ? 2 : 1;  // code dwords per lane and MFMA
+      uint32_t cq[NMAT][2][NW][4];
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          cq[mt][h][0] = w.q[mt][h].x;
-          cq[mt][h][1] = w.q[mt][h].y;
-          cq[mt][h][2] = w.q[mt][h].z;
-          cq[mt][h][3] = w.q[mt][h].w;
-          transpose_groups(cq[mt][h]);
+          if constexpr (Q80) {
+            const uint4 q0 = w.q[mt][2 * h], q1 = w.q[mt][2 * h + 1];  // block 2 g + h
+            const uint32_t lo[4] = {q0.x, q0.z, q1.x, q1.z}, hi[4] = {q0.y, q0.w, q1.y, q1.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              cq[mt][h][0][k] = lo[k];
+              cq[mt][h][NW - 1][k] = hi[k];
+            }
+          } else {
+            cq[mt][h][0][0] = w.q[mt][h].x;
+            cq[mt][h][0][1] = w.q[mt][h].y;
+            cq[mt][h][0][2] = w.q[mt][h].z;
+            cq[mt][h][0][3] = w.q[mt][h].w;
+          }
+#pragma unroll
+          for (int v = 0; v < NW; ++v) transpose_groups(cq[mt][h][v]);
         }
+      // Q8_0: (q ^ 0x80) = q + 128 per byte, each byte widened to 16 bits
+      // in element order: the bits of the fp16 subnormal (q + 128) 2^-24
+      auto operand8 = [](uint32_t lo, uint32_t hi) {
+        lo ^= 0x80808080u;
+        hi ^= 0x80808080u;
+        uint32_t d[4];
+        d[0] = __builtin_amdgcn_perm(lo, lo, 0x0C010C00u);
+        d[1] = __builtin_amdgcn_perm(lo, lo, 0x0C030C02u);
+        d[2] = __builtin_amdgcn_perm(hi, hi, 0x0C010C00u);
+        d[3] = __builtin_amdgcn_perm(hi, hi, 0x0C030C02u);
+        return __builtin_bit_cast(f16x8, d);
+      };
       float sx[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) sx[k] = st.sx[4 * g + k];
@@ -439,7 +519,8 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
         const float4 xs = *reinterpret_cast<const float4 *>(&st.xs[b][4 * g]);
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt) {
-          const f16x8 bq = operand(cq[mt][b & 1][b >> 1] ^ 0x88888888u, 0x00010001u);
+          const f16x8 bq = Q80 ? operand8(cq[mt][b & 1][0][b >> 1], cq[mt][b & 1][NW - 1][b >> 1])
+                               : operand(cq[mt][b & 1][0][b >> 1] ^ 0x88888888u, 0x00010001u);
           f32x4 y = f32x4{0.f, 0.f, 0.f, 0.f};
           y = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi, bq, y, 0, 0, 0);
           y = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo, bq, y, 0, 0, 0);
@@ -559,8 +640,7 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
     }
   };
 
-  // steps i = MV_KS rt + kc; ring slot i % MV_D = kc (MV_D == MV_KS)
-  static_assert(MV_D == MV_KS, "ring slots are the chunk index");
+  // steps i = MV_KS rt + kc: stage kc, ring slot i % MV_D
   float *out = a.out + (size_t)slice * a.out_split;
   // fully unrolled: ring registers carried around a loop back edge get
   // copied there, and copying a register with a load in flight waits for it
@@ -575,8 +655,8 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
       // issued unconditionally: a branch around the loads would leave the
       // compiler unsure how many are outstanding, and it would then wait
       // for all of them
-      issue(ring[(kc + MV_D - 1) % MV_D], i + MV_D - 1);
-      compute(ring[kc], stage[kc], accr);
+      issue(ring[(i + MV_D - 1) % MV_D], i + MV_D - 1);
+      compute(ring[i % MV_D], stage[kc], accr);
       __builtin_amdgcn_sched_barrier(0);
     }
     // partial sums of the slice: lane holds row (lane % 16), pairs 4g .. 4g+3
@@ -613,6 +693,17 @@ __global__ __launch_bounds__(256) void k_mfv_swiglu(const float *__restrict__ pa
   }
 }
 
+// the kernel of a pass for the experts' format
+template <bool GATEUP, int KS>
+void (*mfv_kernel(int fmt))(MfvArgs) {
+  switch (fmt) {
+  case NX_FMT_Q4_0: return k_mfv<GATEUP, KS, NX_FMT_Q4_0, mv_ring<GATEUP, NX_FMT_Q4_0>()>;
+  case NX_FMT_Q8_0: return k_mfv<GATEUP, KS, NX_FMT_Q8_0, mv_ring<GATEUP, NX_FMT_Q8_0>()>;
+  case NX_FMT_Q2_K: return k_mfv<GATEUP, KS, NX_FMT_Q2_K, mv_ring<GATEUP, NX_FMT_Q2_K>()>;
+  default: return k_mfv<GATEUP, KS, NX_FMT_Q4_K, mv_ring<GATEUP, NX_FMT_Q4_K>()>;
+  }
+}
+
 }  // namespace
 
 int mfv_max_tiles(int T, int k, int E, bool shared) {
@@ -623,17 +714,18 @@ int mfv_max_tiles(int T, int k, int E, bool shared) {
 
 bool mfv_supports(const nx_experts *ex) {
   // whole 256-weight chunks in both products: Q4_K and Q2_K always, Q4_0
-  // when H and F are multiples of 256
+  // and Q8_0 when H and F are multiples of 256
   if (ex->fmt == NX_FMT_Q4_K || ex->fmt == NX_FMT_Q2_K) return true;
-  return ex->fmt == NX_FMT_Q4_0 && ex->H % MV_K == 0 && ex->F % MV_K == 0;
+  return (ex->fmt == NX_FMT_Q4_0 || ex->fmt == NX_FMT_Q8_0) && ex->H % MV_K == 0 &&
+         ex->F % MV_K == 0;
 }
 
 int launch_mfv(nx_ctx *c, const MfvPlan &p) {
   const nx_experts *ex = p.ex;
   if (!mfv_supports(ex))
     return fail(NX_ERR_UNSUPPORTED,
-                "the split-activation MFMA path takes Q4_K and Q2_K experts, or Q4_0 experts "
-                "whose hidden and FFN widths are multiples of 256");
+                "the split-activation MFMA path takes Q4_K and Q2_K experts, or Q4_0 and Q8_0 "
+                "experts whose hidden and FFN widths are multiples of 256");
   // activation rows are read as float4 runs of whole chunks
   if (reinterpret_cast<uintptr_t>(p.x) & 15)
     return fail(NX_ERR_UNSUPPORTED, "the split-activation MFMA path needs 16-byte aligned inputs");
@@ -700,15 +792,8 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
     const dim3 grid((unsigned)((a.rows + MV_WG_ROWS - 1) / MV_WG_ROWS), (unsigned)p.max_tiles,
                     (unsigned)nks);
     if (gateup) {
-      NX_TRY(launch(c, "mfv_gateup",
-                    [&] {
-                      if (ex->fmt == NX_FMT_Q4_0)
-                        go(c, k_mfv<true, MV_KS_GATEUP, NX_FMT_Q4_0>, grid, dim3(256), 0, a);
-                      else if (ex->fmt == NX_FMT_Q2_K)
-                        go(c, k_mfv<true, MV_KS_GATEUP, NX_FMT_Q2_K>, grid, dim3(256), 0, a);
-                      else
-                        go(c, k_mfv<true, MV_KS_GATEUP, NX_FMT_Q4_K>, grid, dim3(256), 0, a);
-                    }));
+      const auto kern = mfv_kernel<true, MV_KS_GATEUP>(ex->fmt);
+      NX_TRY(launch(c, "mfv_gateup", [&] { go(c, kern, grid, dim3(256), 0, a); }));
       const size_t n = pairs * F;
       unsigned gs = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
       NX_TRY(launch(c, "mfv_swiglu", [&] {
@@ -716,15 +801,8 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
                            pairs * 2 * F, (int)pairs, F, act, F);
       }));
     } else {
-      NX_TRY(launch(c, "mfv_down",
-                    [&] {
-                      if (ex->fmt == NX_FMT_Q4_0)
-                        go(c, k_mfv<false, MV_KS_DOWN, NX_FMT_Q4_0>, grid, dim3(256), 0, a);
-                      else if (ex->fmt == NX_FMT_Q2_K)
-                        go(c, k_mfv<false, MV_KS_DOWN, NX_FMT_Q2_K>, grid, dim3(256), 0, a);
-                      else
-                        go(c, k_mfv<false, MV_KS_DOWN, NX_FMT_Q4_K>, grid, dim3(256), 0, a);
-                    }));
+      const auto kern = mfv_kernel<false, MV_KS_DOWN>(ex->fmt);
+      NX_TRY(launch(c, "mfv_down", [&] { go(c, kern, grid, dim3(256), 0, a); }));
     }
   }
   return launch_combine(c, ypart, p.rw, p.rcnt, p.inv, p.T, p.k, H, shared, p.out, nks_d,

@@ -8,16 +8,16 @@ against the oracle's dispatch (src/engine/mod.rs:969-1024) over the same
 payloads: 1 to 64 tokens, experts with more than 16 tokens (several tiles),
 top-8 routing, the sigmoid score mode, token rows of very different
 magnitudes and zero rows, Mixtral's full shape, and a shared expert as wide
-as the routed ones (one pair per token, several tiles of 16); Q4_0 experts
-whose widths are whole 256-weight chunks on the same kinds of case; other
-formats, other Q4_0 widths and shared experts of another width are rejected
-with NX_ERR_UNSUPPORTED.
+as the routed ones (one pair per token, several tiles of 16); Q4_0 and Q8_0
+experts whose widths are whole 256-weight chunks on the same kinds of case;
+other formats, other Q4_0 and Q8_0 widths and shared experts of another width
+are rejected with NX_ERR_UNSUPPORTED.
 """
 import numpy as np
 import pytest
 
 import nexus_amd as nx
-from moe_cases import Q2_K, Q4_0, Q4_K, Q8_0, Layer, rel_l2
+from moe_cases import F32, Q2_K, Q4_0, Q4_K, Q8_0, Layer, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -99,23 +99,26 @@ def test_split_mixtral_shape(ctx):
     assert rel_l2(got, L.oracle_out()) <= TOL
 
 
+@pytest.mark.parametrize("fmt", [Q4_0, Q8_0])
 @pytest.mark.parametrize("E,H,F,k,T,Fs,score", [
     (8, 512, 1024, 2, 1, 0, 0), (8, 256, 768, 2, 33, 0, 0), (32, 512, 256, 8, 24, 0, 1),
     (16, 1024, 512, 4, 64, 0, 0), (16, 512, 512, 4, 8, 512, 1), (8, 256, 768, 2, 40, 768, 0)])
-def test_split_parity_q4_0(ctx, E, H, F, k, T, Fs, score):
+def test_split_parity_block_formats(ctx, fmt, E, H, F, k, T, Fs, score):
     """Q4_0 experts (w = d (q - 8) per 32-weight block, src/quant/mod.rs:
-    723-745) on the split path: one MFMA per block with the unsigned codes,
-    the block sums of the staged activations taking off the 8."""
-    print(f"mfma split q4_0 E={E} H={H} F={F} k={k} T={T} Fs={Fs} score={score}", flush=True)
-    L = Layer(Q4_0, E, H, F, k, T, seed=E * 3 + H + F + T, shared_F=Fs, score_mode=score)
+    723-745) and Q8_0 experts (w = d q, q a signed byte, :689-703) on the
+    split path: one MFMA per block with the codes made unsigned, the block
+    sums of the staged activations taking off the offset (8, 128)."""
+    print(f"mfma split fmt={fmt} E={E} H={H} F={F} k={k} T={T} Fs={Fs} score={score}", flush=True)
+    L = Layer(fmt, E, H, F, k, T, seed=E * 3 + H + F + T + fmt, shared_F=Fs, score_mode=score)
     ex = L.upload(nx, ctx)
     got = ex.forward(L.x, L.logits, k, score, nx.PATH_MFMA_SPLIT)
     ex.close()
     assert rel_l2(got, L.oracle_out()) <= TOL
 
 
-def test_split_q4_0_magnitudes_and_mixtral_shape(ctx):
-    L = Layer(Q4_0, 8, 512, 512, 2, 12, seed=43)
+@pytest.mark.parametrize("fmt", [Q4_0, Q8_0])
+def test_split_block_formats_magnitudes_and_mixtral_shape(ctx, fmt):
+    L = Layer(fmt, 8, 512, 512, 2, 12, seed=43 + fmt)
     scale = np.array([1e-30, 1e-6, 1.0, 3e3, 1e6, 0.0, 1.0, 1e-3, 7.0, 0.0, 1e4, 1e-2],
                      np.float32)[:, None]
     L.x = (L.x * scale).astype(np.float32)
@@ -130,7 +133,7 @@ def test_split_q4_0_magnitudes_and_mixtral_shape(ctx):
             assert np.all(got[t] == 0)
         else:
             assert rel_l2(got[t], ref[t]) <= TOL, t
-    M = Layer(Q4_0, 8, 4096, 14336, 2, 8, seed=10)
+    M = Layer(fmt, 8, 4096, 14336, 2, 8, seed=10 + fmt)
     ex = M.upload(nx, ctx)
     got = ex.forward(M.x, M.logits, 2, 0, nx.PATH_MFMA_SPLIT)
     ex.close()
@@ -138,14 +141,15 @@ def test_split_q4_0_magnitudes_and_mixtral_shape(ctx):
 
 
 def test_split_rejects(ctx):
-    L = Layer(Q8_0, 4, 256, 256, 2, 4, seed=3)
+    L = Layer(F32, 4, 256, 256, 2, 4, seed=3)
     ex = L.upload(nx, ctx)
     with pytest.raises(nx.NexusError) as ei:
         ex.forward(L.x, L.logits, 2, 0, nx.PATH_MFMA_SPLIT)
     assert ei.value.code == nx.NX_ERR_UNSUPPORTED
     ex.close()
-    for H, F in ((288, 256), (256, 224)):  # Q4_0 widths that are not whole 256-weight chunks
-        Q = Layer(Q4_0, 4, H, F, 2, 4, seed=5)
+    # Q4_0 and Q8_0 widths that are not whole 256-weight chunks
+    for fmt, H, F in ((Q4_0, 288, 256), (Q4_0, 256, 224), (Q8_0, 288, 256), (Q8_0, 256, 224)):
+        Q = Layer(fmt, 4, H, F, 2, 4, seed=5)
         ex = Q.upload(nx, ctx)
         with pytest.raises(nx.NexusError) as ei:
             ex.forward(Q.x, Q.logits, 2, 0, nx.PATH_MFMA_SPLIT)
@@ -177,7 +181,9 @@ def test_auto_path_choice(ctx, E, H, F, k, T, want):
 
 @pytest.mark.parametrize("fmt,E,H,F,k,T,shared,want", [
     (Q8_0, 8, 512, 1024, 2, 8, 0, nx.PATH_GEMV),        # 2 tokens per expert
-    (Q8_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_BF16),  # 4
+    (Q8_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_SPLIT),  # 4
+    (Q8_0, 8, 512, 1024, 2, 64, 0, nx.PATH_MFMA_BF16),   # 16
+    (Q8_0, 8, 288, 1024, 2, 16, 0, nx.PATH_MFMA_BF16),   # H not whole 256-weight chunks
     (Q4_0, 8, 512, 1024, 2, 4, 0, nx.PATH_GEMV),         # 1 token per expert
     (Q4_0, 8, 512, 1024, 2, 16, 0, nx.PATH_MFMA_SPLIT),  # 4
     (Q4_0, 8, 512, 1024, 2, 64, 0, nx.PATH_MFMA_BF16),   # 16
@@ -199,8 +205,8 @@ def test_auto_path_choice(ctx, E, H, F, k, T, want):
 def test_auto_path_choice_other(ctx, fmt, E, H, F, k, T, shared, want):
     """AUTO for formats other than Q4_K and for layers with a shared expert:
     the grouped GEMM from ~3 tokens per routed expert, or from 6 tokens with
-    a shared expert, the GEMV below; Q4_0 without a shared expert, in whole
-    256-weight chunks, follows Q4_K's rule (split path from ~3 tokens per
+    a shared expert, the GEMV below; Q4_0 and Q8_0 without a shared expert,
+    in whole 256-weight chunks, follow Q4_K's rule (split path from ~3 tokens per
     expert up to 12); Q2_K takes the split path from ~1.8 tokens per expert
     (or 4 tokens with a shared expert as wide as the routed ones), the GEMV
     below; Q4_K with a shared expert as wide as the routed ones
