@@ -6,15 +6,15 @@ from the library's static scratch array instead of context workspace.  The
 outputs must be bit-identical on two calls in a row, the second with fewer
 tokens (so stale scratch contents from the first call are present), on every
 path the dispatcher has: the one-token GEMV with the router inside the gate/up
-kernel, the decode-batch GEMV, the split-activation MFMA path and the grouped
-GEMM, with and without a shared expert.  Calls whose intermediates do not fit
+kernel, the decode-batch GEMV, the split-activation MFMA path (Q4_K, Q4_0,
+Q8_0, Q2_K) and the grouped GEMM, with and without a shared expert.  Calls whose intermediates do not fit
 the array fail with NX_ERR_UNSUPPORTED and leave the output untouched.
 """
 import numpy as np
 import pytest
 
 import nexus_amd as nx
-from moe_cases import Q4_K, Q8_0, DeviceArray, Layer, assert_same_bits
+from moe_cases import Q2_K, Q4_0, Q4_K, Q8_0, DeviceArray, Layer, assert_same_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -49,6 +49,10 @@ CASES = [
     (Q4_K, 16, 512, 512, 4, 512, 1, nx.PATH_MFMA_BF16, (200, 33)),
     (Q4_K, 16, 512, 512, 4, 512, 1, nx.PATH_GEMV, (1, 1)),
     (Q8_0, 8, 512, 1024, 2, 0, 0, nx.PATH_AUTO, (40, 1)),
+    (Q4_0, 8, 512, 1024, 2, 0, 0, nx.PATH_MFMA_SPLIT, (24, 5)),
+    (Q8_0, 8, 512, 1024, 2, 0, 0, nx.PATH_MFMA_SPLIT, (24, 5)),
+    (Q2_K, 8, 512, 1024, 2, 0, 0, nx.PATH_MFMA_SPLIT, (24, 5)),
+    (Q2_K, 16, 512, 512, 4, 512, 1, nx.PATH_MFMA_SPLIT, (12, 4)),
 ]
 
 
