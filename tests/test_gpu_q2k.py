@@ -114,6 +114,25 @@ def test_q2k_split_magnitudes_and_mixtral_shape(ctx):
     assert rel_l2(got, M.oracle_out()) <= GEMV_TOL
 
 
+def test_q2k_prefill_size_split_matches_gemv(ctx):
+    """Q2_K has no grouped GEMM, so prefill-sized batches run on the split
+    path (here 512 tokens at Mixtral's shape: 1024 pairs in 64+ tiles, K-slice
+    partial sums of ~235 MB): every row within 2e-4 of the GEMV's (each path
+    is within 1e-4 of the oracle at this shape with 8 tokens, above)."""
+    T = 512
+    print(f"q2k split vs gemv, Mixtral shape, T={T}", flush=True)
+    L = Layer(Q2_K, 8, 4096, 14336, 2, T, seed=12, experts_needed=[])
+    ex = L.upload(nx, ctx)
+    split = ex.forward(L.x, L.logits, 2, 0, nx.PATH_MFMA_SPLIT)
+    gemv = ex.forward(L.x, L.logits, 2, 0, nx.PATH_GEMV)
+    auto = ex.forward(L.x, L.logits, 2, 0, nx.PATH_AUTO)
+    ex.close()
+    assert np.isfinite(split).all()
+    worst = max(rel_l2(split[t], gemv[t]) for t in range(T))
+    assert worst <= 2 * GEMV_TOL, worst
+    assert_same_bits(auto, split)
+
+
 def test_q2k_rejects_mfma(ctx):
     L = Layer(Q2_K, 4, 256, 256, 2, 4, seed=3)
     ex = L.upload(nx, ctx)
