@@ -35,6 +35,8 @@
 //   k_logits_dot     fast, few tokens.  A workgroup per (expert, block of
 //                    tokens) strides over the row in 16-byte loads and reduces
 //                    with DPP and LDS.
+//   k_logits_rows8   fast, more tokens, at most 8 experts: W in registers,
+//                    the token rows streamed once.
 //   k_logits_mfma    fast, more tokens: f32 MFMA tiles of tokens x experts.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
@@ -632,6 +634,82 @@ __global__ __launch_bounds__(256) void k_logits_dot(const float *__restrict__ W,
   }
 }
 
+// Fast mode, many tokens, at most 8 experts and rows of at most 4 NJ x 256
+// columns: a workgroup holds W in registers (thread t: columns 4 (t + 256 j)
+// .. + 3 of every expert row, j < NJ; absent experts and columns as zeros)
+// and streams the rows of its tokens t0 .. t0 + tpw - 1, the next token's row
+// loaded while the current one is multiplied.  Per token each thread forms
+// 8 partial dots; the wave reduces them by halving exchanges (lane bit 5,
+// then 4, then 3: each step sends the half of its values it drops and adds
+// the partner's half of those it keeps), leaving lane l with expert
+// 4 b5 + 2 b4 + b3 summed over the lanes that share those bits, which three
+// more exchanges complete; the four waves add through LDS at the end.
+template <int NJ>
+__global__ __launch_bounds__(256) void k_logits_rows8(const float *__restrict__ W,
+                                                      const float *__restrict__ X, int T, int E,
+                                                      int H, int tpw, float *__restrict__ out) {
+  constexpr int MAXT = 16;  // tokens per workgroup at most
+  __shared__ float part[MAXT][4][8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const auto rw = make_rsrc(W, (uint32_t)((size_t)E * H * 4));
+  const auto rx = make_rsrc(X, (uint32_t)((size_t)T * H * 4));
+  float w[8][NJ][4];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const F4 v = load_cols<true>(rw, (uint32_t)(e < E ? e : 0) * (uint32_t)H * 4u,
+                                   4 * (tid + 256 * j), H, e < E);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[e][j][i] = v.v[i];
+    }
+  const int t0 = (int)blockIdx.x * tpw;
+  const int nt = min(tpw, T - t0);
+  auto load_row = [&](int t, F4 (&xr)[NJ]) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      xr[j] = load_cols<true>(rx, (uint32_t)(t < T ? t : 0) * (uint32_t)H * 4u,
+                              4 * (tid + 256 * j), H, t < T);
+  };
+  F4 xa[NJ], xb[NJ];
+  load_row(t0, xa);
+  for (int b = 0; b < nt; ++b) {
+    load_row(t0 + b + 1 < t0 + nt ? t0 + b + 1 : T, xb);  // the next row (past the end: zeros)
+    float s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = __builtin_fmaf(w[e][j][i], xa[j].v[i], acc);
+      s[e] = acc;
+    }
+    // halving exchanges over lane bits 5, 4, 3: 8 -> 4 -> 2 -> 1 values
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+    float s4[4], s2[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      s4[i] = (b5 ? s[4 + i] : s[i]) + __shfl_xor(b5 ? s[i] : s[4 + i], 32, 64);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      s2[i] = (b4 ? s4[2 + i] : s4[i]) + __shfl_xor(b4 ? s4[i] : s4[2 + i], 16, 64);
+    float v = (b3 ? s2[1] : s2[0]) + __shfl_xor(b3 ? s2[0] : s2[1], 8, 64);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 1, 64);
+    if ((lane & 7) == 0) part[b][wave][lane >> 3] = v;  // expert 4 b5 + 2 b4 + b3
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) xa[j] = xb[j];
+  }
+  __syncthreads();
+  if (tid < nt * 8) {
+    const int b = tid >> 3, e = tid & 7;
+    if (e < E)
+      out[(size_t)(t0 + b) * E + e] = (part[b][0][e] + part[b][1][e]) + (part[b][2][e] + part[b][3][e]);
+  }
+}
+
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // Fast mode, many tokens, on the matrix cores (v_mfma_f32_16x16x4_f32, f32
@@ -797,6 +875,18 @@ int launch_router_logits(nx_ctx *c, const float *d_w, const float *d_x, int T, i
       if (bt == 1) go(c, k_logits_dot<1, true>, dim3(grid), dim3(256), 0, d_w, d_x, T, E, H, d_out);
       else if (bt == 4) go(c, k_logits_dot<4, true>, dim3(grid), dim3(256), 0, d_w, d_x, T, E, H, d_out);
       else go(c, k_logits_dot<8, true>, dim3(grid), dim3(256), 0, d_w, d_x, T, E, H, d_out);
+    });
+  }
+  if (!exact && vec && E <= 8 && H <= 4096 && (size_t)T * H * 4 < (1u << 31)) {
+    // fast mode, more than a few tokens, at most 8 experts: W in registers,
+    // the token rows streamed once (Mixtral at 2048 tokens on the MFMA tiles
+    // below: 14.4 us, 128 workgroups of 16-token tiles half empty)
+    const int tpw = (int)std::min<long>(16, std::max<long>(1, (T + c->num_cu - 1) / c->num_cu));
+    const dim3 grid((unsigned)((T + tpw - 1) / tpw));
+    return launch(c, "router_logits_rows8", [&] {
+      if (H <= 1024) go(c, k_logits_rows8<1>, grid, dim3(256), 0, d_w, d_x, T, E, H, tpw, d_out);
+      else if (H <= 2048) go(c, k_logits_rows8<2>, grid, dim3(256), 0, d_w, d_x, T, E, H, tpw, d_out);
+      else go(c, k_logits_rows8<4>, grid, dim3(256), 0, d_w, d_x, T, E, H, tpw, d_out);
     });
   }
   if (!exact && (size_t)T * H * 4 < (1u << 31) && (size_t)E * H * 4 < (1u << 31)) {

@@ -8,7 +8,8 @@ for any two summation orders of the same rounded-or-fused products.  The
 shapes cover every kernel the dispatcher picks: eight-lane chains (few
 chains, rows not a multiple of 4 floats, unaligned device pointers), LDS tiles
 with 1x1, 2x2 and 4x4 chains per lane (partial tiles in tokens, experts and
-columns), and the fast workgroup dot product.
+columns), the fast workgroup dot product, the fast register-held weights for
+at most 8 experts, and the fast f32 MFMA tiles.
 """
 import numpy as np
 import pytest
@@ -121,7 +122,9 @@ def test_exact_special_values(ctx):
 FAST_SHAPES = [(1, 8, 4096), (1, 256, 7168), (3, 128, 2048), (8, 60, 2880), (2, 7, 1001),
                (64, 256, 512), (2100, 8, 256), (4096, 128, 256), (9, 8, 4096), (50, 5, 100),
                (1000, 40, 1000), (8200, 250, 72), (1030, 256, 7168), (32, 8, 4096),
-               (27, 128, 2048), (33, 9, 4096)]
+               (27, 128, 2048), (33, 9, 4096),
+               # at most 8 experts from 33 tokens: W held in registers, rows streamed
+               (2048, 8, 4096), (40, 3, 1536), (100, 8, 4000), (4097, 1, 2048), (300, 8, 1024)]
 
 
 @pytest.mark.parametrize("T,E,H", FAST_SHAPES)
