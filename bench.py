@@ -60,7 +60,7 @@ def parse():
                    help="run one workload alone and print its record (for profilers): "
                         "decode, prefill, block, router, dense, or a model shape "
                         "NAME[:T<tokens>] (qwen3_q4k, deepseek_q4k_sigmoid_shared, mixtral_q2k, "
-                        "mixtral_q4_0)")
+                        "mixtral_q4_0, mixtral_q8_0)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="run one device-to-device copy of this size first (calibrates HBM "
                         "byte counters under rocprofv3 --pmc)")
@@ -348,6 +348,7 @@ MODEL_CONFIGS = [
     ("deepseek_q4k_sigmoid_shared", "Q4_K", 256, 7168, 2048, 8, 2048, 1, (1, 4096), 2),
     ("mixtral_q2k", "Q2_K", 8, 4096, 14336, 2, 0, 0, (1, 32), 4),
     ("mixtral_q4_0", "Q4_0", 8, 4096, 14336, 2, 0, 0, (1, 32), 4),
+    ("mixtral_q8_0", "Q8_0", 8, 4096, 14336, 2, 0, 0, (1, 32), 2),
 ]
 
 
@@ -468,7 +469,7 @@ def router_cases(nx, ctx, torch, args):
 
 def model_config_cases(nx, ctx, torch, args, only=None):
     """The other model shapes of the hot-path survey (AUTO path; Q4_K experts,
-    and Mixtral's shape on Q2_K and Q4_0):
+    and Mixtral's shape on Q2_K, Q4_0 and Q8_0):
     per token count, ms/step and the fraction of HBM and dense-fp16 MFMA peak
     on algorithmic bytes / FLOPs (realised routing).  Replicas are rotated so
     that decode steps read HBM rather than the Infinity Cache."""
@@ -481,12 +482,14 @@ def model_config_cases(nx, ctx, torch, args, only=None):
             if only[1] is not None:
                 tokens = (only[1],)
         print(f"bench: {name}", file=sys.stderr, flush=True)
-        fmt = {"Q4_K": nx.Q4_K, "Q2_K": nx.Q2_K, "Q4_0": nx.Q4_0}[fname]
+        fmt = {"Q4_K": nx.Q4_K, "Q2_K": nx.Q2_K, "Q4_0": nx.Q4_0, "Q8_0": nx.Q8_0}[fname]
         # GGUF bytes per weight; Q2_K stays resident as 16 bytes of 2-bit
         # codes and 8 scale-plane bytes per 64 weights (0.375 B/weight read
         # per step)
-        bpw = {"Q4_K": Q4K_BYTES_PER_WEIGHT, "Q2_K": 84.0 / 256.0, "Q4_0": 18.0 / 32.0}[fname]
-        rbpw = {"Q4_K": Q4K_BYTES_PER_WEIGHT, "Q2_K": 0.375, "Q4_0": 18.0 / 32.0}[fname]
+        bpw = {"Q4_K": Q4K_BYTES_PER_WEIGHT, "Q2_K": 84.0 / 256.0, "Q4_0": 18.0 / 32.0,
+               "Q8_0": 34.0 / 32.0}[fname]
+        rbpw = {"Q4_K": Q4K_BYTES_PER_WEIGHT, "Q2_K": 0.375, "Q4_0": 18.0 / 32.0,
+                "Q8_0": 34.0 / 32.0}[fname]
         sets = make_expert_sets(nx, ctx, torch, fmt, E, H, F, reps, args.seed + 31, Fs)
         g = torch.Generator(device=dev)
         g.manual_seed(args.seed + 41)
