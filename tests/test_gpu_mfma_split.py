@@ -140,6 +140,38 @@ def test_split_block_formats_magnitudes_and_mixtral_shape(ctx, fmt):
     assert rel_l2(got, M.oracle_out()) <= TOL
 
 
+def _sweep_cases(n=16, seed=2026):
+    """Seeded random split-path layers: every format, widths in whole
+    256-weight chunks (1 to 6 chunks, so K slices of 1 to 4 chunks and
+    partial last slices), 2 to 40 experts, top-1 to top-8, 1 to 70 tokens,
+    with and without a shared expert, both score modes."""
+    rng = np.random.default_rng(seed)
+    fmts = [Q4_K, Q4_0, Q8_0, Q2_K]
+    out = []
+    for i in range(n):
+        fmt = fmts[i % 4]
+        E = int(rng.integers(2, 41))
+        k = int(rng.integers(1, min(8, E) + 1))
+        H = 256 * int(rng.integers(1, 7))
+        F = 256 * int(rng.integers(1, 7))
+        T = int(rng.integers(1, 71))
+        Fs = F if rng.random() < 0.3 else 0
+        out.append((fmt, E, H, F, k, T, Fs, int(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("case", _sweep_cases(), ids=lambda c: "-".join(map(str, c)))
+def test_split_random_shapes(ctx, case):
+    fmt, E, H, F, k, T, Fs, score = case
+    print(f"mfma split sweep fmt={fmt} E={E} H={H} F={F} k={k} T={T} Fs={Fs} score={score}",
+          flush=True)
+    L = Layer(fmt, E, H, F, k, T, seed=E + H + F + T + fmt, shared_F=Fs, score_mode=score)
+    ex = L.upload(nx, ctx)
+    got = ex.forward(L.x, L.logits, k, score, nx.PATH_MFMA_SPLIT)
+    ex.close()
+    assert rel_l2(got, L.oracle_out()) <= TOL
+
+
 def test_split_rejects(ctx):
     L = Layer(F32, 4, 256, 256, 2, 4, seed=3)
     ex = L.upload(nx, ctx)
