@@ -18,6 +18,8 @@
 // conversion.  With the 6-bit scale inside the operands, one
 // v_mfma_f32_16x16x32_f16 may span several sub-blocks, so the 8 MFMAs of a
 // block accumulate together; d 2^24 and the dmin term apply once per block.
+// sum_s m_s X_s is one more MFMA per block, on the pairs' staged sub-block
+// sums X_s and the row's 6-bit mins.
 //
 // Activations keep close to fp32 precision: per pair and 256-element chunk
 // they are scaled by a power of two so the chunk maximum lies in
@@ -29,12 +31,14 @@
 // Work: a workgroup of 4 waves owns one tile of up to 16 pairs of one
 // expert (the permutation's tile list with tile_m = 16), 256 weight rows
 // (of both matrices for gate/up) and one K slice of 4 (gate/up) or 3 (down)
-// chunks (a chunk is one Q4_K block, 256 positions); wave w streams 64 of
-// the rows as 4 row tiles of 16.  The slice's activations of the tile's
-// pairs are staged once into LDS in MFMA operand layout, with each pair's
-// unscale factor; the codes and scales of the next 3 (gate/up) or 2 (down)
-// (row tile, chunk) steps are in flight while a step is computed.  Slices write partial sums, which the SwiGLU
-// kernel (gate/up) and the weighted combine (down) add in slice order.
+// chunks (a chunk is 256 positions: one Q4_K or Q2_K block, 8 Q4_0 or
+// Q8_0 blocks); wave w streams 64 of the rows as 4 row tiles of 16.  The
+// slice's activations of the tile's pairs are staged once into LDS in MFMA
+// operand layout, with each pair's unscale factor and block or sub-block
+// sums; the codes and scales of the next 3 (gate/up; Q8_0's 2) or 2 (down)
+// (row tile, chunk) steps are in flight while a step is computed.  Slices
+// write partial sums, which the SwiGLU kernel (gate/up) and the weighted
+// combine (down) add in slice order.
 //
 // Q4_0 (w_i = d (q_i - 8) per 32-weight block, src/quant/mod.rs:723-745)
 // runs the same kernel on chunks of 8 blocks: one MFMA pair per block, the
@@ -51,7 +55,8 @@
 // src/quant/mod.rs:913-937): a chunk is one block, its 4 resident segments
 // (64 weights in 16 bytes) one per lane group; MFMA u takes dword u % 4 of
 // half u / 4, 8 weights of sub-block 4 g + u / 2, whose scale goes into the
-// operands (q sc <= 45) and whose min into the min operands, as for Q4_K.
+// operands (q sc <= 45); the min term is one MFMA per chunk on the 16
+// sub-block sums, as for Q4_K.
 #include "nx_device.hpp"
 #include "nx_internal.hpp"
 
@@ -64,7 +69,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int MV_M = 16;   // pairs per tile
-constexpr int MV_K = 256;  // K positions per chunk (one Q4_K block)
+constexpr int MV_K = 256;  // K positions per chunk
 
 struct MfvArgs {
   const uint8_t *qs0, *qs1, *meta0, *meta1;  // role planes (gate, up) or (down, -)
@@ -163,11 +168,11 @@ struct MfvStep<NMAT, NX_FMT_Q2_K> {
 // MV_KS chunks).  Prologue: the slice's activations of the tile's pairs are
 // staged once into LDS (one barrier).  Then wave w streams rows
 // 64 w .. 64 w + 63 of the block as 4 row tiles x MV_KS chunks (16 or 12 steps),
-// with the codes of the next MV_D steps in flight.  Each workgroup writes
+// with the codes of the next MV_D - 1 steps in flight.  Each workgroup writes
 // its slice's partial sums: gate/up to part[slice][pair][2][F] (gate, then
 // up), down to part[slice][pair][H].
-// chunks per K slice: four for gate/up; three for down, whose 48 KB stage
-// and 112 VGPRs then fit three workgroups on a CU (Mixtral 32 tokens: down
+// chunks per K slice: four for gate/up; three for down, whose 48-50 KB stage
+// and at most 155 VGPRs then fit three workgroups on a CU (Mixtral 32 tokens: down
 // 83 -> 80 us; 64 tokens 116 -> 109 us; two chunks, four workgroups per
 // CU, gained no more and added combine work)
 constexpr int MV_KS_GATEUP = 4, MV_KS_DOWN = 3;
