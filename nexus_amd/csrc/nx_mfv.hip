@@ -35,10 +35,10 @@
 // Q8_0 blocks); wave w streams 64 of the rows as 4 row tiles of 16.  The
 // slice's activations of the tile's pairs are staged once into LDS in MFMA
 // operand layout, with each pair's unscale factor and block or sub-block
-// sums; the codes and scales of the next 3 (gate/up; Q8_0's 2) or 2 (down)
-// (row tile, chunk) steps are in flight while a step is computed.  Slices
-// write partial sums, which the SwiGLU kernel (gate/up) and the weighted
-// combine (down) add in slice order.
+// sums; the codes and scales of the next 3 (row tile, chunk) steps (Q8_0:
+// 2) are in flight while a step is computed.  Slices write partial sums,
+// which the SwiGLU kernel (gate/up) and the weighted combine (down) add in
+// slice order.
 //
 // Q4_0 (w_i = d (q_i - 8) per 32-weight block, src/quant/mod.rs:723-745)
 // runs the same kernel on chunks of 8 blocks: one MFMA pair per block, the
@@ -176,12 +176,16 @@ struct MfvStep<NMAT, NX_FMT_Q2_K> {
 // 83 -> 80 us; 64 tokens 116 -> 109 us; two chunks, four workgroups per
 // CU, gained no more and added combine work)
 constexpr int MV_KS_GATEUP = 4, MV_KS_DOWN = 3;
-// steps in flight + 1: one per chunk of the slice, but for Q8_0's gate/up
-// pass, whose steps carry twice the code bytes (two steps in flight, for
-// the registers)
+// steps in flight + 1: gate/up one per chunk of the slice, but Q8_0,
+// whose steps carry twice the code bytes (two steps in flight, for the
+// registers); down one more than its slice's chunks (three steps in flight
+// at 134-150 VGPRs, still three workgroups per CU: Mixtral 32 tokens down
+// 78.4 -> 76.9 us, 64 tokens 94.9 -> 93.1 us; gate/up with four in flight
+// was slower, 144 -> 146 us), Q8_0 as many (four slots spill)
 template <bool GATEUP, int FMT>
 constexpr int mv_ring() {
-  return GATEUP ? (FMT == NX_FMT_Q8_0 ? 3 : MV_KS_GATEUP) : MV_KS_DOWN;
+  if constexpr (GATEUP) return FMT == NX_FMT_Q8_0 ? 3 : MV_KS_GATEUP;
+  return FMT == NX_FMT_Q8_0 ? MV_KS_DOWN : MV_KS_DOWN + 1;
 }
 constexpr int MV_RTW = 4;  // row tiles per wave
 constexpr int MV_WG_ROWS = 4 * 16 * MV_RTW;
