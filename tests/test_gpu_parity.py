@@ -259,6 +259,50 @@ def test_layer_mfma_parity(ctx, path, fmt, E, H, F, k, T, zipf):
     assert err <= MFMA_TOL, err
 
 
+def _layer_sweep(n=12, seed=4242):
+    """Seeded random layers: F32, Q8_0, Q4_0 and Q4_K experts at widths in
+    whole blocks (F32 also odd widths), 2 to 48 experts, top-1 to top-8, 1 to
+    200 tokens, with and without a shared expert (of its own width), both
+    score modes."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        fmt = (F32, Q8_0, Q4_0, Q4_K)[i % 4]
+        blk = {F32: 1, Q8_0: 32, Q4_0: 32, Q4_K: 256}[fmt]
+        unit = 256 if fmt == Q4_K else 32
+        H = int(rng.integers(1, 768 // unit + 1)) * unit
+        F = int(rng.integers(1, 768 // unit + 1)) * unit
+        if fmt == F32 and i % 8 == 0:
+            H, F = H + 3, F + 5  # rows not a multiple of 4 floats
+        E = int(rng.integers(2, 49))
+        k = int(rng.integers(1, min(8, E) + 1))
+        T = int(rng.integers(1, 201))
+        Fs = int(rng.integers(1, 768 // unit + 1)) * unit if rng.random() < 0.3 else 0
+        assert H % blk == 0 and F % blk == 0
+        out.append((fmt, E, H, F, k, T, Fs, int(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("case", _layer_sweep(), ids=lambda c: "-".join(map(str, c)))
+def test_layer_random_shapes(ctx, case):
+    """GEMV (1e-4), bf16 grouped GEMM (1e-2) and AUTO (1e-2: any of its
+    paths) against the oracle's dispatch on the same random layer."""
+    fmt, E, H, F, k, T, Fs, score = case
+    say(f"layer sweep fmt={fmt} E={E} H={H} F={F} k={k} T={T} Fs={Fs} score={score}")
+    L = Layer(fmt, E, H, F, k, T, seed=E + H + F + T + fmt, shared_F=Fs, score_mode=score)
+    ref = L.oracle_out()
+    ex = L.upload(nx, ctx)
+    try:
+        for path, tol in ((nx.PATH_GEMV, GEMV_TOL), (nx.PATH_MFMA_BF16, MFMA_TOL),
+                          (nx.PATH_AUTO, MFMA_TOL)):
+            got = ex.forward(L.x, L.logits, k, score, path)
+            err = rel_l2(got, ref)
+            say(f"  path {path}: rel L2 = {err:.2e}")
+            assert err <= tol, (path, err)
+    finally:
+        ex.close()
+
+
 def test_layer_mfma_shared_expert_sigmoid(ctx):
     # 24 pairs per routed expert: 64-pair M-tiles, the shared expert's 96
     # tokens over two of them
