@@ -88,6 +88,8 @@ struct MfvArgs {
   float *out;                 // partial sums: [slice][pair][out_stride]
   int out_stride;             // gate/up: 2 F (gate rows, then up rows); down: H
   size_t out_split;           // floats between slices
+  int nrb, ntiles_g, nks;     // grid: row blocks, tile bound, K slices
+  int xcd_pairs;              // 1: the 1-D slice-pair grid below, 0: (row block, tile, slice)
 };
 
 // LDS area of one chunk: the A operands (hi, lo) of the 8 MFMAs in lane
@@ -205,7 +207,24 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tile = blockIdx.y;
+  int tile, rb, slice;
+  if (a.xcd_pairs) {
+    // 1-D grid: workgroup L runs on XCD L % 8, and an XCD's consecutive
+    // workgroups take the two K slices of one (row block, tile) item, so the
+    // 128-byte scale lines the two slices share are read through one L2 at
+    // about the same time
+    const int L = (int)blockIdx.x, xcd = L & 7, j = L >> 3;
+    const long it = (long)(j >> 1) * 8 + xcd;
+    rb = (int)(it % a.nrb);
+    const long r2 = it / a.nrb;
+    tile = (int)(r2 % a.ntiles_g);
+    slice = 2 * (int)(r2 / a.ntiles_g) + (j & 1);
+    if (slice >= a.nks) return;  // workgroup-uniform (items past the last)
+  } else {
+    tile = blockIdx.y;
+    rb = blockIdx.x;
+    slice = blockIdx.z;
+  }
   if (tile >= a.tiles[0]) return;  // workgroup-uniform
   // tile t: expert tiles[2 + 2t] (E: the shared expert), first pair
   // tiles[3 + 2t] within the expert.  These and the expert's offsets are
@@ -218,9 +237,8 @@ __global__ __launch_bounds__(256, MV_KS == 3 ? 3 : 2) void k_mfv(const MfvArgs a
   const int pair0 = __builtin_amdgcn_readfirstlane(routed ? a.offsets[e] + m0 : a.T * a.k + m0);
   const int cnt = __builtin_amdgcn_readfirstlane(
       min(MV_M, routed ? a.offsets[e + 1] - pair0 : a.T - m0));
-  const int slice = blockIdx.z;
   const int c0 = slice * MV_KS;  // first chunk of the slice
-  const int row_base = blockIdx.x * MV_WG_ROWS + wave * 16 * MV_RTW;
+  const int row_base = rb * MV_WG_ROWS + wave * 16 * MV_RTW;
 
   // ---- weights: lane holds row (lane % 16) of each row tile and K group
   // (lane / 16) of every sub-block
@@ -798,8 +816,18 @@ int launch_mfv(nx_ctx *c, const MfvPlan &p) {
       a.out_split = pairs * H;
     }
     const int nks = gateup ? nks_g : nks_d;
-    const dim3 grid((unsigned)((a.rows + MV_WG_ROWS - 1) / MV_WG_ROWS), (unsigned)p.max_tiles,
-                    (unsigned)nks);
+    a.nrb = (a.rows + MV_WG_ROWS - 1) / MV_WG_ROWS;
+    a.ntiles_g = p.max_tiles;
+    a.nks = nks;
+    // slice pairs on one XCD where a 128-byte scale line spans two slices
+    // (16 scale bytes per chunk: Q4_K, Q4_0, Q8_0) and the slices pair up
+    // (Qwen3 64 tokens 125 -> 120 us, Mixtral 32 tokens 245.5 -> 243.3 us;
+    // with an odd count the unpaired slices' idle workgroups cost more than
+    // the sharing gains: DeepSeek's 7 gate/up slices 459 -> 488 us)
+    a.xcd_pairs = gateup && nks % 2 == 0 && ex->fmt != NX_FMT_Q2_K ? 1 : 0;
+    const long items = (long)a.nrb * a.ntiles_g * (nks / 2);
+    const dim3 grid = a.xcd_pairs ? dim3((unsigned)(16 * ((items + 7) / 8)))
+                                  : dim3((unsigned)a.nrb, (unsigned)p.max_tiles, (unsigned)nks);
     if (gateup) {
       const auto kern = mfv_kernel<true, MV_KS_GATEUP>(ex->fmt);
       NX_TRY(launch(c, "mfv_gateup", [&] { go(c, kern, grid, dim3(256), 0, a); }));
