@@ -64,10 +64,6 @@
 #ifndef NX_GEMV_COMBINE_SLOTS
 #define NX_GEMV_COMBINE_SLOTS 2
 #endif
-// rows of a workgroup's run interleaved over its row groups (see k_gemv_gateup)
-#ifndef NX_GEMV_WG_INTERLEAVE
-#define NX_GEMV_WG_INTERLEAVE 1
-#endif
 // cache policy of the weight-code loads (2: non-temporal, streamed past the
 // caches so the small activation and route arrays stay resident)
 #ifndef NX_GEMV_WEIGHT_CPOL
@@ -627,18 +623,12 @@ __global__ __launch_bounds__(256, 2) void k_gemv_gateup(const GemvArgs a) {
 
   const SlotView v = slot_view(a, slot, n_active, active, offsets, e_one);
   // this group's logical rows 0 .. nq-1: the workgroup owns one contiguous
-  // run of GROUPS * rpg rows; interleaved, its row groups take every
-  // GROUPS-th row of it (row = run start + q * GROUPS + group), so that at
-  // each stage the waves read neighbouring rows, else one run of rpg rows each
-#if NX_GEMV_WG_INTERLEAVE
+  // run of GROUPS * rpg rows, and its row groups take every GROUPS-th row of
+  // it (row = run start + q * GROUPS + group), so that at each stage the
+  // waves read neighbouring rows
   const int wg0 = bx * GROUPS * rpg;
   const RowMap rm{wg0 + grp, GROUPS, min(v.rows, wg0 + GROUPS * rpg)};
   const int nq = rm.end > rm.base ? (rm.end - rm.base + GROUPS - 1) / GROUPS : 0;
-#else
-  const int gidx = bx * GROUPS + grp;
-  const RowMap rm{gidx * rpg, 1, min(v.rows, gidx * rpg + rpg)};
-  const int nq = max(0, rm.end - rm.base);
-#endif
   // activation row of token t of the slot (one token: row 0, no lookup)
   auto row_of = [&](int t) {
     return PLAIN ? v.pair0 + t
