@@ -609,46 +609,59 @@ __global__ __launch_bounds__(256) void k_combine(const YT *__restrict__ ypair,
   }
 }
 
-// float4 form of y_at: four consecutive columns, the same sums
-template <int NS, typename YT>
-__device__ __forceinline__ float4 y4_at(const YT *__restrict__ y, size_t stride, int ns,
-                                        size_t o) {
-  if constexpr (NS == 1) {
-    return yval4(y, o);
-  } else {
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-      float4 u[8];
+// Slice sums of R rows of four consecutive columns at once (rows with
+// use[r] false are not read and sum to zero): every used row's first SB
+// slices are loaded (those past the last slice clamped to it: cache hits, no
+// branches) before any is added, so with at most SB slices all the rows take
+// one round of loads; the sums are selects, not branches, so nothing waits
+// between the rows.  Per row the same additions in slice order as y_at.
+template <int R, int SB, typename YT>
+__device__ __forceinline__ void y4_rows(const YT *__restrict__ y, size_t stride, int ns,
+                                        const size_t (&o)[R], const bool (&use)[R],
+                                        float4 (&v)[R]) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        u[j] = yval4(y, (size_t)min(s0 + j, ns - 1) * stride + o);
+  for (int r = 0; r < R; ++r) v[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < ns; s0 += SB) {
+    float4 u[R][SB];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (s0 + j < ns) {
-          if (s0 + j == 0) {
-            v = u[j];
-          } else {
-            v.x = v.x + u[j].x;
-            v.y = v.y + u[j].y;
-            v.z = v.z + u[j].z;
-            v.w = v.w + u[j].w;
-          }
-        }
+    for (int r = 0; r < R; ++r) {
+      if (use[r]) {
+#pragma unroll
+        for (int j = 0; j < SB; ++j)
+          u[r][j] = yval4(y, (size_t)min(s0 + j, ns - 1) * stride + o[r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < SB; ++j) u[r][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
     }
-    return v;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const float4 a = v[r], b = u[r][j];
+        const float4 sum = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+        if (j == 0)  // slice s0 < ns always
+          v[r] = s0 == 0 ? b : sum;
+        else
+          v[r] = s0 + j < ns ? sum : a;
+      }
   }
 }
 
 // k_combine with the token's routes read once per workgroup: workgroup
-// blockIdx.x covers 1024 columns (four per thread, float4 stores) of token
-// blockIdx.x / nchunk, so the token's count, pair indices and weights are
-// workgroup-uniform loads and no thread divides its index by H.  (Whole rows
-// per workgroup, with the route loads paid once per token, measured slower
-// at 2048-4096 tokens: the chunks' parallelism matters more.)  Per element
-// the same operations in the same order as k_combine.  Requires H % 4 == 0,
+// blockIdx.x covers 4 * blockDim.x columns (four per thread, float4 stores)
+// of token blockIdx.x / nchunk, so the token's count, pair indices and
+// weights are workgroup-uniform loads and no thread divides its index by H.
+// (Whole rows per workgroup, with the route loads paid once per token,
+// measured slower at 2048-4096 tokens: the chunks' parallelism matters
+// more.)  The residual is loaded with the routes' indices; with K slices
+// (NS == 0) a batch's routes and the shared row load their slices together
+// (up to SB slices in one round: two rounds of dependent loads in all, where
+// a row at a time took one per route and batch of slices).  Per element the
+// same operations in the same order as k_combine.  Requires H % 4 == 0,
 // 16-byte aligned out and residual, and ypair aligned to four of its
 // elements.
-template <int NS, int RB, typename YT>
+template <int NS, int RB, int SB, typename YT>
 __global__ __launch_bounds__(256) void k_combine4(const YT *__restrict__ ypair,
                                                   const float *__restrict__ rw,
                                                   const int32_t *__restrict__ rcnt,
@@ -656,12 +669,17 @@ __global__ __launch_bounds__(256) void k_combine4(const YT *__restrict__ ypair,
                                                   int H, int shared, float *out, int ns,
                                                   size_t stride, const float *residual,
                                                   int nchunk) {
+  static_assert(NS == 1 || (RB + 1) * SB <= 40, "slice batch too large for registers");
   const int t = (int)(blockIdx.x / (unsigned)nchunk);
-  const int c4 = (int)(blockIdx.x - (unsigned)t * (unsigned)nchunk) * 256 + (int)threadIdx.x;
+  const int c4 = (int)(blockIdx.x - (unsigned)t * (unsigned)nchunk) * (int)blockDim.x +
+                 (int)threadIdx.x;
   if (4 * c4 >= H) return;
   const size_t col = 4 * (size_t)c4;
-  const float4 sh = shared ? y4_at<NS>(ypair, stride, ns, ((size_t)T * k + t) * H + col)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+  const size_t i = (size_t)t * H + col;
+  const size_t sh_off = ((size_t)T * k + t) * H + col;
+  const float4 rv = residual ? *reinterpret_cast<const float4 *>(residual + i)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 sh = (NS == 1 && shared) ? yval4(ypair, sh_off) : make_float4(0.f, 0.f, 0.f, 0.f);
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   int n = k;  // the route count arrives with the first batch of routes
   for (int r0 = 0; r0 < n; r0 += RB) {
@@ -675,10 +693,27 @@ __global__ __launch_bounds__(256) void k_combine4(const YT *__restrict__ ypair,
       p[j] = inv ? inv[r] : (int)r;
       w[j] = rw[r];
     }
+    if constexpr (NS == 0) {
+      size_t o[RB + 1];  // the routes, then the shared row
+      bool use[RB + 1];
+      float4 v[RB + 1];
 #pragma unroll
-    for (int j = 0; j < RB; ++j)
-      yv[j] = (!inv || r0 + j < n) ? y4_at<NS>(ypair, stride, ns, (size_t)p[j] * H + col)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int j = 0; j < RB; ++j) {
+        o[j] = (size_t)p[j] * H + col;
+        use[j] = !inv || r0 + j < n;
+      }
+      o[RB] = sh_off;
+      use[RB] = shared && r0 == 0;
+      y4_rows<RB + 1, SB>(ypair, stride, ns, o, use, v);
+#pragma unroll
+      for (int j = 0; j < RB; ++j) yv[j] = v[j];
+      if (r0 == 0) sh = v[RB];
+    } else {
+#pragma unroll
+      for (int j = 0; j < RB; ++j)
+        yv[j] = (!inv || r0 + j < n) ? yval4(ypair, (size_t)p[j] * H + col)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 #pragma unroll
     for (int j = 0; j < RB; ++j)
       if (r0 + j < n) {
@@ -694,9 +729,7 @@ __global__ __launch_bounds__(256) void k_combine4(const YT *__restrict__ ypair,
     acc.z = acc.z + sh.z;
     acc.w = acc.w + sh.w;
   }
-  const size_t i = (size_t)t * H + col;
   if (residual) {
-    const float4 rv = *reinterpret_cast<const float4 *>(residual + i);
     acc.x = rv.x + acc.x;
     acc.y = rv.y + acc.y;
     acc.z = rv.z + acc.z;
@@ -814,24 +847,33 @@ int combine_rows(nx_ctx *c, const YT *d_ypair, const float *d_weight, const int3
   const int sh = shared ? 1 : 0;
   auto al16 = [](const void *q) { return ((uintptr_t)q & 15u) == 0; };
   const bool y_al = ((uintptr_t)d_ypair & (4 * sizeof(YT) - 1)) == 0;
-  const int nchunk = (H / 4 + 255) / 256;
+  // Workgroups of 256 threads (1024 columns).  With K slices (a thread's
+  // loads are the slices of every route) and fewer than two such workgroups
+  // per CU: 128 or 64 threads, so a few tokens' rows spread over more CUs
+  // (measured, Mixtral 32 tokens 19 slices: 7.1 -> 6.9 us; not with one
+  // slice, where a token's 2048 columns on 8 workgroups took longer than on 2).
+  int tpb = 256;
+  while (ns > 1 && tpb > 64 && (long)T * ((H / 4 + tpb - 1) / tpb) < 2L * c->num_cu) tpb /= 2;
+  const int nchunk = (H / 4 + tpb - 1) / tpb;
   if (H % 4 == 0 && y_al && al16(d_out) && al16(d_residual) &&
       (size_t)T * nchunk < (1u << 31)) {
     auto run4 = [&](auto kern) {
       return launch(c, "combine", [&] {
-        go(c, kern, dim3((unsigned)(T * nchunk)), dim3(256), 0, d_ypair, d_weight, d_count, d_inv, T,
-                                                            k, H, sh, d_out, ns, split_stride,
-                                                            d_residual, nchunk);
+        go(c, kern, dim3((unsigned)(T * nchunk)), dim3((unsigned)tpb), 0, d_ypair, d_weight,
+           d_count, d_inv, T, k, H, sh, d_out, ns, split_stride, d_residual, nchunk);
       });
     };
     if (ns == 1) {
-      if (k <= 2) return run4(k_combine4<1, 2, YT>);
-      if (k <= 4) return run4(k_combine4<1, 4, YT>);
-      return run4(k_combine4<1, 8, YT>);
+      if (k <= 2) return run4(k_combine4<1, 2, 8, YT>);
+      if (k <= 4) return run4(k_combine4<1, 4, 8, YT>);
+      return run4(k_combine4<1, 8, 8, YT>);
     }
-    if (k <= 2) return run4(k_combine4<0, 2, YT>);
-    if (k <= 4) return run4(k_combine4<0, 4, YT>);
-    return run4(k_combine4<0, 8, YT>);
+    // slices loaded 8 at a time (4 for more than 4 routes); 24 at a time for
+    // Mixtral's 19 slices measured slower (7.5 against 7.1 us: the registers
+    // halve the waves per SIMD)
+    if (k <= 2) return run4(k_combine4<0, 2, 8, YT>);
+    if (k <= 4) return run4(k_combine4<0, 4, 8, YT>);
+    return run4(k_combine4<0, 8, 4, YT>);
   }
   size_t g = (total + 255) / 256;
   if (g > 65536) g = 65536;
