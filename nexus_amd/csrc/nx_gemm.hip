@@ -619,11 +619,12 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
   // groups of g_e = XCD_WGS / m_e N-tiles with the M-tiles fastest: about
   // XCD_WGS workgroups, as many as an XCD runs at once, share g_e weight
   // tiles and m_e activation tiles through the XCD's L2.  xcd_split 2
-  // (gate/up, few pairs per expert): XCD x runs one contiguous chunk of the
-  // M-tile-major list (N-tiles fastest).  xcd_split 0 (down, whose
-  // activation tiles span K = the expert width and are the larger
-  // operand): N-tiles fastest, so the N-tiles of one activation tile run
-  // together.
+  // (few pairs per expert, gate/up or down): XCD x runs one contiguous chunk
+  // of the M-tile-major list (N-tiles fastest), so an M-tile's N-tiles share
+  // its activation tile through one L2.  xcd_split 0 (down, many pairs per
+  // expert, whose activation tiles span K = the expert width and are the
+  // larger operand): N-tiles fastest, so the N-tiles of one activation tile
+  // run together.
   constexpr int XCD_WGS = 32 * Shape::OCC;  // 32 CUs x OCC workgroups
   int L = blockIdx.x;
   // down: K split `split` of ksplit (whole loop bodies each)
@@ -1107,13 +1108,21 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   // expert on average takes the XCD-chunked M-tile-major order (an M-tile's
   // N-tiles share its activation tile in one L2), with more the XCD split
   // by N-tiles (an N-tile group's weights serve all of the expert's
-  // M-tiles); down N-tiles fastest.  Measured: Qwen3 T = 512 gate/up
-  // 120 -> 101 us and DeepSeek T = 4096 2.93 -> 2.82 ms (HBM reads 14.7 ->
-  // 9.9 GB) with the chunked order; Mixtral Q8_0 prefill (four M-tiles per
-  // expert) 0.98 -> 1.17 ms with it, so it keeps the split.
+  // M-tiles).  Down takes the chunked order on the same condition, else
+  // N-tiles fastest.  Measured: Qwen3 T = 512 gate/up 120 -> 101 us and
+  // DeepSeek T = 4096 2.93 -> 2.82 ms (HBM reads 14.7 -> 9.9 GB) with the
+  // chunked order; Mixtral Q8_0 prefill (four M-tiles per expert) 0.98 ->
+  // 1.17 ms with it, so it keeps the split.  Down, chunked against N-tiles
+  // fastest: Qwen3 T = 512 64.8 -> 62.4 us, T = 256 60.6 -> 59.5 us (the
+  // M-tile's activation rows read through one L2 instead of every XCD's),
+  // DeepSeek T = 4096 unchanged.
   const long pairs = (long)p.T * p.k;
   const long active = std::max<long>(1, std::min<long>(ex->E, pairs));
-  a.xcd_split = gateup ? (pairs <= 2L * p.tile_m * active ? 2 : 1) : 0;
+#ifndef NX_GEMM_DOWN_XCD
+#define NX_GEMM_DOWN_XCD 0
+#endif
+  a.xcd_split = gateup ? (pairs <= 2L * p.tile_m * active ? 2 : 1)
+                       : (NX_GEMM_DOWN_XCD && pairs <= 2L * p.tile_m_down * active ? 2 : 0);
   // enough workgroups for the order at the largest M-tile count
   const long per = a.xcd_split == 1 ? 8L * ((a.n_tiles + 7) / 8) * max_tiles
                    : a.xcd_split == 2 ? 8L * (((long)a.n_tiles * max_tiles + 7) / 8)

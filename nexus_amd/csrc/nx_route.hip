@@ -738,6 +738,95 @@ __global__ __launch_bounds__(256) void k_combine4(const YT *__restrict__ ypair,
   *reinterpret_cast<float4 *>(out + i) = acc;
 }
 
+// k_combine4 for bf16 rows without K splits, eight columns per thread: one
+// 16-byte load per route (eight bf16, widened exactly) and two float4
+// stores, so a wave moves 1 KB per route load instead of 512 bytes.  Per
+// element the same operations in the same order as k_combine.  Requires
+// H % 8 == 0, 16-byte aligned out, residual and ypair.
+__device__ __forceinline__ void bf16x8(const uint16_t *__restrict__ y, size_t o, float4 &a,
+                                       float4 &b) {
+  const uint4 u = *reinterpret_cast<const uint4 *>(y + o);
+  a = make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                  __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+  b = make_float4(__uint_as_float(u.z << 16), __uint_as_float(u.z & 0xffff0000u),
+                  __uint_as_float(u.w << 16), __uint_as_float(u.w & 0xffff0000u));
+}
+__device__ __forceinline__ void fma_add4(float4 &acc, float w, const float4 &y) {
+  acc.x = acc.x + __fmul_rn(w, y.x);
+  acc.y = acc.y + __fmul_rn(w, y.y);
+  acc.z = acc.z + __fmul_rn(w, y.z);
+  acc.w = acc.w + __fmul_rn(w, y.w);
+}
+__device__ __forceinline__ void add4(float4 &acc, const float4 &y) {
+  acc.x = acc.x + y.x;
+  acc.y = acc.y + y.y;
+  acc.z = acc.z + y.z;
+  acc.w = acc.w + y.w;
+}
+__device__ __forceinline__ void radd4(float4 &acc, const float4 &r) {  // residual first
+  acc.x = r.x + acc.x;
+  acc.y = r.y + acc.y;
+  acc.z = r.z + acc.z;
+  acc.w = r.w + acc.w;
+}
+template <int RB>
+__global__ __launch_bounds__(256) void k_combine8(const uint16_t *__restrict__ ypair,
+                                                  const float *__restrict__ rw,
+                                                  const int32_t *__restrict__ rcnt,
+                                                  const int32_t *__restrict__ inv, int T, int k,
+                                                  int H, int shared, float *out,
+                                                  const float *residual, int nchunk) {
+  const int t = (int)(blockIdx.x / (unsigned)nchunk);
+  const int c8 = (int)(blockIdx.x - (unsigned)t * (unsigned)nchunk) * (int)blockDim.x +
+                 (int)threadIdx.x;
+  if (8 * c8 >= H) return;
+  const size_t col = 8 * (size_t)c8;
+  const size_t i = (size_t)t * H + col;
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 r0v = z, r1v = z, sh0 = z, sh1 = z;
+  if (residual) {
+    r0v = *reinterpret_cast<const float4 *>(residual + i);
+    r1v = *reinterpret_cast<const float4 *>(residual + i + 4);
+  }
+  if (shared) bf16x8(ypair, ((size_t)T * k + t) * H + col, sh0, sh1);
+  float4 acc0 = z, acc1 = z;
+  int n = k;  // the route count arrives with the first batch of routes
+  for (int r0 = 0; r0 < n; r0 += RB) {
+    int p[RB];
+    float w[RB];
+    float4 y0[RB], y1[RB];
+    if (r0 == 0) n = rcnt[t];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      const size_t r = (size_t)t * k + min(r0 + j, k - 1);
+      p[j] = inv ? inv[r] : (int)r;
+      w[j] = rw[r];
+    }
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      y0[j] = z;
+      y1[j] = z;
+      if (!inv || r0 + j < n) bf16x8(ypair, (size_t)p[j] * H + col, y0[j], y1[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+      if (r0 + j < n) {
+        fma_add4(acc0, w[j], y0[j]);
+        fma_add4(acc1, w[j], y1[j]);
+      }
+  }
+  if (shared) {
+    add4(acc0, sh0);
+    add4(acc1, sh1);
+  }
+  if (residual) {
+    radd4(acc0, r0v);
+    radd4(acc1, r1v);
+  }
+  *reinterpret_cast<float4 *>(out + i) = acc0;
+  *reinterpret_cast<float4 *>(out + i + 4) = acc1;
+}
+
 }  // namespace
 
 int launch_route(nx_ctx *c, const float *d_logits, int T, int E, int k, int score_mode,
@@ -854,6 +943,26 @@ int combine_rows(nx_ctx *c, const YT *d_ypair, const float *d_weight, const int3
   // slice, where a token's 2048 columns on 8 workgroups took longer than on 2).
   int tpb = 256;
   while (ns > 1 && tpb > 64 && (long)T * ((H / 4 + tpb - 1) / tpb) < 2L * c->num_cu) tpb /= 2;
+  if constexpr (std::is_same<YT, uint16_t>::value) {
+    // bf16 rows without K splits: eight columns per thread; workgroups of
+    // 128 threads when a row's eighths fill those and not 256 (DeepSeek's
+    // 7168 columns: 7 of 128, not 4 of 256 with one half idle)
+    if (ns == 1 && H % 8 == 0 && al16(d_ypair) && al16(d_out) && al16(d_residual)) {
+      const int t8 = (H / 8) % 256 && (H / 8) % 128 == 0 ? 128 : 256;
+      const int nch8 = (H / 8 + t8 - 1) / t8;
+      if ((size_t)T * nch8 < (1u << 31)) {
+        auto run8 = [&](auto kern) {
+          return launch(c, "combine", [&] {
+            go(c, kern, dim3((unsigned)(T * nch8)), dim3((unsigned)t8), 0, d_ypair, d_weight,
+               d_count, d_inv, T, k, H, sh, d_out, d_residual, nch8);
+          });
+        };
+        if (k <= 2) return run8(k_combine8<2>);
+        if (k <= 4) return run8(k_combine8<4>);
+        return run8(k_combine8<8>);
+      }
+    }
+  }
   const int nchunk = (H / 4 + tpb - 1) / tpb;
   if (H % 4 == 0 && y_al && al16(d_out) && al16(d_residual) &&
       (size_t)T * nchunk < (1u << 31)) {
