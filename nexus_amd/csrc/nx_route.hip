@@ -977,11 +977,23 @@ int combine_rows(nx_ctx *c, const YT *d_ypair, const float *d_weight, const int3
       if (k <= 4) return run4(k_combine4<1, 4, 8, YT>);
       return run4(k_combine4<1, 8, 8, YT>);
     }
-    // slices loaded 8 at a time (4 for more than 4 routes); 24 at a time for
-    // Mixtral's 19 slices measured slower (7.5 against 7.1 us: the registers
-    // halve the waves per SIMD)
-    if (k <= 2) return run4(k_combine4<0, 2, 8, YT>);
-    if (k <= 4) return run4(k_combine4<0, 4, 8, YT>);
+    // slices loaded 2, 4 or 8 at a time, the fewest that cover the slice
+    // count (at most 4 for more than 4 routes): a wider batch than the
+    // slices only repeats the last slice's loads and costs registers
+    // (Mixtral prefill, 2 K splits of bf16 rows, 8 at a time: 29 -> 46 us).
+    // 24 at a time for Mixtral's 19 slices measured slower (7.5 against
+    // 7.1 us: the registers halve the waves per SIMD).
+    if (k <= 2) {
+      if (ns <= 2) return run4(k_combine4<0, 2, 2, YT>);
+      if (ns <= 4) return run4(k_combine4<0, 2, 4, YT>);
+      return run4(k_combine4<0, 2, 8, YT>);
+    }
+    if (k <= 4) {
+      if (ns <= 2) return run4(k_combine4<0, 4, 2, YT>);
+      if (ns <= 4) return run4(k_combine4<0, 4, 4, YT>);
+      return run4(k_combine4<0, 4, 8, YT>);
+    }
+    if (ns <= 2) return run4(k_combine4<0, 8, 2, YT>);
     return run4(k_combine4<0, 8, 4, YT>);
   }
   size_t g = (total + 255) / 256;
