@@ -188,6 +188,9 @@ struct GemmArgs {
   // grid decomposition (see k_gemm): N-tiles, the tile order, and (down)
   // the K splits, each over wg_per_split workgroups
   int n_tiles, xcd_split, ksplit, wg_per_split;
+  // Q4_K down pass: the window that holds only one block (the expert width
+  // is 256 past a multiple of 512), routed and shared expert, or -1
+  int half_win, shalf_win;
 };
 
 __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -275,15 +278,35 @@ __device__ __forceinline__ uint32_t code_win_off(int win, int p, int rows, int n
          (uint32_t)(p * panel_gsz(g, nseg) * 16 + (win & 7) * 128);
 }
 
-// codes of step S of window win
+// Q4_K half window (a row's last window when its width is 256 past a
+// multiple of 512: one block, 2u, of the two).  Its four steps take the
+// block's sub-blocks in order: quarter q of step S holds sub-block
+// 2S + q/2, half q%2, i.e. operand position j of the window is element
+// 512u + j.  In the code plane that is plane half S/2, 16-byte group
+// 2(S%2) + q/2 of the block's 64 bytes of the line: lane base row + 16(q/2)
+// + 8(q%2) (the full window's base minus 48(q/2)), uniform part line + 32(S%2).
+// All four quarters use block 2u's scales (lane base minus 16(q/2)).
+__host__ __device__ constexpr int half_win_of(int fmt, int cols) {
+  return fmt == NX_FMT_Q4_K && cols % 512 == 256 ? cols / 512 : -1;
+}
+
+// codes of step S of window win (half: the Q4_K half window, lane bases lqh)
 template <int FMT, int S, int NT>
 __device__ __forceinline__ void fetch_codes(WCodes<FMT, NT> &w, __amdgpu_buffer_rsrc_t rq,
-                                            const uint32_t (&lq)[NT], int win, int rows, int nseg) {
-  if constexpr (FMT == NX_FMT_Q8_0) {
+                                            const uint32_t (&lq)[NT], int win, int rows, int nseg,
+                                            bool half = false, const uint32_t *lqh = nullptr) {
+  if constexpr (FMT == NX_FMT_Q4_K) {
+    const uint32_t u = code_win_off(win, S >> 2, rows, nseg) + 16u * (S & 3);
+    // steps 4..7 of a half window do not exist: out of range, read as zero
+    const uint32_t uh = S < 4 ? code_win_off(win, S >> 1, rows, nseg) + 32u * (S & 1) : 0u;
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+      w.c[n] = bload8(rq, half ? (S < 4 ? lqh[n] + uh : OOB) : lq[n] + u);
+  } else if constexpr (FMT == NX_FMT_Q8_0) {
     const uint32_t u = code_win_off(win, S >> 1, rows, nseg);
 #pragma unroll
     for (int n = 0; n < NT; ++n) w.c[n] = bload16(rq, lq[n] + u + 16u * (S & 1));
-  } else if constexpr (FMT == NX_FMT_Q4_K || FMT == NX_FMT_Q4_0) {
+  } else if constexpr (FMT == NX_FMT_Q4_0) {
     const uint32_t u = code_win_off(win, S >> 2, rows, nseg);
 #pragma unroll
     for (int n = 0; n < NT; ++n) w.c[n] = bload8(rq, lq[n] + u + 16u * (S & 3));
@@ -302,7 +325,8 @@ __device__ __forceinline__ void fetch_codes(WCodes<FMT, NT> &w, __amdgpu_buffer_
 // bytes per segment), full panel rows 64 MU.
 template <int FMT, int NT>
 __device__ __forceinline__ void fetch_meta(WMeta<FMT, NT> &m, __amdgpu_buffer_rsrc_t rm,
-                                           const uint32_t (&lm)[NT], int win, int rows, int nseg) {
+                                           const uint32_t (&lm)[NT], int win, int rows, int nseg,
+                                           bool half = false, const uint32_t *lmh = nullptr) {
   constexpr int MU = Seg<FMT>::MU;
   if constexpr (MU > 0) {
     const int g = win >> 3;
@@ -311,6 +335,7 @@ __device__ __forceinline__ void fetch_meta(WMeta<FMT, NT> &m, __amdgpu_buffer_rs
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
       if constexpr (FMT == NX_FMT_Q8_0) m.m[n] = bload4(rm, lm[n] + u);
+      else if constexpr (FMT == NX_FMT_Q4_K) m.m[n] = bload16(rm, (half ? lmh[n] : lm[n]) + u);
       else m.m[n] = bload16(rm, lm[n] + u);
     }
   }
@@ -338,9 +363,12 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return r;
 }
 
-// values 8M .. 8M+7 of the 16 of row n at step S of the window, as a B operand
-template <int FMT, bool BF16, int S, int M, typename WC, typename WM>
-__device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WC &w, const WM &mt, int n) {
+// values 8M .. 8M+7 of the 16 of row n at step S of the window, as a B
+// operand (HALF: step S of a Q4_K half window, for the lane's quarter pair
+// qh = q / 2)
+template <int FMT, bool BF16, int S, int M, bool HALF = false, typename WC, typename WM>
+__device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WC &w, const WM &mt, int n,
+                                                            int qh = 0) {
   using Op = OpT<BF16>;
   if constexpr (FMT == NX_FMT_Q8_0 && !BF16) {
     // fp16 without a float detour: byte u = q ^ 0x80 becomes the f16 1024 + u
@@ -375,10 +403,12 @@ __device__ __forceinline__ typename OpT<BF16>::V8 w_operand(const WC &w, const W
       // Q4_K (src/quant/mod.rs:841) d * sc * q - dmin * m, A = d sc and
       // B = -dmin m; Q4_0 (q - 8) d, A = d and B = -8 d (exact, so the fma
       // rounds (q - 8) d once)
-      constexpr int t = S & 3, p = S >> 2;
+      // sub-block t + 4p of the block: in a half window t = 2(S%2) + q/2,
+      // p = S/2 (t per lane)
+      const int t = HALF ? 2 * (S & 1) + qh : (S & 3);
+      constexpr int p = HALF ? (S >> 1) : (S >> 2);
       float A, B;
       if constexpr (FMT == NX_FMT_Q4_K) {
-        // sub-block t + 4p of the block
         const uint4 Q = mt.m[n];
         const float d = h2f(Q.x & 0xFFFFu), dmin = h2f(Q.x >> 16);
         const uint32_t b0 = (Q.y >> (8 * t)) & 0xFFu;
@@ -566,7 +596,9 @@ struct LoadSchedule {
   }
 };
 
-template <int FMT, bool BF16, bool GATEUP, int BMT>
+// HWK: the Q4_K down pass of experts with a half window (its own
+// instances, so that the others keep their registers)
+template <int FMT, bool BF16, bool GATEUP, int BMT, bool HWK = false>
 __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gemm(const GemmArgs g) {
   using Op = OpT<BF16>;
   using V8 = typename Op::V8;
@@ -730,6 +762,18 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
     lq[n] = code_lane_off<FMT>(wrow * rbq, q);
     lm[n] = meta_lane_off<FMT>(wrow * rbm, q);
   }
+  // Q4_K down: the row's last window may be a half window (see
+  // half_win_of), run as 4 steps of its one block instead of 8 half-empty
+  // steps; its lane bases
+  constexpr bool HW = HWK && FMT == NX_FMT_Q4_K && !GATEUP;
+  static_assert(!HW || NB == WS, "a half window is one loop body");
+  const int half_win = HW ? (routed ? g.half_win : g.shalf_win) : -1;
+  uint32_t lqh[NT], lmh[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    lqh[n] = lq[n] - 48u * (uint32_t)(q >> 1);
+    lmh[n] = lm[n] - 16u * (uint32_t)(q >> 1);
+  }
 
   // activation loads I0 .. I1-1 of stage ks
   auto issue_a_part = [&](auto stage, int ks, auto i0, auto i1) {
@@ -754,22 +798,27 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
     constexpr int J = decltype(pos)::value;
     constexpr int S = J % WS;
     const int win = wbase + J / WS;
+    const bool hwin = HW && win == half_win;
     if constexpr (META2 && S == 0) {
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
-        fetch_meta<FMT, NT>(mbuf[(J / WS) % NMB][mt], mt == 0 ? rm0 : rm1, lm, win, rows, nseg);
+        fetch_meta<FMT, NT>(mbuf[(J / WS) % NMB][mt], mt == 0 ? rm0 : rm1, lm, win, rows, nseg,
+                            hwin, lmh);
     }
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
-      fetch_codes<FMT, S, NT>(wbuf[J % NBUF][mt], mt == 0 ? rq0 : rq1, lq, win, rows, nseg);
+      fetch_codes<FMT, S, NT>(wbuf[J % NBUF][mt], mt == 0 ? rq0 : rq1, lq, win, rows, nseg, hwin,
+                              lqh);
   };
   // single-buffered scales of the window that starts at step J
   auto issue_meta1 = [&](auto pos, int wbase) {
     constexpr int J = decltype(pos)::value;
     if constexpr (!META2 && n_meta_loads<FMT>() > 0) {
+      const int win = wbase + J / WS;
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
-        fetch_meta<FMT, NT>(mbuf[0][mt], mt == 0 ? rm0 : rm1, lm, wbase + J / WS, rows, nseg);
+        fetch_meta<FMT, NT>(mbuf[0][mt], mt == 0 ? rm0 : rm1, lm, win, rows, nseg,
+                            HW && win == half_win, lmh);
     }
   };
   // the late issues of step T (see LoadSchedule)
@@ -805,9 +854,14 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
   const int sw = swz(l16);
   // 16-row sets of the tile holding pairs (workgroup-uniform)
   const int msub = __builtin_amdgcn_readfirstlane((mrows + 15) >> 4);
-  auto step = [&](auto pos, int ks0, int wbase) {
+  // HB: the body of a Q4_K half window, of which only steps 0..3 run (the
+  // loads they issue for later steps are past the row and are drained by
+  // the last wait)
+  auto step = [&](auto pos, int ks0, int wbase, auto hb) {
     constexpr int P = decltype(pos)::value;
     constexpr int S = P % WS;
+    constexpr bool HB = decltype(hb)::value;
+    static_assert(!HB || (HW && S < 4), "half-window steps");
     wait_vm<sched.outstanding(P)>();
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
@@ -842,7 +896,8 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
         for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
           for (int n = 0; n < NT; ++n) {
-            bf[mt][n] = w_operand<FMT, BF16, S, M>(wbuf[P % NBUF][mt], mbuf[(P / WS) % NMB][mt], n);
+            bf[mt][n] = w_operand<FMT, BF16, S, M, HB>(wbuf[P % NBUF][mt], mbuf[(P / WS) % NMB][mt],
+                                                       n, q >> 1);
             // float decodes: one operand's temporaries at a time
             if constexpr (!(FMT == NX_FMT_Q8_0 && !BF16)) __builtin_amdgcn_sched_barrier(0);
           }
@@ -890,13 +945,25 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
       issue_w(IC<t + WDIST>{}, wb0);
     }
   });
-  for (int ks0 = ks_begin, wbase = wb0; ks0 < ks_end; ks0 += NB, wbase += NB / WS)
-    static_for<0, NB>([&](auto pos) { step(pos, ks0, wbase); });
+  // a split whose last body is the row's half window runs it on its own
+  const bool tail_half = HW && half_win >= 0 && ks_end / WS - 1 == half_win;
+  const int ks_full = tail_half ? ks_end - NB : ks_end;
+  int ks0 = ks_begin, wbase = wb0;
+  for (; ks0 < ks_full; ks0 += NB, wbase += NB / WS)
+    static_for<0, NB>([&](auto pos) { step(pos, ks0, wbase, IC<false>{}); });
+  if constexpr (HW) {
+    if (tail_half) static_for<0, 4>([&](auto pos) { step(pos, ks0, wbase, IC<true>{}); });
+  }
   // no direct-to-LDS write may land after the workgroup has ended
   wait_vm<0>();
 
   // ---- epilogue.  16x16 accumulator layout: lane holds column (lane % 16),
   // register j holds row 4 * (lane / 16) + j.
+  // gate/up: act slot of down-pass K position e (operand order; element
+  // order over a Q4_K half window, the down pass's last window when the
+  // width is 256 past a multiple of 512)
+  const int act_hs = half_win_of(FMT, rows) >= 0 ? rows - 256 : 0x7fffffff;
+  auto act_slot = [&](int e) { return e >= act_hs ? e : kslot<FMT>(e); };
   if constexpr (!GATEUP && BF16) {
     if (g.yb) {
       // bf16 partial sums, two columns per 32-bit store: lanes 2c and 2c+1
@@ -940,7 +1007,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
           const size_t p = (size_t)(pair0 + m0 + row);
           if constexpr (GATEUP) {
             const float v = silu_mul(acc[0][n][i][j], acc[1][n][i][j]);
-            g.act[p * g.act_stride + kslot<FMT>(col)] = Op::bits(v);
+            g.act[p * g.act_stride + act_slot(col)] = Op::bits(v);
           } else {
             g.y[split * g.y_split + p * g.y_stride + col] = acc[0][n][i][j];
           }
@@ -956,7 +1023,7 @@ __global__ __launch_bounds__(256, (GemmShape<FMT, GATEUP, BMT>::OCC)) void k_gem
     if (span > 0 && n0 + BN >= rows) {
       for (int i = tid; i < mrows * span; i += 256) {
         const int r = i / span, e = rows + (i - r * span);
-        g.act[(size_t)(pair0 + m0 + r) * g.act_stride + kslot<FMT>(e)] = 0;
+        g.act[(size_t)(pair0 + m0 + r) * g.act_stride + act_slot(e)] = 0;
       }
     }
   }
@@ -1014,9 +1081,13 @@ __global__ __launch_bounds__(256) void k_to_half(const float *__restrict__ x, in
 using GemmFn = void (*)(GemmArgs);
 
 template <bool BF16, bool GATEUP, int BMT>
-GemmFn pick_fmt(int fmt) {
+GemmFn pick_fmt(int fmt, bool half) {
   switch (fmt) {
-  case NX_FMT_Q4_K: return k_gemm<NX_FMT_Q4_K, BF16, GATEUP, BMT>;
+  case NX_FMT_Q4_K:
+    if constexpr (!GATEUP) {
+      if (half) return k_gemm<NX_FMT_Q4_K, BF16, GATEUP, BMT, true>;
+    }
+    return k_gemm<NX_FMT_Q4_K, BF16, GATEUP, BMT>;
   case NX_FMT_Q4_0: return k_gemm<NX_FMT_Q4_0, BF16, GATEUP, BMT>;
   }
   if constexpr (!GATEUP || BMT <= BM_GATEUP) {
@@ -1028,18 +1099,24 @@ GemmFn pick_fmt(int fmt) {
   return nullptr;
 }
 
-GemmFn pick(int fmt, bool bf16, bool gateup, int bm) {
+GemmFn pick(int fmt, bool bf16, bool gateup, int bm, bool half = false) {
   if (bm == BM_NARROW) {
     if (gateup)
-      return bf16 ? pick_fmt<true, true, BM_NARROW>(fmt) : pick_fmt<false, true, BM_NARROW>(fmt);
-    return bf16 ? pick_fmt<true, false, BM_NARROW>(fmt) : pick_fmt<false, false, BM_NARROW>(fmt);
+      return bf16 ? pick_fmt<true, true, BM_NARROW>(fmt, half)
+                  : pick_fmt<false, true, BM_NARROW>(fmt, half);
+    return bf16 ? pick_fmt<true, false, BM_NARROW>(fmt, half)
+                : pick_fmt<false, false, BM_NARROW>(fmt, half);
   }
   if (bm == BM_WIDE) {
-    if (gateup) return bf16 ? pick_fmt<true, true, BM_WIDE>(fmt) : pick_fmt<false, true, BM_WIDE>(fmt);
-    return bf16 ? pick_fmt<true, false, BM_WIDE>(fmt) : pick_fmt<false, false, BM_WIDE>(fmt);
+    if (gateup)
+      return bf16 ? pick_fmt<true, true, BM_WIDE>(fmt, half) : pick_fmt<false, true, BM_WIDE>(fmt, half);
+    return bf16 ? pick_fmt<true, false, BM_WIDE>(fmt, half) : pick_fmt<false, false, BM_WIDE>(fmt, half);
   }
-  if (gateup) return bf16 ? pick_fmt<true, true, BM_GATEUP>(fmt) : pick_fmt<false, true, BM_GATEUP>(fmt);
-  return bf16 ? pick_fmt<true, false, BM_GATEUP>(fmt) : pick_fmt<false, false, BM_GATEUP>(fmt);
+  if (gateup)
+    return bf16 ? pick_fmt<true, true, BM_GATEUP>(fmt, half)
+                : pick_fmt<false, true, BM_GATEUP>(fmt, half);
+  return bf16 ? pick_fmt<true, false, BM_GATEUP>(fmt, half)
+              : pick_fmt<false, false, BM_GATEUP>(fmt, half);
 }
 
 void fill_weights(GemmArgs &a, const nx_experts *ex, bool gateup) {
@@ -1075,6 +1152,8 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   const nx_experts *ex = p.ex;
   GemmArgs a{};
   fill_weights(a, ex, gateup);
+  a.half_win = gateup ? -1 : half_win_of(ex->fmt, a.cols);
+  a.shalf_win = gateup || ex->Fs <= 0 ? -1 : half_win_of(ex->fmt, a.scols);
   a.offsets = p.offsets;
   a.tiles = gateup ? p.tiles : p.tiles_down;
   const int max_tiles = gateup ? p.max_tiles : p.max_tiles_down;
@@ -1131,7 +1210,8 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   a.wg_per_split = (int)per;
   const long wgs = per * a.ksplit;
   if (wgs > 0x7FFFFFFFL) return fail(NX_ERR_UNSUPPORTED, "grouped GEMM grid too large");
-  GemmFn fn = pick(ex->fmt, p.bf16, gateup, gateup ? p.tile_m : p.tile_m_down);
+  GemmFn fn = pick(ex->fmt, p.bf16, gateup, gateup ? p.tile_m : p.tile_m_down,
+                   a.half_win >= 0 || a.shalf_win >= 0);
   if (!fn) return fail(NX_ERR_UNSUPPORTED, "no grouped-GEMM kernel for this format");
   const char *name = gateup ? "gemm_gateup" : "gemm_down";
   return launch(c, name,

@@ -246,6 +246,14 @@ MFMA_TOL = 1e-2
     (Q8_0, 16, 512, 640, 2, 300, 1.2),
     (Q4_0, 16, 256, 320, 2, 200, 1.1),
     (Q4_K, 16, 512, 768, 4, 150, None),
+    # Q4_K widths 256 past a multiple of 512: the down pass's last window
+    # holds one block and runs as 4 steps in element order (the only window;
+    # after two full ones; on 160-pair tiles; after eight, with the K split
+    # in two so that only the second split has it)
+    (Q4_K, 8, 256, 256, 2, 200, None),
+    (Q4_K, 4, 256, 1280, 2, 300, None),
+    (Q4_K, 4, 256, 768, 2, 560, None),
+    (Q4_K, 8, 512, 7424, 2, 64, None),
     # output rows the bf16 per-pair rows cannot take in pairs (odd H: f32
     # rows) or in fours (H % 4 == 2: bf16 rows through the scalar combine)
     (F32, 4, 37, 24, 2, 70, None),
@@ -301,6 +309,18 @@ def test_layer_random_shapes(ctx, case):
             assert err <= tol, (path, err)
     finally:
         ex.close()
+
+
+@pytest.mark.parametrize("path", [nx.PATH_MFMA_F16, nx.PATH_MFMA_BF16])
+@pytest.mark.parametrize("F,Fs", [(512, 768), (768, 512), (768, 256)])
+def test_layer_mfma_half_window_shared(ctx, path, F, Fs):
+    """Q4_K routed and shared experts of different widths, one or both 256
+    past a multiple of 512 (the down pass's half window per expert kind)."""
+    L = Layer(Q4_K, 8, 256, F, 2, 150, seed=F + Fs, shared_F=Fs, score_mode=1)
+    say(f"layer mfma half window path={path} F={F} Fs={Fs}")
+    err = rel_l2(run_layer(ctx, L, path), L.oracle_out())
+    say(f"  rel L2 = {err:.2e}")
+    assert err <= MFMA_TOL, err
 
 
 def test_layer_mfma_shared_expert_sigmoid(ctx):
