@@ -769,26 +769,90 @@ __device__ __forceinline__ void radd4(float4 &acc, const float4 &r) {  // residu
   acc.z = r.z + acc.z;
   acc.w = r.w + acc.w;
 }
-template <int RB>
+__device__ __forceinline__ float4 sel4(bool c, const float4 &a, const float4 &b) {
+  return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
+
+// Slice sums of R bf16 rows of eight consecutive columns, as y4_rows (every
+// used row's first SB slices loaded before any is added, slices past the
+// last clamped to it, the sums in slice order): v0 the first four columns,
+// v1 the last four.
+template <int R, int SB>
+__device__ __forceinline__ void y8_rows(const uint16_t *__restrict__ y, size_t stride, int ns,
+                                        const size_t (&o)[R], const bool (&use)[R],
+                                        float4 (&v0)[R], float4 (&v1)[R]) {
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int r = 0; r < R; ++r) v0[r] = v1[r] = z;
+  for (int s0 = 0; s0 < ns; s0 += SB) {
+    // raw words, widened only when added (values, not references: the
+    // arrays stay in registers)
+    uint4 u[R][SB];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (use[r]) {
+#pragma unroll
+        for (int j = 0; j < SB; ++j)
+          u[r][j] = *reinterpret_cast<const uint4 *>(y + (size_t)min(s0 + j, ns - 1) * stride + o[r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < SB; ++j) u[r][j] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < SB; ++j) {
+        const uint4 w = u[r][j];
+        const float4 b0 = make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                                      __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u));
+        const float4 b1 = make_float4(__uint_as_float(w.z << 16), __uint_as_float(w.z & 0xffff0000u),
+                                      __uint_as_float(w.w << 16), __uint_as_float(w.w & 0xffff0000u));
+        float4 a0 = v0[r], a1 = v1[r];
+        add4(a0, b0);
+        add4(a1, b1);
+        // component selects (a select of whole float4 values can become a
+        // select of their addresses, and the values go to scratch memory)
+        if (j == 0) {  // slice s0 < ns always
+          v0[r] = sel4(s0 == 0, b0, a0);
+          v1[r] = sel4(s0 == 0, b1, a1);
+        } else {
+          v0[r] = sel4(s0 + j < ns, a0, v0[r]);
+          v1[r] = sel4(s0 + j < ns, a1, v1[r]);
+        }
+      }
+  }
+}
+
+// k_combine4 for bf16 rows, eight columns per thread: one 16-byte load per
+// route row (and K slice) and two float4 stores, so a wave moves 1 KB per
+// load instead of 512 bytes.  With K slices (NS == 0) a batch's routes and
+// the shared row load their first SB slices together, as in k_combine4.
+// Per element the same operations in the same order as k_combine.
+// Requires H % 8 == 0, 16-byte aligned out, residual and ypair.
+template <int NS, int RB, int SB>
 __global__ __launch_bounds__(256) void k_combine8(const uint16_t *__restrict__ ypair,
                                                   const float *__restrict__ rw,
                                                   const int32_t *__restrict__ rcnt,
                                                   const int32_t *__restrict__ inv, int T, int k,
-                                                  int H, int shared, float *out,
-                                                  const float *residual, int nchunk) {
+                                                  int H, int shared, float *out, int ns,
+                                                  size_t stride, const float *residual,
+                                                  int nchunk) {
+  static_assert(NS == 1 || (RB + 1) * SB <= 20, "slice batch too large for registers");
   const int t = (int)(blockIdx.x / (unsigned)nchunk);
   const int c8 = (int)(blockIdx.x - (unsigned)t * (unsigned)nchunk) * (int)blockDim.x +
                  (int)threadIdx.x;
   if (8 * c8 >= H) return;
   const size_t col = 8 * (size_t)c8;
   const size_t i = (size_t)t * H + col;
+  const size_t sh_off = ((size_t)T * k + t) * H + col;
   const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
   float4 r0v = z, r1v = z, sh0 = z, sh1 = z;
   if (residual) {
     r0v = *reinterpret_cast<const float4 *>(residual + i);
     r1v = *reinterpret_cast<const float4 *>(residual + i + 4);
   }
-  if (shared) bf16x8(ypair, ((size_t)T * k + t) * H + col, sh0, sh1);
+  if (NS == 1 && shared) bf16x8(ypair, sh_off, sh0, sh1);
   float4 acc0 = z, acc1 = z;
   int n = k;  // the route count arrives with the first batch of routes
   for (int r0 = 0; r0 < n; r0 += RB) {
@@ -802,11 +866,34 @@ __global__ __launch_bounds__(256) void k_combine8(const uint16_t *__restrict__ y
       p[j] = inv ? inv[r] : (int)r;
       w[j] = rw[r];
     }
+    if constexpr (NS == 0) {
+      size_t o[RB + 1];  // the routes, then the shared row
+      bool use[RB + 1];
+      float4 v0[RB + 1], v1[RB + 1];
 #pragma unroll
-    for (int j = 0; j < RB; ++j) {
-      y0[j] = z;
-      y1[j] = z;
-      if (!inv || r0 + j < n) bf16x8(ypair, (size_t)p[j] * H + col, y0[j], y1[j]);
+      for (int j = 0; j < RB; ++j) {
+        o[j] = (size_t)p[j] * H + col;
+        use[j] = !inv || r0 + j < n;
+      }
+      o[RB] = sh_off;
+      use[RB] = shared && r0 == 0;
+      y8_rows<RB + 1, SB>(ypair, stride, ns, o, use, v0, v1);
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        y0[j] = v0[j];
+        y1[j] = v1[j];
+      }
+      if (r0 == 0) {
+        sh0 = v0[RB];
+        sh1 = v1[RB];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        y0[j] = z;
+        y1[j] = z;
+        if (!inv || r0 + j < n) bf16x8(ypair, (size_t)p[j] * H + col, y0[j], y1[j]);
+      }
     }
 #pragma unroll
     for (int j = 0; j < RB; ++j)
@@ -944,22 +1031,28 @@ int combine_rows(nx_ctx *c, const YT *d_ypair, const float *d_weight, const int3
   int tpb = 256;
   while (ns > 1 && tpb > 64 && (long)T * ((H / 4 + tpb - 1) / tpb) < 2L * c->num_cu) tpb /= 2;
   if constexpr (std::is_same<YT, uint16_t>::value) {
-    // bf16 rows without K splits: eight columns per thread; workgroups of
-    // 128 threads when a row's eighths fill those and not 256 (DeepSeek's
-    // 7168 columns: 7 of 128, not 4 of 256 with one half idle)
-    if (ns == 1 && H % 8 == 0 && al16(d_ypair) && al16(d_out) && al16(d_residual)) {
+    // bf16 rows (the grouped GEMM's down pass, up to 4 K splits): eight
+    // columns per thread; workgroups of 128 threads when a row's eighths
+    // fill those and not 256 (DeepSeek's 7168 columns: 7 of 128, not 4 of
+    // 256 with one half idle)
+    if (ns <= 4 && H % 8 == 0 && al16(d_ypair) && al16(d_out) && al16(d_residual)) {
       const int t8 = (H / 8) % 256 && (H / 8) % 128 == 0 ? 128 : 256;
       const int nch8 = (H / 8 + t8 - 1) / t8;
       if ((size_t)T * nch8 < (1u << 31)) {
         auto run8 = [&](auto kern) {
           return launch(c, "combine", [&] {
             go(c, kern, dim3((unsigned)(T * nch8)), dim3((unsigned)t8), 0, d_ypair, d_weight,
-               d_count, d_inv, T, k, H, sh, d_out, d_residual, nch8);
+               d_count, d_inv, T, k, H, sh, d_out, ns, split_stride, d_residual, nch8);
           });
         };
-        if (k <= 2) return run8(k_combine8<2>);
-        if (k <= 4) return run8(k_combine8<4>);
-        return run8(k_combine8<8>);
+        if (ns == 1) {
+          if (k <= 2) return run8(k_combine8<1, 2, 1>);
+          if (k <= 4) return run8(k_combine8<1, 4, 1>);
+          return run8(k_combine8<1, 8, 1>);
+        }
+        if (k <= 2) return ns <= 2 ? run8(k_combine8<0, 2, 2>) : run8(k_combine8<0, 2, 4>);
+        if (k <= 4) return ns <= 2 ? run8(k_combine8<0, 4, 2>) : run8(k_combine8<0, 4, 4>);
+        return run8(k_combine8<0, 8, 2>);  // two slices per round
       }
     }
   }
