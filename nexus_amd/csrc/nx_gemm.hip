@@ -1193,15 +1193,15 @@ int run(nx_ctx *c, const GemmPlan &p, bool gateup) {
   // chunked order; Mixtral Q8_0 prefill (four M-tiles per expert) 0.98 ->
   // 1.17 ms with it, so it keeps the split.  Down, chunked against N-tiles
   // fastest: Qwen3 T = 512 64.8 -> 62.4 us, T = 256 60.6 -> 59.5 us (the
-  // M-tile's activation rows read through one L2 instead of every XCD's),
-  // DeepSeek T = 4096 unchanged.
+  // M-tile's activation rows read through one L2 instead of every XCD's;
+  // 49.7 -> 48.3 us and 46.2 -> 45.9 us with the half-window tail),
+  // DeepSeek T = 4096 unchanged.  For many pairs per expert (Mixtral Q8_0
+  // prefill) the chunked order or gate/up's XCD split by N-tiles is slower
+  // (down 0.550 -> 0.559-0.569 ms).
   const long pairs = (long)p.T * p.k;
   const long active = std::max<long>(1, std::min<long>(ex->E, pairs));
-#ifndef NX_GEMM_DOWN_XCD
-#define NX_GEMM_DOWN_XCD 0
-#endif
   a.xcd_split = gateup ? (pairs <= 2L * p.tile_m * active ? 2 : 1)
-                       : (NX_GEMM_DOWN_XCD && pairs <= 2L * p.tile_m_down * active ? 2 : 0);
+                       : (pairs <= 2L * p.tile_m_down * active ? 2 : 0);
   // enough workgroups for the order at the largest M-tile count
   const long per = a.xcd_split == 1 ? 8L * ((a.n_tiles + 7) / 8) * max_tiles
                    : a.xcd_split == 2 ? 8L * (((long)a.n_tiles * max_tiles + 7) / 8)
