@@ -15,7 +15,7 @@ import pytest
 
 import nexus_amd as nx
 import oracle
-from moe_cases import Q4_K, Q8_0, DeviceArray, Layer, assert_same_bits, rel_l2
+from moe_cases import F32, Q4_K, Q8_0, DeviceArray, Layer, assert_same_bits, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -198,14 +198,21 @@ def test_moe_block_exact_prologue_special_rows(ctx, H):
     ex.close()
 
 
-def test_moe_block_mfma_residual(ctx):
-    E, H, F, k, T = 8, 512, 512, 2, 192
-    L, hidden, norm_w, router = block_case(Q8_0, E, H, F, k, T, seed=31, shared_F=512)
+# the residual added by the combine over each kind of per-pair rows: f32
+# (fp16 GEMM), bf16 in eight-column runs without and with K splits (the
+# down pass split in two at F = 4096), bf16 in four-column runs (H % 8 == 4)
+@pytest.mark.parametrize("path,H,F", [(nx.PATH_MFMA_F16, 512, 512), (nx.PATH_MFMA_BF16, 512, 512),
+                                      (nx.PATH_MFMA_BF16, 512, 4096), (nx.PATH_MFMA_BF16, 516, 512)])
+def test_moe_block_mfma_residual(ctx, path, H, F):
+    E, k, T = 8, 2, 192
+    fmt = Q8_0 if H % 32 == 0 else F32
+    print(f"moe block mfma residual path={path} fmt={fmt} H={H} F={F}", flush=True)
+    L, hidden, norm_w, router = block_case(fmt, E, H, F, k, T, seed=31, shared_F=512)
     eps = 1e-5
     normed, logits, ffn = oracle_block(L, hidden, norm_w, eps, router)
     ex = L.upload(nx, ctx)
-    got = ex.block(hidden, norm_w, eps, router, k, path=nx.PATH_MFMA_F16, exact=True)
-    want = (hidden + ex.forward(normed, logits, k, path=nx.PATH_MFMA_F16)).astype(np.float32)
+    got = ex.block(hidden, norm_w, eps, router, k, path=path, exact=True)
+    want = (hidden + ex.forward(normed, logits, k, path=path)).astype(np.float32)
     assert_same_bits(got, want)
     assert rel_l2(got.astype(np.float64) - hidden, ffn) <= 1e-2
     ex.close()
