@@ -609,6 +609,12 @@ __global__ __launch_bounds__(256) void k_combine(const YT *__restrict__ ypair,
   }
 }
 
+// c ? a : b per component (a select of whole float4 values can become a
+// select of their addresses, with the values in scratch memory)
+__device__ __forceinline__ float4 sel4(bool c, const float4 &a, const float4 &b) {
+  return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
+
 // Slice sums of R rows of four consecutive columns at once (rows with
 // use[r] false are not read and sum to zero): every used row's first SB
 // slices are loaded (those past the last slice clamped to it: cache hits, no
@@ -641,9 +647,9 @@ __device__ __forceinline__ void y4_rows(const YT *__restrict__ y, size_t stride,
         const float4 a = v[r], b = u[r][j];
         const float4 sum = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
         if (j == 0)  // slice s0 < ns always
-          v[r] = s0 == 0 ? b : sum;
+          v[r] = sel4(s0 == 0, b, sum);
         else
-          v[r] = s0 + j < ns ? sum : a;
+          v[r] = sel4(s0 + j < ns, sum, a);
       }
   }
 }
@@ -769,10 +775,6 @@ __device__ __forceinline__ void radd4(float4 &acc, const float4 &r) {  // residu
   acc.z = r.z + acc.z;
   acc.w = r.w + acc.w;
 }
-__device__ __forceinline__ float4 sel4(bool c, const float4 &a, const float4 &b) {
-  return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
-}
-
 // Slice sums of R bf16 rows of eight consecutive columns, as y4_rows (every
 // used row's first SB slices loaded before any is added, slices past the
 // last clamped to it, the sums in slice order): v0 the first four columns,
@@ -811,8 +813,6 @@ __device__ __forceinline__ void y8_rows(const uint16_t *__restrict__ y, size_t s
         float4 a0 = v0[r], a1 = v1[r];
         add4(a0, b0);
         add4(a1, b1);
-        // component selects (a select of whole float4 values can become a
-        // select of their addresses, and the values go to scratch memory)
         if (j == 0) {  // slice s0 < ns always
           v0[r] = sel4(s0 == 0, b0, a0);
           v1[r] = sel4(s0 == 0, b1, a1);
