@@ -25,7 +25,9 @@
 // for several steps sit in one load (kpos below).  The activations are
 // written in the same order by their producers (k_to_half for x, the gate/up
 // epilogue for act), so the activation tile of a step is still one
-// contiguous 128-byte run per row.
+// contiguous 128-byte run per row.  A Q4_K row whose width is 256 past a
+// multiple of 512 ends in a half window of one block, which the down pass
+// takes in element order over 4 steps (half_win_of, the HWK instances).
 //
 // Pipeline.  The activation tile of a step goes into a 4-stage LDS ring by
 // direct-to-LDS loads, shared by the four waves.  The weights never pass
