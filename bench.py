@@ -139,7 +139,7 @@ def cpu_baseline(nx, ctx, torch, x, logits, E, H, F, k, seed, ntok):
             e = int(e)
             oracle.swiglu_ffn(xs_h[t], mats[1][e], mats[0][e], mats[2][e], H, F)
     dts = time.perf_counter() - t2
-    ncores = oracle.default_threads()  # the box's CPU share for one GPU
+    ncores = oracle.default_threads()  # the host CPU share for one GPU
     # one-token decode in CpuBackend::matmul's pattern (src/backend/cpu.rs:23-38):
     # each product of each routed expert as C[rows x 1] = W[rows x cols] . x,
     # its rows split over every core, token by token

@@ -80,7 +80,7 @@ __device__ __forceinline__ uint4 ld_stream16(const uint8_t *p) {
 // group, when shorter, is followed by zeros up to the panel row's end.  A
 // kernel that streams one group of many rows (the K-sliced decode down pass)
 // then reads one contiguous run: 2 KB pieces of rows 7 KB apart (the
-// row-major form of Mixtral's down rows) read at 3.6 TB/s on the box, the
+// row-major form of Mixtral's down rows) read at 3.6 TB/s on one MI355X, the
 // same bytes in panels at 5.3 TB/s.  Rows of at most 64 segments are one
 // panel without padding: the plain row-major layout.
 __host__ __device__ __forceinline__ int panel_gsz(int g, int nseg) {
