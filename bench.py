@@ -560,7 +560,7 @@ def only_case(nx, ctx, torch, args):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; run with --gpus 1"}))
+        print(json.dumps({"error": "this benchmark measures one GPU only; run with --gpus 1"}))
         sys.exit(2)
     import torch
 

@@ -64,7 +64,7 @@ extern "C" {
 #define NX_OK 0
 #define NX_ERR_INVALID_ARG 1 /* null pointer, bad enum, negative size */
 #define NX_ERR_SHAPE 2       /* sizes inconsistent with each other */
-#define NX_ERR_UNSUPPORTED 3 /* valid request this build does not implement */
+#define NX_ERR_UNSUPPORTED 3 /* valid request the library does not implement */
 #define NX_ERR_DEVICE 4      /* HIP runtime failure or no gfx950 device */
 #define NX_ERR_OOM 5         /* device allocation failed */
 #define NX_ERR_TRUNCATED 6   /* quantized payload shorter than its element count */

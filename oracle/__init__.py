@@ -1,6 +1,6 @@
 """CPU oracle for the Nexus MoE routed-FFN path (ctypes wrapper over nx_oracle.c).
 
-TEST INFRASTRUCTURE ONLY: this is the checker.  Only ``tests/``,
+TEST INFRASTRUCTURE ONLY: the oracle the HIP path is tested against.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  The product package ``nexus_amd`` never imports it.
 

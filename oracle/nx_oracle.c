@@ -1,7 +1,7 @@
 /*
  * nx_oracle.c — CPU restatement of the Nexus MoE routed-FFN path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker).  It is never linked into or called
+ * TEST INFRASTRUCTURE ONLY (the test oracle).  It is never linked into or called
  * by the product library; only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py load it.
  *

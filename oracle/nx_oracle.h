@@ -1,7 +1,7 @@
 /*
  * nx_oracle.h — CPU restatement of the Nexus MoE routed-FFN path.
  *
- * TEST INFRASTRUCTURE ONLY.  This is the checker that the HIP product is
+ * TEST INFRASTRUCTURE ONLY.  This is the oracle that the HIP product is
  * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may load it; the product library never links it.
  *
