@@ -1133,10 +1133,20 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   const long groups = (long)c->num_cu * wg_per_cu * groups_per_wg;
   long rpg = (work_rows + groups - 1) / groups;
   if (rpg < 1) rpg = 1;
+  const long grid_y = per_slot ? (long)slots_max * kslices : 1;
+  // Q4_K and Q8_0 gate/up rows of one wave each (no cross-wave sums): twice
+  // the rows per group, half the workgroups, while those still cover every
+  // CU.  Measured, one token (us per layer step): Mixtral Q4_K 40.7 -> 40.4,
+  // Q8_0 68.5 -> 66.9; Qwen3 and DeepSeek unchanged; Q4_0 40.1 -> 43.1 and
+  // Q2_K 37.6 -> 41.4, so not those; the same for the down passes: Qwen3
+  // 20.8 -> 19.8 but DeepSeek 53.4 -> 54.8, Q4_0 and Q2_K 3-4 us slower.
+  if (gateup && sh.ksplit == 1 && (ex->fmt == NX_FMT_Q4_K || ex->fmt == NX_FMT_Q8_0)) {
+    const long rpw2 = 2 * rpg * groups_per_wg;
+    if ((rows + rpw2 - 1) / rpw2 * grid_y >= c->num_cu) rpg *= 2;
+  }
   // whole row blocks per slot round the grid up: lengthen the runs until
   // it fits one round (a workgroup left over for a second round runs alone
   // and nearly doubles the launch)
-  const long grid_y = per_slot ? (long)slots_max * kslices : 1;
   rpg = fit_one_round(rows, rpg, groups_per_wg, grid_y, (long)c->num_cu * wg_per_cu);
   a.rows_per_group = (int)rpg;
   a.one_token = p.T == 1 ? 1 : 0;
