@@ -1140,7 +1140,14 @@ int run_gemv(nx_ctx *c, const GemvPlan &p, bool gateup) {
   // Q8_0 68.5 -> 66.9; Qwen3 and DeepSeek unchanged; Q4_0 40.1 -> 43.1 and
   // Q2_K 37.6 -> 41.4, so not those; the same for the down passes: Qwen3
   // 20.8 -> 19.8 but DeepSeek 53.4 -> 54.8, Q4_0 and Q2_K 3-4 us slower.
-  if (gateup && sh.ksplit == 1 && (ex->fmt == NX_FMT_Q4_K || ex->fmt == NX_FMT_Q8_0)) {
+  // Q4_K down rows of at most 16 lanes (Qwen3's 768-wide experts) or in K
+  // slices (Mixtral's 14336) take the longer runs too (one token: Qwen3
+  // 20.7 -> 19.7 us, Mixtral 40.4 -> 39.9 us; DeepSeek, Q8_0 unchanged).
+  const bool longer =
+      sh.ksplit == 1 &&
+      (gateup ? (ex->fmt == NX_FMT_Q4_K || ex->fmt == NX_FMT_Q8_0)
+              : (ex->fmt == NX_FMT_Q4_K && (sh.lpr <= 16 || kslices > 1)));
+  if (longer) {
     const long rpw2 = 2 * rpg * groups_per_wg;
     if ((rows + rpw2 - 1) / rpw2 * grid_y >= c->num_cu) rpg *= 2;
   }
